@@ -1,0 +1,168 @@
+/*
+ * superl8_hip.h — C ABI of libsuperl8_hip.so, the gfx950 (MI355X) kernels
+ * behind the superl8 INT8-attention / Q4_K-GEMV operator API.
+ *
+ * This library replaces the pybind11 module built from the reference's
+ * csrc/fni8_api.cpp (superl8._C). Each entry point below names the reference
+ * binding it stands in for. Conventions shared by every entry point:
+ *
+ *   - All tensor arguments are raw device pointers to contiguous row-major
+ *     buffers, sizes are int64_t element counts, the stream is a hipStream_t
+ *     passed as void* (NULL = the legacy default stream).
+ *   - Outputs are allocated by the caller. Entry points never allocate,
+ *     free or synchronise; work is enqueued on `stream` only.
+ *   - Return value: SL8_OK (0) or a negative SL8_ERR_* code. The message for
+ *     the last failure on the calling host thread is sl8_last_error().
+ *     Argument checks mirror the reference's TORCH_CHECKs (same key phrases).
+ *   - Scales are fp32. "Folded" Q scales carry softmax_scale*log2(e), so the
+ *     kernels produce exp2-domain logits (reference superl8/quant/core.py:186-195).
+ */
+#ifndef SUPERL8_HIP_H
+#define SUPERL8_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define SL8_OK 0
+#define SL8_ERR_INVALID (-1) /* bad argument (shape, dtype, alignment, range) */
+#define SL8_ERR_LAUNCH (-2)  /* HIP launch / runtime failure */
+
+/* element types for dtype arguments */
+#define SL8_DTYPE_F16 0
+#define SL8_DTYPE_BF16 1
+#define SL8_DTYPE_F32 2
+
+/* Message of the last failed call on this host thread ("" if none). */
+const char* sl8_last_error(void);
+
+/* Library version string, e.g. "superl8-hip 0.1 gfx950". */
+const char* sl8_version(void);
+
+/* ------------------------------------------------------------------------
+ * Per-row symmetric int8 quantisation.
+ * Replaces _C.quantize_i8_rowwise (reference csrc/fni8_api.cpp:286-291,
+ * csrc/kernel/quant_rowwise.cu:84-121, csrc/include/quant_rowwise.cuh:42-92).
+ *   x [M,K] (x_dtype f16/bf16/f32) -> q int8 [M,K], scale fp32 [M]
+ *   scale = amax|x_row| * fp32(1/127) (1 if 0); q = clamp(rint(x/scale), +-127)
+ * ---------------------------------------------------------------------- */
+int sl8_quantize_i8_rowwise(const void* x, int x_dtype, int64_t M, int64_t K,
+                            int8_t* q, float* scale, void* stream);
+
+/* ------------------------------------------------------------------------
+ * K-smoothing mean: mean[g, d] = (1/N) * sum_n k[g, n, d], fp32.
+ * Replaces the torch reduction in superl8/quant/core.py:29-44,70-95
+ * (_mean_k_fp32_bounded / smooth_k). fp16 input is summed exactly in int64
+ * fixed point (order-independent); bf16/f32 in fp64, rows in order.
+ *   k [G, N, D] (dtype f16/bf16/f32) -> mean fp32 [G, D]
+ * ---------------------------------------------------------------------- */
+int sl8_k_mean(const void* k, int dtype, int64_t G, int64_t N, int64_t D,
+               float* mean, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Fused smooth + quantise (quantize_qk's K side, and Q with mean=NULL):
+ *   xs[g,n,:] = dtype(x[g,n,:] - mean[g,:])      (mean may be NULL -> no shift)
+ *   q, s      = per-row int8 of xs                 (as sl8_quantize_i8_rowwise)
+ *   scale[g,n]= s * scale_mul                      (fp32 multiply; 1.0 = none)
+ * Reference: superl8/quant/core.py:164-196 (smooth_k, quantize_int8_rowwise,
+ * q_scale * (softmax_scale*LOG2E)).
+ *   x [G, N, D] -> q int8 [G, N, D], scale fp32 [G, N]
+ * ---------------------------------------------------------------------- */
+int sl8_quantize_i8_rows_centered(const void* x, int x_dtype, int64_t G, int64_t N,
+                                  int64_t D, const float* mean, float scale_mul,
+                                  int8_t* q, float* scale, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Prefill FlashAttention-2: int8 QK^T on MFMA (int32 accumulate), fp32
+ * online softmax in the exp2 domain, fp16/bf16 PV on MFMA, output dtype = V's.
+ * Replaces _C.attn_int8_fwd / _C.attn_int8_fwd_train (reference
+ * csrc/fni8_api.cpp:12-19,225-233, csrc/kernel/attn_int8_fwd.cu:101-200,
+ * csrc/include/attn_int8_fwd.cuh:47-209).
+ *   q int8 [B,Hq,M,D], q_scale fp32 [B,Hq,M] (folded), k int8 [B,Hkv,N,D],
+ *   k_scale fp32 [B,Hkv,N], v [B,Hkv,N,D] (v_dtype f16/bf16),
+ *   out [B,Hq,M,D] (v_dtype), lse fp32 [B,Hq,M] natural log or NULL.
+ *   causal: bottom-right aligned (query i sees keys <= i + N - M).
+ *   window_left >= 0: also require key > i + N - M - window_left.
+ *   D in {64, 128}. workspace: sl8_attn_int8_fwd_workspace() bytes (V^T staging).
+ * ---------------------------------------------------------------------- */
+size_t sl8_attn_int8_fwd_workspace(int64_t B, int64_t Hkv, int64_t N, int64_t D);
+int sl8_attn_int8_fwd(const int8_t* q, const float* q_scale, const int8_t* k,
+                      const float* k_scale, const void* v, int v_dtype, void* out,
+                      float* lse, int64_t B, int64_t Hq, int64_t Hkv, int64_t M,
+                      int64_t N, int64_t D, int causal, int64_t window_left,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* Test hook: the int32 Q.K^T scores exactly as the prefill kernel's MFMA
+ * tiles produce them (same code path, scores dumped instead of softmaxed).
+ *   scores int32 [B,Hq,M,N]. No reference counterpart (the reference never
+ *   exposes its dp4a accumulators); used to prove bit-exact int32 QK^T. */
+int sl8_attn_int8_qk_scores(const int8_t* q, const int8_t* k, int32_t* scores,
+                            int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N,
+                            int64_t D, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Full W8A8 prefill: int8 QK^T and int8 PV (P re-quantised in-loop, per row
+ * or per 32-key half), V int8 with per-channel scale, output fp16.
+ * Replaces _C.attn_w8a8_fwd (reference csrc/fni8_api.cpp:30-33,249-255,
+ * csrc/kernel/attn_w8a8_fwd.cu:76-165, csrc/include/attn_w8a8_fwd.cuh:30-444).
+ *   v int8 [B,Hkv,N,D], v_scale fp32 [B,Hkv,D], causal_diag: query i sees
+ *   keys <= i + causal_diag when causal. D in {64, 128, 256}.
+ * ---------------------------------------------------------------------- */
+size_t sl8_attn_w8a8_fwd_workspace(int64_t B, int64_t Hkv, int64_t N, int64_t D);
+int sl8_attn_w8a8_fwd(const int8_t* q, const float* q_scale, const int8_t* k,
+                      const float* k_scale, const int8_t* v, const float* v_scale,
+                      void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t M,
+                      int64_t N, int64_t D, int causal, int64_t causal_diag,
+                      int per_warp_quant, void* workspace, size_t workspace_bytes,
+                      void* stream);
+
+/* ------------------------------------------------------------------------
+ * Split-KV decode (M = 1): int8 K with per-token fp32 scales, fp16 V,
+ * per-split partials (O, m, l) merged by log-sum-exp, output fp16.
+ * Replaces _C.attn_int8_decode (reference csrc/fni8_api.cpp:34-36,260-263,
+ * csrc/kernel/attn_decode.cu:33-53,163-240, csrc/include/attn_decode.cuh:47-132,430-466).
+ *   q int8 [B,Hq,1,D], q_scale fp32 [B,Hq] (folded), k int8 [B,Hkv,N,D],
+ *   k_scale fp32 [B,Hkv,N], v fp16 [B,Hkv,N,D] -> out fp16 [B,Hq,1,D].
+ *   num_splits: -1 = auto (sl8_choose_num_splits), else 1..256.
+ *   D in {64, 128, 256}. workspace: sl8_attn_int8_decode_workspace() bytes.
+ * ---------------------------------------------------------------------- */
+int sl8_choose_num_splits(int64_t N, int64_t B, int64_t Hkv);
+size_t sl8_attn_int8_decode_workspace(int64_t B, int64_t Hq, int64_t D, int64_t num_splits);
+int sl8_attn_int8_decode(const int8_t* q, const float* q_scale, const int8_t* k,
+                         const float* k_scale, const void* v, void* out, int64_t B,
+                         int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                         int64_t num_splits, void* workspace, size_t workspace_bytes,
+                         void* stream);
+
+/* ------------------------------------------------------------------------
+ * Q4_K GEMM/GEMV over native GGUF super-blocks (144 B per 256 weights:
+ * fp16 d, fp16 dmin, 12 B packed 6-bit sub-scales/mins, 128 B nibbles).
+ *   y[m,n] = x_scale[m] * sum_j (d*sc_j*<x_j,q_j> - dmin*m_j*sum(x_j))
+ *   x int8 [M,K] (K % 256 == 0), x_scale fp32 [M], w uint8 [N, K/256*144],
+ *   out [M,N] out_dtype (f16 / bf16 as the reference; f32 also accepted).
+ * sl8_gemm_decode_q4k replaces _C.gemm_decode_q4k (reference
+ * csrc/fni8_api.cpp:346-352, csrc/kernel/gemm_decode_dp4a.cu:375-436,
+ * csrc/include/gemm_decode_dp4a.cuh:476-537); M <= 16.
+ * sl8_gemm_q4k replaces _C.gemm_q4k (reference csrc/fni8_api.cpp:331-337,
+ * csrc/kernel/gemm_dp4a.cu:146-193, csrc/include/gemm_q4k_dp4a.cuh:60-199); any M.
+ * ---------------------------------------------------------------------- */
+int sl8_gemm_decode_q4k(const int8_t* x, const float* x_scale, const uint8_t* w,
+                        void* out, int out_dtype, int64_t M, int64_t N, int64_t K,
+                        void* stream);
+int sl8_gemm_q4k(const int8_t* x, const float* x_scale, const uint8_t* w, void* out,
+                 int out_dtype, int64_t M, int64_t N, int64_t K, void* stream);
+
+/* Dequantise native Q4_K bytes to fp32 [N,K]: w = fp32(d)*sc*q - fp32(dmin)*m
+ * (exact in fp32). Reference math: csrc/include/gemm_q4k_dp4a.cuh:35-51 and
+ * the test decoder tests/test_gemm_q4k.py:132-148. */
+int sl8_dequant_q4k(const uint8_t* w, float* out, int64_t N, int64_t K, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SUPERL8_HIP_H */

@@ -1,0 +1,167 @@
+"""INT8 attention: prefill, W8A8 prefill and split-KV decode (numpy restatement).
+
+Reference kernels restated:
+  csrc/include/attn_int8_fwd.cuh:72-208  (GQA head map, bottom-right causal,
+      window, exp2-domain logits acc*q_scale*k_scale, online softmax, O/l,
+      l == 0 -> 0, LSE = m*ln2 + ln l)
+  csrc/include/attn_w8a8_fwd.cuh:96-224  (64-key tiles, P re-quantised per row
+      or per 32-key half: p_scale = max(pmax*(1/127), 2e-38), int8 PV,
+      dequant p_scale * v_scale[d])
+  csrc/include/attn_decode.cuh:47-132,430-466 (split s owns keys
+      [s*per, min(N,(s+1)*per)), per = ceil(N/ns); partial (O, m, l);
+      empty split -> m = -1e30; LSE merge)
+
+Softmax and PV are evaluated in float64 here (the reference keeps fp32 state);
+the kernels are checked against this within stated tolerances, while the
+int32 Q.K^T scores are checked bit-exactly.
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+LN2 = math.log(2.0)
+DEC_NEG_INF = -1e30
+
+
+def kv_head_index(Hq: int, Hkv: int) -> np.ndarray:
+    """Query head h reads K/V head h // (Hq/Hkv) (reference attn_int8_fwd.cuh:72)."""
+    return np.arange(Hq) // (Hq // Hkv)
+
+
+def scores_i32(q_i8: np.ndarray, k_i8: np.ndarray) -> np.ndarray:
+    """Exact int32 Q.K^T [B,Hq,M,N] (float64 products of int8 are exact)."""
+    kk = k_i8[:, kv_head_index(q_i8.shape[1], k_i8.shape[1])]
+    s = np.matmul(q_i8.astype(np.float64), np.swapaxes(kk.astype(np.float64), -1, -2))
+    return s.astype(np.int64).astype(np.int32)
+
+
+def logits(acc: np.ndarray, q_scale: np.ndarray, k_scale: np.ndarray, Hq: int) -> np.ndarray:
+    """fp32 exp2-domain logits ((float)acc * qs) * ks, as the reference evaluates them."""
+    ks = k_scale[:, kv_head_index(Hq, k_scale.shape[1])]
+    t = (acc.astype(np.float32) * q_scale[..., :, None].astype(np.float32)).astype(np.float32)
+    return (t * ks[..., None, :].astype(np.float32)).astype(np.float32)
+
+
+def valid_mask(M: int, N: int, causal: bool, window_left: int = -1,
+               causal_diag: int | None = None) -> np.ndarray:
+    """[M,N] bool. Query i sits at key position i + (N - M) when causal."""
+    diag = (N - M if causal_diag is None else causal_diag) if causal else 0
+    i = np.arange(M)[:, None] + diag
+    j = np.arange(N)[None, :]
+    ok = np.ones((M, N), bool)
+    if causal:
+        ok &= j <= i
+    if window_left >= 0:
+        ok &= j > i - window_left
+    return ok
+
+
+def attn_int8_fwd(q_i8, q_scale, k_i8, k_scale, v, causal=False, window_left=-1):
+    """Prefill output [B,Hq,M,D] float64 and natural-log LSE [B,Hq,M].
+
+    v: fp32 values of the fp16/bf16 V [B,Hkv,N,D].
+    """
+    B, Hq, M, D = q_i8.shape
+    N = k_i8.shape[2]
+    s = logits(scores_i32(q_i8, k_i8), q_scale, k_scale, Hq).astype(np.float64)
+    ok = valid_mask(M, N, causal, window_left)
+    s = np.where(ok, s, -np.inf)
+    m = s.max(axis=-1, keepdims=True) if N else np.full((B, Hq, M, 1), -np.inf)
+    live = np.isfinite(m)
+    p = np.where(live, np.exp2(s - np.where(live, m, 0.0)), 0.0)
+    l = p.sum(-1, keepdims=True)
+    vv = v[:, kv_head_index(Hq, v.shape[1])].astype(np.float64)
+    o = np.matmul(p, vv)
+    out = np.where(l > 0, o / np.where(l > 0, l, 1.0), 0.0)
+    with np.errstate(divide="ignore"):
+        lse = np.where(l[..., 0] > 0, m[..., 0] * LN2 + np.log(np.where(l[..., 0] > 0, l[..., 0], 1.0)),
+                       -np.inf)
+    return out, lse
+
+
+def attn_w8a8_fwd(q_i8, q_scale, k_i8, k_scale, v_i8, v_scale, causal=False, causal_diag=0,
+                  per_warp_quant=True, block_n=64):
+    """W8A8 prefill with the reference's in-loop P requantisation, float64 state otherwise."""
+    B, Hq, M, D = q_i8.shape
+    N = k_i8.shape[2]
+    kvh = kv_head_index(Hq, k_i8.shape[1])
+    s_all = logits(scores_i32(q_i8, k_i8), q_scale, k_scale, Hq)
+    ok = valid_mask(M, N, causal, -1, causal_diag if causal else 0)
+    s_all = np.where(ok, s_all, np.float32(-np.inf))
+    vq = v_i8[:, kvh].astype(np.float64)            # [B,Hq,N,D]
+    vs = v_scale[:, kvh].astype(np.float64)         # [B,Hq,D]
+    o = np.zeros((B, Hq, M, D))
+    m_i = np.full((B, Hq, M), -np.inf)
+    l_i = np.zeros((B, Hq, M))
+    half = block_n // 2
+    for n0 in range(0, N, block_n):
+        s = s_all[..., n0:n0 + block_n]
+        nb = s.shape[-1]
+        tmax = s.max(-1).astype(np.float64)
+        m_new = np.maximum(m_i, tmax)
+        alive = np.isfinite(m_new)
+        with np.errstate(invalid="ignore"):
+            p = np.where(np.isfinite(s) & alive[..., None],
+                         np.exp2(s.astype(np.float64) - np.where(alive, m_new, 0)[..., None]), 0.0)
+        p32 = p.astype(np.float32)
+        acc = np.zeros((B, Hq, M, D))
+        for h0 in range(0, nb, half if per_warp_quant else block_n):
+            h1 = min(nb, h0 + (half if per_warp_quant else block_n))
+            pm = p32[..., h0:h1].max(-1)
+            ps = np.maximum((pm * np.float32(1.0 / 127.0)).astype(np.float32), np.float32(2e-38))
+            inv = (np.float32(1.0) / ps).astype(np.float32)
+            pq = np.rint((p32[..., h0:h1] * inv[..., None]).astype(np.float32))
+            acc += np.matmul(pq.astype(np.float64), vq[..., n0 + h0:n0 + h1, :]) * ps[..., None]
+        with np.errstate(invalid="ignore"):
+            resc = np.where(np.isfinite(m_i) & alive, np.exp2(m_i - np.where(alive, m_new, 0)), 1.0)
+        o = o * resc[..., None] + np.where(alive[..., None], acc * vs[:, :, None, :], 0.0)
+        l_i = l_i * resc + p.sum(-1)
+        m_i = np.maximum(m_i, m_new)
+    return np.where(l_i[..., None] > 0, o / np.where(l_i > 0, l_i, 1.0)[..., None], 0.0)
+
+
+def attn_int8_decode(q_i8, q_scale, k_i8, k_scale, v, num_splits):
+    """Split-KV decode: q_i8 [B,Hq,D], q_scale [B,Hq] -> out [B,Hq,D] float64,
+    via per-split partials and the LSE merge (reference attn_decode.cuh:68-71,129,430-466)."""
+    B, Hq, D = q_i8.shape
+    N = k_i8.shape[2]
+    s_all = logits(scores_i32(q_i8[:, :, None, :], k_i8), q_scale[..., None], k_scale, Hq)[:, :, 0, :]
+    vv = v[:, kv_head_index(Hq, v.shape[1])].astype(np.float64)
+    per = (N + num_splits - 1) // num_splits
+    parts = []
+    for sp in range(num_splits):
+        n0, n1 = sp * per, min(N, (sp + 1) * per)
+        if n1 <= n0:
+            parts.append((np.zeros((B, Hq, D)), np.full((B, Hq), DEC_NEG_INF), np.zeros((B, Hq))))
+            continue
+        s = s_all[..., n0:n1].astype(np.float64)
+        m = s.max(-1)
+        p = np.exp2(s - m[..., None])
+        parts.append((np.einsum("bhn,bhnd->bhd", p, vv[:, :, n0:n1]), m, p.sum(-1)))
+    gm = np.max([pm for _, pm, _ in parts], axis=0)
+    num = np.zeros((B, Hq, D))
+    den = np.zeros((B, Hq))
+    for o, m, l in parts:
+        w = np.where(m == DEC_NEG_INF, 0.0, np.exp2(m - gm))
+        num += o * w[..., None]
+        den += l * w
+    return np.where(den[..., None] > 0, num / np.where(den > 0, den, 1.0)[..., None], 0.0)
+
+
+def attention_fp64(q, k, v, causal=False, scale=None):
+    """Textbook softmax attention in float64 on real-valued q [B,Hq,M,D], k, v [B,Hkv,N,D]."""
+    B, Hq, M, D = q.shape
+    N = k.shape[2]
+    idx = kv_head_index(Hq, k.shape[1])
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    s = np.matmul(q.astype(np.float64), np.swapaxes(k[:, idx].astype(np.float64), -1, -2)) * scale
+    if causal:
+        s = np.where(valid_mask(M, N, True), s, -np.inf)
+    s = s - s.max(-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(-1, keepdims=True)
+    return np.matmul(p, v[:, idx].astype(np.float64))

@@ -1,0 +1,296 @@
+"""`superl8._C` operator surface, served by libsuperl8_hip.so through its C ABI.
+
+Each function keeps the name, positional/keyword signature, output
+allocation and argument checks of the reference pybind11 binding it replaces
+(reference csrc/fni8_api.cpp). Outputs and scratch are allocated here with
+torch (the caching allocator); the kernels are enqueued on torch's current
+stream of the input's device. Error messages keep the reference's key
+phrases, and every failure raises RuntimeError.
+
+There is no CPU implementation: a non-GPU tensor is rejected, exactly like the
+reference's "must be CUDA tensors" checks.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+from ._lib import call, dtype_code, stream_of
+
+_HEAD_DIMS_FWD = (64, 128)
+_HEAD_DIMS_W8A8 = (64, 128, 256)
+_HEAD_DIMS_DECODE = (64, 128, 256)
+DEC_MAX_SPLITS = 256
+DEC_MAX_M = 16
+Q4K_TYPE_SIZE = 144
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(f"fni8: {msg}")
+
+
+def _on_gpu(*ts: torch.Tensor) -> None:
+    _check(all(t.is_cuda for t in ts), "all inputs (incl. scales) must be CUDA tensors")
+    dev = ts[0].device
+    _check(all(t.device == dev for t in ts), "all inputs must be on the same device")
+
+
+def _contig(*ts: torch.Tensor) -> None:
+    _check(all(t.is_contiguous() for t in ts), "inputs must be contiguous")
+
+
+# ---------------------------------------------------------------------------
+# quantisation (reference csrc/kernel/quant_rowwise.cu:84-121)
+# ---------------------------------------------------------------------------
+def quantize_i8_rowwise(x: torch.Tensor):
+    """x[M,K] fp16/bf16/fp32 -> (q int8 [M,K], scale fp32 [M])."""
+    _check(x.is_cuda, "quantize_i8_rowwise expects a CUDA tensor")
+    _check(x.dim() == 2, f"expect x[M,K], got dim={x.dim()}")
+    _check(x.dtype in (torch.float16, torch.bfloat16, torch.float32),
+           "quantize_i8_rowwise input must be float16/bfloat16/float32")
+    x = x.contiguous()
+    M, K = x.shape
+    q = torch.empty((M, K), device=x.device, dtype=torch.int8)
+    scale = torch.empty((M,), device=x.device, dtype=torch.float32)
+    if M and K:
+        with torch.cuda.device(x.device):
+            call("sl8_quantize_i8_rowwise", x.data_ptr(), dtype_code(x.dtype), M, K,
+                 q.data_ptr(), scale.data_ptr(), stream_of(x))
+    return q, scale
+
+
+def k_mean(k: torch.Tensor) -> torch.Tensor:
+    """fp32 mean over the key axis of k[..., N, D] -> [..., 1, D] (order-independent)."""
+    _check(k.is_cuda, "k_mean expects a CUDA tensor")
+    _check(k.dtype in (torch.float16, torch.bfloat16, torch.float32),
+           "k_mean input must be float16/bfloat16/float32")
+    k = k.contiguous()
+    *lead, N, D = k.shape
+    G = math.prod(lead)
+    mean = torch.empty((*lead, 1, D), device=k.device, dtype=torch.float32)
+    if G and D:
+        with torch.cuda.device(k.device):
+            call("sl8_k_mean", k.data_ptr(), dtype_code(k.dtype), G, N, D, mean.data_ptr(),
+                 stream_of(k))
+    return mean
+
+
+def quantize_rows_centered(x: torch.Tensor, mean: torch.Tensor | None, scale_mul: float = 1.0):
+    """Fused smooth + per-row int8 of x[..., N, D]: rows of group g have
+    mean[g] subtracted (rounded back to x's dtype) before quantising; the
+    returned scale [..., N] is multiplied by fp32(scale_mul)."""
+    _check(x.is_cuda, "quantize expects a CUDA tensor")
+    _check(x.dtype in (torch.float16, torch.bfloat16, torch.float32),
+           "quantize input must be float16/bfloat16/float32")
+    x = x.contiguous()
+    *lead, N, D = x.shape
+    G = math.prod(lead)
+    if mean is not None:
+        mean = mean.to(torch.float32).contiguous()
+        _check(mean.numel() == G * D, "mean shape mismatch")
+    q = torch.empty(x.shape, device=x.device, dtype=torch.int8)
+    scale = torch.empty((*lead, N), device=x.device, dtype=torch.float32)
+    if G and N and D:
+        with torch.cuda.device(x.device):
+            call("sl8_quantize_i8_rows_centered", x.data_ptr(), dtype_code(x.dtype), G, N, D,
+                 None if mean is None else mean.data_ptr(), float(scale_mul), q.data_ptr(),
+                 scale.data_ptr(), stream_of(x))
+    return q, scale
+
+
+# ---------------------------------------------------------------------------
+# prefill attention (reference csrc/kernel/attn_int8_fwd.cu:101-200)
+# ---------------------------------------------------------------------------
+def _fwd_checks(q, q_scale, k, k_scale, v):
+    _on_gpu(q, q_scale, k, k_scale, v)
+    _check(q.dtype == torch.int8 and k.dtype == torch.int8, "q/k must be int8")
+    _check(q_scale.dtype == torch.float32 and k_scale.dtype == torch.float32,
+           "scales must be float32")
+    _check(q.dim() == 4 and k.dim() == 4 and v.dim() == 4, "expect [B,H,S,D]")
+    _contig(q, q_scale, k, k_scale, v)
+    _check(q.data_ptr() % 4 == 0 and k.data_ptr() % 4 == 0,
+           "q/k must be 4-byte aligned for int32 loads")
+    B, H, M, D = q.shape
+    N, Hkv = k.shape[2], k.shape[1]
+    _check(k.shape[0] == B and v.shape[0] == B and v.shape[1] == Hkv, "batch/head mismatch")
+    _check(Hkv > 0 and H % Hkv == 0, "H_q must be divisible by H_kv (GQA)")
+    _check(k.shape[3] == D and v.shape[3] == D and v.shape[2] == N, "K/V shape mismatch")
+    return B, H, Hkv, M, N, D
+
+
+def _attn_fwd(q, q_scale, k, k_scale, v, causal, window_left, want_lse):
+    B, H, Hkv, M, N, D = _fwd_checks(q, q_scale, k, k_scale, v)
+    _check(v.dtype in (torch.float16, torch.bfloat16), "v must be float16 or bfloat16")
+    _check(q_scale.numel() == B * H * M and k_scale.numel() == B * Hkv * N, "scale shape mismatch")
+    _check(D in _HEAD_DIMS_FWD, f"head dim must be one of {_HEAD_DIMS_FWD}, got {D}")
+    out = torch.empty((B, H, M, D), device=v.device, dtype=v.dtype)
+    lse = torch.empty((B, H, M) if want_lse else (0,), device=q.device, dtype=torch.float32)
+    if M == 0 or B == 0 or H == 0:
+        return out, lse
+    ws_bytes = _lib.load().sl8_attn_int8_fwd_workspace(B, Hkv, N, D)
+    ws = torch.empty((max(ws_bytes, 1),), device=q.device, dtype=torch.uint8)
+    with torch.cuda.device(q.device):
+        call("sl8_attn_int8_fwd", q.data_ptr(), q_scale.data_ptr(), k.data_ptr(),
+             k_scale.data_ptr(), v.data_ptr(), dtype_code(v.dtype), out.data_ptr(),
+             lse.data_ptr() if want_lse else None, B, H, Hkv, M, N, D, int(bool(causal)),
+             int(window_left), ws.data_ptr(), ws_bytes, stream_of(q))
+    return out, lse
+
+
+def attn_int8_fwd(q, q_scale, k, k_scale, v, causal=False, window_left=-1):
+    """q int8 [B,Hq,M,D], q_scale fp32 [B,Hq,M] (folded), k int8 [B,Hkv,N,D],
+    k_scale fp32 [B,Hkv,N], v fp16/bf16 [B,Hkv,N,D] -> out [B,Hq,M,D] (v's dtype)."""
+    return _attn_fwd(q, q_scale, k, k_scale, v, causal, window_left, False)[0]
+
+
+def attn_int8_fwd_train(q, q_scale, k, k_scale, v, causal=False):
+    """Same forward, also returns the natural-log LSE fp32 [B,Hq,M]."""
+    return _attn_fwd(q, q_scale, k, k_scale, v, causal, -1, True)
+
+
+def attn_int8_qk_scores(q, k):
+    """int32 Q.K^T [B,Hq,M,N] straight from the prefill kernel's MFMA tiles (test hook)."""
+    _on_gpu(q, k)
+    _check(q.dtype == torch.int8 and k.dtype == torch.int8, "q/k must be int8")
+    _contig(q, k)
+    B, H, M, D = q.shape
+    Hkv, N = k.shape[1], k.shape[2]
+    _check(H % Hkv == 0 and k.shape[3] == D and k.shape[0] == B, "q/k shape mismatch")
+    _check(D in _HEAD_DIMS_FWD, f"head dim must be one of {_HEAD_DIMS_FWD}, got {D}")
+    s = torch.empty((B, H, M, N), device=q.device, dtype=torch.int32)
+    if s.numel():
+        with torch.cuda.device(q.device):
+            call("sl8_attn_int8_qk_scores", q.data_ptr(), k.data_ptr(), s.data_ptr(), B, H, Hkv,
+                 M, N, D, stream_of(q))
+    return s
+
+
+# ---------------------------------------------------------------------------
+# W8A8 prefill (reference csrc/kernel/attn_w8a8_fwd.cu:76-165)
+# ---------------------------------------------------------------------------
+def attn_w8a8_fwd(q, q_scale, k, k_scale, v, v_scale, causal=False, causal_diag=0,
+                  per_warp_quant=True):
+    """int8 QK^T + int8 PV; v int8 [B,Hkv,N,D], v_scale fp32 [B,Hkv,D] -> fp16 out."""
+    _on_gpu(v_scale)
+    B, H, Hkv, M, N, D = _fwd_checks(q, q_scale, k, k_scale, v)
+    _check(v.dtype == torch.int8, "q/k/v must be int8")
+    _check(v_scale.dtype == torch.float32, "scales must be float32")
+    _contig(v_scale)
+    _check(q_scale.numel() == B * H * M and k_scale.numel() == B * Hkv * N
+           and v_scale.numel() == B * Hkv * D, "scale shape mismatch")
+    _check(D in _HEAD_DIMS_W8A8, f"head dim must be one of {_HEAD_DIMS_W8A8}, got {D}")
+    out = torch.empty((B, H, M, D), device=q.device, dtype=torch.float16)
+    if M == 0 or B == 0 or H == 0:
+        return out
+    ws_bytes = _lib.load().sl8_attn_w8a8_fwd_workspace(B, Hkv, N, D)
+    ws = torch.empty((max(ws_bytes, 1),), device=q.device, dtype=torch.uint8)
+    with torch.cuda.device(q.device):
+        call("sl8_attn_w8a8_fwd", q.data_ptr(), q_scale.data_ptr(), k.data_ptr(),
+             k_scale.data_ptr(), v.data_ptr(), v_scale.data_ptr(), out.data_ptr(), B, H, Hkv, M,
+             N, D, int(bool(causal)), int(causal_diag), int(bool(per_warp_quant)),
+             ws.data_ptr(), ws_bytes, stream_of(q))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# split-KV decode (reference csrc/kernel/attn_decode.cu:163-240)
+# ---------------------------------------------------------------------------
+def choose_n_splits(n_len: int, batch: int, h_kv: int) -> int:
+    return int(_lib.load().sl8_choose_num_splits(n_len, batch, h_kv))
+
+
+def attn_int8_decode(q, q_scale, k, k_scale, v, num_splits=-1):
+    """q int8 [B,Hq,1,D], q_scale fp32 [B,Hq,1], k int8 [B,Hkv,N,D], k_scale fp32
+    [B,Hkv,N], v fp16 [B,Hkv,N,D] -> fp16 [B,Hq,1,D]."""
+    _on_gpu(q, q_scale, k, k_scale, v)
+    _check(q.dtype == torch.int8 and k.dtype == torch.int8, "decode: q/k must be int8")
+    _check(q_scale.dtype == torch.float32 and k_scale.dtype == torch.float32,
+           "decode: scales must be float32")
+    _check(v.dtype == torch.float16, "decode: v must be float16")
+    _check(q.dim() == 4 and k.dim() == 4 and v.dim() == 4, "decode: expect [B,H,S,D]")
+    _check(q.shape[2] == 1, "decode: query length M must be 1 (decode)")
+    _contig(q, q_scale, k, k_scale, v)
+    B, H, _, D = q.shape
+    Hkv, N = k.shape[1], k.shape[2]
+    _check(k.shape[0] == B and v.shape[0] == B and v.shape[1] == Hkv, "decode: batch/head mismatch")
+    _check(Hkv > 0 and H % Hkv == 0, "decode: H_q must be divisible by H_kv (GQA)")
+    _check(k.shape[3] == D and v.shape[3] == D and v.shape[2] == N, "decode: K/V shape mismatch")
+    _check(q_scale.numel() == B * H and k_scale.numel() == B * Hkv * N,
+           "decode: scale shape mismatch")
+    _check(D in _HEAD_DIMS_DECODE, f"decode: head dim must be one of {_HEAD_DIMS_DECODE}, got {D}")
+    num_splits = int(num_splits)
+    _check(num_splits != 0, f"decode: num_splits=0 is invalid; use -1 for auto or 1..{DEC_MAX_SPLITS}")
+    out = torch.empty((B, H, 1, D), device=v.device, dtype=torch.float16)
+    if B == 0 or H == 0:
+        return out
+    if N == 0:
+        return out.zero_()
+    ns = choose_n_splits(N, B, Hkv) if num_splits < 0 else num_splits
+    _check(1 <= ns <= DEC_MAX_SPLITS, f"decode: num_splits must be 1..{DEC_MAX_SPLITS}, got {ns}")
+    ws_bytes = _lib.load().sl8_attn_int8_decode_workspace(B, H, D, ns)
+    ws = torch.empty((ws_bytes,), device=q.device, dtype=torch.uint8)
+    with torch.cuda.device(q.device):
+        call("sl8_attn_int8_decode", q.data_ptr(), q_scale.data_ptr(), k.data_ptr(),
+             k_scale.data_ptr(), v.data_ptr(), out.data_ptr(), B, H, Hkv, N, D, ns,
+             ws.data_ptr(), ws_bytes, stream_of(q))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Q4_K (reference csrc/kernel/gemm_dp4a.cu:146-193, gemm_decode_dp4a.cu:375-436)
+# ---------------------------------------------------------------------------
+def _q4k_checks(x, x_scale, w, out_dtype, tag):
+    _on_gpu(x, x_scale, w)
+    _check(x.dtype == torch.int8, "x must be int8")
+    _check(w.dtype == torch.uint8, f"w must be uint8 (native {tag} bytes)")
+    _check(x_scale.dtype == torch.float32, "x_scale must be float32")
+    _check(x.dim() == 2 and w.dim() == 2, "expect x[M,K] and w[N,(K/256)*144]")
+    _contig(x, x_scale, w)
+    _check(out_dtype in (torch.float16, torch.bfloat16, torch.float32),
+           f"out_dtype must be float16 or bfloat16, got {out_dtype}")
+    M, K = x.shape
+    N = w.shape[0]
+    _check(K % 256 == 0, f"Q4_K contraction dim K must be %256==0, got {K}")
+    _check(w.shape[1] == (K // 256) * Q4K_TYPE_SIZE,
+           f"Q4_K weight must be [N, (K/256)*144], got [{N},{w.shape[1]}] for K={K}")
+    _check(x_scale.numel() == M, "x_scale must be [M]")
+    return M, N, K
+
+
+def _q4k(sym, x, x_scale, w, out_dtype):
+    M, N, K = _q4k_checks(x, x_scale, w, out_dtype, "Q4_K")
+    out = torch.empty((M, N), device=x.device, dtype=out_dtype)
+    if M and N:
+        with torch.cuda.device(x.device):
+            call(sym, x.data_ptr(), x_scale.data_ptr(), w.data_ptr(), out.data_ptr(),
+                 dtype_code(out_dtype), M, N, K, stream_of(x))
+    return out
+
+
+def gemm_q4k(x, x_scale, w, out_dtype=torch.float16):
+    """x int8 [M,K], x_scale fp32 [M], w uint8 [N,(K/256)*144] -> [M,N] out_dtype."""
+    return _q4k("sl8_gemm_q4k", x, x_scale, w, out_dtype)
+
+
+def gemm_decode_q4k(x, x_scale, w, out_dtype=torch.float16):
+    """Decode-shape (M <= 16) Q4_K GEMV; same math as gemm_q4k."""
+    _check(x.dim() == 2 and x.shape[0] <= DEC_MAX_M,
+           f"gemm_decode_q4k supports M<={DEC_MAX_M}, got M={x.shape[0] if x.dim() else 0}"
+           " -- use the tile gemm_q4k for prefill")
+    return _q4k("sl8_gemm_decode_q4k", x, x_scale, w, out_dtype)
+
+
+def dequant_q4k(w: torch.Tensor, K: int) -> torch.Tensor:
+    """Native Q4_K bytes [N,(K/256)*144] -> fp32 [N,K] (exact)."""
+    _on_gpu(w)
+    _check(w.dtype == torch.uint8 and w.dim() == 2, "w must be uint8 [N,(K/256)*144]")
+    _check(K % 256 == 0 and w.shape[1] == (K // 256) * Q4K_TYPE_SIZE, "Q4_K weight/K mismatch")
+    w = w.contiguous()
+    out = torch.empty((w.shape[0], K), device=w.device, dtype=torch.float32)
+    if out.numel():
+        with torch.cuda.device(w.device):
+            call("sl8_dequant_q4k", w.data_ptr(), out.data_ptr(), w.shape[0], K, stream_of(w))
+    return out

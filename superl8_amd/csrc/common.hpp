@@ -1,0 +1,91 @@
+// Shared helpers for the gfx950 kernels and the C-ABI entry points.
+//
+// Every entry point returns an sl8 status code (0 = ok) and records a message
+// readable through sl8_last_error(); nothing throws across the C boundary.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <hip/hip_bfloat16.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+
+#include "../../include/superl8_hip.h"
+
+namespace sl8 {
+
+// Last-error slot (per host thread).
+void set_error(const char* fmt, ...);
+void clear_error();
+
+#define SL8_CHECK_ARG(cond, ...)                 \
+  do {                                           \
+    if (!(cond)) {                               \
+      ::sl8::set_error(__VA_ARGS__);             \
+      return SL8_ERR_INVALID;                    \
+    }                                            \
+  } while (0)
+
+#define SL8_CHECK_LAUNCH(what)                                                  \
+  do {                                                                          \
+    hipError_t e_ = hipGetLastError();                                          \
+    if (e_ != hipSuccess) {                                                     \
+      ::sl8::set_error("%s: kernel launch failed: %s", what, hipGetErrorString(e_)); \
+      return SL8_ERR_LAUNCH;                                                    \
+    }                                                                           \
+  } while (0)
+
+inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// ---- scalar conversions (round-to-nearest-even everywhere) ----
+__device__ __forceinline__ float ld_f(const __half* p) { return __half2float(*p); }
+__device__ __forceinline__ float ld_f(const hip_bfloat16* p) { return static_cast<float>(*p); }
+__device__ __forceinline__ float ld_f(const float* p) { return *p; }
+
+__device__ __forceinline__ float h2f(uint16_t bits) {
+  return __half2float(__ushort_as_half(bits));
+}
+__device__ __forceinline__ float bf2f(uint16_t bits) {
+  return __uint_as_float(static_cast<uint32_t>(bits) << 16);
+}
+// fp32 -> bf16 bits, round-to-nearest-even (NaN kept quiet).
+__device__ __forceinline__ uint16_t f2bf_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+__device__ __forceinline__ uint16_t f2h_bits(float f) { return __half_as_ushort(__float2half_rn(f)); }
+
+// Typed store of one fp32 value as fp16 / bf16 / fp32.
+template <int DT> __device__ __forceinline__ void st_out(void* base, int64_t i, float v);
+template <> __device__ __forceinline__ void st_out<SL8_DTYPE_F16>(void* b, int64_t i, float v) {
+  reinterpret_cast<uint16_t*>(b)[i] = f2h_bits(v);
+}
+template <> __device__ __forceinline__ void st_out<SL8_DTYPE_BF16>(void* b, int64_t i, float v) {
+  reinterpret_cast<uint16_t*>(b)[i] = f2bf_bits(v);
+}
+template <> __device__ __forceinline__ void st_out<SL8_DTYPE_F32>(void* b, int64_t i, float v) {
+  reinterpret_cast<float*>(b)[i] = v;
+}
+
+// 16-bit storage element -> fp32 for fp16 / bf16.
+template <int DT> __device__ __forceinline__ float u16_to_f(uint16_t b);
+template <> __device__ __forceinline__ float u16_to_f<SL8_DTYPE_F16>(uint16_t b) { return h2f(b); }
+template <> __device__ __forceinline__ float u16_to_f<SL8_DTYPE_BF16>(uint16_t b) { return bf2f(b); }
+
+// Wave64 reductions (DPP/bpermute chosen by the compiler from __shfl_xor).
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+}  // namespace sl8

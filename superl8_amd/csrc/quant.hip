@@ -1,0 +1,252 @@
+// Per-row symmetric int8 quantisation and K-smoothing for gfx950.
+//
+// Numerics contract (reference csrc/include/quant_rowwise.cuh:33-91 and
+// superl8/quant/core.py:47-62,70-95):
+//   scale = amax|row| * fp32(1/127)   (reciprocal multiply, not division)
+//   safe  = scale == 0 ? 1 : scale
+//   q     = clamp(rint(x / safe), -127, 127)   with IEEE round-to-nearest
+//           division and round-half-to-even.
+// K-smoothing subtracts the fp32 per-channel key mean and rounds back to the
+// storage dtype before quantising, exactly as torch.sub(k, mean, out=k_s).
+//
+// Layout: one row is handled by LPR lanes of a wave64 (LPR in {16,32,64});
+// 256-thread blocks hold 256/LPR rows. Rows are read twice (amax pass, code
+// pass); the second read is served by L2 for the row sizes used here.
+
+#include "common.hpp"
+
+#include <cmath>
+#include <string>
+
+namespace sl8 {
+
+static thread_local std::string g_last_error;
+
+void set_error(const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+}
+void clear_error() { g_last_error.clear(); }
+
+namespace {
+
+constexpr int QTHREADS = 256;
+
+template <int DT> struct Elem;
+template <> struct Elem<SL8_DTYPE_F16> {
+  using T = uint16_t;
+  __device__ static float ld(const T* p, int64_t i) { return h2f(p[i]); }
+  __device__ static float round(float v) { return h2f(f2h_bits(v)); }
+};
+template <> struct Elem<SL8_DTYPE_BF16> {
+  using T = uint16_t;
+  __device__ static float ld(const T* p, int64_t i) { return bf2f(p[i]); }
+  __device__ static float round(float v) { return bf2f(f2bf_bits(v)); }
+};
+template <> struct Elem<SL8_DTYPE_F32> {
+  using T = float;
+  __device__ static float ld(const T* p, int64_t i) { return p[i]; }
+  __device__ static float round(float v) { return v; }
+};
+
+// Value of element d of a row after the optional mean shift.
+template <int DT, bool MEAN>
+__device__ __forceinline__ float row_val(const typename Elem<DT>::T* xr, const float* mr, int d) {
+  float v = Elem<DT>::ld(xr, d);
+  if constexpr (MEAN) v = Elem<DT>::round(v - mr[d]);
+  return v;
+}
+
+__device__ __forceinline__ int8_t code_of(float v, float safe) {
+  float r = rintf(__fdiv_rn(v, safe));
+  r = fminf(fmaxf(r, -127.f), 127.f);
+  return static_cast<int8_t>(r);
+}
+
+// rows = G*N; row r uses mean row r / rows_per_mean.
+template <int DT, int LPR, bool MEAN>
+__global__ void __launch_bounds__(QTHREADS)
+quant_rows_kernel(const typename Elem<DT>::T* __restrict__ x, const float* __restrict__ mean,
+                  int8_t* __restrict__ q, float* __restrict__ scale, int64_t rows,
+                  int64_t rows_per_mean, int K, float scale_mul) {
+  using T = typename Elem<DT>::T;
+  const int lane = threadIdx.x % LPR;
+  const int64_t row = (int64_t)blockIdx.x * (QTHREADS / LPR) + threadIdx.x / LPR;
+  const bool live = row < rows;
+  const int64_t r = live ? row : 0;
+  const T* xr = x + r * K;
+  const float* mr = MEAN ? mean + (r / rows_per_mean) * K : nullptr;
+
+  float amax = 0.f;
+  if (live) {
+    for (int d = lane; d < K; d += LPR) amax = fmaxf(amax, fabsf(row_val<DT, MEAN>(xr, mr, d)));
+  }
+#pragma unroll
+  for (int o = LPR / 2; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+  if (!live) return;
+
+  const float s = amax * (1.0f / 127.0f);
+  const float safe = (s == 0.f) ? 1.f : s;
+  if (lane == 0) scale[row] = safe * scale_mul;
+
+  int8_t* qr = q + r * K;
+  if ((K & 3) == 0) {
+    // 4 codes per 32-bit store.
+    for (int d = lane * 4; d < K; d += LPR * 4) {
+      uint32_t packed = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        packed |= (uint32_t)(uint8_t)code_of(row_val<DT, MEAN>(xr, mr, d + e), safe) << (8 * e);
+      *reinterpret_cast<uint32_t*>(qr + d) = packed;
+    }
+  } else {
+    for (int d = lane; d < K; d += LPR) qr[d] = code_of(row_val<DT, MEAN>(xr, mr, d), safe);
+  }
+}
+
+template <int DT, bool MEAN>
+int launch_quant(const void* x, const float* mean, int8_t* q, float* scale, int64_t rows,
+                 int64_t rows_per_mean, int64_t K, float scale_mul, hipStream_t st) {
+  using T = typename Elem<DT>::T;
+  const T* xp = static_cast<const T*>(x);
+  auto go = [&](auto lpr_tag) {
+    constexpr int LPR = decltype(lpr_tag)::value;
+    const int64_t rpb = QTHREADS / LPR;
+    const dim3 grid((unsigned)((rows + rpb - 1) / rpb));
+    quant_rows_kernel<DT, LPR, MEAN><<<grid, QTHREADS, 0, st>>>(xp, mean, q, scale, rows,
+                                                                rows_per_mean, (int)K, scale_mul);
+  };
+  if (K <= 128) go(std::integral_constant<int, 16>{});
+  else if (K <= 512) go(std::integral_constant<int, 32>{});
+  else go(std::integral_constant<int, 64>{});
+  SL8_CHECK_LAUNCH("quantize_i8_rowwise");
+  return SL8_OK;
+}
+
+int dispatch_quant(const void* x, int dt, const float* mean, int8_t* q, float* scale,
+                   int64_t rows, int64_t rows_per_mean, int64_t K, float scale_mul,
+                   hipStream_t st) {
+  if (mean) {
+    switch (dt) {
+      case SL8_DTYPE_F16: return launch_quant<SL8_DTYPE_F16, true>(x, mean, q, scale, rows, rows_per_mean, K, scale_mul, st);
+      case SL8_DTYPE_BF16: return launch_quant<SL8_DTYPE_BF16, true>(x, mean, q, scale, rows, rows_per_mean, K, scale_mul, st);
+      default: return launch_quant<SL8_DTYPE_F32, true>(x, mean, q, scale, rows, rows_per_mean, K, scale_mul, st);
+    }
+  }
+  switch (dt) {
+    case SL8_DTYPE_F16: return launch_quant<SL8_DTYPE_F16, false>(x, nullptr, q, scale, rows, 1, K, scale_mul, st);
+    case SL8_DTYPE_BF16: return launch_quant<SL8_DTYPE_BF16, false>(x, nullptr, q, scale, rows, 1, K, scale_mul, st);
+    default: return launch_quant<SL8_DTYPE_F32, false>(x, nullptr, q, scale, rows, 1, K, scale_mul, st);
+  }
+}
+
+// ---- K mean -------------------------------------------------------------
+// fp16: every value is an integer multiple of 2^-24 below 2^16 in magnitude,
+// so sum(x * 2^24) is an exact int64 for N < 2^23 rows: the mean does not
+// depend on summation order. Block = 64 columns x 16 row phases.
+constexpr int MEAN_COLS = 64;
+constexpr int MEAN_PHASES = 16;
+
+__global__ void __launch_bounds__(MEAN_COLS * MEAN_PHASES)
+k_mean_f16_kernel(const uint16_t* __restrict__ k, float* __restrict__ mean, int64_t N, int D) {
+  __shared__ long long part[MEAN_PHASES][MEAN_COLS];
+  const int col = threadIdx.x % MEAN_COLS;
+  const int ph = threadIdx.x / MEAN_COLS;
+  const int64_t g = blockIdx.y;
+  const int d = blockIdx.x * MEAN_COLS + col;
+  long long acc = 0;
+  if (d < D) {
+    const uint16_t* kg = k + g * N * D + d;
+    for (int64_t n = ph; n < N; n += MEAN_PHASES) {
+      const float v = h2f(kg[n * D]);
+      acc += (long long)ldexpf(v, 24);  // exact: |v| * 2^24 < 2^40, integral
+    }
+  }
+  part[ph][col] = acc;
+  __syncthreads();
+  if (ph == 0 && d < D) {
+    long long s = 0;
+#pragma unroll
+    for (int p = 0; p < MEAN_PHASES; ++p) s += part[p][col];
+    mean[g * D + d] = (float)(((double)s * 0x1p-24) / (double)N);
+  }
+}
+
+// bf16 / f32: fp64 running sum over rows in index order (one thread per column).
+template <int DT>
+__global__ void __launch_bounds__(MEAN_COLS)
+k_mean_seq_kernel(const typename Elem<DT>::T* __restrict__ k, float* __restrict__ mean,
+                  int64_t N, int D) {
+  const int64_t g = blockIdx.y;
+  const int d = blockIdx.x * MEAN_COLS + threadIdx.x;
+  if (d >= D) return;
+  const typename Elem<DT>::T* kg = k + g * N * D + d;
+  double s = 0.0;
+  for (int64_t n = 0; n < N; ++n) s += (double)Elem<DT>::ld(kg, n * D);
+  mean[g * D + d] = (float)(s / (double)N);
+}
+
+}  // namespace
+}  // namespace sl8
+
+using namespace sl8;
+
+extern "C" const char* sl8_last_error(void) { return g_last_error.c_str(); }
+extern "C" const char* sl8_version(void) { return "superl8-hip 0.1 gfx950"; }
+
+extern "C" int sl8_quantize_i8_rowwise(const void* x, int x_dtype, int64_t M, int64_t K,
+                                       int8_t* q, float* scale, void* stream) {
+  clear_error();
+  SL8_CHECK_ARG(x_dtype == SL8_DTYPE_F16 || x_dtype == SL8_DTYPE_BF16 || x_dtype == SL8_DTYPE_F32,
+                "quantize_i8_rowwise input must be float16/bfloat16/float32");
+  SL8_CHECK_ARG(M >= 0 && K >= 0 && K < (1LL << 31), "quantize_i8_rowwise: bad shape [%lld,%lld]",
+                (long long)M, (long long)K);
+  if (M == 0 || K == 0) return SL8_OK;
+  SL8_CHECK_ARG(x && q && scale, "quantize_i8_rowwise: null pointer");
+  SL8_CHECK_ARG((K & 3) != 0 || aligned(q, 4), "quantize_i8_rowwise: q must be 4-byte aligned");
+  return dispatch_quant(x, x_dtype, nullptr, q, scale, M, 1, K, 1.0f,
+                        static_cast<hipStream_t>(stream));
+}
+
+extern "C" int sl8_quantize_i8_rows_centered(const void* x, int x_dtype, int64_t G, int64_t N,
+                                             int64_t D, const float* mean, float scale_mul,
+                                             int8_t* q, float* scale, void* stream) {
+  clear_error();
+  SL8_CHECK_ARG(x_dtype == SL8_DTYPE_F16 || x_dtype == SL8_DTYPE_BF16 || x_dtype == SL8_DTYPE_F32,
+                "quantize: input must be float16/bfloat16/float32");
+  SL8_CHECK_ARG(G >= 0 && N >= 0 && D >= 0 && D < (1LL << 31), "quantize: bad shape");
+  if (G == 0 || N == 0 || D == 0) return SL8_OK;
+  SL8_CHECK_ARG(x && q && scale, "quantize: null pointer");
+  SL8_CHECK_ARG((D & 3) != 0 || aligned(q, 4), "quantize: q must be 4-byte aligned");
+  return dispatch_quant(x, x_dtype, mean, q, scale, G * N, N, D, scale_mul,
+                        static_cast<hipStream_t>(stream));
+}
+
+extern "C" int sl8_k_mean(const void* k, int dtype, int64_t G, int64_t N, int64_t D,
+                          float* mean, void* stream) {
+  clear_error();
+  SL8_CHECK_ARG(dtype == SL8_DTYPE_F16 || dtype == SL8_DTYPE_BF16 || dtype == SL8_DTYPE_F32,
+                "k_mean: input must be float16/bfloat16/float32");
+  SL8_CHECK_ARG(G >= 0 && N >= 0 && D >= 0 && D < (1LL << 31), "k_mean: bad shape");
+  SL8_CHECK_ARG(N < (1LL << 23), "k_mean: N must be < 2^23 keys, got %lld", (long long)N);
+  if (G == 0 || D == 0) return SL8_OK;
+  SL8_CHECK_ARG(N > 0, "k_mean: mean over zero keys");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)((D + MEAN_COLS - 1) / MEAN_COLS), (unsigned)G);
+  if (dtype == SL8_DTYPE_F16) {
+    k_mean_f16_kernel<<<grid, MEAN_COLS * MEAN_PHASES, 0, st>>>(
+        static_cast<const uint16_t*>(k), mean, N, (int)D);
+  } else if (dtype == SL8_DTYPE_BF16) {
+    k_mean_seq_kernel<SL8_DTYPE_BF16><<<grid, MEAN_COLS, 0, st>>>(
+        static_cast<const uint16_t*>(k), mean, N, (int)D);
+  } else {
+    k_mean_seq_kernel<SL8_DTYPE_F32><<<grid, MEAN_COLS, 0, st>>>(
+        static_cast<const float*>(k), mean, N, (int)D);
+  }
+  SL8_CHECK_LAUNCH("k_mean");
+  return SL8_OK;
+}

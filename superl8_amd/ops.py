@@ -1,0 +1,106 @@
+"""Public operators of the hot path, drop-in for superl8/ops.py of the reference.
+
+Same names, keyword arguments, routing and error behaviour as the reference
+wrappers (reference superl8/ops.py:70-175 attn_int8_fwd, :230-267
+attn_int8_decode, :975-991 quantize_i8_rowwise, :1254-1325 linear_q4k /
+_linear_kquant), dispatching to the gfx950 kernels through `_C`.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _C
+
+# Decode-shape M cap for the k-quant linear (reference ops.py:1289).
+_KQUANT_DECODE_MAX_M = 16
+
+
+def attn_int8_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool = False,
+                  scale: float | None = None, int8_pv: bool = False, rotate: bool = False,
+                  window_left: int = -1, per_warp_quant: bool = True,
+                  internal_accuracy_gate: bool = True) -> torch.Tensor:
+    """INT8-QK^T FlashAttention-2 prefill (MFMA), fp16/bf16 PV; ``int8_pv`` = full W8A8.
+
+    q, k, v: fp16/bf16 [B, H, S, D]. Q/K are quantised per row (K smoothed) in
+    the prologue; causal attention is bottom-right aligned; ``window_left>=0``
+    adds a left window (fp16-PV path only). With ``internal_accuracy_gate``,
+    a Q row whose max/median magnitude ratio exceeds 12 sends the whole call
+    to full-precision attention (reference ops.py:115-147).
+    """
+    from . import quant
+
+    if internal_accuracy_gate and quant.detect_q_outlier_domination(q):
+        import torch.nn.functional as F
+
+        s = (1.0 / math.sqrt(q.shape[-1])) if scale is None else scale
+        attn_mask = None
+        if causal and q.shape[-2] != k.shape[-2]:
+            m, n = q.shape[-2], k.shape[-2]
+            attn_mask = torch.ones(m, n, device=q.device, dtype=torch.bool).tril(n - m)
+        if window_left >= 0:
+            m, n = q.shape[-2], k.shape[-2]
+            i = torch.arange(m, device=q.device)[:, None] + (n - m)
+            j = torch.arange(n, device=q.device)[None, :]
+            attn_mask = (j <= i) & (j > i - window_left)
+        return F.scaled_dot_product_attention(
+            q, k, v.to(q.dtype) if v.dtype != q.dtype else v, attn_mask=attn_mask,
+            is_causal=causal and attn_mask is None, scale=s,
+            enable_gqa=q.shape[1] != k.shape[1]).to(v.dtype)
+
+    q_i8, q_scale, k_i8, k_scale, _k_mean = quant.quantize_qk(q, k, softmax_scale=scale,
+                                                              rotate=rotate)
+    q_scale = q_scale.squeeze(-1).contiguous()
+    k_scale = k_scale.squeeze(-1).contiguous()
+    if int8_pv:
+        if window_left >= 0:
+            raise ValueError("window_left is only supported on the fp16-PV path (int8_pv=False)")
+        v_i8, v_scale = quant.quantize_v_perchannel(v)
+        return _C.attn_w8a8_fwd(q_i8, q_scale, k_i8, k_scale, v_i8,
+                                v_scale.squeeze(-2).contiguous(), causal,
+                                causal_diag=k.shape[-2] - q.shape[-2] if causal else 0,
+                                per_warp_quant=per_warp_quant)
+    return _C.attn_int8_fwd(q_i8, q_scale, k_i8, k_scale, v.contiguous(), causal, window_left)
+
+
+def attn_int8_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
+                     scale: float | None = None, rotate: bool = False,
+                     num_splits: int | None = None) -> torch.Tensor:
+    """Split-KV decode: q fp16 [B, Hq, 1, D] against k, v fp16 [B, Hkv, N, D]."""
+    from .quant import quantize_qk
+
+    if q.shape[-2] != 1:
+        raise AssertionError(f"decode expects M=1, got M={q.shape[-2]}")
+    q_i8, q_scale, k_i8, k_scale, _k_mean = quantize_qk(q, k, softmax_scale=scale, rotate=rotate)
+    q_scale = q_scale.reshape(q.shape[0], q.shape[1], 1).contiguous()
+    k_scale = k_scale.squeeze(-1).contiguous()
+    ns = -1 if num_splits is None else int(num_splits)
+    return _C.attn_int8_decode(q_i8, q_scale, k_i8, k_scale, v.contiguous(), ns)
+
+
+def quantize_i8_rowwise(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Fused per-row symmetric int8: x[M,K] -> (q int8 [M,K], scale fp32 [M])."""
+    return _C.quantize_i8_rowwise(x)
+
+
+def linear_q4k(x: torch.Tensor, w_bytes: torch.Tensor, *, bias: torch.Tensor | None = None,
+               out_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """GGUF Q4_K linear on native 144-byte super-blocks: x [..., K] -> [..., N]."""
+    return _linear_kquant(x, w_bytes, bias, out_dtype, _C.gemm_q4k,
+                          getattr(_C, "gemm_decode_q4k", None))
+
+
+def _linear_kquant(x, w_bytes, bias, out_dtype, tile_op, decode_op):
+    *lead, K = x.shape
+    x2 = x.reshape(-1, K).contiguous()
+    w_bytes = w_bytes.contiguous()
+    x_i8, x_scale = quantize_i8_rowwise(x2)
+    M = x2.shape[0]
+    if decode_op is not None and x2.is_cuda and 0 < M <= _KQUANT_DECODE_MAX_M:
+        y = decode_op(x_i8, x_scale, w_bytes, out_dtype)
+    else:
+        y = tile_op(x_i8, x_scale, w_bytes, out_dtype)
+    if bias is not None:
+        y = (y.float() + bias.float()).to(y.dtype)
+    return y.reshape(*lead, y.shape[-1])

@@ -1,0 +1,110 @@
+"""Quantisation prologue of the int8 attention path, on the gfx950 kernels.
+
+Restates superl8/quant/core.py of the reference with the same functions,
+arguments and return shapes. The numerics contract (reference
+core.py:47-62,70-110,164-196 and csrc/include/quant_rowwise.cuh:33-91):
+
+  * per-row symmetric int8: scale = amax * fp32(1/127), 1 for a zero row;
+    q = clamp(rint(x / scale), -127, 127) with IEEE division;
+  * K-smoothing: k_s = dtype(k - mean_n(k)) with an fp32 per-channel mean;
+  * quantize_qk folds softmax_scale * log2(e) into the Q scale (fp32 multiply)
+    so the attention kernels work in the exp2 domain.
+
+The key mean is computed order-independently (exact integer sum for fp16 keys),
+where the reference sums 1024-key chunks in torch's reduction order; softmax
+is invariant to the shift, so attention outputs are unaffected.
+
+These functions run only on GPU tensors; there is no CPU implementation in the
+product (the CPU restatement used to check it lives in the test oracle).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .. import _C
+
+LOG2E = math.log2(math.e)
+Q_MAX = 127.0
+
+
+def _need_gpu(t: torch.Tensor, what: str) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(f"superl8: {what} runs on the GPU kernels only; got a {t.device} tensor")
+
+
+def quantize_int8_rowwise(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Symmetric per-row RTN int8. Returns (q int8 [..., d], scale fp32 [..., 1])."""
+    _need_gpu(x, "quantize_int8_rowwise")
+    shape = x.shape
+    q, scale = _C.quantize_i8_rowwise(x.reshape(-1, shape[-1]))
+    return q.reshape(shape), scale.reshape(*shape[:-1], 1)
+
+
+def dequantize_int8_rowwise(q: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """Inverse of quantize_int8_rowwise (fp32 out)."""
+    return q.float() * scale
+
+
+def smooth_k(k: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Subtract K's per-channel mean over keys. Returns (k_smoothed [..., n, d], k_mean [..., 1, d])."""
+    _need_gpu(k, "smooth_k")
+    k_mean = _C.k_mean(k)
+    k_s = torch.empty_like(k)
+    torch.sub(k, k_mean, out=k_s)  # fp32 subtract, rounded to k's dtype
+    return k_s, k_mean
+
+
+def quantize_v_perchannel(v: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Symmetric per-channel int8 for V (scale over keys). Returns (v_int8, v_scale [..., 1, d])."""
+    _need_gpu(v, "quantize_v_perchannel")
+    q, scale = _C.quantize_v_perchannel(v)
+    return q, scale
+
+
+def quantize_v_rowwise(v: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Symmetric per-token int8 for V (scale per key)."""
+    return quantize_int8_rowwise(v)
+
+
+def detect_q_outlier_domination(q: torch.Tensor, *, ratio_threshold: float = 12.0) -> bool:
+    """True when any Q row has max|q| / median|q| > ratio_threshold (reference core.py:113-145).
+
+    Skipped (False) while the current stream is capturing a graph, because the
+    decision needs a device-to-host read.
+    """
+    try:
+        if torch.cuda.is_current_stream_capturing():
+            return False
+    except Exception:
+        pass
+    q_abs = q.float().abs()
+    row_max = q_abs.amax(dim=-1)
+    row_med = q_abs.median(dim=-1).values
+    return bool(((row_max / (row_med + 1e-10)) > ratio_threshold).any())
+
+
+def quantize_qk(q: torch.Tensor, k: torch.Tensor, *, softmax_scale: float | None = None,
+                rotate: bool = False):
+    """Quantise Q and smoothed K for the int8 QK^T.
+
+    Returns (q_int8, q_scale[..., m, 1] folded with softmax_scale*log2(e),
+    k_int8, k_scale[..., n, 1], k_mean[..., 1, d]). Smoothing and quantising K
+    is one fused kernel (the smoothed fp16 K is never written).
+    """
+    _need_gpu(q, "quantize_qk")
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(q.shape[-1])
+    if rotate:
+        from .rotation import rotate_last
+
+        k_s, k_mean = smooth_k(k)
+        q = rotate_last(q)
+        k_src, mean = rotate_last(k_s), None
+    else:
+        k_mean = _C.k_mean(k)
+        k_src, mean = k, k_mean
+    q_i8, q_scale = _C.quantize_rows_centered(q, None, softmax_scale * LOG2E)
+    k_i8, k_scale = _C.quantize_rows_centered(k_src, mean, 1.0)
+    return q_i8, q_scale.unsqueeze(-1), k_i8, k_scale.unsqueeze(-1), k_mean

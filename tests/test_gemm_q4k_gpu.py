@@ -1,0 +1,93 @@
+"""GPU parity of the Q4_K path: dequant bit-exact, GEMV vs the oracle's exact sum."""
+import numpy as np
+import pytest
+import torch
+
+import superl8_amd
+from oracle import q4k as oq
+from oracle import quant as oqn
+from superl8_amd import _C
+from tests.tolerances import assert_int8_quality
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(x):
+    return x.detach().cpu().numpy()
+
+
+def _case(M, N, K, seed, device):
+    w = oq.random_weights(N, K, seed)
+    r = np.random.default_rng(seed + 1)
+    x = torch.from_numpy(r.standard_normal((M, K)).astype(np.float16)).to(device)
+    return x, w, torch.from_numpy(w).to(device)
+
+
+@pytest.mark.parametrize("N,K", [(64, 256), (130, 512), (17408, 5120), (33, 4096)])
+def test_dequant_bit_exact(device, N, K):
+    w = oq.random_weights(N, K, seed=N)
+    got = _C.dequant_q4k(torch.from_numpy(w).to(device), K)
+    np.testing.assert_array_equal(_np(got), oq.dequant(w, K))
+
+
+SHAPES = [(1, 4096, 3072), (1, 1024, 4096), (4, 4096, 4096), (8, 512, 768), (16, 4096, 3072),
+          (1, 130, 256), (1, 4864, 1024), (1, 17408, 5120), (8, 17408, 5120), (5, 7, 256),
+          (11, 96, 512)]
+
+
+@pytest.mark.parametrize("odt", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_gemv_matches_exact_sum(device, M, N, K, odt):
+    x, w, wd = _case(M, N, K, seed=M * 131 + N, device=device)
+    x_i8, xs = _C.quantize_i8_rowwise(x)
+    y = _C.gemm_decode_q4k(x_i8, xs, wd, odt)
+    assert y.shape == (M, N) and y.dtype == odt
+    ref = oq.gemv(_np(x_i8), _np(xs), w, K)
+    # one fp32 accumulation per super-block, then the output rounding of odt
+    rtol = {torch.float16: 2e-3, torch.bfloat16: 1.6e-2, torch.float32: 1e-5}[odt]
+    err = np.abs(_np(y.float()).astype(np.float64) - ref)
+    scale = np.abs(ref).max()
+    assert (err <= rtol * np.abs(ref) + 1e-5 * scale).all(), f"max err {err.max():.3e}"
+    assert_int8_quality(y, ref, min_cos=0.9999, max_rel_l1=1e-3 if odt != torch.bfloat16 else 1e-2,
+                        min_sqnr_db=40.0)
+
+
+def test_tile_matches_decode_and_large_m(device):
+    x, w, wd = _case(40, 256, 1024, seed=5, device=device)
+    x_i8, xs = _C.quantize_i8_rowwise(x)
+    y = _C.gemm_q4k(x_i8, xs, wd)
+    ref = oq.gemv(_np(x_i8), _np(xs), w, 1024)
+    assert_int8_quality(y, ref, min_cos=0.9999, max_rel_l1=1e-3, min_sqnr_db=40.0)
+    y16 = _C.gemm_decode_q4k(x_i8[:16].contiguous(), xs[:16].contiguous(), wd)
+    assert torch.equal(y16, y[:16])
+
+
+def test_linear_q4k_routes_decode_and_is_deterministic(device, monkeypatch):
+    x, w, wd = _case(1, 4096, 1024, seed=7, device=device)
+    called = {}
+    orig = _C.gemm_decode_q4k
+
+    def spy(*a, **k):
+        called["decode"] = True
+        return orig(*a, **k)
+
+    monkeypatch.setattr(_C, "gemm_decode_q4k", spy)
+    y = superl8_amd.linear_q4k(x, wd)
+    assert called.get("decode")
+    monkeypatch.undo()
+    for _ in range(3):
+        assert torch.equal(superl8_amd.linear_q4k(x, wd), y)
+    bias = torch.randn(4096, device=device, dtype=torch.float16)
+    yb = superl8_amd.linear_q4k(x, wd, bias=bias)
+    assert torch.equal(yb, (y.float() + bias.float()).half())
+
+
+def test_rejects_bad_k(device):
+    x_i8 = torch.randint(-127, 128, (4, 128), device=device, dtype=torch.int8)
+    xs = torch.ones(4, device=device)
+    blk = torch.zeros(8, 144, device=device, dtype=torch.uint8)
+    with pytest.raises(RuntimeError):
+        _C.gemm_q4k(x_i8, xs, blk, torch.float16)
+    with pytest.raises(RuntimeError, match="M<=16"):
+        _C.gemm_decode_q4k(torch.zeros(17, 256, device=device, dtype=torch.int8),
+                           torch.ones(17, device=device), blk[:, :144].contiguous())

@@ -1,0 +1,57 @@
+"""CPU checks of the C-ABI library and the host-side operator surface (no GPU needed)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+import superl8_amd
+from superl8_amd import _C, _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "superl8_hip.h"
+
+
+def _declared_symbols():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(sl8_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    syms = _declared_symbols()
+    assert len(syms) >= 15
+    missing = [s for s in syms if not hasattr(lib, s)]
+    assert not missing, f"not exported: {missing}"
+    assert set(syms) == set(_lib.SIGNATURES), "ctypes table and header disagree"
+
+
+def test_version_and_error_slot():
+    lib = _lib.load()
+    assert lib.sl8_version().startswith(b"superl8-hip")
+    # argument validation runs before any device work, so it works without a GPU
+    rc = lib.sl8_gemm_decode_q4k(None, None, None, None, 0, 1, 8, 100, None)
+    assert rc == -1 and b"K%256" in lib.sl8_last_error()
+    rc = lib.sl8_quantize_i8_rowwise(None, 7, 1, 1, None, None, None)
+    assert rc == -1 and b"float16/bfloat16/float32" in lib.sl8_last_error()
+    assert lib.sl8_quantize_i8_rowwise(None, 0, 0, 5, None, None, None) == 0  # empty is a no-op
+
+
+def test_decode_split_heuristic_and_workspace():
+    lib = _lib.load()
+    ns = lib.sl8_choose_num_splits(32768, 16, 8)
+    assert 1 <= ns <= 256
+    assert lib.sl8_choose_num_splits(1, 1, 1) == 1
+    assert lib.sl8_attn_int8_decode_workspace(16, 32, 128, 16) >= 16 * 16 * 32 * (128 + 2) * 4
+
+
+def test_ops_reject_cpu_tensors():
+    """No CPU path in the product: CPU tensors raise instead of silently falling back."""
+    x = torch.randn(4, 256, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        superl8_amd.quantize_i8_rowwise(x)
+    q = torch.randn(1, 2, 8, 64, dtype=torch.float16)
+    with pytest.raises(RuntimeError):
+        superl8_amd.attn_int8_fwd(q, q, q, internal_accuracy_gate=False)
+    with pytest.raises(RuntimeError):
+        superl8_amd.linear_q4k(x, torch.zeros(8, 144, dtype=torch.uint8))

@@ -1,0 +1,280 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the GPU checker.
+
+Each oracle function is checked against something other than its own
+formula: known answers from the reference's tests, closed forms, brute-force
+loops on tiny inputs, invariants, and an independent textbook formulation.
+The plausible mistakes each test would catch are named in its docstring.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import attention as oa
+from oracle import q4k as oq
+from oracle import quant as oqn
+from tests.tolerances import assert_int8_quality
+
+RNG = np.random.default_rng(1234)
+
+
+# ---------------------------------------------------------------- quantisation
+def test_quant_zero_and_outlier_rows():
+    """Reference test_quant_rowwise.py:75-86: zero row -> scale 1 and codes 0;
+    a single outlier sets the scale and quantises to 127."""
+    x = np.zeros((3, 128), np.float16)
+    x[1, 40] = 50.0
+    q, s = oqn.quantize_rows(x.astype(np.float32))
+    assert s[0] == 1.0 and not q[0].any()
+    assert s[1] == np.float32(np.float32(50.0) * np.float32(1 / np.float32(127)))
+    assert q[1, 40] == 127 and np.count_nonzero(q[1]) == 1
+    assert not q[2].any() and s[2] == 1.0
+
+
+def test_quant_scale_is_reciprocal_multiply():
+    """scale = amax * fp32(1/127) (quant_rowwise.cuh:33-38), not amax/127.
+    Rows are chosen where the two differ, so a true-division oracle fails."""
+    amax = np.arange(1, 30000, dtype=np.float32).astype(np.float16).astype(np.float32) / 64
+    mul = (amax * oqn.INV127).astype(np.float32)
+    div = (amax / np.float32(127)).astype(np.float32)
+    differ = amax[mul != div][:64]
+    assert differ.size > 10
+    x = np.zeros((differ.size, 8), np.float32)
+    x[:, 3] = differ
+    _, s = oqn.quantize_rows(x)
+    np.testing.assert_array_equal(s, (differ * oqn.INV127).astype(np.float32))
+    assert (s != (differ / np.float32(127))).all()
+
+
+def test_quant_rounding_brute_force():
+    """Codes satisfy |x/s - q| <= 0.5 with ties to even, clamp at +-127 (never -128)."""
+    x = (RNG.standard_normal((64, 96)) * 3).astype(np.float16).astype(np.float32)
+    q, s = oqn.quantize_rows(x)
+    quo = (x / s[:, None]).astype(np.float32).astype(np.float64)
+    assert np.all(np.abs(quo - q) <= 0.5)
+    tie = np.abs(quo - np.trunc(quo)) == 0.5
+    assert np.all(q[tie] % 2 == 0)
+    assert q.min() >= -127 and q.max() <= 127
+    # explicit half-way case: s a power of two so (k + 0.5) * s divides exactly
+    row = np.zeros((1, 8), np.float32)
+    row[0, 0] = np.float32(127.0)  # amax 127
+    s0 = oqn.quantize_rows(row)[1][0]
+    ties = [np.float32(k + 0.5) * s0 for k in (2, 3, -2, -5)]
+    if all(np.float32(t) / s0 == np.float32(k + 0.5) for t, k in zip(ties, (2, 3, -2, -5))):
+        row[0, 1:5] = ties
+        q1 = oqn.quantize_rows(row)[0][0]
+        assert list(q1[1:5]) == [2, 4, -2, -4]
+
+
+def test_k_mean_exact_and_order_free():
+    """fp16 mean: exact sum, so equal to the float64 mean rounded once, and
+    invariant under any key permutation (catches a plain fp32 running sum)."""
+    k = (RNG.standard_normal((2, 3, 2000, 64)) * 4).astype(np.float16)
+    m = oqn.k_mean(k, "f16")
+    ref = k.astype(np.float64).mean(axis=-2, keepdims=True)
+    np.testing.assert_array_equal(m, ref.astype(np.float32))
+    perm = RNG.permutation(2000)
+    np.testing.assert_array_equal(m, oqn.k_mean(k[:, :, perm], "f16"))
+    const = np.full((1, 1, 777, 8), 0.3, np.float16)
+    np.testing.assert_array_equal(oqn.k_mean(const, "f16"), np.float16(0.3).astype(np.float32))
+
+
+def test_k_mean_bf16_and_smooth():
+    bits = oqn.f32_to_bf16_bits(RNG.standard_normal((1, 2, 300, 16)).astype(np.float32))
+    m = oqn.k_mean(bits, "bf16")
+    ref = oqn.bf16_bits_to_f32(bits).astype(np.float64).mean(axis=-2, keepdims=True)
+    assert np.abs(m - ref).max() <= np.spacing(np.abs(ref).astype(np.float32)).max()
+    k = (RNG.standard_normal((1, 1, 50, 8))).astype(np.float16)
+    ks, mean = oqn.smooth_k(k, "f16")
+    for n, d in [(0, 0), (7, 3), (49, 7)]:
+        want = float(np.float16(np.float32(k[0, 0, n, d]) - mean[0, 0, 0, d]))
+        assert ks[0, 0, n, d] == want
+
+
+def test_bf16_rounding_helpers():
+    vals = np.array([1.0, 1.00390625, 1.01171875, -3.0e38, 1e-40], np.float32)
+    bits = oqn.f32_to_bf16_bits(vals)
+    # 1 + 2^-8 is a tie between 1 and 1+2^-7 -> even (1.0); 1+3*2^-8 -> 1+2^-6
+    assert bits[0] == 0x3F80 and bits[1] == 0x3F80 and bits[2] == 0x3F82
+
+
+def test_quantize_qk_fold():
+    """q_scale = safe * fp32(softmax_scale*log2 e) (core.py:195)."""
+    q = RNG.standard_normal((1, 2, 5, 64)).astype(np.float16)
+    k = RNG.standard_normal((1, 2, 7, 64)).astype(np.float16)
+    q_i8, qs, k_i8, ks, _ = oqn.quantize_qk(q, k)
+    _, safe = oqn.quantize_rows(q.astype(np.float32))
+    fold = np.float32(1.0 / math.sqrt(64) * math.log2(math.e))
+    np.testing.assert_array_equal(qs, (safe * fold).astype(np.float32))
+
+
+# ---------------------------------------------------------------- Q4_K
+def _scale_min_literal(s, j):
+    """get_scale_min_k4 as a per-byte scalar routine (llama.cpp convert.cu form)."""
+    if j < 4:
+        return s[j] & 63, s[j + 4] & 63
+    return (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4), (s[j + 4] >> 4) | ((s[j] >> 6) << 4)
+
+
+def test_q4k_scale_min_matches_literal_and_roundtrips():
+    s12 = RNG.integers(0, 256, (500, 12), dtype=np.uint8)
+    sc, mn = oq.scale_min_k4(s12)
+    for r in range(0, 500, 37):
+        for j in range(8):
+            assert (sc[r, j], mn[r, j]) == _scale_min_literal([int(b) for b in s12[r]], j)
+    a = np.arange(64, dtype=np.uint8)
+    sc_all = np.stack(np.meshgrid(a, a, indexing="ij"), -1).reshape(-1, 2)  # all (sc,m) pairs
+    sc8 = np.repeat(sc_all[:, :1], 8, 1)
+    mn8 = np.repeat(sc_all[:, 1:], 8, 1)
+    sc8[:, 3], mn8[:, 6] = sc_all[::-1, 0], sc_all[::-1, 1]
+    back = oq.scale_min_k4(oq.pack_scale_min_k4(sc8, mn8))
+    np.testing.assert_array_equal(back[0], sc8)
+    np.testing.assert_array_equal(back[1], mn8)
+
+
+def test_q4k_dequant_known_answer():
+    """d=1, dmin=0.5, sc_j=j+1, m_j=2j, q[j][l]=(l+j)%16 -> w = (j+1)*q - j."""
+    j = np.arange(8)
+    q = (np.arange(32)[None, :] + j[:, None]) % 16
+    blk = oq.make_blocks(np.array([1.0]), np.array([0.5]), (j + 1)[None], (2 * j)[None], q[None])
+    w = oq.dequant(blk, 256)[0].reshape(8, 32)
+    np.testing.assert_array_equal(w, ((j[:, None] + 1) * q - j[:, None]).astype(np.float32))
+
+
+def test_q4k_nibble_positions():
+    """Byte 32g+l: low nibble -> element 64g+l, high nibble -> element 64g+32+l
+    (gemm_decode_dp4a.cuh:502-503). Catches swapped halves / interleave."""
+    blk = oq.make_blocks(np.array([1.0]), np.array([0.0]), np.ones((1, 8), np.uint8),
+                         np.zeros((1, 8), np.uint8), np.zeros((1, 8, 32), np.uint8))
+    blk[0, 16 + 32 * 2 + 5] = 0x93  # g=2, l=5: low 3, high 9
+    w = oq.dequant(blk, 256)[0]
+    nz = np.nonzero(w)[0]
+    assert list(nz) == [64 * 2 + 5, 64 * 2 + 32 + 5]
+    assert w[133] == 3 and w[165] == 9
+
+
+def test_q4k_gemv_matches_dequant_matmul():
+    w = oq.random_weights(40, 512, seed=3)
+    x = RNG.integers(-127, 128, (5, 512), dtype=np.int8)
+    xs = RNG.random(5).astype(np.float32)
+    y = oq.gemv(x, xs, w, 512)
+    ref = (x.astype(np.float64) @ oq.dequant(w, 512).astype(np.float64).T) * xs[:, None]
+    # dequant rounds d*sc*q - dmin*m to fp32 once; the oracle sums exactly
+    np.testing.assert_allclose(y, ref, rtol=1e-6, atol=1e-6)
+
+
+# ---------------------------------------------------------------- attention
+def test_scores_brute_force_gqa():
+    q = RNG.integers(-127, 128, (1, 4, 3, 8), dtype=np.int8)
+    k = RNG.integers(-127, 128, (1, 2, 5, 8), dtype=np.int8)
+    s = oa.scores_i32(q, k)
+    for h in range(4):
+        for i in range(3):
+            for j in range(5):
+                assert s[0, h, i, j] == sum(int(q[0, h, i, d]) * int(k[0, h // 2, j, d])
+                                            for d in range(8))
+
+
+def _case(B=1, Hq=4, Hkv=2, M=37, N=53, D=64, seed=0):
+    r = np.random.default_rng(seed)
+    q = r.standard_normal((B, Hq, M, D)).astype(np.float16)
+    k = r.standard_normal((B, Hkv, N, D)).astype(np.float16)
+    v = r.standard_normal((B, Hkv, N, D)).astype(np.float16)
+    return q, k, v
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_prefill_oracle_vs_textbook(causal):
+    """Online/exp2 oracle == dense e-base softmax on dequantised operands
+    (catches transposes, GQA head map, causal alignment M != N, log2e fold)."""
+    q, k, v = _case()
+    q_i8, qs, k_i8, ks, _ = oqn.quantize_qk(q, k)
+    out, lse = oa.attn_int8_fwd(q_i8, qs, k_i8, ks, v.astype(np.float32), causal)
+    qd = q_i8.astype(np.float64) * qs[..., None]
+    kd = k_i8.astype(np.float64) * ks[..., None]
+    ref = oa.attention_fp64(qd, kd, v.astype(np.float64), causal, scale=math.log(2))
+    np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-5)
+    # LSE in natural log of ln2-scaled logits
+    s = np.matmul(qd, np.swapaxes(kd[:, oa.kv_head_index(4, 2)], -1, -2)) * math.log(2)
+    if causal:
+        s = np.where(oa.valid_mask(37, 53, True), s, -np.inf)
+    mx = s.max(-1, keepdims=True)
+    np.testing.assert_allclose(lse, (mx + np.log(np.exp(s - mx).sum(-1, keepdims=True)))[..., 0],
+                               rtol=1e-5)
+
+
+def test_prefill_oracle_quality_vs_true_attention():
+    """The whole prologue + int8 attention meets the reference's int8 gate
+    against fp64 attention on the original fp16 inputs (test_attn_fwd.py:44-51)."""
+    q, k, v = _case(B=1, Hq=2, Hkv=2, M=128, N=128, D=64, seed=5)
+    for causal in (False, True):
+        q_i8, qs, k_i8, ks, _ = oqn.quantize_qk(q, k)
+        out, _ = oa.attn_int8_fwd(q_i8, qs, k_i8, ks, v.astype(np.float32), causal)
+        assert_int8_quality(out, oa.attention_fp64(q, k, v, causal))
+
+
+def test_window_mask_brute_force():
+    M, N, wl = 6, 9, 3
+    ok = oa.valid_mask(M, N, True, wl)
+    for i in range(M):
+        for j in range(N):
+            pos = i + N - M
+            assert ok[i, j] == (j <= pos and j > pos - wl)
+    empty = oa.valid_mask(4, 4, True, 0)
+    assert not empty.any()  # window 0 masks everything -> rows output 0
+
+
+def test_fully_masked_rows_output_zero():
+    q, k, v = _case(M=4, N=4, Hq=2, Hkv=2)
+    q_i8, qs, k_i8, ks, _ = oqn.quantize_qk(q, k)
+    out, lse = oa.attn_int8_fwd(q_i8, qs, k_i8, ks, v.astype(np.float32), True, window_left=0)
+    assert not out.any() and np.isneginf(lse).all()
+
+
+@pytest.mark.parametrize("ns", [1, 3, 16, 64])
+def test_decode_split_invariance(ns):
+    """Split partials + LSE merge equal the unsplit softmax for any split count,
+    including splits that are empty (ns=64 > N/…)."""
+    q, k, v = _case(B=2, Hq=8, Hkv=2, M=1, N=50, D=64, seed=9)
+    q_i8, qs, k_i8, ks, _ = oqn.quantize_qk(q, k)
+    dec = oa.attn_int8_decode(q_i8[:, :, 0], qs[:, :, 0], k_i8, ks, v.astype(np.float32), ns)
+    pre, _ = oa.attn_int8_fwd(q_i8, qs, k_i8, ks, v.astype(np.float32), False)
+    np.testing.assert_allclose(dec, pre[:, :, 0], rtol=1e-12, atol=1e-12)
+
+
+def test_w8a8_oracle_close_to_fp16v():
+    """Int8 PV (per-row and per-half P scales) stays within the reference's int8-PV
+    bars of the fp16-V result (test_attn_fwd_w8a8.py:37)."""
+    q, k, v = _case(B=1, Hq=4, Hkv=2, M=96, N=160, D=64, seed=11)
+    q_i8, qs, k_i8, ks, _ = oqn.quantize_qk(q, k)
+    v_i8, vs = oqn.quantize_v_perchannel(v)
+    for causal in (False, True):
+        ref, _ = oa.attn_int8_fwd(q_i8, qs, k_i8, ks, v.astype(np.float32), causal)
+        for pw in (True, False):
+            out = oa.attn_w8a8_fwd(q_i8, qs, k_i8, ks, v_i8, vs, causal, 160 - 96, pw)
+            assert_int8_quality(out, ref, min_cos=0.998, max_rel_l1=0.03, min_sqnr_db=18)
+
+
+def test_w8a8_p_requant_known_answer():
+    """One query, 2 keys in one tile with p = (1, 1/3): p_scale = fp32(1/127),
+    codes (127, rint(127/3)=42); output = (127*v0 + 42*v1)*ps*vs / (1 + 1/3)."""
+    q_i8 = np.zeros((1, 1, 1, 4), np.int8)
+    q_i8[..., 0] = 1
+    k_i8 = np.zeros((1, 1, 2, 4), np.int8)
+    k_i8[0, 0, 0, 0] = 2
+    k_i8[0, 0, 1, 0] = 1
+    l3 = np.float32(math.log2(3.0))
+    qs = np.array([[[l3]]], np.float32)
+    ks = np.array([[[1.0, 0.0]]], np.float32)
+    # logits: key0 = 2*log2(3)... use ks to make key1 logit 0 and key0 log2(3)
+    ks[0, 0, 0] = np.float32(0.5)
+    v_i8 = np.array([[[[10, 0, 0, 0], [-20, 0, 0, 0]]]], np.int8)
+    vs = np.ones((1, 1, 4), np.float32)
+    out = oa.attn_w8a8_fwd(q_i8, qs, k_i8, ks, v_i8, vs, per_warp_quant=False)
+    s0 = np.float32(np.float32(2.0) * l3) * np.float32(0.5)
+    p1 = 2.0 ** (0.0 - float(s0))
+    ps = np.float32(np.float32(1.0) * np.float32(1.0 / 127.0))
+    inv = np.float32(1.0) / ps
+    c1 = np.rint(np.float32(np.float32(p1) * inv))
+    want = (127 * 10 + float(c1) * -20) * float(ps) / (1.0 + p1)
+    assert abs(out[0, 0, 0, 0] - want) < 1e-9
