@@ -1,0 +1,512 @@
+// Prefill FlashAttention-2 for gfx950: int8 Q.K^T on MFMA, fp32 exp2-domain
+// online softmax, fp16/bf16 P.V on MFMA.
+//
+// Semantics follow the reference (csrc/include/attn_int8_fwd.cuh:47-209):
+//   logit  = ((float)<q_i8, k_i8> * q_scale[m]) * k_scale[n]   (exp2 domain)
+//   causal = bottom-right aligned: query m sees keys n <= m + N - M
+//   window = window_left >= 0 also requires n > m + N - M - window_left
+//            (position m itself when not causal)
+//   out    = sum_n 2^(s - max) v_n / sum_n 2^(s - max); a row with no visible
+//            key is 0 and its LSE -inf; LSE = max*ln2 + ln(l).
+//   GQA: query head h reads K/V head h / (Hq/Hkv).
+//
+// Work decomposition. A workgroup (4 waves) owns 128 queries of one head; each
+// wave owns 32 queries for the whole key loop. Key tiles of 64 are staged in
+// LDS (double buffered, one barrier per tile) and shared by the 4 waves.
+//
+// The scores are computed transposed, S^T = K . Q^T, with
+// v_mfma_i32_32x32x32_i8 (A = 32 keys x 32 channels from LDS, B = the wave's
+// 32 queries x 32 channels held in registers). In the 32x32 accumulator
+// layout a lane then holds one query (lane % 32) and 16 of the keys, which is
+// exactly the B-operand layout of the next product O^T = V^T . P^T
+// (v_mfma_f32_32x32x16_f16): P never leaves registers. The 8 keys a lane feeds
+// per 16-key MFMA step are {4h..4h+3, 8+4h..8+4h+3} (h = lane / 32); V^T is
+// stored with bits 2 and 3 of the key index swapped inside each 16-key group
+// so that those 8 keys are one contiguous 16-byte LDS read.
+// V^T is produced once per call by a transpose kernel into the workspace
+// ([B*Hkv][D][Npad], Npad = N rounded up to 64, zero padded).
+//
+// Scheduling: workgroups are issued heaviest-first (causal), and, when the
+// KV-head count is a multiple of 8, all query heads of one KV head go to the
+// same XCD so its K/V tiles stay in that XCD's L2.
+
+#include "common.hpp"
+
+namespace sl8 {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+constexpr int FWD_THREADS = 256;
+constexpr int FWD_WAVES = 4;
+constexpr int BM = 128;  // queries per workgroup
+constexpr int BN = 64;   // keys per tile
+constexpr int KPAD = 16; // bytes of padding per K row in LDS
+constexpr int VPAD = 8;  // halves of padding per V^T row in LDS
+constexpr float LN2F = 0.6931471805599453f;
+
+// key index inside a 16-key group -> storage position (swap bits 2 and 3)
+__host__ __device__ __forceinline__ int vt_pos(int k) {
+  return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1);
+}
+
+// ---------------------------------------------------------------------------
+// V [BHkv][N][D] (16-bit) -> V^T [BHkv][D][Npad], key-permuted, zero padded.
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ void __launch_bounds__(256)
+v_transpose_kernel(const uint16_t* __restrict__ v, uint16_t* __restrict__ vt, int N, int Npad) {
+  __shared__ uint16_t tile[BN][D + 2];
+  const int64_t bh = blockIdx.y;
+  const int n0 = blockIdx.x * BN;
+  const uint16_t* src = v + bh * (int64_t)N * D;
+  for (int i = threadIdx.x; i < BN * D / 8; i += 256) {
+    const int r = i / (D / 8), c = (i % (D / 8)) * 8;
+    uint4 val = {0, 0, 0, 0};
+    if (n0 + r < N) val = *reinterpret_cast<const uint4*>(src + (int64_t)(n0 + r) * D + c);
+    const uint16_t* pv = reinterpret_cast<const uint16_t*>(&val);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) tile[r][c + e] = pv[e];
+  }
+  __syncthreads();
+  uint16_t* dst = vt + bh * (int64_t)D * Npad + n0;
+  for (int i = threadIdx.x; i < D * (BN / 2); i += 256) {
+    const int d = i / (BN / 2), pr = (i % (BN / 2)) * 2;  // storage positions pr, pr+1
+    const int base = pr & ~15;
+    const int k0 = base + vt_pos(pr & 15);                 // vt_pos is an involution
+    const uint32_t lo = tile[k0][d], hi = tile[k0 + 1][d];
+    *reinterpret_cast<uint32_t*>(dst + (int64_t)d * Npad + pr) = lo | (hi << 16);
+  }
+}
+
+template <int VDT> struct PvOp;
+template <> struct PvOp<SL8_DTYPE_F16> {
+  typedef v8h vec;
+  __device__ static vec pack(const float* p) {
+    vec r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = (_Float16)p[e];
+    return r;
+  }
+  __device__ static v16f mfma(vec a, vec b, v16f c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct PvOp<SL8_DTYPE_BF16> {
+  typedef v8bf vec;
+  __device__ static vec pack(const float* p) {
+    vec r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = (__bf16)p[e];
+    return r;
+  }
+  __device__ static v16f mfma(vec a, vec b, v16f c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+struct FwdArgs {
+  const int8_t* q;
+  const float* qs;
+  const int8_t* k;
+  const float* ks;
+  const uint16_t* vt;  // V^T workspace
+  void* out;
+  float* lse;
+  int32_t* scores;     // DUMP mode
+  int M, N, Npad, Hq, Hkv, nqb, window_left;
+  int xcd_map;         // 1: XCD-aware block order
+};
+
+template <int D>
+struct FwdSmem {
+  int8_t k[2][BN][D + KPAD];
+  uint16_t vt[2][D][BN + VPAD];
+  float ks[2][BN];
+};
+
+// blockIdx.x -> (b*Hq + h, query block), heaviest query block first.
+__device__ __forceinline__ void block_coords(const FwdArgs& a, int& bh, int& qb) {
+  const int id = blockIdx.x;
+  const int total = gridDim.x;
+  const int gsz = a.Hq / a.Hkv;
+  const int nbkv = total / (a.nqb * gsz);  // B * Hkv
+  if (a.xcd_map) {
+    // id = 8*slot + xcd; XCD x serves KV heads {x, x+8, ...}
+    const int xcd = id & 7, slot = id >> 3;
+    const int kv_per_xcd = nbkv / 8;
+    const int per_qb = kv_per_xcd * gsz;
+    const int r = slot / per_qb;         // rank of the query block (0 = heaviest)
+    const int rem = slot % per_qb;
+    const int bkv = xcd + 8 * (rem / gsz);
+    const int j = rem % gsz;
+    const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
+    bh = b * a.Hq + kvh * gsz + j;
+    qb = a.nqb - 1 - r;
+  } else {
+    const int nbh = total / a.nqb;
+    qb = a.nqb - 1 - id / nbh;
+    bh = id % nbh;
+  }
+}
+
+template <int D, bool CAUSAL, int VDT, bool DUMP, bool LSE>
+__global__ void __launch_bounds__(FWD_THREADS, 2)
+attn_fwd_kernel(const FwdArgs a) {
+  constexpr int DC = D / 32;  // 32-channel chunks
+  __shared__ FwdSmem<D> sm;
+  using PV = PvOp<VDT>;
+
+  int bh, qb;
+  block_coords(a, bh, qb);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = lane >> 5, l32 = lane & 31;
+  const int gsz = a.Hq / a.Hkv;
+  const int b = bh / a.Hq, hq = bh % a.Hq;
+  const int64_t bkv = (int64_t)b * a.Hkv + hq / gsz;
+  const int M = a.M, N = a.N;
+  const int diag = CAUSAL ? N - M : 0;
+
+  const int m_blk = qb * BM;
+  const int mq = m_blk + wave * 32 + l32;  // this lane's query
+  const bool m_ok = mq < M;
+  const int qpos = mq + diag;
+
+  // Q as the B operand: 32 channels per chunk, 16 bytes per lane
+  v4i qop[DC];
+  {
+    const int8_t* qrow = a.q + ((int64_t)bh * M + (m_ok ? mq : 0)) * D + 16 * h;
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      qop[c] = m_ok ? *reinterpret_cast<const v4i*>(qrow + 32 * c) : v4i{0, 0, 0, 0};
+    }
+  }
+  const float qsc = (m_ok && !DUMP) ? a.qs[(int64_t)bh * M + mq] : 0.f;
+
+  // key range of the workgroup and of this wave
+  int n_end = N;
+  if (CAUSAL) n_end = max(0, min(N, m_blk + BM + diag));
+  int n_beg = 0;
+  if (a.window_left >= 0) n_beg = max(0, m_blk + diag - a.window_left + 1) & ~(BN - 1);
+  const int wq_lo = m_blk + wave * 32 + diag;  // first query position of the wave
+  const int wq_hi = wq_lo + 31;
+
+  const int8_t* kb = a.k + bkv * (int64_t)N * D;
+  const float* ksb = a.ks + bkv * (int64_t)N;
+  const uint16_t* vtb = a.vt + bkv * (int64_t)D * a.Npad;
+
+  // per-thread staging slots
+  constexpr int KCH = BN * D / 16 / FWD_THREADS;  // 16-B K chunks per thread
+  constexpr int VCH = D * BN * 2 / 16 / FWD_THREADS;
+  uint4 kreg[KCH], vreg[VCH];
+  float ksreg = 0.f;
+
+  auto load_tile = [&](int n0) {
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      const int idx = tid + i * FWD_THREADS;
+      const int r = idx / (D / 16), c = (idx % (D / 16)) * 16;
+      kreg[i] = (n0 + r < N) ? *reinterpret_cast<const uint4*>(kb + (int64_t)(n0 + r) * D + c)
+                             : uint4{0, 0, 0, 0};
+    }
+    if constexpr (!DUMP) {
+#pragma unroll
+      for (int i = 0; i < VCH; ++i) {
+        const int idx = tid + i * FWD_THREADS;
+        const int d = idx / (BN / 8), c = (idx % (BN / 8)) * 8;
+        vreg[i] = *reinterpret_cast<const uint4*>(vtb + (int64_t)d * a.Npad + n0 + c);
+      }
+      if (tid < BN) ksreg = (n0 + tid < N) ? ksb[n0 + tid] : 0.f;
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      const int idx = tid + i * FWD_THREADS;
+      const int r = idx / (D / 16), c = (idx % (D / 16)) * 16;
+      *reinterpret_cast<uint4*>(&sm.k[buf][r][c]) = kreg[i];
+    }
+    if constexpr (!DUMP) {
+#pragma unroll
+      for (int i = 0; i < VCH; ++i) {
+        const int idx = tid + i * FWD_THREADS;
+        const int d = idx / (BN / 8), c = (idx % (BN / 8)) * 8;
+        *reinterpret_cast<uint4*>(&sm.vt[buf][d][c]) = vreg[i];
+      }
+      if (tid < BN) sm.ks[buf][tid] = ksreg;
+    }
+  };
+
+  v16f oacc[DC];
+#pragma unroll
+  for (int t = 0; t < DC; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[t][r] = 0.f;
+  float m_run = -INFINITY, l_lane = 0.f;
+
+  if (n_beg < n_end) {
+    load_tile(n_beg);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  int buf = 0;
+  for (int n0 = n_beg; n0 < n_end; n0 += BN, buf ^= 1) {
+    const bool has_next = n0 + BN < n_end;
+    if (has_next) load_tile(n0 + BN);
+
+    // does this wave see any key of the tile?
+    bool wave_live = true;
+    if (CAUSAL && n0 > wq_hi) wave_live = false;
+    if (a.window_left >= 0 && n0 + BN - 1 <= wq_lo - a.window_left) wave_live = false;
+    if (DUMP) wave_live = true;
+
+    if (wave_live) {
+      // ---- S^T = K . Q^T, two 32-key sub-tiles ----
+      v16i sacc[2];
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        v16i c = {0};
+#pragma unroll
+        for (int r = 0; r < 16; ++r) c[r] = 0;
+#pragma unroll
+        for (int ch = 0; ch < DC; ++ch) {
+          const v4i kop = *reinterpret_cast<const v4i*>(&sm.k[buf][st * 32 + l32][32 * ch + 16 * h]);
+          c = __builtin_amdgcn_mfma_i32_32x32x32_i8(kop, qop[ch], c, 0, 0, 0);
+        }
+        sacc[st] = c;
+      }
+
+      if constexpr (DUMP) {
+        if (m_ok) {
+          int32_t* srow = a.scores + ((int64_t)bh * M + mq) * N;
+#pragma unroll
+          for (int st = 0; st < 2; ++st)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int n = n0 + st * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+              if (n < N) srow[n] = sacc[st][r];
+            }
+        }
+      } else {
+        // ---- logits, mask, running max ----
+        const bool need_mask = (n0 + BN > N) || (CAUSAL && n0 + BN - 1 > wq_lo) ||
+                               (a.window_left >= 0 && n0 <= wq_hi - a.window_left);
+        float s[2][16];
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int kl = st * 32 + 8 * g + 4 * h;
+            const float4 k4 = *reinterpret_cast<const float4*>(&sm.ks[buf][kl]);
+            const float kk[4] = {k4.x, k4.y, k4.z, k4.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              float x = ((float)sacc[st][4 * g + e] * qsc) * kk[e];
+              if (need_mask) {
+                const int n = n0 + kl + e;
+                bool ok = n < N;
+                if (CAUSAL) ok = ok && n <= qpos;
+                if (a.window_left >= 0) ok = ok && n > qpos - a.window_left;
+                x = ok ? x : -INFINITY;
+              }
+              s[st][4 * g + e] = x;
+              tmax = fmaxf(tmax, x);
+            }
+          }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float m_new = fmaxf(m_run, tmax);
+        const float resc = (m_run == -INFINITY || m_new == -INFINITY) ? 1.f : exp2f(m_run - m_new);
+        const float msub = (m_new == -INFINITY) ? 0.f : m_new;
+        float psum = 0.f;
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float p = exp2f(s[st][r] - msub);  // -inf -> 0
+            s[st][r] = p;
+            psum += p;
+          }
+        l_lane = l_lane * resc + psum;
+        m_run = m_new;
+#pragma unroll
+        for (int t = 0; t < DC; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[t][r] *= resc;
+
+        // ---- O^T += V^T . P^T, four 16-key steps ----
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+#pragma unroll
+          for (int c2 = 0; c2 < 2; ++c2) {
+            const typename PV::vec pop = PV::pack(&s[st][8 * c2]);
+            const int kcol = st * 32 + 16 * c2 + 8 * h;  // storage position of the 8 keys
+#pragma unroll
+            for (int t = 0; t < DC; ++t) {
+              const typename PV::vec vop =
+                  *reinterpret_cast<const typename PV::vec*>(&sm.vt[buf][32 * t + l32][kcol]);
+              oacc[t] = PV::mfma(vop, pop, oacc[t]);
+            }
+          }
+      }
+    }
+
+    if (has_next) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  if constexpr (!DUMP) {
+    const float l = l_lane + __shfl_xor(l_lane, 32, 64);
+    if (m_ok) {
+      const float inv = (l > 0.f) ? 1.f / l : 0.f;
+      uint16_t* orow = reinterpret_cast<uint16_t*>(a.out) + ((int64_t)bh * M + mq) * D;
+#pragma unroll
+      for (int t = 0; t < DC; ++t)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          uint16_t hv[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float x = oacc[t][4 * g + e] * inv;
+            hv[e] = (VDT == SL8_DTYPE_F16) ? f2h_bits(x) : f2bf_bits(x);
+          }
+          uint2 pk;
+          pk.x = hv[0] | ((uint32_t)hv[1] << 16);
+          pk.y = hv[2] | ((uint32_t)hv[3] << 16);
+          *reinterpret_cast<uint2*>(orow + 32 * t + 8 * g + 4 * h) = pk;
+        }
+      if (LSE && h == 0)
+        a.lse[(int64_t)bh * M + mq] = (l > 0.f) ? (m_run * LN2F + logf(l)) : -INFINITY;
+    }
+  }
+}
+
+template <int D, bool CAUSAL, int VDT, bool DUMP, bool LSE>
+void launch_fwd(const FwdArgs& a, int grid, hipStream_t st) {
+  attn_fwd_kernel<D, CAUSAL, VDT, DUMP, LSE><<<grid, FWD_THREADS, 0, st>>>(a);
+}
+
+template <int D, int VDT, bool DUMP>
+void dispatch_causal_lse(const FwdArgs& a, int grid, bool causal, bool lse, hipStream_t st) {
+  if (causal) {
+    if (lse) launch_fwd<D, true, VDT, DUMP, true>(a, grid, st);
+    else launch_fwd<D, true, VDT, DUMP, false>(a, grid, st);
+  } else {
+    if (lse) launch_fwd<D, false, VDT, DUMP, true>(a, grid, st);
+    else launch_fwd<D, false, VDT, DUMP, false>(a, grid, st);
+  }
+}
+
+int64_t npad_of(int64_t N) { return (N + BN - 1) / BN * BN; }
+
+int launch_transpose(const void* v, uint16_t* vt, int64_t BHkv, int64_t N, int64_t D,
+                     hipStream_t st) {
+  const int64_t npad = npad_of(N);
+  const dim3 grid((unsigned)(npad / BN), (unsigned)BHkv);
+  if (D == 64)
+    v_transpose_kernel<64><<<grid, 256, 0, st>>>(static_cast<const uint16_t*>(v), vt, (int)N, (int)npad);
+  else
+    v_transpose_kernel<128><<<grid, 256, 0, st>>>(static_cast<const uint16_t*>(v), vt, (int)N, (int)npad);
+  SL8_CHECK_LAUNCH("attn_int8_fwd v transpose");
+  return SL8_OK;
+}
+
+int check_fwd_shape(int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N, int64_t D) {
+  SL8_CHECK_ARG(B >= 0 && Hq >= 0 && Hkv > 0 && M >= 0 && N >= 0, "fni8: bad shape");
+  SL8_CHECK_ARG(Hq % Hkv == 0, "fni8: H_q must be divisible by H_kv (GQA)");
+  SL8_CHECK_ARG(D == 64 || D == 128, "fni8: head dim must be 64/128, got %lld", (long long)D);
+  SL8_CHECK_ARG(M < (1 << 30) && N < (1 << 30) && B * Hq < (1 << 24), "fni8: shape too large");
+  return SL8_OK;
+}
+
+FwdArgs make_args(int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N, int& grid) {
+  FwdArgs a{};
+  a.M = (int)M;
+  a.N = (int)N;
+  a.Npad = (int)npad_of(N);
+  a.Hq = (int)Hq;
+  a.Hkv = (int)Hkv;
+  a.nqb = (int)((M + BM - 1) / BM);
+  a.window_left = -1;
+  grid = (int)(B * Hq * a.nqb);
+  a.xcd_map = ((B * Hkv) % 8 == 0) ? 1 : 0;
+  return a;
+}
+
+}  // namespace
+}  // namespace sl8
+
+using namespace sl8;
+
+extern "C" size_t sl8_attn_int8_fwd_workspace(int64_t B, int64_t Hkv, int64_t N, int64_t D) {
+  if (B <= 0 || Hkv <= 0 || N <= 0 || D <= 0) return 0;
+  return (size_t)(B * Hkv * D * npad_of(N)) * sizeof(uint16_t);
+}
+
+extern "C" int sl8_attn_int8_fwd(const int8_t* q, const float* q_scale, const int8_t* k,
+                                 const float* k_scale, const void* v, int v_dtype, void* out,
+                                 float* lse, int64_t B, int64_t Hq, int64_t Hkv, int64_t M,
+                                 int64_t N, int64_t D, int causal, int64_t window_left,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  int rc = check_fwd_shape(B, Hq, Hkv, M, N, D);
+  if (rc) return rc;
+  SL8_CHECK_ARG(v_dtype == SL8_DTYPE_F16 || v_dtype == SL8_DTYPE_BF16,
+                "fni8: v must be float16 or bfloat16");
+  SL8_CHECK_ARG(window_left >= -1 && window_left < (1LL << 30), "fni8: bad window_left");
+  if (B == 0 || Hq == 0 || M == 0) return SL8_OK;
+  SL8_CHECK_ARG(q && q_scale && out && (N == 0 || (k && k_scale && v)), "fni8: null pointer");
+  SL8_CHECK_ARG(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(out, 16),
+                "fni8: q/k/v/out must be 16-byte aligned");
+  const size_t need = sl8_attn_int8_fwd_workspace(B, Hkv, N, D);
+  SL8_CHECK_ARG(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 16)),
+                "fni8: attn_int8_fwd workspace needs %zu bytes", need);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (N > 0) {
+    rc = launch_transpose(v, static_cast<uint16_t*>(workspace), B * Hkv, N, D, st);
+    if (rc) return rc;
+  }
+  int grid;
+  FwdArgs a = make_args(B, Hq, Hkv, M, N, grid);
+  a.q = q; a.qs = q_scale; a.k = k; a.ks = k_scale;
+  a.vt = static_cast<const uint16_t*>(workspace);
+  a.out = out; a.lse = lse; a.window_left = (int)window_left;
+  const bool c = causal != 0, want_lse = lse != nullptr;
+  if (D == 64) {
+    if (v_dtype == SL8_DTYPE_F16) dispatch_causal_lse<64, SL8_DTYPE_F16, false>(a, grid, c, want_lse, st);
+    else dispatch_causal_lse<64, SL8_DTYPE_BF16, false>(a, grid, c, want_lse, st);
+  } else {
+    if (v_dtype == SL8_DTYPE_F16) dispatch_causal_lse<128, SL8_DTYPE_F16, false>(a, grid, c, want_lse, st);
+    else dispatch_causal_lse<128, SL8_DTYPE_BF16, false>(a, grid, c, want_lse, st);
+  }
+  SL8_CHECK_LAUNCH("attn_int8_fwd");
+  return SL8_OK;
+}
+
+extern "C" int sl8_attn_int8_qk_scores(const int8_t* q, const int8_t* k, int32_t* scores,
+                                       int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N,
+                                       int64_t D, void* stream) {
+  clear_error();
+  int rc = check_fwd_shape(B, Hq, Hkv, M, N, D);
+  if (rc) return rc;
+  if (B == 0 || Hq == 0 || M == 0 || N == 0) return SL8_OK;
+  SL8_CHECK_ARG(q && k && scores, "fni8: null pointer");
+  SL8_CHECK_ARG(aligned(q, 16) && aligned(k, 16), "fni8: q/k must be 16-byte aligned");
+  int grid;
+  FwdArgs a = make_args(B, Hq, Hkv, M, N, grid);
+  a.q = q; a.k = k; a.scores = scores;
+  // The dump path never reads V or the scales.
+  a.vt = nullptr;
+  a.qs = nullptr;
+  a.ks = nullptr;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (D == 64) launch_fwd<64, false, SL8_DTYPE_F16, true, false>(a, grid, st);
+  else launch_fwd<128, false, SL8_DTYPE_F16, true, false>(a, grid, st);
+  SL8_CHECK_LAUNCH("attn_int8_qk_scores");
+  return SL8_OK;
+}

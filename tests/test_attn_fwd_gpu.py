@@ -1,0 +1,181 @@
+"""GPU parity of the prefill attention (attn_int8_fwd) against the oracle.
+
+* int32 Q.K^T from the kernel's MFMA tiles: bit-exact.
+* kernel output on identical int8 inputs vs the oracle's float64 softmax/PV:
+  within the fp16-P rounding of the PV MFMA (cos >= 0.9999, rel-L1 <= 3e-3).
+* end to end (prologue + kernel) vs fp32 attention on the original fp16
+  inputs: the reference's int8 gate (cos >= 0.999, rel-L1 <= 0.02, 20 dB).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import superl8_amd as sl8
+from oracle import attention as oa
+from oracle import quant as oqn
+from superl8_amd import _C, quant
+from tests.tolerances import assert_close_abs, assert_finite, assert_int8_quality
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(x):
+    return x.detach().cpu().numpy()
+
+
+def _qkv(B, Hq, Hkv, M, N, D, device, dtype=torch.float16):
+    q = torch.randn(B, Hq, M, D, device=device, dtype=dtype)
+    k = torch.randn(B, Hkv, N, D, device=device, dtype=dtype)
+    v = torch.randn(B, Hkv, N, D, device=device, dtype=dtype)
+    return q, k, v
+
+
+def _v_f32(v):
+    if v.dtype == torch.bfloat16:
+        return oqn.bf16_bits_to_f32(_np(v.view(torch.int16)).view(np.uint16))
+    return _np(v.float())
+
+
+def _fp32_oracle(q, k, v, causal=False):
+    """reference tests/reference.py:26-54 (fp32 einsum attention, bottom-right causal)."""
+    return oa.attention_fp64(_np(q.float()), _np(k.float()), _np(v.float()), causal)
+
+
+QK_SHAPES = [(1, 2, 2, 128, 128, 64), (2, 4, 2, 257, 300, 64), (1, 4, 1, 1, 77, 128),
+             (1, 2, 2, 333, 129, 128), (1, 8, 8, 64, 1, 64)]
+
+
+@pytest.mark.parametrize("shape", QK_SHAPES)
+def test_qk_scores_bit_exact(device, shape):
+    B, Hq, Hkv, M, N, D = shape
+    q = torch.randint(-127, 128, (B, Hq, M, D), device=device, dtype=torch.int8)
+    k = torch.randint(-127, 128, (B, Hkv, N, D), device=device, dtype=torch.int8)
+    s = _C.attn_int8_qk_scores(q, k)
+    np.testing.assert_array_equal(_np(s), oa.scores_i32(_np(q), _np(k)))
+
+
+KERNEL_CASES = [
+    # B, Hq, Hkv, M, N, D, causal, window
+    (1, 2, 2, 128, 128, 64, False, -1),
+    (1, 2, 2, 128, 128, 64, True, -1),
+    (2, 4, 2, 257, 257, 64, True, -1),
+    (1, 4, 1, 100, 333, 128, True, -1),     # rectangular causal, MQA
+    (1, 2, 2, 333, 333, 128, False, -1),
+    (1, 4, 2, 200, 260, 64, True, 50),      # sliding window
+    (1, 2, 2, 64, 64, 128, False, 16),      # window without causal
+    (1, 2, 1, 5, 9, 64, True, 0),           # window 0: every row fully masked
+    (1, 2, 2, 300, 40, 64, True, -1),       # M > N: leading rows see nothing
+]
+
+
+@pytest.mark.parametrize("case", KERNEL_CASES)
+@pytest.mark.parametrize("vdt", [torch.float16, torch.bfloat16])
+def test_kernel_matches_oracle(device, case, vdt):
+    B, Hq, Hkv, M, N, D, causal, wl = case
+    q, k, v = _qkv(B, Hq, Hkv, M, N, D, device)
+    v = v.to(vdt)
+    q_i8, qs, k_i8, ks, _ = quant.quantize_qk(q, k)
+    qs, ks = qs.squeeze(-1).contiguous(), ks.squeeze(-1).contiguous()
+    out, lse = _C.attn_int8_fwd_train(q_i8, qs, k_i8, ks, v, causal) if wl < 0 else (
+        _C.attn_int8_fwd(q_i8, qs, k_i8, ks, v, causal, wl), None)
+    assert out.dtype == vdt and out.shape == (B, Hq, M, D)
+    ref, ref_lse = oa.attn_int8_fwd(_np(q_i8), _np(qs), _np(k_i8), _np(ks), _v_f32(v), causal, wl)
+    assert_finite(out)
+    tol = 1e-2 if vdt == torch.float16 else 4e-2
+    assert_close_abs(out, ref, atol=tol, what="attn_int8_fwd vs oracle")
+    if np.abs(ref).sum() > 0:
+        assert_int8_quality(out, ref, min_cos=0.9999 if vdt == torch.float16 else 0.999,
+                            max_rel_l1=3e-3 if vdt == torch.float16 else 1e-2, min_sqnr_db=40)
+    else:
+        assert not out.float().abs().sum().item()
+    if lse is not None:
+        finite = np.isfinite(ref_lse)
+        np.testing.assert_array_equal(np.isfinite(_np(lse)), finite)
+        np.testing.assert_allclose(_np(lse)[finite], ref_lse[finite], rtol=1e-5, atol=1e-5)
+
+
+SHAPES = [(1, 2, 128, 64), (2, 4, 512, 64), (2, 4, 257, 64), (1, 2, 333, 128),
+          (1, 8, 2048, 64), (1, 8, 2048, 128)]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("causal", [False, True])
+def test_end_to_end_quality(device, shape, causal):
+    """reference tests/test_attn_fwd.py:44-51."""
+    b, h, m, d = shape
+    q, k, v = _qkv(b, h, h, m, m, d, device)
+    out = sl8.attn_int8_fwd(q, k, v, causal=causal)
+    assert out.shape == q.shape and out.dtype == torch.float16
+    assert_int8_quality(out, _fp32_oracle(q, k, v, causal), what=f"{shape} causal={causal}")
+
+
+def test_gqa_rectangular_and_bf16(device):
+    q, k, v = _qkv(1, 8, 2, 96, 300, 128, device)
+    out = sl8.attn_int8_fwd(q, k, v, causal=True)
+    assert_int8_quality(out, _fp32_oracle(q, k, v, True), what="gqa rectangular")
+    qb, kb, vb = q.bfloat16(), k.bfloat16(), v.bfloat16()
+    outb = sl8.attn_int8_fwd(qb, kb, vb, causal=True)
+    assert outb.dtype == torch.bfloat16
+    assert_int8_quality(outb, _fp32_oracle(qb, kb, vb, True), what="bf16")
+
+
+def test_outlier_k_and_peaked_softmax(device):
+    """reference tests/test_attn_fwd.py:55-104."""
+    q, k, v = _qkv(2, 4, 4, 512, 512, 64, device)
+    k = k.clone()
+    k[..., 13] += 8.0
+    assert_int8_quality(sl8.attn_int8_fwd(q, k, v), _fp32_oracle(q, k, v), what="outlier-K")
+    q = torch.randn(1, 4, 256, 64, device=device, dtype=torch.float16)
+    k = torch.randn(1, 4, 256, 64, device=device, dtype=torch.float16) * 0.1
+    v = torch.randn(1, 4, 256, 64, device=device, dtype=torch.float16)
+    k[:, :, 0] += 4.0
+    k[:, :, 1] += 3.98
+    assert_int8_quality(sl8.attn_int8_fwd(q, k, v), _fp32_oracle(q, k, v), what="near-tie")
+
+
+def test_deterministic_and_rejects(device):
+    q, k, v = _qkv(2, 4, 4, 512, 512, 64, device)
+    r0 = sl8.attn_int8_fwd(q, k, v)
+    for _ in range(3):
+        assert torch.equal(sl8.attn_int8_fwd(q, k, v), r0)
+    q, k, v = _qkv(1, 2, 2, 128, 128, 96, device)
+    with pytest.raises(RuntimeError):
+        sl8.attn_int8_fwd(q, k, v)
+    q8 = torch.zeros(1, 2, 8, 64, device=device, dtype=torch.int8)
+    s = torch.ones(1, 2, 8, device=device)
+    with pytest.raises(RuntimeError, match="float16|bfloat16"):
+        _C.attn_int8_fwd(q8, s, q8, s, torch.zeros(1, 2, 8, 64, device=device))
+
+
+def test_accuracy_gate_and_rotate(device, monkeypatch):
+    """Gate: an outlier-dominated Q row routes to full precision (reference ops.py:115-147);
+    internal_accuracy_gate=False skips the detector; rotate=True keeps quality."""
+    q, k, v = _qkv(1, 4, 4, 257, 257, 128, device)
+    out = sl8.attn_int8_fwd(q, k, v, rotate=True, internal_accuracy_gate=False)
+    assert_int8_quality(out, _fp32_oracle(q, k, v), what="rotate")
+    q2 = q.clone()
+    q2[0, 0, 5, 7] = 500.0
+    called = {}
+    orig = _C.attn_int8_fwd
+    monkeypatch.setattr(_C, "attn_int8_fwd", lambda *a, **kw: called.setdefault("x", orig(*a, **kw)))
+    out2 = sl8.attn_int8_fwd(q2, k, v)
+    assert "x" not in called
+    assert_int8_quality(out2, _fp32_oracle(q2, k, v), min_cos=0.9999, what="gate fallback")
+
+
+def test_config2_shape_against_oracle(device):
+    """BASELINE config 2 (B1 Hq32 Hkv8 S4096 D128 causal), checked on a head subset."""
+    torch.manual_seed(2)
+    q, k, v = _qkv(1, 32, 8, 4096, 4096, 128, device)
+    q_i8, qs, k_i8, ks, _ = quant.quantize_qk(q, k)
+    qs, ks = qs.squeeze(-1).contiguous(), ks.squeeze(-1).contiguous()
+    out = _C.attn_int8_fwd(q_i8, qs, k_i8, ks, v, True)
+    for h in (0, 13, 31):
+        kvh = h // 4
+        ref, _ = oa.attn_int8_fwd(_np(q_i8[:, h:h + 1]), _np(qs[:, h:h + 1]),
+                                  _np(k_i8[:, kvh:kvh + 1]), _np(ks[:, kvh:kvh + 1]),
+                                  _np(v[:, kvh:kvh + 1].float()), True)
+        assert_int8_quality(out[:, h:h + 1], ref, min_cos=0.9999, max_rel_l1=3e-3, min_sqnr_db=40,
+                            what=f"config2 head {h}")

@@ -1,0 +1,101 @@
+"""GPU parity of split-KV decode against the oracle's per-split partials + LSE merge."""
+import numpy as np
+import pytest
+import torch
+
+import superl8_amd as sl8
+from oracle import attention as oa
+from superl8_amd import _C, quant
+from tests.tolerances import assert_close_abs, assert_finite, assert_int8_quality
+
+pytestmark = pytest.mark.gpu
+
+DECODE_SHAPES = [  # reference tests/test_decode.py:28-43
+    (1, 8, 8, 512, 64), (4, 8, 8, 1024, 128), (1, 16, 4, 2000, 128), (2, 8, 1, 777, 64),
+    (1, 32, 8, 4096, 128), (1, 4, 4, 512, 256), (2, 8, 2, 1024, 256), (1, 16, 4, 777, 256),
+    (1, 32, 1, 300, 128),  # MQA with 32 query heads per KV head
+    (3, 6, 2, 5, 64),      # fewer keys than splits
+]
+
+
+def _np(x):
+    return x.detach().cpu().numpy()
+
+
+def _qkv(shape, device):
+    b, hq, hkv, n, d = shape
+    q = torch.randn(b, hq, 1, d, device=device, dtype=torch.float16)
+    k = torch.randn(b, hkv, n, d, device=device, dtype=torch.float16)
+    v = torch.randn(b, hkv, n, d, device=device, dtype=torch.float16)
+    return q, k, v
+
+
+def _prep(q, k):
+    q_i8, qs, k_i8, ks, _ = quant.quantize_qk(q, k)
+    return q_i8, qs.reshape(q.shape[0], q.shape[1], 1).contiguous(), k_i8, ks.squeeze(-1).contiguous()
+
+
+@pytest.mark.parametrize("shape", DECODE_SHAPES)
+@pytest.mark.parametrize("ns", [-1, 1, 16, 256])
+def test_kernel_matches_oracle(device, shape, ns):
+    q, k, v = _qkv(shape, device)
+    q_i8, qs, k_i8, ks = _prep(q, k)
+    out = _C.attn_int8_decode(q_i8, qs, k_i8, ks, v, ns)
+    n_splits = ns if ns > 0 else _C.choose_n_splits(shape[3], shape[0], shape[2])
+    ref = oa.attn_int8_decode(_np(q_i8)[:, :, 0], _np(qs)[:, :, 0], _np(k_i8), _np(ks),
+                              _np(v.float()), n_splits)
+    assert out.shape == q.shape and out.dtype == torch.float16
+    assert_close_abs(out[:, :, 0], ref, atol=2e-3, rtol=2e-3, what=f"decode {shape} ns={ns}")
+
+
+@pytest.mark.parametrize("shape", DECODE_SHAPES[:8])
+def test_end_to_end_quality(device, shape):
+    q, k, v = _qkv(shape, device)
+    out = sl8.attn_int8_decode(q, k, v)
+    ref = oa.attention_fp64(_np(q.float()), _np(k.float()), _np(v.float()))
+    assert_finite(out)
+    assert_int8_quality(out, ref, what=f"decode {shape}")
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_decode_matches_prefill(device, d):
+    """reference tests/test_decode.py:60-66."""
+    from tests.tolerances import cos_sim
+
+    q, k, v = _qkv((2, 8, 2, 1536, d), device)
+    a = sl8.attn_int8_decode(q, k, v)
+    b = sl8.attn_int8_fwd(q, k, v)
+    assert cos_sim(a, b) >= 0.999
+
+
+def test_deterministic_and_validation(device):
+    q, k, v = _qkv((2, 8, 8, 1024, 64), device)
+    r0 = sl8.attn_int8_decode(q, k, v)
+    for _ in range(3):
+        assert torch.equal(sl8.attn_int8_decode(q, k, v), r0)
+    q_i8, qs, k_i8, ks = _prep(q, k)
+    with pytest.raises(RuntimeError, match="num_splits"):
+        _C.attn_int8_decode(q_i8, qs, k_i8, ks, v, 0)
+    with pytest.raises(RuntimeError, match="num_splits"):
+        _C.attn_int8_decode(q_i8, qs, k_i8, ks, v, 257)
+    empty = _C.attn_int8_decode(q_i8, qs, k_i8[:, :, :0].contiguous(), ks[:, :, :0].contiguous(),
+                                v[:, :, :0].contiguous(), -1)
+    assert not empty.any()
+
+
+def test_config3_shape_against_oracle(device):
+    """BASELINE config 3 (B16 Hq32 Hkv8 N32768 D128, 16 splits), checked on 2 sequences."""
+    torch.manual_seed(3)
+    B, Hq, Hkv, N, D = 16, 32, 8, 32768, 128
+    q = torch.randn(B, Hq, 1, D, device=device, dtype=torch.float16)
+    k_i8 = torch.randint(-127, 128, (B, Hkv, N, D), device=device, dtype=torch.int8)
+    ks = torch.rand(B, Hkv, N, device=device) * 0.02
+    v = torch.randn(B, Hkv, N, D, device=device, dtype=torch.float16)
+    q_i8, qs = _C.quantize_i8_rowwise(q.reshape(-1, D))
+    qs = (qs * 0.1275).reshape(B, Hq, 1).contiguous()
+    q_i8 = q_i8.reshape(B, Hq, 1, D)
+    out = _C.attn_int8_decode(q_i8, qs, k_i8, ks, v, 16)
+    for b in (0, 15):
+        ref = oa.attn_int8_decode(_np(q_i8[b:b + 1])[:, :, 0], _np(qs[b:b + 1])[:, :, 0],
+                                  _np(k_i8[b:b + 1]), _np(ks[b:b + 1]), _np(v[b:b + 1].float()), 16)
+        assert_close_abs(out[b:b + 1, :, 0], ref, atol=2e-3, rtol=2e-3, what=f"config3 b={b}")
