@@ -1,0 +1,240 @@
+"""Benchmark of the INT8 attention / Q4_K hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-secondary]
+
+A "step" is one `_C.attn_int8_fwd` call (the V^T staging kernel plus the
+prefill kernel) at BASELINE config 2: B=1, Hq=32, Hkv=8, S=4096, D=128,
+causal, on seeded synthetic N(0,1) fp16 Q/K/V quantised by the prologue
+beforehand (inputs resident in HBM when the timed region starts).
+`value` = algorithmic ops per step / step time, in TOPS, where the ops are
+the reference harness's attention_flops(causal) = 2*B*H*S*S*D
+(bench/harness.py:220-223 of the reference).
+
+Also reported (under "secondary"): split-KV decode at config 3 and the Q4_K
+GEMV at config 4 (M=1 and M=8), as HBM GB/s over their algorithmic bytes,
+and (under "cpu_baseline") the numpy restatement of config 1 timed on the
+host cores. One JSON line is printed on stdout.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+
+PEAK_INT8_TOPS = 5000.0  # MI355X dense INT8 MFMA (vendor)
+PEAK_HBM_GBS = 8000.0    # MI355X HBM3E
+
+CFG2 = dict(B=1, Hq=32, Hkv=8, S=4096, D=128)
+CFG2_OPS = 4 * 1 * 32 * 4096 * 4096 * 128 // 2  # 137,438,953,472
+
+
+def _events_time(fn, iters, stream):
+    """Average ms per call of fn(), HIP events on `stream` around the whole batch."""
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(iters):
+        fn()
+    e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / iters
+
+
+def bench_prefill(steps, warmup):
+    from superl8_amd import _C, quant
+
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(2)
+    q = torch.randn(1, 32, 4096, 128, device=dev, dtype=torch.float16, generator=g)
+    k = torch.randn(1, 8, 4096, 128, device=dev, dtype=torch.float16, generator=g)
+    v = torch.randn(1, 8, 4096, 128, device=dev, dtype=torch.float16, generator=g)
+    q_i8, qs, k_i8, ks, _ = quant.quantize_qk(q, k)
+    qs, ks = qs.squeeze(-1).contiguous(), ks.squeeze(-1).contiguous()
+
+    def step():
+        return _C.attn_int8_fwd(q_i8, qs, k_i8, ks, v, True)
+
+    for _ in range(warmup):
+        step()
+    stream = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ms = _events_time(step, steps, stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    return ms, wall
+
+
+def bench_decode(iters=20):
+    from superl8_amd import _C
+
+    dev = "cuda"
+    B, Hq, Hkv, N, D = 16, 32, 8, 32768, 128
+    g = torch.Generator(device=dev).manual_seed(3)
+    q = torch.randn(B * Hq, D, device=dev, dtype=torch.float16, generator=g)
+    k = torch.randn(B * Hkv * N, D, device=dev, dtype=torch.float16, generator=g)
+    q_i8, qs = _C.quantize_i8_rowwise(q)
+    k_i8, ks = _C.quantize_i8_rowwise(k)  # per-token int8 K cache
+    del k
+    q_i8 = q_i8.reshape(B, Hq, 1, D)
+    qs = (qs * (1.0 / np.sqrt(D) * np.log2(np.e))).reshape(B, Hq, 1).contiguous()
+    k_i8 = k_i8.reshape(B, Hkv, N, D)
+    ks = ks.reshape(B, Hkv, N)
+    v = torch.randn(B, Hkv, N, D, device=dev, dtype=torch.float16, generator=g)
+    fn = lambda: _C.attn_int8_decode(q_i8, qs, k_i8, ks, v, 16)  # noqa: E731
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    ms = _events_time(fn, iters, torch.cuda.current_stream())
+    nbytes = k_i8.numel() + ks.numel() * 4 + v.numel() * 2 + q_i8.numel() + qs.numel() * 4 \
+        + B * Hq * D * 2
+    return ms, nbytes
+
+
+def bench_gemv(M, iters_graph=10, copies=8):
+    from oracle import q4k as oq  # synthetic GGUF bytes generator (data only)
+    from superl8_amd import _C
+
+    dev = "cuda"
+    N, K = 17408, 5120
+    base = torch.from_numpy(oq.random_weights(N, K, seed=4)).to(dev)
+    ws = [base] + [base.roll(i * 1, 0).contiguous() for i in range(1, copies)]  # > 256 MB MALL
+    g = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randn(M, K, device=dev, dtype=torch.float16, generator=g)
+    x_i8, xs = _C.quantize_i8_rowwise(x)
+    for w in ws:
+        _C.gemm_decode_q4k(x_i8, xs, w)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    per_graph = 8 * copies
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            for i in range(per_graph):
+                _C.gemm_decode_q4k(x_i8, xs, ws[i % copies])
+    for _ in range(2):
+        graph.replay()
+    torch.cuda.synchronize()
+    cur = torch.cuda.current_stream()
+    ms = _events_time(graph.replay, iters_graph, cur) / per_graph
+    nbytes = N * (K // 256) * 144 + M * K + M * 4 + M * N * 2
+    return ms, nbytes
+
+
+def cpu_baseline(budget_s=12.0):
+    """numpy restatement (oracle) of config 1: prologue + causal attention,
+    B=1, H=8, S=512, D=64, timed on this host; trimmed median over repeats."""
+    from oracle import attention as oa
+    from oracle import quant as oqn
+
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover
+        threads = os.cpu_count() or 1
+    rng = np.random.default_rng(1)
+    q, k, v = (rng.standard_normal((1, 8, 512, 64)).astype(np.float16) for _ in range(3))
+
+    def run():
+        q_i8, qs, k_i8, ks, _ = oqn.quantize_qk(q, k)
+        return oa.attn_int8_fwd(q_i8, qs, k_i8, ks, v.astype(np.float32), True)
+
+    run()
+    samples = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end and len(samples) < 200:
+        t0 = time.perf_counter()
+        run()
+        samples.append(time.perf_counter() - t0)
+    samples.sort()
+    k_trim = max(1, len(samples) // 10) if len(samples) > 4 else 0
+    trimmed = samples[k_trim:len(samples) - k_trim] if k_trim else samples
+    med = float(np.median(trimmed))
+    ops = 4 * 1 * 8 * 512 * 512 * 64 // 2
+    return {
+        "value": round(ops / med / 1e9, 3),
+        "unit": "GOPS",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"config 1 (B1 H8 S512 D64 causal, quantize_qk + attention), numpy oracle, "
+                  f"{len(samples)} runs, trimmed median {med * 1e3:.1f} ms/run",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(see the sharding plan in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+
+    ms, wall = bench_prefill(args.steps, args.warmup)
+    tops = CFG2_OPS / (ms * 1e-3) / 1e12
+    out = {
+        "metric": "INT8 attn fwd TOPS (%MFMA peak); decode + Q4_K GEMV HBM GB/s (%peak)",
+        "value": round(tops, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 QK^T / fp16 PV",
+        "data": "synthetic (seeded N(0,1) fp16 Q/K/V, int8 per-row quantised with K smoothing)",
+        "config": {"workload": "attn_int8_fwd prefill, BASELINE config 2", "batch": 1,
+                   "heads_q": 32, "heads_kv": 8, "seq_len": 4096, "head_dim": 128,
+                   "causal": True},
+        "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": PEAK_INT8_TOPS,
+                     "unit": "TOP/s", "frac": round(tops / PEAK_INT8_TOPS, 4),
+                     "traffic": _traffic("attn_int8_fwd")},
+    }
+    if not args.no_secondary:
+        sec = {}
+        dms, dbytes = bench_decode()
+        gbs = dbytes / (dms * 1e-3) / 1e9
+        sec["attn_int8_decode_cfg3"] = {"us": round(dms * 1e3, 2), "GB/s": round(gbs, 1),
+                                        "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+                                        "bytes": dbytes}
+        for M in (1, 8):
+            gms, gbytes = bench_gemv(M)
+            gbs = gbytes / (gms * 1e-3) / 1e9
+            sec[f"gemm_decode_q4k_cfg4_m{M}"] = {"us": round(gms * 1e3, 2), "GB/s": round(gbs, 1),
+                                                 "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+                                                 "bytes": gbytes}
+        out["secondary"] = sec
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+
+
+def _traffic(kernel: str):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, if present."""
+    path = os.path.join(HERE, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(kernel)
+    except (OSError, ValueError):
+        return None
+
+
+if __name__ == "__main__":
+    main()

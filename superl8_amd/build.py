@@ -29,6 +29,8 @@ COMMON_FLAGS = [
     "-mcode-object-version=5",
     # packed-FP32 VALU forms are kept out of every kernel
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # keep per-thread arrays (MFMA operands) in VGPRs, never in LDS
+    "-mllvm", "-disable-promote-alloca-to-lds",
     f"-I{INCLUDE}",
     "-Wno-unused-command-line-argument",
 ]

@@ -45,8 +45,6 @@ constexpr int FWD_THREADS = 256;
 constexpr int FWD_WAVES = 4;
 constexpr int BM = 128;  // queries per workgroup
 constexpr int BN = 64;   // keys per tile
-constexpr int KPAD = 16; // bytes of padding per K row in LDS
-constexpr int VPAD = 8;  // halves of padding per V^T row in LDS
 constexpr float LN2F = 0.6931471805599453f;
 
 // key index inside a 16-key group -> storage position (swap bits 2 and 3)
@@ -122,266 +120,323 @@ struct FwdArgs {
   int xcd_map;         // 1: XCD-aware block order
 };
 
+// LDS tiles are dense; 16-byte chunks are XOR-swizzled within each row
+// (chunk c of row r is stored at c ^ (r % chunks_per_row)) so that the
+// MFMA operand reads of 8 consecutive rows hit distinct banks.
 template <int D>
 struct FwdSmem {
-  int8_t k[2][BN][D + KPAD];
-  uint16_t vt[2][D][BN + VPAD];
-  float ks[2][BN];
+  __attribute__((aligned(16))) int8_t k[2][BN * D];
+  __attribute__((aligned(16))) uint16_t vt[2][D * BN];
+  __attribute__((aligned(16))) float ks[3][BN];
 };
 
-// blockIdx.x -> (b*Hq + h, query block), heaviest query block first.
-__device__ __forceinline__ void block_coords(const FwdArgs& a, int& bh, int& qb) {
+typedef __attribute__((address_space(1))) const void* gptr_t;
+typedef __attribute__((address_space(3))) void* lptr_t;
+
+// Direct global -> LDS copy: lane i of the wave writes `bytes` at lds + i*bytes.
+__device__ __forceinline__ void dma16_to_lds(const void* g, void* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((gptr_t)g, (lptr_t)lds_wave_base, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4_to_lds(const void* g, void* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds((gptr_t)g, (lptr_t)lds_wave_base, 4, 0, 0);
+}
+__device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+
+// blockIdx.x -> (b*Hq + h, query-block slot), heaviest slot first.
+__device__ __forceinline__ void block_coords(const FwdArgs& a, int nslot, int& bh, int& slot) {
   const int id = blockIdx.x;
   const int total = gridDim.x;
   const int gsz = a.Hq / a.Hkv;
-  const int nbkv = total / (a.nqb * gsz);  // B * Hkv
   if (a.xcd_map) {
-    // id = 8*slot + xcd; XCD x serves KV heads {x, x+8, ...}
-    const int xcd = id & 7, slot = id >> 3;
-    const int kv_per_xcd = nbkv / 8;
-    const int per_qb = kv_per_xcd * gsz;
-    const int r = slot / per_qb;         // rank of the query block (0 = heaviest)
-    const int rem = slot % per_qb;
+    // id = 8*k + xcd; XCD x serves KV heads {x, x+8, ...}
+    const int nbkv = total / (nslot * gsz);  // B * Hkv
+    const int xcd = id & 7, k = id >> 3;
+    const int per_slot = (nbkv / 8) * gsz;
+    const int r = k / per_slot;
+    const int rem = k % per_slot;
     const int bkv = xcd + 8 * (rem / gsz);
     const int j = rem % gsz;
     const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
     bh = b * a.Hq + kvh * gsz + j;
-    qb = a.nqb - 1 - r;
+    slot = r;
   } else {
-    const int nbh = total / a.nqb;
-    qb = a.nqb - 1 - id / nbh;
+    const int nbh = total / nslot;
+    slot = id / nbh;
     bh = id % nbh;
+  }
+}
+
+template <int DC>
+struct QOp {
+  v4i c[DC];
+};
+
+// S^T tile (64 keys x 32 queries) of one wave: two 32-key MFMA accumulators.
+// kt: the lane's K row base in LDS; koff[ch]: swizzled byte offset of chunk ch.
+template <int D>
+__device__ __forceinline__ void qk_tile(const int8_t* kt, const int (&koff)[D / 32],
+                                        const QOp<D / 32>& q, v16i& s0, v16i& s1) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    s0[r] = 0;
+    s1[r] = 0;
+  }
+#pragma unroll
+  for (int ch = 0; ch < D / 32; ++ch) {
+    const v4i k0 = *reinterpret_cast<const v4i*>(kt + koff[ch]);
+    const v4i k1 = *reinterpret_cast<const v4i*>(kt + 32 * D + koff[ch]);
+    s0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(k0, q.c[ch], s0, 0, 0, 0);
+    s1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(k1, q.c[ch], s1, 0, 0, 0);
   }
 }
 
 template <int D, bool CAUSAL, int VDT, bool DUMP, bool LSE>
 __global__ void __launch_bounds__(FWD_THREADS, 2)
 attn_fwd_kernel(const FwdArgs a) {
-  constexpr int DC = D / 32;  // 32-channel chunks
+  constexpr int DC = D / 32;                          // 32-channel chunks
+  constexpr int KCH = BN * D / 16 / FWD_THREADS;      // 16-B K chunks per thread
+  constexpr int VCH = D * BN * 2 / 16 / FWD_THREADS;  // 16-B V^T chunks per thread
+  static_assert(KCH >= 1 && VCH >= 1, "tile copies cover D in {64,128}");
   __shared__ FwdSmem<D> sm;
   using PV = PvOp<VDT>;
 
-  int bh, qb;
-  block_coords(a, bh, qb);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // Causal launches pair query block qb with nqb-1-qb so every workgroup
+  // does the same amount of work.
+  const int nslot = CAUSAL ? (a.nqb + 1) / 2 : a.nqb;
+  int bh, slot;
+  block_coords(a, nslot, bh, slot);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, l32 = lane & 31;
   const int gsz = a.Hq / a.Hkv;
   const int b = bh / a.Hq, hq = bh % a.Hq;
   const int64_t bkv = (int64_t)b * a.Hkv + hq / gsz;
   const int M = a.M, N = a.N;
   const int diag = CAUSAL ? N - M : 0;
-
-  const int m_blk = qb * BM;
-  const int mq = m_blk + wave * 32 + l32;  // this lane's query
-  const bool m_ok = mq < M;
-  const int qpos = mq + diag;
-
-  // Q as the B operand: 32 channels per chunk, 16 bytes per lane
-  v4i qop[DC];
-  {
-    const int8_t* qrow = a.q + ((int64_t)bh * M + (m_ok ? mq : 0)) * D + 16 * h;
-#pragma unroll
-    for (int c = 0; c < DC; ++c) {
-      qop[c] = m_ok ? *reinterpret_cast<const v4i*>(qrow + 32 * c) : v4i{0, 0, 0, 0};
-    }
-  }
-  const float qsc = (m_ok && !DUMP) ? a.qs[(int64_t)bh * M + mq] : 0.f;
-
-  // key range of the workgroup and of this wave
-  int n_end = N;
-  if (CAUSAL) n_end = max(0, min(N, m_blk + BM + diag));
-  int n_beg = 0;
-  if (a.window_left >= 0) n_beg = max(0, m_blk + diag - a.window_left + 1) & ~(BN - 1);
-  const int wq_lo = m_blk + wave * 32 + diag;  // first query position of the wave
-  const int wq_hi = wq_lo + 31;
+  const int wl = a.window_left;
 
   const int8_t* kb = a.k + bkv * (int64_t)N * D;
   const float* ksb = a.ks + bkv * (int64_t)N;
   const uint16_t* vtb = a.vt + bkv * (int64_t)D * a.Npad;
 
-  // per-thread staging slots
-  constexpr int KCH = BN * D / 16 / FWD_THREADS;  // 16-B K chunks per thread
-  constexpr int VCH = D * BN * 2 / 16 / FWD_THREADS;
-  uint4 kreg[KCH], vreg[VCH];
-  float ksreg = 0.f;
+  int qbs[2];
+  int npass = 1;
+  qbs[0] = a.nqb - 1 - slot;
+  qbs[1] = slot;
+  if (CAUSAL) npass = (qbs[1] != qbs[0]) ? 2 : 1;
 
-  auto load_tile = [&](int n0) {
+  // LDS operand offsets (swizzled chunks), fixed for the whole kernel
+  constexpr int KCPR = D / 16;  // 16-B chunks per K row
+  int koff[DC], voff[4];
 #pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int idx = tid + i * FWD_THREADS;
-      const int r = idx / (D / 16), c = (idx % (D / 16)) * 16;
-      kreg[i] = (n0 + r < N) ? *reinterpret_cast<const uint4*>(kb + (int64_t)(n0 + r) * D + c)
-                             : uint4{0, 0, 0, 0};
-    }
-    if constexpr (!DUMP) {
+  for (int ch = 0; ch < DC; ++ch) koff[ch] = ((2 * ch + h) ^ (l32 & (KCPR - 1))) * 16;
 #pragma unroll
-      for (int i = 0; i < VCH; ++i) {
-        const int idx = tid + i * FWD_THREADS;
-        const int d = idx / (BN / 8), c = (idx % (BN / 8)) * 8;
-        vreg[i] = *reinterpret_cast<const uint4*>(vtb + (int64_t)d * a.Npad + n0 + c);
+  for (int c4 = 0; c4 < 4; ++c4) voff[c4] = ((2 * c4 + h) ^ (l32 & 7)) * 8;  // in halves
+
+  for (int pass = 0; pass < npass; ++pass) {
+    const int m_blk = qbs[pass] * BM;
+    const int mq = m_blk + wave * 32 + l32;  // this lane's query
+    const bool m_ok = mq < M;
+    const int qpos = mq + diag;
+
+    QOp<DC> qop;
+    {
+      const int8_t* qrow = a.q + ((int64_t)bh * M + (m_ok ? mq : M - 1)) * D + 16 * h;
+#pragma unroll
+      for (int c = 0; c < DC; ++c) {
+        qop.c[c] = *reinterpret_cast<const v4i*>(qrow + 32 * c);
+        if (!m_ok) qop.c[c] = v4i{0, 0, 0, 0};
       }
-      if (tid < BN) ksreg = (n0 + tid < N) ? ksb[n0 + tid] : 0.f;
     }
-  };
-  auto store_tile = [&](int buf) {
+    // rows past M use scale 1 so no NaN appears in their (unstored) lanes
+    const float qsc = (m_ok && !DUMP) ? a.qs[(int64_t)bh * M + mq] : 1.f;
+
+    // key tiles of the workgroup: [n_beg, n_end)
+    int n_end = N;
+    if (CAUSAL) n_end = max(0, min(N, m_blk + BM + diag));
+    int n_beg = 0;
+    if (wl >= 0) n_beg = min(n_end, max(0, m_blk + diag - wl + 1) & ~(BN - 1));
+    const int ntiles = (n_end - n_beg + BN - 1) / BN;
+    const int wq_lo = m_blk + wave * 32 + diag;  // first query position of the wave
+    const int wq_hi = wq_lo + 31;
+    auto live = [&](int n0) {
+      bool ok = true;
+      if (CAUSAL && n0 > wq_hi) ok = false;
+      if (wl >= 0 && n0 + BN - 1 <= wq_lo - wl) ok = false;
+      return DUMP || ok;
+    };
+
+    // global -> LDS tile copies (no staging registers)
+#define SL8_LOAD_K(N0, KB, SB)                                                            \
+    do {                                                                                  \
+      _Pragma("unroll") for (int i = 0; i < KCH; ++i) {                                   \
+        const int slot = i * FWD_THREADS + tid;                                           \
+        const int row = slot / KCPR;                                                      \
+        const int c = (slot % KCPR) ^ (row & (KCPR - 1));                                 \
+        dma16_to_lds(kb + (int64_t)min((N0) + row, N - 1) * D + 16 * c,                 \
+                       &sm.k[KB][(i * FWD_THREADS + wave * 64) * 16]);                    \
+      }                                                                                   \
+      if (!DUMP && wave == 0) dma4_to_lds(ksb + min((N0) + lane, N - 1), &sm.ks[SB][0]); \
+    } while (0)
+#define SL8_LOAD_V(N0, VB)                                                                \
+    do {                                                                                  \
+      if constexpr (!DUMP) {                                                              \
+        _Pragma("unroll") for (int i = 0; i < VCH; ++i) {                                 \
+          const int slot = i * FWD_THREADS + tid;                                         \
+          const int row = slot / 8;                                                       \
+          const int c = (slot % 8) ^ (row & 7);                                           \
+          dma16_to_lds(vtb + (int64_t)row * a.Npad + (N0) + 8 * c,                      \
+                         &sm.vt[VB][(i * FWD_THREADS + wave * 64) * 8]);                  \
+        }                                                                                 \
+      }                                                                                   \
+    } while (0)
+
+    v16f oacc[DC];
 #pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int idx = tid + i * FWD_THREADS;
-      const int r = idx / (D / 16), c = (idx % (D / 16)) * 16;
-      *reinterpret_cast<uint4*>(&sm.k[buf][r][c]) = kreg[i];
+    for (int t = 0; t < DC; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) oacc[t][r] = 0.f;
+    float m_run = -INFINITY, l_lane = 0.f;
+
+    // Pipeline: while the softmax and P.V of tile j run, the MFMAs of
+    // S_{j+1} are already in flight and tile j+2's K / tile j+1's V loads are
+    // outstanding. LDS: K double buffered (K_{j+1} resident at iteration j),
+    // V double buffered, k_scale triple buffered; one barrier per tile.
+    if (ntiles > 0) {
+      SL8_LOAD_K(n_beg, 0, 0);
+      SL8_LOAD_V(n_beg, 0);
+      if (ntiles > 1) SL8_LOAD_K(n_beg + BN, 1, 1);
     }
-    if constexpr (!DUMP) {
-#pragma unroll
-      for (int i = 0; i < VCH; ++i) {
-        const int idx = tid + i * FWD_THREADS;
-        const int d = idx / (BN / 8), c = (idx % (BN / 8)) * 8;
-        *reinterpret_cast<uint4*>(&sm.vt[buf][d][c]) = vreg[i];
-      }
-      if (tid < BN) sm.ks[buf][tid] = ksreg;
-    }
-  };
+    wait_dma();
+    __syncthreads();
 
-  v16f oacc[DC];
-#pragma unroll
-  for (int t = 0; t < DC; ++t)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) oacc[t][r] = 0.f;
-  float m_run = -INFINITY, l_lane = 0.f;
+    v16i sc0, sc1;  // S_j
+    if (ntiles > 0 && live(n_beg)) qk_tile<D>(&sm.k[0][l32 * D], koff, qop, sc0, sc1);
 
-  if (n_beg < n_end) {
-    load_tile(n_beg);
-    store_tile(0);
-  }
-  __syncthreads();
+    for (int j = 0; j < ntiles; ++j) {
+      const int n0 = n_beg + j * BN;
+      const int kb_cur = j & 1, sb_cur = j % 3;
+      // buffers last read in iteration j-1 receive tiles j+2 (K) and j+1 (V)
+      if (j + 2 < ntiles) SL8_LOAD_K(n0 + 2 * BN, kb_cur, (j + 2) % 3);
+      if (j + 1 < ntiles) SL8_LOAD_V(n0 + BN, kb_cur ^ 1);
 
-  int buf = 0;
-  for (int n0 = n_beg; n0 < n_end; n0 += BN, buf ^= 1) {
-    const bool has_next = n0 + BN < n_end;
-    if (has_next) load_tile(n0 + BN);
+      // S_{j+1}: issue its MFMAs before the softmax of tile j
+      v16i sn0, sn1;
+      if (j + 1 < ntiles && live(n0 + BN)) qk_tile<D>(&sm.k[kb_cur ^ 1][l32 * D], koff, qop, sn0, sn1);
 
-    // does this wave see any key of the tile?
-    bool wave_live = true;
-    if (CAUSAL && n0 > wq_hi) wave_live = false;
-    if (a.window_left >= 0 && n0 + BN - 1 <= wq_lo - a.window_left) wave_live = false;
-    if (DUMP) wave_live = true;
-
-    if (wave_live) {
-      // ---- S^T = K . Q^T, two 32-key sub-tiles ----
-      v16i sacc[2];
-#pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        v16i c = {0};
-#pragma unroll
-        for (int r = 0; r < 16; ++r) c[r] = 0;
-#pragma unroll
-        for (int ch = 0; ch < DC; ++ch) {
-          const v4i kop = *reinterpret_cast<const v4i*>(&sm.k[buf][st * 32 + l32][32 * ch + 16 * h]);
-          c = __builtin_amdgcn_mfma_i32_32x32x32_i8(kop, qop[ch], c, 0, 0, 0);
-        }
-        sacc[st] = c;
-      }
-
-      if constexpr (DUMP) {
-        if (m_ok) {
-          int32_t* srow = a.scores + ((int64_t)bh * M + mq) * N;
-#pragma unroll
-          for (int st = 0; st < 2; ++st)
+      if (live(n0)) {
+        if constexpr (DUMP) {
+          if (m_ok) {
+            int32_t* srow = a.scores + ((int64_t)bh * M + mq) * N;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-              const int n = n0 + st * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-              if (n < N) srow[n] = sacc[st][r];
+              const int n = n0 + 8 * (r >> 2) + 4 * h + (r & 3);
+              if (n < N) srow[n] = sc0[r];
+              if (n + 32 < N) srow[n + 32] = sc1[r];
             }
-        }
-      } else {
-        // ---- logits, mask, running max ----
-        const bool need_mask = (n0 + BN > N) || (CAUSAL && n0 + BN - 1 > wq_lo) ||
-                               (a.window_left >= 0 && n0 <= wq_hi - a.window_left);
-        float s[2][16];
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int st = 0; st < 2; ++st)
+          }
+        } else {
+          // t = acc * k_scale; logit = t * q_scale (q_scale > 0, so max(t) gives max(logit))
+          float t[32];
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
-            const int kl = st * 32 + 8 * g + 4 * h;
-            const float4 k4 = *reinterpret_cast<const float4*>(&sm.ks[buf][kl]);
-            const float kk[4] = {k4.x, k4.y, k4.z, k4.w};
+            const float4 ka = *reinterpret_cast<const float4*>(&sm.ks[sb_cur][8 * g + 4 * h]);
+            const float4 kc = *reinterpret_cast<const float4*>(&sm.ks[sb_cur][32 + 8 * g + 4 * h]);
+            t[4 * g + 0] = (float)sc0[4 * g + 0] * ka.x;
+            t[4 * g + 1] = (float)sc0[4 * g + 1] * ka.y;
+            t[4 * g + 2] = (float)sc0[4 * g + 2] * ka.z;
+            t[4 * g + 3] = (float)sc0[4 * g + 3] * ka.w;
+            t[16 + 4 * g + 0] = (float)sc1[4 * g + 0] * kc.x;
+            t[16 + 4 * g + 1] = (float)sc1[4 * g + 1] * kc.y;
+            t[16 + 4 * g + 2] = (float)sc1[4 * g + 2] * kc.z;
+            t[16 + 4 * g + 3] = (float)sc1[4 * g + 3] * kc.w;
+          }
+          const bool need_mask = (n0 + BN > N) || (CAUSAL && n0 + BN - 1 > wq_lo) ||
+                                 (wl >= 0 && n0 <= wq_hi - wl);
+          if (need_mask) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              float x = ((float)sacc[st][4 * g + e] * qsc) * kk[e];
-              if (need_mask) {
-                const int n = n0 + kl + e;
-                bool ok = n < N;
-                if (CAUSAL) ok = ok && n <= qpos;
-                if (a.window_left >= 0) ok = ok && n > qpos - a.window_left;
-                x = ok ? x : -INFINITY;
-              }
-              s[st][4 * g + e] = x;
-              tmax = fmaxf(tmax, x);
+            for (int e = 0; e < 32; ++e) {
+              const int n = n0 + 32 * (e >> 4) + 8 * ((e & 15) >> 2) + 4 * h + (e & 3);
+              bool ok = n < N;
+              if (CAUSAL) ok = ok && n <= qpos;
+              if (wl >= 0) ok = ok && n > qpos - wl;
+              t[e] = ok ? t[e] : -INFINITY;
             }
           }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const float m_new = fmaxf(m_run, tmax);
-        const float resc = (m_run == -INFINITY || m_new == -INFINITY) ? 1.f : exp2f(m_run - m_new);
-        const float msub = (m_new == -INFINITY) ? 0.f : m_new;
-        float psum = 0.f;
+          float tmax = -INFINITY;
 #pragma unroll
-        for (int st = 0; st < 2; ++st)
+          for (int e = 0; e < 32; ++e) tmax = fmaxf(tmax, t[e]);
+          tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+          // Lazy rescaling: the reference point m_run (exp2 domain) only moves
+          // when the tile max exceeds it by more than 8, so P <= 2^8 (safe in
+          // fp16/bf16 and fp32). Any reference point gives the same softmax.
+          const float m_new = fmaxf(m_run, tmax * qsc);
+          const bool need = m_new > m_run + 8.f;
+          if (__any(need)) {
+            const float resc = need ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;
+            if (need) m_run = m_new;
+            l_lane *= resc;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float p = exp2f(s[st][r] - msub);  // -inf -> 0
-            s[st][r] = p;
+            for (int tt = 0; tt < DC; ++tt)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) oacc[tt][r] *= resc;
+          }
+          const float msub = (m_run == -INFINITY) ? 0.f : m_run;
+          float psum = 0.f;
+#pragma unroll
+          for (int e = 0; e < 32; ++e) {
+            const float p = __builtin_amdgcn_exp2f(fmaf(t[e], qsc, -msub));  // -inf -> 0
+            t[e] = p;
             psum += p;
           }
-        l_lane = l_lane * resc + psum;
-        m_run = m_new;
-#pragma unroll
-        for (int t = 0; t < DC; ++t)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) oacc[t][r] *= resc;
+          l_lane += psum;
 
-        // ---- O^T += V^T . P^T, four 16-key steps ----
+          // ---- O^T += V^T . P^T, four 16-key steps ----
+          const uint16_t* vrow = &sm.vt[kb_cur][l32 * BN];
 #pragma unroll
-        for (int st = 0; st < 2; ++st)
+          for (int c4 = 0; c4 < 4; ++c4) {
+            const typename PV::vec pop = PV::pack(&t[8 * c4]);
 #pragma unroll
-          for (int c2 = 0; c2 < 2; ++c2) {
-            const typename PV::vec pop = PV::pack(&s[st][8 * c2]);
-            const int kcol = st * 32 + 16 * c2 + 8 * h;  // storage position of the 8 keys
-#pragma unroll
-            for (int t = 0; t < DC; ++t) {
-              const typename PV::vec vop =
-                  *reinterpret_cast<const typename PV::vec*>(&sm.vt[buf][32 * t + l32][kcol]);
-              oacc[t] = PV::mfma(vop, pop, oacc[t]);
+            for (int tt = 0; tt < DC; ++tt) {
+              const typename PV::vec vop = *reinterpret_cast<const typename PV::vec*>(
+                  vrow + 32 * tt * BN + voff[c4]);
+              oacc[tt] = PV::mfma(vop, pop, oacc[tt]);
             }
           }
-      }
-    }
-
-    if (has_next) store_tile(buf ^ 1);
-    __syncthreads();
-  }
-
-  if constexpr (!DUMP) {
-    const float l = l_lane + __shfl_xor(l_lane, 32, 64);
-    if (m_ok) {
-      const float inv = (l > 0.f) ? 1.f / l : 0.f;
-      uint16_t* orow = reinterpret_cast<uint16_t*>(a.out) + ((int64_t)bh * M + mq) * D;
-#pragma unroll
-      for (int t = 0; t < DC; ++t)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          uint16_t hv[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float x = oacc[t][4 * g + e] * inv;
-            hv[e] = (VDT == SL8_DTYPE_F16) ? f2h_bits(x) : f2bf_bits(x);
-          }
-          uint2 pk;
-          pk.x = hv[0] | ((uint32_t)hv[1] << 16);
-          pk.y = hv[2] | ((uint32_t)hv[3] << 16);
-          *reinterpret_cast<uint2*>(orow + 32 * t + 8 * g + 4 * h) = pk;
         }
-      if (LSE && h == 0)
-        a.lse[(int64_t)bh * M + mq] = (l > 0.f) ? (m_run * LN2F + logf(l)) : -INFINITY;
+      }
+
+      wait_dma();
+      __syncthreads();
+      sc0 = sn0;
+      sc1 = sn1;
+    }
+#undef SL8_LOAD_K
+#undef SL8_LOAD_V
+
+    if constexpr (!DUMP) {
+      const float l = l_lane + __shfl_xor(l_lane, 32, 64);
+      if (m_ok) {
+        const float inv = (l > 0.f) ? 1.f / l : 0.f;
+        uint16_t* orow = reinterpret_cast<uint16_t*>(a.out) + ((int64_t)bh * M + mq) * D;
+#pragma unroll
+        for (int tt = 0; tt < DC; ++tt)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            uint16_t hv[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float x = oacc[tt][4 * g + e] * inv;
+              hv[e] = (VDT == SL8_DTYPE_F16) ? f2h_bits(x) : f2bf_bits(x);
+            }
+            uint2 pk;
+            pk.x = hv[0] | ((uint32_t)hv[1] << 16);
+            pk.y = hv[2] | ((uint32_t)hv[3] << 16);
+            *reinterpret_cast<uint2*>(orow + 32 * tt + 8 * g + 4 * h) = pk;
+          }
+        if (LSE && h == 0)
+          a.lse[(int64_t)bh * M + mq] = (l > 0.f) ? (m_run * LN2F + logf(l)) : -INFINITY;
+      }
     }
   }
 }
@@ -433,7 +488,7 @@ FwdArgs make_args(int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N, int&
   a.Hkv = (int)Hkv;
   a.nqb = (int)((M + BM - 1) / BM);
   a.window_left = -1;
-  grid = (int)(B * Hq * a.nqb);
+  grid = (int)(B * Hq * a.nqb);  // causal kernels halve this (paired query blocks)
   a.xcd_map = ((B * Hkv) % 8 == 0) ? 1 : 0;
   return a;
 }
@@ -477,6 +532,7 @@ extern "C" int sl8_attn_int8_fwd(const int8_t* q, const float* q_scale, const in
   a.vt = static_cast<const uint16_t*>(workspace);
   a.out = out; a.lse = lse; a.window_left = (int)window_left;
   const bool c = causal != 0, want_lse = lse != nullptr;
+  if (c) grid = (int)(B * Hq * ((a.nqb + 1) / 2));
   if (D == 64) {
     if (v_dtype == SL8_DTYPE_F16) dispatch_causal_lse<64, SL8_DTYPE_F16, false>(a, grid, c, want_lse, st);
     else dispatch_causal_lse<64, SL8_DTYPE_BF16, false>(a, grid, c, want_lse, st);
