@@ -123,13 +123,6 @@ struct FwdArgs {
 // LDS tiles are dense; 16-byte chunks are XOR-swizzled within each row
 // (chunk c of row r is stored at c ^ (r % chunks_per_row)) so that the
 // MFMA operand reads of 8 consecutive rows hit distinct banks.
-template <int D>
-struct FwdSmem {
-  __attribute__((aligned(16))) int8_t k[2][BN * D];
-  __attribute__((aligned(16))) uint16_t vt[2][D * BN];
-  __attribute__((aligned(16))) float ks[3][BN];
-};
-
 typedef __attribute__((address_space(1))) const void* gptr_t;
 typedef __attribute__((address_space(3))) void* lptr_t;
 
@@ -197,7 +190,13 @@ attn_fwd_kernel(const FwdArgs a) {
   constexpr int KCH = BN * D / 16 / FWD_THREADS;      // 16-B K chunks per thread
   constexpr int VCH = D * BN * 2 / 16 / FWD_THREADS;  // 16-B V^T chunks per thread
   static_assert(KCH >= 1 && VCH >= 1, "tile copies cover D in {64,128}");
-  __shared__ FwdSmem<D> sm;
+  // tile buffers: separate LDS objects (see the pipeline comment below)
+  __shared__ __attribute__((aligned(16))) int8_t sm_k0[BN * D];
+  __shared__ __attribute__((aligned(16))) int8_t sm_k1[BN * D];
+  __shared__ __attribute__((aligned(16))) uint16_t sm_v0[D * BN];
+  __shared__ __attribute__((aligned(16))) uint16_t sm_v1[D * BN];
+  __shared__ __attribute__((aligned(16))) float sm_s0[BN];
+  __shared__ __attribute__((aligned(16))) float sm_s1[BN];
   using PV = PvOp<VDT>;
 
   // Causal launches pair query block qb with nqb-1-qb so every workgroup
@@ -267,29 +266,29 @@ attn_fwd_kernel(const FwdArgs a) {
     };
 
     // global -> LDS tile copies (no staging registers)
-#define SL8_LOAD_K(N0, KB, SB)                                                            \
-    do {                                                                                  \
-      _Pragma("unroll") for (int i = 0; i < KCH; ++i) {                                   \
-        const int slot = i * FWD_THREADS + tid;                                           \
-        const int row = slot / KCPR;                                                      \
-        const int c = (slot % KCPR) ^ (row & (KCPR - 1));                                 \
-        dma16_to_lds(kb + (int64_t)min((N0) + row, N - 1) * D + 16 * c,                 \
-                       &sm.k[KB][(i * FWD_THREADS + wave * 64) * 16]);                    \
-      }                                                                                   \
-      if (!DUMP && wave == 0) dma4_to_lds(ksb + min((N0) + lane, N - 1), &sm.ks[SB][0]); \
-    } while (0)
-#define SL8_LOAD_V(N0, VB)                                                                \
-    do {                                                                                  \
-      if constexpr (!DUMP) {                                                              \
-        _Pragma("unroll") for (int i = 0; i < VCH; ++i) {                                 \
-          const int slot = i * FWD_THREADS + tid;                                         \
-          const int row = slot / 8;                                                       \
-          const int c = (slot % 8) ^ (row & 7);                                           \
-          dma16_to_lds(vtb + (int64_t)row * a.Npad + (N0) + 8 * c,                      \
-                         &sm.vt[VB][(i * FWD_THREADS + wave * 64) * 8]);                  \
-        }                                                                                 \
-      }                                                                                   \
-    } while (0)
+    auto load_k = [&](int n0, int8_t* dst) {
+#pragma unroll
+      for (int i = 0; i < KCH; ++i) {
+        const int slot = i * FWD_THREADS + tid;
+        const int row = slot / KCPR;
+        const int c = (slot % KCPR) ^ (row & (KCPR - 1));
+        dma16_to_lds(kb + (int64_t)min(n0 + row, N - 1) * D + 16 * c,
+                     dst + (i * FWD_THREADS + wave * 64) * 16);
+      }
+    };
+    auto load_v = [&](int n0, uint16_t* dst, float* kdst) {
+      if constexpr (!DUMP) {
+#pragma unroll
+        for (int i = 0; i < VCH; ++i) {
+          const int slot = i * FWD_THREADS + tid;
+          const int row = slot / 8;
+          const int c = (slot % 8) ^ (row & 7);
+          dma16_to_lds(vtb + (int64_t)row * a.Npad + n0 + 8 * c,
+                       dst + (i * FWD_THREADS + wave * 64) * 8);
+        }
+        if (wave == 0) dma4_to_lds(ksb + min(n0 + lane, N - 1), kdst);
+      }
+    };
 
     v16f oacc[DC];
 #pragma unroll
@@ -299,30 +298,31 @@ attn_fwd_kernel(const FwdArgs a) {
     float m_run = -INFINITY, l_lane = 0.f;
 
     // Pipeline: while the softmax and P.V of tile j run, the MFMAs of
-    // S_{j+1} are already in flight and tile j+2's K / tile j+1's V loads are
-    // outstanding. LDS: K double buffered (K_{j+1} resident at iteration j),
-    // V double buffered, k_scale triple buffered; one barrier per tile.
+    // S_{j+1} are already in flight and the copies of K_{j+2} and
+    // V_{j+1}/k_scale_{j+1} are landing in LDS. Every buffer is a separate LDS
+    // object and the loop is unrolled by two, so the compiler can see that the
+    // in-flight copies never alias the tiles being read (no early vmcnt wait).
     if (ntiles > 0) {
-      SL8_LOAD_K(n_beg, 0, 0);
-      SL8_LOAD_V(n_beg, 0);
-      if (ntiles > 1) SL8_LOAD_K(n_beg + BN, 1, 1);
+      load_k(n_beg, sm_k0);
+      load_v(n_beg, sm_v0, sm_s0);
+      if (ntiles > 1) load_k(n_beg + BN, sm_k1);
     }
     wait_dma();
     __syncthreads();
 
     v16i sc0, sc1;  // S_j
-    if (ntiles > 0 && live(n_beg)) qk_tile<D>(&sm.k[0][l32 * D], koff, qop, sc0, sc1);
+    if (ntiles > 0 && live(n_beg)) qk_tile<D>(sm_k0 + l32 * D, koff, qop, sc0, sc1);
+    __syncthreads();  // all waves done with K_0 before K_2 lands there
 
-    for (int j = 0; j < ntiles; ++j) {
+    auto body = [&](int j, int8_t* kc, const int8_t* kn, const uint16_t* vc, uint16_t* vn,
+                    const float* scur, float* snext) {
       const int n0 = n_beg + j * BN;
-      const int kb_cur = j & 1, sb_cur = j % 3;
-      // buffers last read in iteration j-1 receive tiles j+2 (K) and j+1 (V)
-      if (j + 2 < ntiles) SL8_LOAD_K(n0 + 2 * BN, kb_cur, (j + 2) % 3);
-      if (j + 1 < ntiles) SL8_LOAD_V(n0 + BN, kb_cur ^ 1);
+      if (j + 2 < ntiles) load_k(n0 + 2 * BN, kc);
+      if (j + 1 < ntiles) load_v(n0 + BN, vn, snext);
 
       // S_{j+1}: issue its MFMAs before the softmax of tile j
       v16i sn0, sn1;
-      if (j + 1 < ntiles && live(n0 + BN)) qk_tile<D>(&sm.k[kb_cur ^ 1][l32 * D], koff, qop, sn0, sn1);
+      if (j + 1 < ntiles && live(n0 + BN)) qk_tile<D>(kn + l32 * D, koff, qop, sn0, sn1);
 
       if (live(n0)) {
         if constexpr (DUMP) {
@@ -340,16 +340,16 @@ attn_fwd_kernel(const FwdArgs a) {
           float t[32];
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
-            const float4 ka = *reinterpret_cast<const float4*>(&sm.ks[sb_cur][8 * g + 4 * h]);
-            const float4 kc = *reinterpret_cast<const float4*>(&sm.ks[sb_cur][32 + 8 * g + 4 * h]);
+            const float4 ka = *reinterpret_cast<const float4*>(scur + 8 * g + 4 * h);
+            const float4 kc4 = *reinterpret_cast<const float4*>(scur + 32 + 8 * g + 4 * h);
             t[4 * g + 0] = (float)sc0[4 * g + 0] * ka.x;
             t[4 * g + 1] = (float)sc0[4 * g + 1] * ka.y;
             t[4 * g + 2] = (float)sc0[4 * g + 2] * ka.z;
             t[4 * g + 3] = (float)sc0[4 * g + 3] * ka.w;
-            t[16 + 4 * g + 0] = (float)sc1[4 * g + 0] * kc.x;
-            t[16 + 4 * g + 1] = (float)sc1[4 * g + 1] * kc.y;
-            t[16 + 4 * g + 2] = (float)sc1[4 * g + 2] * kc.z;
-            t[16 + 4 * g + 3] = (float)sc1[4 * g + 3] * kc.w;
+            t[16 + 4 * g + 0] = (float)sc1[4 * g + 0] * kc4.x;
+            t[16 + 4 * g + 1] = (float)sc1[4 * g + 1] * kc4.y;
+            t[16 + 4 * g + 2] = (float)sc1[4 * g + 2] * kc4.z;
+            t[16 + 4 * g + 3] = (float)sc1[4 * g + 3] * kc4.w;
           }
           const bool need_mask = (n0 + BN > N) || (CAUSAL && n0 + BN - 1 > wq_lo) ||
                                  (wl >= 0 && n0 <= wq_hi - wl);
@@ -392,7 +392,7 @@ attn_fwd_kernel(const FwdArgs a) {
           l_lane += psum;
 
           // ---- O^T += V^T . P^T, four 16-key steps ----
-          const uint16_t* vrow = &sm.vt[kb_cur][l32 * BN];
+          const uint16_t* vrow = vc + l32 * BN;
 #pragma unroll
           for (int c4 = 0; c4 < 4; ++c4) {
             const typename PV::vec pop = PV::pack(&t[8 * c4]);
@@ -405,14 +405,16 @@ attn_fwd_kernel(const FwdArgs a) {
           }
         }
       }
-
       wait_dma();
       __syncthreads();
       sc0 = sn0;
       sc1 = sn1;
+    };
+
+    for (int j = 0; j < ntiles; j += 2) {
+      body(j, sm_k0, sm_k1, sm_v0, sm_v1, sm_s0, sm_s1);
+      if (j + 1 < ntiles) body(j + 1, sm_k1, sm_k0, sm_v1, sm_v0, sm_s1, sm_s0);
     }
-#undef SL8_LOAD_K
-#undef SL8_LOAD_V
 
     if constexpr (!DUMP) {
       const float l = l_lane + __shfl_xor(l_lane, 32, 64);
