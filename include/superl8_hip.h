@@ -77,6 +77,16 @@ int sl8_quantize_i8_rows_centered(const void* x, int x_dtype, int64_t G, int64_t
                                   int8_t* q, float* scale, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Per-channel int8 of V over the key axis (W8A8 path).
+ * Replaces quantize_v_perchannel, reference superl8/quant/core.py:98-110
+ * (on the GPU torch evaluates amax/127 as amax * fp32(1/127)).
+ *   x [G, N, D] -> q int8 [G, N, D], scale fp32 [G, D]
+ *   scale = amax_n|x| * fp32(1/127) (1 if 0); q = clamp(rint(x/scale), +-127)
+ * ---------------------------------------------------------------------- */
+int sl8_quantize_i8_cols(const void* x, int dtype, int64_t G, int64_t N, int64_t D, int8_t* q,
+                         float* scale, void* stream);
+
+/* ------------------------------------------------------------------------
  * Prefill FlashAttention-2: int8 QK^T on MFMA (int32 accumulate), fp32
  * online softmax in the exp2 domain, fp16/bf16 PV on MFMA, output dtype = V's.
  * Replaces _C.attn_int8_fwd / _C.attn_int8_fwd_train (reference

@@ -101,6 +101,23 @@ def quantize_rows_centered(x: torch.Tensor, mean: torch.Tensor | None, scale_mul
     return q, scale
 
 
+def quantize_v_perchannel(v: torch.Tensor):
+    """Per-channel int8 of v[..., N, D] over N -> (q int8 [..., N, D], scale fp32 [..., 1, D])."""
+    _check(v.is_cuda, "quantize_v_perchannel expects a CUDA tensor")
+    _check(v.dtype in (torch.float16, torch.bfloat16, torch.float32),
+           "quantize_v_perchannel input must be float16/bfloat16/float32")
+    v = v.contiguous()
+    *lead, N, D = v.shape
+    G = math.prod(lead)
+    q = torch.empty(v.shape, device=v.device, dtype=torch.int8)
+    scale = torch.empty((*lead, 1, D), device=v.device, dtype=torch.float32)
+    if G and D:
+        with torch.cuda.device(v.device):
+            call("sl8_quantize_i8_cols", v.data_ptr(), dtype_code(v.dtype), G, N, D, q.data_ptr(),
+                 scale.data_ptr(), stream_of(v))
+    return q, scale
+
+
 # ---------------------------------------------------------------------------
 # prefill attention (reference csrc/kernel/attn_int8_fwd.cu:101-200)
 # ---------------------------------------------------------------------------

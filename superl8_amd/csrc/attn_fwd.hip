@@ -30,16 +30,10 @@
 // KV-head count is a multiple of 8, all query heads of one KV head go to the
 // same XCD so its K/V tiles stay in that XCD's L2.
 
-#include "common.hpp"
+#include "attn_common.hpp"
 
 namespace sl8 {
 namespace {
-
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
-typedef float v16f __attribute__((ext_vector_type(16)));
-typedef _Float16 v8h __attribute__((ext_vector_type(8)));
-typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
 constexpr int FWD_THREADS = 256;
 constexpr int FWD_WAVES = 4;
@@ -123,40 +117,10 @@ struct FwdArgs {
 // LDS tiles are dense; 16-byte chunks are XOR-swizzled within each row
 // (chunk c of row r is stored at c ^ (r % chunks_per_row)) so that the
 // MFMA operand reads of 8 consecutive rows hit distinct banks.
-typedef __attribute__((address_space(1))) const void* gptr_t;
-typedef __attribute__((address_space(3))) void* lptr_t;
-
-// Direct global -> LDS copy: lane i of the wave writes `bytes` at lds + i*bytes.
-__device__ __forceinline__ void dma16_to_lds(const void* g, void* lds_wave_base) {
-  __builtin_amdgcn_global_load_lds((gptr_t)g, (lptr_t)lds_wave_base, 16, 0, 0);
-}
-__device__ __forceinline__ void dma4_to_lds(const void* g, void* lds_wave_base) {
-  __builtin_amdgcn_global_load_lds((gptr_t)g, (lptr_t)lds_wave_base, 4, 0, 0);
-}
-__device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
 
 // blockIdx.x -> (b*Hq + h, query-block slot), heaviest slot first.
 __device__ __forceinline__ void block_coords(const FwdArgs& a, int nslot, int& bh, int& slot) {
-  const int id = blockIdx.x;
-  const int total = gridDim.x;
-  const int gsz = a.Hq / a.Hkv;
-  if (a.xcd_map) {
-    // id = 8*k + xcd; XCD x serves KV heads {x, x+8, ...}
-    const int nbkv = total / (nslot * gsz);  // B * Hkv
-    const int xcd = id & 7, k = id >> 3;
-    const int per_slot = (nbkv / 8) * gsz;
-    const int r = k / per_slot;
-    const int rem = k % per_slot;
-    const int bkv = xcd + 8 * (rem / gsz);
-    const int j = rem % gsz;
-    const int b = bkv / a.Hkv, kvh = bkv % a.Hkv;
-    bh = b * a.Hq + kvh * gsz + j;
-    slot = r;
-  } else {
-    const int nbh = total / nslot;
-    slot = id / nbh;
-    bh = id % nbh;
-  }
+  attn_block_coords(a.Hq, a.Hkv, nslot, a.xcd_map != 0, bh, slot);
 }
 
 template <int DC>

@@ -190,10 +190,82 @@ k_mean_seq_kernel(const typename Elem<DT>::T* __restrict__ k, float* __restrict_
   mean[g * D + d] = (float)(s / (double)N);
 }
 
+// ---- per-channel (column) quantisation over the key axis ----------------
+// scale[g,d] = amax_n |x[g,n,d]| * fp32(1/127) (1 if 0); max is order-free.
+template <int DT>
+__global__ void __launch_bounds__(MEAN_COLS * MEAN_PHASES)
+col_amax_kernel(const typename Elem<DT>::T* __restrict__ x, float* __restrict__ scale, int64_t N,
+                int D) {
+  __shared__ float part[MEAN_PHASES][MEAN_COLS];
+  const int col = threadIdx.x % MEAN_COLS, ph = threadIdx.x / MEAN_COLS;
+  const int64_t g = blockIdx.y;
+  const int d = blockIdx.x * MEAN_COLS + col;
+  float m = 0.f;
+  if (d < D) {
+    const typename Elem<DT>::T* xg = x + g * N * D + d;
+    for (int64_t n = ph; n < N; n += MEAN_PHASES) m = fmaxf(m, fabsf(Elem<DT>::ld(xg, n * D)));
+  }
+  part[ph][col] = m;
+  __syncthreads();
+  if (ph == 0 && d < D) {
+#pragma unroll
+    for (int p = 1; p < MEAN_PHASES; ++p) m = fmaxf(m, part[p][col]);
+    const float s = m * (1.0f / 127.0f);
+    scale[g * D + d] = (s == 0.f) ? 1.f : s;
+  }
+}
+
+template <int DT>
+__global__ void __launch_bounds__(256)
+col_quant_kernel(const typename Elem<DT>::T* __restrict__ x, const float* __restrict__ scale,
+                 int8_t* __restrict__ q, int64_t N, int D, int64_t total) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const int d = (int)(i % D);
+  const int64_t g = i / ((int64_t)N * D);
+  q[i] = code_of(Elem<DT>::ld(x, i), scale[g * D + d]);
+}
+
 }  // namespace
 }  // namespace sl8
 
 using namespace sl8;
+
+extern "C" int sl8_quantize_i8_cols(const void* x, int dtype, int64_t G, int64_t N, int64_t D,
+                                    int8_t* q, float* scale, void* stream) {
+  clear_error();
+  SL8_CHECK_ARG(dtype == SL8_DTYPE_F16 || dtype == SL8_DTYPE_BF16 || dtype == SL8_DTYPE_F32,
+                "quantize_v_perchannel: input must be float16/bfloat16/float32");
+  SL8_CHECK_ARG(G >= 0 && N >= 0 && D >= 0 && D < (1LL << 31), "quantize_v_perchannel: bad shape");
+  if (G == 0 || D == 0) return SL8_OK;
+  SL8_CHECK_ARG(x && q && scale, "quantize_v_perchannel: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)((D + MEAN_COLS - 1) / MEAN_COLS), (unsigned)G);
+  const int64_t total = G * N * D;
+  const unsigned qgrid = (unsigned)((total + 255) / 256);
+  switch (dtype) {
+    case SL8_DTYPE_F16:
+      col_amax_kernel<SL8_DTYPE_F16><<<grid, MEAN_COLS * MEAN_PHASES, 0, st>>>(
+          static_cast<const uint16_t*>(x), scale, N, (int)D);
+      if (total) col_quant_kernel<SL8_DTYPE_F16><<<qgrid, 256, 0, st>>>(
+          static_cast<const uint16_t*>(x), scale, q, N, (int)D, total);
+      break;
+    case SL8_DTYPE_BF16:
+      col_amax_kernel<SL8_DTYPE_BF16><<<grid, MEAN_COLS * MEAN_PHASES, 0, st>>>(
+          static_cast<const uint16_t*>(x), scale, N, (int)D);
+      if (total) col_quant_kernel<SL8_DTYPE_BF16><<<qgrid, 256, 0, st>>>(
+          static_cast<const uint16_t*>(x), scale, q, N, (int)D, total);
+      break;
+    default:
+      col_amax_kernel<SL8_DTYPE_F32><<<grid, MEAN_COLS * MEAN_PHASES, 0, st>>>(
+          static_cast<const float*>(x), scale, N, (int)D);
+      if (total) col_quant_kernel<SL8_DTYPE_F32><<<qgrid, 256, 0, st>>>(
+          static_cast<const float*>(x), scale, q, N, (int)D, total);
+      break;
+  }
+  SL8_CHECK_LAUNCH("quantize_v_perchannel");
+  return SL8_OK;
+}
 
 extern "C" const char* sl8_last_error(void) { return g_last_error.c_str(); }
 extern "C" const char* sl8_version(void) { return "superl8-hip 0.1 gfx950"; }

@@ -1,0 +1,111 @@
+"""GPU parity of the full-W8A8 prefill (attn_w8a8_fwd) and the V per-channel prologue."""
+import numpy as np
+import pytest
+import torch
+
+import superl8_amd as sl8
+from oracle import attention as oa
+from oracle import quant as oqn
+from superl8_amd import _C, quant
+from tests.tolerances import assert_close_abs, assert_finite, assert_int8_quality
+
+pytestmark = pytest.mark.gpu
+
+PV_BARS = dict(min_cos=0.998, max_rel_l1=0.03, min_sqnr_db=18.0)  # reference test_attn_fwd_w8a8.py:37
+
+
+def _np(x):
+    return x.detach().cpu().numpy()
+
+
+def _qkv(B, Hq, Hkv, M, N, D, device):
+    return (torch.randn(B, Hq, M, D, device=device, dtype=torch.float16),
+            torch.randn(B, Hkv, N, D, device=device, dtype=torch.float16),
+            torch.randn(B, Hkv, N, D, device=device, dtype=torch.float16))
+
+
+@pytest.mark.parametrize("shape", [(1, 2, 128, 64), (2, 3, 257, 128), (1, 1, 77, 256)])
+def test_v_perchannel_bit_exact(device, shape):
+    v = torch.randn(*shape, device=device, dtype=torch.float16) * 2
+    q, s = _C.quantize_v_perchannel(v)
+    rq, rs = oqn.quantize_v_perchannel(_np(v))
+    np.testing.assert_array_equal(_np(q), rq)
+    np.testing.assert_array_equal(_np(s)[..., 0, :], rs)
+
+
+CASES = [  # B, Hq, Hkv, M, N, D, causal
+    (1, 2, 2, 128, 128, 64, False), (1, 2, 2, 128, 128, 64, True), (2, 4, 2, 257, 257, 64, True),
+    (1, 2, 2, 333, 333, 128, False), (1, 4, 1, 100, 333, 128, True), (1, 2, 1, 200, 200, 256, True),
+    (1, 2, 2, 70, 90, 256, False),
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+@pytest.mark.parametrize("per_warp", [True, False])
+def test_kernel_matches_oracle(device, case, per_warp):
+    B, Hq, Hkv, M, N, D, causal = case
+    q, k, v = _qkv(B, Hq, Hkv, M, N, D, device)
+    q_i8, qs, k_i8, ks, _ = quant.quantize_qk(q, k)
+    qs, ks = qs.squeeze(-1).contiguous(), ks.squeeze(-1).contiguous()
+    v_i8, vs = _C.quantize_v_perchannel(v)
+    vs = vs.squeeze(-2).contiguous()
+    diag = N - M if causal else 0
+    out = _C.attn_w8a8_fwd(q_i8, qs, k_i8, ks, v_i8, vs, causal, diag, per_warp)
+    assert out.dtype == torch.float16 and out.shape == (B, Hq, M, D)
+    ref = oa.attn_w8a8_fwd(_np(q_i8), _np(qs), _np(k_i8), _np(ks), _np(v_i8), _np(vs), causal, diag,
+                           per_warp)
+    assert_finite(out)
+    # P codes follow the oracle up to exp2 rounding (an occasional code off by one)
+    assert_close_abs(out, ref, atol=2e-2, what="w8a8 vs oracle")
+    assert_int8_quality(out, ref, min_cos=0.9999, max_rel_l1=5e-3, min_sqnr_db=35)
+
+
+@pytest.mark.parametrize("shape", [(1, 2, 128, 64), (2, 4, 257, 64), (1, 2, 333, 128), (1, 8, 2048, 64)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_end_to_end_quality(device, shape, causal):
+    """reference tests/test_attn_fwd_w8a8.py:44-51."""
+    b, h, m, d = shape
+    q, k, v = _qkv(b, h, h, m, m, d, device)
+    out = sl8.attn_int8_fwd(q, k, v, causal=causal, int8_pv=True)
+    ref = oa.attention_fp64(_np(q.float()), _np(k.float()), _np(v.float()), causal)
+    assert_int8_quality(out, ref, what=f"w8a8 {shape} causal={causal}", **PV_BARS)
+
+
+def test_per_warp_not_worse_and_deterministic(device):
+    """reference tests/test_attn_fwd_w8a8_perwarp.py: per-half P scales are no worse."""
+    from tests.tolerances import rel_l1
+
+    q, k, v = _qkv(1, 8, 8, 1024, 1024, 128, device)
+    ref = oa.attention_fp64(_np(q.float()), _np(k.float()), _np(v.float()), True)
+    pw = sl8.attn_int8_fwd(q, k, v, causal=True, int8_pv=True, per_warp_quant=True)
+    pr = sl8.attn_int8_fwd(q, k, v, causal=True, int8_pv=True, per_warp_quant=False)
+    assert rel_l1(pw, ref) <= rel_l1(pr, ref) * 1.02
+    for _ in range(2):
+        assert torch.equal(sl8.attn_int8_fwd(q, k, v, causal=True, int8_pv=True), pw)
+
+
+def test_config5_outliers_small(device):
+    """BASELINE config 5 recipe at reduced size: 1% of channels x20 in Q/K, D=256,
+    gate bypassed (internal_accuracy_gate=False) so the int8 kernel runs."""
+    torch.manual_seed(5)
+    B, Hq, Hkv, S, D = 1, 4, 1, 1024, 256
+    q, k, v = _qkv(B, Hq, Hkv, S, S, D, device)
+    idx = torch.randperm(D, generator=torch.Generator().manual_seed(5))[:3]
+    q[..., idx] *= 20
+    k[..., idx] *= 20
+    out = sl8.attn_int8_fwd(q, k, v, causal=True, int8_pv=True, internal_accuracy_gate=False)
+    assert_finite(out)
+    q_i8, qs, k_i8, ks, _ = quant.quantize_qk(q, k)
+    v_i8, vs = _C.quantize_v_perchannel(v)
+    ref = oa.attn_w8a8_fwd(_np(q_i8), _np(qs[..., 0]), _np(k_i8), _np(ks[..., 0]), _np(v_i8),
+                           _np(vs[..., 0, :]), True, 0, True)
+    assert_int8_quality(out, ref, min_cos=0.9999, max_rel_l1=5e-3, min_sqnr_db=35)
+
+
+def test_rejects(device):
+    q, k, v = _qkv(1, 2, 2, 64, 64, 96, device)
+    with pytest.raises(RuntimeError):
+        sl8.attn_int8_fwd(q, k, v, int8_pv=True)
+    q, k, v = _qkv(1, 2, 2, 64, 64, 64, device)
+    with pytest.raises(ValueError):
+        sl8.attn_int8_fwd(q, k, v, int8_pv=True, causal=True, window_left=8)
