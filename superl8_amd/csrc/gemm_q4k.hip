@@ -6,8 +6,9 @@
 // over 32-element sub-blocks j; q in [0,15]; sc_j, m_j 6-bit.
 //
 // MI355X design. The weight stream (144 B per 256 weights) is the only HBM
-// traffic that matters, so every weight byte is loaded once with 16-byte
-// loads and unpacked in registers. The integer dot products run on the int8
+// traffic that matters, so every weight byte is loaded once (each lane owns
+// distinct bytes) and unpacked in registers; a wave issues all loads of a
+// chunk of super-blocks before consuming any of them. The integer dot products run on the int8
 // MFMA (v_mfma_i32_16x16x64_i8) instead of VALU dot4: one 16x16x64 MFMA
 // covers one 32-byte nibble group (two sub-blocks, 64 weights) of 16 weight
 // rows against up to 8 activation rows. The trick that keeps the two
@@ -16,15 +17,17 @@
 // high-nibble sub-block, so C[i][n] is <x_m, q> of sub-block 2g + i/8.
 //   A (16 x 64, "x"):  row i = (m = i%8, parity p = i/8)
 //   B (64 x 16, "w"):  column n = weight row, k = the group's 64 nibbles
-// k-slot mapping (lane group h = lane/16, byte b): h=0,1 -> low nibble of
-// group byte 16h+b; h=2,3 -> high nibble of byte 16(h-2)+b. A and B use the
-// same mapping, which is all the contraction needs.
+// k-slot mapping (lane group h = lane/16, slot b = 0..15): slot b < 8 is the
+// low nibble of group byte 8h+b, slot b >= 8 the high nibble of byte 8h+b-8;
+// so a lane unpacks one 8-byte load into its 16 slots. A and B use the same
+// mapping, which is all the contraction needs.
 // Per-sub-block affine scales are then applied in the integer domain:
 //   T += sc_j * S_j (v_mad_i32_i24), U += m_j * xsum_j, and once per
 //   super-block f += d*T - dmin*U (fp32). |T| < 2^24, so this is exact until
 //   the final fp32 accumulate.
 // Workgroup: 4 waves, 16 weight rows; the waves split the super-blocks of K
-// and reduce through LDS in a fixed order (deterministic output).
+// and reduce through LDS in a fixed order (deterministic output). The x
+// sub-block sums each wave needs are formed in its own LDS slice.
 
 #include "common.hpp"
 
@@ -34,7 +37,6 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int Q4K_BYTES = 144;
-constexpr int GEMV_THREADS = 256;
 constexpr int GEMV_ROWS = 16;
 constexpr int XS_MPAD = 16;  // xsum LDS row pitch (activation rows)
 
@@ -52,129 +54,179 @@ __device__ __forceinline__ ScMin unpack_scmin(uint32_t s0, uint32_t s1, uint32_t
 }
 __device__ __forceinline__ int byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xFF; }
 
-template <int OUT_DT, int MT>
-__global__ void __launch_bounds__(GEMV_THREADS)
+// Work split: a workgroup = GTILES 16-row MFMA tiles = 4 waves, each wave
+// taking one quarter of the super-blocks of K; partial sums are reduced
+// through LDS in a fixed order. Each wave issues every weight load of its
+// share (up to GCH super-blocks per tile) before it waits for any of them,
+// so a wave costs one memory round trip; meanwhile the workgroup stages the
+// activations (M x K int8) into LDS, where the x operands are read from.
+// At the config shape (N = 17408, K = 5120) this is 4352 waves at 4 waves
+// per SIMD.
+// Per group and row tile: one MFMA for <x, q> (scaled by sc_j in the integer
+// domain with v_mad_i32_i24) and one MFMA whose B operand holds m_j in every
+// slot of the sub-block, so it accumulates m_j * sum(x_j) over the
+// super-block in its own accumulator.
+constexpr int GCH = 5;     // super-blocks per wave and chunk
+constexpr int GWAVES = 4;  // K split
+constexpr int GTILES = 1;  // 16-row tiles per wave
+constexpr int XLDS_MAX = 48 * 1024;
+
+template <int OUT_DT, int MT, bool XLDS>
+__global__ void __launch_bounds__(64 * GWAVES)
 gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
                 const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K) {
-  extern __shared__ int xs_lds[];  // [K/32][XS_MPAD] sub-block sums of x
-  __shared__ float red[MT][4][64][4];
+  __shared__ float red[GWAVES - 1][GTILES][MT][32][4];
+  extern __shared__ __attribute__((aligned(16))) int8_t x_lds[];  // XLDS: x [M][K]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int nsub = K >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nsb = K >> 8;
-
-  // ---- x sub-block sums (rows >= M are zero) ----
-  for (int idx = tid; idx < nsub * XS_MPAD; idx += GEMV_THREADS) {
-    const int j = idx / XS_MPAD, m = idx % XS_MPAD;
-    int s = 0;
-    if (m < M) {
-      const int4* p = reinterpret_cast<const int4*>(x + (int64_t)m * K + 32 * j);
-      const int4 a = p[0], b = p[1];
-      s = __builtin_amdgcn_sdot4(a.x, 0x01010101, s, false);
-      s = __builtin_amdgcn_sdot4(a.y, 0x01010101, s, false);
-      s = __builtin_amdgcn_sdot4(a.z, 0x01010101, s, false);
-      s = __builtin_amdgcn_sdot4(a.w, 0x01010101, s, false);
-      s = __builtin_amdgcn_sdot4(b.x, 0x01010101, s, false);
-      s = __builtin_amdgcn_sdot4(b.y, 0x01010101, s, false);
-      s = __builtin_amdgcn_sdot4(b.z, 0x01010101, s, false);
-      s = __builtin_amdgcn_sdot4(b.w, 0x01010101, s, false);
-    }
-    xs_lds[idx] = s;
-  }
-  __syncthreads();
-
-  const int lj = lane & 15;  // B column (weight row) / A row
-  const int h = lane >> 4;   // k-slot group
-  const int hp = h >> 1;     // nibble half this lane's B slots / C rows belong to
-  const int n = blockIdx.x * GEMV_ROWS + lj;
-  const bool n_ok = n < N;
-  const uint8_t* wrow = w + (int64_t)(n_ok ? n : 0) * nsb * Q4K_BYTES;
-
-  // A-operand row of this lane: m = mt*8 + (lj & 7), active iff parity matches.
-  const int a_m = lj & 7;
-  const bool a_on = ((lj >> 3) == hp);
-
-  float f[MT][4];
+  const int lj = lane & 15;  // B column (weight row in the tile) / A row
+  const int h = lane >> 4;   // k-slot group: bytes 8h..8h+7 of each 32-byte nibble group
+  const int hp = h >> 1;     // sub-block parity of this lane's C rows
+  const int n0 = blockIdx.x * (GEMV_ROWS * GTILES);
+  const int64_t row_bytes = (int64_t)nsb * Q4K_BYTES;
+  const uint8_t* wrow[GTILES];
 #pragma unroll
-  for (int t = 0; t < MT; ++t)
+  for (int rt = 0; rt < GTILES; ++rt)
+    wrow[rt] = w + (int64_t)min(n0 + rt * GEMV_ROWS + lj, N - 1) * row_bytes;
+  const int a_m = lj & 7;    // A-operand row: activation t*8 + a_m, sub-block parity a_p
+  const int a_p = lj >> 3;
+  const uint32_t mlo = a_p == 0 ? 0xFFFFFFFFu : 0u, mhi = ~mlo;
+  bool a_on[MT];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) f[t][r] = 0.f;
+  for (int t = 0; t < MT; ++t) a_on[t] = t * 8 + a_m < M;
+  const int sh = 8 * hp;     // byte of the lane's sub-block inside a scale dword pair
 
-  const int sb0 = (wave * nsb) / 4, sb1 = ((wave + 1) * nsb) / 4;
-  for (int sb = sb0; sb < sb1; ++sb) {
-    const uint8_t* blk = wrow + (int64_t)sb * Q4K_BYTES;
-    const uint4 hdr = *reinterpret_cast<const uint4*>(blk);
-    uint4 qv[4];
+  float f[GTILES][MT][4];
 #pragma unroll
-    for (int g = 0; g < 4; ++g)
-      qv[g] = *reinterpret_cast<const uint4*>(blk + 16 + 32 * g + 16 * (h & 1));
-    const ScMin sm = unpack_scmin(hdr.y, hdr.z, hdr.w);
-    const float d = h2f(hdr.x & 0xFFFFu);
-    const float dmin = h2f(hdr.x >> 16);
-
-    int T[MT][4], U[MT][4];
+  for (int rt = 0; rt < GTILES; ++rt)
 #pragma unroll
     for (int t = 0; t < MT; ++t)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) { T[t][r] = 0; U[t][r] = 0; }
+      for (int r = 0; r < 4; ++r) f[rt][t][r] = 0.f;
 
+  const int sb0 = (wave * nsb) / GWAVES, sb1 = ((wave + 1) * nsb) / GWAVES;  // may be empty
+  // the same chunk count for every wave keeps the staging barrier uniform
+  const int nch = ((nsb + GWAVES - 1) / GWAVES + GCH - 1) / GCH;
+  for (int c = 0; c < nch; ++c) {
+    const int c0 = sb0 + c * GCH;
+    uint4 hdr[GCH][GTILES];
+    uint2 qv[GCH][GTILES][4];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      v4i bop;
-      if (hp == 0) {
-        bop.x = qv[g].x & 0x0F0F0F0F; bop.y = qv[g].y & 0x0F0F0F0F;
-        bop.z = qv[g].z & 0x0F0F0F0F; bop.w = qv[g].w & 0x0F0F0F0F;
-      } else {
-        bop.x = (qv[g].x >> 4) & 0x0F0F0F0F; bop.y = (qv[g].y >> 4) & 0x0F0F0F0F;
-        bop.z = (qv[g].z >> 4) & 0x0F0F0F0F; bop.w = (qv[g].w >> 4) & 0x0F0F0F0F;
-      }
-      const int j = 2 * g + hp;  // sub-block of this lane's C rows
-      const int sc = byte_of(j < 4 ? sm.sc_lo : sm.sc_hi, j & 3);
-      const int mn = byte_of(j < 4 ? sm.mn_lo : sm.mn_hi, j & 3);
-      const int jg = sb * 8 + j;  // global sub-block index
+    for (int i = 0; i < GCH; ++i) {
+      const int sb = min(c0 + i, nsb - 1);  // always a valid block; unused ones are skipped
 #pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        v4i aop = {0, 0, 0, 0};
-        const int am = t * 8 + a_m;
-        if (a_on && am < M)
-          aop = *reinterpret_cast<const v4i*>(x + (int64_t)am * K + sb * 256 + 64 * g + 16 * h);
-        v4i c = {0, 0, 0, 0};
-        c = __builtin_amdgcn_mfma_i32_16x16x64_i8(aop, bop, c, 0, 0, 0);
-        const int4 xs4 = *reinterpret_cast<const int4*>(&xs_lds[jg * XS_MPAD + t * 8 + 4 * (h & 1)]);
-        T[t][0] += __mul24(sc, c.x); T[t][1] += __mul24(sc, c.y);
-        T[t][2] += __mul24(sc, c.z); T[t][3] += __mul24(sc, c.w);
-        U[t][0] += __mul24(mn, xs4.x); U[t][1] += __mul24(mn, xs4.y);
-        U[t][2] += __mul24(mn, xs4.z); U[t][3] += __mul24(mn, xs4.w);
+      for (int rt = 0; rt < GTILES; ++rt) {
+        const uint8_t* blk = wrow[rt] + (int64_t)sb * Q4K_BYTES;
+        hdr[i][rt] = *reinterpret_cast<const uint4*>(blk);
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          qv[i][rt][g] = *reinterpret_cast<const uint2*>(blk + 16 + 32 * g + 8 * h);
       }
     }
+    if (XLDS && c == 0) {
+      // activations into LDS while the first weight loads are in flight
+      const int n16 = M * K / 16;
+      for (int v = tid; v < n16; v += 64 * GWAVES)
+        reinterpret_cast<int4*>(x_lds)[v] = reinterpret_cast<const int4*>(x)[v];
+      __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < GCH; ++i) {
+      if (c0 + i < sb1) {
+        const int sb = c0 + i;
+        ScMin sm[GTILES];
+        int T[GTILES][MT][4];
+        v4i U[GTILES][MT];
+#pragma unroll
+        for (int rt = 0; rt < GTILES; ++rt) {
+          sm[rt] = unpack_scmin(hdr[i][rt].y, hdr[i][rt].z, hdr[i][rt].w);
+#pragma unroll
+          for (int t = 0; t < MT; ++t) {
+            U[rt][t] = v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) T[rt][t][r] = 0;
+          }
+        }
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          v4i aop[MT];
+#pragma unroll
+          for (int t = 0; t < MT; ++t) {
+            const int64_t xo = (int64_t)min(t * 8 + a_m, M - 1) * K + sb * 256 + 64 * g + 32 * a_p + 8 * h;
+            const uint2 xv = XLDS ? *reinterpret_cast<const uint2*>(x_lds + xo)
+                                  : *reinterpret_cast<const uint2*>(x + xo);
+            const uint32_t xlo = a_on[t] ? xv.x : 0u, xhi = a_on[t] ? xv.y : 0u;
+            aop[t] = v4i{(int)(xlo & mlo), (int)(xhi & mlo), (int)(xlo & mhi), (int)(xhi & mhi)};
+          }
+#pragma unroll
+          for (int rt = 0; rt < GTILES; ++rt) {
+            const uint32_t w0 = qv[i][rt][g].x, w1 = qv[i][rt][g].y;
+            const v4i bop = {(int)(w0 & 0x0F0F0F0Fu), (int)(w1 & 0x0F0F0F0Fu),
+                             (int)((w0 >> 4) & 0x0F0F0F0Fu), (int)((w1 >> 4) & 0x0F0F0F0Fu)};
+            // sub-blocks 2g (low slots) and 2g+1 (high slots) of this column's row
+            const uint32_t scw = g < 2 ? sm[rt].sc_lo : sm[rt].sc_hi;
+            const uint32_t mnw = g < 2 ? sm[rt].mn_lo : sm[rt].mn_hi;
+            const int sc = (scw >> (16 * (g & 1) + sh)) & 0xFF;
+            const uint32_t m_lo = ((mnw >> (16 * (g & 1))) & 0xFF) * 0x01010101u;
+            const uint32_t m_hi = ((mnw >> (16 * (g & 1) + 8)) & 0xFF) * 0x01010101u;
+            const v4i bmin = {(int)m_lo, (int)m_lo, (int)m_hi, (int)m_hi};
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+              const v4i z = {0, 0, 0, 0};
+              const v4i cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(aop[t], bop, z, 0, 0, 0);
+              U[rt][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aop[t], bmin, U[rt][t], 0, 0, 0);
+#pragma unroll
+              for (int r = 0; r < 4; ++r) T[rt][t][r] += __mul24(sc, cc[r]);
+            }
+          }
+        }
+#pragma unroll
+        for (int rt = 0; rt < GTILES; ++rt) {
+          const float d = h2f(hdr[i][rt].x & 0xFFFFu);
+          const float dmin = h2f(hdr[i][rt].x >> 16);
+#pragma unroll
+          for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              f[rt][t][r] += d * (float)T[rt][t][r] - dmin * (float)U[rt][t][r];
+        }
+      }
+    }
+  }
+
+  // C row i = 4h + r holds activation row t*8 + (i & 7) of sub-block parity i >> 3:
+  // add the two parities (lanes h and h^2), then the K quarters, in fixed order.
+#pragma unroll
+  for (int rt = 0; rt < GTILES; ++rt)
 #pragma unroll
     for (int t = 0; t < MT; ++t)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) f[t][r] += d * (float)T[t][r] - dmin * (float)U[t][r];
+      for (int r = 0; r < 4; ++r) f[rt][t][r] += __shfl_xor(f[rt][t][r], 32, 64);
+  if (wave > 0 && lane < 32) {
+#pragma unroll
+    for (int rt = 0; rt < GTILES; ++rt)
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[wave - 1][rt][t][lane][r] = f[rt][t][r];
   }
-
-#pragma unroll
-  for (int t = 0; t < MT; ++t)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) red[t][wave][lane][r] = f[t][r];
   __syncthreads();
-
-  // One thread per output (m, n): fixed-order sum over waves and nibble halves.
-  if (tid < MT * 8 * GEMV_ROWS) {
-    const int mloc = tid / GEMV_ROWS, col = tid % GEMV_ROWS;
-    const int t = mloc >> 3, mm = mloc & 7;
-    const int gn = blockIdx.x * GEMV_ROWS + col;
-    if (mloc < M && gn < N) {
-      const int r = mm & 3, hl = mm >> 2;
-      float s = 0.f;
+  if (wave == 0 && lane < 32) {
 #pragma unroll
-      for (int wv = 0; wv < 4; ++wv)
+    for (int rt = 0; rt < GTILES; ++rt)
 #pragma unroll
-        for (int p = 0; p < 2; ++p) s += red[t][wv][((p << 1) | hl) * 16 + col][r];
-      st_out<OUT_DT>(out, (int64_t)mloc * N + gn, s * x_scale[mloc]);
-    }
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float v = f[rt][t][r];
+#pragma unroll
+          for (int wv = 0; wv < GWAVES - 1; ++wv) v += red[wv][rt][t][lane][r];
+          const int m = t * 8 + 4 * (h & 1) + r, gn = n0 + rt * GEMV_ROWS + lj;
+          if (m < M && gn < N) st_out<OUT_DT>(out, (int64_t)m * N + gn, v * x_scale[m]);
+        }
   }
 }
 
@@ -200,23 +252,38 @@ __global__ void dequant_q4k_kernel(const uint8_t* __restrict__ w, float* __restr
   for (int e = 0; e < 32; ++e) o[e] = dsc * (float)((qs[e] >> shift) & 0xF) - dm;
 }
 
-template <int MT>
-void launch_gemv_mt(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
-                    int M, int N, int K, hipStream_t st) {
-  const dim3 grid((unsigned)((N + GEMV_ROWS - 1) / GEMV_ROWS));
-  const size_t lds = (size_t)(K / 32) * XS_MPAD * sizeof(int);
+template <int MT, bool XLDS>
+void launch_gemv_mtx(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
+                     int M, int N, int K, hipStream_t st) {
+  const dim3 grid((unsigned)((N + GEMV_ROWS * GTILES - 1) / (GEMV_ROWS * GTILES)));
+  const size_t lds = XLDS ? (size_t)M * K : 0;
   switch (odt) {
     case SL8_DTYPE_F16:
-      gemv_q4k_kernel<SL8_DTYPE_F16, MT><<<grid, GEMV_THREADS, lds, st>>>(x, xs, w, out, M, N, K);
+      gemv_q4k_kernel<SL8_DTYPE_F16, MT, XLDS><<<grid, 64 * GWAVES, lds, st>>>(x, xs, w, out, M, N, K);
       break;
     case SL8_DTYPE_BF16:
-      gemv_q4k_kernel<SL8_DTYPE_BF16, MT><<<grid, GEMV_THREADS, lds, st>>>(x, xs, w, out, M, N, K);
+      gemv_q4k_kernel<SL8_DTYPE_BF16, MT, XLDS><<<grid, 64 * GWAVES, lds, st>>>(x, xs, w, out, M, N, K);
       break;
     default:
-      gemv_q4k_kernel<SL8_DTYPE_F32, MT><<<grid, GEMV_THREADS, lds, st>>>(x, xs, w, out, M, N, K);
+      gemv_q4k_kernel<SL8_DTYPE_F32, MT, XLDS><<<grid, 64 * GWAVES, lds, st>>>(x, xs, w, out, M, N, K);
       break;
   }
 }
+
+// x goes to LDS when it is small (the decode shapes); otherwise operands are
+// read from global memory (L2-resident).
+template <int MT>
+void launch_gemv_mt(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
+                    int M, int N, int K, hipStream_t st) {
+  if ((int64_t)M * K <= XLDS_MAX) launch_gemv_mtx<MT, true>(x, xs, w, out, odt, M, N, K, st);
+  else launch_gemv_mtx<MT, false>(x, xs, w, out, odt, M, N, K, st);
+}
+
+}  // namespace
+}  // namespace sl8
+
+namespace sl8 {
+namespace {
 
 int check_q4k(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
               int64_t M, int64_t N, int64_t K) {
@@ -237,7 +304,7 @@ int check_q4k(const int8_t* x, const float* xs, const uint8_t* w, void* out, int
 
 using namespace sl8;
 
-// LDS budget for the x sub-block sums: K/32 * 16 ints.
+// K bound keeping every integer partial sum well inside int32.
 static constexpr int64_t kMaxGemvK = 65536;
 
 extern "C" int sl8_gemm_decode_q4k(const int8_t* x, const float* x_scale, const uint8_t* w,
