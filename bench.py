@@ -129,6 +129,18 @@ def bench_gemv(M, iters_graph=10, copies=8):
     return ms, nbytes
 
 
+def bench_copy(nbytes=256 << 20, iters=20):
+    """A plain device-to-device copy (torch): the practical HBM ceiling on this box.
+    Returns GB/s counting bytes read + bytes written."""
+    src = torch.empty(nbytes, device="cuda", dtype=torch.uint8)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    ms = _events_time(lambda: dst.copy_(src), iters, torch.cuda.current_stream())
+    return 2 * nbytes / (ms * 1e-3) / 1e9
+
+
 def cpu_baseline(budget_s=12.0):
     """numpy restatement (oracle) of config 1: prologue + causal attention,
     B=1, H=8, S=512, D=64, timed on this host; trimmed median over repeats."""
@@ -176,6 +188,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a plain 256 MiB device copy (scale for PMC byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -185,6 +199,13 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
 
+    if args.copy_calibration:
+        src = torch.empty(256 << 20, device="cuda", dtype=torch.uint8)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     ms, wall = bench_prefill(args.steps, args.warmup)
     tops = CFG2_OPS / (ms * 1e-3) / 1e12
     out = {
@@ -220,6 +241,7 @@ def main():
             sec[f"gemm_decode_q4k_cfg4_m{M}"] = {"us": round(gms * 1e3, 2), "GB/s": round(gbs, 1),
                                                  "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
                                                  "bytes": gbytes}
+        sec["hbm_copy_256MiB_GBps"] = round(bench_copy(), 1)
         out["secondary"] = sec
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
