@@ -20,6 +20,8 @@
 //     state and are merged by LSE in LDS at the end (fixed order, so results
 //     are deterministic).
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace sl8 {
@@ -211,25 +213,300 @@ decode_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sc
   }
 }
 
-// One block per query head; thread = channel.
+// One block per query head; thread = channel. The split maxima and sums are
+// read once into LDS; the partial vectors are read with one coalesced load
+// per split and channel.
 __global__ void decode_combine_kernel(const float* __restrict__ o_part,
                                       const float* __restrict__ m_part,
                                       const float* __restrict__ l_part,
                                       uint16_t* __restrict__ out, int n_splits, int bhq, int D) {
+  __shared__ float sm_m[DEC_MAX_SPLITS], sm_l[DEC_MAX_SPLITS];
+  __shared__ float sm_gm;
   const int64_t hq = blockIdx.x;
-  float gm = DEC_NEG_INF;
-  for (int s = 0; s < n_splits; ++s) gm = fmaxf(gm, m_part[(int64_t)s * bhq + hq]);
+  for (int s = threadIdx.x; s < n_splits; s += blockDim.x) {
+    sm_m[s] = m_part[(int64_t)s * bhq + hq];
+    sm_l[s] = l_part[(int64_t)s * bhq + hq];
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float gm = DEC_NEG_INF;
+    for (int s = 0; s < n_splits; ++s) gm = fmaxf(gm, sm_m[s]);
+    sm_gm = gm;
+  }
+  __syncthreads();
+  const float gm = sm_gm;
   for (int d = threadIdx.x; d < D; d += blockDim.x) {
     float acc = 0.f, den = 0.f;
+#pragma unroll 8
     for (int s = 0; s < n_splits; ++s) {
-      const int64_t row = (int64_t)s * bhq + hq;
-      const float ms = m_part[row];
+      const float ms = sm_m[s];
+      const float o = o_part[((int64_t)s * bhq + hq) * D + d];
       if (ms == DEC_NEG_INF) continue;
       const float wt = exp2f(ms - gm);
-      den += l_part[row] * wt;
-      acc += o_part[row * D + d] * wt;
+      den += sm_l[s] * wt;
+      acc += o * wt;
     }
     out[hq * D + d] = f2h_bits(den > 0.f ? acc / den : 0.f);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Streaming variant for GQA groups of 2 (D = 128), 4 or 8 query heads (the serving
+// shapes). Each wave is an independent stream over every 4th T-key tile of
+// the split: it copies its tiles HBM -> LDS with global_load_lds into a
+// private NB-stage ring and waits only on its own copies (no workgroup
+// barrier inside the loop), so loads of later tiles stay in flight while the
+// current tile is computed. Lane roles inside a wave (KL = 64 / GS lanes per
+// query head):
+//   * QK:  lane = (head h, key kl): v_dot4 over the int8 K row read from LDS
+//          (rows XOR-swizzled by 16-byte chunk, so the KL rows read together
+//          hit distinct banks) against that head's Q held in registers;
+//   * softmax: tile max / sums reduce over the KL lanes of a head;
+//   * PV:  lane = (head h, channel slice kl): CPL = D / KL channels, fp16 V
+//          converted inside v_fma_mix against P broadcast from LDS.
+// The 4 waves' states are merged by LSE in LDS at the end (fixed order).
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(1))) const void* gptr_t;
+typedef __attribute__((address_space(3))) void* lptr_t;
+
+// Value of lane (lane & ~(G-1)) + r, for G = 8, 16 or 32 (r a constant):
+// ds_swizzle bit mode within 32 lanes, lane' = (lane & and_mask) | or_mask.
+// It moves registers only (no LDS memory access), so it never waits on
+// LDS copies in flight.
+template <int G, int R>
+__device__ __forceinline__ float lane_bcast(float x) {
+  static_assert(G == 8 || G == 16 || G == 32, "group width");
+  static_assert(R >= 0 && R < G, "source lane");
+  constexpr int AND = 31 & ~(G - 1);
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), AND | (R << 5)));
+}
+
+// f(std::integral_constant<int, I>) for I = 0 .. N-1, fully unrolled.
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+template <int D, int GS>
+struct WaveCfg {
+  static constexpr int KL = 64 / GS;                  // lanes (keys) per head per sub-block
+  static constexpr int SUB = KL >= 16 ? 1 : 16 / KL;  // sub-blocks per tile
+  static constexpr int T = KL * SUB;                  // keys per tile
+  static constexpr int CPL = D / KL;                  // PV channels per lane
+  static constexpr int KC = D / 16;                   // 16-byte chunks per K row
+  static constexpr int KSW = (KC < 8 ? KC : 8) - 1;
+  static constexpr int KBYTES = T * D, VBYTES = 2 * T * D;
+  static constexpr int KDMA = KBYTES / 1024, VDMA = VBYTES / 1024;  // 1 KiB copies per wave
+  static constexpr int STAGE = KBYTES + VBYTES + 256;               // + k_scale (64 floats)
+  static_assert(KDMA >= 1 && KBYTES % 1024 == 0, "tile copy granularity");
+  static_assert(CPL % 8 == 0 || CPL == 4, "PV slice: 4 or a multiple of 8 channels");
+};
+
+template <int D, int GS, int NB>
+__global__ void __launch_bounds__(DEC_THREADS)
+decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_scale,
+                   const int8_t* __restrict__ k, const float* __restrict__ k_scale,
+                   const uint16_t* __restrict__ v, float* __restrict__ o_part,
+                   float* __restrict__ m_part, float* __restrict__ l_part, int n_len,
+                   int n_splits, int h_q, int h_kv, int bhq) {
+  using C = WaveCfg<D, GS>;
+  constexpr int KL = C::KL, SUB = C::SUB, T = C::T, CPL = C::CPL, KC = C::KC, KSW = C::KSW;
+  constexpr int STAGE = C::STAGE;
+  static_assert(NB >= 2 && NB <= 4, "ring depth");
+  // One LDS object per ring stage: the compiler then knows a copy into one
+  // stage never aliases reads of another and inserts no early vmcnt waits.
+  __shared__ __attribute__((aligned(16))) int8_t st0[DEC_WAVES * STAGE];
+  __shared__ __attribute__((aligned(16))) int8_t st1[DEC_WAVES * STAGE];
+  __shared__ __attribute__((aligned(16))) int8_t st2[NB > 2 ? DEC_WAVES * STAGE : 16];
+  __shared__ __attribute__((aligned(16))) int8_t st3[NB > 3 ? DEC_WAVES * STAGE : 16];
+  static_assert(DEC_WAVES * STAGE >= DEC_WAVES * GS * (D + 2) * 4, "merge area fits stage 0");
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  auto stage = [&](int u) -> int8_t* {
+    int8_t* s = u == 0 ? st0 : (u == 1 ? st1 : (u == 2 ? st2 : st3));
+    return s + wave * STAGE;
+  };
+
+  const int split = blockIdx.x;
+  const int bkv = blockIdx.y;
+  const int b = bkv / h_kv, kvh = bkv % h_kv;
+  const int per = (n_len + n_splits - 1) / n_splits;
+  const int n0 = split * per;
+  const int n1 = min(n_len, n0 + per);
+  const int ntiles = n1 > n0 ? (n1 - n0 + T - 1) / T : 0;
+  const int nt = ntiles > wave ? (ntiles - wave + DEC_WAVES - 1) / DEC_WAVES : 0;  // this wave's
+  const int8_t* kb = k + (int64_t)bkv * n_len * D;
+  const float* ksb = k_scale + (int64_t)bkv * n_len;
+  const uint16_t* vb = v + (int64_t)bkv * n_len * D;
+
+  const int h = lane / KL, kl = lane % KL;
+  const int64_t hq = (int64_t)b * h_q + (int64_t)kvh * GS + h;
+  int qv[D / 4];
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c) {
+    const int4 x = reinterpret_cast<const int4*>(q + hq * D)[c];
+    qv[4 * c] = x.x; qv[4 * c + 1] = x.y; qv[4 * c + 2] = x.z; qv[4 * c + 3] = x.w;
+  }
+  const float qsc = q_scale[hq];
+
+  // tile i of this wave = tile (wave + 4 i) of the split
+  auto load_tile = [&](int i, int8_t* sb) {
+    const int base = n0 + (wave + DEC_WAVES * i) * T;
+#pragma unroll
+    for (int j = 0; j < C::KDMA; ++j) {
+      const int id = j * 64 + lane, row = id / KC;
+      const int c = (id % KC) ^ (row & KSW);
+      __builtin_amdgcn_global_load_lds((gptr_t)(kb + (int64_t)min(base + row, n_len - 1) * D + 16 * c),
+                                       (lptr_t)(sb + j * 1024), 16, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < C::VDMA; ++j) {
+      const int id = j * 64 + lane, row = id / (D / 8);
+      __builtin_amdgcn_global_load_lds(
+          (gptr_t)(vb + (int64_t)min(base + row, n_len - 1) * D + 8 * (id % (D / 8))),
+          (lptr_t)(sb + C::KBYTES + j * 1024), 16, 0, 0);
+    }
+    __builtin_amdgcn_global_load_lds((gptr_t)(ksb + min(base + lane, n_len - 1)),
+                                     (lptr_t)(sb + C::KBYTES + C::VBYTES), 4, 0, 0);
+  };
+
+  float m_run = -INFINITY, l_lane = 0.f, oacc[CPL];
+#pragma unroll
+  for (int e = 0; e < CPL; ++e) oacc[e] = 0.f;
+
+  auto compute_tile = [&](int i, int8_t* sb) {
+    const int base = n0 + (wave + DEC_WAVES * i) * T;
+    const float* kst = reinterpret_cast<const float*>(sb + C::KBYTES + C::VBYTES);
+    const uint16_t* vt = reinterpret_cast<const uint16_t*>(sb + C::KBYTES);
+    float s[SUB];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < SUB; ++u) {
+      const int r = u * KL + kl;
+      int acc = 0;
+#pragma unroll
+      for (int c = 0; c < KC; ++c) {
+        const int4 kr = *reinterpret_cast<const int4*>(sb + r * D + 16 * (c ^ (r & KSW)));
+        acc = __builtin_amdgcn_sdot4(qv[4 * c + 0], kr.x, acc, false);
+        acc = __builtin_amdgcn_sdot4(qv[4 * c + 1], kr.y, acc, false);
+        acc = __builtin_amdgcn_sdot4(qv[4 * c + 2], kr.z, acc, false);
+        acc = __builtin_amdgcn_sdot4(qv[4 * c + 3], kr.w, acc, false);
+      }
+      s[u] = (base + r < n1) ? ((float)acc * qsc) * kst[r] : -INFINITY;
+      mx = fmaxf(mx, s[u]);
+    }
+#pragma unroll
+    for (int o = 1; o < KL; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    // key `base` is valid, so mx is finite for every head
+    const float mn = fmaxf(m_run, mx);
+    const float resc = __builtin_amdgcn_exp2f(m_run - mn);  // first tile: exp2(-inf) = 0
+    m_run = mn;
+    float ps = 0.f, p[SUB];
+#pragma unroll
+    for (int u = 0; u < SUB; ++u) {
+      p[u] = __builtin_amdgcn_exp2f(s[u] - mn);
+      ps += p[u];
+    }
+    l_lane = l_lane * resc + ps;
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) oacc[e] *= resc;
+#pragma unroll
+    for (int u = 0; u < SUB; ++u) {
+      static_for<0, KL>([&](auto rc) {
+        constexpr int rr = decltype(rc)::value;
+        // P of key u*KL+rr (held by lane h*KL+rr) to every lane of head h
+        const float pk = lane_bcast<KL, rr>(p[u]);
+        const uint16_t* vrow = vt + (u * KL + rr) * D + kl * CPL;
+        uint32_t vw[CPL / 2];
+        if constexpr (CPL % 8 == 0) {
+#pragma unroll
+          for (int c8 = 0; c8 < CPL; c8 += 8) {
+            const uint4 x = *reinterpret_cast<const uint4*>(vrow + c8);
+            vw[c8 / 2] = x.x; vw[c8 / 2 + 1] = x.y; vw[c8 / 2 + 2] = x.z; vw[c8 / 2 + 3] = x.w;
+          }
+        } else {
+          const uint2 x = *reinterpret_cast<const uint2*>(vrow);
+          vw[0] = x.x; vw[1] = x.y;
+        }
+#pragma unroll
+        for (int c = 0; c < CPL / 2; ++c) {
+          oacc[2 * c] = fmaf(pk, h2f(vw[c] & 0xFFFF), oacc[2 * c]);
+          oacc[2 * c + 1] = fmaf(pk, h2f(vw[c] >> 16), oacc[2 * c + 1]);
+        }
+      });
+    }
+  };
+
+  // Copies per tile per lane: KDMA + VDMA + 1, all from this wave. Before
+  // tile i is read, wait until only the copies of tiles i+1 .. i+NB-2 (issued
+  // later) may still be in flight; vmcnt retires in issue order.
+  constexpr int AHEAD = (NB - 1) * (C::KDMA + C::VDMA + 1);
+  static_assert(AHEAD < 64, "vmcnt range");
+  constexpr unsigned WAIT_AHEAD = 0x0F70u | (AHEAD & 15) | ((AHEAD >> 4) << 14);
+  // The Q loads above were issued before any copy, so the in-order vmcnt waits
+  // below also cover them.
+#pragma unroll
+  for (int i = 0; i < NB - 1; ++i)
+    if (i < nt) load_tile(i, stage(i));
+  for (int i0 = 0; i0 < nt; i0 += NB) {
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int i = i0 + u;
+      if (i < nt) {
+        if (i + NB - 1 < nt) {
+          // refills the stage read by tile i-1 (already consumed by this wave)
+          load_tile(i + NB - 1, stage((u + NB - 1) % NB));
+          __builtin_amdgcn_s_waitcnt(WAIT_AHEAD);
+        } else {
+          __builtin_amdgcn_s_waitcnt(0x0F70);
+        }
+        compute_tile(i, stage(u));
+      }
+    }
+  }
+
+  // ---- per-wave state -> LDS (this wave's own stage-0 area), then LSE merge ----
+#pragma unroll
+  for (int o = 1; o < KL; o <<= 1) l_lane += __shfl_xor(l_lane, o, 64);
+  float* red = reinterpret_cast<float*>(st0);  // [wave][GS][D] o, then [wave][GS] m, l
+  float* ro = red + wave * GS * D;
+  float* rm = red + DEC_WAVES * GS * D + wave * GS;
+  float* rl = red + DEC_WAVES * GS * D + DEC_WAVES * GS + wave * GS;
+  __syncthreads();  // every wave is past its last read of stage 0
+#pragma unroll
+  for (int e = 0; e < CPL; e += 4)
+    *reinterpret_cast<float4*>(ro + h * D + kl * CPL + e) =
+        make_float4(oacc[e], oacc[e + 1], oacc[e + 2], oacc[e + 3]);
+  if (kl == 0) {
+    rm[h] = m_run;
+    rl[h] = l_lane;
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < GS * D; idx += DEC_THREADS) {
+    const int hh = idx / D, d = idx % D;
+    float mm = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < DEC_WAVES; ++w) mm = fmaxf(mm, red[DEC_WAVES * GS * D + w * GS + hh]);
+    float acc = 0.f, den = 0.f;
+    if (mm != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < DEC_WAVES; ++w) {
+        const float mw = red[DEC_WAVES * GS * D + w * GS + hh];
+        const float wt = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - mm);
+        acc += red[w * GS * D + hh * D + d] * wt;
+        den += red[DEC_WAVES * GS * D + DEC_WAVES * GS + w * GS + hh] * wt;
+      }
+    }
+    const int64_t row = (int64_t)split * bhq + (int64_t)b * h_q + (int64_t)kvh * GS + hh;
+    o_part[row * D + d] = acc;
+    if (d == 0) {
+      m_part[row] = mm == -INFINITY ? DEC_NEG_INF : mm;
+      l_part[row] = den;
+    }
   }
 }
 
@@ -310,7 +587,23 @@ extern "C" int sl8_attn_int8_decode(const int8_t* q, const float* q_scale, const
   float* lp = mp + (size_t)ns * bhq;
   const dim3 grid((unsigned)ns, (unsigned)(B * Hkv), (unsigned)((gsz + G - 1) / G));
   const uint16_t* vp = static_cast<const uint16_t*>(v);
-  switch (D) {
+  if ((gsz == 2 && D == 128) || gsz == 4 || gsz == 8) {
+    const dim3 g2((unsigned)ns, (unsigned)(B * Hkv));
+#define SL8_WAVE(DD, GS, NB)                                                                   \
+    decode_wave_kernel<DD, GS, NB><<<g2, DEC_THREADS, 0, st>>>(q, q_scale, k, k_scale, vp, op, mp, lp, \
+                                                             (int)N, ns, (int)Hq, (int)Hkv, bhq)
+#define SL8_WAVE_D(GS)                         \
+    if (D == 64) SL8_WAVE(64, GS, 4);          \
+    else if (D == 128) SL8_WAVE(128, GS, 3);   \
+    else SL8_WAVE(256, GS, 3);
+    switch (gsz) {
+      case 2: SL8_WAVE(128, 2, 3); break;
+      case 4: SL8_WAVE_D(4); break;
+      default: SL8_WAVE_D(8); break;
+    }
+#undef SL8_WAVE_D
+#undef SL8_WAVE
+  } else switch (D) {
     case 64: launch_d<64>(G, grid, q, q_scale, k, k_scale, vp, op, mp, lp, (int)N, ns, (int)Hq, (int)Hkv, gsz, bhq, st); break;
     case 128: launch_d<128>(G, grid, q, q_scale, k, k_scale, vp, op, mp, lp, (int)N, ns, (int)Hq, (int)Hkv, gsz, bhq, st); break;
     default: launch_d<256>(G, grid, q, q_scale, k, k_scale, vp, op, mp, lp, (int)N, ns, (int)Hq, (int)Hkv, gsz, bhq, st); break;

@@ -15,6 +15,7 @@ DECODE_SHAPES = [  # reference tests/test_decode.py:28-43
     (1, 32, 8, 4096, 128), (1, 4, 4, 512, 256), (2, 8, 2, 1024, 256), (1, 16, 4, 777, 256),
     (1, 32, 1, 300, 128),  # MQA with 32 query heads per KV head
     (3, 6, 2, 5, 64),      # fewer keys than splits
+    (2, 8, 2, 1000, 64), (1, 64, 8, 1500, 128), (1, 16, 2, 333, 256), (2, 8, 4, 999, 128),  # streaming paths
 ]
 
 
