@@ -54,179 +54,339 @@ __device__ __forceinline__ ScMin unpack_scmin(uint32_t s0, uint32_t s1, uint32_t
 }
 __device__ __forceinline__ int byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xFF; }
 
-// Work split: a workgroup = GTILES 16-row MFMA tiles = 4 waves, each wave
-// taking one quarter of the super-blocks of K; partial sums are reduced
-// through LDS in a fixed order. Each wave issues every weight load of its
-// share (up to GCH super-blocks per tile) before it waits for any of them,
-// so a wave costs one memory round trip; meanwhile the workgroup stages the
-// activations (M x K int8) into LDS, where the x operands are read from.
-// At the config shape (N = 17408, K = 5120) this is 4352 waves at 4 waves
-// per SIMD.
-// Per group and row tile: one MFMA for <x, q> (scaled by sc_j in the integer
-// domain with v_mad_i32_i24) and one MFMA whose B operand holds m_j in every
-// slot of the sub-block, so it accumulates m_j * sum(x_j) over the
-// super-block in its own accumulator.
+// Work split: a workgroup = one 16-row MFMA tile = 4 waves, each wave taking
+// one quarter of the super-blocks of K (in chunks of up to GCH); partial
+// sums are reduced through LDS in a fixed order.
+// Loads: for a coalesced stream, lane 4*r + c reads 16-byte piece c of weight
+// row r (64 contiguous bytes per row and instruction) -- the MFMA operand
+// layout wants lane r + 16*c instead, so after the loads land the pieces are
+// moved across lanes with ds_bpermute (no LDS memory traffic). Every load of
+// a chunk is issued before any is consumed (one round trip per chunk); the
+// activation slice is copied into the wave's LDS area meanwhile.
+// Operand mapping (lane = column lj + 16*h): lane h holds bytes 16h..16h+15
+// of each 64-byte half L of the row's nibble array, i.e. elements
+// 16(h&1)..+15 of sub-block 4L + 2(h>>1) (low nibbles) or 4L + 2(h>>1) + 1
+// (high nibbles). A-operand rows 0..7 are activation rows for lane groups
+// h = 0,1 (zero in groups 2,3), rows 8..15 the same activations for groups
+// 2,3: C row 4h'+r then holds the sum over exactly one sub-block. Each
+// (half, nibble) pair is one MFMA for <x, q> (scaled by sc_j in the integer
+// domain with v_mad_i32_i24) plus one MFMA whose B operand holds m_j in
+// every slot, accumulating m_j * sum(x_j) per super-block.
 constexpr int GCH = 5;     // super-blocks per wave and chunk
 constexpr int GWAVES = 4;  // K split
-constexpr int GTILES = 1;  // 16-row tiles per wave
-constexpr int XLDS_MAX = 48 * 1024;
+constexpr int GXPITCH = GCH * 256;  // LDS bytes per activation row and wave
 
-template <int OUT_DT, int MT, bool XLDS>
-__global__ void __launch_bounds__(64 * GWAVES)
+typedef __attribute__((address_space(1))) const void* q4_gptr_t;
+typedef __attribute__((address_space(3))) void* q4_lptr_t;
+
+
+__device__ __forceinline__ uint32_t lane_pull(uint32_t v, int src_lane) {
+  return (uint32_t)__builtin_amdgcn_ds_bpermute(src_lane << 2, (int)v);
+}
+
+// MT = 1: at most 96 registers, so 5 waves per SIMD and every workgroup of
+// the decode shapes (N / 16 = 1088 at N = 17408) is resident at once.
+template <int OUT_DT, int MT>
+__global__ void __launch_bounds__(64 * GWAVES, MT == 1 ? 5 : 1)
 gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
                 const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K) {
-  __shared__ float red[GWAVES - 1][GTILES][MT][32][4];
-  extern __shared__ __attribute__((aligned(16))) int8_t x_lds[];  // XLDS: x [M][K]
-
+  extern __shared__ __attribute__((aligned(16))) int8_t xl[];  // per wave: [M][GXPITCH]
+  __shared__ float red[GWAVES - 1][MT][32][4];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nsb = K >> 8;
-  const int lj = lane & 15;  // B column (weight row in the tile) / A row
-  const int h = lane >> 4;   // k-slot group: bytes 8h..8h+7 of each 32-byte nibble group
-  const int hp = h >> 1;     // sub-block parity of this lane's C rows
-  const int n0 = blockIdx.x * (GEMV_ROWS * GTILES);
+  const int lj = lane & 15;  // operand column (weight row in the tile) / A row
+  const int h = lane >> 4;   // operand k-slot group
+  const int hp = h >> 1;     // sub-block parity of this lane's k-slots and C rows
+  const int lr = lane >> 2, lc = lane & 3;  // load role: weight row, 16-byte piece
+  const int src_q = 4 * lj + h;             // lane holding (row lj, piece h)
+  const int n0 = blockIdx.x * GEMV_ROWS;
   const int64_t row_bytes = (int64_t)nsb * Q4K_BYTES;
-  const uint8_t* wrow[GTILES];
-#pragma unroll
-  for (int rt = 0; rt < GTILES; ++rt)
-    wrow[rt] = w + (int64_t)min(n0 + rt * GEMV_ROWS + lj, N - 1) * row_bytes;
-  const int a_m = lj & 7;    // A-operand row: activation t*8 + a_m, sub-block parity a_p
-  const int a_p = lj >> 3;
-  const uint32_t mlo = a_p == 0 ? 0xFFFFFFFFu : 0u, mhi = ~mlo;
+  const uint8_t* wrow = w + (int64_t)min(n0 + lr, N - 1) * row_bytes;
+  const int a_m = lj & 7;    // A-operand row: activation t*8 + a_m, parity lj >> 3
+  const bool a_side = (lj >> 3) == hp;  // this lane's k-slots feed its A row
   bool a_on[MT];
 #pragma unroll
-  for (int t = 0; t < MT; ++t) a_on[t] = t * 8 + a_m < M;
-  const int sh = 8 * hp;     // byte of the lane's sub-block inside a scale dword pair
+  for (int t = 0; t < MT; ++t) a_on[t] = a_side && (t * 8 + a_m < M);
+  // per-wave area rounded up to whole 1 KiB copies (a copy writes 64 x 16 B)
+  int8_t* xw = xl + (int64_t)wave * ((M * GXPITCH + 1023) & ~1023);
 
-  float f[GTILES][MT][4];
+  float f[MT][4];
 #pragma unroll
-  for (int rt = 0; rt < GTILES; ++rt)
+  for (int t = 0; t < MT; ++t)
 #pragma unroll
-    for (int t = 0; t < MT; ++t)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) f[rt][t][r] = 0.f;
+    for (int r = 0; r < 4; ++r) f[t][r] = 0.f;
 
-  const int sb0 = (wave * nsb) / GWAVES, sb1 = ((wave + 1) * nsb) / GWAVES;  // may be empty
-  // the same chunk count for every wave keeps the staging barrier uniform
-  const int nch = ((nsb + GWAVES - 1) / GWAVES + GCH - 1) / GCH;
-  for (int c = 0; c < nch; ++c) {
-    const int c0 = sb0 + c * GCH;
-    uint4 hdr[GCH][GTILES];
-    uint2 qv[GCH][GTILES][4];
+  // One chunk of up to GCH super-blocks starting at c0.
+  auto chunk = [&](const int c0, const int cnt) {
+    // ---- weights: header dword lc and two 16-byte nibble pieces per super-block ----
+    uint32_t hd[GCH];
+    uint4 qa[GCH], qb[GCH];
 #pragma unroll
     for (int i = 0; i < GCH; ++i) {
-      const int sb = min(c0 + i, nsb - 1);  // always a valid block; unused ones are skipped
-#pragma unroll
-      for (int rt = 0; rt < GTILES; ++rt) {
-        const uint8_t* blk = wrow[rt] + (int64_t)sb * Q4K_BYTES;
-        hdr[i][rt] = *reinterpret_cast<const uint4*>(blk);
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-          qv[i][rt][g] = *reinterpret_cast<const uint2*>(blk + 16 + 32 * g + 8 * h);
-      }
+      const uint8_t* blk = wrow + (int64_t)min(c0 + i, nsb - 1) * Q4K_BYTES;
+      hd[i] = *reinterpret_cast<const uint32_t*>(blk + 4 * lc);
+      qa[i] = *reinterpret_cast<const uint4*>(blk + 16 + 16 * lc);
+      qb[i] = *reinterpret_cast<const uint4*>(blk + 80 + 16 * lc);
     }
-    if (XLDS && c == 0) {
-      // activations into LDS while the first weight loads are in flight
-      const int n16 = M * K / 16;
-      for (int v = tid; v < n16; v += 64 * GWAVES)
-        reinterpret_cast<int4*>(x_lds)[v] = reinterpret_cast<const int4*>(x)[v];
-      __syncthreads();
+    // ---- activations of the chunk: M rows x cnt*256 bytes -> this wave's LDS area ----
+    const int xch = M * (GXPITCH / 16);
+    for (int j = 0; j * 64 < xch; ++j) {
+      const int id = min(j * 64 + lane, xch - 1);
+      const int m = id / (GXPITCH / 16), pos = min(id % (GXPITCH / 16), cnt * 16 - 1);
+      __builtin_amdgcn_global_load_lds((q4_gptr_t)(x + (int64_t)m * K + (int64_t)c0 * 256 + 16 * pos),
+                                       (q4_lptr_t)(xw + j * 1024), 16, 0, 0);
     }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): weights and activations landed
 #pragma unroll
     for (int i = 0; i < GCH; ++i) {
-      if (c0 + i < sb1) {
-        const int sb = c0 + i;
-        ScMin sm[GTILES];
-        int T[GTILES][MT][4];
-        v4i U[GTILES][MT];
+      if (i < cnt) {
+        // ---- pieces to the operand layout ----
+        const uint32_t h0 = lane_pull(hd[i], 4 * lj + 0), h1 = lane_pull(hd[i], 4 * lj + 1);
+        const uint32_t h2 = lane_pull(hd[i], 4 * lj + 2), h3 = lane_pull(hd[i], 4 * lj + 3);
+        uint32_t qw[2][4];
+        qw[0][0] = lane_pull(qa[i].x, src_q); qw[0][1] = lane_pull(qa[i].y, src_q);
+        qw[0][2] = lane_pull(qa[i].z, src_q); qw[0][3] = lane_pull(qa[i].w, src_q);
+        qw[1][0] = lane_pull(qb[i].x, src_q); qw[1][1] = lane_pull(qb[i].y, src_q);
+        qw[1][2] = lane_pull(qb[i].z, src_q); qw[1][3] = lane_pull(qb[i].w, src_q);
+        const ScMin sm = unpack_scmin(h1, h2, h3);
+        int T[MT][4];
+        v4i U[MT];
 #pragma unroll
-        for (int rt = 0; rt < GTILES; ++rt) {
-          sm[rt] = unpack_scmin(hdr[i][rt].y, hdr[i][rt].z, hdr[i][rt].w);
+        for (int t = 0; t < MT; ++t) {
+          U[t] = v4i{0, 0, 0, 0};
 #pragma unroll
-          for (int t = 0; t < MT; ++t) {
-            U[rt][t] = v4i{0, 0, 0, 0};
-#pragma unroll
-            for (int r = 0; r < 4; ++r) T[rt][t][r] = 0;
-          }
+          for (int r = 0; r < 4; ++r) T[t][r] = 0;
         }
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          v4i aop[MT];
+        for (int L = 0; L < 2; ++L) {
 #pragma unroll
-          for (int t = 0; t < MT; ++t) {
-            const int64_t xo = (int64_t)min(t * 8 + a_m, M - 1) * K + sb * 256 + 64 * g + 32 * a_p + 8 * h;
-            const uint2 xv = XLDS ? *reinterpret_cast<const uint2*>(x_lds + xo)
-                                  : *reinterpret_cast<const uint2*>(x + xo);
-            const uint32_t xlo = a_on[t] ? xv.x : 0u, xhi = a_on[t] ? xv.y : 0u;
-            aop[t] = v4i{(int)(xlo & mlo), (int)(xhi & mlo), (int)(xlo & mhi), (int)(xhi & mhi)};
-          }
-#pragma unroll
-          for (int rt = 0; rt < GTILES; ++rt) {
-            const uint32_t w0 = qv[i][rt][g].x, w1 = qv[i][rt][g].y;
-            const v4i bop = {(int)(w0 & 0x0F0F0F0Fu), (int)(w1 & 0x0F0F0F0Fu),
-                             (int)((w0 >> 4) & 0x0F0F0F0Fu), (int)((w1 >> 4) & 0x0F0F0F0Fu)};
-            // sub-blocks 2g (low slots) and 2g+1 (high slots) of this column's row
-            const uint32_t scw = g < 2 ? sm[rt].sc_lo : sm[rt].sc_hi;
-            const uint32_t mnw = g < 2 ? sm[rt].mn_lo : sm[rt].mn_hi;
-            const int sc = (scw >> (16 * (g & 1) + sh)) & 0xFF;
-            const uint32_t m_lo = ((mnw >> (16 * (g & 1))) & 0xFF) * 0x01010101u;
-            const uint32_t m_hi = ((mnw >> (16 * (g & 1) + 8)) & 0xFF) * 0x01010101u;
-            const v4i bmin = {(int)m_lo, (int)m_lo, (int)m_hi, (int)m_hi};
+          for (int nb = 0; nb < 2; ++nb) {
+            const int sh = 4 * nb;
+            const v4i bop = {(int)((qw[L][0] >> sh) & 0x0F0F0F0Fu), (int)((qw[L][1] >> sh) & 0x0F0F0F0Fu),
+                             (int)((qw[L][2] >> sh) & 0x0F0F0F0Fu), (int)((qw[L][3] >> sh) & 0x0F0F0F0Fu)};
+            // sub-block 4L + 2hp + nb of this column's row
+            const int bsel = 8 * (2 * hp + nb);
+            const int sc = ((L == 0 ? sm.sc_lo : sm.sc_hi) >> bsel) & 0xFF;
+            const uint32_t mn = (((L == 0 ? sm.mn_lo : sm.mn_hi) >> bsel) & 0xFF) * 0x01010101u;
+            const v4i bmin = {(int)mn, (int)mn, (int)mn, (int)mn};
+            const int sub = 4 * L + 2 * hp + nb;
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
+              const int m = min(t * 8 + a_m, M - 1);
+              const int4 xv = *reinterpret_cast<const int4*>(xw + m * GXPITCH + i * 256 + 32 * sub +
+                                                             16 * (h & 1));
+              const v4i aop = a_on[t] ? v4i{xv.x, xv.y, xv.z, xv.w} : v4i{0, 0, 0, 0};
               const v4i z = {0, 0, 0, 0};
-              const v4i cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(aop[t], bop, z, 0, 0, 0);
-              U[rt][t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aop[t], bmin, U[rt][t], 0, 0, 0);
+              const v4i cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(aop, bop, z, 0, 0, 0);
+              U[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aop, bmin, U[t], 0, 0, 0);
 #pragma unroll
-              for (int r = 0; r < 4; ++r) T[rt][t][r] += __mul24(sc, cc[r]);
+              for (int r = 0; r < 4; ++r) T[t][r] += __mul24(sc, cc[r]);
             }
           }
         }
+        const float d = h2f(h0 & 0xFFFFu);
+        const float dmin = h2f(h0 >> 16);
 #pragma unroll
-        for (int rt = 0; rt < GTILES; ++rt) {
-          const float d = h2f(hdr[i][rt].x & 0xFFFFu);
-          const float dmin = h2f(hdr[i][rt].x >> 16);
+        for (int t = 0; t < MT; ++t)
 #pragma unroll
-          for (int t = 0; t < MT; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              f[rt][t][r] += d * (float)T[rt][t][r] - dmin * (float)U[rt][t][r];
-        }
+          for (int r = 0; r < 4; ++r) f[t][r] += d * (float)T[t][r] - dmin * (float)U[t][r];
       }
     }
+    __builtin_amdgcn_wave_barrier();  // the next chunk's copies overwrite xw
+  };
+
+  const int sb0 = (wave * nsb) / GWAVES, sb1 = ((wave + 1) * nsb) / GWAVES;  // may be empty
+  if (sb1 - sb0 <= GCH) {
+    // the decode shapes: one chunk, straight-line code (precise load waits)
+    if (sb1 > sb0) chunk(sb0, sb1 - sb0);
+  } else {
+    for (int c0 = sb0; c0 < sb1; c0 += GCH) chunk(c0, min(GCH, sb1 - c0));
   }
 
   // C row i = 4h + r holds activation row t*8 + (i & 7) of sub-block parity i >> 3:
   // add the two parities (lanes h and h^2), then the K quarters, in fixed order.
 #pragma unroll
-  for (int rt = 0; rt < GTILES; ++rt)
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) f[t][r] += __shfl_xor(f[t][r], 32, 64);
+  if (wave > 0 && lane < 32) {
 #pragma unroll
     for (int t = 0; t < MT; ++t)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) f[rt][t][r] += __shfl_xor(f[rt][t][r], 32, 64);
-  if (wave > 0 && lane < 32) {
-#pragma unroll
-    for (int rt = 0; rt < GTILES; ++rt)
-#pragma unroll
-      for (int t = 0; t < MT; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) red[wave - 1][rt][t][lane][r] = f[rt][t][r];
+      for (int r = 0; r < 4; ++r) red[wave - 1][t][lane][r] = f[t][r];
   }
   __syncthreads();
   if (wave == 0 && lane < 32) {
 #pragma unroll
-    for (int rt = 0; rt < GTILES; ++rt)
+    for (int t = 0; t < MT; ++t)
 #pragma unroll
-      for (int t = 0; t < MT; ++t)
+      for (int r = 0; r < 4; ++r) {
+        float v = f[t][r];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float v = f[rt][t][r];
+        for (int wv = 0; wv < GWAVES - 1; ++wv) v += red[wv][t][lane][r];
+        const int m = t * 8 + 4 * (h & 1) + r, gn = n0 + lj;
+        if (m < M && gn < N) st_out<OUT_DT>(out, (int64_t)m * N + gn, v * x_scale[m]);
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// M <= 2: the same workgroup/K split, but the dot products run on VALU
+// v_dot4 in the load layout itself -- lane 4r + c owns 16-byte piece c of
+// each 64-byte half of weight row r, i.e. elements 16(c&1)..+15 of
+// sub-blocks j = 2(c>>1) (low nibbles) and j+1 (high nibbles) of that half
+// -- so nothing moves across lanes except the row's header dwords (a DPP
+// quad broadcast). Activations are loaded first, then every weight load of
+// the chunk; the activations go to LDS (with their 16-element sums, shared
+// by all rows) as soon as they land, and super-block i is computed as soon
+// as its own loads land while later ones are still in flight.
+// ---------------------------------------------------------------------------
+template <int R>
+__device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, R * 0x55, 0xF, 0xF, false);
+}
+
+template <int OUT_DT, int MR>
+__global__ void __launch_bounds__(64 * GWAVES)
+gemv_q4k_small_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
+                      const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K) {
+  constexpr int XC = (MR * GXPITCH + 1023) / 1024;  // 16-byte activation pieces per lane
+  __shared__ __attribute__((aligned(16))) int8_t xs_l[GWAVES][XC * 1024];
+  __shared__ __attribute__((aligned(16))) int xsum_l[GWAVES][MR][GCH][2][8];  // [m][i][half][j]
+  __shared__ float red[GWAVES - 1][16][MR];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nsb = K >> 8;
+  const int r = lane >> 2, c = lane & 3;
+  const int g = c >> 1, half = c & 1;
+  const int n0 = blockIdx.x * GEMV_ROWS;
+  const int64_t row_bytes = (int64_t)nsb * Q4K_BYTES;
+  const uint8_t* wrow = w + (int64_t)min(n0 + r, N - 1) * row_bytes;
+  int8_t* xw = &xs_l[wave][0];
+
+  float f[MR];
 #pragma unroll
-          for (int wv = 0; wv < GWAVES - 1; ++wv) v += red[wv][rt][t][lane][r];
-          const int m = t * 8 + 4 * (h & 1) + r, gn = n0 + rt * GEMV_ROWS + lj;
-          if (m < M && gn < N) st_out<OUT_DT>(out, (int64_t)m * N + gn, v * x_scale[m]);
+  for (int m = 0; m < MR; ++m) f[m] = 0.f;
+
+  auto chunk = [&](const int c0, const int cnt) {
+    // ---- activations first: M rows x cnt*256 bytes, lane-linear 16-byte pieces ----
+    const int xch = M * (GXPITCH / 16);
+    static_assert(XC <= 3, "activation pieces per lane");
+    auto xload = [&](int j) -> uint4 {
+      const int id = min(j * 64 + lane, xch - 1);
+      const int m = id / (GXPITCH / 16), pos = min(id % (GXPITCH / 16), cnt * 16 - 1);
+      return *reinterpret_cast<const uint4*>(x + (int64_t)m * K + (int64_t)c0 * 256 + 16 * pos);
+    };
+    const uint4 xq0 = xload(0);
+    const uint4 xq1 = XC > 1 ? xload(1) : xq0;
+    const uint4 xq2 = XC > 2 ? xload(2) : xq0;
+    __builtin_amdgcn_sched_barrier(0);
+    // ---- then every weight load of the chunk ----
+    // (two per-lane base pointers plus immediate offsets; a partial chunk
+    // re-reads its last super-block instead of running past the row)
+    uint32_t hd[GCH];
+    uint4 qa[GCH], qb[GCH];
+    const uint8_t* bh = wrow + (int64_t)c0 * Q4K_BYTES + 4 * c;
+    const uint8_t* bq = wrow + (int64_t)c0 * Q4K_BYTES + 16 * c;
+#pragma unroll
+    for (int i = 0; i < GCH; ++i) {
+      const int ii = cnt == GCH ? i : min(i, cnt - 1);
+      hd[i] = *reinterpret_cast<const uint32_t*>(bh + ii * Q4K_BYTES);
+      qa[i] = *reinterpret_cast<const uint4*>(bq + ii * Q4K_BYTES + 16);
+      qb[i] = *reinterpret_cast<const uint4*>(bq + ii * Q4K_BYTES + 80);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // ---- activations to LDS ([m][GXPITCH]) and their 16-element sums ----
+    *reinterpret_cast<uint4*>(xw + 16 * lane) = xq0;
+    if (XC > 1) *reinterpret_cast<uint4*>(xw + 1024 + 16 * lane) = xq1;
+    if (XC > 2) *reinterpret_cast<uint4*>(xw + 2048 + 16 * lane) = xq2;
+    __builtin_amdgcn_wave_barrier();
+    // sum over elements 16*half2..+15 of sub-block j2 of super-block i2, row m2
+    for (int e = lane; e < MR * GCH * 16; e += 64) {
+      const int m2 = e / (GCH * 16), i2 = (e / 16) % GCH, half2 = (e / 8) & 1, j2 = e & 7;
+      const int4 v = *reinterpret_cast<const int4*>(xw + m2 * GXPITCH + i2 * 256 + 32 * j2 + 16 * half2);
+      int sacc = __builtin_amdgcn_sdot4(v.x, 0x01010101, 0, false);
+      sacc = __builtin_amdgcn_sdot4(v.y, 0x01010101, sacc, false);
+      sacc = __builtin_amdgcn_sdot4(v.z, 0x01010101, sacc, false);
+      sacc = __builtin_amdgcn_sdot4(v.w, 0x01010101, sacc, false);
+      xsum_l[wave][m2][i2][half2][j2] = sacc;
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int i = 0; i < GCH; ++i) {
+      if (i < cnt) {
+        // header dwords of row r, from the quad's lanes 4r .. 4r+3
+        const uint32_t h0 = quad_bcast<0>(hd[i]), h1 = quad_bcast<1>(hd[i]);
+        const uint32_t h2 = quad_bcast<2>(hd[i]), h3 = quad_bcast<3>(hd[i]);
+        const ScMin sm = unpack_scmin(h1, h2, h3);
+        // this lane's sub-blocks: j0 = 2g, j0+1 (half 0 of the row), j0+4, j0+5 (half 1)
+        const int bs = 16 * g;
+        const int sc0 = (sm.sc_lo >> bs) & 0xFF, sc1 = (sm.sc_lo >> (bs + 8)) & 0xFF;
+        const int sc4 = (sm.sc_hi >> bs) & 0xFF, sc5 = (sm.sc_hi >> (bs + 8)) & 0xFF;
+        const int mn0 = (sm.mn_lo >> bs) & 0xFF, mn1 = (sm.mn_lo >> (bs + 8)) & 0xFF;
+        const int mn4 = (sm.mn_hi >> bs) & 0xFF, mn5 = (sm.mn_hi >> (bs + 8)) & 0xFF;
+        const uint32_t wa[4] = {qa[i].x, qa[i].y, qa[i].z, qa[i].w};
+        const uint32_t wbq[4] = {qb[i].x, qb[i].y, qb[i].z, qb[i].w};
+        const float d = h2f(h0 & 0xFFFFu), dmin = h2f(h0 >> 16);
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+          const int8_t* xb = xw + m * GXPITCH + i * 256 + 16 * half;
+          const int4 x0 = *reinterpret_cast<const int4*>(xb + 32 * (2 * g));
+          const int4 x1 = *reinterpret_cast<const int4*>(xb + 32 * (2 * g + 1));
+          const int4 x4 = *reinterpret_cast<const int4*>(xb + 32 * (2 * g + 4));
+          const int4 x5 = *reinterpret_cast<const int4*>(xb + 32 * (2 * g + 5));
+          const int xa0[4] = {x0.x, x0.y, x0.z, x0.w}, xa1[4] = {x1.x, x1.y, x1.z, x1.w};
+          const int xa4[4] = {x4.x, x4.y, x4.z, x4.w}, xa5[4] = {x5.x, x5.y, x5.z, x5.w};
+          int p0 = 0, p1 = 0, p4 = 0, p5 = 0;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            p0 = __builtin_amdgcn_sdot4(xa0[k], (int)(wa[k] & 0x0F0F0F0Fu), p0, false);
+            p1 = __builtin_amdgcn_sdot4(xa1[k], (int)((wa[k] >> 4) & 0x0F0F0F0Fu), p1, false);
+            p4 = __builtin_amdgcn_sdot4(xa4[k], (int)(wbq[k] & 0x0F0F0F0Fu), p4, false);
+            p5 = __builtin_amdgcn_sdot4(xa5[k], (int)((wbq[k] >> 4) & 0x0F0F0F0Fu), p5, false);
+          }
+          const int* xsr = &xsum_l[wave][m][i][half][0];
+          const int2 s01 = *reinterpret_cast<const int2*>(xsr + 2 * g);
+          const int2 s45 = *reinterpret_cast<const int2*>(xsr + 4 + 2 * g);
+          const int T = __mul24(sc0, p0) + __mul24(sc1, p1) + __mul24(sc4, p4) + __mul24(sc5, p5);
+          const int U = __mul24(mn0, s01.x) + __mul24(mn1, s01.y) + __mul24(mn4, s45.x) +
+                        __mul24(mn5, s45.y);
+          f[m] += d * (float)T - dmin * (float)U;
         }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();  // the next chunk rewrites xw / xsum_l
+  };
+
+  const int sb0 = (wave * nsb) / GWAVES, sb1 = ((wave + 1) * nsb) / GWAVES;  // may be empty
+  if (sb1 - sb0 == GCH) {
+    chunk(sb0, GCH);  // the decode shapes: one full chunk, immediate offsets
+  } else {
+    for (int c0 = sb0; c0 < sb1; c0 += GCH) chunk(c0, min(GCH, sb1 - c0));
+  }
+
+  // quad sum (the 4 pieces of a row), then the K quarters in fixed order
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    f[m] += __shfl_xor(f[m], 1, 64);
+    f[m] += __shfl_xor(f[m], 2, 64);
+  }
+  if (wave > 0 && c == 0) {
+#pragma unroll
+    for (int m = 0; m < MR; ++m) red[wave - 1][r][m] = f[m];
+  }
+  __syncthreads();
+  if (wave == 0 && c == 0) {
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      float v = f[m];
+#pragma unroll
+      for (int wv = 0; wv < GWAVES - 1; ++wv) v += red[wv][r][m];
+      const int gn = n0 + r;
+      if (m < M && gn < N) st_out<OUT_DT>(out, (int64_t)m * N + gn, v * x_scale[m]);
+    }
   }
 }
 
@@ -252,31 +412,39 @@ __global__ void dequant_q4k_kernel(const uint8_t* __restrict__ w, float* __restr
   for (int e = 0; e < 32; ++e) o[e] = dsc * (float)((qs[e] >> shift) & 0xF) - dm;
 }
 
-template <int MT, bool XLDS>
-void launch_gemv_mtx(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
-                     int M, int N, int K, hipStream_t st) {
-  const dim3 grid((unsigned)((N + GEMV_ROWS * GTILES - 1) / (GEMV_ROWS * GTILES)));
-  const size_t lds = XLDS ? (size_t)M * K : 0;
+template <int MR>
+void launch_gemv_small(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
+                       int M, int N, int K, hipStream_t st) {
+  const dim3 grid((unsigned)((N + GEMV_ROWS - 1) / GEMV_ROWS));
   switch (odt) {
     case SL8_DTYPE_F16:
-      gemv_q4k_kernel<SL8_DTYPE_F16, MT, XLDS><<<grid, 64 * GWAVES, lds, st>>>(x, xs, w, out, M, N, K);
+      gemv_q4k_small_kernel<SL8_DTYPE_F16, MR><<<grid, 64 * GWAVES, 0, st>>>(x, xs, w, out, M, N, K);
       break;
     case SL8_DTYPE_BF16:
-      gemv_q4k_kernel<SL8_DTYPE_BF16, MT, XLDS><<<grid, 64 * GWAVES, lds, st>>>(x, xs, w, out, M, N, K);
+      gemv_q4k_small_kernel<SL8_DTYPE_BF16, MR><<<grid, 64 * GWAVES, 0, st>>>(x, xs, w, out, M, N, K);
       break;
     default:
-      gemv_q4k_kernel<SL8_DTYPE_F32, MT, XLDS><<<grid, 64 * GWAVES, lds, st>>>(x, xs, w, out, M, N, K);
+      gemv_q4k_small_kernel<SL8_DTYPE_F32, MR><<<grid, 64 * GWAVES, 0, st>>>(x, xs, w, out, M, N, K);
       break;
   }
 }
 
-// x goes to LDS when it is small (the decode shapes); otherwise operands are
-// read from global memory (L2-resident).
 template <int MT>
 void launch_gemv_mt(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
                     int M, int N, int K, hipStream_t st) {
-  if ((int64_t)M * K <= XLDS_MAX) launch_gemv_mtx<MT, true>(x, xs, w, out, odt, M, N, K, st);
-  else launch_gemv_mtx<MT, false>(x, xs, w, out, odt, M, N, K, st);
+  const dim3 grid((unsigned)((N + GEMV_ROWS - 1) / GEMV_ROWS));
+  const size_t lds = (size_t)GWAVES * (((size_t)M * GXPITCH + 1023) & ~(size_t)1023);
+  switch (odt) {
+    case SL8_DTYPE_F16:
+      gemv_q4k_kernel<SL8_DTYPE_F16, MT><<<grid, 64 * GWAVES, lds, st>>>(x, xs, w, out, M, N, K);
+      break;
+    case SL8_DTYPE_BF16:
+      gemv_q4k_kernel<SL8_DTYPE_BF16, MT><<<grid, 64 * GWAVES, lds, st>>>(x, xs, w, out, M, N, K);
+      break;
+    default:
+      gemv_q4k_kernel<SL8_DTYPE_F32, MT><<<grid, 64 * GWAVES, lds, st>>>(x, xs, w, out, M, N, K);
+      break;
+  }
 }
 
 }  // namespace
@@ -319,7 +487,9 @@ extern "C" int sl8_gemm_decode_q4k(const int8_t* x, const float* x_scale, const 
                 (long long)kMaxGemvK);
   SL8_CHECK_ARG(N < (1LL << 31), "gemm_decode_q4k: N too large");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (M <= 8) launch_gemv_mt<1>(x, x_scale, w, out, out_dtype, (int)M, (int)N, (int)K, st);
+  if (M == 1) launch_gemv_small<1>(x, x_scale, w, out, out_dtype, (int)M, (int)N, (int)K, st);
+  else if (M == 2) launch_gemv_small<2>(x, x_scale, w, out, out_dtype, (int)M, (int)N, (int)K, st);
+  else if (M <= 8) launch_gemv_mt<1>(x, x_scale, w, out, out_dtype, (int)M, (int)N, (int)K, st);
   else launch_gemv_mt<2>(x, x_scale, w, out, out_dtype, (int)M, (int)N, (int)K, st);
   SL8_CHECK_LAUNCH("gemm_decode_q4k");
   return SL8_OK;

@@ -32,7 +32,9 @@ def test_dequant_bit_exact(device, N, K):
 
 SHAPES = [(1, 4096, 3072), (1, 1024, 4096), (4, 4096, 4096), (8, 512, 768), (16, 4096, 3072),
           (1, 130, 256), (1, 4864, 1024), (1, 17408, 5120), (8, 17408, 5120), (5, 7, 256),
-          (11, 96, 512)]
+          (11, 96, 512),
+          # M <= 2 (VALU path), partial and multi-chunk K splits
+          (2, 4096, 3072), (2, 130, 256), (1, 64, 16384), (2, 50, 12544), (3, 40, 16384)]
 
 
 @pytest.mark.parametrize("odt", [torch.float16, torch.bfloat16, torch.float32])
