@@ -30,6 +30,8 @@
 // KV-head count is a multiple of 8, all query heads of one KV head go to the
 // same XCD so its K/V tiles stay in that XCD's L2.
 
+#include <climits>
+
 #include "attn_common.hpp"
 
 namespace sl8 {
@@ -87,6 +89,16 @@ template <> struct PvOp<SL8_DTYPE_F16> {
   __device__ static v16f mfma(vec a, vec b, v16f c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
+  // acc + sum of the 8 fp32 values the vector was packed from
+  __device__ static float sum(vec, const float* p, float acc) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc += p[e];
+    return acc;
+  }
+  __device__ static void scale(vec& v, float s) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (_Float16)((float)v[e] * s);
+  }
 };
 template <> struct PvOp<SL8_DTYPE_BF16> {
   typedef v8bf vec;
@@ -98,6 +110,16 @@ template <> struct PvOp<SL8_DTYPE_BF16> {
   }
   __device__ static v16f mfma(vec a, vec b, v16f c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  // acc + sum of the 8 fp32 values the vector was packed from
+  __device__ static float sum(vec, const float* p, float acc) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc += p[e];
+    return acc;
+  }
+  __device__ static void scale(vec& v, float s) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (__bf16)((float)v[e] * s);
   }
 };
 
@@ -407,6 +429,391 @@ attn_fwd_kernel(const FwdArgs a) {
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Wide variant (the production path): a wave owns 64 queries -- two 32-query
+// MFMA column blocks that share every K / V^T operand read from LDS, which
+// halves LDS traffic per query -- and the workgroup owns 256 queries (one
+// workgroup per CU, one wave per SIMD; the O accumulators live in the MFMA
+// accumulator registers). The key loop is software-pipelined so the matrix
+// cores always have independent work queued while the softmax runs:
+//   iteration j:  QK of tile j+1  ||  max / scaling of tile j
+//                 PV of tile j-1  ||  exp2 / pack / row sums of tile j
+// P of tile j stays in registers until iteration j+1. Lazy rescaling (see the
+// narrow kernel) happens before PV of tile j-1 is issued, so that pending P
+// block is scaled together with O.
+// ---------------------------------------------------------------------------
+
+#ifndef SL8_FWD_OCC
+#define SL8_FWD_OCC 2
+#endif
+// NG = 32-query MFMA column blocks per wave (1 or 2).
+template <int D, bool CAUSAL, int VDT, bool LSE, int NG>
+__global__ void __launch_bounds__(FWD_THREADS, NG == 1 ? SL8_FWD_OCC : 1)
+attn_fwd_wide_kernel(const FwdArgs a) {
+  constexpr int WQ = 32 * NG;                  // queries per wave
+  constexpr int WBM = FWD_WAVES * WQ;          // queries per workgroup
+  constexpr int DC = D / 32;
+  constexpr int KCH = BN * D / 16 / FWD_THREADS;
+  constexpr int VCH = D * BN * 2 / 16 / FWD_THREADS;
+  static_assert(KCH >= 1 && VCH >= 1, "tile copies cover D in {64,128}");
+  __shared__ __attribute__((aligned(16))) int8_t sm_k0[BN * D];
+  __shared__ __attribute__((aligned(16))) int8_t sm_k1[BN * D];
+  __shared__ __attribute__((aligned(16))) uint16_t sm_v0[D * BN];
+  __shared__ __attribute__((aligned(16))) uint16_t sm_v1[D * BN];
+  __shared__ __attribute__((aligned(16))) float sm_s0[BN];
+  __shared__ __attribute__((aligned(16))) float sm_s1[BN];
+  using PV = PvOp<VDT>;
+  typedef typename PV::vec pvec;
+
+  const int nslot = CAUSAL ? (a.nqb + 1) / 2 : a.nqb;
+  int bh, slot;
+  block_coords(a, nslot, bh, slot);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = lane >> 5, l32 = lane & 31;
+  const int gsz = a.Hq / a.Hkv;
+  const int b = bh / a.Hq, hq = bh % a.Hq;
+  const int64_t bkv = (int64_t)b * a.Hkv + hq / gsz;
+  const int M = a.M, N = a.N;
+  const int diag = CAUSAL ? N - M : 0;
+  const int wl = a.window_left;
+  const int8_t* kb = a.k + bkv * (int64_t)N * D;
+  const float* ksb = a.ks + bkv * (int64_t)N;
+  const uint16_t* vtb = a.vt + bkv * (int64_t)D * a.Npad;
+
+  int qbs[2];
+  int npass = 1;
+  qbs[0] = a.nqb - 1 - slot;
+  qbs[1] = slot;
+  if (CAUSAL) npass = (qbs[1] != qbs[0]) ? 2 : 1;
+
+  constexpr int KCPR = D / 16;
+  int koff[DC], voff[4];
+#pragma unroll
+  for (int ch = 0; ch < DC; ++ch) koff[ch] = ((2 * ch + h) ^ (l32 & (KCPR - 1))) * 16;
+#pragma unroll
+  for (int c4 = 0; c4 < 4; ++c4) voff[c4] = ((2 * c4 + h) ^ (l32 & 7)) * 8;
+  // V buffers start as zeros (finite): the pipeline's first half-steps
+  // multiply them by P = 0.
+  for (int i = tid; i < D * BN / 8; i += FWD_THREADS) {
+    reinterpret_cast<uint4*>(sm_v0)[i] = make_uint4(0, 0, 0, 0);
+    reinterpret_cast<uint4*>(sm_v1)[i] = make_uint4(0, 0, 0, 0);
+  }
+
+  for (int pass = 0; pass < npass; ++pass) {
+    const int m_blk = qbs[pass] * WBM;
+    const int q0 = m_blk + wave * WQ;
+    int mq[NG], qpos[NG];
+    bool m_ok[NG];
+    float qsc[NG];
+    QOp<DC> qop[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      mq[g] = q0 + 32 * g + l32;
+      m_ok[g] = mq[g] < M;
+      qpos[g] = mq[g] + diag;
+      const int8_t* qrow = a.q + ((int64_t)bh * M + (m_ok[g] ? mq[g] : M - 1)) * D + 16 * h;
+#pragma unroll
+      for (int c = 0; c < DC; ++c) {
+        qop[g].c[c] = *reinterpret_cast<const v4i*>(qrow + 32 * c);
+        if (!m_ok[g]) qop[g].c[c] = v4i{0, 0, 0, 0};
+      }
+      qsc[g] = m_ok[g] ? a.qs[(int64_t)bh * M + mq[g]] : 1.f;
+    }
+
+    int n_end = N;
+    if (CAUSAL) n_end = max(0, min(N, m_blk + WBM + diag));
+    int n_beg = 0;
+    if (wl >= 0) n_beg = min(n_end, max(0, m_blk + diag - wl + 1) & ~(BN - 1));
+    const int ntiles = (n_end - n_beg + BN - 1) / BN;
+    const int wq_lo = q0 + diag, wq_hi = q0 + WQ - 1 + diag;
+    auto live = [&](int t) __attribute__((always_inline)) {
+      if (t < 0 || t >= ntiles) return false;
+      const int n0 = n_beg + t * BN;
+      bool ok = true;
+      if (CAUSAL && n0 > wq_hi) ok = false;
+      if (wl >= 0 && n0 + BN - 1 <= wq_lo - wl) ok = false;
+      return ok;
+    };
+    // the tile holds keys the wave must not see (bounds, causal, window)
+    auto masked = [&](int t) __attribute__((always_inline)) {
+      const int n0 = n_beg + t * BN;
+      return (n0 + BN > N) || (CAUSAL && n0 + BN - 1 > wq_lo) || (wl >= 0 && n0 <= wq_hi - wl);
+    };
+
+    auto load_k = [&](int n0, int8_t* dst) __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < KCH; ++i) {
+        const int sl = i * FWD_THREADS + tid;
+        const int row = sl / KCPR;
+        const int c = (sl % KCPR) ^ (row & (KCPR - 1));
+        dma16_to_lds(kb + (int64_t)min(n0 + row, N - 1) * D + 16 * c,
+                     dst + (i * FWD_THREADS + wave * 64) * 16);
+      }
+    };
+    auto load_v = [&](int n0, uint16_t* dst) __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < VCH; ++i) {
+        const int sl = i * FWD_THREADS + tid;
+        const int row = sl / 8;
+        const int c = (sl % 8) ^ (row & 7);
+        dma16_to_lds(vtb + (int64_t)row * a.Npad + n0 + 8 * c,
+                     dst + (i * FWD_THREADS + wave * 64) * 8);
+      }
+    };
+    auto load_s = [&](int n0, float* dst) __attribute__((always_inline)) {
+      if (wave == 0) dma4_to_lds(ksb + min(n0 + lane, N - 1), dst);
+    };
+
+    v16f oacc[NG][DC];
+    float m_run[NG], l_lane[NG], mx_all[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) mx_all[g] = -INFINITY;
+    bool ovf = false;
+
+    // The key loop runs in half-steps of 32 keys (two per 64-key LDS tile).
+    // Half-step h issues, as independent work for the matrix cores and VALU:
+    //   QK of half h (MFMA)          scores of half h   (cvt, k_scale, mask, max)
+    //   PV of half h-2 (MFMA)        P of half h-1      (exp2, pack, row sums)
+    // then settles the reference point against the max of half h.
+    typedef float xblk[NG][16];  // scaled scores of one half: [query block][key slot]
+    typedef pvec pblk[NG][2];    // packed P of one half: [query block][16-key step]
+
+    auto half_qk = [&](const int8_t* kt, int s, v16i (&sc)[NG]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int g = 0; g < NG; ++g)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sc[g][r] = 0;
+#pragma unroll
+      for (int ch = 0; ch < DC; ++ch) {
+        const v4i kop = *reinterpret_cast<const v4i*>(kt + (32 * s + l32) * D + koff[ch]);
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+          sc[g] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kop, qop[g].c[ch], sc[g], 0, 0, 0);
+      }
+    };
+    auto half_pv = [&](const uint16_t* vt, int s, const pblk& p) __attribute__((always_inline)) {
+      const uint16_t* vrow = vt + l32 * BN;
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int tt = 0; tt < DC; ++tt) {
+          const pvec vop = *reinterpret_cast<const pvec*>(vrow + 32 * tt * BN + voff[2 * s + c]);
+#pragma unroll
+          for (int g = 0; g < NG; ++g) oacc[g][tt] = PV::mfma(vop, p[g][c], oacc[g][tt]);
+        }
+    };
+    // t = acc * k_scale (logit = t * q_scale, q_scale > 0), masked; tile max
+    auto half_scores = [&](const v16i (&sc)[NG], const float* st, int t, int s, bool do_mask,
+                           bool dead, xblk& xo, float (&tmax)[NG]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const float4 kv = *reinterpret_cast<const float4*>(st + 32 * s + 8 * gq + 4 * h);
+        const float kk[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) xo[g][4 * gq + e] = (float)sc[g][4 * gq + e] * kk[e];
+      }
+      // Interleave the half-step's MFMAs (QK of this half, PV of half h-2)
+      // with its LDS operand reads and VALU work (P of half h-1, the
+      // conversion above), instead of issuing them as separate clusters.
+      __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);  // LDS reads
+#pragma unroll
+      for (int i = 0; i < 12 * NG; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+      }
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        if (do_mask) {
+          const int nb = n_beg + t * BN + 32 * s;
+          // key n is visible iff n < N, n <= qpos (causal), n > qpos - wl
+          // (window), i.e. (n - lo) unsigned < (hi - lo) with [lo, hi) the
+          // visible range; one compare and one select per score
+          const int hi = dead ? nb : min(N, CAUSAL ? qpos[g] + 1 : N);
+          const int lo = (wl >= 0) ? qpos[g] - wl + 1 : INT_MIN / 2;
+          const int lo_c = max(lo, nb - 64);
+          const uint32_t span = hi > lo_c ? (uint32_t)(hi - lo_c) : 0u;
+          const uint32_t rel = (uint32_t)(nb + 4 * h - lo_c);
+          __builtin_amdgcn_sched_barrier(0);  // keep the mask compact (register pressure)
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            xo[g][e] = (rel + (uint32_t)(8 * (e >> 2) + (e & 3)) < span) ? xo[g][e] : -INFINITY;
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, xo[g][e]);
+        tmax[g] = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      }
+    };
+    // P = 2^(t*q_scale - m), packed per 16-key step, plus the row sums
+    auto half_probs = [&](const xblk& xi, pblk& pc) __attribute__((always_inline)) {
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        const float msub = (m_run[g] == -INFINITY) ? 0.f : m_run[g];
+        float ls = l_lane[g];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          float pe[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) pe[e] = __builtin_amdgcn_exp2f(fmaf(xi[g][8 * c + e], qsc[g], -msub));
+          pc[g][c] = PV::pack(pe);
+          ls = PV::sum(pc[g][c], pe, ls);
+        }
+        l_lane[g] = ls;
+      }
+    };
+    // Reference point (exp2 domain) per query: fixed by the first tile that
+    // has a visible key (O and l are still zero then, so nothing needs
+    // rescaling) and never moved afterwards, so O is only ever touched by the
+    // MFMAs inside the loop. P = 2^(logit - m_ref) must stay <= 2^15 (fp16
+    // range); a later logit more than 15 above m_ref sets ovf, and the pass is
+    // then run again with m_ref = the row max seen in the first run.
+    auto settle = [&](const float (&tmax)[NG]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        const float mt = tmax[g] * qsc[g];
+        mx_all[g] = fmaxf(mx_all[g], mt);
+        if (m_run[g] == -INFINITY) m_run[g] = mt;
+        else ovf = ovf || (mt > m_run[g] + 15.f);
+      }
+    };
+
+    xblk xA, xB;  // scores of the last two halves (alternating)
+    pblk pA, pB;  // P of the last two halves (alternating)
+    // One half-step, a single straight-line block per variant: xi/p1 = the
+    // half before (scores in, P out), xo = this half (scores out), p2 = P of
+    // the half two back (consumed by PV). dead = this half has no tile (all
+    // its scores -inf).
+    auto half_step = [&](int j, int s, const int8_t* kt, const float* st, const uint16_t* vt,
+                         bool mask, bool dead, xblk& xi, pblk& p1, xblk& xo,
+                         pblk& p2) __attribute__((always_inline)) {
+      v16i sc[NG];
+      float tmax[NG];
+      half_qk(kt, s, sc);
+      half_pv(vt, s, p2);
+      half_probs(xi, p1);
+      half_scores(sc, st, j, s, mask, dead, xo, tmax);
+      settle(tmax);
+    };
+    auto body = [&](int j, const int8_t* kcur, int8_t* knext, uint16_t* vcopy, const uint16_t* vprev,
+                    const float* scur, float* snext) __attribute__((always_inline)) {
+      const int n0 = n_beg + j * BN;
+      if (j + 1 < ntiles) {
+        load_k(n0 + BN, knext);
+        load_s(n0 + BN, snext);
+      }
+      if (j < ntiles) load_v(n0, vcopy);
+      const bool dead = !live(j);
+      const bool mask = dead || masked(j);
+      half_step(j, 0, kcur, scur, vprev, mask, dead, xB, pB, xA, pA);
+      half_step(j, 1, kcur, scur, vprev, mask, dead, xA, pA, xB, pB);
+      wait_dma();
+      __syncthreads();
+    };
+    for (int attempt = 0; attempt < 2; ++attempt) {
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+#pragma unroll
+        for (int t = 0; t < DC; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[g][t][r] = 0.f;
+        // second run: the row max of the first one, which no logit exceeds
+        m_run[g] = attempt ? mx_all[g] : -INFINITY;
+        l_lane[g] = 0.f;
+      }
+      ovf = false;
+      // Iteration j reads K_j, k_scale_j (halves 2j, 2j+1) and V_{j-1} (PV of
+      // halves 2j-2, 2j-1), and copies K_{j+1}, k_scale_{j+1} and V_j into the
+      // other buffers.
+      if (ntiles > 0) {
+        load_k(n_beg, sm_k0);
+        load_s(n_beg, sm_s0);
+      }
+      wait_dma();
+      __syncthreads();
+
+      // Pipeline state before the first half: scores -inf (P = 0) and P = 0, so
+      // the first two half-steps add nothing; the V buffers are zeroed once so
+      // those products are 0 * finite.
+  #pragma unroll
+      for (int g = 0; g < NG; ++g) {
+  #pragma unroll
+        for (int e = 0; e < 16; ++e) xA[g][e] = xB[g][e] = -INFINITY;
+  #pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+          pA[g][c] = PV::pack(z);
+          pB[g][c] = pA[g][c];
+        }
+      }
+      // both bodies unconditional inside the loop (keeps every accumulator
+      // update in place); an odd last iteration is peeled
+      int j = 0;
+      for (; j + 1 <= ntiles; j += 2) {
+        body(j, sm_k0, sm_k1, sm_v0, sm_v1, sm_s0, sm_s1);
+        body(j + 1, sm_k1, sm_k0, sm_v1, sm_v0, sm_s1, sm_s0);
+      }
+      if (j <= ntiles) body(j, sm_k0, sm_k1, sm_v0, sm_v1, sm_s0, sm_s1);
+
+      if (!__syncthreads_or(ovf ? 1 : 0)) break;
+    }
+
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      const float l = l_lane[g] + __shfl_xor(l_lane[g], 32, 64);
+      if (m_ok[g]) {
+        const float inv = (l > 0.f) ? 1.f / l : 0.f;
+        uint16_t* orow = reinterpret_cast<uint16_t*>(a.out) + ((int64_t)bh * M + mq[g]) * D;
+#pragma unroll
+        for (int tt = 0; tt < DC; ++tt)
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq) {
+            uint16_t hv[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float xo = oacc[g][tt][4 * gq + e] * inv;
+              hv[e] = (VDT == SL8_DTYPE_F16) ? f2h_bits(xo) : f2bf_bits(xo);
+            }
+            uint2 pk;
+            pk.x = hv[0] | ((uint32_t)hv[1] << 16);
+            pk.y = hv[2] | ((uint32_t)hv[3] << 16);
+            *reinterpret_cast<uint2*>(orow + 32 * tt + 8 * gq + 4 * h) = pk;
+          }
+        if (LSE && h == 0)
+          a.lse[(int64_t)bh * M + mq[g]] = (l > 0.f) ? (m_run[g] * LN2F + logf(l)) : -INFINITY;
+      }
+    }
+  }
+}
+
+// query-column blocks per wave of the production kernel
+#ifndef SL8_FWD_NG
+#define SL8_FWD_NG 1
+#endif
+constexpr int WIDE_NG = SL8_FWD_NG;
+constexpr int WIDE_BM = FWD_WAVES * 32 * WIDE_NG;  // queries per workgroup
+
+template <int D, bool CAUSAL, int VDT, bool LSE>
+void launch_wide(const FwdArgs& a, int grid, hipStream_t st) {
+  attn_fwd_wide_kernel<D, CAUSAL, VDT, LSE, WIDE_NG><<<grid, FWD_THREADS, 0, st>>>(a);
+}
+
+template <int D, int VDT>
+void dispatch_wide(const FwdArgs& a, int grid, bool causal, bool lse, hipStream_t st) {
+  if (causal) {
+    if (lse) launch_wide<D, true, VDT, true>(a, grid, st);
+    else launch_wide<D, true, VDT, false>(a, grid, st);
+  } else {
+    if (lse) launch_wide<D, false, VDT, true>(a, grid, st);
+    else launch_wide<D, false, VDT, false>(a, grid, st);
+  }
+}
+
 template <int D, bool CAUSAL, int VDT, bool DUMP, bool LSE>
 void launch_fwd(const FwdArgs& a, int grid, hipStream_t st) {
   attn_fwd_kernel<D, CAUSAL, VDT, DUMP, LSE><<<grid, FWD_THREADS, 0, st>>>(a);
@@ -498,13 +905,14 @@ extern "C" int sl8_attn_int8_fwd(const int8_t* q, const float* q_scale, const in
   a.vt = static_cast<const uint16_t*>(workspace);
   a.out = out; a.lse = lse; a.window_left = (int)window_left;
   const bool c = causal != 0, want_lse = lse != nullptr;
-  if (c) grid = (int)(B * Hq * ((a.nqb + 1) / 2));
+  a.nqb = (int)((M + WIDE_BM - 1) / WIDE_BM);
+  grid = (int)(B * Hq * (c ? (a.nqb + 1) / 2 : a.nqb));
   if (D == 64) {
-    if (v_dtype == SL8_DTYPE_F16) dispatch_causal_lse<64, SL8_DTYPE_F16, false>(a, grid, c, want_lse, st);
-    else dispatch_causal_lse<64, SL8_DTYPE_BF16, false>(a, grid, c, want_lse, st);
+    if (v_dtype == SL8_DTYPE_F16) dispatch_wide<64, SL8_DTYPE_F16>(a, grid, c, want_lse, st);
+    else dispatch_wide<64, SL8_DTYPE_BF16>(a, grid, c, want_lse, st);
   } else {
-    if (v_dtype == SL8_DTYPE_F16) dispatch_causal_lse<128, SL8_DTYPE_F16, false>(a, grid, c, want_lse, st);
-    else dispatch_causal_lse<128, SL8_DTYPE_BF16, false>(a, grid, c, want_lse, st);
+    if (v_dtype == SL8_DTYPE_F16) dispatch_wide<128, SL8_DTYPE_F16>(a, grid, c, want_lse, st);
+    else dispatch_wide<128, SL8_DTYPE_BF16>(a, grid, c, want_lse, st);
   }
   SL8_CHECK_LAUNCH("attn_int8_fwd");
   return SL8_OK;

@@ -179,3 +179,25 @@ def test_config2_shape_against_oracle(device):
                                   _np(v[:, kvh:kvh + 1].float()), True)
         assert_int8_quality(out[:, h:h + 1], ref, min_cos=0.9999, max_rel_l1=3e-3, min_sqnr_db=40,
                             what=f"config2 head {h}")
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_reference_point_restart(device, causal):
+    """Logits of later key tiles exceed the first tile's maximum by far more than
+    the kernel's fixed-reference headroom (2^15), which forces the second run of
+    the pass with the row maximum; results must still match the oracle."""
+    B, Hq, Hkv, M, N, D = 1, 2, 2, 192, 320, 128
+    g = torch.Generator(device="cpu").manual_seed(7)
+    q_i8 = torch.randint(-127, 128, (B, Hq, M, D), generator=g, dtype=torch.int8)
+    k_i8 = torch.randint(-127, 128, (B, Hkv, N, D), generator=g, dtype=torch.int8)
+    qs = torch.full((B, Hq, M), 1.0 / (127.0 * 127.0 * np.sqrt(D) / 3.0), dtype=torch.float32)
+    ks = torch.full((B, Hkv, N), 12.0, dtype=torch.float32)
+    ks[..., :64] = 1e-3  # the first tile is nearly flat
+    v = torch.randn(B, Hkv, N, D, generator=g).to(torch.float16)
+    out, lse = _C.attn_int8_fwd_train(q_i8.to(device), qs.to(device), k_i8.to(device),
+                                      ks.to(device), v.to(device), causal)
+    ref, ref_lse = oa.attn_int8_fwd(_np(q_i8), _np(qs), _np(k_i8), _np(ks), _v_f32(v), causal, -1)
+    assert_finite(out)
+    assert_close_abs(out, ref, atol=1e-2, what="restart path vs oracle")
+    finite = np.isfinite(ref_lse)
+    np.testing.assert_allclose(_np(lse)[finite], ref_lse[finite], rtol=1e-5, atol=1e-5)
