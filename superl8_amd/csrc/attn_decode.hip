@@ -297,7 +297,11 @@ struct WaveCfg {
   static constexpr int T = KL * SUB;                  // keys per tile
   static constexpr int CPL = D / KL;                  // PV channels per lane
   static constexpr int KC = D / 16;                   // 16-byte chunks per K row
-  static constexpr int KSW = (KC < 8 ? KC : 8) - 1;
+  // K rows (D bytes) are read 16 rows per 16 lanes; LDS has 64 four-byte
+  // banks (256 B), so chunks are XOR-swizzled with the row index above the
+  // rows that share one 256-byte bank line.
+  static constexpr int KSW = KC - 1;
+  static constexpr int KSH = D == 64 ? 2 : (D == 128 ? 1 : 0);
   static constexpr int KBYTES = T * D, VBYTES = 2 * T * D;
   static constexpr int KDMA = KBYTES / 1024, VDMA = VBYTES / 1024;  // 1 KiB copies per wave
   static constexpr int STAGE = KBYTES + VBYTES + 256;               // + k_scale (64 floats)
@@ -314,6 +318,7 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
                    int n_splits, int h_q, int h_kv, int bhq) {
   using C = WaveCfg<D, GS>;
   constexpr int KL = C::KL, SUB = C::SUB, T = C::T, CPL = C::CPL, KC = C::KC, KSW = C::KSW;
+  constexpr int KSH = C::KSH;
   constexpr int STAGE = C::STAGE;
   static_assert(NB >= 2 && NB <= 4, "ring depth");
   // One LDS object per ring stage: the compiler then knows a copy into one
@@ -359,7 +364,7 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
 #pragma unroll
     for (int j = 0; j < C::KDMA; ++j) {
       const int id = j * 64 + lane, row = id / KC;
-      const int c = (id % KC) ^ (row & KSW);
+      const int c = (id % KC) ^ ((row >> KSH) & KSW);
       __builtin_amdgcn_global_load_lds((gptr_t)(kb + (int64_t)min(base + row, n_len - 1) * D + 16 * c),
                                        (lptr_t)(sb + j * 1024), 16, 0, 0);
     }
@@ -390,7 +395,7 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
       int acc = 0;
 #pragma unroll
       for (int c = 0; c < KC; ++c) {
-        const int4 kr = *reinterpret_cast<const int4*>(sb + r * D + 16 * (c ^ (r & KSW)));
+        const int4 kr = *reinterpret_cast<const int4*>(sb + r * D + 16 * (c ^ ((r >> KSH) & KSW)));
         acc = __builtin_amdgcn_sdot4(qv[4 * c + 0], kr.x, acc, false);
         acc = __builtin_amdgcn_sdot4(qv[4 * c + 1], kr.y, acc, false);
         acc = __builtin_amdgcn_sdot4(qv[4 * c + 2], kr.z, acc, false);

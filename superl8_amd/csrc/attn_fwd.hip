@@ -489,11 +489,16 @@ attn_fwd_wide_kernel(const FwdArgs a) {
   if (CAUSAL) npass = (qbs[1] != qbs[0]) ? 2 : 1;
 
   constexpr int KCPR = D / 16;
+  // LDS has 64 four-byte banks (256 B): 16 lanes of a 16-byte read cover 16
+  // consecutive tile rows, so a row's chunks are XOR-swizzled with the row's
+  // index above the rows that share one 256-byte bank line (K rows: D bytes,
+  // V^T rows: 128 bytes).
+  constexpr int KSH = D == 128 ? 1 : 2;
   int koff[DC], voff[4];
 #pragma unroll
-  for (int ch = 0; ch < DC; ++ch) koff[ch] = ((2 * ch + h) ^ (l32 & (KCPR - 1))) * 16;
+  for (int ch = 0; ch < DC; ++ch) koff[ch] = ((2 * ch + h) ^ ((l32 >> KSH) & (KCPR - 1))) * 16;
 #pragma unroll
-  for (int c4 = 0; c4 < 4; ++c4) voff[c4] = ((2 * c4 + h) ^ (l32 & 7)) * 8;
+  for (int c4 = 0; c4 < 4; ++c4) voff[c4] = ((2 * c4 + h) ^ ((l32 >> 1) & 7)) * 8;
   // V buffers start as zeros (finite): the pipeline's first half-steps
   // multiply them by P = 0.
   for (int i = tid; i < D * BN / 8; i += FWD_THREADS) {
@@ -547,7 +552,7 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       for (int i = 0; i < KCH; ++i) {
         const int sl = i * FWD_THREADS + tid;
         const int row = sl / KCPR;
-        const int c = (sl % KCPR) ^ (row & (KCPR - 1));
+        const int c = (sl % KCPR) ^ ((row >> KSH) & (KCPR - 1));
         dma16_to_lds(kb + (int64_t)min(n0 + row, N - 1) * D + 16 * c,
                      dst + (i * FWD_THREADS + wave * 64) * 16);
       }
@@ -557,7 +562,7 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       for (int i = 0; i < VCH; ++i) {
         const int sl = i * FWD_THREADS + tid;
         const int row = sl / 8;
-        const int c = (sl % 8) ^ (row & 7);
+        const int c = (sl % 8) ^ ((row >> 1) & 7);
         dma16_to_lds(vtb + (int64_t)row * a.Npad + n0 + 8 * c,
                      dst + (i * FWD_THREADS + wave * 64) * 8);
       }

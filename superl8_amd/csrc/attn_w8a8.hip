@@ -83,7 +83,11 @@ __global__ void __launch_bounds__(WT, (D <= 128 ? 2 : 1))
 attn_w8a8_kernel(const W8Args a) {
   constexpr int DC = D / 32;
   constexpr int KCPR = D / 16;                 // 16-B chunks per K row
-  constexpr int KSW = (KCPR < 8 ? KCPR : 8) - 1;
+  // LDS has 64 four-byte banks: 16 lanes of a 16-byte read touch 16
+  // consecutive tile rows, so chunks are XOR-swizzled with the row index above
+  // the rows sharing one 256-byte bank line (K rows: D bytes; V^T rows: 64).
+  constexpr int KSW = KCPR - 1;
+  constexpr int KSH = D == 64 ? 2 : (D == 128 ? 1 : 0);
   constexpr int KCH = WBN * D / 16 / WT;       // K chunks per thread
   constexpr int VCH = D * WBN / 16 / WT;       // V^T chunks per thread
   static_assert(KCH >= 1 && VCH >= 1, "tile copy covers D >= 64");
@@ -112,9 +116,9 @@ attn_w8a8_kernel(const W8Args a) {
 
   int koff[DC], voff[2];
 #pragma unroll
-  for (int ch = 0; ch < DC; ++ch) koff[ch] = ((2 * ch + h) ^ (l32 & KSW)) * 16;
+  for (int ch = 0; ch < DC; ++ch) koff[ch] = ((2 * ch + h) ^ ((l32 >> KSH) & KSW)) * 16;
 #pragma unroll
-  for (int st = 0; st < 2; ++st) voff[st] = ((2 * st + h) ^ (l32 & 3)) * 16;
+  for (int st = 0; st < 2; ++st) voff[st] = ((2 * st + h) ^ ((l32 >> 2) & 3)) * 16;
 
   int qbs[2] = {a.nqb - 1 - slot, slot};
   const int npass = (CAUSAL && qbs[1] != qbs[0]) ? 2 : 1;
@@ -145,14 +149,14 @@ attn_w8a8_kernel(const W8Args a) {
       for (int i = 0; i < KCH; ++i) {
         const int s = i * WT + tid;
         const int row = s / KCPR;
-        const int c = (s % KCPR) ^ (row & KSW);
+        const int c = (s % KCPR) ^ ((row >> KSH) & KSW);
         dma16_to_lds(kb + (int64_t)min(n0 + row, N - 1) * D + 16 * c, kd + (i * WT + wave * 64) * 16);
       }
 #pragma unroll
       for (int i = 0; i < VCH; ++i) {
         const int s = i * WT + tid;
         const int row = s / 4;
-        const int c = (s % 4) ^ (row & 3);
+        const int c = (s % 4) ^ ((row >> 2) & 3);
         dma16_to_lds(vtb + (int64_t)row * a.Npad + n0 + 16 * c, vd + (i * WT + wave * 64) * 16);
       }
       if (wave == 0) dma4_to_lds(ksb + min(n0 + lane, N - 1), sd);
