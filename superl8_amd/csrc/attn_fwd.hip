@@ -611,7 +611,7 @@ attn_fwd_wide_kernel(const FwdArgs a) {
     };
     // t = acc * k_scale (logit = t * q_scale, q_scale > 0), masked; tile max
     auto half_scores = [&](const v16i (&sc)[NG], const float* st, int t, int s, bool do_mask,
-                           bool dead, xblk& xo, float (&tmax)[NG]) __attribute__((always_inline)) {
+                           bool dead, xblk& xo) __attribute__((always_inline)) {
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq) {
         const float4 kv = *reinterpret_cast<const float4*>(st + 32 * s + 8 * gq + 4 * h);
@@ -649,6 +649,11 @@ attn_fwd_wide_kernel(const FwdArgs a) {
             xo[g][e] = (rel + (uint32_t)(8 * (e >> 2) + (e & 3)) < span) ? xo[g][e] : -INFINITY;
           __builtin_amdgcn_sched_barrier(0);
         }
+      }
+    };
+    auto half_max = [&](const xblk& xo, float (&tmax)[NG]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
         float mx = -INFINITY;
 #pragma unroll
         for (int e = 0; e < 16; ++e) mx = fmaxf(mx, xo[g][e]);
@@ -660,31 +665,37 @@ attn_fwd_wide_kernel(const FwdArgs a) {
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
         const float msub = (m_run[g] == -INFINITY) ? 0.f : m_run[g];
-        float ls = l_lane[g];
+        float hs = 0.f;
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
           float pe[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) pe[e] = __builtin_amdgcn_exp2f(fmaf(xi[g][8 * c + e], qsc[g], -msub));
           pc[g][c] = PV::pack(pe);
-          ls = PV::sum(pc[g][c], pe, ls);
+          hs = PV::sum(pc[g][c], pe, hs);
         }
-        l_lane[g] = ls;
+        l_lane[g] += hs;
+        // some P above 2^15 (outside fp16) => the half's sum is too
+        ovf = ovf || (hs > 32768.f);
       }
     };
-    // Reference point (exp2 domain) per query: fixed by the first tile that
+    // Reference point (exp2 domain) per query: fixed by the first half that
     // has a visible key (O and l are still zero then, so nothing needs
     // rescaling) and never moved afterwards, so O is only ever touched by the
-    // MFMAs inside the loop. P = 2^(logit - m_ref) must stay <= 2^15 (fp16
-    // range); a later logit more than 15 above m_ref sets ovf, and the pass is
-    // then run again with m_ref = the row max seen in the first run.
-    auto settle = [&](const float (&tmax)[NG]) __attribute__((always_inline)) {
+    // MFMAs inside the loop and no per-tile max is needed. P = 2^(logit -
+    // m_ref) must stay within fp16; a half whose P sum exceeds 2^15 (implied
+    // by any P > 2^15) sets ovf, and the pass is run again with m_ref = the
+    // row max (found by a QK-only sweep).
+    auto settle = [&](const xblk& xo) __attribute__((always_inline)) {
+      bool unset = false;
 #pragma unroll
-      for (int g = 0; g < NG; ++g) {
-        const float mt = tmax[g] * qsc[g];
-        mx_all[g] = fmaxf(mx_all[g], mt);
-        if (m_run[g] == -INFINITY) m_run[g] = mt;
-        else ovf = ovf || (mt > m_run[g] + 15.f);
+      for (int g = 0; g < NG; ++g) unset = unset || (m_run[g] == -INFINITY);
+      if (__any(unset)) {
+        float tmax[NG];
+        half_max(xo, tmax);
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+          if (m_run[g] == -INFINITY) m_run[g] = tmax[g] * qsc[g];
       }
     };
 
@@ -698,12 +709,11 @@ attn_fwd_wide_kernel(const FwdArgs a) {
                          bool mask, bool dead, xblk& xi, pblk& p1, xblk& xo,
                          pblk& p2) __attribute__((always_inline)) {
       v16i sc[NG];
-      float tmax[NG];
       half_qk(kt, s, sc);
       half_pv(vt, s, p2);
       half_probs(xi, p1);
-      half_scores(sc, st, j, s, mask, dead, xo, tmax);
-      settle(tmax);
+      half_scores(sc, st, j, s, mask, dead, xo);
+      settle(xo);
     };
     auto body = [&](int j, const int8_t* kcur, int8_t* knext, uint16_t* vcopy, const uint16_t* vprev,
                     const float* scur, float* snext) __attribute__((always_inline)) {
@@ -766,6 +776,26 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       if (j <= ntiles) body(j, sm_k0, sm_k1, sm_v0, sm_v1, sm_s0, sm_s1);
 
       if (!__syncthreads_or(ovf ? 1 : 0)) break;
+      // QK-only sweep for the exact row max (the whole workgroup takes part)
+      for (int t = 0; t < ntiles; ++t) {
+        load_k(n_beg + t * BN, sm_k0);
+        load_s(n_beg + t * BN, sm_s0);
+        wait_dma();
+        __syncthreads();
+        if (live(t)) {
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2) {
+            v16i sc[NG];
+            float tmax[NG];
+            half_qk(sm_k0, s2, sc);
+            half_scores(sc, sm_s0, t, s2, true, false, xA);
+            half_max(xA, tmax);
+#pragma unroll
+            for (int g = 0; g < NG; ++g) mx_all[g] = fmaxf(mx_all[g], tmax[g] * qsc[g]);
+          }
+        }
+        __syncthreads();
+      }
     }
 
 #pragma unroll
