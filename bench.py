@@ -12,8 +12,13 @@ the reference harness's attention_flops(causal) = 2*B*H*S*S*D
 
 Also reported (under "secondary"): split-KV decode at config 3 and the Q4_K
 GEMV at config 4 (M=1 and M=8), as HBM GB/s over their algorithmic bytes,
-and (under "cpu_baseline") the numpy restatement of config 1 timed on the
-host cores. One JSON line is printed on stdout.
+the full-W8A8 prefill at config 5 (TOPS), and (under "cpu_baseline") the
+numpy restatement of config 1 timed on the host cores. One JSON line is
+printed on stdout.
+
+Before the warmup steps the GPU runs ~0.3 s of untimed prefill calls: the
+MI355X clocks ramp up over the first milliseconds of load, and the figures
+are steady-state ones.
 """
 from __future__ import annotations
 
@@ -48,6 +53,16 @@ def _events_time(fn, iters, stream):
     return e0.elapsed_time(e1) / iters
 
 
+def spin_up(fn, seconds=0.3):
+    """Untimed calls until `seconds` of GPU work have run (clock ramp-up)."""
+    torch.cuda.synchronize()
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        for _ in range(8):
+            fn()
+        torch.cuda.synchronize()
+
+
 def bench_prefill(steps, warmup):
     from superl8_amd import _C, quant
 
@@ -62,6 +77,7 @@ def bench_prefill(steps, warmup):
     def step():
         return _C.attn_int8_fwd(q_i8, qs, k_i8, ks, v, True)
 
+    spin_up(step)
     for _ in range(warmup):
         step()
     stream = torch.cuda.current_stream()
@@ -90,13 +106,37 @@ def bench_decode(iters=20):
     ks = ks.reshape(B, Hkv, N)
     v = torch.randn(B, Hkv, N, D, device=dev, dtype=torch.float16, generator=g)
     fn = lambda: _C.attn_int8_decode(q_i8, qs, k_i8, ks, v, 16)  # noqa: E731
-    for _ in range(3):
-        fn()
-    torch.cuda.synchronize()
+    spin_up(fn, 0.2)
     ms = _events_time(fn, iters, torch.cuda.current_stream())
     nbytes = k_i8.numel() + ks.numel() * 4 + v.numel() * 2 + q_i8.numel() + qs.numel() * 4 \
         + B * Hq * D * 2
     return ms, nbytes
+
+
+def bench_w8a8(iters=5):
+    """Full-W8A8 prefill at BASELINE config 5: Q/K/V [2, 16|2, 8192, 256], causal,
+    1% of Q/K channels (3 of 256, fixed) scaled by 20, V per-channel int8."""
+    from superl8_amd import _C, quant
+
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(6)
+    B, Hq, Hkv, S, D = 2, 16, 2, 8192, 256
+    q = torch.randn(B, Hq, S, D, device=dev, dtype=torch.float16, generator=g)
+    k = torch.randn(B, Hkv, S, D, device=dev, dtype=torch.float16, generator=g)
+    v = torch.randn(B, Hkv, S, D, device=dev, dtype=torch.float16, generator=g)
+    ch = torch.tensor([17, 101, 203], device=dev)
+    q[..., ch] *= 20
+    k[..., ch] *= 20
+    q_i8, qs, k_i8, ks, _ = quant.quantize_qk(q, k)
+    qs, ks = qs.squeeze(-1).contiguous(), ks.squeeze(-1).contiguous()
+    v_i8, vs = _C.quantize_v_perchannel(v)
+    vs = vs.reshape(B, Hkv, D).contiguous()
+    del q, k, v
+    fn = lambda: _C.attn_w8a8_fwd(q_i8, qs, k_i8, ks, v_i8, vs, True)  # noqa: E731
+    spin_up(fn, 0.2)
+    ms = _events_time(fn, iters, torch.cuda.current_stream())
+    ops = 4 * B * Hq * S * S * D // 2
+    return ms, ops
 
 
 def bench_gemv(M, iters_graph=10, copies=8):
@@ -241,6 +281,10 @@ def main():
             sec[f"gemm_decode_q4k_cfg4_m{M}"] = {"us": round(gms * 1e3, 2), "GB/s": round(gbs, 1),
                                                  "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
                                                  "bytes": gbytes}
+        wms, wops = bench_w8a8()
+        wt = wops / (wms * 1e-3) / 1e12
+        sec["attn_w8a8_fwd_cfg5"] = {"us": round(wms * 1e3, 1), "TOPS": round(wt, 1),
+                                     "frac_int8_peak": round(wt / PEAK_INT8_TOPS, 4), "ops": wops}
         sec["hbm_copy_256MiB_GBps"] = round(bench_copy(), 1)
         out["secondary"] = sec
     if not args.no_cpu:

@@ -24,15 +24,25 @@ __device__ __forceinline__ void dma4_to_lds(const void* g, void* lds_wave_base) 
 __device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
 
 // blockIdx.x -> (b*Hq + h, slot). Slots are issued in increasing order, so
-// callers put their heaviest work in slot 0. With xcd_map (B*Hkv a multiple
-// of 8) workgroup ids are dealt so that XCD x (= id % 8) only serves KV heads
-// x, x+8, ...: the query heads sharing a KV head then share that XCD's L2.
-__device__ __forceinline__ void attn_block_coords(int Hq, int Hkv, int nslot, bool xcd_map,
+// callers put their heaviest work in slot 0. With xcd_map, workgroup ids are
+// dealt so that each KV head's query heads stay on one XCD (id % 8 is the
+// XCD) and share its L2:
+//   B*Hkv a multiple of 8: XCD x serves KV heads x, x+8, ...;
+//   B*Hkv dividing 8 (rep = 8 / (B*Hkv) XCDs per KV head): XCD x serves KV
+//   head x % (B*Hkv), taking every rep-th (slot, head) unit of it.
+// xcd_mode(): 1 / 2 for those cases, 0 = plain order (host-side choice).
+inline int xcd_mode(long long nbkv, long long gsz, long long nslot) {
+  if (nbkv % 8 == 0) return 1;
+  if (8 % nbkv == 0 && (gsz * nslot) % (8 / nbkv) == 0) return 2;
+  return 0;
+}
+
+__device__ __forceinline__ void attn_block_coords(int Hq, int Hkv, int nslot, int xcd_map,
                                                   int& bh, int& slot) {
   const int id = blockIdx.x;
   const int total = gridDim.x;
   const int gsz = Hq / Hkv;
-  if (xcd_map) {
+  if (xcd_map == 1) {
     const int nbkv = total / (nslot * gsz);  // B * Hkv
     const int xcd = id & 7, k = id >> 3;
     const int per_slot = (nbkv / 8) * gsz;
@@ -43,6 +53,15 @@ __device__ __forceinline__ void attn_block_coords(int Hq, int Hkv, int nslot, bo
     const int b = bkv / Hkv, kvh = bkv % Hkv;
     bh = b * Hq + kvh * gsz + j;
     slot = r;
+  } else if (xcd_map == 2) {
+    const int nbkv = total / (nslot * gsz);  // divides 8
+    const int rep = 8 / nbkv;
+    const int xcd = id & 7, k = id >> 3;
+    const int bkv = xcd % nbkv, sub = xcd / nbkv;
+    const int u = k * rep + sub;             // (slot, head) unit of this KV head
+    const int b = bkv / Hkv, kvh = bkv % Hkv;
+    bh = b * Hq + kvh * gsz + u % gsz;
+    slot = u / gsz;
   } else {
     const int nbh = total / nslot;
     slot = id / nbh;

@@ -375,7 +375,8 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
           (gptr_t)(vb + (int64_t)min(base + row, n_len - 1) * D + 8 * (id % (D / 8))),
           (lptr_t)(sb + C::KBYTES + j * 1024), 16, 0, 0);
     }
-    __builtin_amdgcn_global_load_lds((gptr_t)(ksb + min(base + lane, n_len - 1)),
+    // lanes past the tile repeat its keys (same cache lines: no extra traffic)
+    __builtin_amdgcn_global_load_lds((gptr_t)(ksb + min(base + (lane % T), n_len - 1)),
                                      (lptr_t)(sb + C::KBYTES + C::VBYTES), 4, 0, 0);
   };
 

@@ -133,7 +133,7 @@ struct FwdArgs {
   float* lse;
   int32_t* scores;     // DUMP mode
   int M, N, Npad, Hq, Hkv, nqb, window_left;
-  int xcd_map;         // 1: XCD-aware block order
+  int xcd_map;         // xcd_mode(): XCD-aware block order
 };
 
 // LDS tiles are dense; 16-byte chunks are XOR-swizzled within each row
@@ -142,7 +142,7 @@ struct FwdArgs {
 
 // blockIdx.x -> (b*Hq + h, query-block slot), heaviest slot first.
 __device__ __forceinline__ void block_coords(const FwdArgs& a, int nslot, int& bh, int& slot) {
-  attn_block_coords(a.Hq, a.Hkv, nslot, a.xcd_map != 0, bh, slot);
+  attn_block_coords(a.Hq, a.Hkv, nslot, a.xcd_map, bh, slot);
 }
 
 template <int DC>
@@ -897,7 +897,7 @@ FwdArgs make_args(int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N, int&
   a.nqb = (int)((M + BM - 1) / BM);
   a.window_left = -1;
   grid = (int)(B * Hq * a.nqb);  // causal kernels halve this (paired query blocks)
-  a.xcd_map = ((B * Hkv) % 8 == 0) ? 1 : 0;
+  a.xcd_map = xcd_mode(B * Hkv, Hq / Hkv, a.nqb);  // non-causal slot count
   return a;
 }
 
@@ -941,7 +941,9 @@ extern "C" int sl8_attn_int8_fwd(const int8_t* q, const float* q_scale, const in
   a.out = out; a.lse = lse; a.window_left = (int)window_left;
   const bool c = causal != 0, want_lse = lse != nullptr;
   a.nqb = (int)((M + WIDE_BM - 1) / WIDE_BM);
-  grid = (int)(B * Hq * (c ? (a.nqb + 1) / 2 : a.nqb));
+  const int nslot = c ? (a.nqb + 1) / 2 : a.nqb;
+  grid = (int)(B * Hq * nslot);
+  a.xcd_map = xcd_mode(B * Hkv, Hq / Hkv, nslot);
   if (D == 64) {
     if (v_dtype == SL8_DTYPE_F16) dispatch_wide<64, SL8_DTYPE_F16>(a, grid, c, want_lse, st);
     else dispatch_wide<64, SL8_DTYPE_BF16>(a, grid, c, want_lse, st);

@@ -100,7 +100,7 @@ attn_w8a8_kernel(const W8Args a) {
 
   const int nslot = CAUSAL ? (a.nqb + 1) / 2 : a.nqb;
   int bh, slot;
-  attn_block_coords(a.Hq, a.Hkv, nslot, a.xcd_map != 0, bh, slot);
+  attn_block_coords(a.Hq, a.Hkv, nslot, a.xcd_map, bh, slot);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, l32 = lane & 31;
@@ -372,9 +372,10 @@ extern "C" int sl8_attn_w8a8_fwd(const int8_t* q, const float* q_scale, const in
   a.M = (int)M; a.N = (int)N; a.Npad = (int)Npad; a.Hq = (int)Hq; a.Hkv = (int)Hkv;
   a.nqb = (int)((M + WBM - 1) / WBM);
   a.causal_diag = (int)causal_diag;
-  a.xcd_map = ((B * Hkv) % 8 == 0) ? 1 : 0;
   const bool c = causal != 0, pw = per_warp_quant != 0;
-  const int grid = (int)(B * Hq * (c ? (a.nqb + 1) / 2 : a.nqb));
+  const int nslot = c ? (a.nqb + 1) / 2 : a.nqb;
+  a.xcd_map = xcd_mode(B * Hkv, Hq / Hkv, nslot);
+  const int grid = (int)(B * Hq * nslot);
   if (D == 64) launch_w8_d<64>(a, grid, c, pw, st);
   else if (D == 128) launch_w8_d<128>(a, grid, c, pw, st);
   else launch_w8_d<256>(a, grid, c, pw, st);
