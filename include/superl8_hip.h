@@ -59,9 +59,12 @@ int sl8_quantize_i8_rowwise(const void* x, int x_dtype, int64_t M, int64_t K,
  * (_mean_k_fp32_bounded / smooth_k). fp16 input is summed exactly in int64
  * fixed point (order-independent); bf16/f32 in fp64, rows in order.
  *   k [G, N, D] (dtype f16/bf16/f32) -> mean fp32 [G, D]
+ * workspace: sl8_k_mean_workspace(G, D) bytes, 8-byte aligned (used for fp16:
+ * the int64 partial sums; contents need not be initialised).
  * ---------------------------------------------------------------------- */
+size_t sl8_k_mean_workspace(int64_t G, int64_t D);
 int sl8_k_mean(const void* k, int dtype, int64_t G, int64_t N, int64_t D,
-               float* mean, void* stream);
+               float* mean, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Fused smooth + quantise (quantize_qk's K side, and Q with mean=NULL):

@@ -72,9 +72,11 @@ def k_mean(k: torch.Tensor) -> torch.Tensor:
     G = math.prod(lead)
     mean = torch.empty((*lead, 1, D), device=k.device, dtype=torch.float32)
     if G and D:
+        ws_bytes = _lib.load().sl8_k_mean_workspace(G, D)
+        ws = torch.empty((max(ws_bytes, 8),), device=k.device, dtype=torch.uint8)
         with torch.cuda.device(k.device):
             call("sl8_k_mean", k.data_ptr(), dtype_code(k.dtype), G, N, D, mean.data_ptr(),
-                 stream_of(k))
+                 ws.data_ptr(), ws_bytes, stream_of(k))
     return mean
 
 

@@ -25,7 +25,8 @@ SIGNATURES = {
     "sl8_last_error": (ctypes.c_char_p, []),
     "sl8_version": (ctypes.c_char_p, []),
     "sl8_quantize_i8_rowwise": (_I, [_P, _I, _I64, _I64, _P, _P, _P]),
-    "sl8_k_mean": (_I, [_P, _I, _I64, _I64, _I64, _P, _P]),
+    "sl8_k_mean_workspace": (_SZ, [_I64, _I64]),
+    "sl8_k_mean": (_I, [_P, _I, _I64, _I64, _I64, _P, _P, _SZ, _P]),
     "sl8_quantize_i8_rows_centered": (_I, [_P, _I, _I64, _I64, _I64, _P, _F, _P, _P, _P]),
     "sl8_quantize_i8_cols": (_I, [_P, _I, _I64, _I64, _I64, _P, _P, _P]),
     "sl8_attn_int8_fwd_workspace": (_SZ, [_I64, _I64, _I64, _I64]),

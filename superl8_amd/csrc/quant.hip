@@ -16,6 +16,7 @@
 #include "common.hpp"
 
 #include <cmath>
+#include <type_traits>
 #include <string>
 
 namespace sl8 {
@@ -108,6 +109,103 @@ quant_rows_kernel(const typename Elem<DT>::T* __restrict__ x, const float* __res
   }
 }
 
+
+// Vectorised variant: LPR lanes per row (LPR = 256: one workgroup per row),
+// each lane holding NV 16-byte vectors of the row in registers for both the
+// amax and the code pass (one HBM read per element). Needs K a multiple of
+// the elements per 16 bytes (EPV) and a 16-byte aligned base.
+template <int DT> struct VecIO;
+template <> struct VecIO<SL8_DTYPE_F16> {
+  static constexpr int EPV = 8;
+  __device__ static void unpack(uint4 v, float* f) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { f[2 * i] = h2f(w[i] & 0xFFFF); f[2 * i + 1] = h2f(w[i] >> 16); }
+  }
+};
+template <> struct VecIO<SL8_DTYPE_BF16> {
+  static constexpr int EPV = 8;
+  __device__ static void unpack(uint4 v, float* f) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { f[2 * i] = bf2f(w[i] & 0xFFFF); f[2 * i + 1] = bf2f(w[i] >> 16); }
+  }
+};
+template <> struct VecIO<SL8_DTYPE_F32> {
+  static constexpr int EPV = 4;
+  __device__ static void unpack(uint4 v, float* f) {
+    f[0] = __uint_as_float(v.x); f[1] = __uint_as_float(v.y);
+    f[2] = __uint_as_float(v.z); f[3] = __uint_as_float(v.w);
+  }
+};
+
+template <int DT, int LPR, int NV, bool MEAN>
+__global__ void __launch_bounds__(QTHREADS)
+quant_rows_vec_kernel(const typename Elem<DT>::T* __restrict__ x, const float* __restrict__ mean,
+                      int8_t* __restrict__ q, float* __restrict__ scale, int64_t rows,
+                      int64_t rows_per_mean, int K, float scale_mul) {
+  using T = typename Elem<DT>::T;
+  constexpr int EPV = VecIO<DT>::EPV;
+  const int lane = threadIdx.x % LPR;
+  const int64_t row = (int64_t)blockIdx.x * (QTHREADS / LPR) + threadIdx.x / LPR;
+  const bool live = row < rows;
+  const int64_t r = live ? row : 0;
+  const T* xr = x + r * K;
+  const float* mr = MEAN ? mean + (r / rows_per_mean) * K : nullptr;
+  const int nvec = K / EPV;
+
+  float f[NV][EPV];
+  float amax = 0.f;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int vi = v * LPR + lane;
+    const bool ok = live && vi < nvec;
+    uint4 raw = make_uint4(0, 0, 0, 0);
+    if (ok) raw = reinterpret_cast<const uint4*>(xr)[vi];
+    VecIO<DT>::unpack(raw, f[v]);
+    if constexpr (MEAN) {
+#pragma unroll
+      for (int e = 0; e < EPV; ++e)
+        f[v][e] = ok ? Elem<DT>::round(f[v][e] - mr[vi * EPV + e]) : 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) amax = fmaxf(amax, fabsf(f[v][e]));
+  }
+  if constexpr (LPR <= 64) {
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+  } else {
+    __shared__ float red[QTHREADS / 64];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < QTHREADS / 64; ++w) amax = fmaxf(amax, red[w]);
+  }
+  if (!live) return;
+  const float s = amax * (1.0f / 127.0f);
+  const float safe = (s == 0.f) ? 1.f : s;
+  if (lane == 0) scale[row] = safe * scale_mul;
+  int8_t* qr = q + r * K;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    const int vi = v * LPR + lane;
+    if (vi < nvec) {
+      uint32_t w[EPV / 4];
+#pragma unroll
+      for (int i = 0; i < EPV / 4; ++i) {
+        w[i] = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          w[i] |= (uint32_t)(uint8_t)code_of(f[v][4 * i + e], safe) << (8 * e);
+      }
+      if constexpr (EPV == 8) *reinterpret_cast<uint2*>(qr + vi * EPV) = make_uint2(w[0], w[1]);
+      else *reinterpret_cast<uint32_t*>(qr + vi * EPV) = w[0];
+    }
+  }
+}
+
 template <int DT, bool MEAN>
 int launch_quant(const void* x, const float* mean, int8_t* q, float* scale, int64_t rows,
                  int64_t rows_per_mean, int64_t K, float scale_mul, hipStream_t st) {
@@ -120,9 +218,32 @@ int launch_quant(const void* x, const float* mean, int8_t* q, float* scale, int6
     quant_rows_kernel<DT, LPR, MEAN><<<grid, QTHREADS, 0, st>>>(xp, mean, q, scale, rows,
                                                                 rows_per_mean, (int)K, scale_mul);
   };
-  if (K <= 128) go(std::integral_constant<int, 16>{});
-  else if (K <= 512) go(std::integral_constant<int, 32>{});
-  else go(std::integral_constant<int, 64>{});
+  constexpr int EPV = VecIO<DT>::EPV;
+  if (K % EPV == 0 && aligned(x, 16) && aligned(q, EPV) && K / EPV <= 8 * QTHREADS) {
+    const int64_t nvec = K / EPV;
+    auto gv = [&](auto lpr_tag, auto nv_tag) {
+      constexpr int LPR = decltype(lpr_tag)::value, NV = decltype(nv_tag)::value;
+      const int64_t rpb = QTHREADS / LPR;
+      const dim3 grid((unsigned)((rows + rpb - 1) / rpb));
+      quant_rows_vec_kernel<DT, LPR, NV, MEAN><<<grid, QTHREADS, 0, st>>>(
+          xp, mean, q, scale, rows, rows_per_mean, (int)K, scale_mul);
+    };
+    using I = std::integral_constant<int, 1>;
+    if (nvec <= 16) gv(std::integral_constant<int, 16>{}, I{});
+    else if (nvec <= 32) gv(std::integral_constant<int, 32>{}, I{});
+    else if (nvec <= 64) gv(std::integral_constant<int, 64>{}, I{});
+    else if (nvec <= 128) gv(std::integral_constant<int, 64>{}, std::integral_constant<int, 2>{});
+    else if (nvec <= 256) gv(std::integral_constant<int, 256>{}, I{});
+    else if (nvec <= 512) gv(std::integral_constant<int, 256>{}, std::integral_constant<int, 2>{});
+    else if (nvec <= 1024) gv(std::integral_constant<int, 256>{}, std::integral_constant<int, 4>{});
+    else gv(std::integral_constant<int, 256>{}, std::integral_constant<int, 8>{});
+  } else if (K <= 128) {
+    go(std::integral_constant<int, 16>{});
+  } else if (K <= 512) {
+    go(std::integral_constant<int, 32>{});
+  } else {
+    go(std::integral_constant<int, 64>{});
+  }
   SL8_CHECK_LAUNCH("quantize_i8_rowwise");
   return SL8_OK;
 }
@@ -147,33 +268,50 @@ int dispatch_quant(const void* x, int dt, const float* mean, int8_t* q, float* s
 // ---- K mean -------------------------------------------------------------
 // fp16: every value is an integer multiple of 2^-24 below 2^16 in magnitude,
 // so sum(x * 2^24) is an exact int64 for N < 2^23 rows: the mean does not
-// depend on summation order. Block = 64 columns x 16 row phases.
+// depend on summation order. Blocks take (64 columns, a chunk of rows); a
+// block's exact partial sum is added to the int64 workspace with an integer
+// atomic (exact, so still order free), and a last pass scales it.
 constexpr int MEAN_COLS = 64;
 constexpr int MEAN_PHASES = 16;
+constexpr int MEAN_CHUNK = 256;  // rows per block
+
+__global__ void __launch_bounds__(256) i64_zero_kernel(unsigned long long* p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0ull;
+}
 
 __global__ void __launch_bounds__(MEAN_COLS * MEAN_PHASES)
-k_mean_f16_kernel(const uint16_t* __restrict__ k, float* __restrict__ mean, int64_t N, int D) {
+k_mean_f16_kernel(const uint16_t* __restrict__ k, unsigned long long* __restrict__ acc, int64_t N,
+                  int D) {
   __shared__ long long part[MEAN_PHASES][MEAN_COLS];
   const int col = threadIdx.x % MEAN_COLS;
   const int ph = threadIdx.x / MEAN_COLS;
   const int64_t g = blockIdx.y;
   const int d = blockIdx.x * MEAN_COLS + col;
-  long long acc = 0;
+  const int64_t n0 = (int64_t)blockIdx.z * MEAN_CHUNK;
+  const int64_t n1 = min(N, n0 + MEAN_CHUNK);
+  long long a = 0;
   if (d < D) {
     const uint16_t* kg = k + g * N * D + d;
-    for (int64_t n = ph; n < N; n += MEAN_PHASES) {
-      const float v = h2f(kg[n * D]);
-      acc += (long long)ldexpf(v, 24);  // exact: |v| * 2^24 < 2^40, integral
-    }
+#pragma unroll 4
+    for (int64_t n = n0 + ph; n < n1; n += MEAN_PHASES)
+      a += (long long)ldexpf(h2f(kg[n * D]), 24);  // exact: |v| * 2^24 < 2^40, integral
   }
-  part[ph][col] = acc;
+  part[ph][col] = a;
   __syncthreads();
   if (ph == 0 && d < D) {
-    long long s = 0;
+    long long t = 0;
 #pragma unroll
-    for (int p = 0; p < MEAN_PHASES; ++p) s += part[p][col];
-    mean[g * D + d] = (float)(((double)s * 0x1p-24) / (double)N);
+    for (int p = 0; p < MEAN_PHASES; ++p) t += part[p][col];
+    atomicAdd(acc + g * D + d, (unsigned long long)t);  // two's complement: exact mod 2^64
   }
+}
+
+__global__ void __launch_bounds__(256)
+k_mean_finish_kernel(const unsigned long long* __restrict__ acc, float* __restrict__ mean,
+                     int64_t n, int64_t N) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) mean[i] = (float)(((double)(long long)acc[i] * 0x1p-24) / (double)N);
 }
 
 // bf16 / f32: fp64 running sum over rows in index order (one thread per column).
@@ -192,27 +330,44 @@ k_mean_seq_kernel(const typename Elem<DT>::T* __restrict__ k, float* __restrict_
 
 // ---- per-channel (column) quantisation over the key axis ----------------
 // scale[g,d] = amax_n |x[g,n,d]| * fp32(1/127) (1 if 0); max is order-free.
+// Blocks take (64 columns, a chunk of rows) and fold their max into the
+// scale buffer with an integer atomic max on the (non-negative) float bits;
+// a last pass turns the maxima into scales.
 template <int DT>
 __global__ void __launch_bounds__(MEAN_COLS * MEAN_PHASES)
-col_amax_kernel(const typename Elem<DT>::T* __restrict__ x, float* __restrict__ scale, int64_t N,
-                int D) {
+col_amax_kernel(const typename Elem<DT>::T* __restrict__ x, unsigned int* __restrict__ amax_bits,
+                int64_t N, int D) {
   __shared__ float part[MEAN_PHASES][MEAN_COLS];
   const int col = threadIdx.x % MEAN_COLS, ph = threadIdx.x / MEAN_COLS;
   const int64_t g = blockIdx.y;
   const int d = blockIdx.x * MEAN_COLS + col;
+  const int64_t n0 = (int64_t)blockIdx.z * MEAN_CHUNK;
+  const int64_t n1 = min(N, n0 + MEAN_CHUNK);
   float m = 0.f;
   if (d < D) {
     const typename Elem<DT>::T* xg = x + g * N * D + d;
-    for (int64_t n = ph; n < N; n += MEAN_PHASES) m = fmaxf(m, fabsf(Elem<DT>::ld(xg, n * D)));
+#pragma unroll 4
+    for (int64_t n = n0 + ph; n < n1; n += MEAN_PHASES) m = fmaxf(m, fabsf(Elem<DT>::ld(xg, n * D)));
   }
   part[ph][col] = m;
   __syncthreads();
   if (ph == 0 && d < D) {
 #pragma unroll
     for (int p = 1; p < MEAN_PHASES; ++p) m = fmaxf(m, part[p][col]);
-    const float s = m * (1.0f / 127.0f);
-    scale[g * D + d] = (s == 0.f) ? 1.f : s;
+    atomicMax(amax_bits + g * D + d, __float_as_uint(m));
   }
+}
+
+__global__ void __launch_bounds__(256) col_scale_kernel(float* __restrict__ scale, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float s = scale[i] * (1.0f / 127.0f);  // scale holds the column max here
+  scale[i] = (s == 0.f) ? 1.f : s;
+}
+
+__global__ void __launch_bounds__(256) u32_zero_kernel(unsigned int* p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0u;
 }
 
 template <int DT>
@@ -240,25 +395,33 @@ extern "C" int sl8_quantize_i8_cols(const void* x, int dtype, int64_t G, int64_t
   if (G == 0 || D == 0) return SL8_OK;
   SL8_CHECK_ARG(x && q && scale, "quantize_v_perchannel: null pointer");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 grid((unsigned)((D + MEAN_COLS - 1) / MEAN_COLS), (unsigned)G);
+  const int64_t nsc = G * D;
+  const dim3 grid((unsigned)((D + MEAN_COLS - 1) / MEAN_COLS), (unsigned)G,
+                  (unsigned)((N + MEAN_CHUNK - 1) / MEAN_CHUNK));
   const int64_t total = G * N * D;
   const unsigned qgrid = (unsigned)((total + 255) / 256);
+  const unsigned sgrid = (unsigned)((nsc + 255) / 256);
+  unsigned int* bits = reinterpret_cast<unsigned int*>(scale);
+  u32_zero_kernel<<<sgrid, 256, 0, st>>>(bits, nsc);
   switch (dtype) {
     case SL8_DTYPE_F16:
-      col_amax_kernel<SL8_DTYPE_F16><<<grid, MEAN_COLS * MEAN_PHASES, 0, st>>>(
-          static_cast<const uint16_t*>(x), scale, N, (int)D);
+      if (N) col_amax_kernel<SL8_DTYPE_F16><<<grid, MEAN_COLS * MEAN_PHASES, 0, st>>>(
+          static_cast<const uint16_t*>(x), bits, N, (int)D);
+      col_scale_kernel<<<sgrid, 256, 0, st>>>(scale, nsc);
       if (total) col_quant_kernel<SL8_DTYPE_F16><<<qgrid, 256, 0, st>>>(
           static_cast<const uint16_t*>(x), scale, q, N, (int)D, total);
       break;
     case SL8_DTYPE_BF16:
-      col_amax_kernel<SL8_DTYPE_BF16><<<grid, MEAN_COLS * MEAN_PHASES, 0, st>>>(
-          static_cast<const uint16_t*>(x), scale, N, (int)D);
+      if (N) col_amax_kernel<SL8_DTYPE_BF16><<<grid, MEAN_COLS * MEAN_PHASES, 0, st>>>(
+          static_cast<const uint16_t*>(x), bits, N, (int)D);
+      col_scale_kernel<<<sgrid, 256, 0, st>>>(scale, nsc);
       if (total) col_quant_kernel<SL8_DTYPE_BF16><<<qgrid, 256, 0, st>>>(
           static_cast<const uint16_t*>(x), scale, q, N, (int)D, total);
       break;
     default:
-      col_amax_kernel<SL8_DTYPE_F32><<<grid, MEAN_COLS * MEAN_PHASES, 0, st>>>(
-          static_cast<const float*>(x), scale, N, (int)D);
+      if (N) col_amax_kernel<SL8_DTYPE_F32><<<grid, MEAN_COLS * MEAN_PHASES, 0, st>>>(
+          static_cast<const float*>(x), bits, N, (int)D);
+      col_scale_kernel<<<sgrid, 256, 0, st>>>(scale, nsc);
       if (total) col_quant_kernel<SL8_DTYPE_F32><<<qgrid, 256, 0, st>>>(
           static_cast<const float*>(x), scale, q, N, (int)D, total);
       break;
@@ -298,8 +461,13 @@ extern "C" int sl8_quantize_i8_rows_centered(const void* x, int x_dtype, int64_t
                         static_cast<hipStream_t>(stream));
 }
 
+extern "C" size_t sl8_k_mean_workspace(int64_t G, int64_t D) {
+  if (G <= 0 || D <= 0) return 0;
+  return (size_t)(G * D) * sizeof(long long);
+}
+
 extern "C" int sl8_k_mean(const void* k, int dtype, int64_t G, int64_t N, int64_t D,
-                          float* mean, void* stream) {
+                          float* mean, void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
   SL8_CHECK_ARG(dtype == SL8_DTYPE_F16 || dtype == SL8_DTYPE_BF16 || dtype == SL8_DTYPE_F32,
                 "k_mean: input must be float16/bfloat16/float32");
@@ -307,17 +475,29 @@ extern "C" int sl8_k_mean(const void* k, int dtype, int64_t G, int64_t N, int64_
   SL8_CHECK_ARG(N < (1LL << 23), "k_mean: N must be < 2^23 keys, got %lld", (long long)N);
   if (G == 0 || D == 0) return SL8_OK;
   SL8_CHECK_ARG(N > 0, "k_mean: mean over zero keys");
+  SL8_CHECK_ARG(k && mean, "k_mean: null pointer");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 grid((unsigned)((D + MEAN_COLS - 1) / MEAN_COLS), (unsigned)G);
   if (dtype == SL8_DTYPE_F16) {
-    k_mean_f16_kernel<<<grid, MEAN_COLS * MEAN_PHASES, 0, st>>>(
-        static_cast<const uint16_t*>(k), mean, N, (int)D);
-  } else if (dtype == SL8_DTYPE_BF16) {
-    k_mean_seq_kernel<SL8_DTYPE_BF16><<<grid, MEAN_COLS, 0, st>>>(
-        static_cast<const uint16_t*>(k), mean, N, (int)D);
+    const size_t need = sl8_k_mean_workspace(G, D);
+    SL8_CHECK_ARG(workspace && workspace_bytes >= need && aligned(workspace, 8),
+                  "k_mean: workspace needs %zu bytes", need);
+    unsigned long long* acc = static_cast<unsigned long long*>(workspace);
+    const int64_t n = G * D;
+    const unsigned ng = (unsigned)((n + 255) / 256);
+    i64_zero_kernel<<<ng, 256, 0, st>>>(acc, n);
+    const dim3 grid((unsigned)((D + MEAN_COLS - 1) / MEAN_COLS), (unsigned)G,
+                    (unsigned)((N + MEAN_CHUNK - 1) / MEAN_CHUNK));
+    k_mean_f16_kernel<<<grid, MEAN_COLS * MEAN_PHASES, 0, st>>>(static_cast<const uint16_t*>(k),
+                                                                 acc, N, (int)D);
+    k_mean_finish_kernel<<<ng, 256, 0, st>>>(acc, mean, n, N);
   } else {
-    k_mean_seq_kernel<SL8_DTYPE_F32><<<grid, MEAN_COLS, 0, st>>>(
-        static_cast<const float*>(k), mean, N, (int)D);
+    const dim3 grid((unsigned)((D + MEAN_COLS - 1) / MEAN_COLS), (unsigned)G);
+    if (dtype == SL8_DTYPE_BF16)
+      k_mean_seq_kernel<SL8_DTYPE_BF16><<<grid, MEAN_COLS, 0, st>>>(static_cast<const uint16_t*>(k),
+                                                                    mean, N, (int)D);
+    else
+      k_mean_seq_kernel<SL8_DTYPE_F32><<<grid, MEAN_COLS, 0, st>>>(static_cast<const float*>(k),
+                                                                   mean, N, (int)D);
   }
   SL8_CHECK_LAUNCH("k_mean");
   return SL8_OK;

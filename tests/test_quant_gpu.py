@@ -11,7 +11,9 @@ from superl8_amd import _C, quant
 pytestmark = pytest.mark.gpu
 
 SHAPES = [(1, 896), (3, 896), (8, 896), (16, 4864), (4096, 896), (2, 17), (5, 4097), (7, 64),
-          (33, 128), (1, 5120), (8, 5120)]
+          (33, 128), (1, 5120), (8, 5120),
+          # vectorised paths: 1..8 vectors per lane, one workgroup per row
+          (2, 16384), (3, 12288), (4, 8), (9, 2048), (17, 1024), (1000, 256)]
 
 
 def _np(x):
@@ -55,7 +57,8 @@ def test_quantize_deterministic(device):
 
 @pytest.mark.parametrize("dtype,tag", [(torch.float16, "f16"), (torch.bfloat16, "bf16"),
                                        (torch.float32, "f32")])
-@pytest.mark.parametrize("shape", [(1, 8, 4096, 128), (2, 3, 777, 64), (1, 1, 5, 256)])
+@pytest.mark.parametrize("shape", [(1, 8, 4096, 128), (2, 3, 777, 64), (1, 1, 5, 256),
+                                   (1, 2, 70000, 64)])
 def test_k_mean_bit_exact(device, dtype, tag, shape):
     k = (torch.randn(shape, device=device) * 2).to(dtype)
     m = _C.k_mean(k)
