@@ -89,10 +89,13 @@ template <> struct PvOp<SL8_DTYPE_F16> {
   __device__ static v16f mfma(vec a, vec b, v16f c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
-  // acc + sum of the 8 fp32 values the vector was packed from
-  __device__ static float sum(vec, const float* p, float acc) {
+  // acc + sum of the 8 packed values (v_dot2_f32_f16 against ones): the row
+  // sum of exactly the P that enters the PV product
+  __device__ static float sum(vec v, const float*, float acc) {
+    typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+    const v2h one = {(_Float16)1.0f, (_Float16)1.0f};
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc += p[e];
+    for (int e = 0; e < 8; e += 2) acc = __builtin_amdgcn_fdot2(v2h{v[e], v[e + 1]}, one, acc, false);
     return acc;
   }
   __device__ static void scale(vec& v, float s) {
@@ -111,10 +114,13 @@ template <> struct PvOp<SL8_DTYPE_BF16> {
   __device__ static v16f mfma(vec a, vec b, v16f c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
-  // acc + sum of the 8 fp32 values the vector was packed from
-  __device__ static float sum(vec, const float* p, float acc) {
+  // acc + sum of the 8 packed values (v_dot2_f32_bf16 against ones)
+  __device__ static float sum(vec v, const float*, float acc) {
+    typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+    const v2bf one = {(__bf16)1.0f, (__bf16)1.0f};
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc += p[e];
+    for (int e = 0; e < 8; e += 2)
+      acc = __builtin_amdgcn_fdot2_f32_bf16(v2bf{v[e], v[e + 1]}, one, acc, false);
     return acc;
   }
   __device__ static void scale(vec& v, float s) {

@@ -93,7 +93,11 @@ def test_kernel_matches_oracle(device, case, vdt):
     if lse is not None:
         finite = np.isfinite(ref_lse)
         np.testing.assert_array_equal(np.isfinite(_np(lse)), finite)
-        np.testing.assert_allclose(_np(lse)[finite], ref_lse[finite], rtol=1e-5, atol=1e-5)
+        # l sums the fp16/bf16-rounded P that enters the PV product (the oracle sums
+        # fp32 P): |dLSE| up to the relative P rounding (2^-11 fp16, 2^-8 bf16),
+        # undamped on rows with few keys
+        lse_tol = 5e-4 if vdt == torch.float16 else 4e-3
+        np.testing.assert_allclose(_np(lse)[finite], ref_lse[finite], rtol=0, atol=lse_tol)
 
 
 SHAPES = [(1, 2, 128, 64), (2, 4, 512, 64), (2, 4, 257, 64), (1, 2, 333, 128),
@@ -200,4 +204,4 @@ def test_reference_point_restart(device, causal):
     assert_finite(out)
     assert_close_abs(out, ref, atol=1e-2, what="restart path vs oracle")
     finite = np.isfinite(ref_lse)
-    np.testing.assert_allclose(_np(lse)[finite], ref_lse[finite], rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(_np(lse)[finite], ref_lse[finite], rtol=0, atol=5e-4)
