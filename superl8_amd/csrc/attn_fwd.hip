@@ -437,31 +437,33 @@ attn_fwd_kernel(const FwdArgs a) {
 
 
 // ---------------------------------------------------------------------------
-// Wide variant (the production path): a wave owns 64 queries -- two 32-query
-// MFMA column blocks that share every K / V^T operand read from LDS, which
-// halves LDS traffic per query -- and the workgroup owns 256 queries (one
-// workgroup per CU, one wave per SIMD; the O accumulators live in the MFMA
-// accumulator registers). The key loop is software-pipelined so the matrix
-// cores always have independent work queued while the softmax runs:
-//   iteration j:  QK of tile j+1  ||  max / scaling of tile j
-//                 PV of tile j-1  ||  exp2 / pack / row sums of tile j
-// P of tile j stays in registers until iteration j+1. Lazy rescaling (see the
-// narrow kernel) happens before PV of tile j-1 is issued, so that pending P
-// block is scaled together with O.
+// Production kernel. A wave owns NG x 32 queries (NG = 1: one MFMA column
+// block) for the whole key loop; WV waves per workgroup (8 for D = 128, 4 for
+// D = 64; two waves per SIMD) share each 64-key K / k_scale / V^T tile, copied
+// global -> LDS one tile ahead, so a larger workgroup means fewer copies per
+// query. Each tile is processed as two 32-key half-steps; half-step h issues
+// QK of half h and PV of half h-2 on the matrix cores while the VALU does the
+// softmax of half h-1, so P stays in registers for one half-step. The
+// reference point of the softmax is set once per row (see settle()) and O is
+// never rescaled inside the loop.
+// Per wave and tile (D = 128): 8 i8 + 16 f16 32x32 MFMAs, 24 KB of LDS
+// operand reads (1 KB per MFMA), ~7 VALU operations per score.
 // ---------------------------------------------------------------------------
 
 #ifndef SL8_FWD_OCC
 #define SL8_FWD_OCC 2
 #endif
-// NG = 32-query MFMA column blocks per wave (1 or 2).
-template <int D, bool CAUSAL, int VDT, bool LSE, int NG>
-__global__ void __launch_bounds__(FWD_THREADS, NG == 1 ? SL8_FWD_OCC : 1)
+// NG = 32-query MFMA column blocks per wave (1 or 2), WV = waves per
+// workgroup (they share every K / V^T tile copied into LDS).
+template <int D, bool CAUSAL, int VDT, bool LSE, int NG, int WV>
+__global__ void __launch_bounds__(WV * 64, NG == 1 ? SL8_FWD_OCC * 4 / WV : 1)
 attn_fwd_wide_kernel(const FwdArgs a) {
+  constexpr int WT = WV * 64;                  // threads per workgroup
   constexpr int WQ = 32 * NG;                  // queries per wave
-  constexpr int WBM = FWD_WAVES * WQ;          // queries per workgroup
+  constexpr int WBM = WV * WQ;                 // queries per workgroup
   constexpr int DC = D / 32;
-  constexpr int KCH = BN * D / 16 / FWD_THREADS;
-  constexpr int VCH = D * BN * 2 / 16 / FWD_THREADS;
+  constexpr int KCH = BN * D / 16 / WT;
+  constexpr int VCH = D * BN * 2 / 16 / WT;
   static_assert(KCH >= 1 && VCH >= 1, "tile copies cover D in {64,128}");
   __shared__ __attribute__((aligned(16))) int8_t sm_k0[BN * D];
   __shared__ __attribute__((aligned(16))) int8_t sm_k1[BN * D];
@@ -507,7 +509,7 @@ attn_fwd_wide_kernel(const FwdArgs a) {
   for (int c4 = 0; c4 < 4; ++c4) voff[c4] = ((2 * c4 + h) ^ ((l32 >> 1) & 7)) * 8;
   // V buffers start as zeros (finite): the pipeline's first half-steps
   // multiply them by P = 0.
-  for (int i = tid; i < D * BN / 8; i += FWD_THREADS) {
+  for (int i = tid; i < D * BN / 8; i += WT) {
     reinterpret_cast<uint4*>(sm_v0)[i] = make_uint4(0, 0, 0, 0);
     reinterpret_cast<uint4*>(sm_v1)[i] = make_uint4(0, 0, 0, 0);
   }
@@ -556,21 +558,21 @@ attn_fwd_wide_kernel(const FwdArgs a) {
     auto load_k = [&](int n0, int8_t* dst) __attribute__((always_inline)) {
 #pragma unroll
       for (int i = 0; i < KCH; ++i) {
-        const int sl = i * FWD_THREADS + tid;
+        const int sl = i * WT + tid;
         const int row = sl / KCPR;
         const int c = (sl % KCPR) ^ ((row >> KSH) & (KCPR - 1));
         dma16_to_lds(kb + (int64_t)min(n0 + row, N - 1) * D + 16 * c,
-                     dst + (i * FWD_THREADS + wave * 64) * 16);
+                     dst + (i * WT + wave * 64) * 16);
       }
     };
     auto load_v = [&](int n0, uint16_t* dst) __attribute__((always_inline)) {
 #pragma unroll
       for (int i = 0; i < VCH; ++i) {
-        const int sl = i * FWD_THREADS + tid;
+        const int sl = i * WT + tid;
         const int row = sl / 8;
         const int c = (sl % 8) ^ ((row >> 1) & 7);
         dma16_to_lds(vtb + (int64_t)row * a.Npad + n0 + 8 * c,
-                     dst + (i * FWD_THREADS + wave * 64) * 8);
+                     dst + (i * WT + wave * 64) * 8);
       }
     };
     auto load_s = [&](int n0, float* dst) __attribute__((always_inline)) {
@@ -837,11 +839,21 @@ attn_fwd_wide_kernel(const FwdArgs a) {
 #define SL8_FWD_NG 1
 #endif
 constexpr int WIDE_NG = SL8_FWD_NG;
-constexpr int WIDE_BM = FWD_WAVES * 32 * WIDE_NG;  // queries per workgroup
+// waves per workgroup of the production kernel, per head dim
+#ifndef SL8_FWD_WV128
+#define SL8_FWD_WV128 8
+#endif
+#ifndef SL8_FWD_WV64
+#define SL8_FWD_WV64 4
+#endif
+constexpr int wide_waves(int64_t D) { return D == 128 ? SL8_FWD_WV128 : SL8_FWD_WV64; }
+// queries per workgroup
+constexpr int wide_bm(int64_t D) { return wide_waves(D) * 32 * WIDE_NG; }
 
 template <int D, bool CAUSAL, int VDT, bool LSE>
 void launch_wide(const FwdArgs& a, int grid, hipStream_t st) {
-  attn_fwd_wide_kernel<D, CAUSAL, VDT, LSE, WIDE_NG><<<grid, FWD_THREADS, 0, st>>>(a);
+  constexpr int WV = wide_waves(D);
+  attn_fwd_wide_kernel<D, CAUSAL, VDT, LSE, WIDE_NG, WV><<<grid, WV * 64, 0, st>>>(a);
 }
 
 template <int D, int VDT>
@@ -946,7 +958,7 @@ extern "C" int sl8_attn_int8_fwd(const int8_t* q, const float* q_scale, const in
   a.vt = static_cast<const uint16_t*>(workspace);
   a.out = out; a.lse = lse; a.window_left = (int)window_left;
   const bool c = causal != 0, want_lse = lse != nullptr;
-  a.nqb = (int)((M + WIDE_BM - 1) / WIDE_BM);
+  a.nqb = (int)((M + wide_bm(D) - 1) / wide_bm(D));
   const int nslot = c ? (a.nqb + 1) / 2 : a.nqb;
   grid = (int)(B * Hq * nslot);
   a.xcd_map = xcd_mode(B * Hkv, Hq / Hkv, nslot);
