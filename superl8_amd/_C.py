@@ -19,7 +19,7 @@ import torch
 from . import _lib
 from ._lib import call, dtype_code, stream_of
 
-_HEAD_DIMS_FWD = (64, 128)
+_HEAD_DIMS_FWD = (64, 128, 256)
 _HEAD_DIMS_W8A8 = (64, 128, 256)
 _HEAD_DIMS_DECODE = (64, 128, 256)
 DEC_MAX_SPLITS = 256
@@ -178,7 +178,7 @@ def attn_int8_qk_scores(q, k):
     B, H, M, D = q.shape
     Hkv, N = k.shape[1], k.shape[2]
     _check(H % Hkv == 0 and k.shape[3] == D and k.shape[0] == B, "q/k shape mismatch")
-    _check(D in _HEAD_DIMS_FWD, f"head dim must be one of {_HEAD_DIMS_FWD}, got {D}")
+    _check(D in (64, 128), f"head dim must be one of (64, 128), got {D}")
     s = torch.empty((B, H, M, N), device=q.device, dtype=torch.int32)
     if s.numel():
         with torch.cuda.device(q.device):

@@ -77,6 +77,33 @@ v_transpose_kernel(const uint16_t* __restrict__ v, uint16_t* __restrict__ vt, in
   }
 }
 
+// int8 V [BHkv][N][D] -> bf16 V^T [BHkv][D][Npad] (exact: |code| <= 127),
+// same key permutation and padding as v_transpose_kernel.
+template <int D>
+__global__ void __launch_bounds__(256)
+v8_to_bf16_transpose_kernel(const int8_t* __restrict__ v, uint16_t* __restrict__ vt, int N, int Npad) {
+  __shared__ int8_t tile[BN][D + 4];
+  const int64_t bh = blockIdx.y;
+  const int n0 = blockIdx.x * BN;
+  const int8_t* src = v + bh * (int64_t)N * D;
+  for (int i = threadIdx.x; i < BN * D / 16; i += 256) {
+    const int r = i / (D / 16), c = (i % (D / 16)) * 16;
+    uint4 val = {0, 0, 0, 0};
+    if (n0 + r < N) val = *reinterpret_cast<const uint4*>(src + (int64_t)(n0 + r) * D + c);
+    const uint32_t w[4] = {val.x, val.y, val.z, val.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) *reinterpret_cast<uint32_t*>(&tile[r][c + 4 * e]) = w[e];
+  }
+  __syncthreads();
+  uint16_t* dst = vt + bh * (int64_t)D * Npad + n0;
+  for (int i = threadIdx.x; i < D * (BN / 2); i += 256) {
+    const int d = i / (BN / 2), pr = (i % (BN / 2)) * 2;
+    const int k0 = (pr & ~15) + vt_pos(pr & 15);
+    const uint32_t lo = f2bf_bits((float)tile[k0][d]), hi = f2bf_bits((float)tile[k0 + 1][d]);
+    *reinterpret_cast<uint32_t*>(dst + (int64_t)d * Npad + pr) = lo | (hi << 16);
+  }
+}
+
 template <int VDT> struct PvOp;
 template <> struct PvOp<SL8_DTYPE_F16> {
   typedef v8h vec;
@@ -138,7 +165,9 @@ struct FwdArgs {
   void* out;
   float* lse;
   int32_t* scores;     // DUMP mode
+  const float* vs;     // W8A8: per-channel V scale [B*Hkv][D]
   int M, N, Npad, Hq, Hkv, nqb, window_left;
+  int diag;            // causal: query i sees keys <= i + diag
   int xcd_map;         // xcd_mode(): XCD-aware block order
 };
 
@@ -203,7 +232,7 @@ attn_fwd_kernel(const FwdArgs a) {
   const int b = bh / a.Hq, hq = bh % a.Hq;
   const int64_t bkv = (int64_t)b * a.Hkv + hq / gsz;
   const int M = a.M, N = a.N;
-  const int diag = CAUSAL ? N - M : 0;
+  const int diag = CAUSAL ? a.diag : 0;
   const int wl = a.window_left;
 
   const int8_t* kb = a.k + bkv * (int64_t)N * D;
@@ -454,9 +483,11 @@ attn_fwd_kernel(const FwdArgs a) {
 #define SL8_FWD_OCC 2
 #endif
 // NG = 32-query MFMA column blocks per wave (1 or 2), WV = waves per
-// workgroup (they share every K / V^T tile copied into LDS).
-template <int D, bool CAUSAL, int VDT, bool LSE, int NG, int WV>
-__global__ void __launch_bounds__(WV * 64, NG == 1 ? SL8_FWD_OCC * 4 / WV : 1)
+// workgroup (they share every K / V^T tile copied into LDS). W8 = the full
+// W8A8 semantics (P re-quantised to int8 per 32-key half, int8 V with a
+// per-channel scale); see half_probs_w8.
+template <int D, bool CAUSAL, int VDT, bool LSE, int NG, int WV, bool W8>
+__global__ void __launch_bounds__(WV * 64, (NG == 1 && D <= 128) ? SL8_FWD_OCC * 4 / WV : 1)
 attn_fwd_wide_kernel(const FwdArgs a) {
   constexpr int WT = WV * 64;                  // threads per workgroup
   constexpr int WQ = 32 * NG;                  // queries per wave
@@ -464,7 +495,8 @@ attn_fwd_wide_kernel(const FwdArgs a) {
   constexpr int DC = D / 32;
   constexpr int KCH = BN * D / 16 / WT;
   constexpr int VCH = D * BN * 2 / 16 / WT;
-  static_assert(KCH >= 1 && VCH >= 1, "tile copies cover D in {64,128}");
+  static_assert(KCH >= 1 && VCH >= 1, "tile copies cover D in {64,128,256}");
+  static_assert(!W8 || (VDT == SL8_DTYPE_BF16 && !LSE), "W8A8: bf16 PV, no LSE");
   __shared__ __attribute__((aligned(16))) int8_t sm_k0[BN * D];
   __shared__ __attribute__((aligned(16))) int8_t sm_k1[BN * D];
   __shared__ __attribute__((aligned(16))) uint16_t sm_v0[D * BN];
@@ -501,7 +533,7 @@ attn_fwd_wide_kernel(const FwdArgs a) {
   // consecutive tile rows, so a row's chunks are XOR-swizzled with the row's
   // index above the rows that share one 256-byte bank line (K rows: D bytes,
   // V^T rows: 128 bytes).
-  constexpr int KSH = D == 128 ? 1 : 2;
+  constexpr int KSH = D == 256 ? 0 : (D == 128 ? 1 : 2);
   int koff[DC], voff[4];
 #pragma unroll
   for (int ch = 0; ch < DC; ++ch) koff[ch] = ((2 * ch + h) ^ ((l32 >> KSH) & (KCPR - 1))) * 16;
@@ -634,7 +666,7 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       // conversion above), instead of issuing them as separate clusters.
       __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);  // LDS reads
 #pragma unroll
-      for (int i = 0; i < 12 * NG; ++i) {
+      for (int i = 0; i < 3 * DC * NG; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
         __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
@@ -707,6 +739,41 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       }
     };
 
+    // W8A8 (reference attn_w8a8_fwd.cuh, per-warp quantisation): P of each
+    // 32-key half is re-quantised against the half's own max,
+    //   code = rint(127 * 2^(t - tmax_h)),
+    // and enters the bf16 PV operand as code * 2^(tmax_h - m) / 127 (an
+    // integer <= 127 times one per-row factor, applied before the product
+    // instead of after the int32 sum), with m the exact row max from a
+    // QK-only sweep that precedes the pass: logits with large outliers leave
+    // no usable first guess for m, and O is never rescaled. The denominator
+    // sums the unquantised 2^(t - m).
+    auto half_probs_w8 = [&](const xblk& xi, pblk& pc) __attribute__((always_inline)) {
+      constexpr float LOG2_127 = 6.988684686772166f;
+      float tm[NG];
+      half_max(xi, tm);
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        tm[g] *= qsc[g];
+        const bool any_key = tm[g] != -INFINITY;
+        const float sub = any_key ? tm[g] - LOG2_127 : 0.f;
+        const float fac = any_key ? __builtin_amdgcn_exp2f(tm[g] - m_run[g]) * (1.0f / 127.0f) : 0.f;
+        float hs = 0.f;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          float pe[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float y = __builtin_amdgcn_exp2f(fmaf(xi[g][8 * c + e], qsc[g], -sub));
+            hs += y;
+            pe[e] = rintf(y) * fac;
+          }
+          pc[g][c] = PV::pack(pe);
+        }
+        l_lane[g] += hs * fac;
+      }
+    };
+
     xblk xA, xB;  // scores of the last two halves (alternating)
     pblk pA, pB;  // P of the last two halves (alternating)
     // One half-step, a single straight-line block per variant: xi/p1 = the
@@ -723,6 +790,56 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       half_scores(sc, st, j, s, mask, dead, xo);
       settle(xo);
     };
+    auto half_step_w8 = [&](int j, int s, const int8_t* kt, const float* st, const uint16_t* vt,
+                            bool mask, bool dead, xblk& xi, pblk& p1, xblk& xo,
+                            pblk& p2) __attribute__((always_inline)) {
+      v16i sc[NG];
+      half_qk(kt, s, sc);
+      half_pv(vt, s, p2);
+      half_probs_w8(xi, p1);
+      half_scores(sc, st, j, s, mask, dead, xo);
+    };
+    // QK-only sweep: mx_all = the exact row max (exp2 domain) of the
+    // visible logits, with the same double-buffered tile copies as the pass.
+    auto sweep_tile = [&](int t, const int8_t* kc, const float* sc_, int8_t* kn, float* sn)
+        __attribute__((always_inline)) {
+      if (t + 1 < ntiles) {
+        load_k(n_beg + (t + 1) * BN, kn);
+        load_s(n_beg + (t + 1) * BN, sn);
+      }
+      if (live(t)) {
+        const bool mk = masked(t);
+        // both halves' MFMAs first: the second half's run under the first
+        // half's conversion and max
+        v16i sc0[NG], sc1[NG];
+        xblk x0, x1;
+        float t0[NG], t1[NG];
+        half_qk(kc, 0, sc0);
+        half_qk(kc, 1, sc1);
+        half_scores(sc0, sc_, t, 0, mk, false, x0);
+        half_max(x0, t0);
+        half_scores(sc1, sc_, t, 1, mk, false, x1);
+        half_max(x1, t1);
+#pragma unroll
+        for (int g = 0; g < NG; ++g) mx_all[g] = fmaxf(mx_all[g], fmaxf(t0[g], t1[g]) * qsc[g]);
+      }
+      wait_dma();
+      __syncthreads();
+    };
+    auto sweep = [&]() __attribute__((always_inline)) {
+      if (ntiles > 0) {
+        load_k(n_beg, sm_k0);
+        load_s(n_beg, sm_s0);
+      }
+      wait_dma();
+      __syncthreads();
+      int t = 0;
+      for (; t + 1 < ntiles; t += 2) {
+        sweep_tile(t, sm_k0, sm_s0, sm_k1, sm_s1);
+        sweep_tile(t + 1, sm_k1, sm_s1, sm_k0, sm_s0);
+      }
+      if (t < ntiles) sweep_tile(t, sm_k0, sm_s0, sm_k1, sm_s1);
+    };
     auto body = [&](int j, const int8_t* kcur, int8_t* knext, uint16_t* vcopy, const uint16_t* vprev,
                     const float* scur, float* snext) __attribute__((always_inline)) {
       const int n0 = n_beg + j * BN;
@@ -733,12 +850,18 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       if (j < ntiles) load_v(n0, vcopy);
       const bool dead = !live(j);
       const bool mask = dead || masked(j);
-      half_step(j, 0, kcur, scur, vprev, mask, dead, xB, pB, xA, pA);
-      half_step(j, 1, kcur, scur, vprev, mask, dead, xA, pA, xB, pB);
+      if constexpr (W8) {
+        half_step_w8(j, 0, kcur, scur, vprev, mask, dead, xB, pB, xA, pA);
+        half_step_w8(j, 1, kcur, scur, vprev, mask, dead, xA, pA, xB, pB);
+      } else {
+        half_step(j, 0, kcur, scur, vprev, mask, dead, xB, pB, xA, pA);
+        half_step(j, 1, kcur, scur, vprev, mask, dead, xA, pA, xB, pB);
+      }
       wait_dma();
       __syncthreads();
     };
-    for (int attempt = 0; attempt < 2; ++attempt) {
+    if constexpr (W8) sweep();
+    for (int attempt = W8 ? 1 : 0; attempt < 2; ++attempt) {
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
 #pragma unroll
@@ -785,25 +908,7 @@ attn_fwd_wide_kernel(const FwdArgs a) {
 
       if (!__syncthreads_or(ovf ? 1 : 0)) break;
       // QK-only sweep for the exact row max (the whole workgroup takes part)
-      for (int t = 0; t < ntiles; ++t) {
-        load_k(n_beg + t * BN, sm_k0);
-        load_s(n_beg + t * BN, sm_s0);
-        wait_dma();
-        __syncthreads();
-        if (live(t)) {
-#pragma unroll
-          for (int s2 = 0; s2 < 2; ++s2) {
-            v16i sc[NG];
-            float tmax[NG];
-            half_qk(sm_k0, s2, sc);
-            half_scores(sc, sm_s0, t, s2, true, false, xA);
-            half_max(xA, tmax);
-#pragma unroll
-            for (int g = 0; g < NG; ++g) mx_all[g] = fmaxf(mx_all[g], tmax[g] * qsc[g]);
-          }
-        }
-        __syncthreads();
-      }
+      sweep();
     }
 
 #pragma unroll
@@ -816,11 +921,16 @@ attn_fwd_wide_kernel(const FwdArgs a) {
         for (int tt = 0; tt < DC; ++tt)
 #pragma unroll
           for (int gq = 0; gq < 4; ++gq) {
+            float vsc[4] = {1.f, 1.f, 1.f, 1.f};
+            if constexpr (W8) {
+              const float4 v4 = *reinterpret_cast<const float4*>(a.vs + bkv * D + 32 * tt + 8 * gq + 4 * h);
+              vsc[0] = v4.x; vsc[1] = v4.y; vsc[2] = v4.z; vsc[3] = v4.w;
+            }
             uint16_t hv[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              const float xo = oacc[g][tt][4 * gq + e] * inv;
-              hv[e] = (VDT == SL8_DTYPE_F16) ? f2h_bits(xo) : f2bf_bits(xo);
+              const float xo = oacc[g][tt][4 * gq + e] * inv * vsc[e];
+              hv[e] = (W8 || VDT == SL8_DTYPE_F16) ? f2h_bits(xo) : f2bf_bits(xo);  // W8A8 out: fp16
             }
             uint2 pk;
             pk.x = hv[0] | ((uint32_t)hv[1] << 16);
@@ -846,14 +956,15 @@ constexpr int WIDE_NG = SL8_FWD_NG;
 #ifndef SL8_FWD_WV64
 #define SL8_FWD_WV64 4
 #endif
-constexpr int wide_waves(int64_t D) { return D == 128 ? SL8_FWD_WV128 : SL8_FWD_WV64; }
+// (D = 256 keeps 4: one wave per SIMD, whose O needs the whole register file)
+constexpr int wide_waves(int64_t D) { return D == 128 ? SL8_FWD_WV128 : (D == 64 ? SL8_FWD_WV64 : 4); }
 // queries per workgroup
 constexpr int wide_bm(int64_t D) { return wide_waves(D) * 32 * WIDE_NG; }
 
-template <int D, bool CAUSAL, int VDT, bool LSE>
+template <int D, bool CAUSAL, int VDT, bool LSE, bool W8 = false>
 void launch_wide(const FwdArgs& a, int grid, hipStream_t st) {
   constexpr int WV = wide_waves(D);
-  attn_fwd_wide_kernel<D, CAUSAL, VDT, LSE, WIDE_NG, WV><<<grid, WV * 64, 0, st>>>(a);
+  attn_fwd_wide_kernel<D, CAUSAL, VDT, LSE, WIDE_NG, WV, W8><<<grid, WV * 64, 0, st>>>(a);
 }
 
 template <int D, int VDT>
@@ -889,10 +1000,10 @@ int launch_transpose(const void* v, uint16_t* vt, int64_t BHkv, int64_t N, int64
                      hipStream_t st) {
   const int64_t npad = npad_of(N);
   const dim3 grid((unsigned)(npad / BN), (unsigned)BHkv);
-  if (D == 64)
-    v_transpose_kernel<64><<<grid, 256, 0, st>>>(static_cast<const uint16_t*>(v), vt, (int)N, (int)npad);
-  else
-    v_transpose_kernel<128><<<grid, 256, 0, st>>>(static_cast<const uint16_t*>(v), vt, (int)N, (int)npad);
+  const uint16_t* v16 = static_cast<const uint16_t*>(v);
+  if (D == 64) v_transpose_kernel<64><<<grid, 256, 0, st>>>(v16, vt, (int)N, (int)npad);
+  else if (D == 128) v_transpose_kernel<128><<<grid, 256, 0, st>>>(v16, vt, (int)N, (int)npad);
+  else v_transpose_kernel<256><<<grid, 256, 0, st>>>(v16, vt, (int)N, (int)npad);
   SL8_CHECK_LAUNCH("attn_int8_fwd v transpose");
   return SL8_OK;
 }
@@ -900,7 +1011,8 @@ int launch_transpose(const void* v, uint16_t* vt, int64_t BHkv, int64_t N, int64
 int check_fwd_shape(int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N, int64_t D) {
   SL8_CHECK_ARG(B >= 0 && Hq >= 0 && Hkv > 0 && M >= 0 && N >= 0, "fni8: bad shape");
   SL8_CHECK_ARG(Hq % Hkv == 0, "fni8: H_q must be divisible by H_kv (GQA)");
-  SL8_CHECK_ARG(D == 64 || D == 128, "fni8: head dim must be 64/128, got %lld", (long long)D);
+  SL8_CHECK_ARG(D == 64 || D == 128 || D == 256, "fni8: head dim must be 64/128/256, got %lld",
+                (long long)D);
   SL8_CHECK_ARG(M < (1 << 30) && N < (1 << 30) && B * Hq < (1 << 24), "fni8: shape too large");
   return SL8_OK;
 }
@@ -914,12 +1026,58 @@ FwdArgs make_args(int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N, int&
   a.Hkv = (int)Hkv;
   a.nqb = (int)((M + BM - 1) / BM);
   a.window_left = -1;
+  a.diag = (int)(N - M);
   grid = (int)(B * Hq * a.nqb);  // causal kernels halve this (paired query blocks)
   a.xcd_map = xcd_mode(B * Hkv, Hq / Hkv, a.nqb);  // non-causal slot count
   return a;
 }
 
 }  // namespace
+
+// W8A8 prefill with per-warp P quantisation on the production pipeline
+// (called from attn_w8a8.hip). v: int8 [B*Hkv][N][D]; vt_ws: bf16 V^T
+// workspace of w8a8_wide_workspace() bytes.
+size_t w8a8_wide_workspace(int64_t B, int64_t Hkv, int64_t N, int64_t D) {
+  return (size_t)(B * Hkv * D * npad_of(N)) * sizeof(uint16_t);
+}
+
+int w8a8_wide_launch(const int8_t* q, const float* q_scale, const int8_t* k, const float* k_scale,
+                     const int8_t* v, const float* v_scale, void* out, int64_t B, int64_t Hq,
+                     int64_t Hkv, int64_t M, int64_t N, int64_t D, bool causal, int64_t causal_diag,
+                     void* vt_ws, hipStream_t st) {
+  const int64_t npad = npad_of(N);
+  uint16_t* vt = static_cast<uint16_t*>(vt_ws);
+  if (N > 0) {
+    const dim3 tg((unsigned)(npad / BN), (unsigned)(B * Hkv));
+    if (D == 64) v8_to_bf16_transpose_kernel<64><<<tg, 256, 0, st>>>(v, vt, (int)N, (int)npad);
+    else if (D == 128) v8_to_bf16_transpose_kernel<128><<<tg, 256, 0, st>>>(v, vt, (int)N, (int)npad);
+    else v8_to_bf16_transpose_kernel<256><<<tg, 256, 0, st>>>(v, vt, (int)N, (int)npad);
+    SL8_CHECK_LAUNCH("attn_w8a8_fwd v transpose");
+  }
+  int grid;
+  FwdArgs a = make_args(B, Hq, Hkv, M, N, grid);
+  a.q = q; a.qs = q_scale; a.k = k; a.ks = k_scale;
+  a.vt = vt; a.vs = v_scale; a.out = out; a.lse = nullptr;
+  a.diag = (int)causal_diag;
+  a.nqb = (int)((M + wide_bm(D) - 1) / wide_bm(D));
+  const int nslot = causal ? (a.nqb + 1) / 2 : a.nqb;
+  grid = (int)(B * Hq * nslot);
+  a.xcd_map = xcd_mode(B * Hkv, Hq / Hkv, nslot);
+  constexpr int F = SL8_DTYPE_BF16;
+  if (D == 64) {
+    if (causal) launch_wide<64, true, F, false, true>(a, grid, st);
+    else launch_wide<64, false, F, false, true>(a, grid, st);
+  } else if (D == 128) {
+    if (causal) launch_wide<128, true, F, false, true>(a, grid, st);
+    else launch_wide<128, false, F, false, true>(a, grid, st);
+  } else {
+    if (causal) launch_wide<256, true, F, false, true>(a, grid, st);
+    else launch_wide<256, false, F, false, true>(a, grid, st);
+  }
+  SL8_CHECK_LAUNCH("attn_w8a8_fwd");
+  return SL8_OK;
+}
+
 }  // namespace sl8
 
 using namespace sl8;
@@ -962,12 +1120,16 @@ extern "C" int sl8_attn_int8_fwd(const int8_t* q, const float* q_scale, const in
   const int nslot = c ? (a.nqb + 1) / 2 : a.nqb;
   grid = (int)(B * Hq * nslot);
   a.xcd_map = xcd_mode(B * Hkv, Hq / Hkv, nslot);
+  const bool f16 = v_dtype == SL8_DTYPE_F16;
   if (D == 64) {
-    if (v_dtype == SL8_DTYPE_F16) dispatch_wide<64, SL8_DTYPE_F16>(a, grid, c, want_lse, st);
+    if (f16) dispatch_wide<64, SL8_DTYPE_F16>(a, grid, c, want_lse, st);
     else dispatch_wide<64, SL8_DTYPE_BF16>(a, grid, c, want_lse, st);
-  } else {
-    if (v_dtype == SL8_DTYPE_F16) dispatch_wide<128, SL8_DTYPE_F16>(a, grid, c, want_lse, st);
+  } else if (D == 128) {
+    if (f16) dispatch_wide<128, SL8_DTYPE_F16>(a, grid, c, want_lse, st);
     else dispatch_wide<128, SL8_DTYPE_BF16>(a, grid, c, want_lse, st);
+  } else {
+    if (f16) dispatch_wide<256, SL8_DTYPE_F16>(a, grid, c, want_lse, st);
+    else dispatch_wide<256, SL8_DTYPE_BF16>(a, grid, c, want_lse, st);
   }
   SL8_CHECK_LAUNCH("attn_int8_fwd");
   return SL8_OK;
@@ -979,6 +1141,7 @@ extern "C" int sl8_attn_int8_qk_scores(const int8_t* q, const int8_t* k, int32_t
   clear_error();
   int rc = check_fwd_shape(B, Hq, Hkv, M, N, D);
   if (rc) return rc;
+  SL8_CHECK_ARG(D != 256, "fni8: qk_scores supports head dim 64/128");
   if (B == 0 || Hq == 0 || M == 0 || N == 0) return SL8_OK;
   SL8_CHECK_ARG(q && k && scores, "fni8: null pointer");
   SL8_CHECK_ARG(aligned(q, 16) && aligned(k, 16), "fni8: q/k must be 16-byte aligned");

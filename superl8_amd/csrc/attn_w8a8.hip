@@ -1,5 +1,11 @@
-// Full-W8A8 prefill attention for gfx950: int8 Q.K^T and int8 P.V, both on
-// the int8 MFMA (v_mfma_i32_32x32x32_i8).
+// Full-W8A8 prefill attention for gfx950.
+//
+// per_warp_quant (the reference default) runs on the prefill pipeline of
+// attn_fwd.hip (attn_fwd_wide_kernel, W8 = true): int8 Q.K^T on the int8
+// MFMA, P codes re-quantised per 32-key half and fed to the bf16 MFMA as
+// code * per-row factor against int8 V held exactly in bf16 (w8a8_wide_launch).
+// This file holds the per-tile variant (per_warp_quant = false): int8 Q.K^T
+// and int8 P.V, both on the int8 MFMA (v_mfma_i32_32x32x32_i8).
 //
 // Semantics follow the reference (csrc/include/attn_w8a8_fwd.cuh:30-235):
 //   logits and the online softmax as attn_int8_fwd, over 64-key tiles, with
@@ -323,13 +329,25 @@ void launch_w8_d(const W8Args& a, int grid, bool causal, bool per_warp, hipStrea
 }
 
 }  // namespace
+
+// per-warp quantisation runs on the prefill pipeline of attn_fwd.hip
+size_t w8a8_wide_workspace(int64_t B, int64_t Hkv, int64_t N, int64_t D);
+int w8a8_wide_launch(const int8_t* q, const float* q_scale, const int8_t* k, const float* k_scale,
+                     const int8_t* v, const float* v_scale, void* out, int64_t B, int64_t Hq,
+                     int64_t Hkv, int64_t M, int64_t N, int64_t D, bool causal, int64_t causal_diag,
+                     void* vt_ws, hipStream_t st);
+
 }  // namespace sl8
 
 using namespace sl8;
 
 extern "C" size_t sl8_attn_w8a8_fwd_workspace(int64_t B, int64_t Hkv, int64_t N, int64_t D) {
   if (B <= 0 || Hkv <= 0 || N <= 0 || D <= 0) return 0;
-  return (size_t)(B * Hkv * D * npad8(N));
+  // the larger of the two layouts: fp16 V^T (per-warp quantisation) and the
+  // int8 V^T of the per-tile kernel
+  const size_t i8 = (size_t)(B * Hkv * D * npad8(N));
+  const size_t f16 = w8a8_wide_workspace(B, Hkv, N, D);
+  return f16 > i8 ? f16 : i8;
 }
 
 extern "C" int sl8_attn_w8a8_fwd(const int8_t* q, const float* q_scale, const int8_t* k,
@@ -355,6 +373,9 @@ extern "C" int sl8_attn_w8a8_fwd(const int8_t* q, const float* q_scale, const in
   SL8_CHECK_ARG(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 16)),
                 "fni8: attn_w8a8_fwd workspace needs %zu bytes", need);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (per_warp_quant)
+    return w8a8_wide_launch(q, q_scale, k, k_scale, v, v_scale, out, B, Hq, Hkv, M, N, D,
+                            causal != 0, causal_diag, workspace, st);
   const int64_t Npad = npad8(N);
   if (N > 0) {
     const dim3 g((unsigned)(Npad / WBN), (unsigned)(B * Hkv));

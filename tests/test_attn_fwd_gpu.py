@@ -67,6 +67,8 @@ KERNEL_CASES = [
     (1, 2, 2, 64, 64, 128, False, 16),      # window without causal
     (1, 2, 1, 5, 9, 64, True, 0),           # window 0: every row fully masked
     (1, 2, 2, 300, 40, 64, True, -1),       # M > N: leading rows see nothing
+    (1, 2, 1, 200, 200, 256, True, -1),     # head dim 256 (one wave per SIMD)
+    (1, 2, 2, 70, 90, 256, False, 20),
 ]
 
 

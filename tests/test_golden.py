@@ -56,7 +56,9 @@ def test_kernels_reproduce_fixtures(device):
     qs2, ks2 = qs.squeeze(-1).contiguous(), ks.squeeze(-1).contiguous()
     out, lse = _C.attn_int8_fwd_train(q_i8, qs2, k_i8, ks2, t(a["v"]), True)
     assert_close_abs(out, a["out_causal"], atol=1e-2, what="golden prefill causal")
-    np.testing.assert_allclose(lse.cpu().numpy(), a["lse_causal"], rtol=1e-5, atol=1e-5)
+    # the kernel's row sums add the fp16-rounded P that enters the PV product
+    # (2^-11 relative per term), as test_attn_fwd_gpu's LSE checks
+    np.testing.assert_allclose(lse.cpu().numpy(), a["lse_causal"], rtol=0, atol=5e-4)
     out = _C.attn_int8_fwd(q_i8, qs2, k_i8, ks2, t(a["v"]), False)
     assert_close_abs(out, a["out_full"], atol=1e-2, what="golden prefill")
     v_i8, vs = _C.quantize_v_perchannel(t(a["v"]))
