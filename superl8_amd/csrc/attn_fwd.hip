@@ -959,12 +959,16 @@ constexpr int WIDE_NG = SL8_FWD_NG;
 // (D = 256 keeps 4: one wave per SIMD, whose O needs the whole register file)
 constexpr int wide_waves(int64_t D) { return D == 128 ? SL8_FWD_WV128 : (D == 64 ? SL8_FWD_WV64 : 4); }
 // queries per workgroup
-constexpr int wide_bm(int64_t D) { return wide_waves(D) * 32 * WIDE_NG; }
+#ifndef SL8_FWD_NG256
+#define SL8_FWD_NG256 1
+#endif
+constexpr int wide_ng(int64_t D) { return D == 256 ? SL8_FWD_NG256 : WIDE_NG; }
+constexpr int wide_bm(int64_t D) { return wide_waves(D) * 32 * wide_ng(D); }
 
 template <int D, bool CAUSAL, int VDT, bool LSE, bool W8 = false>
 void launch_wide(const FwdArgs& a, int grid, hipStream_t st) {
   constexpr int WV = wide_waves(D);
-  attn_fwd_wide_kernel<D, CAUSAL, VDT, LSE, WIDE_NG, WV, W8><<<grid, WV * 64, 0, st>>>(a);
+  attn_fwd_wide_kernel<D, CAUSAL, VDT, LSE, wide_ng(D), WV, W8><<<grid, WV * 64, 0, st>>>(a);
 }
 
 template <int D, int VDT>

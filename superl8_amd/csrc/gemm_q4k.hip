@@ -233,7 +233,10 @@ gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
 }
 
 // ---------------------------------------------------------------------------
-// M <= 2: the same workgroup/K split, but the dot products run on VALU
+// M <= 2: 16 weight rows per workgroup like the kernel above, with K split
+// over SWAVES = 8 waves of up to SCH = 3 super-blocks (half the per-wave
+// work of a 4-way split: the compute left after the last loads land is
+// shorter), and the dot products run on VALU
 // v_dot4 in the load layout itself -- lane 4r + c owns 16-byte piece c of
 // each 64-byte half of weight row r, i.e. elements 16(c&1)..+15 of
 // sub-blocks j = 2(c>>1) (low nibbles) and j+1 (high nibbles) of that half
@@ -248,14 +251,23 @@ __device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, R * 0x55, 0xF, 0xF, false);
 }
 
+#ifndef SL8_GEMV_SWAVES
+#define SL8_GEMV_SWAVES 8
+#endif
+#ifndef SL8_GEMV_SCH
+#define SL8_GEMV_SCH 3
+#endif
+constexpr int SWAVES = SL8_GEMV_SWAVES;  // K split of the M <= 2 kernel
+constexpr int SCH = SL8_GEMV_SCH;        // its super-blocks per wave and chunk
+constexpr int SXPITCH = SCH * 256;
 template <int OUT_DT, int MR>
-__global__ void __launch_bounds__(64 * GWAVES)
+__global__ void __launch_bounds__(64 * SWAVES)
 gemv_q4k_small_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
                       const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K) {
-  constexpr int XC = (MR * GXPITCH + 1023) / 1024;  // 16-byte activation pieces per lane
-  __shared__ __attribute__((aligned(16))) int8_t xs_l[GWAVES][XC * 1024];
-  __shared__ __attribute__((aligned(16))) int xsum_l[GWAVES][MR][GCH][2][8];  // [m][i][half][j]
-  __shared__ float red[GWAVES - 1][16][MR];
+  constexpr int XC = (MR * SXPITCH + 1023) / 1024;  // 16-byte activation pieces per lane
+  __shared__ __attribute__((aligned(16))) int8_t xs_l[SWAVES][XC * 1024];
+  __shared__ __attribute__((aligned(16))) int xsum_l[SWAVES][MR][SCH][2][8];  // [m][i][half][j]
+  __shared__ float red[SWAVES - 1][16][MR];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nsb = K >> 8;
@@ -272,11 +284,11 @@ gemv_q4k_small_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_
 
   auto chunk = [&](const int c0, const int cnt) {
     // ---- activations first: M rows x cnt*256 bytes, lane-linear 16-byte pieces ----
-    const int xch = M * (GXPITCH / 16);
+    const int xch = M * (SXPITCH / 16);
     static_assert(XC <= 3, "activation pieces per lane");
     auto xload = [&](int j) -> uint4 {
       const int id = min(j * 64 + lane, xch - 1);
-      const int m = id / (GXPITCH / 16), pos = min(id % (GXPITCH / 16), cnt * 16 - 1);
+      const int m = id / (SXPITCH / 16), pos = min(id % (SXPITCH / 16), cnt * 16 - 1);
       return *reinterpret_cast<const uint4*>(x + (int64_t)m * K + (int64_t)c0 * 256 + 16 * pos);
     };
     const uint4 xq0 = xload(0);
@@ -286,27 +298,27 @@ gemv_q4k_small_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_
     // ---- then every weight load of the chunk ----
     // (two per-lane base pointers plus immediate offsets; a partial chunk
     // re-reads its last super-block instead of running past the row)
-    uint32_t hd[GCH];
-    uint4 qa[GCH], qb[GCH];
+    uint32_t hd[SCH];
+    uint4 qa[SCH], qb[SCH];
     const uint8_t* bh = wrow + (int64_t)c0 * Q4K_BYTES + 4 * c;
     const uint8_t* bq = wrow + (int64_t)c0 * Q4K_BYTES + 16 * c;
 #pragma unroll
-    for (int i = 0; i < GCH; ++i) {
-      const int ii = cnt == GCH ? i : min(i, cnt - 1);
+    for (int i = 0; i < SCH; ++i) {
+      const int ii = cnt == SCH ? i : min(i, cnt - 1);
       hd[i] = *reinterpret_cast<const uint32_t*>(bh + ii * Q4K_BYTES);
       qa[i] = *reinterpret_cast<const uint4*>(bq + ii * Q4K_BYTES + 16);
       qb[i] = *reinterpret_cast<const uint4*>(bq + ii * Q4K_BYTES + 80);
     }
     __builtin_amdgcn_sched_barrier(0);
-    // ---- activations to LDS ([m][GXPITCH]) and their 16-element sums ----
+    // ---- activations to LDS ([m][SXPITCH]) and their 16-element sums ----
     *reinterpret_cast<uint4*>(xw + 16 * lane) = xq0;
     if (XC > 1) *reinterpret_cast<uint4*>(xw + 1024 + 16 * lane) = xq1;
     if (XC > 2) *reinterpret_cast<uint4*>(xw + 2048 + 16 * lane) = xq2;
     __builtin_amdgcn_wave_barrier();
     // sum over elements 16*half2..+15 of sub-block j2 of super-block i2, row m2
-    for (int e = lane; e < MR * GCH * 16; e += 64) {
-      const int m2 = e / (GCH * 16), i2 = (e / 16) % GCH, half2 = (e / 8) & 1, j2 = e & 7;
-      const int4 v = *reinterpret_cast<const int4*>(xw + m2 * GXPITCH + i2 * 256 + 32 * j2 + 16 * half2);
+    for (int e = lane; e < MR * SCH * 16; e += 64) {
+      const int m2 = e / (SCH * 16), i2 = (e / 16) % SCH, half2 = (e / 8) & 1, j2 = e & 7;
+      const int4 v = *reinterpret_cast<const int4*>(xw + m2 * SXPITCH + i2 * 256 + 32 * j2 + 16 * half2);
       int sacc = __builtin_amdgcn_sdot4(v.x, 0x01010101, 0, false);
       sacc = __builtin_amdgcn_sdot4(v.y, 0x01010101, sacc, false);
       sacc = __builtin_amdgcn_sdot4(v.z, 0x01010101, sacc, false);
@@ -315,7 +327,7 @@ gemv_q4k_small_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_
     }
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int i = 0; i < GCH; ++i) {
+    for (int i = 0; i < SCH; ++i) {
       if (i < cnt) {
         // header dwords of row r, from the quad's lanes 4r .. 4r+3
         const uint32_t h0 = quad_bcast<0>(hd[i]), h1 = quad_bcast<1>(hd[i]);
@@ -332,7 +344,7 @@ gemv_q4k_small_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_
         const float d = h2f(h0 & 0xFFFFu), dmin = h2f(h0 >> 16);
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
-          const int8_t* xb = xw + m * GXPITCH + i * 256 + 16 * half;
+          const int8_t* xb = xw + m * SXPITCH + i * 256 + 16 * half;
           const int4 x0 = *reinterpret_cast<const int4*>(xb + 32 * (2 * g));
           const int4 x1 = *reinterpret_cast<const int4*>(xb + 32 * (2 * g + 1));
           const int4 x4 = *reinterpret_cast<const int4*>(xb + 32 * (2 * g + 4));
@@ -360,11 +372,11 @@ gemv_q4k_small_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_
     __builtin_amdgcn_wave_barrier();  // the next chunk rewrites xw / xsum_l
   };
 
-  const int sb0 = (wave * nsb) / GWAVES, sb1 = ((wave + 1) * nsb) / GWAVES;  // may be empty
-  if (sb1 - sb0 == GCH) {
-    chunk(sb0, GCH);  // the decode shapes: one full chunk, immediate offsets
+  const int sb0 = (wave * nsb) / SWAVES, sb1 = ((wave + 1) * nsb) / SWAVES;  // may be empty
+  if (sb1 - sb0 == SCH) {
+    chunk(sb0, SCH);  // the decode shapes: one full chunk, immediate offsets
   } else {
-    for (int c0 = sb0; c0 < sb1; c0 += GCH) chunk(c0, min(GCH, sb1 - c0));
+    for (int c0 = sb0; c0 < sb1; c0 += SCH) chunk(c0, min(SCH, sb1 - c0));
   }
 
   // quad sum (the 4 pieces of a row), then the K quarters in fixed order
@@ -383,7 +395,7 @@ gemv_q4k_small_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_
     for (int m = 0; m < MR; ++m) {
       float v = f[m];
 #pragma unroll
-      for (int wv = 0; wv < GWAVES - 1; ++wv) v += red[wv][r][m];
+      for (int wv = 0; wv < SWAVES - 1; ++wv) v += red[wv][r][m];
       const int gn = n0 + r;
       if (m < M && gn < N) st_out<OUT_DT>(out, (int64_t)m * N + gn, v * x_scale[m]);
     }
@@ -418,13 +430,13 @@ void launch_gemv_small(const int8_t* x, const float* xs, const uint8_t* w, void*
   const dim3 grid((unsigned)((N + GEMV_ROWS - 1) / GEMV_ROWS));
   switch (odt) {
     case SL8_DTYPE_F16:
-      gemv_q4k_small_kernel<SL8_DTYPE_F16, MR><<<grid, 64 * GWAVES, 0, st>>>(x, xs, w, out, M, N, K);
+      gemv_q4k_small_kernel<SL8_DTYPE_F16, MR><<<grid, 64 * SWAVES, 0, st>>>(x, xs, w, out, M, N, K);
       break;
     case SL8_DTYPE_BF16:
-      gemv_q4k_small_kernel<SL8_DTYPE_BF16, MR><<<grid, 64 * GWAVES, 0, st>>>(x, xs, w, out, M, N, K);
+      gemv_q4k_small_kernel<SL8_DTYPE_BF16, MR><<<grid, 64 * SWAVES, 0, st>>>(x, xs, w, out, M, N, K);
       break;
     default:
-      gemv_q4k_small_kernel<SL8_DTYPE_F32, MR><<<grid, 64 * GWAVES, 0, st>>>(x, xs, w, out, M, N, K);
+      gemv_q4k_small_kernel<SL8_DTYPE_F32, MR><<<grid, 64 * SWAVES, 0, st>>>(x, xs, w, out, M, N, K);
       break;
   }
 }
