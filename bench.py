@@ -113,6 +113,35 @@ def bench_decode(iters=20):
     return ms, nbytes
 
 
+def bench_decode_kv8(iters=20):
+    """Decode over an int8 V cache (per-channel scale) at config 3's shape: K and V
+    int8 [16, 8, 32768, 128], the row of reference attn_int8_decode_kv8 (survey next)."""
+    from superl8_amd import _C
+
+    dev = "cuda"
+    B, Hq, Hkv, N, D = 16, 32, 8, 32768, 128
+    g = torch.Generator(device=dev).manual_seed(7)
+    q = torch.randn(B * Hq, D, device=dev, dtype=torch.float16, generator=g)
+    k = torch.randn(B * Hkv * N, D, device=dev, dtype=torch.float16, generator=g)
+    q_i8, qs = _C.quantize_i8_rowwise(q)
+    k_i8, ks = _C.quantize_i8_rowwise(k)
+    del k
+    q_i8 = q_i8.reshape(B, Hq, 1, D)
+    qs = (qs * (1.0 / np.sqrt(D) * np.log2(np.e))).reshape(B, Hq, 1).contiguous()
+    k_i8 = k_i8.reshape(B, Hkv, N, D)
+    ks = ks.reshape(B, Hkv, N)
+    v = torch.randn(B, Hkv, N, D, device=dev, dtype=torch.float16, generator=g)
+    v_i8, vs = _C.quantize_v_perchannel(v)
+    del v
+    vs = vs.reshape(B, Hkv, D).contiguous()
+    fn = lambda: _C.attn_int8_decode_kv8(q_i8, qs, k_i8, ks, v_i8, vs, 16)  # noqa: E731
+    spin_up(fn, 0.2)
+    ms = _events_time(fn, iters, torch.cuda.current_stream())
+    nbytes = k_i8.numel() + ks.numel() * 4 + v_i8.numel() + vs.numel() * 4 + q_i8.numel() \
+        + qs.numel() * 4 + B * Hq * D * 2
+    return ms, nbytes
+
+
 def bench_w8a8(iters=5):
     """Full-W8A8 prefill at BASELINE config 5: Q/K/V [2, 16|2, 8192, 256], causal,
     1% of Q/K channels (3 of 256, fixed) scaled by 20, V per-channel int8."""
@@ -275,6 +304,11 @@ def main():
         sec["attn_int8_decode_cfg3"] = {"us": round(dms * 1e3, 2), "GB/s": round(gbs, 1),
                                         "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
                                         "bytes": dbytes}
+        kms, kbytes = bench_decode_kv8()
+        gbs = kbytes / (kms * 1e-3) / 1e9
+        sec["attn_int8_decode_kv8_cfg3shape"] = {"us": round(kms * 1e3, 2), "GB/s": round(gbs, 1),
+                                                 "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+                                                 "bytes": kbytes}
         for M in (1, 8):
             gms, gbytes = bench_gemv(M)
             gbs = gbytes / (gms * 1e-3) / 1e9

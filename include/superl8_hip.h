@@ -151,6 +151,17 @@ int sl8_attn_int8_decode(const int8_t* q, const float* q_scale, const int8_t* k,
                          int64_t num_splits, void* workspace, size_t workspace_bytes,
                          void* stream);
 
+/* Split-KV decode over an int8 V cache: v int8 [B,Hkv,N,D] with per-channel
+ * v_scale fp32 [B,Hkv,D], folded into each split's partial O. Otherwise as
+ * sl8_attn_int8_decode (same workspace). Replaces _C.attn_int8_decode_kv8
+ * (reference csrc/fni8_api.cpp:37-39,264-266, csrc/kernel/attn_decode.cu:100-118,242-320,
+ * csrc/include/attn_decode.cuh:141-224). */
+int sl8_attn_int8_decode_kv8(const int8_t* q, const float* q_scale, const int8_t* k,
+                             const float* k_scale, const int8_t* v, const float* v_scale,
+                             void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                             int64_t num_splits, void* workspace, size_t workspace_bytes,
+                             void* stream);
+
 /* ------------------------------------------------------------------------
  * Q4_K GEMM/GEMV over native GGUF super-blocks (144 B per 256 weights:
  * fp16 d, fp16 dmin, 12 B packed 6-bit sub-scales/mins, 128 B nibbles).

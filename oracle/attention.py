@@ -10,6 +10,9 @@ Reference kernels restated:
   csrc/include/attn_decode.cuh:47-132,430-466 (split s owns keys
       [s*per, min(N,(s+1)*per)), per = ceil(N/ns); partial (O, m, l);
       empty split -> m = -1e30; LSE merge)
+  csrc/include/attn_decode.cuh:141-224 (int8 V cache: O accumulates
+      p * v_i8 and each split's partial O is multiplied by the per-channel
+      v_scale[d] of its KV head before the merge)
 
 Softmax and PV are evaluated in float64 here (the reference keeps fp32 state);
 the kernels are checked against this within stated tolerances, while the
@@ -143,6 +146,39 @@ def attn_int8_decode(q_i8, q_scale, k_i8, k_scale, v, num_splits):
         p = np.exp2(s - m[..., None])
         parts.append((np.einsum("bhn,bhnd->bhd", p, vv[:, :, n0:n1]), m, p.sum(-1)))
     gm = np.max([pm for _, pm, _ in parts], axis=0)
+    num = np.zeros((B, Hq, D))
+    den = np.zeros((B, Hq))
+    for o, m, l in parts:
+        w = np.where(m == DEC_NEG_INF, 0.0, np.exp2(m - gm))
+        num += o * w[..., None]
+        den += l * w
+    return np.where(den[..., None] > 0, num / np.where(den > 0, den, 1.0)[..., None], 0.0)
+
+
+def attn_int8_decode_kv8(q_i8, q_scale, k_i8, k_scale, v_i8, v_scale, num_splits):
+    """Split-KV decode over an int8 V cache with per-channel scale v_scale [B,Hkv,D]
+    (reference attn_decode.cuh:141-224): per split, O = (sum_n p_n * v_i8[n]) *
+    v_scale[d], then the same LSE merge as attn_int8_decode."""
+    B, Hq, D = q_i8.shape
+    N = k_i8.shape[2]
+    idx = kv_head_index(Hq, v_i8.shape[1])
+    s_all = logits(scores_i32(q_i8[:, :, None, :], k_i8), q_scale[..., None], k_scale, Hq)[:, :, 0, :]
+    vv = v_i8[:, idx].astype(np.float64)
+    vs = v_scale[:, idx].astype(np.float64)  # [B,Hq,D]
+    per = (N + num_splits - 1) // num_splits
+    gm = np.full((B, Hq), DEC_NEG_INF)
+    parts = []
+    for sp in range(num_splits):
+        n0, n1 = sp * per, min(N, (sp + 1) * per)
+        if n1 <= n0:
+            parts.append((np.zeros((B, Hq, D)), np.full((B, Hq), DEC_NEG_INF), np.zeros((B, Hq))))
+            continue
+        s = s_all[..., n0:n1].astype(np.float64)
+        m = s.max(-1)
+        p = np.exp2(s - m[..., None])
+        o = np.einsum("bhn,bhnd->bhd", p, vv[:, :, n0:n1]) * vs
+        parts.append((o, m, p.sum(-1)))
+        gm = np.maximum(gm, m)
     num = np.zeros((B, Hq, D))
     den = np.zeros((B, Hq))
     for o, m, l in parts:

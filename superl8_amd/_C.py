@@ -258,6 +258,46 @@ def attn_int8_decode(q, q_scale, k, k_scale, v, num_splits=-1):
     return out
 
 
+def attn_int8_decode_kv8(q, q_scale, k, k_scale, v, v_scale, num_splits=-1):
+    """Decode over an int8 K/V cache (reference csrc/kernel/attn_decode.cu:245-320):
+    q int8 [B,Hq,1,D], q_scale fp32 [B,Hq,1], k int8 [B,Hkv,N,D], k_scale fp32 [B,Hkv,N],
+    v int8 [B,Hkv,N,D], v_scale fp32 [B,Hkv,D] (per channel) -> fp16 [B,Hq,1,D]."""
+    _on_gpu(q, q_scale, k, k_scale, v, v_scale)
+    _check(q.dtype == torch.int8 and k.dtype == torch.int8 and v.dtype == torch.int8,
+           "decode_kv8: q/k/v must be int8")
+    _check(q_scale.dtype == torch.float32 and k_scale.dtype == torch.float32 and
+           v_scale.dtype == torch.float32, "decode_kv8: scales must be float32")
+    _check(q.dim() == 4 and k.dim() == 4 and v.dim() == 4, "decode_kv8: expect [B,H,S,D]")
+    _check(q.shape[2] == 1, "decode_kv8: query length M must be 1 (decode)")
+    _contig(q, q_scale, k, k_scale, v, v_scale)
+    B, H, _, D = q.shape
+    Hkv, N = k.shape[1], k.shape[2]
+    _check(k.shape[0] == B and v.shape[0] == B and v.shape[1] == Hkv,
+           "decode_kv8: batch/head mismatch")
+    _check(Hkv > 0 and H % Hkv == 0, "decode_kv8: H_q must be divisible by H_kv (GQA)")
+    _check(k.shape[3] == D and v.shape[3] == D and v.shape[2] == N, "decode_kv8: K/V shape mismatch")
+    _check(q_scale.numel() == B * H and k_scale.numel() == B * Hkv * N and
+           v_scale.numel() == B * Hkv * D, "decode_kv8: scale shape mismatch")
+    _check(D in _HEAD_DIMS_DECODE, f"decode_kv8: head dim must be one of {_HEAD_DIMS_DECODE}, got {D}")
+    num_splits = int(num_splits)
+    _check(num_splits != 0,
+           f"decode_kv8: num_splits=0 is invalid; use -1 for auto or 1..{DEC_MAX_SPLITS}")
+    out = torch.empty((B, H, 1, D), device=q.device, dtype=torch.float16)
+    if B == 0 or H == 0:
+        return out
+    if N == 0:
+        return out.zero_()
+    ns = choose_n_splits(N, B, Hkv) if num_splits < 0 else num_splits
+    _check(1 <= ns <= DEC_MAX_SPLITS, f"decode_kv8: num_splits must be 1..{DEC_MAX_SPLITS}, got {ns}")
+    ws_bytes = _lib.load().sl8_attn_int8_decode_workspace(B, H, D, ns)
+    ws = torch.empty((ws_bytes,), device=q.device, dtype=torch.uint8)
+    with torch.cuda.device(q.device):
+        call("sl8_attn_int8_decode_kv8", q.data_ptr(), q_scale.data_ptr(), k.data_ptr(),
+             k_scale.data_ptr(), v.data_ptr(), v_scale.data_ptr(), out.data_ptr(), B, H, Hkv, N,
+             D, ns, ws.data_ptr(), ws_bytes, stream_of(q))
+    return out
+
+
 # ---------------------------------------------------------------------------
 # Q4_K (reference csrc/kernel/gemm_dp4a.cu:146-193, gemm_decode_dp4a.cu:375-436)
 # ---------------------------------------------------------------------------

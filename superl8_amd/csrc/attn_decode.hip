@@ -43,11 +43,14 @@ struct DecSmem {
   float o[DEC_WAVES][G][D];
 };
 
-template <int D, int G>
+// VI8: V is the int8 cache [B,Hkv,N,D] with per-channel scale vsc [B,Hkv,D]
+// (reference attn_decode.cuh:141-224), folded into the partial O.
+template <int D, int G, bool VI8>
 __global__ void __launch_bounds__(DEC_THREADS)
 decode_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_scale,
                     const int8_t* __restrict__ k, const float* __restrict__ k_scale,
-                    const uint16_t* __restrict__ v, float* __restrict__ o_part,
+                    const void* __restrict__ v, const float* __restrict__ vsc,
+                    float* __restrict__ o_part,
                     float* __restrict__ m_part, float* __restrict__ l_part, int n_len,
                     int n_splits, int h_q, int h_kv, int gsz, int bhq) {
   constexpr int D4 = D / 4;
@@ -84,7 +87,8 @@ decode_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sc
   const int n1 = min(n_len, n0 + per);
   const int8_t* kb = k + (int64_t)bkv * n_len * D;
   const float* ksb = k_scale + (int64_t)bkv * n_len;
-  const uint16_t* vb = v + (int64_t)bkv * n_len * D;
+  constexpr int VES = VI8 ? 1 : 2;  // V element bytes
+  const uint8_t* vb = static_cast<const uint8_t*>(v) + (int64_t)bkv * n_len * D * VES;
 
   float m_run[G], l_lane[G], oacc[G][8];
 #pragma unroll
@@ -148,12 +152,21 @@ decode_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sc
       const int kk = kph + i * KPH;
       const int nn = t0 + kk;
       if (nn < n1) {
-        const uint4 vv = *reinterpret_cast<const uint4*>(vb + (int64_t)nn * D + dg * 8);
         float vf[8];
-        vf[0] = h2f(vv.x & 0xFFFF); vf[1] = h2f(vv.x >> 16);
-        vf[2] = h2f(vv.y & 0xFFFF); vf[3] = h2f(vv.y >> 16);
-        vf[4] = h2f(vv.z & 0xFFFF); vf[5] = h2f(vv.z >> 16);
-        vf[6] = h2f(vv.w & 0xFFFF); vf[7] = h2f(vv.w >> 16);
+        if constexpr (VI8) {
+          const uint2 vv = *reinterpret_cast<const uint2*>(vb + (int64_t)nn * D + dg * 8);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            vf[e] = (float)(int8_t)(vv.x >> (8 * e));
+            vf[4 + e] = (float)(int8_t)(vv.y >> (8 * e));
+          }
+        } else {
+          const uint4 vv = *reinterpret_cast<const uint4*>(vb + ((int64_t)nn * D + dg * 8) * 2);
+          vf[0] = h2f(vv.x & 0xFFFF); vf[1] = h2f(vv.x >> 16);
+          vf[2] = h2f(vv.y & 0xFFFF); vf[3] = h2f(vv.y >> 16);
+          vf[4] = h2f(vv.z & 0xFFFF); vf[5] = h2f(vv.z >> 16);
+          vf[6] = h2f(vv.w & 0xFFFF); vf[7] = h2f(vv.w >> 16);
+        }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
           const float p = sm.p[wave][kk][g];
@@ -205,7 +218,7 @@ decode_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sc
     }
     const int64_t hq = (int64_t)b * h_q + kvh * gsz + j0 + g;
     const int64_t row = (int64_t)split * bhq + hq;
-    o_part[row * D + d] = acc;
+    o_part[row * D + d] = VI8 ? acc * vsc[(int64_t)bkv * D + d] : acc;
     if (d == 0) {
       m_part[row] = (mm == -INFINITY) ? DEC_NEG_INF : mm;
       l_part[row] = den;
@@ -290,7 +303,7 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-template <int D, int GS>
+template <int D, int GS, bool VI8 = false>
 struct WaveCfg {
   static constexpr int KL = 64 / GS;                  // lanes (keys) per head per sub-block
   static constexpr int SUB = KL >= 16 ? 1 : 16 / KL;  // sub-blocks per tile
@@ -302,21 +315,23 @@ struct WaveCfg {
   // rows that share one 256-byte bank line.
   static constexpr int KSW = KC - 1;
   static constexpr int KSH = D == 64 ? 2 : (D == 128 ? 1 : 0);
-  static constexpr int KBYTES = T * D, VBYTES = 2 * T * D;
+  static constexpr int VRB = VI8 ? D : 2 * D;  // bytes per V row
+  static constexpr int KBYTES = T * D, VBYTES = T * VRB;
   static constexpr int KDMA = KBYTES / 1024, VDMA = VBYTES / 1024;  // 1 KiB copies per wave
   static constexpr int STAGE = KBYTES + VBYTES + 256;               // + k_scale (64 floats)
   static_assert(KDMA >= 1 && KBYTES % 1024 == 0, "tile copy granularity");
   static_assert(CPL % 8 == 0 || CPL == 4, "PV slice: 4 or a multiple of 8 channels");
 };
 
-template <int D, int GS, int NB>
+template <int D, int GS, int NB, bool VI8>
 __global__ void __launch_bounds__(DEC_THREADS)
 decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_scale,
                    const int8_t* __restrict__ k, const float* __restrict__ k_scale,
-                   const uint16_t* __restrict__ v, float* __restrict__ o_part,
+                   const void* __restrict__ v, const float* __restrict__ vsc,
+                   float* __restrict__ o_part,
                    float* __restrict__ m_part, float* __restrict__ l_part, int n_len,
                    int n_splits, int h_q, int h_kv, int bhq) {
-  using C = WaveCfg<D, GS>;
+  using C = WaveCfg<D, GS, VI8>;
   constexpr int KL = C::KL, SUB = C::SUB, T = C::T, CPL = C::CPL, KC = C::KC, KSW = C::KSW;
   constexpr int KSH = C::KSH;
   constexpr int STAGE = C::STAGE;
@@ -346,7 +361,7 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
   const int nt = ntiles > wave ? (ntiles - wave + DEC_WAVES - 1) / DEC_WAVES : 0;  // this wave's
   const int8_t* kb = k + (int64_t)bkv * n_len * D;
   const float* ksb = k_scale + (int64_t)bkv * n_len;
-  const uint16_t* vb = v + (int64_t)bkv * n_len * D;
+  const uint8_t* vb = static_cast<const uint8_t*>(v) + (int64_t)bkv * n_len * C::VRB;
 
   const int h = lane / KL, kl = lane % KL;
   const int64_t hq = (int64_t)b * h_q + (int64_t)kvh * GS + h;
@@ -370,9 +385,9 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
     }
 #pragma unroll
     for (int j = 0; j < C::VDMA; ++j) {
-      const int id = j * 64 + lane, row = id / (D / 8);
+      const int id = j * 64 + lane, row = id / (C::VRB / 16);
       __builtin_amdgcn_global_load_lds(
-          (gptr_t)(vb + (int64_t)min(base + row, n_len - 1) * D + 8 * (id % (D / 8))),
+          (gptr_t)(vb + (int64_t)min(base + row, n_len - 1) * C::VRB + 16 * (id % (C::VRB / 16))),
           (lptr_t)(sb + C::KBYTES + j * 1024), 16, 0, 0);
     }
     // lanes past the tile repeat its keys (same cache lines: no extra traffic)
@@ -426,6 +441,37 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
         constexpr int rr = decltype(rc)::value;
         // P of key u*KL+rr (held by lane h*KL+rr) to every lane of head h
         const float pk = lane_bcast<KL, rr>(p[u]);
+        if constexpr (VI8) {
+          // int8 codes v -> fp16 1024 + (v + 128), exact: flip the sign bit
+          // (u = v + 128 as an unsigned byte) and pair it with the exponent
+          // byte 0x64 (fp16 0x64uu = 1024 + uu); the 1152 * sum(p) offset is
+          // removed once at the end
+          const uint8_t* vrow8 = reinterpret_cast<const uint8_t*>(vt) + (u * KL + rr) * D + kl * CPL;
+          uint32_t vw[CPL / 4];
+          if constexpr (CPL % 16 == 0) {
+#pragma unroll
+            for (int c16 = 0; c16 < CPL; c16 += 16) {
+              const uint4 x = *reinterpret_cast<const uint4*>(vrow8 + c16);
+              vw[c16 / 4] = x.x; vw[c16 / 4 + 1] = x.y; vw[c16 / 4 + 2] = x.z; vw[c16 / 4 + 3] = x.w;
+            }
+          } else if constexpr (CPL == 8) {
+            const uint2 x = *reinterpret_cast<const uint2*>(vrow8);
+            vw[0] = x.x; vw[1] = x.y;
+          } else {
+            vw[0] = *reinterpret_cast<const uint32_t*>(vrow8);
+          }
+#pragma unroll
+          for (int c = 0; c < CPL / 4; ++c) {
+            const uint32_t w = vw[c] ^ 0x80808080u;
+            const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, w, 0x04010400u);
+            const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, w, 0x04030402u);
+            oacc[4 * c] = fmaf(pk, h2f(lo & 0xFFFF), oacc[4 * c]);
+            oacc[4 * c + 1] = fmaf(pk, h2f(lo >> 16), oacc[4 * c + 1]);
+            oacc[4 * c + 2] = fmaf(pk, h2f(hi & 0xFFFF), oacc[4 * c + 2]);
+            oacc[4 * c + 3] = fmaf(pk, h2f(hi >> 16), oacc[4 * c + 3]);
+          }
+          return;
+        }
         const uint16_t* vrow = vt + (u * KL + rr) * D + kl * CPL;
         uint32_t vw[CPL / 2];
         if constexpr (CPL % 8 == 0) {
@@ -478,6 +524,13 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
   // ---- per-wave state -> LDS (this wave's own stage-0 area), then LSE merge ----
 #pragma unroll
   for (int o = 1; o < KL; o <<= 1) l_lane += __shfl_xor(l_lane, o, 64);
+  if constexpr (VI8) {
+    // remove the 1152 offset per key (l_lane is now the head's sum of p,
+    // rescaled exactly like oacc) and fold in the per-channel scale
+#pragma unroll
+    for (int e = 0; e < CPL; ++e)
+      oacc[e] = (oacc[e] - 1152.f * l_lane) * vsc[(int64_t)bkv * D + kl * CPL + e];
+  }
   float* red = reinterpret_cast<float*>(st0);  // [wave][GS][D] o, then [wave][GS] m, l
   float* ro = red + wave * GS * D;
   float* rm = red + DEC_WAVES * GS * D + wave * GS;
@@ -516,24 +569,27 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
   }
 }
 
-template <int D, int G>
+template <int D, int G, bool VI8>
 void launch_split(dim3 grid, const int8_t* q, const float* qs, const int8_t* k, const float* ks,
-                  const uint16_t* v, float* op, float* mp, float* lp, int N, int ns, int hq,
-                  int hkv, int gsz, int bhq, hipStream_t st) {
-  decode_split_kernel<D, G><<<grid, DEC_THREADS, 0, st>>>(q, qs, k, ks, v, op, mp, lp, N, ns, hq,
-                                                          hkv, gsz, bhq);
+                  const void* v, const float* vsc, float* op, float* mp, float* lp, int N, int ns,
+                  int hq, int hkv, int gsz, int bhq, hipStream_t st) {
+  decode_split_kernel<D, G, VI8><<<grid, DEC_THREADS, 0, st>>>(q, qs, k, ks, v, vsc, op, mp, lp, N,
+                                                               ns, hq, hkv, gsz, bhq);
 }
 
-template <int D>
+template <int D, bool VI8>
 void launch_d(int G, dim3 grid, const int8_t* q, const float* qs, const int8_t* k,
-              const float* ks, const uint16_t* v, float* op, float* mp, float* lp, int N, int ns,
-              int hq, int hkv, int gsz, int bhq, hipStream_t st) {
+              const float* ks, const void* v, const float* vsc, float* op, float* mp, float* lp,
+              int N, int ns, int hq, int hkv, int gsz, int bhq, hipStream_t st) {
+#define SL8_SPLIT(GG) \
+  launch_split<D, GG, VI8>(grid, q, qs, k, ks, v, vsc, op, mp, lp, N, ns, hq, hkv, gsz, bhq, st)
   switch (G) {
-    case 1: launch_split<D, 1>(grid, q, qs, k, ks, v, op, mp, lp, N, ns, hq, hkv, gsz, bhq, st); break;
-    case 2: launch_split<D, 2>(grid, q, qs, k, ks, v, op, mp, lp, N, ns, hq, hkv, gsz, bhq, st); break;
-    case 4: launch_split<D, 4>(grid, q, qs, k, ks, v, op, mp, lp, N, ns, hq, hkv, gsz, bhq, st); break;
-    default: launch_split<D, 8>(grid, q, qs, k, ks, v, op, mp, lp, N, ns, hq, hkv, gsz, bhq, st); break;
+    case 1: SL8_SPLIT(1); break;
+    case 2: SL8_SPLIT(2); break;
+    case 4: SL8_SPLIT(4); break;
+    default: SL8_SPLIT(8); break;
   }
+#undef SL8_SPLIT
 }
 
 int group_width(int gsz) { return gsz >= 8 ? 8 : gsz >= 4 ? 4 : gsz >= 2 ? 2 : 1; }
@@ -562,6 +618,52 @@ extern "C" size_t sl8_attn_int8_decode_workspace(int64_t B, int64_t Hq, int64_t 
   return (size_t)(num_splits * B * Hq * (D + 2)) * sizeof(float);
 }
 
+namespace sl8 {
+namespace {
+
+// Split kernels + combine. v: fp16 [B,Hkv,N,D], or int8 with vsc [B,Hkv,D] (VI8).
+template <bool VI8>
+int decode_launch(const int8_t* q, const float* q_scale, const int8_t* k, const float* k_scale,
+                  const void* v, const float* vsc, void* out, int64_t B, int64_t Hq, int64_t Hkv,
+                  int64_t N, int64_t D, int64_t num_splits, void* workspace, hipStream_t st) {
+  const int ns = (int)num_splits, bhq = (int)(B * Hq), gsz = (int)(Hq / Hkv);
+  const int G = group_width(gsz);
+  float* op = static_cast<float*>(workspace);
+  float* mp = op + (size_t)ns * bhq * D;
+  float* lp = mp + (size_t)ns * bhq;
+  const dim3 grid((unsigned)ns, (unsigned)(B * Hkv), (unsigned)((gsz + G - 1) / G));
+  if ((gsz == 2 && D == 128) || gsz == 4 || gsz == 8) {
+    const dim3 g2((unsigned)ns, (unsigned)(B * Hkv));
+#define SL8_WAVE(DD, GS, NB)                                                                     \
+    decode_wave_kernel<DD, GS, NB, VI8><<<g2, DEC_THREADS, 0, st>>>(q, q_scale, k, k_scale, v, vsc, \
+                                                                  op, mp, lp, (int)N, ns, (int)Hq, \
+                                                                  (int)Hkv, bhq)
+#define SL8_WAVE_D(GS)                         \
+    if (D == 64) SL8_WAVE(64, GS, 4);          \
+    else if (D == 128) SL8_WAVE(128, GS, 3);   \
+    else SL8_WAVE(256, GS, 3);
+    switch (gsz) {
+      case 2: SL8_WAVE(128, 2, 3); break;
+      case 4: SL8_WAVE_D(4); break;
+      default: SL8_WAVE_D(8); break;
+    }
+#undef SL8_WAVE_D
+#undef SL8_WAVE
+  } else switch (D) {
+    case 64: launch_d<64, VI8>(G, grid, q, q_scale, k, k_scale, v, vsc, op, mp, lp, (int)N, ns, (int)Hq, (int)Hkv, gsz, bhq, st); break;
+    case 128: launch_d<128, VI8>(G, grid, q, q_scale, k, k_scale, v, vsc, op, mp, lp, (int)N, ns, (int)Hq, (int)Hkv, gsz, bhq, st); break;
+    default: launch_d<256, VI8>(G, grid, q, q_scale, k, k_scale, v, vsc, op, mp, lp, (int)N, ns, (int)Hq, (int)Hkv, gsz, bhq, st); break;
+  }
+  SL8_CHECK_LAUNCH("attn_int8_decode split");
+  decode_combine_kernel<<<bhq, (unsigned)(D < 256 ? D : 256), 0, st>>>(
+      op, mp, lp, static_cast<uint16_t*>(out), ns, bhq, (int)D);
+  SL8_CHECK_LAUNCH("attn_int8_decode combine");
+  return SL8_OK;
+}
+
+}  // namespace
+}  // namespace sl8
+
 extern "C" int sl8_attn_int8_decode(const int8_t* q, const float* q_scale, const int8_t* k,
                                     const float* k_scale, const void* v, void* out, int64_t B,
                                     int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
@@ -585,38 +687,33 @@ extern "C" int sl8_attn_int8_decode(const int8_t* q, const float* q_scale, const
   const size_t need = sl8_attn_int8_decode_workspace(B, Hq, D, num_splits);
   SL8_CHECK_ARG(workspace && workspace_bytes >= need && aligned(workspace, 16),
                 "fni8 decode: workspace needs %zu bytes", need);
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const int ns = (int)num_splits, bhq = (int)(B * Hq), gsz = (int)(Hq / Hkv);
-  const int G = group_width(gsz);
-  float* op = static_cast<float*>(workspace);
-  float* mp = op + (size_t)ns * bhq * D;
-  float* lp = mp + (size_t)ns * bhq;
-  const dim3 grid((unsigned)ns, (unsigned)(B * Hkv), (unsigned)((gsz + G - 1) / G));
-  const uint16_t* vp = static_cast<const uint16_t*>(v);
-  if ((gsz == 2 && D == 128) || gsz == 4 || gsz == 8) {
-    const dim3 g2((unsigned)ns, (unsigned)(B * Hkv));
-#define SL8_WAVE(DD, GS, NB)                                                                   \
-    decode_wave_kernel<DD, GS, NB><<<g2, DEC_THREADS, 0, st>>>(q, q_scale, k, k_scale, vp, op, mp, lp, \
-                                                             (int)N, ns, (int)Hq, (int)Hkv, bhq)
-#define SL8_WAVE_D(GS)                         \
-    if (D == 64) SL8_WAVE(64, GS, 4);          \
-    else if (D == 128) SL8_WAVE(128, GS, 3);   \
-    else SL8_WAVE(256, GS, 3);
-    switch (gsz) {
-      case 2: SL8_WAVE(128, 2, 3); break;
-      case 4: SL8_WAVE_D(4); break;
-      default: SL8_WAVE_D(8); break;
-    }
-#undef SL8_WAVE_D
-#undef SL8_WAVE
-  } else switch (D) {
-    case 64: launch_d<64>(G, grid, q, q_scale, k, k_scale, vp, op, mp, lp, (int)N, ns, (int)Hq, (int)Hkv, gsz, bhq, st); break;
-    case 128: launch_d<128>(G, grid, q, q_scale, k, k_scale, vp, op, mp, lp, (int)N, ns, (int)Hq, (int)Hkv, gsz, bhq, st); break;
-    default: launch_d<256>(G, grid, q, q_scale, k, k_scale, vp, op, mp, lp, (int)N, ns, (int)Hq, (int)Hkv, gsz, bhq, st); break;
-  }
-  SL8_CHECK_LAUNCH("attn_int8_decode split");
-  decode_combine_kernel<<<bhq, (unsigned)(D < 256 ? D : 256), 0, st>>>(
-      op, mp, lp, static_cast<uint16_t*>(out), ns, bhq, (int)D);
-  SL8_CHECK_LAUNCH("attn_int8_decode combine");
-  return SL8_OK;
+  return decode_launch<false>(q, q_scale, k, k_scale, v, nullptr, out, B, Hq, Hkv, N, D,
+                              num_splits, workspace, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int sl8_attn_int8_decode_kv8(const int8_t* q, const float* q_scale, const int8_t* k,
+                                        const float* k_scale, const int8_t* v, const float* v_scale,
+                                        void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t N,
+                                        int64_t D, int64_t num_splits, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+  clear_error();
+  SL8_CHECK_ARG(B >= 0 && Hq >= 0 && Hkv > 0 && N >= 0, "fni8 decode_kv8: bad shape");
+  SL8_CHECK_ARG(Hq % Hkv == 0, "fni8 decode_kv8: H_q must be divisible by H_kv (GQA)");
+  SL8_CHECK_ARG(D == 64 || D == 128 || D == 256, "fni8 decode_kv8: head dim must be 64/128/256, got %lld",
+                (long long)D);
+  if (num_splits < 0) num_splits = sl8_choose_num_splits(N, B, Hkv);
+  SL8_CHECK_ARG(num_splits >= 1 && num_splits <= DEC_MAX_SPLITS,
+                "fni8 decode_kv8: num_splits must be 1..%d, got %lld", DEC_MAX_SPLITS,
+                (long long)num_splits);
+  SL8_CHECK_ARG(B * Hq < (1LL << 31) && N < (1LL << 31), "fni8 decode_kv8: shape too large");
+  if (B == 0 || Hq == 0) return SL8_OK;
+  SL8_CHECK_ARG(N > 0, "fni8 decode_kv8: empty KV cache (the caller zero-fills the output)");
+  SL8_CHECK_ARG(q && q_scale && k && k_scale && v && v_scale && out, "fni8 decode_kv8: null pointer");
+  SL8_CHECK_ARG(aligned(q, 16) && aligned(k, 16) && aligned(v, 16),
+                "fni8 decode_kv8: q/k/v must be 16-byte aligned");
+  const size_t need = sl8_attn_int8_decode_workspace(B, Hq, D, num_splits);
+  SL8_CHECK_ARG(workspace && workspace_bytes >= need && aligned(workspace, 16),
+                "fni8 decode_kv8: workspace needs %zu bytes", need);
+  return decode_launch<true>(q, q_scale, k, k_scale, v, v_scale, out, B, Hq, Hkv, N, D,
+                             num_splits, workspace, static_cast<hipStream_t>(stream));
 }

@@ -2,8 +2,9 @@
 
 Same names, keyword arguments, routing and error behaviour as the reference
 wrappers (reference superl8/ops.py:70-175 attn_int8_fwd, :230-267
-attn_int8_decode, :975-991 quantize_i8_rowwise, :1254-1325 linear_q4k /
-_linear_kquant), dispatching to the gfx950 kernels through `_C`.
+attn_int8_decode, :531-584 quantize_kv_cache, :671-727 attn_decode_cached,
+:975-991 quantize_i8_rowwise, :1254-1325 linear_q4k / _linear_kquant),
+dispatching to the gfx950 kernels through `_C`.
 """
 from __future__ import annotations
 
@@ -77,6 +78,58 @@ def attn_int8_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     k_scale = k_scale.squeeze(-1).contiguous()
     ns = -1 if num_splits is None else int(num_splits)
     return _C.attn_int8_decode(q_i8, q_scale, k_i8, k_scale, v.contiguous(), ns)
+
+
+def quantize_kv_cache(k: torch.Tensor, v: torch.Tensor, *, rotate: bool = False,
+                      v_quant: str = "per_channel"):
+    """Quantise a K/V cache once for persistent int8 storage (reference ops.py:531-584):
+    K smoothed (+ optional Hadamard rotation) then per-row int8; V per-channel int8
+    (v_scale [B,Hkv,D]) or, with v_quant="per_token", per-key int8 (v_scale [B,Hkv,N]).
+    Returns (k_i8, k_scale [B,Hkv,N], v_i8, v_scale)."""
+    from .quant import quantize_int8_rowwise, quantize_v_perchannel, quantize_v_rowwise, smooth_k
+
+    if v_quant not in ("per_channel", "per_token"):
+        raise ValueError(f"v_quant must be 'per_channel' or 'per_token', got {v_quant!r}")
+    k_s, _k_mean = smooth_k(k)
+    if rotate:
+        from .quant.rotation import rotate_last
+
+        k_s = rotate_last(k_s)
+    k_i8, k_scale = quantize_int8_rowwise(k_s)
+    if v_quant == "per_channel":
+        v_i8, v_scale = quantize_v_perchannel(v)
+        v_scale = v_scale.squeeze(-2)
+    else:
+        v_i8, v_scale = quantize_v_rowwise(v)
+        v_scale = v_scale.squeeze(-1)
+    return k_i8.contiguous(), k_scale.squeeze(-1).contiguous(), v_i8.contiguous(), v_scale.contiguous()
+
+
+def attn_decode_cached(q: torch.Tensor, k_i8: torch.Tensor, k_scale: torch.Tensor,
+                       v_i8: torch.Tensor, v_scale: torch.Tensor, *, scale: float | None = None,
+                       rotate: bool = False, num_splits: int | None = None) -> torch.Tensor:
+    """Decode (M=1) against a pre-quantised int8 K/V cache from quantize_kv_cache
+    (reference ops.py:671-727): only q is quantised per call. q fp16 [B,Hq,1,D] ->
+    fp16 [B,Hq,1,D]; `rotate` must match the flag the cache was built with."""
+    from .quant import LOG2E
+    from .quant.rotation import rotate_last
+
+    if q.shape[-2] != 1:
+        raise AssertionError(f"decode expects M=1, got M={q.shape[-2]}")
+    if v_scale.shape[-1] == k_i8.shape[2]:
+        raise RuntimeError(
+            "attn_decode_cached received a per-token V scale [B,H,N]; the contiguous int8-V "
+            "decode kernel (attn_int8_decode_kv8) supports per-channel V scales [B,H,D] only")
+    softmax_scale = (1.0 / (q.shape[-1] ** 0.5)) if scale is None else scale
+    if rotate:
+        q = rotate_last(q)
+    q_shape = q.shape
+    q_i8, q_scale = quantize_i8_rowwise(q.reshape(-1, q_shape[-1]).contiguous())
+    q_i8 = q_i8.reshape(q_shape)
+    q_scale = (q_scale.float() * (softmax_scale * LOG2E)).reshape(q_shape[0], q_shape[1], 1).contiguous()
+    ns = -1 if num_splits is None else int(num_splits)
+    return _C.attn_int8_decode_kv8(q_i8.contiguous(), q_scale, k_i8.contiguous(),
+                                   k_scale.contiguous(), v_i8.contiguous(), v_scale.contiguous(), ns)
 
 
 def quantize_i8_rowwise(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:

@@ -100,3 +100,51 @@ def test_config3_shape_against_oracle(device):
         ref = oa.attn_int8_decode(_np(q_i8[b:b + 1])[:, :, 0], _np(qs[b:b + 1])[:, :, 0],
                                   _np(k_i8[b:b + 1]), _np(ks[b:b + 1]), _np(v[b:b + 1].float()), 16)
         assert_close_abs(out[b:b + 1, :, 0], ref, atol=2e-3, rtol=2e-3, what=f"config3 b={b}")
+
+
+# ---------------------------------------------------------------------------
+# int8 V cache (reference attn_decode.cuh:141-224, ops.py:531-584,671-727)
+# ---------------------------------------------------------------------------
+def _kv8(v):
+    v_i8, vs = _C.quantize_v_perchannel(v)
+    return v_i8, vs.squeeze(-2).contiguous()
+
+
+@pytest.mark.parametrize("shape", DECODE_SHAPES)
+@pytest.mark.parametrize("ns", [-1, 1, 16])
+def test_kv8_kernel_matches_oracle(device, shape, ns):
+    q, k, v = _qkv(shape, device)
+    q_i8, qs, k_i8, ks = _prep(q, k)
+    v_i8, vs = _kv8(v)
+    out = _C.attn_int8_decode_kv8(q_i8, qs, k_i8, ks, v_i8, vs, ns)
+    n_splits = ns if ns > 0 else _C.choose_n_splits(shape[3], shape[0], shape[2])
+    ref = oa.attn_int8_decode_kv8(_np(q_i8)[:, :, 0], _np(qs)[:, :, 0], _np(k_i8), _np(ks),
+                                  _np(v_i8), _np(vs), n_splits)
+    assert out.shape == q.shape and out.dtype == torch.float16
+    assert_close_abs(out[:, :, 0], ref, atol=2e-3, rtol=2e-3, what=f"decode_kv8 {shape} ns={ns}")
+
+
+@pytest.mark.parametrize("shape", [(1, 8, 8, 512, 64), (2, 32, 8, 3000, 128), (1, 16, 2, 333, 256)])
+@pytest.mark.parametrize("rotate", [False, True])
+def test_decode_cached_end_to_end(device, shape, rotate):
+    """quantize_kv_cache once, then attn_decode_cached per step: the reference's
+    int8-PV quality bars against fp64 attention on the fp16 inputs."""
+    q, k, v = _qkv(shape, device)
+    cache = sl8.quantize_kv_cache(k, v, rotate=rotate)
+    out = sl8.attn_decode_cached(q, *cache, rotate=rotate)
+    ref = oa.attention_fp64(_np(q.float()), _np(k.float()), _np(v.float()))
+    assert_finite(out)
+    assert_int8_quality(out, ref, min_cos=0.998, max_rel_l1=0.03, min_sqnr_db=18,
+                        what=f"decode_cached {shape}")
+
+
+def test_decode_cached_rejects(device):
+    q, k, v = _qkv((1, 4, 4, 64, 64), device)
+    k_i8, ks, v_i8, vs_tok = sl8.quantize_kv_cache(k, v, v_quant="per_token")
+    with pytest.raises(RuntimeError, match="per-token"):
+        sl8.attn_decode_cached(q, k_i8, ks, v_i8, vs_tok)
+    with pytest.raises(ValueError):
+        sl8.quantize_kv_cache(k, v, v_quant="per_block")
+    k_i8, ks, v_i8, vs = sl8.quantize_kv_cache(k, v)
+    with pytest.raises(RuntimeError, match="int8"):
+        _C.attn_int8_decode_kv8(k_i8[:, :, :1], ks[:, :, :1], k_i8, ks, v.contiguous(), vs)

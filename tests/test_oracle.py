@@ -242,6 +242,27 @@ def test_decode_split_invariance(ns):
     np.testing.assert_allclose(dec, pre[:, :, 0], rtol=1e-12, atol=1e-12)
 
 
+@pytest.mark.parametrize("ns", [1, 5, 64])
+def test_decode_kv8_equals_dequantised_v(ns):
+    """int8-V decode: folding v_scale[d] into each split's partial commutes with the
+    LSE merge, so it equals the fp decode on V = v_i8 * v_scale (scaled here, per KV
+    head, independently of the oracle's head map); v_scale = 1 reduces to v_i8."""
+    q, k, v = _case(B=2, Hq=8, Hkv=2, M=1, N=70, D=64, seed=13)
+    q_i8, qs, k_i8, ks, _ = oqn.quantize_qk(q, k)
+    v_i8, vs = oqn.quantize_v_perchannel(v)  # vs [B,Hkv,D]
+    got = oa.attn_int8_decode_kv8(q_i8[:, :, 0], qs[:, :, 0], k_i8, ks, v_i8, vs, ns)
+    deq = v_i8.astype(np.float64) * vs[:, :, None, :].astype(np.float64)
+    ref = oa.attn_int8_decode(q_i8[:, :, 0], qs[:, :, 0], k_i8, ks, deq, ns)
+    np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-12)
+    ones = np.ones_like(vs)
+    got1 = oa.attn_int8_decode_kv8(q_i8[:, :, 0], qs[:, :, 0], k_i8, ks, v_i8, ones, ns)
+    ref1 = oa.attn_int8_decode(q_i8[:, :, 0], qs[:, :, 0], k_i8, ks, v_i8.astype(np.float64), ns)
+    np.testing.assert_allclose(got1, ref1, rtol=1e-12, atol=1e-12)
+    # the dequantised cache is close to the fp16 one (per-channel int8 V)
+    fp = oa.attn_int8_decode(q_i8[:, :, 0], qs[:, :, 0], k_i8, ks, v.astype(np.float64), ns)
+    assert_int8_quality(got, fp, min_cos=0.998, max_rel_l1=0.03, min_sqnr_db=18)
+
+
 def test_w8a8_oracle_close_to_fp16v():
     """Int8 PV (per-row and per-half P scales) stays within the reference's int8-PV
     bars of the fp16-V result (test_attn_fwd_w8a8.py:37)."""
