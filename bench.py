@@ -142,6 +142,32 @@ def bench_decode_kv8(iters=20):
     return ms, nbytes
 
 
+def bench_paged_decode(iters=20, bs=16):
+    """Paged int8 KV decode at config 3's shape: 16 sequences of 32768 keys in
+    16-key blocks scattered over the pool by a shuffled block table, per-token
+    K and V scales (reference attn_paged_decode)."""
+    from superl8_amd import _C
+
+    dev = "cuda"
+    B, Hq, Hkv, N, D = 16, 32, 8, 32768, 128
+    g = torch.Generator(device=dev).manual_seed(8)
+    nblk = B * N // bs
+    kc = torch.randint(-127, 128, (nblk, Hkv, bs, D), device=dev, dtype=torch.int8, generator=g)
+    vc = torch.randint(-127, 128, (nblk, Hkv, bs, D), device=dev, dtype=torch.int8, generator=g)
+    ks = torch.rand(nblk, Hkv, bs, device=dev, generator=g) * 0.02 + 1e-3
+    vs = torch.rand(nblk, Hkv, bs, device=dev, generator=g) * 0.02 + 1e-3
+    bt = torch.randperm(nblk, device=dev, generator=g).to(torch.int32).reshape(B, N // bs)
+    ctx = torch.full((B,), N, device=dev, dtype=torch.int32)
+    q = torch.randint(-127, 128, (B, Hq, 1, D), device=dev, dtype=torch.int8, generator=g)
+    qs = torch.rand(B, Hq, 1, device=dev, generator=g) * 0.01 + 1e-3
+    fn = lambda: _C.attn_paged_decode(q, qs, kc, ks, vc, vs, bt, ctx, bs, N, 16)  # noqa: E731
+    spin_up(fn, 0.2)
+    ms = _events_time(fn, iters, torch.cuda.current_stream())
+    nbytes = kc.numel() + vc.numel() + (ks.numel() + vs.numel()) * 4 + bt.numel() * 4 \
+        + q.numel() + qs.numel() * 4 + B * Hq * D * 2
+    return ms, nbytes
+
+
 def bench_w8a8(iters=5):
     """Full-W8A8 prefill at BASELINE config 5: Q/K/V [2, 16|2, 8192, 256], causal,
     1% of Q/K channels (3 of 256, fixed) scaled by 20, V per-channel int8."""

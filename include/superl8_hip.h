@@ -163,6 +163,33 @@ int sl8_attn_int8_decode_kv8(const int8_t* q, const float* q_scale, const int8_t
                              void* stream);
 
 /* ------------------------------------------------------------------------
+ * Paged int8 KV cache (reference csrc/fni8_api.cpp:138-143,152-154,509-527,
+ * csrc/kernel/attn_paged_decode.cu:14-31,107-240,360-421,
+ * csrc/include/attn_paged_decode.cuh:55-262).
+ *   k_cache, v_cache int8 [num_blocks, Hkv, block_size, D]; k_scale, v_scale
+ *   fp32 [num_blocks, Hkv, block_size] (per token). block_table int32
+ *   [B, max_blocks_per_seq]: physical block of each logical block of a
+ *   sequence; context_lens int32 [B]. Splits are sized on max_context_len
+ *   (<= max_blocks_per_seq * block_size); num_splits -1 = auto
+ *   (sl8_paged_choose_num_splits). Workspace: sl8_attn_int8_decode_workspace.
+ * sl8_kv_write_paged: quantise one new token per (batch, KV head) from fp16
+ *   k_new, v_new [B, Hkv, D] into flat slot_mapping[b] = block*bs + offset,
+ *   in place (scale = amax / 127, code = rint(x / scale)).
+ * ---------------------------------------------------------------------- */
+int sl8_paged_choose_num_splits(int64_t n_len_max, int64_t bhq);
+int sl8_attn_paged_decode(const int8_t* q, const float* q_scale, const int8_t* k_cache,
+                          const float* k_scale, const int8_t* v_cache, const float* v_scale,
+                          const int32_t* block_table, const int32_t* context_lens, void* out,
+                          int64_t B, int64_t Hq, int64_t Hkv, int64_t D, int64_t num_blocks,
+                          int64_t block_size, int64_t max_blocks_per_seq,
+                          int64_t max_context_len, int64_t num_splits, void* workspace,
+                          size_t workspace_bytes, void* stream);
+int sl8_kv_write_paged(const void* k_new, const void* v_new, const int32_t* slot_mapping,
+                       int8_t* k_cache, float* k_scale, int8_t* v_cache, float* v_scale,
+                       int64_t B, int64_t Hkv, int64_t D, int64_t num_blocks,
+                       int64_t block_size, void* stream);
+
+/* ------------------------------------------------------------------------
  * Q4_K GEMM/GEMV over native GGUF super-blocks (144 B per 256 weights:
  * fp16 d, fp16 dmin, 12 B packed 6-bit sub-scales/mins, 128 B nibbles).
  *   y[m,n] = x_scale[m] * sum_j (d*sc_j*<x_j,q_j> - dmin*m_j*sum(x_j))

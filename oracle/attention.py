@@ -10,6 +10,10 @@ Reference kernels restated:
   csrc/include/attn_decode.cuh:47-132,430-466 (split s owns keys
       [s*per, min(N,(s+1)*per)), per = ceil(N/ns); partial (O, m, l);
       empty split -> m = -1e30; LSE merge)
+  csrc/include/attn_paged_decode.cuh:126-262 (paged cache addressed by a
+      per-sequence block table and context length, splits sized on the
+      launch's max context length, per-token V scale inside the key sum)
+  csrc/kernel/attn_paged_decode.cu:14-31 (its split-count heuristic)
   csrc/include/attn_decode.cuh:141-224 (int8 V cache: O accumulates
       p * v_i8 and each split's partial O is multiplied by the per-channel
       v_scale[d] of its KV head before the merge)
@@ -186,6 +190,70 @@ def attn_int8_decode_kv8(q_i8, q_scale, k_i8, k_scale, v_i8, v_scale, num_splits
         num += o * w[..., None]
         den += l * w
     return np.where(den[..., None] > 0, num / np.where(den > 0, den, 1.0)[..., None], 0.0)
+
+
+def paged_choose_num_splits(n_len_max: int, bhq: int) -> int:
+    """Auto split count of the paged decode (reference attn_paged_decode.cu:14-31)."""
+    if n_len_max <= 0 or bhq <= 0:
+        return 1
+    s_occ = (2048 + bhq - 1) // bhq
+    s_lo = (n_len_max + 255) // 256
+    s_hi = max(1, (n_len_max + 47) // 48)
+    s = min(max(s_occ, s_lo), s_hi)
+    return max(1, min(s, 256))
+
+
+def gather_paged(cache, block_table, b, n, Hkv_axis=1):
+    """Rows 0..n-1 of sequence b from a paged cache [num_blocks, Hkv, bs, ...] -> [Hkv, n, ...]."""
+    bs = cache.shape[2]
+    pos = np.arange(n)
+    blk = np.asarray(block_table)[b, pos // bs]
+    return np.swapaxes(cache[blk, :, pos % bs], 0, 1)
+
+
+def attn_paged_decode(q_i8, q_scale, k_cache, k_scale, v_cache, v_scale, block_table,
+                      context_lens, max_context_len, num_splits):
+    """Paged split-KV decode (reference attn_paged_decode.cuh:126-262): q_i8 [B,Hq,D],
+    q_scale [B,Hq]; sequence b has context_lens[b] keys at logical positions mapped
+    through block_table; split s covers [s*per, min(len_b, (s+1)*per)) with
+    per = ceil(max_context_len / ns); O accumulates p * v_i8 * v_scale[token];
+    same LSE merge as attn_int8_decode. Returns [B,Hq,D] float64."""
+    B, Hq, D = q_i8.shape
+    Hkv = k_cache.shape[1]
+    idx = kv_head_index(Hq, Hkv)
+    per = (max_context_len + num_splits - 1) // num_splits
+    out = np.zeros((B, Hq, D))
+    for b in range(B):
+        n = int(context_lens[b])
+        if n == 0:
+            continue
+        kb = gather_paged(k_cache, block_table, b, n)[idx]          # [Hq, n, D]
+        ksb = gather_paged(k_scale, block_table, b, n)[idx]         # [Hq, n]
+        vb = gather_paged(v_cache, block_table, b, n)[idx].astype(np.float64)
+        vsb = gather_paged(v_scale, block_table, b, n)[idx].astype(np.float64)
+        acc = np.einsum("hd,hnd->hn", q_i8[b].astype(np.float64), kb.astype(np.float64))
+        s_all = ((acc.astype(np.float32) * q_scale[b][:, None].astype(np.float32))
+                 * ksb.astype(np.float32)).astype(np.float64)
+        gm = np.full(Hq, DEC_NEG_INF)
+        parts = []
+        for sp in range(num_splits):
+            n0, n1 = sp * per, min(n, (sp + 1) * per)
+            if n1 <= n0:
+                continue
+            s = s_all[:, n0:n1]
+            m = s.max(-1)
+            p = np.exp2(s - m[:, None])
+            o = np.einsum("hn,hnd->hd", p * vsb[:, n0:n1], vb[:, n0:n1])
+            parts.append((o, m, p.sum(-1)))
+            gm = np.maximum(gm, m)
+        num = np.zeros((Hq, D))
+        den = np.zeros(Hq)
+        for o, m, l in parts:
+            w = np.exp2(m - gm)
+            num += o * w[:, None]
+            den += l * w
+        out[b] = np.where(den[:, None] > 0, num / np.where(den > 0, den, 1.0)[:, None], 0.0)
+    return out
 
 
 def attention_fp64(q, k, v, causal=False, scale=None):

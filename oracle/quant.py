@@ -3,7 +3,10 @@
 Reference: csrc/include/quant_rowwise.cuh:33-91 (scale = amax * fp32(1/127),
 zero row -> 1, q = clamp(rint(x / scale), +-127) with correctly rounded fp32
 division), superl8/quant/core.py:29-44,70-95 (K mean / smoothing),
-core.py:164-196 (quantize_qk: fold softmax_scale*log2(e) into the Q scale).
+core.py:164-196 (quantize_qk: fold softmax_scale*log2(e) into the Q scale),
+csrc/include/attn_paged_decode.cuh:55-115 (quantize-on-write of one token per
+paged row: scale = amax / 127 as an fp32 division, zero row -> 1, code =
+rint(clamp(x / scale, +-127))).
 
 TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
 """
@@ -102,3 +105,32 @@ def quantize_v_perchannel(v: np.ndarray, dtype: str = "f16"):
     vf = to_f32(v, dtype)
     q, s = quantize_rows(np.swapaxes(vf, -1, -2))
     return np.swapaxes(q, -1, -2).copy(), s
+
+
+def quantize_row_div(x: np.ndarray):
+    """Per-row int8 with an IEEE-division scale (reference attn_paged_decode.cuh:74-110):
+    scale = fp32(amax) / 127 (fp32), 1 for an all-zero row; code = rint(clamp(x / scale,
+    -127, 127)). Rows are the last axis; returns (int8 codes, fp32 scales [...])."""
+    xf = np.asarray(x, dtype=np.float32)
+    amax = np.abs(xf).max(-1)
+    scale = np.where(amax > 0, (amax / np.float32(127.0)).astype(np.float32), np.float32(1.0))
+    scale = scale.astype(np.float32)
+    y = (xf / scale[..., None]).astype(np.float32)
+    q = np.rint(np.clip(y, -127.0, 127.0)).astype(np.int8)
+    return q, scale
+
+
+def kv_write_paged(k_new, v_new, slot_mapping, k_cache, k_scale, v_cache, v_scale):
+    """Quantise one new token per (batch, KV head) and store it at the flat slot
+    block * block_size + offset (reference attn_paged_decode.cuh:55-115); caches are
+    updated in place: k_cache/v_cache int8 [num_blocks, Hkv, block_size, D],
+    k_scale/v_scale fp32 [num_blocks, Hkv, block_size]; k_new/v_new [B, Hkv, D]."""
+    bs = k_cache.shape[2]
+    kq, ks = quantize_row_div(k_new)
+    vq, vs = quantize_row_div(v_new)
+    for b, slot in enumerate(np.asarray(slot_mapping).tolist()):
+        blk, off = divmod(int(slot), bs)
+        k_cache[blk, :, off] = kq[b]
+        v_cache[blk, :, off] = vq[b]
+        k_scale[blk, :, off] = ks[b]
+        v_scale[blk, :, off] = vs[b]

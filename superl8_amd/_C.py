@@ -298,6 +298,96 @@ def attn_int8_decode_kv8(q, q_scale, k, k_scale, v, v_scale, num_splits=-1):
     return out
 
 
+def paged_choose_n_splits(n_len_max, bhq):
+    """Auto split count of the paged decode (reference attn_paged_decode.cu:14-31)."""
+    return int(_lib.load().sl8_paged_choose_num_splits(int(n_len_max), int(bhq)))
+
+
+def attn_paged_decode(q, q_scale, k_cache, k_scale, v_cache, v_scale, block_table, context_lens,
+                      block_size, max_context_len, num_splits=-1):
+    """Paged-KV decode (reference csrc/kernel/attn_paged_decode.cu:107-240): q int8
+    [B,Hq,1,D], q_scale fp32 [B,Hq,1], k_cache/v_cache int8 [num_blocks,Hkv,bs,D],
+    k_scale/v_scale fp32 [num_blocks,Hkv,bs], block_table int32 [B,max_blocks],
+    context_lens int32 [B] -> fp16 [B,Hq,1,D]."""
+    _on_gpu(q, q_scale, k_cache, k_scale, v_cache, v_scale, block_table, context_lens)
+    _check(q.dtype == torch.int8 and k_cache.dtype == torch.int8 and v_cache.dtype == torch.int8,
+           "paged_decode: q/k_cache/v_cache must be int8")
+    _check(q_scale.dtype == torch.float32 and k_scale.dtype == torch.float32 and
+           v_scale.dtype == torch.float32, "paged_decode: scales must be float32")
+    _check(block_table.dtype == torch.int32 and context_lens.dtype == torch.int32,
+           "paged_decode: block_table/context_lens must be int32")
+    _check(q.dim() == 4 and q.shape[2] == 1, "paged_decode: q must be [B,H_q,1,D]")
+    _check(k_cache.dim() == 4 and v_cache.dim() == 4,
+           "paged_decode: k_cache/v_cache must be [num_blocks,H_kv,block_size,D]")
+    _contig(q, q_scale, k_cache, k_scale, v_cache, v_scale, block_table, context_lens)
+    B, H, _, D = q.shape
+    nblk, Hkv, bs = k_cache.shape[0], k_cache.shape[1], k_cache.shape[2]
+    _check(bs == block_size, "paged_decode: block_size mismatch vs k_cache.size(2)")
+    _check(k_cache.shape[3] == D and v_cache.shape == k_cache.shape,
+           "paged_decode: k_cache/v_cache shape mismatch")
+    _check(Hkv > 0 and H % Hkv == 0, "paged_decode: H_q must be divisible by H_kv (GQA)")
+    _check(k_cache.numel() == k_scale.numel() * D and v_cache.numel() == v_scale.numel() * D,
+           "paged_decode: scale shape mismatch vs cache")
+    _check(q_scale.numel() == B * H, "paged_decode: q_scale shape mismatch")
+    _check(block_table.dim() == 2 and block_table.shape[0] == B,
+           "paged_decode: block_table must be [B, max_blocks_per_seq]")
+    _check(context_lens.dim() == 1 and context_lens.shape[0] == B,
+           "paged_decode: context_lens must be [B]")
+    _check(D in _HEAD_DIMS_DECODE, f"paged_decode: head dim must be one of {_HEAD_DIMS_DECODE}, got {D}")
+    maxb = block_table.shape[1]
+    _check(0 <= max_context_len <= maxb * bs,
+           "paged_decode: max_context_len exceeds block_table capacity")
+    num_splits = int(num_splits)
+    _check(num_splits != 0,
+           f"paged_decode: num_splits=0 is invalid; use -1 for auto or 1..{DEC_MAX_SPLITS}")
+    out = torch.empty((B, H, 1, D), device=q.device, dtype=torch.float16)
+    if B == 0 or H == 0:
+        return out
+    ns = paged_choose_n_splits(max_context_len, B * H) if num_splits < 0 else num_splits
+    _check(1 <= ns <= DEC_MAX_SPLITS, f"paged_decode: num_splits must be 1..{DEC_MAX_SPLITS}, got {ns}")
+    ws_bytes = _lib.load().sl8_attn_int8_decode_workspace(B, H, D, ns)
+    ws = torch.empty((ws_bytes,), device=q.device, dtype=torch.uint8)
+    with torch.cuda.device(q.device):
+        call("sl8_attn_paged_decode", q.data_ptr(), q_scale.data_ptr(), k_cache.data_ptr(),
+             k_scale.data_ptr(), v_cache.data_ptr(), v_scale.data_ptr(), block_table.data_ptr(),
+             context_lens.data_ptr(), out.data_ptr(), B, H, Hkv, D, nblk, bs, maxb,
+             int(max_context_len), ns, ws.data_ptr(), ws_bytes, stream_of(q))
+    return out
+
+
+def kv_write_paged(k_new, v_new, slot_mapping, k_cache, k_scale, v_cache, v_scale):
+    """Quantize-on-write of one new token per (batch, KV head) into the paged int8
+    cache, in place (reference csrc/kernel/attn_paged_decode.cu:360-421)."""
+    _on_gpu(k_new, v_new, slot_mapping, k_cache, k_scale, v_cache, v_scale)
+    _check(k_new.dtype == torch.float16 and v_new.dtype == torch.float16,
+           "kv_write_paged: k_new/v_new must be float16")
+    _check(slot_mapping.dtype == torch.int32, "kv_write_paged: slot_mapping must be int32")
+    _check(k_cache.dtype == torch.int8 and v_cache.dtype == torch.int8,
+           "kv_write_paged: k_cache/v_cache must be int8")
+    _check(k_new.dim() == 3 and v_new.dim() == 3, "kv_write_paged: k_new/v_new must be [B,H_kv,D]")
+    _contig(k_new, v_new, slot_mapping, k_cache, v_cache)
+    B, Hkv, D = k_new.shape
+    _check(tuple(v_new.shape) == (B, Hkv, D), "kv_write_paged: k_new/v_new shape mismatch")
+    _check(slot_mapping.dim() == 1 and slot_mapping.shape[0] == B,
+           "kv_write_paged: slot_mapping must be [B]")
+    _check(k_cache.dim() == 4 and k_cache.shape[1] == Hkv and k_cache.shape[3] == D,
+           "kv_write_paged: k_cache must be [num_blocks,H_kv,block_size,D]")
+    _check(v_cache.shape == k_cache.shape, "kv_write_paged: v_cache shape must match k_cache")
+    _check(k_scale.is_contiguous() and v_scale.is_contiguous(),
+           "kv_write_paged: k_scale/v_scale must be contiguous")
+    _check(k_scale.dtype == torch.float32 and v_scale.dtype == torch.float32,
+           "kv_write_paged: k_scale/v_scale must be float32")
+    _check(k_scale.numel() == k_cache.numel() // D and v_scale.numel() == v_cache.numel() // D,
+           "kv_write_paged: scale shape mismatch vs cache")
+    _check(D in _HEAD_DIMS_DECODE, f"kv_write_paged: head dim must be one of {_HEAD_DIMS_DECODE}, got {D}")
+    if B == 0:
+        return
+    with torch.cuda.device(k_new.device):
+        call("sl8_kv_write_paged", k_new.data_ptr(), v_new.data_ptr(), slot_mapping.data_ptr(),
+             k_cache.data_ptr(), k_scale.data_ptr(), v_cache.data_ptr(), v_scale.data_ptr(),
+             B, Hkv, D, k_cache.shape[0], k_cache.shape[2], stream_of(k_new))
+
+
 # ---------------------------------------------------------------------------
 # Q4_K (reference csrc/kernel/gemm_dp4a.cu:146-193, gemm_decode_dp4a.cu:375-436)
 # ---------------------------------------------------------------------------

@@ -45,14 +45,26 @@ struct DecSmem {
 
 // VI8: V is the int8 cache [B,Hkv,N,D] with per-channel scale vsc [B,Hkv,D]
 // (reference attn_decode.cuh:141-224), folded into the partial O.
-template <int D, int G, bool VI8>
+// PG (paged, reference attn_paged_decode.cuh:126-262): K/V int8 caches
+// [num_blocks,Hkv,bs,D] with per-token scales [num_blocks,Hkv,bs] for both;
+// key n of sequence b is row (bt[b][n / bs] * Hkv + kvh) * bs + n % bs; the
+// sequence has ctx[b] keys and the splits are sized on n_len (the launch's
+// maximum); the per-token V scale multiplies p inside the key sum.
+struct PagedArgs {
+  const int32_t* bt;   // [B, maxb] physical block per logical block
+  const int32_t* ctx;  // [B] keys per sequence
+  int maxb, bs;
+};
+
+template <int D, int G, bool VI8, bool PG>
 __global__ void __launch_bounds__(DEC_THREADS)
 decode_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_scale,
                     const int8_t* __restrict__ k, const float* __restrict__ k_scale,
                     const void* __restrict__ v, const float* __restrict__ vsc,
                     float* __restrict__ o_part,
                     float* __restrict__ m_part, float* __restrict__ l_part, int n_len,
-                    int n_splits, int h_q, int h_kv, int gsz, int bhq) {
+                    int n_splits, int h_q, int h_kv, int gsz, int bhq, const PagedArgs pg) {
+  static_assert(!PG || VI8, "the paged cache holds int8 V");
   constexpr int D4 = D / 4;
   constexpr int DG = D / 8;           // 8-channel groups
   constexpr int KPH = 64 / DG;        // key phases in the PV lane map
@@ -84,11 +96,17 @@ decode_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sc
 
   const int per = (n_len + n_splits - 1) / n_splits;
   const int n0 = split * per;
-  const int n1 = min(n_len, n0 + per);
-  const int8_t* kb = k + (int64_t)bkv * n_len * D;
-  const float* ksb = k_scale + (int64_t)bkv * n_len;
+  const int n1 = min(PG ? pg.ctx[b] : n_len, n0 + per);
+  // cache row of key n (contiguous: relative to this (batch, KV head))
+  const int32_t* btb = PG ? pg.bt + (int64_t)b * pg.maxb : nullptr;
+  auto krow = [&](int n) -> int64_t {
+    if constexpr (PG) return ((int64_t)btb[n / pg.bs] * h_kv + kvh) * pg.bs + n % pg.bs;
+    else return n;
+  };
+  const int8_t* kb = k + (PG ? 0 : (int64_t)bkv * n_len * D);
+  const float* ksb = k_scale + (PG ? 0 : (int64_t)bkv * n_len);
   constexpr int VES = VI8 ? 1 : 2;  // V element bytes
-  const uint8_t* vb = static_cast<const uint8_t*>(v) + (int64_t)bkv * n_len * D * VES;
+  const uint8_t* vb = static_cast<const uint8_t*>(v) + (PG ? 0 : (int64_t)bkv * n_len * D * VES);
 
   float m_run[G], l_lane[G], oacc[G][8];
 #pragma unroll
@@ -107,10 +125,11 @@ decode_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sc
     float s[G];
     {
       int4 kr[D / 16];
-      const int4* kp = reinterpret_cast<const int4*>(kb + (int64_t)(valid ? n : n0) * D);
+      const int64_t kr_row = krow(valid ? n : n0);
+      const int4* kp = reinterpret_cast<const int4*>(kb + kr_row * D);
 #pragma unroll
       for (int c = 0; c < D / 16; ++c) kr[c] = kp[c];
-      const float ks = valid ? ksb[n] : 0.f;
+      const float ks = valid ? ksb[kr_row] : 0.f;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         int acc = 0;
@@ -153,15 +172,17 @@ decode_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sc
       const int nn = t0 + kk;
       if (nn < n1) {
         float vf[8];
+        const int64_t vr = krow(nn);
+        const float pvs = PG ? vsc[vr] : 1.f;  // per-token V scale (paged)
         if constexpr (VI8) {
-          const uint2 vv = *reinterpret_cast<const uint2*>(vb + (int64_t)nn * D + dg * 8);
+          const uint2 vv = *reinterpret_cast<const uint2*>(vb + vr * D + dg * 8);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             vf[e] = (float)(int8_t)(vv.x >> (8 * e));
             vf[4 + e] = (float)(int8_t)(vv.y >> (8 * e));
           }
         } else {
-          const uint4 vv = *reinterpret_cast<const uint4*>(vb + ((int64_t)nn * D + dg * 8) * 2);
+          const uint4 vv = *reinterpret_cast<const uint4*>(vb + (vr * D + dg * 8) * 2);
           vf[0] = h2f(vv.x & 0xFFFF); vf[1] = h2f(vv.x >> 16);
           vf[2] = h2f(vv.y & 0xFFFF); vf[3] = h2f(vv.y >> 16);
           vf[4] = h2f(vv.z & 0xFFFF); vf[5] = h2f(vv.z >> 16);
@@ -169,7 +190,7 @@ decode_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sc
         }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-          const float p = sm.p[wave][kk][g];
+          const float p = sm.p[wave][kk][g] * pvs;
 #pragma unroll
           for (int e = 0; e < 8; ++e) oacc[g][e] = fmaf(p, vf[e], oacc[g][e]);
         }
@@ -218,7 +239,7 @@ decode_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sc
     }
     const int64_t hq = (int64_t)b * h_q + kvh * gsz + j0 + g;
     const int64_t row = (int64_t)split * bhq + hq;
-    o_part[row * D + d] = VI8 ? acc * vsc[(int64_t)bkv * D + d] : acc;
+    o_part[row * D + d] = (VI8 && !PG) ? acc * vsc[(int64_t)bkv * D + d] : acc;
     if (d == 0) {
       m_part[row] = (mm == -INFINITY) ? DEC_NEG_INF : mm;
       l_part[row] = den;
@@ -569,20 +590,21 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
   }
 }
 
-template <int D, int G, bool VI8>
+template <int D, int G, bool VI8, bool PG>
 void launch_split(dim3 grid, const int8_t* q, const float* qs, const int8_t* k, const float* ks,
                   const void* v, const float* vsc, float* op, float* mp, float* lp, int N, int ns,
-                  int hq, int hkv, int gsz, int bhq, hipStream_t st) {
-  decode_split_kernel<D, G, VI8><<<grid, DEC_THREADS, 0, st>>>(q, qs, k, ks, v, vsc, op, mp, lp, N,
-                                                               ns, hq, hkv, gsz, bhq);
+                  int hq, int hkv, int gsz, int bhq, const PagedArgs& pg, hipStream_t st) {
+  decode_split_kernel<D, G, VI8, PG><<<grid, DEC_THREADS, 0, st>>>(q, qs, k, ks, v, vsc, op, mp, lp,
+                                                                   N, ns, hq, hkv, gsz, bhq, pg);
 }
 
-template <int D, bool VI8>
+template <int D, bool VI8, bool PG = false>
 void launch_d(int G, dim3 grid, const int8_t* q, const float* qs, const int8_t* k,
               const float* ks, const void* v, const float* vsc, float* op, float* mp, float* lp,
-              int N, int ns, int hq, int hkv, int gsz, int bhq, hipStream_t st) {
+              int N, int ns, int hq, int hkv, int gsz, int bhq, hipStream_t st,
+              const PagedArgs& pg = PagedArgs{nullptr, nullptr, 0, 1}) {
 #define SL8_SPLIT(GG) \
-  launch_split<D, GG, VI8>(grid, q, qs, k, ks, v, vsc, op, mp, lp, N, ns, hq, hkv, gsz, bhq, st)
+  launch_split<D, GG, VI8, PG>(grid, q, qs, k, ks, v, vsc, op, mp, lp, N, ns, hq, hkv, gsz, bhq, pg, st)
   switch (G) {
     case 1: SL8_SPLIT(1); break;
     case 2: SL8_SPLIT(2); break;
@@ -716,4 +738,151 @@ extern "C" int sl8_attn_int8_decode_kv8(const int8_t* q, const float* q_scale, c
                 "fni8 decode_kv8: workspace needs %zu bytes", need);
   return decode_launch<true>(q, q_scale, k, k_scale, v, v_scale, out, B, Hq, Hkv, N, D,
                              num_splits, workspace, static_cast<hipStream_t>(stream));
+}
+
+// ---------------------------------------------------------------------------
+// Paged KV cache (reference csrc/include/attn_paged_decode.cuh,
+// csrc/kernel/attn_paged_decode.cu)
+// ---------------------------------------------------------------------------
+namespace sl8 {
+namespace {
+
+// Quantize-on-write: one wave per (batch, KV head) row of the new token.
+// scale = amax / 127 (IEEE division), 1 for a zero row; code = rint(clamp(x /
+// scale, +-127)); stored at flat slot = block * bs + offset.
+template <int D>
+__global__ void __launch_bounds__(64)
+kv_write_paged_kernel(const uint16_t* __restrict__ k_new, const uint16_t* __restrict__ v_new,
+                      const int32_t* __restrict__ slot_mapping, int8_t* __restrict__ k_cache,
+                      float* __restrict__ k_scale, int8_t* __restrict__ v_cache,
+                      float* __restrict__ v_scale, int h_kv, int bs) {
+  constexpr int E = D / 64;  // elements per lane
+  const int lane = threadIdx.x;
+  const int64_t bh = blockIdx.x;
+  const int64_t b = bh / h_kv, h = bh % h_kv;
+  float kx[E], vx[E];
+  float ka = 0.f, va = 0.f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    kx[e] = h2f(k_new[bh * D + lane * E + e]);
+    vx[e] = h2f(v_new[bh * D + lane * E + e]);
+    ka = fmaxf(ka, fabsf(kx[e]));
+    va = fmaxf(va, fabsf(vx[e]));
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    ka = fmaxf(ka, __shfl_xor(ka, o, 64));
+    va = fmaxf(va, __shfl_xor(va, o, 64));
+  }
+  const float ks = ka > 0.f ? __fdiv_rn(ka, 127.f) : 1.f;
+  const float vs = va > 0.f ? __fdiv_rn(va, 127.f) : 1.f;
+  const int64_t slot = slot_mapping[b];
+  const int64_t row = ((slot / bs) * h_kv + h) * bs + slot % bs;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    k_cache[row * D + lane * E + e] = (int8_t)rintf(fminf(fmaxf(__fdiv_rn(kx[e], ks), -127.f), 127.f));
+    v_cache[row * D + lane * E + e] = (int8_t)rintf(fminf(fmaxf(__fdiv_rn(vx[e], vs), -127.f), 127.f));
+  }
+  if (lane == 0) {
+    k_scale[row] = ks;
+    v_scale[row] = vs;
+  }
+}
+
+}  // namespace
+}  // namespace sl8
+
+// Auto split count of the paged decode (reference attn_paged_decode.cu:14-31):
+// ~2048 (split, head) blocks, 48..256 keys per split, at most DEC_MAX_SPLITS.
+extern "C" int sl8_paged_choose_num_splits(int64_t n_len_max, int64_t bhq) {
+  if (n_len_max <= 0 || bhq <= 0) return 1;
+  const int64_t s_occ = (2048 + bhq - 1) / bhq;
+  const int64_t s_lo = (n_len_max + 255) / 256;
+  int64_t s_hi = (n_len_max + 47) / 48;
+  if (s_hi < 1) s_hi = 1;
+  int64_t s = s_occ > s_lo ? s_occ : s_lo;
+  if (s > s_hi) s = s_hi;
+  if (s < 1) s = 1;
+  if (s > DEC_MAX_SPLITS) s = DEC_MAX_SPLITS;
+  return (int)s;
+}
+
+extern "C" int sl8_attn_paged_decode(const int8_t* q, const float* q_scale, const int8_t* k_cache,
+                                     const float* k_scale, const int8_t* v_cache,
+                                     const float* v_scale, const int32_t* block_table,
+                                     const int32_t* context_lens, void* out, int64_t B,
+                                     int64_t Hq, int64_t Hkv, int64_t D, int64_t num_blocks,
+                                     int64_t block_size, int64_t max_blocks_per_seq,
+                                     int64_t max_context_len, int64_t num_splits,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  SL8_CHECK_ARG(B >= 0 && Hq >= 0 && Hkv > 0 && num_blocks >= 0 && block_size > 0 &&
+                    max_blocks_per_seq >= 0,
+                "fni8 paged_decode: bad shape");
+  SL8_CHECK_ARG(Hq % Hkv == 0, "fni8 paged_decode: H_q must be divisible by H_kv (GQA)");
+  SL8_CHECK_ARG(D == 64 || D == 128 || D == 256,
+                "fni8 paged_decode: head dim must be 64/128/256, got %lld", (long long)D);
+  SL8_CHECK_ARG(max_context_len >= 0 && max_context_len <= max_blocks_per_seq * block_size,
+                "fni8 paged_decode: max_context_len exceeds block_table capacity");
+  SL8_CHECK_ARG(B * Hq < (1LL << 31) && num_blocks * Hkv * block_size < (1LL << 40) &&
+                    max_context_len < (1LL << 31),
+                "fni8 paged_decode: shape too large");
+  const int64_t bhq = B * Hq;
+  if (num_splits < 0) num_splits = sl8_paged_choose_num_splits(max_context_len, bhq);
+  SL8_CHECK_ARG(num_splits >= 1 && num_splits <= DEC_MAX_SPLITS,
+                "fni8 paged_decode: num_splits must be 1..%d, got %lld", DEC_MAX_SPLITS,
+                (long long)num_splits);
+  if (B == 0 || Hq == 0) return SL8_OK;
+  SL8_CHECK_ARG(q && q_scale && block_table && context_lens && out &&
+                    (num_blocks == 0 || (k_cache && k_scale && v_cache && v_scale)),
+                "fni8 paged_decode: null pointer");
+  SL8_CHECK_ARG(aligned(q, 16) && aligned(k_cache, 16) && aligned(v_cache, 16),
+                "fni8 paged_decode: q/k_cache/v_cache must be 16-byte aligned");
+  const size_t need = sl8_attn_int8_decode_workspace(B, Hq, D, num_splits);
+  SL8_CHECK_ARG(workspace && workspace_bytes >= need && aligned(workspace, 16),
+                "fni8 paged_decode: workspace needs %zu bytes", need);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int ns = (int)num_splits, ibhq = (int)bhq, gsz = (int)(Hq / Hkv);
+  const int G = group_width(gsz);
+  float* op = static_cast<float*>(workspace);
+  float* mp = op + (size_t)ns * ibhq * D;
+  float* lp = mp + (size_t)ns * ibhq;
+  const dim3 grid((unsigned)ns, (unsigned)(B * Hkv), (unsigned)((gsz + G - 1) / G));
+  const PagedArgs pg{block_table, context_lens, (int)max_blocks_per_seq, (int)block_size};
+  const int nmax = (int)max_context_len;
+#define SL8_PAGED(DD)                                                                          \
+  launch_d<DD, true, true>(G, grid, q, q_scale, k_cache, k_scale, v_cache, v_scale, op, mp, lp, \
+                           nmax, ns, (int)Hq, (int)Hkv, gsz, ibhq, st, pg)
+  if (D == 64) SL8_PAGED(64);
+  else if (D == 128) SL8_PAGED(128);
+  else SL8_PAGED(256);
+#undef SL8_PAGED
+  SL8_CHECK_LAUNCH("attn_paged_decode split");
+  decode_combine_kernel<<<ibhq, (unsigned)(D < 256 ? D : 256), 0, st>>>(
+      op, mp, lp, static_cast<uint16_t*>(out), ns, ibhq, (int)D);
+  SL8_CHECK_LAUNCH("attn_paged_decode combine");
+  return SL8_OK;
+}
+
+extern "C" int sl8_kv_write_paged(const void* k_new, const void* v_new, const int32_t* slot_mapping,
+                                  int8_t* k_cache, float* k_scale, int8_t* v_cache, float* v_scale,
+                                  int64_t B, int64_t Hkv, int64_t D, int64_t num_blocks,
+                                  int64_t block_size, void* stream) {
+  clear_error();
+  SL8_CHECK_ARG(B >= 0 && Hkv > 0 && num_blocks >= 0 && block_size > 0,
+                "fni8 kv_write_paged: bad shape");
+  SL8_CHECK_ARG(D == 64 || D == 128 || D == 256,
+                "fni8 kv_write_paged: head dim must be 64/128/256, got %lld", (long long)D);
+  if (B == 0) return SL8_OK;
+  SL8_CHECK_ARG(k_new && v_new && slot_mapping && k_cache && k_scale && v_cache && v_scale,
+                "fni8 kv_write_paged: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)(B * Hkv));
+  const uint16_t* kn = static_cast<const uint16_t*>(k_new);
+  const uint16_t* vn = static_cast<const uint16_t*>(v_new);
+  if (D == 64) kv_write_paged_kernel<64><<<grid, 64, 0, st>>>(kn, vn, slot_mapping, k_cache, k_scale, v_cache, v_scale, (int)Hkv, (int)block_size);
+  else if (D == 128) kv_write_paged_kernel<128><<<grid, 64, 0, st>>>(kn, vn, slot_mapping, k_cache, k_scale, v_cache, v_scale, (int)Hkv, (int)block_size);
+  else kv_write_paged_kernel<256><<<grid, 64, 0, st>>>(kn, vn, slot_mapping, k_cache, k_scale, v_cache, v_scale, (int)Hkv, (int)block_size);
+  SL8_CHECK_LAUNCH("kv_write_paged");
+  return SL8_OK;
 }

@@ -3,6 +3,7 @@
 Same names, keyword arguments, routing and error behaviour as the reference
 wrappers (reference superl8/ops.py:70-175 attn_int8_fwd, :230-267
 attn_int8_decode, :531-584 quantize_kv_cache, :671-727 attn_decode_cached,
+:730-849 quantize_kv_write_paged / attn_paged_decode_cached,
 :975-991 quantize_i8_rowwise, :1254-1325 linear_q4k / _linear_kquant),
 dispatching to the gfx950 kernels through `_C`.
 """
@@ -130,6 +131,50 @@ def attn_decode_cached(q: torch.Tensor, k_i8: torch.Tensor, k_scale: torch.Tenso
     ns = -1 if num_splits is None else int(num_splits)
     return _C.attn_int8_decode_kv8(q_i8.contiguous(), q_scale, k_i8.contiguous(),
                                    k_scale.contiguous(), v_i8.contiguous(), v_scale.contiguous(), ns)
+
+
+def quantize_kv_write_paged(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor,
+                            k_scale: torch.Tensor, v_cache: torch.Tensor, v_scale: torch.Tensor,
+                            slot_mapping: torch.Tensor, *, rotate: bool = True) -> None:
+    """Quantise-on-write of one new token per sequence into the paged int8 KV pool,
+    in place (reference ops.py:730-775): per-token scales for K and V; `rotate`
+    applies the Hadamard rotation to K (the smoothing usable one token at a time)."""
+    from .quant.rotation import rotate_last
+
+    if rotate:
+        k_new = rotate_last(k_new)
+    _C.kv_write_paged(k_new.contiguous(), v_new.contiguous(), slot_mapping.contiguous(),
+                      k_cache, k_scale, v_cache, v_scale)
+
+
+def attn_paged_decode_cached(q: torch.Tensor, k_cache: torch.Tensor, k_scale: torch.Tensor,
+                             v_cache: torch.Tensor, v_scale: torch.Tensor,
+                             block_table: torch.Tensor, context_lens: torch.Tensor,
+                             block_size: int, *, max_context_len: int | None = None,
+                             scale: float | None = None, rotate: bool = True,
+                             num_splits: int | None = None) -> torch.Tensor:
+    """Decode (M=1) against a paged int8 KV cache (reference ops.py:778-849): one
+    launch for a batch of mixed-length sequences. `rotate` must match the flag the
+    cache was written with; max_context_len defaults to max(context_lens) (a host sync)."""
+    from .quant import LOG2E
+    from .quant.rotation import rotate_last
+
+    if q.shape[-2] != 1:
+        raise AssertionError(f"paged decode expects M=1, got M={q.shape[-2]}")
+    if max_context_len is None:
+        max_context_len = int(context_lens.max().item())
+    softmax_scale = (1.0 / (q.shape[-1] ** 0.5)) if scale is None else scale
+    if rotate:
+        q = rotate_last(q)
+    q_shape = q.shape
+    q_i8, q_scale = quantize_i8_rowwise(q.reshape(-1, q_shape[-1]).contiguous())
+    q_i8 = q_i8.reshape(q_shape)
+    q_scale = (q_scale.float() * (softmax_scale * LOG2E)).reshape(q_shape[0], q_shape[1], 1).contiguous()
+    ns = -1 if num_splits is None else int(num_splits)
+    return _C.attn_paged_decode(q_i8.contiguous(), q_scale, k_cache.contiguous(),
+                                k_scale.contiguous(), v_cache.contiguous(), v_scale.contiguous(),
+                                block_table.contiguous(), context_lens.contiguous(),
+                                int(block_size), int(max_context_len), ns)
 
 
 def quantize_i8_rowwise(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:

@@ -148,3 +148,122 @@ def test_decode_cached_rejects(device):
     k_i8, ks, v_i8, vs = sl8.quantize_kv_cache(k, v)
     with pytest.raises(RuntimeError, match="int8"):
         _C.attn_int8_decode_kv8(k_i8[:, :, :1], ks[:, :, :1], k_i8, ks, v.contiguous(), vs)
+
+
+# ---------------------------------------------------------------------------
+# Paged int8 KV cache (reference attn_paged_decode.cuh, ops.py:730-849)
+# ---------------------------------------------------------------------------
+from oracle import quant as oqn  # noqa: E402
+
+PAGED_CASES = [  # B, Hq, Hkv, D, block_size, lens
+    (2, 8, 2, 64, 16, (50, 7)), (3, 32, 8, 128, 16, (1000, 1, 333)), (1, 16, 4, 256, 32, (257,)),
+    (2, 8, 8, 128, 64, (64, 0)), (4, 12, 4, 64, 8, (9, 100, 31, 64)), (1, 32, 1, 128, 16, (600,)),
+]
+
+
+def _paged_cache(case, device, seed=0):
+    B, Hq, Hkv, D, bs, lens = case
+    g = torch.Generator().manual_seed(seed)
+    nb_seq = [max(1, (n + bs - 1) // bs) for n in lens]
+    nblk = sum(nb_seq) + 3
+    kc = torch.randint(-127, 128, (nblk, Hkv, bs, D), generator=g, dtype=torch.int8)
+    vc = torch.randint(-127, 128, (nblk, Hkv, bs, D), generator=g, dtype=torch.int8)
+    ks = torch.rand(nblk, Hkv, bs, generator=g) * 0.02 + 1e-3
+    vs = torch.rand(nblk, Hkv, bs, generator=g) * 0.02 + 1e-3
+    perm = torch.randperm(nblk, generator=g)
+    bt = torch.zeros(B, max(nb_seq), dtype=torch.int32)
+    used = 0
+    for b, nb in enumerate(nb_seq):
+        bt[b, :nb] = perm[used:used + nb]
+        used += nb
+    q = torch.randint(-127, 128, (B, Hq, 1, D), generator=g, dtype=torch.int8)
+    qs = torch.rand(B, Hq, 1, generator=g) * 0.01 + 1e-3
+    ctx = torch.tensor(lens, dtype=torch.int32)
+    return [t.to(device) for t in (q, qs, kc, ks, vc, vs, bt, ctx)]
+
+
+@pytest.mark.parametrize("case", PAGED_CASES)
+@pytest.mark.parametrize("ns", [-1, 1, 7])
+def test_paged_kernel_matches_oracle(device, case, ns):
+    B, Hq, Hkv, D, bs, lens = case
+    q, qs, kc, ks, vc, vs, bt, ctx = _paged_cache(case, device)
+    nmax = max(lens)
+    out = _C.attn_paged_decode(q, qs, kc, ks, vc, vs, bt, ctx, bs, nmax, ns)
+    n_splits = ns if ns > 0 else _C.paged_choose_n_splits(nmax, B * Hq)
+    assert n_splits == oa.paged_choose_num_splits(nmax, B * Hq) or ns > 0
+    ref = oa.attn_paged_decode(_np(q)[:, :, 0], _np(qs)[:, :, 0], _np(kc), _np(ks), _np(vc),
+                               _np(vs), _np(bt), _np(ctx), nmax, n_splits)
+    assert out.shape == (B, Hq, 1, D) and out.dtype == torch.float16
+    assert_close_abs(out[:, :, 0], ref, atol=2e-3, rtol=2e-3, what=f"paged {case} ns={ns}")
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_kv_write_paged_bit_exact(device, D):
+    B, Hkv, nblk, bs = 3, 4, 5, 8
+    g = torch.Generator().manual_seed(D)
+    kn = (torch.randn(B, Hkv, D, generator=g) * 3).half()
+    vn = torch.randn(B, Hkv, D, generator=g).half()
+    kn[1, 2] = 0  # a zero row: scale 1, codes 0
+    slots = torch.tensor([3, 8 * 4 + 7, 8 * 2], dtype=torch.int32)
+    kc = torch.full((nblk, Hkv, bs, D), 5, dtype=torch.int8)
+    vc = kc.clone()
+    ks = torch.full((nblk, Hkv, bs), -1.0)
+    vs = ks.clone()
+    tens = [t.to(device) for t in (kn, vn, slots, kc, ks, vc, vs)]
+    _C.kv_write_paged(*tens)
+    rk, rks, rv, rvs = _np(kc).copy(), _np(ks).copy(), _np(vc).copy(), _np(vs).copy()
+    oqn.kv_write_paged(_np(kn.float()), _np(vn.float()), _np(slots), rk, rks, rv, rvs)
+    np.testing.assert_array_equal(_np(tens[3]), rk)
+    np.testing.assert_array_equal(_np(tens[4]), rks)
+    np.testing.assert_array_equal(_np(tens[5]), rv)
+    np.testing.assert_array_equal(_np(tens[6]), rvs)
+
+
+@pytest.mark.parametrize("D,lens", [(128, (40, 97, 1)), (64, (130,))])
+def test_paged_end_to_end(device, D, lens):
+    """Token-by-token quantize-on-write into a shuffled block pool, then one paged
+    decode for the ragged batch: the reference's int8 quality bars against fp64
+    attention on the fp16 K/V (per-token V, rotated K)."""
+    B, Hq, Hkv, bs = len(lens), 8, 2, 16
+    nmax = max(lens)
+    nb_seq = [(n + bs - 1) // bs for n in lens]
+    nblk = sum(nb_seq) + 2
+    perm = torch.randperm(nblk, generator=torch.Generator().manual_seed(1))
+    bt = torch.zeros(B, max(nb_seq), dtype=torch.int32)
+    used = 0
+    for b, nb in enumerate(nb_seq):
+        bt[b, :nb] = perm[used:used + nb]
+        used += nb
+    bt = bt.to(device)
+    kc = torch.zeros(nblk, Hkv, bs, D, dtype=torch.int8, device=device)
+    vc = torch.zeros_like(kc)
+    ks = torch.zeros(nblk, Hkv, bs, device=device)
+    vs = torch.zeros_like(ks)
+    k = torch.randn(B, Hkv, nmax, D, device=device, dtype=torch.float16)
+    v = torch.randn(B, Hkv, nmax, D, device=device, dtype=torch.float16)
+    for t in range(nmax):
+        rows = [b for b in range(B) if t < lens[b]]
+        idx = torch.tensor(rows, device=device)
+        slots = torch.tensor([int(bt[b, t // bs]) * bs + t % bs for b in rows], dtype=torch.int32,
+                             device=device)
+        sl8.quantize_kv_write_paged(k[idx, :, t].contiguous(), v[idx, :, t].contiguous(), kc, ks,
+                                    vc, vs, slots)
+    q = torch.randn(B, Hq, 1, D, device=device, dtype=torch.float16)
+    ctx = torch.tensor(lens, dtype=torch.int32, device=device)
+    out = sl8.attn_paged_decode_cached(q, kc, ks, vc, vs, bt, ctx, bs, max_context_len=nmax)
+    assert_finite(out)
+    for b, n in enumerate(lens):
+        ref = oa.attention_fp64(_np(q[b:b + 1].float()), _np(k[b:b + 1, :, :n].float()),
+                                _np(v[b:b + 1, :, :n].float()))
+        assert_int8_quality(out[b:b + 1], ref, min_cos=0.998, max_rel_l1=0.03, min_sqnr_db=18,
+                            what=f"paged e2e b={b} n={n}")
+
+
+def test_paged_rejects(device):
+    q, qs, kc, ks, vc, vs, bt, ctx = _paged_cache(PAGED_CASES[0], device)
+    with pytest.raises(RuntimeError, match="block_size"):
+        _C.attn_paged_decode(q, qs, kc, ks, vc, vs, bt, ctx, 8, 50)
+    with pytest.raises(RuntimeError, match="capacity"):
+        _C.attn_paged_decode(q, qs, kc, ks, vc, vs, bt, ctx, 16, 10 ** 6)
+    with pytest.raises(RuntimeError, match="int32"):
+        _C.attn_paged_decode(q, qs, kc, ks, vc, vs, bt.long(), ctx, 16, 50)

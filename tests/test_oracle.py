@@ -299,3 +299,118 @@ def test_w8a8_p_requant_known_answer():
     c1 = np.rint(np.float32(np.float32(p1) * inv))
     want = (127 * 10 + float(c1) * -20) * float(ps) / (1.0 + p1)
     assert abs(out[0, 0, 0, 0] - want) < 1e-9
+
+
+# ---------------------------------------------------------------------------
+# Paged decode and quantize-on-write (reference attn_paged_decode.cuh)
+# ---------------------------------------------------------------------------
+def _paged_case(B=2, Hq=8, Hkv=2, D=64, bs=16, lens=(50, 50), nblk=12, seed=21, perm=True):
+    rng = np.random.default_rng(seed)
+    maxb = max((n + bs - 1) // bs for n in lens)
+    k_cache = rng.integers(-127, 128, (nblk, Hkv, bs, D)).astype(np.int8)
+    v_cache = rng.integers(-127, 128, (nblk, Hkv, bs, D)).astype(np.int8)
+    k_scale = (rng.random((nblk, Hkv, bs)) * 0.02 + 1e-3).astype(np.float32)
+    v_scale = (rng.random((nblk, Hkv, bs)) * 0.02 + 1e-3).astype(np.float32)
+    blocks = rng.permutation(nblk) if perm else np.arange(nblk)
+    bt = np.zeros((B, maxb), np.int32)
+    used = 0
+    for b, n in enumerate(lens):
+        nb = (n + bs - 1) // bs
+        bt[b, :nb] = blocks[used:used + nb]
+        used += nb
+    q = rng.integers(-127, 128, (B, Hq, D)).astype(np.int8)
+    qs = (rng.random((B, Hq)) * 0.01 + 1e-3).astype(np.float32)
+    return q, qs, k_cache, k_scale, v_cache, v_scale, bt, np.array(lens, np.int32)
+
+
+@pytest.mark.parametrize("ns", [1, 3, 16])
+def test_paged_decode_equals_contiguous(ns):
+    """Equal lengths: gathering through a permuted block table gives the contiguous
+    decode of the gathered cache with the per-token V scale applied to V."""
+    q, qs, kc, ksc, vc, vsc, bt, lens = _paged_case(lens=(50, 50))
+    got = oa.attn_paged_decode(q, qs, kc, ksc, vc, vsc, bt, lens, 50, ns)
+    bs = kc.shape[2]
+    for b in range(2):
+        blk = bt[b, np.arange(50) // bs]
+        off = np.arange(50) % bs
+        k = np.swapaxes(kc[blk, :, off], 0, 1)[None]          # [1,Hkv,50,D]
+        ks = np.swapaxes(ksc[blk, :, off], 0, 1)[None]
+        v = (np.swapaxes(vc[blk, :, off], 0, 1).astype(np.float64)
+             * np.swapaxes(vsc[blk, :, off], 0, 1)[..., None])[None]
+        ref = oa.attn_int8_decode(q[b:b + 1], qs[b:b + 1], k, ks, v, ns)
+        np.testing.assert_allclose(got[b:b + 1], ref, rtol=1e-9, atol=1e-12)
+
+
+def test_paged_decode_ragged_lengths_and_block_order():
+    """Ragged lengths: each sequence sees exactly its own keys (one split = plain
+    softmax over them), and the physical block order does not matter."""
+    q, qs, kc, ksc, vc, vsc, bt, lens = _paged_case(lens=(7, 61), perm=False, seed=23)
+    a = oa.attn_paged_decode(q, qs, kc, ksc, vc, vsc, bt, lens, 61, 1)
+    for b, n in enumerate(lens):
+        kb = oa.gather_paged(kc, bt, b, n)[None]
+        ksb = oa.gather_paged(ksc, bt, b, n)[None]
+        vb = (oa.gather_paged(vc, bt, b, n).astype(np.float64)
+              * oa.gather_paged(vsc, bt, b, n)[..., None])[None]
+        ref = oa.attn_int8_decode(q[b:b + 1], qs[b:b + 1], kb, ksb, vb, 1)
+        np.testing.assert_allclose(a[b:b + 1], ref, rtol=1e-9, atol=1e-12)
+    # move every block to another physical slot: same result
+    nblk = kc.shape[0]
+    perm = np.random.default_rng(5).permutation(nblk)
+    kc2, ksc2, vc2, vsc2 = (np.empty_like(x) for x in (kc, ksc, vc, vsc))
+    kc2[perm], ksc2[perm], vc2[perm], vsc2[perm] = kc, ksc, vc, vsc
+    b2 = oa.attn_paged_decode(q, qs, kc2, ksc2, vc2, vsc2, perm[bt].astype(np.int32), lens, 61, 4)
+    b1 = oa.attn_paged_decode(q, qs, kc, ksc, vc, vsc, bt, lens, 61, 4)
+    np.testing.assert_allclose(b2, b1, rtol=0, atol=0)
+
+
+def test_paged_split_heuristic():
+    """reference attn_paged_decode.cu:20-31 on hand-evaluated cases."""
+    assert oa.paged_choose_num_splits(0, 8) == 1
+    assert oa.paged_choose_num_splits(32768, 512) == 128    # max(4, 128) within [1, 683]
+    assert oa.paged_choose_num_splits(100, 8) == 3          # min(256, 3)
+    assert oa.paged_choose_num_splits(4096, 1) == 86        # min(2048, ceil(4096/48))
+    assert oa.paged_choose_num_splits(10 ** 6, 1) == 256
+
+
+def test_kv_write_quantiser_known_answers():
+    from fractions import Fraction
+
+    x = np.zeros((3, 8), np.float32)
+    x[1, 3] = -0.75
+    rng = np.random.default_rng(3)
+    x[2] = rng.standard_normal(8).astype(np.float32)
+    q, s = oqn.quantize_row_div(x)
+    assert s[0] == 1.0 and not q[0].any()
+    assert s[1] == np.float32(np.float32(0.75) / np.float32(127)) and q[1, 3] == -127 and q[1].sum() == -127
+    # codes = round-half-even of the correctly rounded fp32 quotient (exact rationals)
+    for r in range(3):
+        for c in range(8):
+            quo = np.float32(Fraction(float(x[r, c])) / Fraction(float(s[r])))
+            want = int(np.rint(np.clip(quo, -127, 127)))
+            assert q[r, c] == want
+    # the scale is amax / 127, not amax * fp32(1/127) as in quantize_rows: the two
+    # differ by an ulp on some rows, so a swapped formula fails here
+    xs = rng.standard_normal((4000, 64)).astype(np.float32)
+    _, sd = oqn.quantize_row_div(xs)
+    _, sm = oqn.quantize_rows(xs)
+    amax = np.abs(xs).max(-1)
+    np.testing.assert_array_equal(sd, (amax / np.float32(127)).astype(np.float32))
+    assert (sd != sm.reshape(sd.shape)).any()
+
+
+def test_kv_write_paged_places_rows():
+    kc = np.zeros((4, 2, 8, 16), np.int8)
+    vc = np.zeros_like(kc)
+    ks = np.zeros((4, 2, 8), np.float32)
+    vs = np.zeros_like(ks)
+    rng = np.random.default_rng(8)
+    kn = rng.standard_normal((3, 2, 16)).astype(np.float32)
+    vn = rng.standard_normal((3, 2, 16)).astype(np.float32)
+    slots = np.array([5, 8 * 3 + 7, 8], np.int32)
+    oqn.kv_write_paged(kn, vn, slots, kc, ks, vc, vs)
+    kq, kscl = oqn.quantize_row_div(kn)
+    for b, slot in enumerate(slots):
+        blk, off = divmod(int(slot), 8)
+        np.testing.assert_array_equal(kc[blk, :, off], kq[b])
+        np.testing.assert_array_equal(ks[blk, :, off], kscl[b])
+    assert np.count_nonzero(ks) == 3 * 2
