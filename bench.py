@@ -335,6 +335,11 @@ def main():
         sec["attn_int8_decode_kv8_cfg3shape"] = {"us": round(kms * 1e3, 2), "GB/s": round(gbs, 1),
                                                  "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
                                                  "bytes": kbytes}
+        pms, pbytes = bench_paged_decode()
+        gbs = pbytes / (pms * 1e-3) / 1e9
+        sec["attn_paged_decode_cfg3shape_bs16"] = {"us": round(pms * 1e3, 2), "GB/s": round(gbs, 1),
+                                                   "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+                                                   "bytes": pbytes}
         for M in (1, 8):
             gms, gbytes = bench_gemv(M)
             gbs = gbytes / (gms * 1e-3) / 1e9

@@ -54,7 +54,10 @@ struct PagedArgs {
   const int32_t* bt;   // [B, maxb] physical block per logical block
   const int32_t* ctx;  // [B] keys per sequence
   int maxb, bs;
+  int bs_sh;           // log2(bs) (streaming kernel: bs a power of two)
 };
+// block-table entries of one split staged in LDS by the streaming paged kernel
+constexpr int DEC_BT_MAX = 1024;
 
 template <int D, int G, bool VI8, bool PG>
 __global__ void __launch_bounds__(DEC_THREADS)
@@ -324,7 +327,7 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-template <int D, int GS, bool VI8 = false>
+template <int D, int GS, bool VI8 = false, bool PG = false>
 struct WaveCfg {
   static constexpr int KL = 64 / GS;                  // lanes (keys) per head per sub-block
   static constexpr int SUB = KL >= 16 ? 1 : 16 / KL;  // sub-blocks per tile
@@ -339,20 +342,25 @@ struct WaveCfg {
   static constexpr int VRB = VI8 ? D : 2 * D;  // bytes per V row
   static constexpr int KBYTES = T * D, VBYTES = T * VRB;
   static constexpr int KDMA = KBYTES / 1024, VDMA = VBYTES / 1024;  // 1 KiB copies per wave
-  static constexpr int STAGE = KBYTES + VBYTES + 256;               // + k_scale (64 floats)
+  // + k_scale (64 floats), + the per-token v_scale of a paged cache
+  static constexpr int STAGE = KBYTES + VBYTES + (PG ? 512 : 256);
   static_assert(KDMA >= 1 && KBYTES % 1024 == 0, "tile copy granularity");
   static_assert(CPL % 8 == 0 || CPL == 4, "PV slice: 4 or a multiple of 8 channels");
 };
 
-template <int D, int GS, int NB, bool VI8>
+// PG: paged int8 cache (see PagedArgs): the split's block-table entries are
+// staged in LDS, every copy lane maps its key to a physical row, and the
+// per-token V scale multiplies p before it is broadcast to the PV lanes.
+template <int D, int GS, int NB, bool VI8, bool PG>
 __global__ void __launch_bounds__(DEC_THREADS)
 decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_scale,
                    const int8_t* __restrict__ k, const float* __restrict__ k_scale,
                    const void* __restrict__ v, const float* __restrict__ vsc,
                    float* __restrict__ o_part,
                    float* __restrict__ m_part, float* __restrict__ l_part, int n_len,
-                   int n_splits, int h_q, int h_kv, int bhq) {
-  using C = WaveCfg<D, GS, VI8>;
+                   int n_splits, int h_q, int h_kv, int bhq, const PagedArgs pg) {
+  static_assert(!PG || VI8, "the paged cache holds int8 V");
+  using C = WaveCfg<D, GS, VI8, PG>;
   constexpr int KL = C::KL, SUB = C::SUB, T = C::T, CPL = C::CPL, KC = C::KC, KSW = C::KSW;
   constexpr int KSH = C::KSH;
   constexpr int STAGE = C::STAGE;
@@ -377,12 +385,27 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
   const int b = bkv / h_kv, kvh = bkv % h_kv;
   const int per = (n_len + n_splits - 1) / n_splits;
   const int n0 = split * per;
-  const int n1 = min(n_len, n0 + per);
+  const int n1 = min(PG ? pg.ctx[b] : n_len, n0 + per);
   const int ntiles = n1 > n0 ? (n1 - n0 + T - 1) / T : 0;
   const int nt = ntiles > wave ? (ntiles - wave + DEC_WAVES - 1) / DEC_WAVES : 0;  // this wave's
-  const int8_t* kb = k + (int64_t)bkv * n_len * D;
-  const float* ksb = k_scale + (int64_t)bkv * n_len;
-  const uint8_t* vb = static_cast<const uint8_t*>(v) + (int64_t)bkv * n_len * C::VRB;
+  const int8_t* kb = k + (PG ? 0 : (int64_t)bkv * n_len * D);
+  const float* ksb = k_scale + (PG ? 0 : (int64_t)bkv * n_len);
+  const uint8_t* vb = static_cast<const uint8_t*>(v) + (PG ? 0 : (int64_t)bkv * n_len * C::VRB);
+  __shared__ int32_t sm_bt[PG ? DEC_BT_MAX : 1];
+  const int first_blk = PG ? (n0 >> pg.bs_sh) : 0;
+  if constexpr (PG) {
+    const int nbt = n1 > n0 ? ((n1 - 1) >> pg.bs_sh) - first_blk + 1 : 0;
+    const int32_t* btb = pg.bt + (int64_t)b * pg.maxb + first_blk;
+    for (int i = threadIdx.x; i < nbt; i += DEC_THREADS) sm_bt[i] = btb[i];
+    __syncthreads();
+  }
+  // cache row of key n (clamped into the split; the repeated rows are never used)
+  auto crow = [&](int n) -> int64_t {
+    n = min(n, n1 - 1);
+    if constexpr (PG)
+      return ((int64_t)sm_bt[(n >> pg.bs_sh) - first_blk] * h_kv + kvh) * pg.bs + (n & (pg.bs - 1));
+    else return n;
+  };
 
   const int h = lane / KL, kl = lane % KL;
   const int64_t hq = (int64_t)b * h_q + (int64_t)kvh * GS + h;
@@ -401,22 +424,25 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
     for (int j = 0; j < C::KDMA; ++j) {
       const int id = j * 64 + lane, row = id / KC;
       const int c = (id % KC) ^ ((row >> KSH) & KSW);
-      __builtin_amdgcn_global_load_lds((gptr_t)(kb + (int64_t)min(base + row, n_len - 1) * D + 16 * c),
+      __builtin_amdgcn_global_load_lds((gptr_t)(kb + crow(base + row) * D + 16 * c),
                                        (lptr_t)(sb + j * 1024), 16, 0, 0);
     }
 #pragma unroll
     for (int j = 0; j < C::VDMA; ++j) {
       const int id = j * 64 + lane, row = id / (C::VRB / 16);
       __builtin_amdgcn_global_load_lds(
-          (gptr_t)(vb + (int64_t)min(base + row, n_len - 1) * C::VRB + 16 * (id % (C::VRB / 16))),
+          (gptr_t)(vb + crow(base + row) * C::VRB + 16 * (id % (C::VRB / 16))),
           (lptr_t)(sb + C::KBYTES + j * 1024), 16, 0, 0);
     }
     // lanes past the tile repeat its keys (same cache lines: no extra traffic)
-    __builtin_amdgcn_global_load_lds((gptr_t)(ksb + min(base + (lane % T), n_len - 1)),
-                                     (lptr_t)(sb + C::KBYTES + C::VBYTES), 4, 0, 0);
+    const int64_t sr = crow(base + (lane % T));
+    __builtin_amdgcn_global_load_lds((gptr_t)(ksb + sr), (lptr_t)(sb + C::KBYTES + C::VBYTES), 4, 0, 0);
+    if constexpr (PG)
+      __builtin_amdgcn_global_load_lds((gptr_t)(vsc + sr), (lptr_t)(sb + C::KBYTES + C::VBYTES + 256),
+                                       4, 0, 0);
   };
 
-  float m_run = -INFINITY, l_lane = 0.f, oacc[CPL];
+  float m_run = -INFINITY, l_lane = 0.f, lv_lane = 0.f, oacc[CPL];  // lv: sum of p * v_scale (PG)
 #pragma unroll
   for (int e = 0; e < CPL; ++e) oacc[e] = 0.f;
 
@@ -454,6 +480,17 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
       ps += p[u];
     }
     l_lane = l_lane * resc + ps;
+    if constexpr (PG) {
+      // per-token V scale: PV uses p * v_scale[key]
+      const float* vst = kst + 64;
+      float pvs = 0.f;
+#pragma unroll
+      for (int u = 0; u < SUB; ++u) {
+        p[u] *= vst[u * KL + kl];
+        pvs += p[u];
+      }
+      lv_lane = lv_lane * resc + pvs;
+    }
 #pragma unroll
     for (int e = 0; e < CPL; ++e) oacc[e] *= resc;
 #pragma unroll
@@ -514,10 +551,10 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
     }
   };
 
-  // Copies per tile per lane: KDMA + VDMA + 1, all from this wave. Before
+  // Copies per tile per lane: KDMA + VDMA + 1 (+1 paged), all from this wave. Before
   // tile i is read, wait until only the copies of tiles i+1 .. i+NB-2 (issued
   // later) may still be in flight; vmcnt retires in issue order.
-  constexpr int AHEAD = (NB - 1) * (C::KDMA + C::VDMA + 1);
+  constexpr int AHEAD = (NB - 1) * (C::KDMA + C::VDMA + (PG ? 2 : 1));
   static_assert(AHEAD < 64, "vmcnt range");
   constexpr unsigned WAIT_AHEAD = 0x0F70u | (AHEAD & 15) | ((AHEAD >> 4) << 14);
   // The Q loads above were issued before any copy, so the in-order vmcnt waits
@@ -545,7 +582,13 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
   // ---- per-wave state -> LDS (this wave's own stage-0 area), then LSE merge ----
 #pragma unroll
   for (int o = 1; o < KL; o <<= 1) l_lane += __shfl_xor(l_lane, o, 64);
-  if constexpr (VI8) {
+  if constexpr (PG) {
+    // remove the 1152 offset per key, weighted like the p that entered PV
+#pragma unroll
+    for (int o = 1; o < KL; o <<= 1) lv_lane += __shfl_xor(lv_lane, o, 64);
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) oacc[e] -= 1152.f * lv_lane;
+  } else if constexpr (VI8) {
     // remove the 1152 offset per key (l_lane is now the head's sum of p,
     // rescaled exactly like oacc) and fold in the per-channel scale
 #pragma unroll
@@ -602,7 +645,7 @@ template <int D, bool VI8, bool PG = false>
 void launch_d(int G, dim3 grid, const int8_t* q, const float* qs, const int8_t* k,
               const float* ks, const void* v, const float* vsc, float* op, float* mp, float* lp,
               int N, int ns, int hq, int hkv, int gsz, int bhq, hipStream_t st,
-              const PagedArgs& pg = PagedArgs{nullptr, nullptr, 0, 1}) {
+              const PagedArgs& pg = PagedArgs{nullptr, nullptr, 0, 1, 0}) {
 #define SL8_SPLIT(GG) \
   launch_split<D, GG, VI8, PG>(grid, q, qs, k, ks, v, vsc, op, mp, lp, N, ns, hq, hkv, gsz, bhq, pg, st)
   switch (G) {
@@ -657,9 +700,9 @@ int decode_launch(const int8_t* q, const float* q_scale, const int8_t* k, const 
   if ((gsz == 2 && D == 128) || gsz == 4 || gsz == 8) {
     const dim3 g2((unsigned)ns, (unsigned)(B * Hkv));
 #define SL8_WAVE(DD, GS, NB)                                                                     \
-    decode_wave_kernel<DD, GS, NB, VI8><<<g2, DEC_THREADS, 0, st>>>(q, q_scale, k, k_scale, v, vsc, \
-                                                                  op, mp, lp, (int)N, ns, (int)Hq, \
-                                                                  (int)Hkv, bhq)
+    decode_wave_kernel<DD, GS, NB, VI8, false><<<g2, DEC_THREADS, 0, st>>>(                    \
+        q, q_scale, k, k_scale, v, vsc, op, mp, lp, (int)N, ns, (int)Hq, (int)Hkv, bhq,       \
+        PagedArgs{nullptr, nullptr, 0, 1, 0})
 #define SL8_WAVE_D(GS)                         \
     if (D == 64) SL8_WAVE(64, GS, 4);          \
     else if (D == 128) SL8_WAVE(128, GS, 3);   \
@@ -848,15 +891,40 @@ extern "C" int sl8_attn_paged_decode(const int8_t* q, const float* q_scale, cons
   float* mp = op + (size_t)ns * ibhq * D;
   float* lp = mp + (size_t)ns * ibhq;
   const dim3 grid((unsigned)ns, (unsigned)(B * Hkv), (unsigned)((gsz + G - 1) / G));
-  const PagedArgs pg{block_table, context_lens, (int)max_blocks_per_seq, (int)block_size};
+  int bs_sh = 0;
+  while ((1LL << bs_sh) < block_size) ++bs_sh;
+  const bool pow2 = (1LL << bs_sh) == block_size;
+  const PagedArgs pg{block_table, context_lens, (int)max_blocks_per_seq, (int)block_size, bs_sh};
   const int nmax = (int)max_context_len;
+  const int64_t per = (max_context_len + ns - 1) / ns;
+  const bool stream_ok = pow2 && per / block_size + 2 <= DEC_BT_MAX &&
+                         ((gsz == 2 && D == 128) || gsz == 4 || gsz == 8);
+  if (stream_ok) {
+    const dim3 g2((unsigned)ns, (unsigned)(B * Hkv));
+#define SL8_PWAVE(DD, GS, NB)                                                                   \
+    decode_wave_kernel<DD, GS, NB, true, true><<<g2, DEC_THREADS, 0, st>>>(                      \
+        q, q_scale, k_cache, k_scale, v_cache, v_scale, op, mp, lp, nmax, ns, (int)Hq, (int)Hkv, \
+        ibhq, pg)
+#define SL8_PWAVE_D(GS)                        \
+    if (D == 64) SL8_PWAVE(64, GS, 4);         \
+    else if (D == 128) SL8_PWAVE(128, GS, 3);  \
+    else SL8_PWAVE(256, GS, 3);
+    switch (gsz) {
+      case 2: SL8_PWAVE(128, 2, 3); break;
+      case 4: SL8_PWAVE_D(4); break;
+      default: SL8_PWAVE_D(8); break;
+    }
+#undef SL8_PWAVE_D
+#undef SL8_PWAVE
+  } else {
 #define SL8_PAGED(DD)                                                                          \
-  launch_d<DD, true, true>(G, grid, q, q_scale, k_cache, k_scale, v_cache, v_scale, op, mp, lp, \
-                           nmax, ns, (int)Hq, (int)Hkv, gsz, ibhq, st, pg)
-  if (D == 64) SL8_PAGED(64);
-  else if (D == 128) SL8_PAGED(128);
-  else SL8_PAGED(256);
+    launch_d<DD, true, true>(G, grid, q, q_scale, k_cache, k_scale, v_cache, v_scale, op, mp, lp, \
+                             nmax, ns, (int)Hq, (int)Hkv, gsz, ibhq, st, pg)
+    if (D == 64) SL8_PAGED(64);
+    else if (D == 128) SL8_PAGED(128);
+    else SL8_PAGED(256);
 #undef SL8_PAGED
+  }
   SL8_CHECK_LAUNCH("attn_paged_decode split");
   decode_combine_kernel<<<ibhq, (unsigned)(D < 256 ? D : 256), 0, st>>>(
       op, mp, lp, static_cast<uint16_t*>(out), ns, ibhq, (int)D);
