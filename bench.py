@@ -168,6 +168,23 @@ def bench_paged_decode(iters=20, bs=16):
     return ms, nbytes
 
 
+def bench_gemm_prefill(M=512, iters=10):
+    """Q4_K prefill GEMM (M > 16: the tiled MFMA kernel) on config 4's weights."""
+    from oracle import q4k as oq  # synthetic GGUF bytes generator (data only)
+    from superl8_amd import _C
+
+    dev = "cuda"
+    N, K = 17408, 5120
+    w = torch.from_numpy(oq.random_weights(N, K, seed=4)).to(dev)
+    g = torch.Generator(device=dev).manual_seed(9)
+    x = torch.randn(M, K, device=dev, dtype=torch.float16, generator=g)
+    x_i8, xs = _C.quantize_i8_rowwise(x)
+    fn = lambda: _C.gemm_q4k(x_i8, xs, w)  # noqa: E731
+    spin_up(fn, 0.1)
+    ms = _events_time(fn, iters, torch.cuda.current_stream())
+    return ms, 2 * M * N * K
+
+
 def bench_w8a8(iters=5):
     """Full-W8A8 prefill at BASELINE config 5: Q/K/V [2, 16|2, 8192, 256], causal,
     1% of Q/K channels (3 of 256, fixed) scaled by 20, V per-channel int8."""
@@ -346,6 +363,11 @@ def main():
             sec[f"gemm_decode_q4k_cfg4_m{M}"] = {"us": round(gms * 1e3, 2), "GB/s": round(gbs, 1),
                                                  "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
                                                  "bytes": gbytes}
+        pms2, pops = bench_gemm_prefill()
+        pt = pops / (pms2 * 1e-3) / 1e12
+        sec["gemm_q4k_prefill_m512_cfg4w"] = {"us": round(pms2 * 1e3, 1), "TOPS": round(pt, 1),
+                                              "frac_int8_peak": round(pt / PEAK_INT8_TOPS, 4),
+                                              "ops": pops}
         wms, wops = bench_w8a8()
         wt = wops / (wms * 1e-3) / 1e12
         sec["attn_w8a8_fwd_cfg5"] = {"us": round(wms * 1e3, 1), "TOPS": round(wt, 1),

@@ -402,6 +402,165 @@ gemv_q4k_small_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_
   }
 }
 
+// ---------------------------------------------------------------------------
+// Tiled Q4_K GEMM for M > 16 (prefill; reference csrc/include/gemm_q4k_dp4a.cuh:
+// 60-199, csrc/kernel/gemm_dp4a.cu:146-193): a 128 x 128 output tile per
+// workgroup, 4 waves of 64 x 64 (2 x 2 blocks of 32 x 32). Per super-block the
+// x tile (128 x 256 int8) and the 128 weight super-blocks (144 B each) are
+// copied global -> LDS one super-block ahead (double-buffered). The products
+// stay exact integers on v_mfma_i32_32x32x32_i8, one MFMA per 32-element
+// sub-block j (K = 32):
+//   T_j = <x_j, q_j * sc_j> with the 6-bit sc_j split in 3-bit halves so each
+//         B operand fits int8: q * (sc & 7) and q * (sc >> 3) (<= 105; one
+//         32-bit multiply scales 4 nibbles at once, no carries), combined as
+//         T_lo + 8 T_hi;
+//   U_j = <x_j, m_j> with m_j broadcast in the B operand (the min term);
+// and once per super-block f += d * (T_lo + 8 T_hi) - dmin * U (fp32).
+// x chunks are XOR-swizzled in LDS by row (rows are 256 B = one bank line);
+// weight rows are 144 B apart, which already spreads 16 rows over all banks.
+// ---------------------------------------------------------------------------
+constexpr int TBM = 128, TBN = 128;  // output tile
+constexpr int TWCH = (TBN * 9 + 255) / 256 * 256;  // weight-tile 16-B chunks, padded to whole copies
+
+template <int OUT_DT>
+__global__ void __launch_bounds__(256, 1)
+gemm_q4k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
+                     const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K) {
+  __shared__ __attribute__((aligned(16))) int8_t xs0[TBM * 256];
+  __shared__ __attribute__((aligned(16))) int8_t xs1[TBM * 256];
+  __shared__ __attribute__((aligned(16))) uint8_t ws0[TWCH * 16];
+  __shared__ __attribute__((aligned(16))) uint8_t ws1[TWCH * 16];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  const int l32 = lane & 31, h = lane >> 5;
+  const int n0 = blockIdx.x * TBN, m0 = blockIdx.y * TBM;
+  const int nsb = K >> 8;
+  const int64_t row_bytes = (int64_t)nsb * Q4K_BYTES;
+
+  // copies of super-block sb into (xd, wd); chunk P of the tile lands at P*16
+  auto load = [&](int sb, int8_t* xd, uint8_t* wd) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < TBM * 16 / 256; ++i) {
+      const int P = i * 256 + tid, row = P >> 4;
+      const int c = (P & 15) ^ (row & 15);
+      const int8_t* src = x + (int64_t)min(m0 + row, M - 1) * K + (int64_t)sb * 256 + 16 * c;
+      __builtin_amdgcn_global_load_lds((q4_gptr_t)src, (q4_lptr_t)(xd + (i * 256 + wave * 64) * 16), 16, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < TWCH / 256; ++i) {
+      const int P = min(i * 256 + tid, TBN * 9 - 1), row = P / 9, c = P - 9 * row;
+      const uint8_t* src = w + (int64_t)min(n0 + row, N - 1) * row_bytes + (int64_t)sb * Q4K_BYTES + 16 * c;
+      __builtin_amdgcn_global_load_lds((q4_gptr_t)src, (q4_lptr_t)(wd + (i * 256 + wave * 64) * 16), 16, 0, 0);
+    }
+  };
+
+  typedef int v16i_t __attribute__((ext_vector_type(16)));
+  float f[2][2][16];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b2 = 0; b2 < 2; ++b2)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) f[a][b2][e] = 0.f;
+
+  auto compute = [&](const int8_t* xt, const uint8_t* wt) __attribute__((always_inline)) {
+    // A operands: rows 64 wm + 32 rb + l32, elements 32 j + 16 h .. +15
+    v4i A[2][8];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const int row = 64 * wm + 32 * rb + l32;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        A[rb][j] = *reinterpret_cast<const v4i*>(xt + row * 256 + 16 * ((2 * j + h) ^ (row & 15)));
+    }
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      const uint8_t* wr = wt + (64 * wn + 32 * cb + l32) * Q4K_BYTES;
+      const uint4 hd = *reinterpret_cast<const uint4*>(wr);
+      const float d = h2f(hd.x & 0xFFFFu), dmin = h2f(hd.x >> 16);
+      const ScMin sm = unpack_scmin(hd.y, hd.z, hd.w);
+      v16i_t tl[2], th[2], tu[2];
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) tl[rb][e] = th[rb][e] = tu[rb][e] = 0;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const uint4 qv = *reinterpret_cast<const uint4*>(wr + 16 + 32 * g + 16 * h);
+        const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+        for (int hi = 0; hi < 2; ++hi) {
+          const int j = 2 * g + hi;
+          const uint32_t scw = j < 4 ? sm.sc_lo : sm.sc_hi, mnw = j < 4 ? sm.mn_lo : sm.mn_hi;
+          const uint32_t sc = (scw >> (8 * (j & 3))) & 0xFF, mn = (mnw >> (8 * (j & 3))) & 0xFF;
+          v4i bl, bh;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t nib = (qw[e] >> (4 * hi)) & 0x0F0F0F0Fu;
+            bl[e] = (int)(nib * (sc & 7));
+            bh[e] = (int)(nib * (sc >> 3));
+          }
+          const int bmv = (int)(mn * 0x01010101u);
+          const v4i bm = {bmv, bmv, bmv, bmv};
+#pragma unroll
+          for (int rb = 0; rb < 2; ++rb) {
+            tl[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[rb][j], bl, tl[rb], 0, 0, 0);
+            th[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[rb][j], bh, th[rb], 0, 0, 0);
+            tu[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[rb][j], bm, tu[rb], 0, 0, 0);
+          }
+        }
+      }
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          f[rb][cb][e] += d * (float)(tl[rb][e] + (th[rb][e] << 3)) - dmin * (float)tu[rb][e];
+    }
+  };
+
+  load(0, xs0, ws0);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __syncthreads();
+  int sb = 0;
+  for (; sb + 1 < nsb; sb += 2) {
+    load(sb + 1, xs1, ws1);
+    compute(xs0, ws0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+    if (sb + 2 < nsb) load(sb + 2, xs0, ws0);
+    compute(xs1, ws1);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+  }
+  if (sb < nsb) compute(xs0, ws0);
+
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int m = m0 + 64 * wm + 32 * rb + 8 * (e >> 2) + 4 * h + (e & 3);
+      if (m < M) {
+        const float xsm = x_scale[m];
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+          const int n = n0 + 64 * wn + 32 * cb + l32;
+          if (n < N) st_out<OUT_DT>(out, (int64_t)m * N + n, f[rb][cb][e] * xsm);
+        }
+      }
+    }
+}
+
+void launch_gemm_tile(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
+                      int M, int N, int K, hipStream_t st) {
+  const dim3 grid((unsigned)((N + TBN - 1) / TBN), (unsigned)((M + TBM - 1) / TBM));
+  switch (odt) {
+    case SL8_DTYPE_F16: gemm_q4k_tile_kernel<SL8_DTYPE_F16><<<grid, 256, 0, st>>>(x, xs, w, out, M, N, K); break;
+    case SL8_DTYPE_BF16: gemm_q4k_tile_kernel<SL8_DTYPE_BF16><<<grid, 256, 0, st>>>(x, xs, w, out, M, N, K); break;
+    default: gemm_q4k_tile_kernel<SL8_DTYPE_F32><<<grid, 256, 0, st>>>(x, xs, w, out, M, N, K); break;
+  }
+}
+
 __global__ void dequant_q4k_kernel(const uint8_t* __restrict__ w, float* __restrict__ out,
                                    int64_t N, int K) {
   // one thread per (row, sub-block): 32 outputs
@@ -516,7 +675,13 @@ extern "C" int sl8_gemm_q4k(const int8_t* x, const float* x_scale, const uint8_t
   SL8_CHECK_ARG(N < (1LL << 31), "gemm_q4k: N too large");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int esz = out_dtype == SL8_DTYPE_F32 ? 4 : 2;
-  // 16-row activation slabs through the same MFMA kernel.
+  if (M > 16) {
+    SL8_CHECK_ARG(M < (1LL << 31) / 1 && (M + TBM - 1) / TBM < 65536, "gemm_q4k: M too large");
+    launch_gemm_tile(x, x_scale, w, out, out_dtype, (int)M, (int)N, (int)K, st);
+    SL8_CHECK_LAUNCH("gemm_q4k");
+    return SL8_OK;
+  }
+  // M <= 16: one 16-row activation slab through the GEMV MFMA kernel.
   for (int64_t m0 = 0; m0 < M; m0 += 16) {
     const int64_t mt = (M - m0) < 16 ? (M - m0) : 16;
     char* o = static_cast<char*>(out) + m0 * N * esz;
