@@ -150,12 +150,12 @@ def _attn_fwd(q, q_scale, k, k_scale, v, causal, window_left, want_lse):
     if M == 0 or B == 0 or H == 0:
         return out, lse
     ws_bytes = _lib.load().sl8_attn_int8_fwd_workspace(B, Hkv, N, D)
-    ws = torch.empty((max(ws_bytes, 1),), device=q.device, dtype=torch.uint8)
+    ws = torch.empty((ws_bytes,), device=q.device, dtype=torch.uint8) if ws_bytes else None
     with torch.cuda.device(q.device):
         call("sl8_attn_int8_fwd", q.data_ptr(), q_scale.data_ptr(), k.data_ptr(),
              k_scale.data_ptr(), v.data_ptr(), dtype_code(v.dtype), out.data_ptr(),
              lse.data_ptr() if want_lse else None, B, H, Hkv, M, N, D, int(bool(causal)),
-             int(window_left), ws.data_ptr(), ws_bytes, stream_of(q))
+             int(window_left), ws.data_ptr() if ws is not None else None, ws_bytes, stream_of(q))
     return out, lse
 
 

@@ -10,21 +10,22 @@
 //            key is 0 and its LSE -inf; LSE = max*ln2 + ln(l).
 //   GQA: query head h reads K/V head h / (Hq/Hkv).
 //
-// Work decomposition. A workgroup (4 waves) owns 128 queries of one head; each
-// wave owns 32 queries for the whole key loop. Key tiles of 64 are staged in
-// LDS (double buffered, one barrier per tile) and shared by the 4 waves.
+// Work decomposition (attn_fwd_wide_kernel, the production kernel; the
+// narrow attn_fwd_kernel below only serves the int32 score dump): a wave owns
+// 32 queries for the whole key loop, a workgroup 4 or 8 waves; 64-key K,
+// k_scale and V tiles are copied global -> LDS one tile ahead and shared by
+// the waves.
 //
 // The scores are computed transposed, S^T = K . Q^T, with
 // v_mfma_i32_32x32x32_i8 (A = 32 keys x 32 channels from LDS, B = the wave's
 // 32 queries x 32 channels held in registers). In the 32x32 accumulator
 // layout a lane then holds one query (lane % 32) and 16 of the keys, which is
 // exactly the B-operand layout of the next product O^T = V^T . P^T
-// (v_mfma_f32_32x32x16_f16): P never leaves registers. The 8 keys a lane feeds
-// per 16-key MFMA step are {4h..4h+3, 8+4h..8+4h+3} (h = lane / 32); V^T is
-// stored with bits 2 and 3 of the key index swapped inside each 16-key group
-// so that those 8 keys are one contiguous 16-byte LDS read.
-// V^T is produced once per call by a transpose kernel into the workspace
-// ([B*Hkv][D][Npad], Npad = N rounded up to 64, zero padded).
+// (v_mfma_f32_32x32x16_f16/bf16): P never leaves registers. The 8 keys a lane
+// feeds per 16-key MFMA step are {4h..4h+3, 8+4h..8+4h+3} (h = lane / 32);
+// the matching V^T operand is read from V's natural [key][D] layout in LDS
+// with ds_read_b64_tr_b16 (two transposing reads per step), so V is used in
+// place: no transpose pass, no workspace.
 //
 // Scheduling: workgroups are issued heaviest-first (causal), and, when the
 // KV-head count is a multiple of 8, all query heads of one KV head go to the
@@ -43,65 +44,22 @@ constexpr int BM = 128;  // queries per workgroup
 constexpr int BN = 64;   // keys per tile
 constexpr float LN2F = 0.6931471805599453f;
 
-// key index inside a 16-key group -> storage position (swap bits 2 and 3)
-__host__ __device__ __forceinline__ int vt_pos(int k) {
-  return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1);
-}
 
-// ---------------------------------------------------------------------------
-// V [BHkv][N][D] (16-bit) -> V^T [BHkv][D][Npad], key-permuted, zero padded.
-// ---------------------------------------------------------------------------
-template <int D>
+// int8 V -> bf16 V, same [BHkv][N][D] layout (exact: |code| <= 127); 8
+// elements per thread.
 __global__ void __launch_bounds__(256)
-v_transpose_kernel(const uint16_t* __restrict__ v, uint16_t* __restrict__ vt, int N, int Npad) {
-  __shared__ uint16_t tile[BN][D + 2];
-  const int64_t bh = blockIdx.y;
-  const int n0 = blockIdx.x * BN;
-  const uint16_t* src = v + bh * (int64_t)N * D;
-  for (int i = threadIdx.x; i < BN * D / 8; i += 256) {
-    const int r = i / (D / 8), c = (i % (D / 8)) * 8;
-    uint4 val = {0, 0, 0, 0};
-    if (n0 + r < N) val = *reinterpret_cast<const uint4*>(src + (int64_t)(n0 + r) * D + c);
-    const uint16_t* pv = reinterpret_cast<const uint16_t*>(&val);
+v8_to_bf16_kernel(const int8_t* __restrict__ v, uint16_t* __restrict__ o, int64_t n8) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n8) return;
+  const uint2 x = reinterpret_cast<const uint2*>(v)[i];
+  uint32_t r[4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) tile[r][c + e] = pv[e];
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t w = e < 2 ? x.x : x.y;
+    const int sh = 16 * (e & 1);
+    r[e] = f2bf_bits((float)(int8_t)(w >> sh)) | ((uint32_t)f2bf_bits((float)(int8_t)(w >> (sh + 8))) << 16);
   }
-  __syncthreads();
-  uint16_t* dst = vt + bh * (int64_t)D * Npad + n0;
-  for (int i = threadIdx.x; i < D * (BN / 2); i += 256) {
-    const int d = i / (BN / 2), pr = (i % (BN / 2)) * 2;  // storage positions pr, pr+1
-    const int base = pr & ~15;
-    const int k0 = base + vt_pos(pr & 15);                 // vt_pos is an involution
-    const uint32_t lo = tile[k0][d], hi = tile[k0 + 1][d];
-    *reinterpret_cast<uint32_t*>(dst + (int64_t)d * Npad + pr) = lo | (hi << 16);
-  }
-}
-
-// int8 V [BHkv][N][D] -> bf16 V^T [BHkv][D][Npad] (exact: |code| <= 127),
-// same key permutation and padding as v_transpose_kernel.
-template <int D>
-__global__ void __launch_bounds__(256)
-v8_to_bf16_transpose_kernel(const int8_t* __restrict__ v, uint16_t* __restrict__ vt, int N, int Npad) {
-  __shared__ int8_t tile[BN][D + 4];
-  const int64_t bh = blockIdx.y;
-  const int n0 = blockIdx.x * BN;
-  const int8_t* src = v + bh * (int64_t)N * D;
-  for (int i = threadIdx.x; i < BN * D / 16; i += 256) {
-    const int r = i / (D / 16), c = (i % (D / 16)) * 16;
-    uint4 val = {0, 0, 0, 0};
-    if (n0 + r < N) val = *reinterpret_cast<const uint4*>(src + (int64_t)(n0 + r) * D + c);
-    const uint32_t w[4] = {val.x, val.y, val.z, val.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) *reinterpret_cast<uint32_t*>(&tile[r][c + 4 * e]) = w[e];
-  }
-  __syncthreads();
-  uint16_t* dst = vt + bh * (int64_t)D * Npad + n0;
-  for (int i = threadIdx.x; i < D * (BN / 2); i += 256) {
-    const int d = i / (BN / 2), pr = (i % (BN / 2)) * 2;
-    const int k0 = (pr & ~15) + vt_pos(pr & 15);
-    const uint32_t lo = f2bf_bits((float)tile[k0][d]), hi = f2bf_bits((float)tile[k0 + 1][d]);
-    *reinterpret_cast<uint32_t*>(dst + (int64_t)d * Npad + pr) = lo | (hi << 16);
-  }
+  reinterpret_cast<uint4*>(o)[i] = make_uint4(r[0], r[1], r[2], r[3]);
 }
 
 template <int VDT> struct PvOp;
@@ -520,7 +478,7 @@ attn_fwd_wide_kernel(const FwdArgs a) {
   const int wl = a.window_left;
   const int8_t* kb = a.k + bkv * (int64_t)N * D;
   const float* ksb = a.ks + bkv * (int64_t)N;
-  const uint16_t* vtb = a.vt + bkv * (int64_t)D * a.Npad;
+  const uint16_t* vb = a.vt + bkv * (int64_t)N * D;  // V [N][D] (natural layout)
 
   int qbs[2];
   int npass = 1;
@@ -534,11 +492,27 @@ attn_fwd_wide_kernel(const FwdArgs a) {
   // index above the rows that share one 256-byte bank line (K rows: D bytes,
   // V^T rows: 128 bytes).
   constexpr int KSH = D == 256 ? 0 : (D == 128 ? 1 : 2);
-  int koff[DC], voff[4];
+  int koff[DC];
 #pragma unroll
   for (int ch = 0; ch < DC; ++ch) koff[ch] = ((2 * ch + h) ^ ((l32 >> KSH) & (KCPR - 1))) * 16;
+  // V tiles keep V's natural [key][D] layout in LDS; the PV A operand (32 dims
+  // x 8 keys per lane) is read with ds_read_b64_tr_b16, which transposes 4 x 4
+  // blocks of 16-bit values inside each 16-lane group (lane i, slot e <- lane
+  // 4e + i/4, element i%4). Lane j of group G reads 4 dims of key row
+  // kbase + 4h + j/4 (+8 for the second read): dims 32tt + 16(G%2) + 4(j%4).
+  // Rows are XOR-swizzled in 64-byte units by (row & 3) (D = 64: by bit 1 of
+  // the row; two rows share one 256-byte bank line) so the 32 lanes of a half
+  // wave hit 32 distinct 8-byte bank slots. kbase + 4h is a multiple of 4, so
+  // the swizzle is a per-lane constant.
+  constexpr int VRB = 2 * D;  // bytes per V row
+  const int vj = lane & 15, vrow = (vj >> 2) + 4 * h;
+  const int vsw = D == 64 ? ((vj >> 3) & 1) : ((vj >> 2) & 3);
+  int voffb[DC];
 #pragma unroll
-  for (int c4 = 0; c4 < 4; ++c4) voff[c4] = ((2 * c4 + h) ^ ((l32 >> 1) & 7)) * 8;
+  for (int tt = 0; tt < DC; ++tt) {
+    const int slot = 8 * tt + 4 * ((lane >> 4) & 1) + (vj & 3);  // 8-byte slot of the row
+    voffb[tt] = vrow * VRB + 8 * (slot ^ (8 * vsw));
+  }
   // V buffers start as zeros (finite): the pipeline's first half-steps
   // multiply them by P = 0.
   for (int i = tid; i < D * BN / 8; i += WT) {
@@ -598,13 +572,14 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       }
     };
     auto load_v = [&](int n0, uint16_t* dst) __attribute__((always_inline)) {
+      // LDS chunk (row, c) holds V chunk c ^ 4k of key row n0 + row (k: the row's swizzle)
 #pragma unroll
       for (int i = 0; i < VCH; ++i) {
         const int sl = i * WT + tid;
-        const int row = sl / 8;
-        const int c = (sl % 8) ^ ((row >> 1) & 7);
-        dma16_to_lds(vtb + (int64_t)row * a.Npad + n0 + 8 * c,
-                     dst + (i * WT + wave * 64) * 8);
+        const int row = sl / (D / 8);
+        const int k = D == 64 ? ((row >> 1) & 1) : (row & 3);
+        const int c = (sl % (D / 8)) ^ (4 * k);
+        dma16_to_lds(vb + (int64_t)min(n0 + row, N - 1) * D + 8 * c, dst + (i * WT + wave * 64) * 8);
       }
     };
     auto load_s = [&](int n0, float* dst) __attribute__((always_inline)) {
@@ -639,12 +614,19 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       }
     };
     auto half_pv = [&](const uint16_t* vt, int s, const pblk& p) __attribute__((always_inline)) {
-      const uint16_t* vrow = vt + l32 * BN;
+      typedef short v4s __attribute__((ext_vector_type(4)));
+      typedef __attribute__((address_space(3))) v4s* lv4s_t;
+      const char* vbytes = reinterpret_cast<const char*>(vt);
 #pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
         for (int tt = 0; tt < DC; ++tt) {
-          const pvec vop = *reinterpret_cast<const pvec*>(vrow + 32 * tt * BN + voff[2 * s + c]);
+          const char* a0 = vbytes + (32 * s + 16 * c) * VRB + voffb[tt];
+          const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lv4s_t)(a0));
+          const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lv4s_t)(a0 + 8 * VRB));
+          typedef short v8s __attribute__((ext_vector_type(8)));
+          const v8s both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          const pvec vop = __builtin_bit_cast(pvec, both);
 #pragma unroll
           for (int g = 0; g < NG; ++g) oacc[g][tt] = PV::mfma(vop, p[g][c], oacc[g][tt]);
         }
@@ -668,7 +650,7 @@ attn_fwd_wide_kernel(const FwdArgs a) {
 #pragma unroll
       for (int i = 0; i < 3 * DC * NG; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // LDS reads
         __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
       }
 #pragma unroll
@@ -987,30 +969,9 @@ void launch_fwd(const FwdArgs& a, int grid, hipStream_t st) {
   attn_fwd_kernel<D, CAUSAL, VDT, DUMP, LSE><<<grid, FWD_THREADS, 0, st>>>(a);
 }
 
-template <int D, int VDT, bool DUMP>
-void dispatch_causal_lse(const FwdArgs& a, int grid, bool causal, bool lse, hipStream_t st) {
-  if (causal) {
-    if (lse) launch_fwd<D, true, VDT, DUMP, true>(a, grid, st);
-    else launch_fwd<D, true, VDT, DUMP, false>(a, grid, st);
-  } else {
-    if (lse) launch_fwd<D, false, VDT, DUMP, true>(a, grid, st);
-    else launch_fwd<D, false, VDT, DUMP, false>(a, grid, st);
-  }
-}
 
 int64_t npad_of(int64_t N) { return (N + BN - 1) / BN * BN; }
 
-int launch_transpose(const void* v, uint16_t* vt, int64_t BHkv, int64_t N, int64_t D,
-                     hipStream_t st) {
-  const int64_t npad = npad_of(N);
-  const dim3 grid((unsigned)(npad / BN), (unsigned)BHkv);
-  const uint16_t* v16 = static_cast<const uint16_t*>(v);
-  if (D == 64) v_transpose_kernel<64><<<grid, 256, 0, st>>>(v16, vt, (int)N, (int)npad);
-  else if (D == 128) v_transpose_kernel<128><<<grid, 256, 0, st>>>(v16, vt, (int)N, (int)npad);
-  else v_transpose_kernel<256><<<grid, 256, 0, st>>>(v16, vt, (int)N, (int)npad);
-  SL8_CHECK_LAUNCH("attn_int8_fwd v transpose");
-  return SL8_OK;
-}
 
 int check_fwd_shape(int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N, int64_t D) {
   SL8_CHECK_ARG(B >= 0 && Hq >= 0 && Hkv > 0 && M >= 0 && N >= 0, "fni8: bad shape");
@@ -1039,24 +1000,21 @@ FwdArgs make_args(int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N, int&
 }  // namespace
 
 // W8A8 prefill with per-warp P quantisation on the production pipeline
-// (called from attn_w8a8.hip). v: int8 [B*Hkv][N][D]; vt_ws: bf16 V^T
-// workspace of w8a8_wide_workspace() bytes.
+// (called from attn_w8a8.hip). v: int8 [B*Hkv][N][D]; vt_ws: workspace of
+// w8a8_wide_workspace() bytes for V in bf16, same layout.
 size_t w8a8_wide_workspace(int64_t B, int64_t Hkv, int64_t N, int64_t D) {
-  return (size_t)(B * Hkv * D * npad_of(N)) * sizeof(uint16_t);
+  return (size_t)(B * Hkv * N * D) * sizeof(uint16_t);
 }
 
 int w8a8_wide_launch(const int8_t* q, const float* q_scale, const int8_t* k, const float* k_scale,
                      const int8_t* v, const float* v_scale, void* out, int64_t B, int64_t Hq,
                      int64_t Hkv, int64_t M, int64_t N, int64_t D, bool causal, int64_t causal_diag,
                      void* vt_ws, hipStream_t st) {
-  const int64_t npad = npad_of(N);
   uint16_t* vt = static_cast<uint16_t*>(vt_ws);
   if (N > 0) {
-    const dim3 tg((unsigned)(npad / BN), (unsigned)(B * Hkv));
-    if (D == 64) v8_to_bf16_transpose_kernel<64><<<tg, 256, 0, st>>>(v, vt, (int)N, (int)npad);
-    else if (D == 128) v8_to_bf16_transpose_kernel<128><<<tg, 256, 0, st>>>(v, vt, (int)N, (int)npad);
-    else v8_to_bf16_transpose_kernel<256><<<tg, 256, 0, st>>>(v, vt, (int)N, (int)npad);
-    SL8_CHECK_LAUNCH("attn_w8a8_fwd v transpose");
+    const int64_t n8 = B * Hkv * N * D / 8;
+    v8_to_bf16_kernel<<<(unsigned)((n8 + 255) / 256), 256, 0, st>>>(v, vt, n8);
+    SL8_CHECK_LAUNCH("attn_w8a8_fwd v to bf16");
   }
   int grid;
   FwdArgs a = make_args(B, Hq, Hkv, M, N, grid);
@@ -1086,9 +1044,11 @@ int w8a8_wide_launch(const int8_t* q, const float* q_scale, const int8_t* k, con
 
 using namespace sl8;
 
+// The prefill reads V in place (natural layout): no workspace is needed. The
+// entry point keeps its workspace arguments for ABI stability.
 extern "C" size_t sl8_attn_int8_fwd_workspace(int64_t B, int64_t Hkv, int64_t N, int64_t D) {
-  if (B <= 0 || Hkv <= 0 || N <= 0 || D <= 0) return 0;
-  return (size_t)(B * Hkv * D * npad_of(N)) * sizeof(uint16_t);
+  (void)B; (void)Hkv; (void)N; (void)D;
+  return 0;
 }
 
 extern "C" int sl8_attn_int8_fwd(const int8_t* q, const float* q_scale, const int8_t* k,
@@ -1110,14 +1070,10 @@ extern "C" int sl8_attn_int8_fwd(const int8_t* q, const float* q_scale, const in
   SL8_CHECK_ARG(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 16)),
                 "fni8: attn_int8_fwd workspace needs %zu bytes", need);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (N > 0) {
-    rc = launch_transpose(v, static_cast<uint16_t*>(workspace), B * Hkv, N, D, st);
-    if (rc) return rc;
-  }
   int grid;
   FwdArgs a = make_args(B, Hq, Hkv, M, N, grid);
   a.q = q; a.qs = q_scale; a.k = k; a.ks = k_scale;
-  a.vt = static_cast<const uint16_t*>(workspace);
+  a.vt = static_cast<const uint16_t*>(v);  // V [B*Hkv][N][D], read in place
   a.out = out; a.lse = lse; a.window_left = (int)window_left;
   const bool c = causal != 0, want_lse = lse != nullptr;
   a.nqb = (int)((M + wide_bm(D) - 1) / wide_bm(D));
