@@ -162,6 +162,15 @@ int sl8_attn_int8_decode_kv8(const int8_t* q, const float* q_scale, const int8_t
                              int64_t num_splits, void* workspace, size_t workspace_bytes,
                              void* stream);
 
+/* Outlier gate of the prologue: *flag |= 1 when some row of q [rows, D]
+ * (fp16/bf16/fp32, D in {64,128,256}) has max|q| / (median|q| + 1e-10) >
+ * ratio in fp32, median = the lower middle element. flag must be zeroed by the
+ * caller; stats, if not NULL, receives [rows][2] = (max, median). Replaces the
+ * torch evaluation of detect_q_outlier_domination (reference
+ * superl8/quant/core.py:113-145, called by superl8/ops.py:115-147). */
+int sl8_q_outlier_gate(const void* q, int dtype, int64_t rows, int64_t D, float ratio,
+                       int32_t* flag, float* stats, void* stream);
+
 /* ------------------------------------------------------------------------
  * Paged int8 KV cache (reference csrc/fni8_api.cpp:138-143,152-154,509-527,
  * csrc/kernel/attn_paged_decode.cu:14-31,107-240,360-421,

@@ -4,6 +4,8 @@ Reference: csrc/include/quant_rowwise.cuh:33-91 (scale = amax * fp32(1/127),
 zero row -> 1, q = clamp(rint(x / scale), +-127) with correctly rounded fp32
 division), superl8/quant/core.py:29-44,70-95 (K mean / smoothing),
 core.py:164-196 (quantize_qk: fold softmax_scale*log2(e) into the Q scale),
+superl8/quant/core.py:113-145 (outlier gate: any row with
+max|q| / (median|q| + 1e-10) > ratio in fp32, median = the lower middle element),
 csrc/include/attn_paged_decode.cuh:55-115 (quantize-on-write of one token per
 paged row: scale = amax / 127 as an fp32 division, zero row -> 1, code =
 rint(clamp(x / scale, +-127))).
@@ -134,3 +136,19 @@ def kv_write_paged(k_new, v_new, slot_mapping, k_cache, k_scale, v_cache, v_scal
         v_cache[blk, :, off] = vq[b]
         k_scale[blk, :, off] = ks[b]
         v_scale[blk, :, off] = vs[b]
+
+
+def q_outlier_stats(q: np.ndarray):
+    """Per-row max|q| and lower median |q| (the ((D-1)//2)-th smallest, torch.median's
+    choice for even D) of the last axis, fp32 (reference quant/core.py:139-141)."""
+    a = np.abs(np.asarray(q, dtype=np.float32))
+    srt = np.sort(a, axis=-1)
+    return a.max(-1), srt[..., (a.shape[-1] - 1) // 2]
+
+
+def q_outlier_gate(q: np.ndarray, ratio_threshold: float = 12.0) -> bool:
+    """True when any row has max / (median + 1e-10) > ratio_threshold, evaluated in
+    fp32 (reference quant/core.py:113-145)."""
+    mx, md = q_outlier_stats(q)
+    ratio = (mx / (md + np.float32(1e-10))).astype(np.float32)
+    return bool((ratio > np.float32(ratio_threshold)).any())

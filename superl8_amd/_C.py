@@ -103,6 +103,31 @@ def quantize_rows_centered(x: torch.Tensor, mean: torch.Tensor | None, scale_mul
     return q, scale
 
 
+_GATE_HEAD_DIMS = (64, 128, 256)
+
+
+def q_outlier_gate(q: torch.Tensor, ratio: float = 12.0, *, stats: bool = False):
+    """On-device outlier gate over the rows of q[..., D] (D in 64/128/256).
+
+    Returns (flag int32 [1], stats fp32 [rows, 2] or None): flag is 1 when some
+    row has max|q| / (median|q| + 1e-10) > ratio (fp32, median = lower middle
+    element, as torch.median); stats holds each row's (max, median)."""
+    _check(q.is_cuda, "q_outlier_gate expects a CUDA tensor")
+    _check(q.dtype in (torch.float16, torch.bfloat16, torch.float32),
+           "q_outlier_gate input must be float16/bfloat16/float32")
+    D = q.shape[-1]
+    _check(D in _GATE_HEAD_DIMS, f"q_outlier_gate supports D in {_GATE_HEAD_DIMS}, got {D}")
+    q = q.contiguous()
+    rows = q.numel() // D
+    flag = torch.zeros((1,), device=q.device, dtype=torch.int32)
+    st = torch.empty((rows, 2), device=q.device, dtype=torch.float32) if stats else None
+    if rows:
+        with torch.cuda.device(q.device):
+            call("sl8_q_outlier_gate", q.data_ptr(), dtype_code(q.dtype), rows, D, float(ratio),
+                 flag.data_ptr(), None if st is None else st.data_ptr(), stream_of(q))
+    return flag, st
+
+
 def quantize_v_perchannel(v: torch.Tensor):
     """Per-channel int8 of v[..., N, D] over N -> (q int8 [..., N, D], scale fp32 [..., 1, D])."""
     _check(v.is_cuda, "quantize_v_perchannel expects a CUDA tensor")

@@ -43,6 +43,7 @@ SIGNATURES = {
     "sl8_attn_int8_decode_kv8": (_I, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
                                       _I64, _P, _SZ, _P]),
     "sl8_paged_choose_num_splits": (_I, [_I64, _I64]),
+    "sl8_q_outlier_gate": (_I, [_P, _I, _I64, _I64, ctypes.c_float, _P, _P, _P]),
     "sl8_attn_paged_decode": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
                                    _I64, _I64, _I64, _I64, _I64, _P, _SZ, _P]),
     "sl8_kv_write_paged": (_I, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P]),

@@ -71,6 +71,8 @@ def quantize_v_rowwise(v: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
 def detect_q_outlier_domination(q: torch.Tensor, *, ratio_threshold: float = 12.0) -> bool:
     """True when any Q row has max|q| / median|q| > ratio_threshold (reference core.py:113-145).
 
+    One gate kernel (max and exact lower median per row, flag by atomic OR)
+    decides on the GPU for D in 64/128/256; other head dims use torch ops.
     Skipped (False) while the current stream is capturing a graph, because the
     decision needs a device-to-host read.
     """
@@ -79,6 +81,9 @@ def detect_q_outlier_domination(q: torch.Tensor, *, ratio_threshold: float = 12.
             return False
     except Exception:
         pass
+    if q.is_cuda and q.shape[-1] in _C._GATE_HEAD_DIMS:
+        flag, _ = _C.q_outlier_gate(q, ratio_threshold)
+        return bool(flag.item())
     q_abs = q.float().abs()
     row_max = q_abs.amax(dim=-1)
     row_med = q_abs.median(dim=-1).values

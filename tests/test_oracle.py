@@ -414,3 +414,27 @@ def test_kv_write_paged_places_rows():
         np.testing.assert_array_equal(kc[blk, :, off], kq[b])
         np.testing.assert_array_equal(ks[blk, :, off], kscl[b])
     assert np.count_nonzero(ks) == 3 * 2
+
+
+def test_q_outlier_gate_definition():
+    """Lower median for even D (torch.median), the 1e-10 guard, the fp32 ratio."""
+    q = np.array([[1, 2, 3, 40], [4, 3, 2, 1], [0, 0, 0, 0], [-5, 1, 1, 60]], np.float32)
+    mx, md = oqn.q_outlier_stats(q)
+    np.testing.assert_array_equal(mx, [40, 4, 0, 60])
+    np.testing.assert_array_equal(md, [2, 2, 0, 1])  # sorted |q|[(4-1)//2] = index 1
+    assert oqn.q_outlier_gate(q)                      # 40/2 = 20 > 12, 60/1 > 12
+    assert not oqn.q_outlier_gate(q[1:3])             # 4/2 = 2; zero row: 0/1e-10 = 0
+    row = np.full((1, 5), 1.0, np.float32)
+    row[0, 0] = 12.0
+    assert not oqn.q_outlier_gate(row)                # exactly 12 is not > 12
+    row[0, 0] = np.nextafter(np.float32(12.0), np.float32(13.0))
+    assert oqn.q_outlier_gate(row)
+    # brute force on random rows: the k-th smallest by counting
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((50, 33)).astype(np.float32)
+    _, md = oqn.q_outlier_stats(x)
+    a = np.abs(x)
+    for r in range(50):
+        cnt_lt = (a[r] < md[r]).sum()
+        cnt_le = (a[r] <= md[r]).sum()
+        assert cnt_lt <= 16 < cnt_le
