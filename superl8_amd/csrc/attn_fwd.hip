@@ -45,21 +45,40 @@ constexpr int BN = 64;   // keys per tile
 constexpr float LN2F = 0.6931471805599453f;
 
 
-// int8 V -> bf16 V, same [BHkv][N][D] layout (exact: |code| <= 127); 8
-// elements per thread.
+// W8A8 variant: int8 V -> bf16 V^T [BHkv][D][Npad] (Npad = N rounded up to 64,
+// zero padded). Inside each 16-key group the keys are stored with bits 2 and 3
+// of the index swapped, so the 8 keys {4h..4h+3, 8+4h..8+4h+3} a lane feeds
+// per 16-key PV step are one 16-byte read. The per-warp W8A8 kernel reads V^T
+// with plain 16-byte LDS reads: at D = 256 and one wave per SIMD its PV step
+// is LDS-issue bound, where the two transposing reads per operand of the
+// in-place layout cost 12% of the kernel time.
+__host__ __device__ __forceinline__ int vt_pos(int k) {
+  return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1);
+}
+
+template <int D>
 __global__ void __launch_bounds__(256)
-v8_to_bf16_kernel(const int8_t* __restrict__ v, uint16_t* __restrict__ o, int64_t n8) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n8) return;
-  const uint2 x = reinterpret_cast<const uint2*>(v)[i];
-  uint32_t r[4];
+v8_to_bf16_t_kernel(const int8_t* __restrict__ v, uint16_t* __restrict__ vt, int N, int Npad) {
+  __shared__ int8_t tile[64][D + 4];
+  const int64_t bh = blockIdx.y;
+  const int n0 = blockIdx.x * 64;
+  const int8_t* src = v + bh * (int64_t)N * D;
+  for (int i = threadIdx.x; i < 64 * D / 16; i += 256) {
+    const int r = i / (D / 16), c = (i % (D / 16)) * 16;
+    uint4 x = {0, 0, 0, 0};
+    if (n0 + r < N) x = *reinterpret_cast<const uint4*>(src + (int64_t)(n0 + r) * D + c);
+    const uint32_t w[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const uint32_t w = e < 2 ? x.x : x.y;
-    const int sh = 16 * (e & 1);
-    r[e] = f2bf_bits((float)(int8_t)(w >> sh)) | ((uint32_t)f2bf_bits((float)(int8_t)(w >> (sh + 8))) << 16);
+    for (int e = 0; e < 4; ++e) *reinterpret_cast<uint32_t*>(&tile[r][c + 4 * e]) = w[e];
   }
-  reinterpret_cast<uint4*>(o)[i] = make_uint4(r[0], r[1], r[2], r[3]);
+  __syncthreads();
+  uint16_t* dst = vt + bh * (int64_t)D * Npad + n0;
+  for (int i = threadIdx.x; i < D * 32; i += 256) {
+    const int d = i / 32, pr = (i % 32) * 2;  // storage positions pr, pr + 1
+    const int k0 = (pr & ~15) + vt_pos(pr & 15);  // vt_pos is an involution; k0 + 1 pairs pr + 1
+    const uint32_t lo = f2bf_bits((float)tile[k0][d]), hi = f2bf_bits((float)tile[k0 + 1][d]);
+    *reinterpret_cast<uint32_t*>(dst + (int64_t)d * Npad + pr) = lo | (hi << 16);
+  }
 }
 
 template <int VDT> struct PvOp;
@@ -478,7 +497,10 @@ attn_fwd_wide_kernel(const FwdArgs a) {
   const int wl = a.window_left;
   const int8_t* kb = a.k + bkv * (int64_t)N * D;
   const float* ksb = a.ks + bkv * (int64_t)N;
-  const uint16_t* vb = a.vt + bkv * (int64_t)N * D;  // V [N][D] (natural layout)
+  // VT (the W8A8 variant): V^T [D][Npad] from v8_to_bf16_t_kernel; else V [N][D] in place
+  constexpr bool VT = W8;
+  const uint16_t* vb = a.vt + bkv * (int64_t)N * D;
+  const uint16_t* vtb = a.vt + bkv * (int64_t)D * a.Npad;
 
   int qbs[2];
   int npass = 1;
@@ -513,6 +535,10 @@ attn_fwd_wide_kernel(const FwdArgs a) {
     const int slot = 8 * tt + 4 * ((lane >> 4) & 1) + (vj & 3);  // 8-byte slot of the row
     voffb[tt] = vrow * VRB + 8 * (slot ^ (8 * vsw));
   }
+  // VT: V^T tile [D][64 keys], rows of 128 bytes, 16-byte chunks swizzled by (row >> 1) & 7
+  int voff[4];
+#pragma unroll
+  for (int c4 = 0; c4 < 4; ++c4) voff[c4] = ((2 * c4 + h) ^ ((l32 >> 1) & 7)) * 8;
   // V buffers start as zeros (finite): the pipeline's first half-steps
   // multiply them by P = 0.
   for (int i = tid; i < D * BN / 8; i += WT) {
@@ -572,6 +598,16 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       }
     };
     auto load_v = [&](int n0, uint16_t* dst) __attribute__((always_inline)) {
+      if constexpr (VT) {
+#pragma unroll
+        for (int i = 0; i < VCH; ++i) {
+          const int sl = i * WT + tid;
+          const int row = sl / 8;
+          const int c = (sl % 8) ^ ((row >> 1) & 7);
+          dma16_to_lds(vtb + (int64_t)row * a.Npad + n0 + 8 * c, dst + (i * WT + wave * 64) * 8);
+        }
+        return;
+      }
       // LDS chunk (row, c) holds V chunk c ^ 4k of key row n0 + row (k: the row's swizzle)
 #pragma unroll
       for (int i = 0; i < VCH; ++i) {
@@ -617,6 +653,18 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       typedef short v4s __attribute__((ext_vector_type(4)));
       typedef __attribute__((address_space(3))) v4s* lv4s_t;
       const char* vbytes = reinterpret_cast<const char*>(vt);
+      if constexpr (VT) {
+        const uint16_t* vr = vt + l32 * BN;
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int tt = 0; tt < DC; ++tt) {
+            const pvec vop = *reinterpret_cast<const pvec*>(vr + 32 * tt * BN + voff[2 * s + c]);
+#pragma unroll
+            for (int g = 0; g < NG; ++g) oacc[g][tt] = PV::mfma(vop, p[g][c], oacc[g][tt]);
+          }
+        return;
+      }
 #pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -650,7 +698,7 @@ attn_fwd_wide_kernel(const FwdArgs a) {
 #pragma unroll
       for (int i = 0; i < 3 * DC * NG; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // LDS reads
+        __builtin_amdgcn_sched_group_barrier(0x100, VT ? 1 : 2, 0);  // LDS reads
         __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
       }
 #pragma unroll
@@ -1001,9 +1049,9 @@ FwdArgs make_args(int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N, int&
 
 // W8A8 prefill with per-warp P quantisation on the production pipeline
 // (called from attn_w8a8.hip). v: int8 [B*Hkv][N][D]; vt_ws: workspace of
-// w8a8_wide_workspace() bytes for V in bf16, same layout.
+// w8a8_wide_workspace() bytes for bf16 V^T [B*Hkv][D][Npad].
 size_t w8a8_wide_workspace(int64_t B, int64_t Hkv, int64_t N, int64_t D) {
-  return (size_t)(B * Hkv * N * D) * sizeof(uint16_t);
+  return (size_t)(B * Hkv * D * npad_of(N)) * sizeof(uint16_t);
 }
 
 int w8a8_wide_launch(const int8_t* q, const float* q_scale, const int8_t* k, const float* k_scale,
@@ -1012,9 +1060,12 @@ int w8a8_wide_launch(const int8_t* q, const float* q_scale, const int8_t* k, con
                      void* vt_ws, hipStream_t st) {
   uint16_t* vt = static_cast<uint16_t*>(vt_ws);
   if (N > 0) {
-    const int64_t n8 = B * Hkv * N * D / 8;
-    v8_to_bf16_kernel<<<(unsigned)((n8 + 255) / 256), 256, 0, st>>>(v, vt, n8);
-    SL8_CHECK_LAUNCH("attn_w8a8_fwd v to bf16");
+    const int np = (int)npad_of(N);
+    const dim3 tg((unsigned)(np / 64), (unsigned)(B * Hkv));
+    if (D == 64) v8_to_bf16_t_kernel<64><<<tg, 256, 0, st>>>(v, vt, (int)N, np);
+    else if (D == 128) v8_to_bf16_t_kernel<128><<<tg, 256, 0, st>>>(v, vt, (int)N, np);
+    else v8_to_bf16_t_kernel<256><<<tg, 256, 0, st>>>(v, vt, (int)N, np);
+    SL8_CHECK_LAUNCH("attn_w8a8_fwd v to bf16 V^T");
   }
   int grid;
   FwdArgs a = make_args(B, Hq, Hkv, M, N, grid);
