@@ -185,6 +185,35 @@ def bench_gemm_prefill(M=512, iters=10):
     return ms, 2 * M * N * K
 
 
+def bench_prologue(iters=20):
+    """Attention prologue at config 2: the fused two-launch sl8_quantize_qk with the
+    outlier gate, and the separate kernels it replaces (K mean, Q and K quantise,
+    gate). Algorithmic bytes: Q and K read once, codes and scales written once."""
+    from superl8_amd import _C
+    from superl8_amd.quant import LOG2E
+
+    dev = "cuda"
+    B, Hq, Hkv, S, D = 1, 32, 8, 4096, 128
+    g = torch.Generator(device=dev).manual_seed(3)
+    q = torch.randn(B, Hq, S, D, device=dev, dtype=torch.float16, generator=g)
+    k = torch.randn(B, Hkv, S, D, device=dev, dtype=torch.float16, generator=g)
+    mul = LOG2E / D ** 0.5
+    fused = lambda: _C.quantize_qk_fused(q, k, mul, 12.0)  # noqa: E731
+
+    def separate():
+        m = _C.k_mean(k)
+        _C.quantize_rows_centered(q, None, mul)
+        _C.quantize_rows_centered(k, m, 1.0)
+        _C.q_outlier_gate(q, 12.0)
+
+    st = torch.cuda.current_stream()
+    spin_up(fused, 0.1)
+    fms = _events_time(fused, iters, st)
+    sms = _events_time(separate, iters, st)
+    nbytes = (q.numel() + k.numel()) * 3 + (B * Hq * S + B * Hkv * S) * 4
+    return fms, sms, nbytes
+
+
 def bench_w8a8(iters=5):
     """Full-W8A8 prefill at BASELINE config 5: Q/K/V [2, 16|2, 8192, 256], causal,
     1% of Q/K channels (3 of 256, fixed) scaled by 20, V per-channel int8."""
@@ -368,6 +397,12 @@ def main():
         sec["gemm_q4k_prefill_m512_cfg4w"] = {"us": round(pms2 * 1e3, 1), "TOPS": round(pt, 1),
                                               "frac_int8_peak": round(pt / PEAK_INT8_TOPS, 4),
                                               "ops": pops}
+        fms, sms, pb = bench_prologue()
+        gbs = pb / (fms * 1e-3) / 1e9
+        sec["prologue_quantize_qk_gate_cfg2"] = {"us": round(fms * 1e3, 2), "GB/s": round(gbs, 1),
+                                                 "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+                                                 "bytes": pb,
+                                                 "separate_kernels_us": round(sms * 1e3, 2)}
         wms, wops = bench_w8a8()
         wt = wops / (wms * 1e-3) / 1e12
         sec["attn_w8a8_fwd_cfg5"] = {"us": round(wms * 1e3, 1), "TOPS": round(wt, 1),

@@ -80,6 +80,26 @@ int sl8_quantize_i8_rows_centered(const void* x, int x_dtype, int64_t G, int64_t
                                   int8_t* q, float* scale, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Fused fp16 attention prologue: quantize_qk (no rotation) plus, optionally,
+ * the outlier gate, in three launches (six unfused). Replaces superl8/quant/core.py:164-196
+ * (smooth_k + quantize_qk) and detect_q_outlier_domination (core.py:113-145)
+ * as called from superl8/ops.py:115-150; results equal sl8_k_mean,
+ * sl8_quantize_i8_rows_centered and sl8_q_outlier_gate bit for bit.
+ *   q [qrows, D] fp16 (qrows = B*Hq*M), k [G, N, D] fp16 (G = B*Hkv), D in {64,128,256}
+ *   -> q_i8 [qrows, D], q_scale [qrows] (x q_scale_mul), k_i8 [G, N, D],
+ *      k_scale [G, N], k_mean fp32 [G, D]
+ * gate_ratio > 0: *gate_flag = 1 if some Q row has max/(median+1e-10) > ratio,
+ * else 0 (written, not OR-ed: no clearing needed). gate_ratio <= 0: no gate.
+ * workspace: sl8_quantize_qk_workspace(qrows, G, N, D) bytes, 8-byte aligned,
+ * uninitialised. q/k 16-byte aligned, codes 8-byte aligned; N < 2^23.
+ * ---------------------------------------------------------------------- */
+size_t sl8_quantize_qk_workspace(int64_t qrows, int64_t G, int64_t N, int64_t D);
+int sl8_quantize_qk(const void* q, const void* k, int dtype, int64_t qrows, int64_t G, int64_t N,
+                    int64_t D, float q_scale_mul, float gate_ratio, int8_t* q_i8, float* q_scale,
+                    int8_t* k_i8, float* k_scale, float* k_mean, int32_t* gate_flag,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * Per-channel int8 of V over the key axis (W8A8 path).
  * Replaces quantize_v_perchannel, reference superl8/quant/core.py:98-110
  * (on the GPU torch evaluates amax/127 as amax * fp32(1/127)).

@@ -103,6 +103,38 @@ def quantize_rows_centered(x: torch.Tensor, mean: torch.Tensor | None, scale_mul
     return q, scale
 
 
+def quantize_qk_fused(q: torch.Tensor, k: torch.Tensor, q_scale_mul: float,
+                      gate_ratio: float = 0.0):
+    """Fused fp16 prologue: q [B,Hq,M,D], k [B,Hkv,N,D] -> (q_i8, q_scale [B,Hq,M],
+    k_i8, k_scale [B,Hkv,N], k_mean fp32 [B,Hkv,1,D], flag int32 [1] or None).
+
+    K is smoothed by its exact per-channel mean, q_scale carries q_scale_mul;
+    with gate_ratio > 0, flag = 1 when some Q row has max/(median+1e-10) above it."""
+    _on_gpu(q, k)
+    _check(q.dtype == torch.float16 and k.dtype == torch.float16,
+           "fused prologue expects float16 q and k")
+    _check(q.dim() == 4 and k.dim() == 4 and q.shape[-1] == k.shape[-1],
+           "fused prologue expects q[B,Hq,M,D], k[B,Hkv,N,D]")
+    q, k = q.contiguous(), k.contiguous()
+    B, Hq, M, D = q.shape
+    _, Hkv, N, _ = k.shape
+    qrows, G = B * Hq * M, B * Hkv
+    q_i8 = torch.empty(q.shape, device=q.device, dtype=torch.int8)
+    q_scale = torch.empty((B, Hq, M), device=q.device, dtype=torch.float32)
+    k_i8 = torch.empty(k.shape, device=k.device, dtype=torch.int8)
+    k_scale = torch.empty((B, Hkv, N), device=k.device, dtype=torch.float32)
+    k_mean = torch.empty((B, Hkv, 1, D), device=k.device, dtype=torch.float32)
+    flag = torch.empty((1,), device=q.device, dtype=torch.int32) if gate_ratio > 0 else None
+    ws_bytes = _lib.load().sl8_quantize_qk_workspace(qrows, G, N, D)
+    ws = torch.empty((max(ws_bytes, 8),), device=q.device, dtype=torch.uint8)
+    with torch.cuda.device(q.device):
+        call("sl8_quantize_qk", q.data_ptr(), k.data_ptr(), dtype_code(q.dtype), qrows, G, N, D,
+             float(q_scale_mul), float(gate_ratio), q_i8.data_ptr(), q_scale.data_ptr(),
+             k_i8.data_ptr(), k_scale.data_ptr(), k_mean.data_ptr(),
+             None if flag is None else flag.data_ptr(), ws.data_ptr(), ws_bytes, stream_of(q))
+    return q_i8, q_scale, k_i8, k_scale, k_mean, flag
+
+
 _GATE_HEAD_DIMS = (64, 128, 256)
 
 

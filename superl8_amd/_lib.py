@@ -28,6 +28,9 @@ SIGNATURES = {
     "sl8_k_mean_workspace": (_SZ, [_I64, _I64]),
     "sl8_k_mean": (_I, [_P, _I, _I64, _I64, _I64, _P, _P, _SZ, _P]),
     "sl8_quantize_i8_rows_centered": (_I, [_P, _I, _I64, _I64, _I64, _P, _F, _P, _P, _P]),
+    "sl8_quantize_qk_workspace": (_SZ, [_I64, _I64, _I64, _I64]),
+    "sl8_quantize_qk": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _F, _F, _P, _P, _P, _P, _P, _P,
+                             _P, _SZ, _P]),
     "sl8_quantize_i8_cols": (_I, [_P, _I, _I64, _I64, _I64, _P, _P, _P]),
     "sl8_attn_int8_fwd_workspace": (_SZ, [_I64, _I64, _I64, _I64]),
     "sl8_attn_int8_fwd": (_I, [_P, _P, _P, _P, _P, _I, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,

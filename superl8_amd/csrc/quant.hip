@@ -587,3 +587,343 @@ extern "C" int sl8_q_outlier_gate(const void* q, int dtype, int64_t rows, int64_
   SL8_CHECK_LAUNCH("outlier gate");
   return SL8_OK;
 }
+
+// ---------------------------------------------------------------------------
+// Fused attention prologue for fp16 Q/K (reference superl8/quant/core.py
+// quantize_qk + smooth_k, and the outlier gate of superl8/ops.py:115-147):
+// three launches instead of six, Q read once, K read twice, no zeroing pass.
+//
+// Launch A (one grid, two roles chosen per block):
+//   * K-mean partials: block (g, c) sums key rows [128c, 128c + 128) of
+//     group g exactly in int64 fixed point (value * 2^24, decoded from the
+//     fp16 bits) with 16-byte loads, and stores its D partial sums. The
+//     mean is exact, hence independent of the summation order.
+//   * Q: per-row int8 quantisation (scale * q_scale_mul) and, with a gate
+//     ratio, the outlier decision for every row. f(x) = fl(max / fl(x + 1e-10))
+//     is non-increasing in x >= 0, so f(median) > ratio iff more than (D-1)/2
+//     of the row's |x| have f(|x|) > ratio: the row is decided exactly with
+//     no median search (the division is needed only for elements within
+//     2^-18 of max / ratio). A row holding a NaN never fires (torch's amax and
+//     median are NaN there). Each Q block writes one word: whether any of
+//     its rows fired.
+// Launch M: the mean of each (group, column) from its partials (int64 ->
+//   fp64 -> / N -> fp32, as sl8_k_mean); one extra block ORs the Q blocks'
+//   words into the gate flag (so the flag needs no clearing by the caller).
+// Launch B: subtracts the mean from each key row with the fp16 rounding of
+//   torch.sub and quantises it.
+// ---------------------------------------------------------------------------
+namespace sl8 {
+namespace {
+
+constexpr int PRO_CHUNK = 128;      // key rows per mean partial
+constexpr int PRO_KROWS = 32;       // key rows per quantise block
+constexpr int PRO_QBLOCKS_MAX = 16384;
+constexpr int PRO_QP = 1;           // Q rows per thread per pass (1: measured fastest; more rows per thread cost occupancy)
+
+// fp16 bits -> value * 2^24 as an exact integer (finite inputs: |result| < 2^40)
+__device__ __forceinline__ long long f16_fixed24(uint32_t h) {
+  const uint32_t e = (h >> 10) & 31u, m = h & 1023u;
+  const long long v = e ? (long long)(1024u + m) << (e - 1) : (long long)m;
+  return (h & 0x8000u) ? -v : v;
+}
+
+template <int LPR>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int o = LPR / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+template <int LPR>
+__device__ __forceinline__ int group_sum(int v) {
+#pragma unroll
+  for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ void unpack_h8(const uint4& raw, float* f) {
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) { f[2 * i] = h2f(w[i] & 0xFFFFu); f[2 * i + 1] = h2f(w[i] >> 16); }
+}
+
+// Eight codes clamp(rint(fl(x / safe))) without a division per element.
+// |x| <= amax, so |fl(x / safe)| < 128 and r = x * fl(1/safe) is within
+// 1.5 * 2^-23 * 128 < 2^-14 of it. n = r rounded to nearest-even by the
+// 1.5 * 2^23 magic constant; unless |r - n| > 0.5 - 2^-14 (r near a
+// half-integer) both r and fl(x / safe) round to n. Lanes holding such an
+// element (about 1e-4 of them) take the IEEE division, under a wave-uniform
+// branch so the common path never executes it.
+__device__ __forceinline__ uint2 codes8(const float* f, float safe) {
+  const float inv = 1.0f / safe;
+  constexpr float MAGIC = 12582912.f;  // 1.5 * 2^23
+  float n[8];
+  bool amb = false;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float r = f[e] * inv;
+    n[e] = (r + MAGIC) - MAGIC;
+    amb |= !(fabsf(r - n[e]) <= 0.5f - 0x1p-14f);  // also catches inf / NaN
+  }
+  if (__builtin_expect(__ballot(amb) != 0, 0)) {
+    if (amb) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) n[e] = rintf(__fdiv_rn(f[e], safe));
+    }
+  }
+  uint32_t w[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    w[i] = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float c = fminf(fmaxf(n[4 * i + e], -127.f), 127.f);
+      w[i] |= ((uint32_t)(int)c & 0xFFu) << (8 * e);
+    }
+  }
+  return make_uint2(w[0], w[1]);
+}
+
+template <int D, bool GATE>
+__global__ void __launch_bounds__(256, 8)
+prologue_a_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, int64_t qrows,
+                  int64_t N, int nkb, int C, float qmul, float ratio, int8_t* __restrict__ q_i8,
+                  float* __restrict__ q_scale, long long* __restrict__ part,
+                  int32_t* __restrict__ fire) {
+  constexpr int LPR = D / 8;       // lanes per row, 8 elements (16 bytes) each
+  constexpr int RPP = 256 / LPR;   // rows per block pass
+  const int lane = threadIdx.x % LPR, sub = threadIdx.x / LPR;
+  if ((int)blockIdx.x < nkb) {
+    __shared__ long long red[RPP][D];
+    const int64_t g = blockIdx.x / C;
+    const int c = blockIdx.x % C;
+    const int64_t n0 = (int64_t)c * PRO_CHUNK, n1 = min(N, n0 + PRO_CHUNK);
+    const uint16_t* kg = k + g * N * D + lane * 8;
+    long long acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = 0;
+#pragma unroll 2
+    for (int64_t n = n0 + sub; n < n1; n += RPP) {
+      const uint4 raw = *reinterpret_cast<const uint4*>(kg + n * D);
+      const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc[2 * i] += f16_fixed24(w[i] & 0xFFFFu);
+        acc[2 * i + 1] += f16_fixed24(w[i] >> 16);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red[sub][lane * 8 + e] = acc[e];
+    __syncthreads();
+    for (int d = threadIdx.x; d < D; d += 256) {
+      long long t = 0;
+#pragma unroll 8
+      for (int p = 0; p < RPP; ++p) t += red[p][d];
+      part[(g * C + c) * D + d] = t;
+    }
+    return;
+  }
+  const int qb = blockIdx.x - nkb, nqb = gridDim.x - nkb;
+  int fired = 0;
+  const float rinv = 1.f / ratio;
+  for (int64_t base = (int64_t)qb * RPP * PRO_QP; base < qrows;
+       base += (int64_t)nqb * RPP * PRO_QP) {
+    uint4 raw[PRO_QP];  // all of this thread's rows are fetched before any is processed
+#pragma unroll
+    for (int p = 0; p < PRO_QP; ++p) {
+      const int64_t r = base + p * RPP + sub;
+      raw[p] = r < qrows ? reinterpret_cast<const uint4*>(q + r * D)[lane] : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+  for (int p = 0; p < PRO_QP; ++p) {
+    const int64_t r = base + p * RPP + sub;
+    const bool live = r < qrows;
+    float f[8];
+    unpack_h8(raw[p], f);
+    float mx = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(f[e]));
+    mx = group_max<LPR>(mx);
+    const float s = mx * (1.0f / 127.0f);
+    const float safe = (s == 0.f) ? 1.f : s;
+    if (live) {
+      if (lane == 0) q_scale[r] = safe * qmul;
+      reinterpret_cast<uint2*>(q_i8 + r * D)[lane] = codes8(f, safe);
+    }
+    if constexpr (GATE) {
+      // y = fl(|x| + 1e-10) against t = max / ratio: far from t the exact test
+      // fl(max / y) > ratio is decided by y < t; within 2^-18 of t (relative)
+      // the IEEE division decides.
+      // (t below 2^-100: every element takes the division.)
+      const float t = mx * rinv;
+      const bool tiny = t < 0x1p-100f;
+      const float tlo = tiny ? 0.f : t * (1.f - 0x1p-18f);
+      const float thi = tiny ? INFINITY : t * (1.f + 0x1p-18f);
+      int cnt = 0, nan = 0;
+      bool amb = false;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float a = fabsf(f[e]);
+        nan |= a != a;
+        const float y = a + 1e-10f;
+        cnt += y < tlo;
+        amb |= y >= tlo && y <= thi;
+      }
+      if (__builtin_expect(__ballot(amb) != 0, 0)) {
+        if (amb) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float y = fabsf(f[e]) + 1e-10f;
+            if (y >= tlo && y <= thi) cnt += __fdiv_rn(mx, y) > ratio;
+          }
+        }
+      }
+      cnt = group_sum<LPR>(cnt + (nan << 16));  // NaN count in the high half
+      if (live && (cnt >> 16) == 0 && (cnt & 0xFFFF) > (D - 1) / 2) fired = 1;
+    }
+  }
+  }
+  if constexpr (GATE) {
+    fired = __syncthreads_or(fired);
+    if (threadIdx.x == 0) fire[qb] = fired;
+  }
+}
+
+// Mean of each (group, column) from its partial sums, and the gate flag.
+__global__ void __launch_bounds__(256)
+prologue_mean_kernel(const long long* __restrict__ part, int64_t G, int C, int D, int64_t N,
+                     float* __restrict__ k_mean, const int32_t* __restrict__ fire, int nfire,
+                     int32_t* __restrict__ flag) {
+  if (flag && blockIdx.x == 0) {
+    int any = 0;
+#pragma unroll 8
+    for (int i = threadIdx.x; i < nfire; i += 256) any |= fire[i];
+    any = __syncthreads_or(any);
+    if (threadIdx.x == 0) *flag = any;
+    return;  // block 0 only reduces the flag
+  }
+  // 8 lanes per column, each summing every 8th partial, then a lane reduction
+  const int64_t t8 = (int64_t)(blockIdx.x - (flag ? 1 : 0)) * 256 + threadIdx.x;
+  const int64_t i = t8 >> 3;
+  const int cl = (int)(t8 & 7);
+  const bool live = i < G * D;  // uniform per 8-lane group
+  long long t = 0;
+  if (live) {
+    const int64_t g = i / D, d = i % D;
+    const long long* p = part + g * C * D + d;
+#pragma unroll 4
+    for (int c = cl; c < C; c += 8) t += p[(int64_t)c * D];
+  }
+#pragma unroll
+  for (int o = 4; o > 0; o >>= 1) {
+    const int lo = __shfl_xor((int)(unsigned)t, o, 64);
+    const int hi = __shfl_xor((int)(t >> 32), o, 64);
+    t += (long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
+  }
+  if (live && cl == 0) k_mean[i] = (float)(((double)t * 0x1p-24) / (double)N);
+}
+
+template <int D>
+__global__ void __launch_bounds__(256)
+prologue_b_kernel(const uint16_t* __restrict__ k, int64_t N, const float* __restrict__ k_mean,
+                  int8_t* __restrict__ k_i8, float* __restrict__ k_scale) {
+  constexpr int LPR = D / 8, RPP = 256 / LPR;
+  constexpr int NP = PRO_KROWS / RPP;
+  const int64_t g = blockIdx.y;
+  const int lane = threadIdx.x % LPR, sub = threadIdx.x / LPR;
+  const int64_t n0 = (int64_t)blockIdx.x * PRO_KROWS;
+  const uint16_t* kg = k + g * N * D;
+  uint4 raw[NP];
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const int64_t n = n0 + i * RPP + sub;
+    raw[i] = n < N ? reinterpret_cast<const uint4*>(kg + n * D)[lane] : make_uint4(0, 0, 0, 0);
+  }
+  const float4 m0 = reinterpret_cast<const float4*>(k_mean + g * D)[2 * lane];
+  const float4 m1 = reinterpret_cast<const float4*>(k_mean + g * D)[2 * lane + 1];
+  const float mv[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const int64_t n = n0 + i * RPP + sub;
+    const bool live = n < N;
+    float f[8];
+    unpack_h8(raw[i], f);
+    float mx = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      f[e] = Elem<SL8_DTYPE_F16>::round(f[e] - mv[e]);
+      mx = fmaxf(mx, fabsf(f[e]));
+    }
+    mx = group_max<LPR>(mx);
+    const float s = mx * (1.0f / 127.0f);
+    const float safe = (s == 0.f) ? 1.f : s;
+    if (live) {
+      if (lane == 0) k_scale[g * N + n] = safe;
+      reinterpret_cast<uint2*>(k_i8 + (g * N + n) * D)[lane] = codes8(f, safe);
+    }
+  }
+}
+
+int prologue_nqb(int64_t qrows, int64_t D) {
+  const int64_t rpp = 256 / (D / 8) * PRO_QP;
+  return (int)std::min<int64_t>(PRO_QBLOCKS_MAX, (qrows + rpp - 1) / rpp);
+}
+
+}  // namespace
+}  // namespace sl8
+
+extern "C" size_t sl8_quantize_qk_workspace(int64_t BHq_M, int64_t G, int64_t N, int64_t D) {
+  if (G <= 0 || N <= 0 || D <= 0) return 0;
+  const int64_t C = (N + PRO_CHUNK - 1) / PRO_CHUNK;
+  const size_t parts = (size_t)(G * C * D) * sizeof(long long);
+  return parts + (size_t)(BHq_M > 0 ? prologue_nqb(BHq_M, D) : 0) * sizeof(int32_t);
+}
+
+extern "C" int sl8_quantize_qk(const void* q, const void* k, int dtype, int64_t qrows, int64_t G,
+                               int64_t N, int64_t D, float q_scale_mul, float gate_ratio,
+                               int8_t* q_i8, float* q_scale, int8_t* k_i8, float* k_scale,
+                               float* k_mean, int32_t* gate_flag, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  clear_error();
+  SL8_CHECK_ARG(dtype == SL8_DTYPE_F16, "fused prologue: q and k must be float16");
+  SL8_CHECK_ARG(D == 64 || D == 128 || D == 256,
+                "fused prologue: head dim must be 64/128/256, got %lld", (long long)D);
+  SL8_CHECK_ARG(qrows > 0 && G > 0 && N > 0 && N < (1LL << 23),
+                "fused prologue: bad shape (rows %lld, groups %lld, keys %lld)", (long long)qrows,
+                (long long)G, (long long)N);
+  SL8_CHECK_ARG(q && k && q_i8 && q_scale && k_i8 && k_scale && k_mean, "fused prologue: null pointer");
+  SL8_CHECK_ARG(aligned(q, 16) && aligned(k, 16) && aligned(q_i8, 8) && aligned(k_i8, 8),
+                "fused prologue: q/k must be 16-byte and codes 8-byte aligned");
+  const bool gate = gate_ratio > 0.f;
+  SL8_CHECK_ARG(!gate || gate_flag, "fused prologue: gate_flag required with a gate ratio");
+  const size_t need = sl8_quantize_qk_workspace(qrows, G, N, D);
+  SL8_CHECK_ARG(workspace && workspace_bytes >= need && aligned(workspace, 8),
+                "fused prologue: workspace needs %zu bytes", need);
+  const int C = (int)((N + PRO_CHUNK - 1) / PRO_CHUNK);
+  const int64_t nkb64 = G * C;
+  SL8_CHECK_ARG(nkb64 < (1LL << 30) && G < 65536, "fused prologue: too many key groups");
+  const int nkb = (int)nkb64, nqb = prologue_nqb(qrows, D);
+  long long* part = static_cast<long long*>(workspace);
+  int32_t* fire = reinterpret_cast<int32_t*>(part + G * C * D);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const uint16_t* qh = static_cast<const uint16_t*>(q);
+  const uint16_t* kh = static_cast<const uint16_t*>(k);
+  const dim3 gb((unsigned)((N + PRO_KROWS - 1) / PRO_KROWS), (unsigned)G);
+#define SL8_PRO(DD)                                                                              \
+  do {                                                                                          \
+    if (gate)                                                                                   \
+      prologue_a_kernel<DD, true><<<nkb + nqb, 256, 0, st>>>(qh, kh, qrows, N, nkb, C,          \
+          q_scale_mul, gate_ratio, q_i8, q_scale, part, fire);                                  \
+    else                                                                                        \
+      prologue_a_kernel<DD, false><<<nkb + nqb, 256, 0, st>>>(qh, kh, qrows, N, nkb, C,         \
+          q_scale_mul, gate_ratio, q_i8, q_scale, part, fire);                                  \
+    prologue_mean_kernel<<<(unsigned)((G * DD * 8 + 255) / 256 + (gate ? 1 : 0)), 256, 0, st>>>(\
+        part, G, C, DD, N, k_mean, fire, nqb, gate ? gate_flag : nullptr);                       \
+    prologue_b_kernel<DD><<<gb, 256, 0, st>>>(kh, N, k_mean, k_i8, k_scale);                     \
+  } while (0)
+  if (D == 64) SL8_PRO(64);
+  else if (D == 128) SL8_PRO(128);
+  else SL8_PRO(256);
+#undef SL8_PRO
+  SL8_CHECK_LAUNCH("fused prologue");
+  return SL8_OK;
+}

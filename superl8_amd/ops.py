@@ -33,7 +33,11 @@ def attn_int8_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: 
     """
     from . import quant
 
-    if internal_accuracy_gate and quant.detect_q_outlier_domination(q):
+    if internal_accuracy_gate:
+        fired, qk = quant.quantize_qk_gated(q, k, softmax_scale=scale, rotate=rotate)
+    else:
+        fired, qk = False, quant.quantize_qk(q, k, softmax_scale=scale, rotate=rotate)
+    if fired:
         import torch.nn.functional as F
 
         s = (1.0 / math.sqrt(q.shape[-1])) if scale is None else scale
@@ -51,8 +55,7 @@ def attn_int8_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: 
             is_causal=causal and attn_mask is None, scale=s,
             enable_gqa=q.shape[1] != k.shape[1]).to(v.dtype)
 
-    q_i8, q_scale, k_i8, k_scale, _k_mean = quant.quantize_qk(q, k, softmax_scale=scale,
-                                                              rotate=rotate)
+    q_i8, q_scale, k_i8, k_scale, _k_mean = qk
     q_scale = q_scale.squeeze(-1).contiguous()
     k_scale = k_scale.squeeze(-1).contiguous()
     if int8_pv:

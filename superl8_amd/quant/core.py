@@ -90,17 +90,59 @@ def detect_q_outlier_domination(q: torch.Tensor, *, ratio_threshold: float = 12.
     return bool(((row_max / (row_med + 1e-10)) > ratio_threshold).any())
 
 
+def _fused_ok(q: torch.Tensor, k: torch.Tensor) -> bool:
+    """Shapes the fused fp16 prologue (sl8_quantize_qk) serves."""
+    return (q.dtype == torch.float16 and k.dtype == torch.float16 and q.dim() == 4
+            and k.dim() == 4 and q.shape[-1] == k.shape[-1] and q.shape[-1] in (64, 128, 256)
+            and q.shape[0] == k.shape[0] and q.numel() > 0 and k.numel() > 0
+            and k.shape[-2] < (1 << 23))
+
+
+def quantize_qk_gated(q: torch.Tensor, k: torch.Tensor, *, softmax_scale: float | None = None,
+                      rotate: bool = False, ratio_threshold: float = 12.0):
+    """The attention prologue with the outlier gate (reference ops.py:115-150).
+
+    Returns (fired, quantize_qk's five outputs or None). fired is
+    detect_q_outlier_domination(q); when it holds the quantised tensors are
+    not needed (the caller routes to full precision). For fp16 Q/K without
+    rotation the gate is decided inside the fused prologue (one flag read);
+    otherwise it is evaluated first and quantize_qk runs only when it passes.
+    Under graph capture the gate is skipped (False), as in
+    detect_q_outlier_domination.
+    """
+    _need_gpu(q, "quantize_qk")
+    try:
+        capturing = torch.cuda.is_current_stream_capturing()
+    except Exception:
+        capturing = False
+    if not rotate and not capturing and _fused_ok(q, k):
+        s = (1.0 / math.sqrt(q.shape[-1])) if softmax_scale is None else softmax_scale
+        q_i8, q_scale, k_i8, k_scale, k_mean, flag = _C.quantize_qk_fused(
+            q, k, s * LOG2E, ratio_threshold)
+        if bool(flag.item()):
+            return True, None
+        return False, (q_i8, q_scale.unsqueeze(-1), k_i8, k_scale.unsqueeze(-1), k_mean)
+    if detect_q_outlier_domination(q, ratio_threshold=ratio_threshold):
+        return True, None
+    return False, quantize_qk(q, k, softmax_scale=softmax_scale, rotate=rotate)
+
+
 def quantize_qk(q: torch.Tensor, k: torch.Tensor, *, softmax_scale: float | None = None,
                 rotate: bool = False):
     """Quantise Q and smoothed K for the int8 QK^T.
 
     Returns (q_int8, q_scale[..., m, 1] folded with softmax_scale*log2(e),
-    k_int8, k_scale[..., n, 1], k_mean[..., 1, d]). Smoothing and quantising K
-    is one fused kernel (the smoothed fp16 K is never written).
+    k_int8, k_scale[..., n, 1], k_mean[..., 1, d]). fp16 Q/K without rotation
+    take the fused prologue (three launches); otherwise the K mean and the
+    smooth-and-quantise of each side are separate kernels (the smoothed K is
+    never written either way).
     """
     _need_gpu(q, "quantize_qk")
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(q.shape[-1])
+    if not rotate and _fused_ok(q, k):
+        q_i8, q_scale, k_i8, k_scale, k_mean, _ = _C.quantize_qk_fused(q, k, softmax_scale * LOG2E)
+        return q_i8, q_scale.unsqueeze(-1), k_i8, k_scale.unsqueeze(-1), k_mean
     if rotate:
         from .rotation import rotate_last
 
