@@ -241,6 +241,30 @@ int sl8_gemm_q4k(const int8_t* x, const float* x_scale, const uint8_t* w, void* 
  * the test decoder tests/test_gemm_q4k.py:132-148. */
 int sl8_dequant_q4k(const uint8_t* w, float* out, int64_t N, int64_t K, void* stream);
 
+/* ------------------------------------------------------------------------
+ * GGUF Q5_K / Q6_K linear (native 176 / 210-byte super-blocks), same
+ * arguments and contract as the Q4_K pair above:
+ *   Q5_K: y = x_scale * sum_j (d*sc_j*<x_j,q_j> - dmin*m_j*sum(x_j)), q 5-bit
+ *   Q6_K: y = x_scale * sum_i d*sc_i*<x_i, q_i - 32>, 16-element sub-blocks
+ * sl8_gemm_q5k / sl8_gemm_q6k replace _C.gemm_q5k / _C.gemm_q6k (reference
+ * csrc/fni8_api.cpp:64-67,338-347, csrc/include/gemm_q4k_dp4a.cuh:200-489); any M.
+ * sl8_gemm_decode_q5k / _q6k replace _C.gemm_decode_q5k / _q6k (fni8_api.cpp:
+ * 70-73,353-360, csrc/kernel/gemm_decode_dp4a.cu:377-446); M <= 16.
+ * The Q6_K weight buffer is read in whole dwords: it must stay readable up to
+ * its end rounded up to 4 bytes (torch allocations always are).
+ * sl8_dequant_q5k / _q6k: bytes -> fp32 [N, K], as the reference test decoders
+ * (tests/test_gemm_q4k.py:188-190,218-221). */
+int sl8_gemm_q5k(const int8_t* x, const float* x_scale, const uint8_t* w, void* out,
+                 int out_dtype, int64_t M, int64_t N, int64_t K, void* stream);
+int sl8_gemm_q6k(const int8_t* x, const float* x_scale, const uint8_t* w, void* out,
+                 int out_dtype, int64_t M, int64_t N, int64_t K, void* stream);
+int sl8_gemm_decode_q5k(const int8_t* x, const float* x_scale, const uint8_t* w, void* out,
+                        int out_dtype, int64_t M, int64_t N, int64_t K, void* stream);
+int sl8_gemm_decode_q6k(const int8_t* x, const float* x_scale, const uint8_t* w, void* out,
+                        int out_dtype, int64_t M, int64_t N, int64_t K, void* stream);
+int sl8_dequant_q5k(const uint8_t* w, float* out, int64_t N, int64_t K, void* stream);
+int sl8_dequant_q6k(const uint8_t* w, float* out, int64_t N, int64_t K, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,4 +1,4 @@
-"""CPU restatement of the reference's INT8-attention / Q4_K hot path (numpy).
+"""CPU restatement of the reference's INT8-attention / GGUF k-quant hot path (numpy).
 
 TEST INFRASTRUCTURE ONLY. Nothing in the product package imports this; only
 tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it, as the
@@ -8,4 +8,4 @@ Every function cites the reference file:line it restates. How each function is
 pinned (known answers, closed forms, brute force, invariants) is listed in
 tests/test_oracle.py; no function here is left unpinned.
 """
-from . import attention, q4k, quant  # noqa: F401
+from . import attention, kquant, q4k, quant  # noqa: F401

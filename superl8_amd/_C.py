@@ -25,6 +25,8 @@ _HEAD_DIMS_DECODE = (64, 128, 256)
 DEC_MAX_SPLITS = 256
 DEC_MAX_M = 16
 Q4K_TYPE_SIZE = 144
+Q5K_TYPE_SIZE = 176
+Q6K_TYPE_SIZE = 210
 
 
 def _check(cond: bool, msg: str) -> None:
@@ -448,26 +450,26 @@ def kv_write_paged(k_new, v_new, slot_mapping, k_cache, k_scale, v_cache, v_scal
 # ---------------------------------------------------------------------------
 # Q4_K (reference csrc/kernel/gemm_dp4a.cu:146-193, gemm_decode_dp4a.cu:375-436)
 # ---------------------------------------------------------------------------
-def _q4k_checks(x, x_scale, w, out_dtype, tag):
+def _q4k_checks(x, x_scale, w, out_dtype, tag, type_size=Q4K_TYPE_SIZE):
     _on_gpu(x, x_scale, w)
     _check(x.dtype == torch.int8, "x must be int8")
     _check(w.dtype == torch.uint8, f"w must be uint8 (native {tag} bytes)")
     _check(x_scale.dtype == torch.float32, "x_scale must be float32")
-    _check(x.dim() == 2 and w.dim() == 2, "expect x[M,K] and w[N,(K/256)*144]")
+    _check(x.dim() == 2 and w.dim() == 2, f"expect x[M,K] and w[N,(K/256)*{type_size}]")
     _contig(x, x_scale, w)
     _check(out_dtype in (torch.float16, torch.bfloat16, torch.float32),
            f"out_dtype must be float16 or bfloat16, got {out_dtype}")
     M, K = x.shape
     N = w.shape[0]
-    _check(K % 256 == 0, f"Q4_K contraction dim K must be %256==0, got {K}")
-    _check(w.shape[1] == (K // 256) * Q4K_TYPE_SIZE,
-           f"Q4_K weight must be [N, (K/256)*144], got [{N},{w.shape[1]}] for K={K}")
+    _check(K % 256 == 0, f"{tag} contraction dim K must be %256==0, got {K}")
+    _check(w.shape[1] == (K // 256) * type_size,
+           f"{tag} weight must be [N, (K/256)*{type_size}], got [{N},{w.shape[1]}] for K={K}")
     _check(x_scale.numel() == M, "x_scale must be [M]")
     return M, N, K
 
 
-def _q4k(sym, x, x_scale, w, out_dtype):
-    M, N, K = _q4k_checks(x, x_scale, w, out_dtype, "Q4_K")
+def _q4k(sym, x, x_scale, w, out_dtype, tag="Q4_K", type_size=Q4K_TYPE_SIZE):
+    M, N, K = _q4k_checks(x, x_scale, w, out_dtype, tag, type_size)
     out = torch.empty((M, N), device=x.device, dtype=out_dtype)
     if M and N:
         with torch.cuda.device(x.device):
@@ -487,6 +489,54 @@ def gemm_decode_q4k(x, x_scale, w, out_dtype=torch.float16):
            f"gemm_decode_q4k supports M<={DEC_MAX_M}, got M={x.shape[0] if x.dim() else 0}"
            " -- use the tile gemm_q4k for prefill")
     return _q4k("sl8_gemm_decode_q4k", x, x_scale, w, out_dtype)
+
+
+def gemm_q5k(x, x_scale, w, out_dtype=torch.float16):
+    """x int8 [M,K], x_scale fp32 [M], w uint8 [N,(K/256)*176] (native Q5_K) -> [M,N]."""
+    return _q4k("sl8_gemm_q5k", x, x_scale, w, out_dtype, "Q5_K", Q5K_TYPE_SIZE)
+
+
+def gemm_q6k(x, x_scale, w, out_dtype=torch.float16):
+    """x int8 [M,K], x_scale fp32 [M], w uint8 [N,(K/256)*210] (native Q6_K) -> [M,N]."""
+    return _q4k("sl8_gemm_q6k", x, x_scale, w, out_dtype, "Q6_K", Q6K_TYPE_SIZE)
+
+
+def gemm_decode_q5k(x, x_scale, w, out_dtype=torch.float16):
+    """Decode-shape (M <= 16) Q5_K GEMV; same math as gemm_q5k."""
+    _check(x.dim() == 2 and x.shape[0] <= DEC_MAX_M,
+           f"gemm_decode_q5k supports M<={DEC_MAX_M}, got M={x.shape[0] if x.dim() else 0}"
+           " -- use the tile gemm_q5k for prefill")
+    return _q4k("sl8_gemm_decode_q5k", x, x_scale, w, out_dtype, "Q5_K", Q5K_TYPE_SIZE)
+
+
+def gemm_decode_q6k(x, x_scale, w, out_dtype=torch.float16):
+    """Decode-shape (M <= 16) Q6_K GEMV; same math as gemm_q6k."""
+    _check(x.dim() == 2 and x.shape[0] <= DEC_MAX_M,
+           f"gemm_decode_q6k supports M<={DEC_MAX_M}, got M={x.shape[0] if x.dim() else 0}"
+           " -- use the tile gemm_q6k for prefill")
+    return _q4k("sl8_gemm_decode_q6k", x, x_scale, w, out_dtype, "Q6_K", Q6K_TYPE_SIZE)
+
+
+def _dequant_kq(sym, w, K, tag, type_size):
+    _on_gpu(w)
+    _check(w.dtype == torch.uint8 and w.dim() == 2, f"w must be uint8 [N,(K/256)*{type_size}]")
+    _check(K % 256 == 0 and w.shape[1] == (K // 256) * type_size, f"{tag} weight/K mismatch")
+    w = w.contiguous()
+    out = torch.empty((w.shape[0], K), device=w.device, dtype=torch.float32)
+    if out.numel():
+        with torch.cuda.device(w.device):
+            call(sym, w.data_ptr(), out.data_ptr(), w.shape[0], K, stream_of(w))
+    return out
+
+
+def dequant_q5k(w: torch.Tensor, K: int) -> torch.Tensor:
+    """Native Q5_K bytes [N,(K/256)*176] -> fp32 [N,K] (d*sc*q - dmin*m, fp32)."""
+    return _dequant_kq("sl8_dequant_q5k", w, K, "Q5_K", Q5K_TYPE_SIZE)
+
+
+def dequant_q6k(w: torch.Tensor, K: int) -> torch.Tensor:
+    """Native Q6_K bytes [N,(K/256)*210] -> fp32 [N,K] ((d*sc)*(q-32), fp32)."""
+    return _dequant_kq("sl8_dequant_q6k", w, K, "Q6_K", Q6K_TYPE_SIZE)
 
 
 def dequant_q4k(w: torch.Tensor, K: int) -> torch.Tensor:

@@ -53,6 +53,12 @@ SIGNATURES = {
     "sl8_gemm_decode_q4k": (_I, [_P, _P, _P, _P, _I, _I64, _I64, _I64, _P]),
     "sl8_gemm_q4k": (_I, [_P, _P, _P, _P, _I, _I64, _I64, _I64, _P]),
     "sl8_dequant_q4k": (_I, [_P, _P, _I64, _I64, _P]),
+    "sl8_gemm_q5k": (_I, [_P, _P, _P, _P, _I, _I64, _I64, _I64, _P]),
+    "sl8_gemm_q6k": (_I, [_P, _P, _P, _P, _I, _I64, _I64, _I64, _P]),
+    "sl8_gemm_decode_q5k": (_I, [_P, _P, _P, _P, _I, _I64, _I64, _I64, _P]),
+    "sl8_gemm_decode_q6k": (_I, [_P, _P, _P, _P, _I, _I64, _I64, _I64, _P]),
+    "sl8_dequant_q5k": (_I, [_P, _P, _I64, _I64, _P]),
+    "sl8_dequant_q6k": (_I, [_P, _P, _I64, _I64, _P]),
 }
 
 _lib = None

@@ -1,0 +1,514 @@
+// GGUF Q5_K and Q6_K linear layers on native super-blocks, gfx950.
+//
+// Math (reference csrc/include/gemm_q4k_dp4a.cuh:200-489, the dp4a tile
+// kernels, and csrc/include/gemm_decode_dp4a.cuh's decode variants):
+//   Q5_K: y[m,n] = x_scale[m] * sum_j ( d*sc_j*<x_j, q_j> - dmin*m_j*sum(x_j) )
+//         over 32-element sub-blocks j; q in [0,31] (4 bits in qs with
+//         Q4_K's nibble interleave, the 5th bit in qh); sc_j, m_j 6-bit.
+//   Q6_K: y[m,n] = x_scale[m] * sum_i d*sc_i*<x_i, q_i - 32>
+//         over 16-element sub-blocks i; q in [0,63] (4 bits in ql, 2 in qh);
+//         sc_i signed int8.
+// x is the per-row int8 activation with its fp32 scale.
+//
+// Tile GEMM (any M; used for M > 16): a 128 x 128 output tile per workgroup,
+// 4 waves of 64 x 64 (2 x 2 blocks of 32 x 32), the x tile and the 128 weight
+// super-blocks copied global -> LDS one super-block ahead (double-buffered).
+// The integer dot products stay exact:
+//   Q5_K on v_mfma_i32_32x32x32_i8, one K = 32 step per sub-block: with
+//     q = n + 16 b (n the low nibble, b the 5th bit), q * sc_j =
+//     n (sc_j & 7) + 8 (n (sc_j >> 3) + 2 b sc_j), and each of the three B
+//     operands n (sc & 7), n (sc >> 3), 2 b sc is at most 126, so it fits int8
+//     (a 32-bit multiply scales 4 codes at once without carries). Three
+//     MFMAs into T_lo, T_hi, T_hi plus one with m_j broadcast (the min term);
+//     per super-block f += d * (T_lo + 8 T_hi) - dmin * U.
+//   Q6_K on v_mfma_f32_32x32x16_f16, one K = 16 step per sub-block: x (int8)
+//     and (q - 32) * s are small integers, exact in fp16, with sc = 16 s_hi +
+//     s_lo (s_lo in [0,15], s_hi in [-8,7]) so |(q-32) * s| <= 480; the fp32
+//     accumulators T_lo, T_hi stay below 2^24 over a super-block (exact), and
+//     f += d * (T_lo + 16 T_hi).
+// Q6_K super-blocks are 210 bytes, so they start on 2-byte boundaries: each is
+// copied as the 53 dwords from its address rounded down to 4, and read back
+// from LDS with v_alignbyte.
+
+#include "kquant.hpp"
+
+namespace sl8 {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i_t __attribute__((ext_vector_type(16)));
+typedef float v16f_t __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h_t __attribute__((ext_vector_type(8)));
+typedef _Float16 v2h_t __attribute__((ext_vector_type(2)));
+
+constexpr int Q5K_BYTES = 176;
+constexpr int Q6K_BYTES = 210;
+constexpr int KBM = 128, KBN = 128;                       // output tile
+constexpr int T5CH = (KBN * 11 + 255) / 256 * 256;       // Q5_K weight-tile 16-B chunks
+constexpr int Q6DW = 53;                                  // dwords per staged Q6_K block
+constexpr int Q6PITCH = Q6DW * 4;                         // 212 bytes
+constexpr int T6DW = (KBN * Q6DW + 255) / 256 * 256 + 64; // Q6_K weight-tile dwords (+ read slack)
+
+// x tile copy: 128 rows x 256 int8 of super-block sb; 16-byte chunk c of row r
+// lands at r * 256 + 16 * (c ^ (r & 15)) (rows are one 256-byte bank line).
+__device__ __forceinline__ void copy_x_tile(const int8_t* x, int8_t* xd, int m0, int M, int K, int sb,
+                                            int tid, int wave) {
+#pragma unroll
+  for (int i = 0; i < KBM * 16 / 256; ++i) {
+    const int P = i * 256 + tid, row = P >> 4;
+    const int c = (P & 15) ^ (row & 15);
+    const int8_t* src = x + (int64_t)min(m0 + row, M - 1) * K + (int64_t)sb * 256 + 16 * c;
+    __builtin_amdgcn_global_load_lds((kq_gptr_t)src, (kq_lptr_t)(xd + (i * 256 + wave * 64) * 16), 16, 0, 0);
+  }
+}
+
+// 8 int8 -> 8 fp16 (exact): byte u = x + 128 becomes fp16 bits 0x64uu = 1024 + u.
+__device__ __forceinline__ v8h_t i8x8_to_h(uint2 w) {
+  const uint32_t a = w.x ^ 0x80808080u, b = w.y ^ 0x80808080u;
+  uint32_t r[4] = {__builtin_amdgcn_perm(0x64646464u, a, 0x04010400u),
+                   __builtin_amdgcn_perm(0x64646464u, a, 0x04030402u),
+                   __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u),
+                   __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u)};
+  v8h_t v = __builtin_bit_cast(v8h_t, r);
+  const _Float16 off = (_Float16)1152.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] -= off;
+  return v;
+}
+
+// 8 codes (bytes, 0..63) -> 8 fp16 of (q - 32) (exact).
+__device__ __forceinline__ v8h_t q6x8_to_h(uint32_t a, uint32_t b) {
+  uint32_t r[4] = {__builtin_amdgcn_perm(0x64646464u, a, 0x04010400u),
+                   __builtin_amdgcn_perm(0x64646464u, a, 0x04030402u),
+                   __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u),
+                   __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u)};
+  v8h_t v = __builtin_bit_cast(v8h_t, r);
+  const _Float16 off = (_Float16)1056.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] -= off;
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// Q5_K tile GEMM
+// ---------------------------------------------------------------------------
+template <int OUT_DT>
+__global__ void __launch_bounds__(256, 1)
+gemm_q5k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
+                     const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K) {
+  __shared__ __attribute__((aligned(16))) int8_t xs0[KBM * 256];
+  __shared__ __attribute__((aligned(16))) int8_t xs1[KBM * 256];
+  __shared__ __attribute__((aligned(16))) uint8_t ws0[T5CH * 16];
+  __shared__ __attribute__((aligned(16))) uint8_t ws1[T5CH * 16];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  const int l32 = lane & 31, h = lane >> 5;
+  const int n0 = blockIdx.x * KBN, m0 = blockIdx.y * KBM;
+  const int nsb = K >> 8;
+  const int64_t row_bytes = (int64_t)nsb * Q5K_BYTES;
+
+  auto load = [&](int sb, int8_t* xd, uint8_t* wd) __attribute__((always_inline)) {
+    copy_x_tile(x, xd, m0, M, K, sb, tid, wave);
+#pragma unroll
+    for (int i = 0; i < T5CH / 256; ++i) {
+      const int P = min(i * 256 + tid, KBN * 11 - 1), row = P / 11, c = P - 11 * row;
+      const uint8_t* src = w + (int64_t)min(n0 + row, N - 1) * row_bytes + (int64_t)sb * Q5K_BYTES + 16 * c;
+      __builtin_amdgcn_global_load_lds((kq_gptr_t)src, (kq_lptr_t)(wd + (i * 256 + wave * 64) * 16), 16, 0, 0);
+    }
+  };
+
+  float f[2][2][16];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b2 = 0; b2 < 2; ++b2)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) f[a][b2][e] = 0.f;
+
+  auto compute = [&](const int8_t* xt, const uint8_t* wt) __attribute__((always_inline)) {
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      const uint8_t* wr = wt + (64 * wn + 32 * cb + l32) * Q5K_BYTES;
+      const uint4 hd = *reinterpret_cast<const uint4*>(wr);
+      const float d = h2f(hd.x & 0xFFFFu), dmin = h2f(hd.x >> 16);
+      const ScMin sm = unpack_scmin(hd.y, hd.z, hd.w);
+      const uint4 qhv = *reinterpret_cast<const uint4*>(wr + 16 + 16 * h);  // qh of l = 16h..16h+15
+      const uint32_t qh[4] = {qhv.x, qhv.y, qhv.z, qhv.w};
+      v16i_t tl[2], th[2], tu[2];
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) tl[rb][e] = th[rb][e] = tu[rb][e] = 0;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const uint4 qv = *reinterpret_cast<const uint4*>(wr + 48 + 32 * g + 16 * h);
+        const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+        for (int hi = 0; hi < 2; ++hi) {
+          const int j = 2 * g + hi;
+          const uint32_t scw = j < 4 ? sm.sc_lo : sm.sc_hi, mnw = j < 4 ? sm.mn_lo : sm.mn_hi;
+          const uint32_t sc = (scw >> (8 * (j & 3))) & 0xFF, mn = (mnw >> (8 * (j & 3))) & 0xFF;
+          // q = n + 16 b (n the nibble, b the 5th bit): q * sc = n (sc & 7) +
+          // 8 (n (sc >> 3) + 2 b sc); every B byte <= 126
+          v4i bl, bh, bb;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t nib = (qw[e] >> (4 * hi)) & 0x0F0F0F0Fu;
+            const uint32_t hb = (qh[e] >> j) & 0x01010101u;
+            bl[e] = (int)(nib * (sc & 7));
+            bh[e] = (int)(nib * (sc >> 3));
+            bb[e] = (int)(hb * (2 * sc));
+          }
+          const int bmv = (int)(mn * 0x01010101u);
+          const v4i bm = {bmv, bmv, bmv, bmv};
+#pragma unroll
+          for (int rb = 0; rb < 2; ++rb) {
+            // A: rows 64 wm + 32 rb + l32, elements 32 j + 16 h .. +15
+            const int row = 64 * wm + 32 * rb + l32;
+            const v4i A = *reinterpret_cast<const v4i*>(xt + row * 256 + 16 * ((2 * j + h) ^ (row & 15)));
+            tl[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, bl, tl[rb], 0, 0, 0);
+            th[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, bh, th[rb], 0, 0, 0);
+            th[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, bb, th[rb], 0, 0, 0);
+            tu[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, bm, tu[rb], 0, 0, 0);
+          }
+        }
+      }
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          f[rb][cb][e] += d * (float)(tl[rb][e] + 8 * th[rb][e]) - dmin * (float)tu[rb][e];
+    }
+  };
+
+  load(0, xs0, ws0);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __syncthreads();
+  int sb = 0;
+  for (; sb + 1 < nsb; sb += 2) {
+    load(sb + 1, xs1, ws1);
+    compute(xs0, ws0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+    if (sb + 2 < nsb) load(sb + 2, xs0, ws0);
+    compute(xs1, ws1);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+  }
+  if (sb < nsb) compute(xs0, ws0);
+
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int m = m0 + 64 * wm + 32 * rb + 8 * (e >> 2) + 4 * h + (e & 3);
+      if (m < M) {
+        const float xsm = x_scale[m];
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+          const int n = n0 + 64 * wn + 32 * cb + l32;
+          if (n < N) st_out<OUT_DT>(out, (int64_t)m * N + n, f[rb][cb][e] * xsm);
+        }
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Q6_K tile GEMM
+// ---------------------------------------------------------------------------
+// 8 bytes at a 2-byte aligned LDS address (aligned dword reads + v_alignbyte).
+__device__ __forceinline__ uint2 lds8_at(const uint8_t* p) {
+  const uintptr_t ad = reinterpret_cast<uintptr_t>(p);
+  const uint32_t* a = reinterpret_cast<const uint32_t*>(ad & ~(uintptr_t)3);
+  const uint32_t sh = (uint32_t)(ad & 3);
+  const uint32_t d0 = a[0], d1 = a[1], d2 = a[2];
+  return make_uint2(__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh));
+}
+
+template <int OUT_DT>
+__global__ void __launch_bounds__(256, 1)
+gemm_q6k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
+                     const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K) {
+  __shared__ __attribute__((aligned(16))) int8_t xs0[KBM * 256];
+  __shared__ __attribute__((aligned(16))) int8_t xs1[KBM * 256];
+  __shared__ __attribute__((aligned(16))) uint32_t ws0[T6DW];
+  __shared__ __attribute__((aligned(16))) uint32_t ws1[T6DW];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  const int l32 = lane & 31, h = lane >> 5;
+  const int n0 = blockIdx.x * KBN, m0 = blockIdx.y * KBM;
+  const int nsb = K >> 8;
+  const int64_t row_bytes = (int64_t)nsb * Q6K_BYTES;
+
+  // staged block of weight row r: LDS bytes r * 212 + (its global address & 3)
+  auto load = [&](int sb, int8_t* xd, uint32_t* wd) __attribute__((always_inline)) {
+    copy_x_tile(x, xd, m0, M, K, sb, tid, wave);
+    // dword P = 256 i + tid of the tile is dword c of row P / 53; walked as a
+    // recurrence (256 = 4 * 53 + 44) so no per-i row address stays live
+    int t0 = tid;
+    asm volatile("" : "+v"(t0));  // keep the walk inside the super-block loop (no hoisted addresses)
+    int row = t0 / Q6DW, c = t0 - Q6DW * (t0 / Q6DW);
+    const int64_t sboff = (int64_t)sb * Q6K_BYTES;
+#pragma unroll
+    for (int i = 0; i < (T6DW - 64) / 256; ++i) {
+      const int64_t base = (int64_t)min(n0 + min(row, KBN - 1), N - 1) * row_bytes + sboff;
+      const uint8_t* src = w + (base & ~(int64_t)3) + 4 * (row < KBN ? c : Q6DW - 1);
+      __builtin_amdgcn_global_load_lds((kq_gptr_t)src, (kq_lptr_t)(wd + i * 256 + wave * 64), 4, 0, 0);
+      c += 44;
+      row += 4;
+      if (c >= Q6DW) { c -= Q6DW; ++row; }
+    }
+  };
+
+  float f[2][2][16];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b2 = 0; b2 < 2; ++b2)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) f[a][b2][e] = 0.f;
+
+  auto compute = [&](int sb, const int8_t* xt, const uint32_t* wt) __attribute__((always_inline)) {
+    const uint8_t* blk[2];
+    float dcb[2];
+    uint32_t scw[2][4];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      const int r = 64 * wn + 32 * cb + l32;
+      const int64_t base = (int64_t)min(n0 + r, N - 1) * row_bytes + (int64_t)sb * Q6K_BYTES;
+      blk[cb] = reinterpret_cast<const uint8_t*>(wt) + r * Q6PITCH + (int)(base & 3);
+      const uint2 s0 = lds8_at(blk[cb] + 192), s1 = lds8_at(blk[cb] + 200);
+      scw[cb][0] = s0.x; scw[cb][1] = s0.y; scw[cb][2] = s1.x; scw[cb][3] = s1.y;
+      dcb[cb] = h2f((uint16_t)(lds8_at(blk[cb] + 208).x & 0xFFFFu));
+    }
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      v16f_t tl[2], th[2];
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) tl[rb][e] = th[rb][e] = 0.f;
+#pragma unroll 1
+      for (int gi = 0; gi < 4; ++gi) {
+        const int g = gi >> 1, ih = gi & 1;
+          // lane h feeds elements l = 16 ih + 8 h .. +7 of each quadrant of half g
+          const uint2 qla = lds8_at(blk[cb] + 64 * g + 16 * ih + 8 * h);
+          const uint2 qlb = lds8_at(blk[cb] + 64 * g + 32 + 16 * ih + 8 * h);
+          const uint2 qhc = lds8_at(blk[cb] + 128 + 32 * g + 16 * ih + 8 * h);
+#pragma unroll
+          for (int qd = 0; qd < 4; ++qd) {
+            const int i = 8 * g + 2 * qd + ih;  // sub-block (scale index)
+            const uint2 ql = (qd & 1) ? qlb : qla;
+            const int ns = 4 * (qd >> 1), hs = 2 * qd;
+            const uint32_t c0 = ((ql.x >> ns) & 0x0F0F0F0Fu) | (((qhc.x >> hs) & 0x03030303u) << 4);
+            const uint32_t c1 = ((ql.y >> ns) & 0x0F0F0F0Fu) | (((qhc.y >> hs) & 0x03030303u) << 4);
+            const v8h_t v = q6x8_to_h(c0, c1);
+            const uint32_t sw = g ? scw[cb][2 + (qd >> 1)] : scw[cb][qd >> 1];  // scales 4(i>>2)..
+            const int sc = (int)(int8_t)((sw >> (8 * (2 * (qd & 1) + ih))) & 0xFF);
+            const _Float16 slo = (_Float16)(float)(sc & 15), shi = (_Float16)(float)(sc >> 4);
+            v8h_t blo, bhi;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) { blo[e] = v[e] * slo; bhi[e] = v[e] * shi; }
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb) {
+              const int row = 64 * wm + 32 * rb + l32;
+              const v8h_t A = i8x8_to_h(
+                  *reinterpret_cast<const uint2*>(xt + row * 256 + 16 * (i ^ (row & 15)) + 8 * h));
+              tl[rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, blo, tl[rb], 0, 0, 0);
+              th[rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, bhi, th[rb], 0, 0, 0);
+            }
+          }
+        }
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) f[rb][cb][e] += dcb[cb] * (tl[rb][e] + 16.f * th[rb][e]);
+    }
+  };
+
+  load(0, xs0, ws0);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __syncthreads();
+  int sb = 0;
+  for (; sb + 1 < nsb; sb += 2) {
+    load(sb + 1, xs1, ws1);
+    compute(sb, xs0, ws0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+    if (sb + 2 < nsb) load(sb + 2, xs0, ws0);
+    compute(sb + 1, xs1, ws1);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+  }
+  if (sb < nsb) compute(sb, xs0, ws0);
+
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int m = m0 + 64 * wm + 32 * rb + 8 * (e >> 2) + 4 * h + (e & 3);
+      if (m < M) {
+        const float xsm = x_scale[m];
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+          const int n = n0 + 64 * wn + 32 * cb + l32;
+          if (n < N) st_out<OUT_DT>(out, (int64_t)m * N + n, f[rb][cb][e] * xsm);
+        }
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Dequantisation to fp32 (checking and conversion helper)
+// ---------------------------------------------------------------------------
+__global__ void dequant_q5k_kernel(const uint8_t* __restrict__ w, float* __restrict__ out,
+                                   int64_t N, int K) {
+  const int nsub = K >> 5, nsb = K >> 8;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= N * nsub) return;
+  const int64_t n = t / nsub;
+  const int js = (int)(t % nsub), sb = js >> 3, j = js & 7;
+  const uint8_t* b = w + (n * nsb + sb) * Q5K_BYTES;
+  const uint32_t* hd = reinterpret_cast<const uint32_t*>(b);
+  const float d = h2f(hd[0] & 0xFFFFu), dmin = h2f(hd[0] >> 16);
+  const ScMin sm = unpack_scmin(hd[1], hd[2], hd[3]);
+  const uint32_t sc = byte_of(j < 4 ? sm.sc_lo : sm.sc_hi, j & 3);
+  const uint32_t mn = byte_of(j < 4 ? sm.mn_lo : sm.mn_hi, j & 3);
+  const float dsc = d * (float)sc, dm = dmin * (float)mn;
+  float* o = out + n * K + (int64_t)js * 32;
+  for (int l = 0; l < 32; ++l) {
+    const int q = ((b[48 + 32 * (j >> 1) + l] >> (4 * (j & 1))) & 15) | (((b[16 + l] >> j) & 1) << 4);
+    o[l] = __fsub_rn(__fmul_rn(dsc, (float)q), dm);  // two roundings, as the reference decoder
+  }
+}
+
+__global__ void dequant_q6k_kernel(const uint8_t* __restrict__ w, float* __restrict__ out,
+                                   int64_t N, int K) {
+  const int nsub = K >> 4, nsb = K >> 8;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= N * nsub) return;
+  const int64_t n = t / nsub;
+  const int is = (int)(t % nsub), sb = is >> 4, i = is & 15;
+  const uint8_t* b = w + (n * nsb + sb) * Q6K_BYTES;
+  const float d = h2f((uint16_t)(b[208] | (b[209] << 8)));
+  const float rs = d * (float)(int8_t)b[192 + i];
+  const int g = i >> 3, qd = (i & 7) >> 1, l0 = 16 * (i & 1);
+  float* o = out + n * K + (int64_t)is * 16;
+  for (int l = l0; l < l0 + 16; ++l) {
+    const int qlb = b[64 * g + 32 * (qd & 1) + l];
+    const int q = ((qlb >> (4 * (qd >> 1))) & 15) | (((b[128 + 32 * g + l] >> (2 * qd)) & 3) << 4);
+    o[l - l0] = __fmul_rn(rs, (float)(q - 32));
+  }
+}
+
+template <int FMT>
+void launch_kq_tile(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
+                    int M, int N, int K, hipStream_t st) {
+  const dim3 grid((unsigned)((N + KBN - 1) / KBN), (unsigned)((M + KBM - 1) / KBM));
+#define SL8_KQT(KERN)                                                                          \
+  switch (odt) {                                                                               \
+    case SL8_DTYPE_F16: KERN<SL8_DTYPE_F16><<<grid, 256, 0, st>>>(x, xs, w, out, M, N, K); break; \
+    case SL8_DTYPE_BF16: KERN<SL8_DTYPE_BF16><<<grid, 256, 0, st>>>(x, xs, w, out, M, N, K); break; \
+    default: KERN<SL8_DTYPE_F32><<<grid, 256, 0, st>>>(x, xs, w, out, M, N, K); break;        \
+  }
+  if (FMT == 5) { SL8_KQT(gemm_q5k_tile_kernel) }
+  else { SL8_KQT(gemm_q6k_tile_kernel) }
+#undef SL8_KQT
+}
+
+int check_kq(const char* name, const int8_t* x, const float* xs, const uint8_t* w, void* out,
+             int odt, int64_t M, int64_t N, int64_t K) {
+  SL8_CHECK_ARG(odt == SL8_DTYPE_F16 || odt == SL8_DTYPE_BF16 || odt == SL8_DTYPE_F32,
+                "out_dtype must be float16 or bfloat16 (or float32)");
+  SL8_CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "%s: bad shape", name);
+  SL8_CHECK_ARG(K % 256 == 0, "%s needs K%%256==0, got %lld", name, (long long)K);
+  SL8_CHECK_ARG(K <= 65536, "%s: K=%lld exceeds 65536", name, (long long)K);
+  SL8_CHECK_ARG(N < (1LL << 31) && M < (1LL << 31), "%s: shape too large", name);
+  if (M == 0 || N == 0 || K == 0) return SL8_OK;
+  SL8_CHECK_ARG(x && xs && w && out, "%s: null pointer", name);
+  SL8_CHECK_ARG(aligned(x, 16), "x must be 16-byte aligned for the vectorized int4 loads");
+  SL8_CHECK_ARG(aligned(w, 16), "%s: weight must be 16-byte aligned", name);
+  SL8_CHECK_ARG((M + KBM - 1) / KBM < 65536, "%s: M too large", name);
+  return SL8_OK;
+}
+
+}  // namespace
+}  // namespace sl8
+
+using namespace sl8;
+
+extern "C" int sl8_gemm_q5k(const int8_t* x, const float* x_scale, const uint8_t* w, void* out,
+                            int out_dtype, int64_t M, int64_t N, int64_t K, void* stream) {
+  clear_error();
+  int rc = check_kq("gemm_q5k", x, x_scale, w, out, out_dtype, M, N, K);
+  if (rc != SL8_OK || M == 0 || N == 0 || K == 0) return rc;
+  launch_kq_tile<5>(x, x_scale, w, out, out_dtype, (int)M, (int)N, (int)K,
+                    static_cast<hipStream_t>(stream));
+  SL8_CHECK_LAUNCH("gemm_q5k");
+  return SL8_OK;
+}
+
+extern "C" int sl8_gemm_q6k(const int8_t* x, const float* x_scale, const uint8_t* w, void* out,
+                            int out_dtype, int64_t M, int64_t N, int64_t K, void* stream) {
+  clear_error();
+  int rc = check_kq("gemm_q6k", x, x_scale, w, out, out_dtype, M, N, K);
+  if (rc != SL8_OK || M == 0 || N == 0 || K == 0) return rc;
+  launch_kq_tile<6>(x, x_scale, w, out, out_dtype, (int)M, (int)N, (int)K,
+                    static_cast<hipStream_t>(stream));
+  SL8_CHECK_LAUNCH("gemm_q6k");
+  return SL8_OK;
+}
+
+extern "C" int sl8_gemm_decode_q5k(const int8_t* x, const float* x_scale, const uint8_t* w,
+                                   void* out, int out_dtype, int64_t M, int64_t N, int64_t K,
+                                   void* stream) {
+  clear_error();
+  int rc = check_kq("gemm_decode_q5k", x, x_scale, w, out, out_dtype, M, N, K);
+  if (rc != SL8_OK || M == 0 || N == 0 || K == 0) return rc;
+  SL8_CHECK_ARG(M <= 16, "gemm_decode_q5k supports M<=16, got M=%lld -- use the tile gemm_q5k for prefill",
+                (long long)M);
+  launch_kq_tile<5>(x, x_scale, w, out, out_dtype, (int)M, (int)N, (int)K,
+                    static_cast<hipStream_t>(stream));
+  SL8_CHECK_LAUNCH("gemm_decode_q5k");
+  return SL8_OK;
+}
+
+extern "C" int sl8_gemm_decode_q6k(const int8_t* x, const float* x_scale, const uint8_t* w,
+                                   void* out, int out_dtype, int64_t M, int64_t N, int64_t K,
+                                   void* stream) {
+  clear_error();
+  int rc = check_kq("gemm_decode_q6k", x, x_scale, w, out, out_dtype, M, N, K);
+  if (rc != SL8_OK || M == 0 || N == 0 || K == 0) return rc;
+  SL8_CHECK_ARG(M <= 16, "gemm_decode_q6k supports M<=16, got M=%lld -- use the tile gemm_q6k for prefill",
+                (long long)M);
+  launch_kq_tile<6>(x, x_scale, w, out, out_dtype, (int)M, (int)N, (int)K,
+                    static_cast<hipStream_t>(stream));
+  SL8_CHECK_LAUNCH("gemm_decode_q6k");
+  return SL8_OK;
+}
+
+extern "C" int sl8_dequant_q5k(const uint8_t* w, float* out, int64_t N, int64_t K, void* stream) {
+  clear_error();
+  SL8_CHECK_ARG(N >= 0 && K >= 0 && K % 256 == 0, "dequant_q5k needs K%%256==0, got %lld", (long long)K);
+  if (N == 0 || K == 0) return SL8_OK;
+  SL8_CHECK_ARG(w && out && aligned(w, 4), "dequant_q5k: null or misaligned pointer");
+  const int64_t total = N * (K / 32);
+  dequant_q5k_kernel<<<(unsigned)((total + 255) / 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      w, out, N, (int)K);
+  SL8_CHECK_LAUNCH("dequant_q5k");
+  return SL8_OK;
+}
+
+extern "C" int sl8_dequant_q6k(const uint8_t* w, float* out, int64_t N, int64_t K, void* stream) {
+  clear_error();
+  SL8_CHECK_ARG(N >= 0 && K >= 0 && K % 256 == 0, "dequant_q6k needs K%%256==0, got %lld", (long long)K);
+  if (N == 0 || K == 0) return SL8_OK;
+  SL8_CHECK_ARG(w && out, "dequant_q6k: null pointer");
+  const int64_t total = N * (K / 16);
+  dequant_q6k_kernel<<<(unsigned)((total + 255) / 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      w, out, N, (int)K);
+  SL8_CHECK_LAUNCH("dequant_q6k");
+  return SL8_OK;
+}

@@ -29,7 +29,7 @@
 // and reduce through LDS in a fixed order (deterministic output). The x
 // sub-block sums each wave needs are formed in its own LDS slice.
 
-#include "common.hpp"
+#include "kquant.hpp"
 
 namespace sl8 {
 namespace {
@@ -40,19 +40,6 @@ constexpr int Q4K_BYTES = 144;
 constexpr int GEMV_ROWS = 16;
 constexpr int XS_MPAD = 16;  // xsum LDS row pitch (activation rows)
 
-// Packed 6-bit sub-scales / mins of one super-block (4 per dword, byte j%4).
-struct ScMin {
-  uint32_t sc_lo, sc_hi, mn_lo, mn_hi;
-};
-__device__ __forceinline__ ScMin unpack_scmin(uint32_t s0, uint32_t s1, uint32_t s2) {
-  ScMin r;
-  r.sc_lo = s0 & 0x3F3F3F3Fu;
-  r.mn_lo = s1 & 0x3F3F3F3Fu;
-  r.sc_hi = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
-  r.mn_hi = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
-  return r;
-}
-__device__ __forceinline__ int byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xFF; }
 
 // Work split: a workgroup = one 16-row MFMA tile = 4 waves, each wave taking
 // one quarter of the super-blocks of K (in chunks of up to GCH); partial

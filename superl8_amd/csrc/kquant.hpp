@@ -1,0 +1,26 @@
+// Shared pieces of the GGUF k-quant kernels (Q4_K, Q5_K, Q6_K).
+#pragma once
+
+#include "common.hpp"
+
+namespace sl8 {
+
+// Packed 6-bit sub-scales / mins of a Q4_K / Q5_K super-block (4 per dword,
+// byte j % 4), unpacked from the 12-byte get_scale_min_k4 layout.
+struct ScMin {
+  uint32_t sc_lo, sc_hi, mn_lo, mn_hi;
+};
+__device__ __forceinline__ ScMin unpack_scmin(uint32_t s0, uint32_t s1, uint32_t s2) {
+  ScMin r;
+  r.sc_lo = s0 & 0x3F3F3F3Fu;
+  r.mn_lo = s1 & 0x3F3F3F3Fu;
+  r.sc_hi = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
+  r.mn_hi = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
+  return r;
+}
+__device__ __forceinline__ int byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xFF; }
+
+typedef __attribute__((address_space(1))) const void* kq_gptr_t;
+typedef __attribute__((address_space(3))) void* kq_lptr_t;
+
+}  // namespace sl8

@@ -4,7 +4,7 @@ Same names, keyword arguments, routing and error behaviour as the reference
 wrappers (reference superl8/ops.py:70-175 attn_int8_fwd, :230-267
 attn_int8_decode, :531-584 quantize_kv_cache, :671-727 attn_decode_cached,
 :730-849 quantize_kv_write_paged / attn_paged_decode_cached,
-:975-991 quantize_i8_rowwise, :1254-1325 linear_q4k / _linear_kquant),
+:975-991 quantize_i8_rowwise, :1254-1347 linear_q4k / linear_q5k / linear_q6k / _linear_kquant),
 dispatching to the gfx950 kernels through `_C`.
 """
 from __future__ import annotations
@@ -190,6 +190,20 @@ def linear_q4k(x: torch.Tensor, w_bytes: torch.Tensor, *, bias: torch.Tensor | N
     """GGUF Q4_K linear on native 144-byte super-blocks: x [..., K] -> [..., N]."""
     return _linear_kquant(x, w_bytes, bias, out_dtype, _C.gemm_q4k,
                           getattr(_C, "gemm_decode_q4k", None))
+
+
+def linear_q5k(x: torch.Tensor, w_bytes: torch.Tensor, *, bias: torch.Tensor | None = None,
+               out_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """GGUF Q5_K linear on native 176-byte super-blocks (reference ops.py:1328-1336)."""
+    return _linear_kquant(x, w_bytes, bias, out_dtype, _C.gemm_q5k,
+                          getattr(_C, "gemm_decode_q5k", None))
+
+
+def linear_q6k(x: torch.Tensor, w_bytes: torch.Tensor, *, bias: torch.Tensor | None = None,
+               out_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """GGUF Q6_K linear on native 210-byte super-blocks (reference ops.py:1339-1347)."""
+    return _linear_kquant(x, w_bytes, bias, out_dtype, _C.gemm_q6k,
+                          getattr(_C, "gemm_decode_q6k", None))
 
 
 def _linear_kquant(x, w_bytes, bias, out_dtype, tile_op, decode_op):

@@ -11,6 +11,7 @@ import numpy as np
 import pytest
 
 from oracle import attention as oa
+from oracle import kquant as okq
 from oracle import q4k as oq
 from oracle import quant as oqn
 from tests.tolerances import assert_int8_quality
@@ -161,6 +162,116 @@ def test_q4k_gemv_matches_dequant_matmul():
     ref = (x.astype(np.float64) @ oq.dequant(w, 512).astype(np.float64).T) * xs[:, None]
     # dequant rounds d*sc*q - dmin*m to fp32 once; the oracle sums exactly
     np.testing.assert_allclose(y, ref, rtol=1e-6, atol=1e-6)
+
+
+# ---------------------------------------------------------------- Q5_K / Q6_K
+def _q5k_dequant_literal(blk):
+    """dequantize_row_q5_K as a scalar loop over one 176-byte block (llama.cpp
+    ggml-quants.c form: pairs of sub-blocks, qh bit masks u1/u2 shifted by 2)."""
+    d = float(np.frombuffer(blk[0:2].tobytes(), np.float16)[0])
+    dmin = float(np.frombuffer(blk[2:4].tobytes(), np.float16)[0])
+    s = [int(b) for b in blk[4:16]]
+    qh, ql = blk[16:48], blk[48:176]
+    y, u1, u2, is_ = [], 1, 2, 0
+    for g in range(4):
+        sc1, m1 = _scale_min_literal(s, is_)
+        sc2, m2 = _scale_min_literal(s, is_ + 1)
+        d1, mm1 = np.float32(d) * np.float32(sc1), np.float32(dmin) * np.float32(m1)
+        d2, mm2 = np.float32(d) * np.float32(sc2), np.float32(dmin) * np.float32(m2)
+        for l in range(32):
+            y.append(d1 * np.float32((ql[32 * g + l] & 0xF) + (16 if qh[l] & u1 else 0)) - mm1)
+        for l in range(32):
+            y.append(d2 * np.float32((ql[32 * g + l] >> 4) + (16 if qh[l] & u2 else 0)) - mm2)
+        is_ += 2
+        u1 <<= 2
+        u2 <<= 2
+    return np.array(y, np.float32)
+
+
+def _q6k_dequant_literal(blk):
+    """dequantize_row_q6_K as a scalar loop over one 210-byte block (llama.cpp form:
+    two halves of 128, four outputs per l, pointers advanced by 64/32/8)."""
+    d = np.float32(np.frombuffer(blk[208:210].tobytes(), np.float16)[0])
+    sc = blk[192:208].view(np.int8)
+    y = np.zeros(256, np.float32)
+    for n in range(2):
+        ql, qh, s = blk[64 * n:64 * n + 64], blk[128 + 32 * n:160 + 32 * n], sc[8 * n:8 * n + 8]
+        for l in range(32):
+            is_ = l // 16
+            q1 = int((ql[l] & 0xF) | ((qh[l] & 3) << 4)) - 32
+            q2 = int((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32
+            q3 = int((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32
+            q4 = int((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32
+            for off, qq, si in ((0, q1, 0), (32, q2, 2), (64, q3, 4), (96, q4, 6)):
+                y[128 * n + l + off] = (d * np.float32(s[is_ + si])) * np.float32(qq)
+    return y
+
+
+def test_q5k_dequant_matches_literal_loop():
+    w = okq.q5k_random(6, 512, seed=1)
+    deq = okq.q5k_dequant(w, 512)
+    for r in range(6):
+        for b in range(2):
+            np.testing.assert_array_equal(
+                deq[r, 256 * b:256 * b + 256], _q5k_dequant_literal(w[r, 176 * b:176 * b + 176]))
+
+
+def test_q6k_dequant_matches_literal_loop():
+    w = okq.q6k_random(6, 512, seed=2)
+    deq = okq.q6k_dequant(w, 512)
+    for r in range(6):
+        for b in range(2):
+            np.testing.assert_array_equal(
+                deq[r, 256 * b:256 * b + 256], _q6k_dequant_literal(w[r, 210 * b:210 * b + 210]))
+
+
+def test_kquant_bytes_roundtrip():
+    w5 = okq.q5k_random(9, 768, seed=3)
+    np.testing.assert_array_equal(okq.q5k_make(*okq.q5k_fields(w5, 768)).reshape(w5.shape), w5)
+    w6 = okq.q6k_random(9, 768, seed=4)
+    np.testing.assert_array_equal(okq.q6k_make(*okq.q6k_fields(w6, 768)).reshape(w6.shape), w6)
+
+
+def test_q6k_code_positions():
+    """One nonzero code per quadrant lands at e = 128g + 32qd + l with scale sc[e//16]."""
+    for g, qd, l in [(0, 0, 3), (0, 1, 17), (1, 2, 31), (1, 3, 0)]:
+        q = np.full((1, 256), 32, np.uint8)
+        e = 128 * g + 32 * qd + l
+        q[0, e] = 45
+        sc = np.arange(1, 17, dtype=np.int8)[None]
+        blk = okq.q6k_make(np.array([1.0]), sc, q)
+        y = okq.q6k_dequant(blk, 256)[0]
+        assert list(np.nonzero(y)[0]) == [e]
+        assert y[e] == 13 * (e // 16 + 1)
+        np.testing.assert_array_equal(y, _q6k_dequant_literal(blk[0]))
+
+
+def test_kquant_encoders_error_ladder():
+    """Reference tests/test_gemm_q4k.py:440-448,483-496: faithful reconstructions,
+    6-bit tighter than 5-bit tighter than 4-bit."""
+    w = (RNG.standard_normal((16, 1024)) * 0.1).astype(np.float32)
+    _, d5 = okq.q5k_quantize(w)
+    _, d6 = okq.q6k_quantize(w)
+
+    def cos(a, b):
+        return float((a * b).sum() / np.sqrt((a * a).sum() * (b * b).sum()))
+
+    e5, e6 = np.abs(d5 - w).mean(), np.abs(d6 - w).mean()
+    assert cos(d5, w) > 0.99 and cos(d6, w) > 0.99
+    assert e6 < e5
+
+
+def test_kquant_gemv_matches_dequant_matmul():
+    x = RNG.integers(-127, 128, (5, 768), dtype=np.int8)
+    xs = RNG.random(5).astype(np.float32)
+    for gemv, deqf, w in ((okq.q5k_gemv, okq.q5k_dequant, okq.q5k_random(40, 768, seed=5)),
+                          (okq.q6k_gemv, okq.q6k_dequant, okq.q6k_random(40, 768, seed=6))):
+        y = gemv(x, xs, w, 768)
+        dq = deqf(w, 768).astype(np.float64)
+        ref = (x.astype(np.float64) @ dq.T) * xs[:, None]
+        # the dequantised weights carry one or two fp32 roundings each (2^-23 relative)
+        bound = (np.abs(x).astype(np.float64) @ np.abs(dq).T) * xs[:, None] * 2.0 ** -22
+        assert (np.abs(y - ref) <= bound + 1e-12).all()
 
 
 # ---------------------------------------------------------------- attention
