@@ -168,18 +168,18 @@ def bench_paged_decode(iters=20, bs=16):
     return ms, nbytes
 
 
-def bench_gemm_prefill(M=512, iters=10):
-    """Q4_K prefill GEMM (M > 16: the tiled MFMA kernel) on config 4's weights."""
-    from oracle import q4k as oq  # synthetic GGUF bytes generator (data only)
+def bench_gemm_prefill(M=512, iters=10, fmt="q4k"):
+    """k-quant prefill GEMM (M > 16: the tiled MFMA kernel) on config 4's shape."""
     from superl8_amd import _C
 
     dev = "cuda"
     N, K = 17408, 5120
-    w = torch.from_numpy(oq.random_weights(N, K, seed=4)).to(dev)
+    w = _kquant_weights(fmt, N, K, 4).to(dev)
     g = torch.Generator(device=dev).manual_seed(9)
     x = torch.randn(M, K, device=dev, dtype=torch.float16, generator=g)
     x_i8, xs = _C.quantize_i8_rowwise(x)
-    fn = lambda: _C.gemm_q4k(x_i8, xs, w)  # noqa: E731
+    op = getattr(_C, f"gemm_{fmt}")
+    fn = lambda: op(x_i8, xs, w)  # noqa: E731
     spin_up(fn, 0.1)
     ms = _events_time(fn, iters, torch.cuda.current_stream())
     return ms, 2 * M * N * K
@@ -240,19 +240,31 @@ def bench_w8a8(iters=5):
     return ms, ops
 
 
-def bench_gemv(M, iters_graph=10, copies=8):
-    from oracle import q4k as oq  # synthetic GGUF bytes generator (data only)
+def _kquant_weights(fmt, N, K, seed):
+    """Synthetic native GGUF bytes (data generators only; nothing here is measured)."""
+    from oracle import kquant as okq
+    from oracle import q4k as oq
+
+    gen = {"q4k": oq.random_weights, "q5k": okq.q5k_random, "q6k": okq.q6k_random}[fmt]
+    return torch.from_numpy(gen(N, K, seed=seed))
+
+
+KQ_BYTES = {"q4k": 144, "q5k": 176, "q6k": 210}
+
+
+def bench_gemv(M, iters_graph=10, copies=8, fmt="q4k"):
     from superl8_amd import _C
 
     dev = "cuda"
     N, K = 17408, 5120
-    base = torch.from_numpy(oq.random_weights(N, K, seed=4)).to(dev)
+    op = getattr(_C, f"gemm_decode_{fmt}")
+    base = _kquant_weights(fmt, N, K, 4).to(dev)
     ws = [base] + [base.roll(i * 1, 0).contiguous() for i in range(1, copies)]  # > 256 MB MALL
     g = torch.Generator(device=dev).manual_seed(5)
     x = torch.randn(M, K, device=dev, dtype=torch.float16, generator=g)
     x_i8, xs = _C.quantize_i8_rowwise(x)
     for w in ws:
-        _C.gemm_decode_q4k(x_i8, xs, w)
+        op(x_i8, xs, w)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     s = torch.cuda.Stream()
@@ -260,13 +272,13 @@ def bench_gemv(M, iters_graph=10, copies=8):
     with torch.cuda.stream(s):
         with torch.cuda.graph(graph, stream=s):
             for i in range(per_graph):
-                _C.gemm_decode_q4k(x_i8, xs, ws[i % copies])
+                op(x_i8, xs, ws[i % copies])
     for _ in range(2):
         graph.replay()
     torch.cuda.synchronize()
     cur = torch.cuda.current_stream()
     ms = _events_time(graph.replay, iters_graph, cur) / per_graph
-    nbytes = N * (K // 256) * 144 + M * K + M * 4 + M * N * 2
+    nbytes = N * (K // 256) * KQ_BYTES[fmt] + M * K + M * 4 + M * N * 2
     return ms, nbytes
 
 
@@ -397,6 +409,18 @@ def main():
         sec["gemm_q4k_prefill_m512_cfg4w"] = {"us": round(pms2 * 1e3, 1), "TOPS": round(pt, 1),
                                               "frac_int8_peak": round(pt / PEAK_INT8_TOPS, 4),
                                               "ops": pops}
+        for fmt in ("q5k", "q6k"):
+            for M in (1, 8):
+                gms, gbytes = bench_gemv(M, fmt=fmt)
+                gbs = gbytes / (gms * 1e-3) / 1e9
+                sec[f"gemm_decode_{fmt}_cfg4shape_m{M}"] = {
+                    "us": round(gms * 1e3, 2), "GB/s": round(gbs, 1),
+                    "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": gbytes}
+            pms2, pops = bench_gemm_prefill(fmt=fmt)
+            pt = pops / (pms2 * 1e-3) / 1e12
+            sec[f"gemm_{fmt}_prefill_m512_cfg4shape"] = {
+                "us": round(pms2 * 1e3, 1), "TOPS": round(pt, 1),
+                "frac_int8_peak": round(pt / PEAK_INT8_TOPS, 4), "ops": pops}
         fms, sms, pb = bench_prologue()
         gbs = pb / (fms * 1e-3) / 1e9
         sec["prologue_quantize_qk_gate_cfg2"] = {"us": round(fms * 1e3, 2), "GB/s": round(gbs, 1),

@@ -10,7 +10,7 @@
 //         sc_i signed int8.
 // x is the per-row int8 activation with its fp32 scale.
 //
-// Tile GEMM (any M; used for M > 16): a 128 x 128 output tile per workgroup,
+// Tile GEMM (M > 16; the decode GEMV below serves M <= 16): a 128 x 128 output tile per workgroup,
 // 4 waves of 64 x 64 (2 x 2 blocks of 32 x 32), the x tile and the 128 weight
 // super-blocks copied global -> LDS one super-block ahead (double-buffered).
 // The integer dot products stay exact:
@@ -403,6 +403,178 @@ __global__ void dequant_q6k_kernel(const uint8_t* __restrict__ w, float* __restr
   }
 }
 
+// ---------------------------------------------------------------------------
+// Decode GEMV (M <= 16): one wave per weight row, the lanes over units of 64
+// weights (4 per super-block: Q5_K sub-block pair g, Q6_K half g x ql column
+// p), the dot products on VALU v_dot4 in registers; a fixed-order wave
+// reduction keeps the output deterministic. Q6_K fields start on 2-byte
+// boundaries: they are read as dword-aligned loads and v_alignbyte.
+// ---------------------------------------------------------------------------
+typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));
+
+__device__ __forceinline__ void load_x64(const int8_t* p, uint32_t (&v)[16]) {
+  // 64 int8 at a 64-byte aligned address, as 16 dwords
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint4 t = reinterpret_cast<const uint4*>(p)[i];
+    v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+  }
+}
+
+// 8 dwords starting at a 2-byte aligned global address (9 aligned dwords + v_alignbyte)
+__device__ __forceinline__ void load8_a2(const uint8_t* p, uint32_t (&o)[8]) {
+  const uintptr_t ad = reinterpret_cast<uintptr_t>(p);
+  const uint32_t* a = reinterpret_cast<const uint32_t*>(ad & ~(uintptr_t)3);
+  const uint32_t sh = (uint32_t)(ad & 3);
+  const u32x4a d0 = *reinterpret_cast<const u32x4a*>(a);
+  const u32x4a d1 = *reinterpret_cast<const u32x4a*>(a + 4);
+  const uint32_t d8 = a[8];
+  const uint32_t d[9] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w, d8};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = __builtin_amdgcn_alignbyte(d[e + 1], d[e], sh);
+}
+
+template <int FMT, int OUT_DT, int MR>
+__global__ void __launch_bounds__(256)
+gemv_kq_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
+               const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K) {
+  constexpr int BS = FMT == 5 ? Q5K_BYTES : Q6K_BYTES;
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= N) return;  // wave-uniform
+  const int nsb = K >> 8, nu = 4 * nsb;
+  const uint8_t* wr = w + (int64_t)n * nsb * BS;
+  float f[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) f[m] = 0.f;
+
+  for (int u = lane; u < nu; u += 64) {
+    const int sb = u >> 2, g = u & 3;
+    const uint8_t* blk = wr + (int64_t)sb * BS;
+    if constexpr (FMT == 5) {
+      // sub-blocks j0 = 2g (low nibbles) and j1 = 2g + 1 (high nibbles)
+      const uint4 hd = *reinterpret_cast<const uint4*>(blk);
+      const uint4 qh0 = *reinterpret_cast<const uint4*>(blk + 16);
+      const uint4 qh1 = *reinterpret_cast<const uint4*>(blk + 32);
+      const uint4 qs0 = *reinterpret_cast<const uint4*>(blk + 48 + 32 * g);
+      const uint4 qs1 = *reinterpret_cast<const uint4*>(blk + 64 + 32 * g);
+      const float d = h2f(hd.x & 0xFFFFu), dmin = h2f(hd.x >> 16);
+      const ScMin sm = unpack_scmin(hd.y, hd.z, hd.w);
+      const int j0 = 2 * g, j1 = j0 + 1;
+      const uint32_t scw = g < 2 ? sm.sc_lo : sm.sc_hi, mnw = g < 2 ? sm.mn_lo : sm.mn_hi;
+      const int sc0 = byte_of(scw, j0 & 3), sc1 = byte_of(scw, j1 & 3);
+      const int mn0 = byte_of(mnw, j0 & 3), mn1 = byte_of(mnw, j1 & 3);
+      const uint32_t qs[8] = {qs0.x, qs0.y, qs0.z, qs0.w, qs1.x, qs1.y, qs1.z, qs1.w};
+      const uint32_t qh[8] = {qh0.x, qh0.y, qh0.z, qh0.w, qh1.x, qh1.y, qh1.z, qh1.w};
+      uint32_t c0[8], c1[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        c0[e] = (qs[e] & 0x0F0F0F0Fu) | (((qh[e] >> j0) & 0x01010101u) << 4);
+        c1[e] = ((qs[e] >> 4) & 0x0F0F0F0Fu) | (((qh[e] >> j1) & 0x01010101u) << 4);
+      }
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        if (m < M) {
+          uint32_t xv[16];
+          load_x64(x + (int64_t)m * K + (int64_t)sb * 256 + 64 * g, xv);
+          int s0 = 0, s1 = 0, x0 = 0, x1 = 0;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            s0 = __builtin_amdgcn_sdot4((int)xv[e], (int)c0[e], s0, false);
+            x0 = __builtin_amdgcn_sdot4((int)xv[e], 0x01010101, x0, false);
+            s1 = __builtin_amdgcn_sdot4((int)xv[8 + e], (int)c1[e], s1, false);
+            x1 = __builtin_amdgcn_sdot4((int)xv[8 + e], 0x01010101, x1, false);
+          }
+          f[m] += d * (float)(sc0 * s0 + sc1 * s1) - dmin * (float)(mn0 * x0 + mn1 * x1);
+        }
+      }
+    } else {
+      // half hf = g >> 1, ql column p = g & 1: quadrants qd = p (low nibbles)
+      // and p + 2 (high nibbles), l = 0..31 each
+      const int hf = g >> 1, p = g & 1;
+      uint32_t ql[8], qh[8];
+      load8_a2(blk + 64 * hf + 32 * p, ql);
+      load8_a2(blk + 128 + 32 * hf, qh);
+      const uintptr_t sa = reinterpret_cast<uintptr_t>(blk + 192 + 8 * hf);
+      const uint32_t* sp = reinterpret_cast<const uint32_t*>(sa & ~(uintptr_t)3);
+      const uint32_t ssh = (uint32_t)(sa & 3);
+      const uint32_t s0w = __builtin_amdgcn_alignbyte(sp[1], sp[0], ssh);  // scales 8hf + 0..3
+      const uint32_t s1w = __builtin_amdgcn_alignbyte(sp[2], sp[1], ssh);  // scales 8hf + 4..7
+      const uintptr_t da = reinterpret_cast<uintptr_t>(blk + 208);
+      const uint32_t dw = *reinterpret_cast<const uint32_t*>(da & ~(uintptr_t)3);
+      const float d = h2f((uint16_t)((da & 3) ? (dw >> 16) : (dw & 0xFFFFu)));
+      int sc[2][2];  // [quadrant p / p + 2][16-element half]
+      sc[0][0] = (int)(int8_t)byte_of(s0w, 2 * p);
+      sc[0][1] = (int)(int8_t)byte_of(s0w, 2 * p + 1);
+      sc[1][0] = (int)(int8_t)byte_of(s1w, 2 * p);
+      sc[1][1] = (int)(int8_t)byte_of(s1w, 2 * p + 1);
+      uint32_t v[2][8];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int qd = p + 2 * k;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t q = ((ql[e] >> (4 * k)) & 0x0F0F0F0Fu) | (((qh[e] >> (2 * qd)) & 0x03030303u) << 4);
+          const uint32_t t = q ^ 0x20202020u;                  // 6-bit two's complement of q - 32
+          v[k][e] = t | ((t & 0x20202020u) * 6u);              // sign-extended to 8 bits
+        }
+      }
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        if (m < M) {
+          const int8_t* xb = x + (int64_t)m * K + (int64_t)sb * 256 + 128 * hf + 32 * p;
+          int T = 0;
+#pragma unroll
+          for (int k = 0; k < 2; ++k) {
+            const uint4 xa = *reinterpret_cast<const uint4*>(xb + 64 * k);
+            const uint4 xc = *reinterpret_cast<const uint4*>(xb + 64 * k + 16);
+            const uint32_t xv[8] = {xa.x, xa.y, xa.z, xa.w, xc.x, xc.y, xc.z, xc.w};
+            int s0 = 0, s1 = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              s0 = __builtin_amdgcn_sdot4((int)xv[e], (int)v[k][e], s0, false);
+              s1 = __builtin_amdgcn_sdot4((int)xv[4 + e], (int)v[k][4 + e], s1, false);
+            }
+            T += sc[k][0] * s0 + sc[k][1] * s1;
+          }
+          f[m] += d * (float)T;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) f[m] += __shfl_xor(f[m], o, 64);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+      if (m < M) st_out<OUT_DT>(out, (int64_t)m * N + n, f[m] * x_scale[m]);
+  }
+}
+
+template <int FMT, int MR>
+void launch_gemv_kq_m(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
+                      int M, int N, int K, hipStream_t st) {
+  const dim3 grid((unsigned)((N + 3) / 4));
+  switch (odt) {
+    case SL8_DTYPE_F16: gemv_kq_kernel<FMT, SL8_DTYPE_F16, MR><<<grid, 256, 0, st>>>(x, xs, w, out, M, N, K); break;
+    case SL8_DTYPE_BF16: gemv_kq_kernel<FMT, SL8_DTYPE_BF16, MR><<<grid, 256, 0, st>>>(x, xs, w, out, M, N, K); break;
+    default: gemv_kq_kernel<FMT, SL8_DTYPE_F32, MR><<<grid, 256, 0, st>>>(x, xs, w, out, M, N, K); break;
+  }
+}
+
+template <int FMT>
+void launch_gemv_kq(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
+                    int M, int N, int K, hipStream_t st) {
+  if (M == 1) launch_gemv_kq_m<FMT, 1>(x, xs, w, out, odt, M, N, K, st);
+  else if (M == 2) launch_gemv_kq_m<FMT, 2>(x, xs, w, out, odt, M, N, K, st);
+  else if (M <= 4) launch_gemv_kq_m<FMT, 4>(x, xs, w, out, odt, M, N, K, st);
+  else if (M <= 8) launch_gemv_kq_m<FMT, 8>(x, xs, w, out, odt, M, N, K, st);
+  else launch_gemv_kq_m<FMT, 16>(x, xs, w, out, odt, M, N, K, st);
+}
+
 template <int FMT>
 void launch_kq_tile(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
                     int M, int N, int K, hipStream_t st) {
@@ -444,7 +616,9 @@ extern "C" int sl8_gemm_q5k(const int8_t* x, const float* x_scale, const uint8_t
   clear_error();
   int rc = check_kq("gemm_q5k", x, x_scale, w, out, out_dtype, M, N, K);
   if (rc != SL8_OK || M == 0 || N == 0 || K == 0) return rc;
-  launch_kq_tile<5>(x, x_scale, w, out, out_dtype, (int)M, (int)N, (int)K,
+  if (M <= 16) launch_gemv_kq<5>(x, x_scale, w, out, out_dtype, (int)M, (int)N, (int)K,
+                                 static_cast<hipStream_t>(stream));
+  else launch_kq_tile<5>(x, x_scale, w, out, out_dtype, (int)M, (int)N, (int)K,
                     static_cast<hipStream_t>(stream));
   SL8_CHECK_LAUNCH("gemm_q5k");
   return SL8_OK;
@@ -455,7 +629,9 @@ extern "C" int sl8_gemm_q6k(const int8_t* x, const float* x_scale, const uint8_t
   clear_error();
   int rc = check_kq("gemm_q6k", x, x_scale, w, out, out_dtype, M, N, K);
   if (rc != SL8_OK || M == 0 || N == 0 || K == 0) return rc;
-  launch_kq_tile<6>(x, x_scale, w, out, out_dtype, (int)M, (int)N, (int)K,
+  if (M <= 16) launch_gemv_kq<6>(x, x_scale, w, out, out_dtype, (int)M, (int)N, (int)K,
+                                 static_cast<hipStream_t>(stream));
+  else launch_kq_tile<6>(x, x_scale, w, out, out_dtype, (int)M, (int)N, (int)K,
                     static_cast<hipStream_t>(stream));
   SL8_CHECK_LAUNCH("gemm_q6k");
   return SL8_OK;
@@ -469,7 +645,7 @@ extern "C" int sl8_gemm_decode_q5k(const int8_t* x, const float* x_scale, const 
   if (rc != SL8_OK || M == 0 || N == 0 || K == 0) return rc;
   SL8_CHECK_ARG(M <= 16, "gemm_decode_q5k supports M<=16, got M=%lld -- use the tile gemm_q5k for prefill",
                 (long long)M);
-  launch_kq_tile<5>(x, x_scale, w, out, out_dtype, (int)M, (int)N, (int)K,
+  launch_gemv_kq<5>(x, x_scale, w, out, out_dtype, (int)M, (int)N, (int)K,
                     static_cast<hipStream_t>(stream));
   SL8_CHECK_LAUNCH("gemm_decode_q5k");
   return SL8_OK;
@@ -483,7 +659,7 @@ extern "C" int sl8_gemm_decode_q6k(const int8_t* x, const float* x_scale, const 
   if (rc != SL8_OK || M == 0 || N == 0 || K == 0) return rc;
   SL8_CHECK_ARG(M <= 16, "gemm_decode_q6k supports M<=16, got M=%lld -- use the tile gemm_q6k for prefill",
                 (long long)M);
-  launch_kq_tile<6>(x, x_scale, w, out, out_dtype, (int)M, (int)N, (int)K,
+  launch_gemv_kq<6>(x, x_scale, w, out, out_dtype, (int)M, (int)N, (int)K,
                     static_cast<hipStream_t>(stream));
   SL8_CHECK_LAUNCH("gemm_decode_q6k");
   return SL8_OK;
