@@ -62,31 +62,32 @@ __device__ __forceinline__ void copy_x_tile(const int8_t* x, int8_t* xd, int m0,
   }
 }
 
-// 8 int8 -> 8 fp16 (exact): byte u = x + 128 becomes fp16 bits 0x64uu = 1024 + u.
-__device__ __forceinline__ v8h_t i8x8_to_h(uint2 w) {
-  const uint32_t a = w.x ^ 0x80808080u, b = w.y ^ 0x80808080u;
-  uint32_t r[4] = {__builtin_amdgcn_perm(0x64646464u, a, 0x04010400u),
-                   __builtin_amdgcn_perm(0x64646464u, a, 0x04030402u),
-                   __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u),
-                   __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u)};
-  v8h_t v = __builtin_bit_cast(v8h_t, r);
-  const _Float16 off = (_Float16)1152.0f;
+// Four bytes b (as two dwords' halves) -> fp16 1024 + b, packed two per dword.
+struct H4x2 {
+  v2h_t p[4];
+};
+__device__ __forceinline__ H4x2 bytes8_to_h1024(uint32_t a, uint32_t b) {
+  H4x2 r;
+  r.p[0] = __builtin_bit_cast(v2h_t, __builtin_amdgcn_perm(0x64646464u, a, 0x04010400u));
+  r.p[1] = __builtin_bit_cast(v2h_t, __builtin_amdgcn_perm(0x64646464u, a, 0x04030402u));
+  r.p[2] = __builtin_bit_cast(v2h_t, __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u));
+  r.p[3] = __builtin_bit_cast(v2h_t, __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u));
+  return r;
+}
+__device__ __forceinline__ v8h_t h4x2_to_v8(const H4x2& h) {
+  uint32_t u[4];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) v[e] -= off;
-  return v;
+  for (int i = 0; i < 4; ++i) u[i] = __builtin_bit_cast(uint32_t, h.p[i]);
+  return __builtin_bit_cast(v8h_t, u);
 }
 
-// 8 codes (bytes, 0..63) -> 8 fp16 of (q - 32) (exact).
-__device__ __forceinline__ v8h_t q6x8_to_h(uint32_t a, uint32_t b) {
-  uint32_t r[4] = {__builtin_amdgcn_perm(0x64646464u, a, 0x04010400u),
-                   __builtin_amdgcn_perm(0x64646464u, a, 0x04030402u),
-                   __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u),
-                   __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u)};
-  v8h_t v = __builtin_bit_cast(v8h_t, r);
-  const _Float16 off = (_Float16)1056.0f;
+// 8 int8 -> 8 fp16 (exact): byte u = x + 128 becomes fp16 bits 0x64uu = 1024 + u.
+__device__ __forceinline__ v8h_t i8x8_to_h(uint2 w) {
+  H4x2 h = bytes8_to_h1024(w.x ^ 0x80808080u, w.y ^ 0x80808080u);
+  const v2h_t off = {(_Float16)1152.0f, (_Float16)1152.0f};
 #pragma unroll
-  for (int e = 0; e < 8; ++e) v[e] -= off;
-  return v;
+  for (int i = 0; i < 4; ++i) h.p[i] = h.p[i] - off;  // v_pk_add_f16
+  return h4x2_to_v8(h);
 }
 
 // ---------------------------------------------------------------------------
@@ -247,15 +248,19 @@ gemm_q6k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
     copy_x_tile(x, xd, m0, M, K, sb, tid, wave);
     // dword P = 256 i + tid of the tile is dword c of row P / 53; walked as a
     // recurrence (256 = 4 * 53 + 44) so no per-i row address stays live
+    // offsets are 32-bit from the workgroup's (uniform) row-n0 base: 128 rows of
+    // < 2^24 bytes each
     int t0 = tid;
     asm volatile("" : "+v"(t0));  // keep the walk inside the super-block loop (no hoisted addresses)
     int row = t0 / Q6DW, c = t0 - Q6DW * (t0 / Q6DW);
-    const int64_t sboff = (int64_t)sb * Q6K_BYTES;
+    const uint8_t* wbase = w + (int64_t)n0 * row_bytes;
+    const uint32_t rb32 = (uint32_t)row_bytes, sboff = (uint32_t)sb * Q6K_BYTES;
+    const int rmax = min(KBN, N - n0) - 1;
 #pragma unroll
     for (int i = 0; i < (T6DW - 64) / 256; ++i) {
-      const int64_t base = (int64_t)min(n0 + min(row, KBN - 1), N - 1) * row_bytes + sboff;
-      const uint8_t* src = w + (base & ~(int64_t)3) + 4 * (row < KBN ? c : Q6DW - 1);
-      __builtin_amdgcn_global_load_lds((kq_gptr_t)src, (kq_lptr_t)(wd + i * 256 + wave * 64), 4, 0, 0);
+      const uint32_t base = (uint32_t)min(row, rmax) * rb32 + sboff;
+      const uint32_t off = (base & ~3u) + 4u * (uint32_t)(row < KBN ? c : Q6DW - 1);
+      __builtin_amdgcn_global_load_lds((kq_gptr_t)(wbase + off), (kq_lptr_t)(wd + i * 256 + wave * 64), 4, 0, 0);
       c += 44;
       row += 4;
       if (c >= Q6DW) { c -= Q6DW; ++row; }
@@ -277,8 +282,11 @@ gemm_q6k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
       const int r = 64 * wn + 32 * cb + l32;
-      const int64_t base = (int64_t)min(n0 + r, N - 1) * row_bytes + (int64_t)sb * Q6K_BYTES;
-      blk[cb] = reinterpret_cast<const uint8_t*>(wt) + r * Q6PITCH + (int)(base & 3);
+      // n0 * row_bytes is a multiple of 4 (n0 of 128, row_bytes even): the
+      // block's misalignment is that of its offset from the row-n0 base
+      const uint32_t base = (uint32_t)min(r, min(KBN, N - n0) - 1) * (uint32_t)row_bytes +
+                            (uint32_t)sb * Q6K_BYTES;
+      blk[cb] = reinterpret_cast<const uint8_t*>(wt) + r * Q6PITCH + (int)(base & 3u);
       const uint2 s0 = lds8_at(blk[cb] + 192), s1 = lds8_at(blk[cb] + 200);
       scw[cb][0] = s0.x; scw[cb][1] = s0.y; scw[cb][2] = s1.x; scw[cb][3] = s1.y;
       dcb[cb] = h2f((uint16_t)(lds8_at(blk[cb] + 208).x & 0xFFFFu));
@@ -304,13 +312,20 @@ gemm_q6k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
             const int ns = 4 * (qd >> 1), hs = 2 * qd;
             const uint32_t c0 = ((ql.x >> ns) & 0x0F0F0F0Fu) | (((qhc.x >> hs) & 0x03030303u) << 4);
             const uint32_t c1 = ((ql.y >> ns) & 0x0F0F0F0Fu) | (((qhc.y >> hs) & 0x03030303u) << 4);
-            const v8h_t v = q6x8_to_h(c0, c1);
+            H4x2 v = bytes8_to_h1024(c0, c1);  // 1024 + q
             const uint32_t sw = g ? scw[cb][2 + (qd >> 1)] : scw[cb][qd >> 1];  // scales 4(i>>2)..
             const int sc = (int)(int8_t)((sw >> (8 * (2 * (qd & 1) + ih))) & 0xFF);
             const _Float16 slo = (_Float16)(float)(sc & 15), shi = (_Float16)(float)(sc >> 4);
-            v8h_t blo, bhi;
+            const v2h_t slo2 = {slo, slo}, shi2 = {shi, shi};
+            const v2h_t off = {(_Float16)1056.0f, (_Float16)1056.0f};
+            H4x2 lo, hi;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) { blo[e] = v[e] * slo; bhi[e] = v[e] * shi; }
+            for (int k = 0; k < 4; ++k) {
+              const v2h_t q = v.p[k] - off;  // q - 32, exact
+              lo.p[k] = q * slo2;            // v_pk_mul_f16, exact (|.| <= 480)
+              hi.p[k] = q * shi2;
+            }
+            const v8h_t blo = h4x2_to_v8(lo), bhi = h4x2_to_v8(hi);
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb) {
               const int row = 64 * wm + 32 * rb + l32;
@@ -404,22 +419,14 @@ __global__ void dequant_q6k_kernel(const uint8_t* __restrict__ w, float* __restr
 }
 
 // ---------------------------------------------------------------------------
-// Decode GEMV (M <= 16): one wave per weight row, the lanes over units of 64
-// weights (4 per super-block: Q5_K sub-block pair g, Q6_K half g x ql column
-// p), the dot products on VALU v_dot4 in registers; a fixed-order wave
-// reduction keeps the output deterministic. Q6_K fields start on 2-byte
+// Decode GEMV (M <= 16): one wave per weight row (two rows from M = 4 on,
+// sharing every activation load), the lanes over units of 64 weights (4 per
+// super-block: Q5_K sub-block pair g, Q6_K half g >> 1 x ql column g & 1),
+// the dot products on VALU v_dot4 in registers; a fixed-order wave reduction
+// keeps the output deterministic. Q6_K fields start on 2-byte
 // boundaries: they are read as dword-aligned loads and v_alignbyte.
 // ---------------------------------------------------------------------------
 typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));
-
-__device__ __forceinline__ void load_x64(const int8_t* p, uint32_t (&v)[16]) {
-  // 64 int8 at a 64-byte aligned address, as 16 dwords
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint4 t = reinterpret_cast<const uint4*>(p)[i];
-    v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
-  }
-}
 
 // 8 dwords starting at a 2-byte aligned global address (9 aligned dwords + v_alignbyte)
 __device__ __forceinline__ void load8_a2(const uint8_t* p, uint32_t (&o)[8]) {
@@ -434,134 +441,180 @@ __device__ __forceinline__ void load8_a2(const uint8_t* p, uint32_t (&o)[8]) {
   for (int e = 0; e < 8; ++e) o[e] = __builtin_amdgcn_alignbyte(d[e + 1], d[e], sh);
 }
 
-template <int FMT, int OUT_DT, int MR>
+// The 64 weights of one unit, unpacked (codes as int8 lanes of dwords) with
+// their scales.
+template <int FMT> struct UnitCodes;
+template <> struct UnitCodes<5> {
+  uint32_t c[2][8];       // sub-blocks 2g, 2g + 1: codes 0..31
+  int sc[2], mn[2];
+  float d, dmin;
+};
+template <> struct UnitCodes<6> {
+  uint32_t c[2][8];       // quadrants p, p + 2: q - 32 as int8
+  int sc[2][2];           // [quadrant][16-element half]
+  float d;
+};
+
+__device__ __forceinline__ void unit_codes(const uint8_t* blk, int g, UnitCodes<5>& u) {
+  // sub-blocks j0 = 2g (low nibbles) and j1 = 2g + 1 (high nibbles)
+  const uint4 hd = *reinterpret_cast<const uint4*>(blk);
+  const uint4 qh0 = *reinterpret_cast<const uint4*>(blk + 16);
+  const uint4 qh1 = *reinterpret_cast<const uint4*>(blk + 32);
+  const uint4 qs0 = *reinterpret_cast<const uint4*>(blk + 48 + 32 * g);
+  const uint4 qs1 = *reinterpret_cast<const uint4*>(blk + 64 + 32 * g);
+  u.d = h2f(hd.x & 0xFFFFu);
+  u.dmin = h2f(hd.x >> 16);
+  const ScMin sm = unpack_scmin(hd.y, hd.z, hd.w);
+  const int j0 = 2 * g, j1 = j0 + 1;
+  const uint32_t scw = g < 2 ? sm.sc_lo : sm.sc_hi, mnw = g < 2 ? sm.mn_lo : sm.mn_hi;
+  u.sc[0] = byte_of(scw, j0 & 3);
+  u.sc[1] = byte_of(scw, j1 & 3);
+  u.mn[0] = byte_of(mnw, j0 & 3);
+  u.mn[1] = byte_of(mnw, j1 & 3);
+  const uint32_t qs[8] = {qs0.x, qs0.y, qs0.z, qs0.w, qs1.x, qs1.y, qs1.z, qs1.w};
+  const uint32_t qh[8] = {qh0.x, qh0.y, qh0.z, qh0.w, qh1.x, qh1.y, qh1.z, qh1.w};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    u.c[0][e] = (qs[e] & 0x0F0F0F0Fu) | (((qh[e] >> j0) & 0x01010101u) << 4);
+    u.c[1][e] = ((qs[e] >> 4) & 0x0F0F0F0Fu) | (((qh[e] >> j1) & 0x01010101u) << 4);
+  }
+}
+
+__device__ __forceinline__ void unit_codes(const uint8_t* blk, int g, UnitCodes<6>& u) {
+  // half hf = g >> 1, ql column p = g & 1: quadrants qd = p (low nibbles)
+  // and p + 2 (high nibbles), l = 0..31 each
+  const int hf = g >> 1, p = g & 1;
+  uint32_t ql[8], qh[8];
+  load8_a2(blk + 64 * hf + 32 * p, ql);
+  load8_a2(blk + 128 + 32 * hf, qh);
+  const uintptr_t sa = reinterpret_cast<uintptr_t>(blk + 192 + 8 * hf);
+  const uint32_t* sp = reinterpret_cast<const uint32_t*>(sa & ~(uintptr_t)3);
+  const uint32_t ssh = (uint32_t)(sa & 3);
+  const uint32_t s0w = __builtin_amdgcn_alignbyte(sp[1], sp[0], ssh);  // scales 8hf + 0..3
+  const uint32_t s1w = __builtin_amdgcn_alignbyte(sp[2], sp[1], ssh);  // scales 8hf + 4..7
+  const uintptr_t da = reinterpret_cast<uintptr_t>(blk + 208);
+  const uint32_t dw = *reinterpret_cast<const uint32_t*>(da & ~(uintptr_t)3);
+  u.d = h2f((uint16_t)((da & 3) ? (dw >> 16) : (dw & 0xFFFFu)));
+  u.sc[0][0] = (int)(int8_t)byte_of(s0w, 2 * p);
+  u.sc[0][1] = (int)(int8_t)byte_of(s0w, 2 * p + 1);
+  u.sc[1][0] = (int)(int8_t)byte_of(s1w, 2 * p);
+  u.sc[1][1] = (int)(int8_t)byte_of(s1w, 2 * p + 1);
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int qd = p + 2 * k;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t q = ((ql[e] >> (4 * k)) & 0x0F0F0F0Fu) | (((qh[e] >> (2 * qd)) & 0x03030303u) << 4);
+      const uint32_t t = q ^ 0x20202020u;                // 6-bit two's complement of q - 32
+      u.c[k][e] = t | ((t & 0x20202020u) * 6u);          // sign-extended to 8 bits
+    }
+  }
+}
+
+// The unit's 64 activations of one row: Q5_K elements 64g..64g+63 of the
+// super-block; Q6_K quadrants p and p + 2 of half g >> 1 (32 each).
+template <int FMT>
+__device__ __forceinline__ void unit_x(const int8_t* xsb, int g, uint32_t (&v)[2][8]) {
+  const int8_t* a = FMT == 5 ? xsb + 64 * g : xsb + 128 * (g >> 1) + 32 * (g & 1);
+  const int8_t* b = FMT == 5 ? a + 32 : a + 64;
+  const uint4 a0 = reinterpret_cast<const uint4*>(a)[0], a1 = reinterpret_cast<const uint4*>(a)[1];
+  const uint4 b0 = reinterpret_cast<const uint4*>(b)[0], b1 = reinterpret_cast<const uint4*>(b)[1];
+  v[0][0] = a0.x; v[0][1] = a0.y; v[0][2] = a0.z; v[0][3] = a0.w;
+  v[0][4] = a1.x; v[0][5] = a1.y; v[0][6] = a1.z; v[0][7] = a1.w;
+  v[1][0] = b0.x; v[1][1] = b0.y; v[1][2] = b0.z; v[1][3] = b0.w;
+  v[1][4] = b1.x; v[1][5] = b1.y; v[1][6] = b1.z; v[1][7] = b1.w;
+}
+
+__device__ __forceinline__ float unit_dot(const UnitCodes<5>& u, const uint32_t (&x)[2][8]) {
+  int s[2] = {0, 0}, xs[2] = {0, 0};
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      s[k] = __builtin_amdgcn_sdot4((int)x[k][e], (int)u.c[k][e], s[k], false);
+      xs[k] = __builtin_amdgcn_sdot4((int)x[k][e], 0x01010101, xs[k], false);
+    }
+  return u.d * (float)(u.sc[0] * s[0] + u.sc[1] * s[1]) - u.dmin * (float)(u.mn[0] * xs[0] + u.mn[1] * xs[1]);
+}
+
+__device__ __forceinline__ float unit_dot(const UnitCodes<6>& u, const uint32_t (&x)[2][8]) {
+  int T = 0;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    int s0 = 0, s1 = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      s0 = __builtin_amdgcn_sdot4((int)x[k][e], (int)u.c[k][e], s0, false);
+      s1 = __builtin_amdgcn_sdot4((int)x[k][4 + e], (int)u.c[k][4 + e], s1, false);
+    }
+    T += u.sc[k][0] * s0 + u.sc[k][1] * s1;
+  }
+  return u.d * (float)T;
+}
+
+// R weight rows per wave: with several activation rows each activation load
+// serves R weight rows.
+template <int FMT, int OUT_DT, int MR, int R>
 __global__ void __launch_bounds__(256)
 gemv_kq_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
                const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K) {
   constexpr int BS = FMT == 5 ? Q5K_BYTES : Q6K_BYTES;
   const int lane = threadIdx.x & 63;
-  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (n >= N) return;  // wave-uniform
+  const int n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+  if (n0 >= N) return;  // wave-uniform
   const int nsb = K >> 8, nu = 4 * nsb;
-  const uint8_t* wr = w + (int64_t)n * nsb * BS;
-  float f[MR];
+  const int64_t row_bytes = (int64_t)nsb * BS;
+  float f[R][MR];
 #pragma unroll
-  for (int m = 0; m < MR; ++m) f[m] = 0.f;
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int m = 0; m < MR; ++m) f[r][m] = 0.f;
 
   for (int u = lane; u < nu; u += 64) {
     const int sb = u >> 2, g = u & 3;
-    const uint8_t* blk = wr + (int64_t)sb * BS;
-    if constexpr (FMT == 5) {
-      // sub-blocks j0 = 2g (low nibbles) and j1 = 2g + 1 (high nibbles)
-      const uint4 hd = *reinterpret_cast<const uint4*>(blk);
-      const uint4 qh0 = *reinterpret_cast<const uint4*>(blk + 16);
-      const uint4 qh1 = *reinterpret_cast<const uint4*>(blk + 32);
-      const uint4 qs0 = *reinterpret_cast<const uint4*>(blk + 48 + 32 * g);
-      const uint4 qs1 = *reinterpret_cast<const uint4*>(blk + 64 + 32 * g);
-      const float d = h2f(hd.x & 0xFFFFu), dmin = h2f(hd.x >> 16);
-      const ScMin sm = unpack_scmin(hd.y, hd.z, hd.w);
-      const int j0 = 2 * g, j1 = j0 + 1;
-      const uint32_t scw = g < 2 ? sm.sc_lo : sm.sc_hi, mnw = g < 2 ? sm.mn_lo : sm.mn_hi;
-      const int sc0 = byte_of(scw, j0 & 3), sc1 = byte_of(scw, j1 & 3);
-      const int mn0 = byte_of(mnw, j0 & 3), mn1 = byte_of(mnw, j1 & 3);
-      const uint32_t qs[8] = {qs0.x, qs0.y, qs0.z, qs0.w, qs1.x, qs1.y, qs1.z, qs1.w};
-      const uint32_t qh[8] = {qh0.x, qh0.y, qh0.z, qh0.w, qh1.x, qh1.y, qh1.z, qh1.w};
-      uint32_t c0[8], c1[8];
+    UnitCodes<FMT> cd[R];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        c0[e] = (qs[e] & 0x0F0F0F0Fu) | (((qh[e] >> j0) & 0x01010101u) << 4);
-        c1[e] = ((qs[e] >> 4) & 0x0F0F0F0Fu) | (((qh[e] >> j1) & 0x01010101u) << 4);
-      }
+    for (int r = 0; r < R; ++r)
+      if (n0 + r < N) unit_codes(w + (int64_t)(n0 + r) * row_bytes + (int64_t)sb * BS, g, cd[r]);
 #pragma unroll
-      for (int m = 0; m < MR; ++m) {
-        if (m < M) {
-          uint32_t xv[16];
-          load_x64(x + (int64_t)m * K + (int64_t)sb * 256 + 64 * g, xv);
-          int s0 = 0, s1 = 0, x0 = 0, x1 = 0;
+    for (int m = 0; m < MR; ++m) {
+      if (m < M) {
+        uint32_t xv[2][8];
+        unit_x<FMT>(x + (int64_t)m * K + (int64_t)sb * 256, g, xv);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            s0 = __builtin_amdgcn_sdot4((int)xv[e], (int)c0[e], s0, false);
-            x0 = __builtin_amdgcn_sdot4((int)xv[e], 0x01010101, x0, false);
-            s1 = __builtin_amdgcn_sdot4((int)xv[8 + e], (int)c1[e], s1, false);
-            x1 = __builtin_amdgcn_sdot4((int)xv[8 + e], 0x01010101, x1, false);
-          }
-          f[m] += d * (float)(sc0 * s0 + sc1 * s1) - dmin * (float)(mn0 * x0 + mn1 * x1);
-        }
-      }
-    } else {
-      // half hf = g >> 1, ql column p = g & 1: quadrants qd = p (low nibbles)
-      // and p + 2 (high nibbles), l = 0..31 each
-      const int hf = g >> 1, p = g & 1;
-      uint32_t ql[8], qh[8];
-      load8_a2(blk + 64 * hf + 32 * p, ql);
-      load8_a2(blk + 128 + 32 * hf, qh);
-      const uintptr_t sa = reinterpret_cast<uintptr_t>(blk + 192 + 8 * hf);
-      const uint32_t* sp = reinterpret_cast<const uint32_t*>(sa & ~(uintptr_t)3);
-      const uint32_t ssh = (uint32_t)(sa & 3);
-      const uint32_t s0w = __builtin_amdgcn_alignbyte(sp[1], sp[0], ssh);  // scales 8hf + 0..3
-      const uint32_t s1w = __builtin_amdgcn_alignbyte(sp[2], sp[1], ssh);  // scales 8hf + 4..7
-      const uintptr_t da = reinterpret_cast<uintptr_t>(blk + 208);
-      const uint32_t dw = *reinterpret_cast<const uint32_t*>(da & ~(uintptr_t)3);
-      const float d = h2f((uint16_t)((da & 3) ? (dw >> 16) : (dw & 0xFFFFu)));
-      int sc[2][2];  // [quadrant p / p + 2][16-element half]
-      sc[0][0] = (int)(int8_t)byte_of(s0w, 2 * p);
-      sc[0][1] = (int)(int8_t)byte_of(s0w, 2 * p + 1);
-      sc[1][0] = (int)(int8_t)byte_of(s1w, 2 * p);
-      sc[1][1] = (int)(int8_t)byte_of(s1w, 2 * p + 1);
-      uint32_t v[2][8];
-#pragma unroll
-      for (int k = 0; k < 2; ++k) {
-        const int qd = p + 2 * k;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const uint32_t q = ((ql[e] >> (4 * k)) & 0x0F0F0F0Fu) | (((qh[e] >> (2 * qd)) & 0x03030303u) << 4);
-          const uint32_t t = q ^ 0x20202020u;                  // 6-bit two's complement of q - 32
-          v[k][e] = t | ((t & 0x20202020u) * 6u);              // sign-extended to 8 bits
-        }
-      }
-#pragma unroll
-      for (int m = 0; m < MR; ++m) {
-        if (m < M) {
-          const int8_t* xb = x + (int64_t)m * K + (int64_t)sb * 256 + 128 * hf + 32 * p;
-          int T = 0;
-#pragma unroll
-          for (int k = 0; k < 2; ++k) {
-            const uint4 xa = *reinterpret_cast<const uint4*>(xb + 64 * k);
-            const uint4 xc = *reinterpret_cast<const uint4*>(xb + 64 * k + 16);
-            const uint32_t xv[8] = {xa.x, xa.y, xa.z, xa.w, xc.x, xc.y, xc.z, xc.w};
-            int s0 = 0, s1 = 0;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              s0 = __builtin_amdgcn_sdot4((int)xv[e], (int)v[k][e], s0, false);
-              s1 = __builtin_amdgcn_sdot4((int)xv[4 + e], (int)v[k][4 + e], s1, false);
-            }
-            T += sc[k][0] * s0 + sc[k][1] * s1;
-          }
-          f[m] += d * (float)T;
-        }
+        for (int r = 0; r < R; ++r)
+          if (n0 + r < N) f[r][m] += unit_dot(cd[r], xv);
       }
     }
   }
 #pragma unroll
-  for (int m = 0; m < MR; ++m) {
+  for (int r = 0; r < R; ++r)
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) f[m] += __shfl_xor(f[m], o, 64);
-  }
+    for (int m = 0; m < MR; ++m) {
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) f[r][m] += __shfl_xor(f[r][m], o, 64);
+    }
   if (lane == 0) {
 #pragma unroll
-    for (int m = 0; m < MR; ++m)
-      if (m < M) st_out<OUT_DT>(out, (int64_t)m * N + n, f[m] * x_scale[m]);
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int m = 0; m < MR; ++m)
+        if (m < M && n0 + r < N) st_out<OUT_DT>(out, (int64_t)m * N + n0 + r, f[r][m] * x_scale[m]);
   }
 }
 
 template <int FMT, int MR>
 void launch_gemv_kq_m(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
                       int M, int N, int K, hipStream_t st) {
-  const dim3 grid((unsigned)((N + 3) / 4));
+#ifndef SL8_KQ_ROWS
+#define SL8_KQ_ROWS 2  // measured: 2 rows beat 1 (x reuse) and 4 (occupancy) at M = 4..16
+#endif
+  constexpr int R = MR >= 4 ? SL8_KQ_ROWS : 1;
+  const dim3 grid((unsigned)((N + 4 * R - 1) / (4 * R)));
   switch (odt) {
-    case SL8_DTYPE_F16: gemv_kq_kernel<FMT, SL8_DTYPE_F16, MR><<<grid, 256, 0, st>>>(x, xs, w, out, M, N, K); break;
-    case SL8_DTYPE_BF16: gemv_kq_kernel<FMT, SL8_DTYPE_BF16, MR><<<grid, 256, 0, st>>>(x, xs, w, out, M, N, K); break;
-    default: gemv_kq_kernel<FMT, SL8_DTYPE_F32, MR><<<grid, 256, 0, st>>>(x, xs, w, out, M, N, K); break;
+    case SL8_DTYPE_F16: gemv_kq_kernel<FMT, SL8_DTYPE_F16, MR, R><<<grid, 256, 0, st>>>(x, xs, w, out, M, N, K); break;
+    case SL8_DTYPE_BF16: gemv_kq_kernel<FMT, SL8_DTYPE_BF16, MR, R><<<grid, 256, 0, st>>>(x, xs, w, out, M, N, K); break;
+    default: gemv_kq_kernel<FMT, SL8_DTYPE_F32, MR, R><<<grid, 256, 0, st>>>(x, xs, w, out, M, N, K); break;
   }
 }
 
