@@ -2,15 +2,16 @@
 
 Drop-in for the reference package's hot-path surface: `ops` (attn_int8_fwd,
 attn_int8_decode, quantize_kv_cache, attn_decode_cached, quantize_kv_write_paged,
-attn_paged_decode_cached, quantize_i8_rowwise, linear_q4k, linear_q5k,
-linear_q6k), `quant`, and `_C` (the operator surface of the compiled extension,
+attn_paged_decode_cached, quantize_i8_rowwise, linear, linear_q4k, linear_q5k,
+linear_q6k), `quant`, `format` (QTensor), `gguf` (the GGUF reader feeding
+native k-quant bytes) and `_C` (the operator surface of the compiled extension,
 here a C-ABI library).
 """
 from . import _C  # noqa: F401
 from .ops import (attn_decode_cached, attn_int8_decode, attn_int8_fwd, attn_paged_decode_cached,
-                  linear_q4k, linear_q5k, linear_q6k, quantize_i8_rowwise, quantize_kv_cache,
+                  linear, linear_q4k, linear_q5k, linear_q6k, quantize_i8_rowwise, quantize_kv_cache,
                   quantize_kv_write_paged)
 
 __all__ = ["attn_decode_cached", "attn_int8_decode", "attn_int8_fwd", "attn_paged_decode_cached",
-           "linear_q4k", "linear_q5k", "linear_q6k", "quantize_i8_rowwise", "quantize_kv_cache",
+           "linear", "linear_q4k", "linear_q5k", "linear_q6k", "quantize_i8_rowwise", "quantize_kv_cache",
            "quantize_kv_write_paged", "_C"]

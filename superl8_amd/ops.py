@@ -206,6 +206,22 @@ def linear_q6k(x: torch.Tensor, w_bytes: torch.Tensor, *, bias: torch.Tensor | N
                           getattr(_C, "gemm_decode_q6k", None))
 
 
+_FUSED_KQUANT_OPS = {"q4_k": linear_q4k, "q5_k": linear_q5k, "q6_k": linear_q6k}
+
+
+def linear(x: torch.Tensor, qt, *, bias: torch.Tensor | None = None,
+           out_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """Scheme-dispatched linear over a ``superl8_amd.format.QTensor`` (reference
+    ops.py:2088-2150, the ``gguf_kquant`` arm): native Q4_K / Q5_K / Q6_K bytes run
+    on the fused kernels; any other scheme or type tag raises ValueError."""
+    if qt.scheme == "gguf_kquant":
+        op = _FUSED_KQUANT_OPS.get(qt.codebook)
+        if op is not None:
+            return op(x, qt.data, bias=bias, out_dtype=out_dtype)
+        raise ValueError(f"superl8.linear: gguf_kquant type {qt.codebook!r} has no fused kernel")
+    raise ValueError(f"superl8.linear: unsupported weight scheme {qt.scheme!r}")
+
+
 def _linear_kquant(x, w_bytes, bias, out_dtype, tile_op, decode_op):
     *lead, K = x.shape
     x2 = x.reshape(-1, K).contiguous()
