@@ -525,16 +525,30 @@ __device__ __forceinline__ void unit_x(const int8_t* xsb, int g, uint32_t (&v)[2
   v[1][4] = b1.x; v[1][5] = b1.y; v[1][6] = b1.z; v[1][7] = b1.w;
 }
 
-__device__ __forceinline__ float unit_dot(const UnitCodes<5>& u, const uint32_t (&x)[2][8]) {
-  int s[2] = {0, 0}, xs[2] = {0, 0};
+// sums of the unit's two 32-activation sub-blocks (the Q5_K min term)
+__device__ __forceinline__ void unit_xsum(const uint32_t (&x)[2][8], int (&xs)[2]) {
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    xs[k] = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xs[k] = __builtin_amdgcn_sdot4((int)x[k][e], 0x01010101, xs[k], false);
+  }
+}
+
+__device__ __forceinline__ float unit_dot(const UnitCodes<5>& u, const uint32_t (&x)[2][8],
+                                          const int (&xs)[2]) {
+  int s[2] = {0, 0};
 #pragma unroll
   for (int k = 0; k < 2; ++k)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      s[k] = __builtin_amdgcn_sdot4((int)x[k][e], (int)u.c[k][e], s[k], false);
-      xs[k] = __builtin_amdgcn_sdot4((int)x[k][e], 0x01010101, xs[k], false);
-    }
+    for (int e = 0; e < 8; ++e) s[k] = __builtin_amdgcn_sdot4((int)x[k][e], (int)u.c[k][e], s[k], false);
   return u.d * (float)(u.sc[0] * s[0] + u.sc[1] * s[1]) - u.dmin * (float)(u.mn[0] * xs[0] + u.mn[1] * xs[1]);
+}
+
+__device__ __forceinline__ float unit_dot(const UnitCodes<5>& u, const uint32_t (&x)[2][8]) {
+  int xs[2];
+  unit_xsum(x, xs);
+  return unit_dot(u, x, xs);
 }
 
 __device__ __forceinline__ float unit_dot(const UnitCodes<6>& u, const uint32_t (&x)[2][8]) {
@@ -581,9 +595,17 @@ gemv_kq_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
       if (m < M) {
         uint32_t xv[2][8];
         unit_x<FMT>(x + (int64_t)m * K + (int64_t)sb * 256, g, xv);
+        if constexpr (FMT == 5) {
+          int xs[2];  // shared by the R weight rows
+          unit_xsum(xv, xs);
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-          if (n0 + r < N) f[r][m] += unit_dot(cd[r], xv);
+          for (int r = 0; r < R; ++r)
+            if (n0 + r < N) f[r][m] += unit_dot(cd[r], xv, xs);
+        } else {
+#pragma unroll
+          for (int r = 0; r < R; ++r)
+            if (n0 + r < N) f[r][m] += unit_dot(cd[r], xv);
+        }
       }
     }
   }
@@ -603,12 +625,62 @@ gemv_kq_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
   }
 }
 
+// M = 1: RF weight rows per wave with their units laid end to end over the
+// lanes (K = 5120: 4 rows x 80 units = 5 full passes of 64 lanes, where one row
+// per wave leaves 48 of 64 lanes idle in its second pass).
+template <int FMT, int OUT_DT, int RF>
+__global__ void __launch_bounds__(256)
+gemv_kq_flat_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
+                    const uint8_t* __restrict__ w, void* __restrict__ out, int N, int K) {
+  constexpr int BS = FMT == 5 ? Q5K_BYTES : Q6K_BYTES;
+  const int lane = threadIdx.x & 63;
+  const int n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RF;
+  if (n0 >= N) return;  // wave-uniform
+  const int nsb = K >> 8, nu = 4 * nsb;
+  const int nr = min(RF, N - n0);
+  const int64_t row_bytes = (int64_t)nsb * BS;
+  float f[RF];
+#pragma unroll
+  for (int r = 0; r < RF; ++r) f[r] = 0.f;
+  for (int v = lane; v < nr * nu; v += 64) {
+    const int r = v / nu, u = v - r * nu;
+    const int sb = u >> 2, g = u & 3;
+    UnitCodes<FMT> cd;
+    unit_codes(w + (int64_t)(n0 + r) * row_bytes + (int64_t)sb * BS, g, cd);
+    uint32_t xv[2][8];
+    unit_x<FMT>(x + (int64_t)sb * 256, g, xv);
+    const float val = unit_dot(cd, xv);
+#pragma unroll
+    for (int rr = 0; rr < RF; ++rr) f[rr] += (rr == r) ? val : 0.f;
+  }
+#pragma unroll
+  for (int r = 0; r < RF; ++r) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) f[r] += __shfl_xor(f[r], o, 64);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < RF; ++r)
+      if (r < nr) st_out<OUT_DT>(out, (int64_t)(n0 + r), f[r] * x_scale[0]);
+  }
+}
+
 template <int FMT, int MR>
 void launch_gemv_kq_m(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
                       int M, int N, int K, hipStream_t st) {
 #ifndef SL8_KQ_ROWS
 #define SL8_KQ_ROWS 2  // measured: 2 rows beat 1 (x reuse) and 4 (occupancy) at M = 4..16
 #endif
+  if (MR == 1) {
+    constexpr int RF = FMT == 5 ? 4 : 2;  // measured at K = 5120: Q6_K's larger unit state favours 2
+    const dim3 g1((unsigned)((N + 4 * RF - 1) / (4 * RF)));
+    switch (odt) {
+      case SL8_DTYPE_F16: gemv_kq_flat_kernel<FMT, SL8_DTYPE_F16, RF><<<g1, 256, 0, st>>>(x, xs, w, out, N, K); break;
+      case SL8_DTYPE_BF16: gemv_kq_flat_kernel<FMT, SL8_DTYPE_BF16, RF><<<g1, 256, 0, st>>>(x, xs, w, out, N, K); break;
+      default: gemv_kq_flat_kernel<FMT, SL8_DTYPE_F32, RF><<<g1, 256, 0, st>>>(x, xs, w, out, N, K); break;
+    }
+    return;
+  }
   constexpr int R = MR >= 4 ? SL8_KQ_ROWS : 1;
   const dim3 grid((unsigned)((N + 4 * R - 1) / (4 * R)));
   switch (odt) {
