@@ -221,9 +221,9 @@ gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
 
 // ---------------------------------------------------------------------------
 // M <= 2: 16 weight rows per workgroup like the kernel above, with K split
-// over SWAVES = 8 waves of up to SCH = 3 super-blocks (half the per-wave
-// work of a 4-way split: the compute left after the last loads land is
-// shorter), and the dot products run on VALU
+// over SWAVES = 10 waves of up to SCH = 2 super-blocks (a fifth of the
+// per-wave work of a 4-way split: the compute left after the last loads land
+// is short, and at 64 VGPRs 8 waves share each SIMD), and the dot products run on VALU
 // v_dot4 in the load layout itself -- lane 4r + c owns 16-byte piece c of
 // each 64-byte half of weight row r, i.e. elements 16(c&1)..+15 of
 // sub-blocks j = 2(c>>1) (low nibbles) and j+1 (high nibbles) of that half
@@ -239,16 +239,21 @@ __device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
 }
 
 #ifndef SL8_GEMV_SWAVES
-#define SL8_GEMV_SWAVES 8
+#define SL8_GEMV_SWAVES 10
 #endif
 #ifndef SL8_GEMV_SCH
-#define SL8_GEMV_SCH 3
+#define SL8_GEMV_SCH 2
 #endif
 constexpr int SWAVES = SL8_GEMV_SWAVES;  // K split of the M <= 2 kernel
 constexpr int SCH = SL8_GEMV_SCH;        // its super-blocks per wave and chunk
 constexpr int SXPITCH = SCH * 256;
+// M = 1: at most 64 VGPRs, so 8 waves per SIMD and nearly the whole decode
+// grid (1088 workgroups x 10 waves at N = 17408) is resident at once
+#ifndef SL8_GEMV_SOCC
+#define SL8_GEMV_SOCC 8
+#endif
 template <int OUT_DT, int MR>
-__global__ void __launch_bounds__(64 * SWAVES)
+__global__ void __launch_bounds__(64 * SWAVES, (SL8_GEMV_SOCC > 0 && MR == 1) ? SL8_GEMV_SOCC : 1)
 gemv_q4k_small_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
                       const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K) {
   constexpr int XC = (MR * SXPITCH + 1023) / 1024;  // 16-byte activation pieces per lane
