@@ -250,41 +250,89 @@ decode_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sc
   }
 }
 
-// One block per query head; thread = channel. The split maxima and sums are
-// read once into LDS; the partial vectors are read with one coalesced load
-// per split and channel.
-__global__ void decode_combine_kernel(const float* __restrict__ o_part,
-                                      const float* __restrict__ m_part,
-                                      const float* __restrict__ l_part,
-                                      uint16_t* __restrict__ out, int n_splits, int bhq, int D) {
-  __shared__ float sm_m[DEC_MAX_SPLITS], sm_l[DEC_MAX_SPLITS];
-  __shared__ float sm_gm;
-  const int64_t hq = blockIdx.x;
-  for (int s = threadIdx.x; s < n_splits; s += blockDim.x) {
-    sm_m[s] = m_part[(int64_t)s * bhq + hq];
-    sm_l[s] = l_part[(int64_t)s * bhq + hq];
+// Cross-split LSE merge (reference attn_decode.cuh:430-466):
+//   gm = max_s m_s, out = sum_s o_s 2^(m_s - gm) / sum_s l_s 2^(m_s - gm),
+// empty splits (m_s = DEC_NEG_INF) contributing nothing. One wave per query
+// head (4 per workgroup): the lanes
+// hold D / 64 channels each and every partial load of the head is issued
+// before any is used; the split weights 2^(m_s - gm) are formed once per
+// split by the lane that loaded m_s and broadcast, and the sums run over the
+// splits in index order (deterministic).
+template <int D>
+__global__ void __launch_bounds__(256)
+decode_combine_wave_kernel(const float* __restrict__ o_part, const float* __restrict__ m_part,
+                           const float* __restrict__ l_part, uint16_t* __restrict__ out,
+                           int n_splits, int bhq) {
+  constexpr int CPL = D / 64;
+  const int lane = threadIdx.x & 63;
+  const int64_t hq = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (hq >= bhq) return;  // wave-uniform
+  constexpr int SCH = 16;  // splits whose partials are in flight together
+  // m, l of splits lane, lane + 64, ... (n_splits <= DEC_MAX_SPLITS = 4 x 64)
+  float ms[DEC_MAX_SPLITS / 64], ls[DEC_MAX_SPLITS / 64];
+  float gm = DEC_NEG_INF;
+#pragma unroll
+  for (int c = 0; c < DEC_MAX_SPLITS / 64; ++c) {
+    const int sp = c * 64 + lane;
+    ms[c] = sp < n_splits ? m_part[(int64_t)sp * bhq + hq] : DEC_NEG_INF;
+    ls[c] = sp < n_splits ? l_part[(int64_t)sp * bhq + hq] : 0.f;
+    gm = fmaxf(gm, ms[c]);
   }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float gm = DEC_NEG_INF;
-    for (int s = 0; s < n_splits; ++s) gm = fmaxf(gm, sm_m[s]);
-    sm_gm = gm;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) gm = fmaxf(gm, __shfl_xor(gm, o, 64));
+  float wt[DEC_MAX_SPLITS / 64];
+  float den = 0.f;
+#pragma unroll
+  for (int c = 0; c < DEC_MAX_SPLITS / 64; ++c) {
+    wt[c] = (ms[c] == DEC_NEG_INF) ? 0.f : exp2f(ms[c] - gm);
+    den += ls[c] * wt[c];
   }
-  __syncthreads();
-  const float gm = sm_gm;
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float acc = 0.f, den = 0.f;
-#pragma unroll 8
-    for (int s = 0; s < n_splits; ++s) {
-      const float ms = sm_m[s];
-      const float o = o_part[((int64_t)s * bhq + hq) * D + d];
-      if (ms == DEC_NEG_INF) continue;
-      const float wt = exp2f(ms - gm);
-      den += sm_l[s] * wt;
-      acc += o * wt;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) den += __shfl_xor(den, o, 64);
+  float acc[CPL];
+#pragma unroll
+  for (int e = 0; e < CPL; ++e) acc[e] = 0.f;
+  const float* ob = o_part + hq * D + CPL * lane;
+  for (int s0 = 0; s0 < n_splits; s0 += SCH) {
+    // weights of splits s0 .. s0 + SCH - 1 live in register wt[s0 / 64] of lanes (s0 % 64) ..
+    const int c = s0 >> 6;
+    const float wc = c == 0 ? wt[0] : (c == 1 ? wt[1] : (c == 2 ? wt[2] : wt[3]));
+    float ov[SCH][CPL];
+#pragma unroll
+    for (int i = 0; i < SCH; ++i) {
+      const int sp = min(s0 + i, n_splits - 1);
+      const float* src = ob + (int64_t)sp * bhq * D;
+      if constexpr (CPL == 4) {
+        const float4 v4 = *reinterpret_cast<const float4*>(src);
+        ov[i][0] = v4.x; ov[i][1] = v4.y; ov[i][2] = v4.z; ov[i][3] = v4.w;
+      } else if constexpr (CPL == 2) {
+        const float2 v2 = *reinterpret_cast<const float2*>(src);
+        ov[i][0] = v2.x; ov[i][1] = v2.y;
+      } else {
+        ov[i][0] = *src;
+      }
     }
-    out[hq * D + d] = f2h_bits(den > 0.f ? acc / den : 0.f);
+#pragma unroll
+    for (int i = 0; i < SCH; ++i) {
+      const int sp = s0 + i;
+      if (sp < n_splits) {  // wave-uniform
+        const float w = __shfl(wc, sp & 63, 64);
+#pragma unroll
+        for (int e = 0; e < CPL; ++e) acc[e] += ov[i][e] * w;
+      }
+    }
   }
+  const float inv = den > 0.f ? 1.f / den : 0.f;
+#pragma unroll
+  for (int e = 0; e < CPL; ++e) out[hq * D + CPL * lane + e] = f2h_bits(den > 0.f ? acc[e] * inv : 0.f);
+}
+
+template <typename... A>
+void launch_combine(int D, int bhq, hipStream_t st, A... args) {
+  const dim3 g((unsigned)((bhq + 3) / 4));
+  if (D == 64) decode_combine_wave_kernel<64><<<g, 256, 0, st>>>(args...);
+  else if (D == 128) decode_combine_wave_kernel<128><<<g, 256, 0, st>>>(args...);
+  else decode_combine_wave_kernel<256><<<g, 256, 0, st>>>(args...);
 }
 
 // ---------------------------------------------------------------------------
@@ -720,8 +768,7 @@ int decode_launch(const int8_t* q, const float* q_scale, const int8_t* k, const 
     default: launch_d<256, VI8>(G, grid, q, q_scale, k, k_scale, v, vsc, op, mp, lp, (int)N, ns, (int)Hq, (int)Hkv, gsz, bhq, st); break;
   }
   SL8_CHECK_LAUNCH("attn_int8_decode split");
-  decode_combine_kernel<<<bhq, (unsigned)(D < 256 ? D : 256), 0, st>>>(
-      op, mp, lp, static_cast<uint16_t*>(out), ns, bhq, (int)D);
+  launch_combine((int)D, bhq, st, op, mp, lp, static_cast<uint16_t*>(out), ns, bhq);
   SL8_CHECK_LAUNCH("attn_int8_decode combine");
   return SL8_OK;
 }
@@ -926,8 +973,7 @@ extern "C" int sl8_attn_paged_decode(const int8_t* q, const float* q_scale, cons
 #undef SL8_PAGED
   }
   SL8_CHECK_LAUNCH("attn_paged_decode split");
-  decode_combine_kernel<<<ibhq, (unsigned)(D < 256 ? D : 256), 0, st>>>(
-      op, mp, lp, static_cast<uint16_t*>(out), ns, ibhq, (int)D);
+  launch_combine((int)D, ibhq, st, op, mp, lp, static_cast<uint16_t*>(out), ns, ibhq);
   SL8_CHECK_LAUNCH("attn_paged_decode combine");
   return SL8_OK;
 }
