@@ -32,6 +32,10 @@ constexpr int DEC_WAVES = 4;
 constexpr int DEC_TILE = 64;
 constexpr float DEC_NEG_INF = -1e30f;
 constexpr int DEC_MAX_SPLITS = 256;
+#ifndef SL8_DEC_PAIR
+#define SL8_DEC_PAIR 1
+#endif
+constexpr bool DEC_PAIR = SL8_DEC_PAIR;  // int8-V PV: two keys per v_dot2 (see decode_wave_kernel)
 
 template <int D, int G>
 struct DecSmem {
@@ -491,6 +495,7 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
   };
 
   float m_run = -INFINITY, l_lane = 0.f, lv_lane = 0.f, oacc[CPL];  // lv: sum of p * v_scale (PG)
+  float pq_sum = 0.f;  // VI8 pair path: the head's sum of the fp16 p that entered PV
 #pragma unroll
   for (int e = 0; e < CPL; ++e) oacc[e] = 0.f;
 
@@ -541,6 +546,58 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
     }
 #pragma unroll
     for (int e = 0; e < CPL; ++e) oacc[e] *= resc;
+    if constexpr (VI8 && DEC_PAIR) {
+      // Two keys per step: one v_perm per channel packs the unsigned codes
+      // u = v + 128 of keys k0, k1 as the fp16 pair (u0, u1) * 2^-24 (exact
+      // fp16 denormals, byte over a zero byte), and v_dot2_f32_f16 against
+      // the fp16 pair (p0, p1) accumulates both keys. The 2^24 factor and the
+      // 128 * sum(p) offset are removed once per split.
+      pq_sum *= resc;
+      typedef _Float16 v2h_t __attribute__((ext_vector_type(2)));
+      const v2h_t one2 = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+      for (int u = 0; u < SUB; ++u) {
+        static_for<0, KL / 2>([&](auto rc) {
+          constexpr int rr = 2 * decltype(rc)::value;
+          const float pk0 = lane_bcast<KL, rr>(p[u]);
+          const float pk1 = lane_bcast<KL, rr + 1>(p[u]);
+          const v2h_t pp = {(_Float16)pk0, (_Float16)pk1};
+          pq_sum = __builtin_amdgcn_fdot2(pp, one2, pq_sum, false);
+          const uint8_t* r0 = reinterpret_cast<const uint8_t*>(vt) + (u * KL + rr) * D + kl * CPL;
+          const uint8_t* r1 = r0 + D;
+          uint32_t w0[CPL / 4], w1[CPL / 4];
+          if constexpr (CPL % 16 == 0) {
+#pragma unroll
+            for (int c16 = 0; c16 < CPL; c16 += 16) {
+              const uint4 x0 = *reinterpret_cast<const uint4*>(r0 + c16);
+              const uint4 x1 = *reinterpret_cast<const uint4*>(r1 + c16);
+              w0[c16 / 4] = x0.x; w0[c16 / 4 + 1] = x0.y; w0[c16 / 4 + 2] = x0.z; w0[c16 / 4 + 3] = x0.w;
+              w1[c16 / 4] = x1.x; w1[c16 / 4 + 1] = x1.y; w1[c16 / 4 + 2] = x1.z; w1[c16 / 4 + 3] = x1.w;
+            }
+          } else if constexpr (CPL == 8) {
+            const uint2 x0 = *reinterpret_cast<const uint2*>(r0);
+            const uint2 x1 = *reinterpret_cast<const uint2*>(r1);
+            w0[0] = x0.x; w0[1] = x0.y;
+            w1[0] = x1.x; w1[1] = x1.y;
+          } else {
+            w0[0] = *reinterpret_cast<const uint32_t*>(r0);
+            w1[0] = *reinterpret_cast<const uint32_t*>(r1);
+          }
+#pragma unroll
+          for (int c = 0; c < CPL / 4; ++c) {
+            const uint32_t a = w0[c] ^ 0x80808080u, bq = w1[c] ^ 0x80808080u;
+#pragma unroll
+            for (int bb = 0; bb < 4; ++bb) {
+              // bytes: [a_bb, 0, b_bb, 0] (selector 12 = zero byte; 0-3 = a, 4-7 = bq)
+              const uint32_t sel = (uint32_t)bb | (12u << 8) | ((uint32_t)(4 + bb) << 16) | (12u << 24);
+              const uint32_t pr = __builtin_amdgcn_perm(bq, a, sel);
+              oacc[4 * c + bb] = __builtin_amdgcn_fdot2(pp, __builtin_bit_cast(v2h_t, pr), oacc[4 * c + bb], false);
+            }
+          }
+        });
+      }
+      return;
+    }
 #pragma unroll
     for (int u = 0; u < SUB; ++u) {
       static_for<0, KL>([&](auto rc) {
@@ -630,7 +687,15 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
   // ---- per-wave state -> LDS (this wave's own stage-0 area), then LSE merge ----
 #pragma unroll
   for (int o = 1; o < KL; o <<= 1) l_lane += __shfl_xor(l_lane, o, 64);
-  if constexpr (PG) {
+  if constexpr (VI8 && DEC_PAIR) {
+    // codes entered PV as (v + 128) * 2^-24 against the fp16 p: rescale and
+    // remove the 128 offset weighted by exactly those p
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) {
+      oacc[e] = oacc[e] * 16777216.f - 128.f * pq_sum;
+      if constexpr (!PG) oacc[e] *= vsc[(int64_t)bkv * D + kl * CPL + e];
+    }
+  } else if constexpr (PG) {
     // remove the 1152 offset per key, weighted like the p that entered PV
 #pragma unroll
     for (int o = 1; o < KL; o <<= 1) lv_lane += __shfl_xor(lv_lane, o, 64);
