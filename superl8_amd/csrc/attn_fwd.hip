@@ -31,6 +31,7 @@
 // KV-head count is a multiple of 8, all query heads of one KV head go to the
 // same XCD so its K/V tiles stay in that XCD's L2.
 
+#include <algorithm>
 #include <climits>
 
 #include "attn_common.hpp"
@@ -43,6 +44,15 @@ constexpr int FWD_WAVES = 4;
 constexpr int BM = 128;  // queries per workgroup
 constexpr int BN = 64;   // keys per tile
 constexpr float LN2F = 0.6931471805599453f;
+#ifndef SL8_W8_LAZY
+#define SL8_W8_LAZY 1
+#endif
+// W8A8 reference point: set by the row's first visible half and raised
+// lazily (see half_probs_w8) when a half's max exceeds it by more than the
+// launch's w8_excess: P = code * 2^(max_half - m) / 127 then stays below
+// 2^w8_excess, and with |V code| <= 127 the fp32 O and l sums over N keys
+// stay below 2^(w8_excess + 7 + log2 N) <= 2^120 (w8_excess_for()).
+constexpr bool W8_LAZY = SL8_W8_LAZY;
 
 
 // W8A8 variant: int8 V -> bf16 V^T [BHkv][D][Npad] (Npad = N rounded up to 64,
@@ -146,6 +156,7 @@ struct FwdArgs {
   int M, N, Npad, Hq, Hkv, nqb, window_left;
   int diag;            // causal: query i sees keys <= i + diag
   int xcd_map;         // xcd_mode(): XCD-aware block order
+  float w8_excess;     // W8A8: headroom of P above the reference point (log2)
 };
 
 // LDS tiles are dense; 16-byte chunks are XOR-swizzled within each row
@@ -774,17 +785,44 @@ attn_fwd_wide_kernel(const FwdArgs a) {
     //   code = rint(127 * 2^(t - tmax_h)),
     // and enters the bf16 PV operand as code * 2^(tmax_h - m) / 127 (an
     // integer <= 127 times one per-row factor, applied before the product
-    // instead of after the int32 sum), with m the exact row max from a
-    // QK-only sweep that precedes the pass: logits with large outliers leave
-    // no usable first guess for m, and O is never rescaled. The denominator
-    // sums the unquantised 2^(t - m).
+    // instead of after the int32 sum). m is the row's reference point: set by
+    // its first visible half (settle()) and moved up, with O and l rescaled,
+    // only when a half's max exceeds it by more than a.w8_excess (~100 log2
+    // units: bf16 P and the fp32 sums have the range), so rows with large
+    // outliers rescale a few times instead of needing the exact row max from
+    // a separate QK sweep (the W8_LAZY = false build: sweep, then one pass
+    // with O never rescaled). The denominator sums the unquantised 2^(t - m).
     auto half_probs_w8 = [&](const xblk& xi, pblk& pc) __attribute__((always_inline)) {
       constexpr float LOG2_127 = 6.988684686772166f;
       float tm[NG];
       half_max(xi, tm);
 #pragma unroll
+      for (int g = 0; g < NG; ++g) tm[g] *= qsc[g];
+      if constexpr (W8_LAZY) {
+        // lazy rescale: a row whose half max exceeds its reference point by
+        // more than a.w8_excess moves the point to that max, scaling its O
+        // and l (O holds the products of halves up to h - 2, all relative to
+        // the old point)
+        const float excess = a.w8_excess;
+        bool up = false;
+#pragma unroll
+        for (int g = 0; g < NG; ++g) up = up || (tm[g] > m_run[g] + excess);
+        if (__any(up)) {
+#pragma unroll
+          for (int g = 0; g < NG; ++g) {
+            const bool ug = tm[g] > m_run[g] + excess;
+            const float f = ug ? __builtin_amdgcn_exp2f(m_run[g] - tm[g]) : 1.f;
+            if (ug) m_run[g] = tm[g];
+            l_lane[g] *= f;
+#pragma unroll
+            for (int t = 0; t < DC; ++t)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) oacc[g][t][r] *= f;
+          }
+        }
+      }
+#pragma unroll
       for (int g = 0; g < NG; ++g) {
-        tm[g] *= qsc[g];
         const bool any_key = tm[g] != -INFINITY;
         const float sub = any_key ? tm[g] - LOG2_127 : 0.f;
         const float fac = any_key ? __builtin_amdgcn_exp2f(tm[g] - m_run[g]) * (1.0f / 127.0f) : 0.f;
@@ -828,6 +866,7 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       half_pv(vt, s, p2);
       half_probs_w8(xi, p1);
       half_scores(sc, st, j, s, mask, dead, xo);
+      if constexpr (W8_LAZY) settle(xo);
     };
     // QK-only sweep: mx_all = the exact row max (exp2 domain) of the
     // visible logits, with the same double-buffered tile copies as the pass.
@@ -890,8 +929,8 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       wait_dma();
       __syncthreads();
     };
-    if constexpr (W8) sweep();
-    for (int attempt = W8 ? 1 : 0; attempt < 2; ++attempt) {
+    if constexpr (W8 && !W8_LAZY) sweep();
+    for (int attempt = (W8 && !W8_LAZY) ? 1 : 0; attempt < 2; ++attempt) {
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
 #pragma unroll
@@ -1050,6 +1089,13 @@ FwdArgs make_args(int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N, int&
 // W8A8 prefill with per-warp P quantisation on the production pipeline
 // (called from attn_w8a8.hip). v: int8 [B*Hkv][N][D]; vt_ws: workspace of
 // w8a8_wide_workspace() bytes for bf16 V^T [B*Hkv][D][Npad].
+// largest P exponent that keeps the W8A8 sums of N keys below 2^120
+float w8_excess_for(int64_t N) {
+  int lg = 0;
+  while (lg < 62 && (1LL << lg) < N) ++lg;
+  return (float)std::max(16, 120 - 7 - lg);
+}
+
 size_t w8a8_wide_workspace(int64_t B, int64_t Hkv, int64_t N, int64_t D) {
   return (size_t)(B * Hkv * D * npad_of(N)) * sizeof(uint16_t);
 }
@@ -1072,6 +1118,7 @@ int w8a8_wide_launch(const int8_t* q, const float* q_scale, const int8_t* k, con
   a.q = q; a.qs = q_scale; a.k = k; a.ks = k_scale;
   a.vt = vt; a.vs = v_scale; a.out = out; a.lse = nullptr;
   a.diag = (int)causal_diag;
+  a.w8_excess = w8_excess_for(N);
   a.nqb = (int)((M + wide_bm(D) - 1) / wide_bm(D));
   const int nslot = causal ? (a.nqb + 1) / 2 : a.nqb;
   grid = (int)(B * Hq * nslot);

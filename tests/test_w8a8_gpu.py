@@ -61,6 +61,31 @@ def test_kernel_matches_oracle(device, case, per_warp):
     assert_int8_quality(out, ref, min_cos=0.9999, max_rel_l1=5e-3, min_sqnr_db=35)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("D", [128, 256])
+def test_rising_row_max(device, causal, D):
+    """Per-warp W8A8: logits of later key tiles exceed the first tile's maximum
+    by far more than the kernel's lazy-rescale headroom (2^32 on the bf16 P
+    operand), so rows move their reference point (and rescale O and the row
+    sum) several times; the result must still match the oracle."""
+    B, Hq, Hkv, M, N = 1, 2, 1, 160, 288
+    g = torch.Generator(device="cpu").manual_seed(11)
+    q_i8 = torch.randint(-127, 128, (B, Hq, M, D), generator=g, dtype=torch.int8)
+    k_i8 = torch.randint(-127, 128, (B, Hkv, N, D), generator=g, dtype=torch.int8)
+    v_i8 = torch.randint(-127, 128, (B, Hkv, N, D), generator=g, dtype=torch.int8)
+    qs = torch.full((B, Hq, M), 1.0 / (127.0 * 127.0 * np.sqrt(D) / 3.0), dtype=torch.float32)
+    ks = torch.linspace(1e-3, 60.0, N).repeat(B, Hkv, 1).contiguous()  # logit scale rises along the keys
+    vs = (torch.rand(B, Hkv, D, generator=g) * 0.02 + 0.005).to(torch.float32)
+    diag = N - M if causal else 0
+    dv = [t.to(device) for t in (q_i8, qs, k_i8, ks, v_i8, vs)]
+    out = _C.attn_w8a8_fwd(*dv, causal, diag, True)
+    ref = oa.attn_w8a8_fwd(_np(q_i8), _np(qs), _np(k_i8), _np(ks), _np(v_i8), _np(vs), causal, diag,
+                           True)
+    assert_finite(out)
+    assert_close_abs(out, ref, atol=2e-2, what="w8a8 rising row max vs oracle")
+    assert_int8_quality(out, ref, min_cos=0.9999, max_rel_l1=5e-3, min_sqnr_db=35)
+
+
 @pytest.mark.parametrize("shape", [(1, 2, 128, 64), (2, 4, 257, 64), (1, 2, 333, 128), (1, 8, 2048, 64)])
 @pytest.mark.parametrize("causal", [False, True])
 def test_end_to_end_quality(device, shape, causal):
