@@ -490,10 +490,10 @@ gemm_q4k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const uint32_t nib = (qw[e] >> (4 * hi)) & 0x0F0F0F0Fu;
-            bl[e] = (int)(nib * (sc & 7));
-            bh[e] = (int)(nib * (sc >> 3));
+            bl[e] = (int)mul_bytes(nib, sc & 7);  // <= 15 * 7 per byte
+            bh[e] = (int)mul_bytes(nib, sc >> 3);
           }
-          const int bmv = (int)(mn * 0x01010101u);
+          const int bmv = (int)__builtin_amdgcn_perm(0u, mn, 0u);  // byte 0 of mn in all four bytes
           const v4i bm = {bmv, bmv, bmv, bmv};
 #pragma unroll
           for (int rb = 0; rb < 2; ++rb) {

@@ -20,6 +20,17 @@ __device__ __forceinline__ ScMin unpack_scmin(uint32_t s0, uint32_t s1, uint32_t
 }
 __device__ __forceinline__ int byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xFF; }
 
+// Four byte lanes times one small factor, for products that stay below 256
+// per byte (no carries between bytes): one packed 16-bit multiply
+// (v_pk_mul_lo_u16, full rate) instead of a 32-bit integer multiply (quarter
+// rate); each 16-bit half holds two bytes and its product stays below 2^16.
+__device__ __forceinline__ uint32_t mul_bytes(uint32_t bytes, uint32_t f) {
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  const u16x2 a = __builtin_bit_cast(u16x2, bytes);
+  const u16x2 b = {(unsigned short)f, (unsigned short)f};
+  return __builtin_bit_cast(uint32_t, a * b);
+}
+
 typedef __attribute__((address_space(1))) const void* kq_gptr_t;
 typedef __attribute__((address_space(3))) void* kq_lptr_t;
 
