@@ -97,7 +97,14 @@ gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
 #pragma unroll
   for (int t = 0; t < MT; ++t) a_on[t] = a_side && (t * 8 + a_m < M);
   // per-wave area rounded up to whole 1 KiB copies (a copy writes 64 x 16 B)
-  int8_t* xw = xl + (int64_t)wave * ((M * GXPITCH + 1023) & ~1023);
+  // per wave: M activation rows rounded up to whole 1 KiB copies (a copy
+  // writes 64 x 16 B, the last one past row M - 1), then one row of zeros
+  // that the lanes whose A-operand row is unused read instead (no select
+  // per operand)
+  const int xarea = (M * GXPITCH + 1023) & ~1023;
+  int8_t* xw = xl + (int64_t)wave * (xarea + GXPITCH);
+  int8_t* xz = xw + xarea;
+  for (int i = lane; i < GXPITCH / 16; i += 64) reinterpret_cast<uint4*>(xz)[i] = make_uint4(0, 0, 0, 0);
 
   float f[MT][4];
 #pragma unroll
@@ -161,10 +168,9 @@ gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
             const int sub = 4 * L + 2 * hp + nb;
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
-              const int m = min(t * 8 + a_m, M - 1);
-              const int4 xv = *reinterpret_cast<const int4*>(xw + m * GXPITCH + i * 256 + 32 * sub +
-                                                             16 * (h & 1));
-              const v4i aop = a_on[t] ? v4i{xv.x, xv.y, xv.z, xv.w} : v4i{0, 0, 0, 0};
+              const int8_t* xrow = a_on[t] ? xw + (t * 8 + a_m) * GXPITCH : xz;
+              const int4 xv = *reinterpret_cast<const int4*>(xrow + i * 256 + 32 * sub + 16 * (h & 1));
+              const v4i aop = {xv.x, xv.y, xv.z, xv.w};
               const v4i z = {0, 0, 0, 0};
               const v4i cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(aop, bop, z, 0, 0, 0);
               U[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aop, bmin, U[t], 0, 0, 0);
@@ -596,7 +602,7 @@ template <int MT>
 void launch_gemv_mt(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
                     int M, int N, int K, hipStream_t st) {
   const dim3 grid((unsigned)((N + GEMV_ROWS - 1) / GEMV_ROWS));
-  const size_t lds = (size_t)GWAVES * (((size_t)M * GXPITCH + 1023) & ~(size_t)1023);
+  const size_t lds = (size_t)GWAVES * ((((size_t)M * GXPITCH + 1023) & ~(size_t)1023) + GXPITCH);
   switch (odt) {
     case SL8_DTYPE_F16:
       gemv_q4k_kernel<SL8_DTYPE_F16, MT><<<grid, 64 * GWAVES, lds, st>>>(x, xs, w, out, M, N, K);
