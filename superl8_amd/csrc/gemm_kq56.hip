@@ -713,9 +713,16 @@ void launch_gemv_kq_m(const int8_t* x, const float* xs, const uint8_t* w, void* 
   }
 }
 
+#ifndef SL8_Q5_MFMA
+#define SL8_Q5_MFMA 1
+#endif
 template <int FMT>
 void launch_gemv_kq(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
                     int M, int N, int K, hipStream_t st) {
+  if (FMT == 5 && SL8_Q5_MFMA && M >= 3) {  // Q5_K on the int8 MFMA GEMV of gemm_q4k.hip
+    launch_gemv_q5k_mfma(x, xs, w, out, odt, M, N, K, st);
+    return;
+  }
   if (M == 1) launch_gemv_kq_m<FMT, 1>(x, xs, w, out, odt, M, N, K, st);
   else if (M == 2) launch_gemv_kq_m<FMT, 2>(x, xs, w, out, odt, M, N, K, st);
   else if (M <= 4) launch_gemv_kq_m<FMT, 4>(x, xs, w, out, odt, M, N, K, st);

@@ -73,8 +73,13 @@ __device__ __forceinline__ uint32_t lane_pull(uint32_t v, int src_lane) {
 
 // MT = 1: at most 96 registers, so 5 waves per SIMD and every workgroup of
 // the decode shapes (N / 16 = 1088 at N = 17408) is resident at once.
-template <int OUT_DT, int MT>
-__global__ void __launch_bounds__(64 * GWAVES, MT == 1 ? 5 : 1)
+// FMT = 5: the same kernel on Q5_K super-blocks (176 bytes: header, 32 bytes of
+// 5th bits qh, then the Q4_K-style nibbles): byte l of qh holds bit j for
+// element l of sub-block j, so the operand lane of elements 16(h&1)..+15
+// pulls qh bytes 16(h&1)..+15 of its row and the B operand is the code
+// q = n + 16 b <= 31 (exact in int8); scales and mins as Q4_K.
+template <int OUT_DT, int MT, int FMT = 4>
+__global__ void __launch_bounds__(64 * GWAVES, MT == 1 ? (FMT == 4 ? 5 : 4) : 1)
 gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
                 const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K) {
   extern __shared__ __attribute__((aligned(16))) int8_t xl[];  // per wave: [M][GXPITCH]
@@ -89,7 +94,9 @@ gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
   const int lr = lane >> 2, lc = lane & 3;  // load role: weight row, 16-byte piece
   const int src_q = 4 * lj + h;             // lane holding (row lj, piece h)
   const int n0 = blockIdx.x * GEMV_ROWS;
-  const int64_t row_bytes = (int64_t)nsb * Q4K_BYTES;
+  constexpr int BB = FMT == 4 ? Q4K_BYTES : 176;  // bytes per super-block
+  constexpr int QS = FMT == 4 ? 16 : 48;          // offset of the nibbles
+  const int64_t row_bytes = (int64_t)nsb * BB;
   const uint8_t* wrow = w + (int64_t)min(n0 + lr, N - 1) * row_bytes;
   const int a_m = lj & 7;    // A-operand row: activation t*8 + a_m, parity lj >> 3
   const bool a_side = (lj >> 3) == hp;  // this lane's k-slots feed its A row
@@ -117,12 +124,14 @@ gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
     // ---- weights: header dword lc and two 16-byte nibble pieces per super-block ----
     uint32_t hd[GCH];
     uint4 qa[GCH], qb[GCH];
+    uint2 qh8[FMT == 5 ? GCH : 1];  // Q5_K: qh bytes 8 lc .. 8 lc + 7 of the row
 #pragma unroll
     for (int i = 0; i < GCH; ++i) {
-      const uint8_t* blk = wrow + (int64_t)min(c0 + i, nsb - 1) * Q4K_BYTES;
+      const uint8_t* blk = wrow + (int64_t)min(c0 + i, nsb - 1) * BB;
       hd[i] = *reinterpret_cast<const uint32_t*>(blk + 4 * lc);
-      qa[i] = *reinterpret_cast<const uint4*>(blk + 16 + 16 * lc);
-      qb[i] = *reinterpret_cast<const uint4*>(blk + 80 + 16 * lc);
+      qa[i] = *reinterpret_cast<const uint4*>(blk + QS + 16 * lc);
+      qb[i] = *reinterpret_cast<const uint4*>(blk + QS + 64 + 16 * lc);
+      if constexpr (FMT == 5) qh8[i] = *reinterpret_cast<const uint2*>(blk + 16 + 8 * lc);
     }
     // ---- activations of the chunk: M rows x cnt*256 bytes -> this wave's LDS area ----
     const int xch = M * (GXPITCH / 16);
@@ -145,6 +154,14 @@ gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
         qw[1][0] = lane_pull(qb[i].x, src_q); qw[1][1] = lane_pull(qb[i].y, src_q);
         qw[1][2] = lane_pull(qb[i].z, src_q); qw[1][3] = lane_pull(qb[i].w, src_q);
         const ScMin sm = unpack_scmin(h1, h2, h3);
+        uint32_t qhw[4] = {0, 0, 0, 0};  // Q5_K: qh bytes 16(h&1) .. +15 of row lj
+        if constexpr (FMT == 5) {
+          const int s0 = 4 * lj + 2 * (h & 1);
+          qhw[0] = lane_pull(qh8[i].x, s0);
+          qhw[1] = lane_pull(qh8[i].y, s0);
+          qhw[2] = lane_pull(qh8[i].x, s0 + 1);
+          qhw[3] = lane_pull(qh8[i].y, s0 + 1);
+        }
         int T[MT][4];
         v4i U[MT];
 #pragma unroll
@@ -158,14 +175,19 @@ gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
 #pragma unroll
           for (int nb = 0; nb < 2; ++nb) {
             const int sh = 4 * nb;
-            const v4i bop = {(int)((qw[L][0] >> sh) & 0x0F0F0F0Fu), (int)((qw[L][1] >> sh) & 0x0F0F0F0Fu),
-                             (int)((qw[L][2] >> sh) & 0x0F0F0F0Fu), (int)((qw[L][3] >> sh) & 0x0F0F0F0Fu)};
             // sub-block 4L + 2hp + nb of this column's row
+            const int sub = 4 * L + 2 * hp + nb;
+            v4i bop;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              uint32_t c = (qw[L][e] >> sh) & 0x0F0F0F0Fu;
+              if constexpr (FMT == 5) c |= ((qhw[e] >> sub) & 0x01010101u) << 4;
+              bop[e] = (int)c;
+            }
             const int bsel = 8 * (2 * hp + nb);
             const int sc = ((L == 0 ? sm.sc_lo : sm.sc_hi) >> bsel) & 0xFF;
             const uint32_t mn = (((L == 0 ? sm.mn_lo : sm.mn_hi) >> bsel) & 0xFF) * 0x01010101u;
             const v4i bmin = {(int)mn, (int)mn, (int)mn, (int)mn};
-            const int sub = 4 * L + 2 * hp + nb;
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
               const int8_t* xrow = a_on[t] ? xw + (t * 8 + a_m) * GXPITCH : xz;
@@ -617,6 +639,22 @@ void launch_gemv_mt(const int8_t* x, const float* xs, const uint8_t* w, void* ou
 }
 
 }  // namespace
+
+// Q5_K decode GEMV (3 <= M <= 16) on the MFMA kernel above (called from gemm_kq56.hip).
+void launch_gemv_q5k_mfma(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
+                          int M, int N, int K, hipStream_t st) {
+  const dim3 grid((unsigned)((N + GEMV_ROWS - 1) / GEMV_ROWS));
+  const size_t lds = (size_t)GWAVES * ((((size_t)M * GXPITCH + 1023) & ~(size_t)1023) + GXPITCH);
+#define SL8_Q5M(MT)                                                                                   \
+  switch (odt) {                                                                                      \
+    case SL8_DTYPE_F16: gemv_q4k_kernel<SL8_DTYPE_F16, MT, 5><<<grid, 64 * GWAVES, lds, st>>>(x, xs, w, out, M, N, K); break; \
+    case SL8_DTYPE_BF16: gemv_q4k_kernel<SL8_DTYPE_BF16, MT, 5><<<grid, 64 * GWAVES, lds, st>>>(x, xs, w, out, M, N, K); break; \
+    default: gemv_q4k_kernel<SL8_DTYPE_F32, MT, 5><<<grid, 64 * GWAVES, lds, st>>>(x, xs, w, out, M, N, K); break; \
+  }
+  if (M <= 8) { SL8_Q5M(1) } else { SL8_Q5M(2) }
+#undef SL8_Q5M
+}
+
 }  // namespace sl8
 
 namespace sl8 {
