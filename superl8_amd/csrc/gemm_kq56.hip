@@ -713,6 +713,197 @@ void launch_gemv_kq_m(const int8_t* x, const float* xs, const uint8_t* w, void* 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Q6_K decode GEMV for 3 <= M <= 16 on the int8 MFMA (v_mfma_i32_16x16x64_i8).
+// For ql half hf and nibble nb, the 16 k-slots of lane group h of one MFMA
+// are exactly one 16-element sub-block: elements 128 hf + 64 nb + 16 h + 0..15
+// (quadrant (h >> 1) + 2 nb, half-quadrant h & 1), with scale index
+// 8 hf + 4 nb + h. A-operand row i = 4 g + mm carries activation row mm (of
+// a block of 4) on the k-slots of group g only (zeros elsewhere), so the C
+// rows 4 g .. 4 g + 3 a lane holds are the sub-block sums of its own group
+// g = lane / 16 for 4 activation rows. B = q - 32 (6-bit codes, exact in
+// int8). 16 weight rows per workgroup, the K range split over Q6W waves of
+// up to Q6CH super-blocks; a lane 4 r + c loads 16-byte piece c of each
+// 64-byte part (ql halves, qh) of weight row r. Q6_K blocks are 210 bytes,
+// so odd super-blocks start 2 bytes off a dword: pieces are read as 5
+// aligned dwords and v_alignbyte.
+// ---------------------------------------------------------------------------
+#ifndef SL8_Q6W  // measured at config 4's shape, M = 8: 8 x 3 27.6 us, 10 x 2 33.9, 5 x 4 34.3, 6 x 4 34.2
+#define SL8_Q6W 8
+#define SL8_Q6CH 3
+#endif
+constexpr int Q6W = SL8_Q6W, Q6CH = SL8_Q6CH;
+constexpr int Q6XP = Q6CH * 256;  // LDS bytes per activation row and wave
+
+__device__ __forceinline__ uint32_t q6_pull(uint32_t v, int src_lane) {
+  return (uint32_t)__builtin_amdgcn_ds_bpermute(src_lane << 2, (int)v);
+}
+// 16 bytes at a 2-byte aligned address (shift 0 or 2 from its aligned dword)
+__device__ __forceinline__ uint4 load16_a2(const uint8_t* p, uint32_t sh) {
+  const uint32_t* a = reinterpret_cast<const uint32_t*>(reinterpret_cast<uintptr_t>(p) & ~(uintptr_t)3);
+  const u32x4a d = *reinterpret_cast<const u32x4a*>(a);
+  const uint32_t e = a[4];
+  return make_uint4(__builtin_amdgcn_alignbyte(d.y, d.x, sh), __builtin_amdgcn_alignbyte(d.z, d.y, sh),
+                    __builtin_amdgcn_alignbyte(d.w, d.z, sh), __builtin_amdgcn_alignbyte(e, d.w, sh));
+}
+
+template <int OUT_DT, int MB>  // MB blocks of 4 activation rows
+__global__ void __launch_bounds__(64 * Q6W)
+gemv_q6k_mfma_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
+                     const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K) {
+  extern __shared__ __attribute__((aligned(16))) int8_t xq6[];  // per wave: M rows + a zero row
+  __shared__ float red6[Q6W - 1][MB][16][4];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nsb = K >> 8;
+  const int lj = lane & 15, h = lane >> 4;   // operand column / k-group (= C-row group)
+  const int lr = lane >> 2, lc = lane & 3;   // load role: weight row, 16-byte piece
+  const int n0 = blockIdx.x * 16;
+  const int64_t row_bytes = (int64_t)nsb * Q6K_BYTES;
+  const uint8_t* wrow = w + (int64_t)min(n0 + lr, N - 1) * row_bytes;
+  const int gA = lj >> 2, mA = lj & 3;       // A row lj = 4 gA + mA
+  const int xarea = (M * Q6XP + 1023) & ~1023;
+  int8_t* xw = xq6 + (int64_t)wave * (xarea + Q6XP);
+  int8_t* xz = xw + xarea;                   // zero row
+  for (int i = lane; i < Q6XP / 16; i += 64) reinterpret_cast<uint4*>(xz)[i] = make_uint4(0, 0, 0, 0);
+  const int8_t* xrow[MB];
+#pragma unroll
+  for (int t = 0; t < MB; ++t) xrow[t] = (gA == h && 4 * t + mA < M) ? xw + (4 * t + mA) * Q6XP : xz;
+
+  float f[MB][4];
+#pragma unroll
+  for (int t = 0; t < MB; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) f[t][r] = 0.f;
+
+  auto chunk = [&](const int c0, const int cnt) {
+    uint4 qlp[Q6CH][2], qhp[Q6CH];
+    uint32_t scw[Q6CH], dw[Q6CH];
+#pragma unroll
+    for (int i = 0; i < Q6CH; ++i) {
+      const int sb = min(c0 + i, nsb - 1);
+      const uint8_t* blk = wrow + (int64_t)sb * Q6K_BYTES;
+      const uint32_t sh = (uint32_t)(reinterpret_cast<uintptr_t>(blk) & 3);
+      qlp[i][0] = load16_a2(blk + 16 * lc, sh);
+      qlp[i][1] = load16_a2(blk + 64 + 16 * lc, sh);
+      qhp[i] = load16_a2(blk + 128 + 16 * lc, sh);
+      const uint32_t* sp = reinterpret_cast<const uint32_t*>(reinterpret_cast<uintptr_t>(blk + 192 + 4 * lc) & ~(uintptr_t)3);
+      scw[i] = __builtin_amdgcn_alignbyte(sp[1], sp[0], sh);  // scales 4 lc .. 4 lc + 3
+      const uint32_t dd = *reinterpret_cast<const uint32_t*>(reinterpret_cast<uintptr_t>(blk + 208) & ~(uintptr_t)3);
+      dw[i] = sh ? (dd >> 16) : (dd & 0xFFFFu);
+    }
+    const int xch = M * (Q6XP / 16);
+    for (int j = 0; j * 64 < xch; ++j) {
+      const int id = min(j * 64 + lane, xch - 1);
+      const int m = id / (Q6XP / 16), pos = min(id % (Q6XP / 16), cnt * 16 - 1);
+      __builtin_amdgcn_global_load_lds((kq_gptr_t)(x + (int64_t)m * K + (int64_t)c0 * 256 + 16 * pos),
+                                       (kq_lptr_t)(xw + j * 1024), 16, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+#pragma unroll
+    for (int i = 0; i < Q6CH; ++i) {
+      if (i < cnt) {
+        const float d = h2f((uint16_t)q6_pull(dw[i], 4 * lj));  // column lj's d (lane 4 lj loaded it)
+        // exact integer sums of this lane's 4 sub-blocks of the super-block:
+        // |sc * S| < 128 * 16 * 127 * 32 < 2^23 per term
+        int T[MB][4];
+#pragma unroll
+        for (int t = 0; t < MB; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) T[t][r] = 0;
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          // ql bytes 64 hf + 16 h .. +15 (piece h of half hf) and qh bytes
+          // 32 hf + 16 (h & 1) .. +15 (qh piece 2 hf + (h & 1)) of row lj
+          const uint4 qlv = hf ? qlp[i][1] : qlp[i][0];
+          uint32_t ql[4], qh[4];
+          ql[0] = q6_pull(qlv.x, 4 * lj + h); ql[1] = q6_pull(qlv.y, 4 * lj + h);
+          ql[2] = q6_pull(qlv.z, 4 * lj + h); ql[3] = q6_pull(qlv.w, 4 * lj + h);
+          const int sq = 4 * lj + 2 * hf + (h & 1);
+          qh[0] = q6_pull(qhp[i].x, sq); qh[1] = q6_pull(qhp[i].y, sq);
+          qh[2] = q6_pull(qhp[i].z, sq); qh[3] = q6_pull(qhp[i].w, sq);
+#pragma unroll
+          for (int nb = 0; nb < 2; ++nb) {
+            const int qd = (h >> 1) + 2 * nb;  // quadrant of this lane's k-slots
+            v4i bop;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const uint32_t q = ((ql[e] >> (4 * nb)) & 0x0F0F0F0Fu) | (((qh[e] >> (2 * qd)) & 0x03030303u) << 4);
+              const uint32_t tq = q ^ 0x20202020u;             // q - 32 as 6-bit two's complement
+              bop[e] = (int)(tq | ((tq & 0x20202020u) * 6u));  // sign-extended to 8 bits
+            }
+            // scale of this lane's C-row group g = h: index 8 hf + 4 nb + h,
+            // byte h of scale dword 2 hf + nb of column lj
+            const uint32_t sw = q6_pull(scw[i], 4 * lj + 2 * hf + nb);
+            const int sc = (int)(int8_t)((sw >> (8 * h)) & 0xFF);
+#pragma unroll
+            for (int t = 0; t < MB; ++t) {
+              const int4 xv = *reinterpret_cast<const int4*>(xrow[t] + i * 256 + 128 * hf + 64 * nb + 16 * gA);
+              const v4i aop = {xv.x, xv.y, xv.z, xv.w};
+              const v4i cc = __builtin_amdgcn_mfma_i32_16x16x64_i8(aop, bop, v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+              for (int r = 0; r < 4; ++r) T[t][r] += __mul24(sc, cc[r]);
+            }
+          }
+        }
+#pragma unroll
+        for (int t = 0; t < MB; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) f[t][r] += d * (float)T[t][r];
+      }
+    }
+    __builtin_amdgcn_wave_barrier();  // the next chunk's copies overwrite xw
+  };
+
+  const int sb0 = (wave * nsb) / Q6W, sb1 = ((wave + 1) * nsb) / Q6W;
+  if (sb1 - sb0 <= Q6CH) {
+    if (sb1 > sb0) chunk(sb0, sb1 - sb0);
+  } else {
+    for (int c0 = sb0; c0 < sb1; c0 += Q6CH) chunk(c0, min(Q6CH, sb1 - c0));
+  }
+  // C rows 4 g + r (g = lane / 16): sum the 4 sub-block groups, then the waves in fixed order
+#pragma unroll
+  for (int t = 0; t < MB; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      f[t][r] += __shfl_xor(f[t][r], 16, 64);
+      f[t][r] += __shfl_xor(f[t][r], 32, 64);
+    }
+  if (wave > 0 && lane < 16) {
+#pragma unroll
+    for (int t = 0; t < MB; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red6[wave - 1][t][lane][r] = f[t][r];
+  }
+  __syncthreads();
+  if (wave == 0 && lane < 16) {
+#pragma unroll
+    for (int t = 0; t < MB; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float v = f[t][r];
+#pragma unroll
+        for (int wv = 0; wv < Q6W - 1; ++wv) v += red6[wv][t][lane][r];
+        const int m = 4 * t + r, gn = n0 + lane;
+        if (m < M && gn < N) st_out<OUT_DT>(out, (int64_t)m * N + gn, v * x_scale[m]);
+      }
+  }
+}
+
+void launch_gemv_q6k_mfma(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
+                          int M, int N, int K, hipStream_t st) {
+  const dim3 grid((unsigned)((N + 15) / 16));
+  const size_t lds = (size_t)Q6W * ((((size_t)M * Q6XP + 1023) & ~(size_t)1023) + Q6XP);
+#define SL8_Q6M(MB)                                                                                   \
+  switch (odt) {                                                                                      \
+    case SL8_DTYPE_F16: gemv_q6k_mfma_kernel<SL8_DTYPE_F16, MB><<<grid, 64 * Q6W, lds, st>>>(x, xs, w, out, M, N, K); break; \
+    case SL8_DTYPE_BF16: gemv_q6k_mfma_kernel<SL8_DTYPE_BF16, MB><<<grid, 64 * Q6W, lds, st>>>(x, xs, w, out, M, N, K); break; \
+    default: gemv_q6k_mfma_kernel<SL8_DTYPE_F32, MB><<<grid, 64 * Q6W, lds, st>>>(x, xs, w, out, M, N, K); break; \
+  }
+  if (M <= 4) { SL8_Q6M(1) } else if (M <= 8) { SL8_Q6M(2) } else { SL8_Q6M(4) }
+#undef SL8_Q6M
+}
+
 #ifndef SL8_Q5_MFMA
 #define SL8_Q5_MFMA 1
 #endif
@@ -721,6 +912,13 @@ void launch_gemv_kq(const int8_t* x, const float* xs, const uint8_t* w, void* ou
                     int M, int N, int K, hipStream_t st) {
   if (FMT == 5 && SL8_Q5_MFMA && M >= 3) {  // Q5_K on the int8 MFMA GEMV of gemm_q4k.hip
     launch_gemv_q5k_mfma(x, xs, w, out, odt, M, N, K, st);
+    return;
+  }
+#ifndef SL8_Q6_MFMA
+#define SL8_Q6_MFMA 1
+#endif
+  if (FMT == 6 && SL8_Q6_MFMA && M >= 3) {
+    launch_gemv_q6k_mfma(x, xs, w, out, odt, M, N, K, st);
     return;
   }
   if (M == 1) launch_gemv_kq_m<FMT, 1>(x, xs, w, out, odt, M, N, K, st);
