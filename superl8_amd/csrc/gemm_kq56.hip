@@ -566,26 +566,16 @@ __device__ __forceinline__ float unit_dot(const UnitCodes<6>& u, const uint32_t 
   return u.d * (float)T;
 }
 
-// R weight rows per wave: with several activation rows each activation load
-// serves R weight rows.
-// XL: the M x K activations are first copied to LDS (when they fit), so the
-// workgroup's 4 R weight rows read them from LDS instead of each wave
-// re-reading them from L2 for every unit.
-template <int FMT, int OUT_DT, int MR, int R, bool XL>
+// M = 2 (M = 1 runs gemv_kq_flat_kernel, M >= 3 the MFMA kernels): one wave
+// per weight row (R rows per wave share every activation load), lanes over
+// the row's units.
+template <int FMT, int OUT_DT, int MR, int R>
 __global__ void __launch_bounds__(256)
 gemv_kq_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
                const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K) {
   constexpr int BS = FMT == 5 ? Q5K_BYTES : Q6K_BYTES;
-  extern __shared__ __attribute__((aligned(16))) int8_t x_lds[];
   const int lane = threadIdx.x & 63;
   const int n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
-  if constexpr (XL) {
-    const int nx = M * K / 16;  // K % 256 == 0
-    for (int i = threadIdx.x; i < nx; i += 256)
-      reinterpret_cast<uint4*>(x_lds)[i] = reinterpret_cast<const uint4*>(x)[i];
-    __syncthreads();
-  }
-  const int8_t* xb = XL ? x_lds : x;
   if (n0 >= N) return;  // wave-uniform
   const int nsb = K >> 8, nu = 4 * nsb;
   const int64_t row_bytes = (int64_t)nsb * BS;
@@ -605,7 +595,7 @@ gemv_kq_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
     for (int m = 0; m < MR; ++m) {
       if (m < M) {
         uint32_t xv[2][8];
-        unit_x<FMT>(xb + (int64_t)m * K + (int64_t)sb * 256, g, xv);
+        unit_x<FMT>(x + (int64_t)m * K + (int64_t)sb * 256, g, xv);
         if constexpr (FMT == 5) {
           int xs[2];  // shared by the R weight rows
           unit_xsum(xv, xs);
@@ -679,9 +669,6 @@ gemv_kq_flat_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_sc
 template <int FMT, int MR>
 void launch_gemv_kq_m(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
                       int M, int N, int K, hipStream_t st) {
-#ifndef SL8_KQ_ROWS
-#define SL8_KQ_ROWS 2  // measured: 2 rows beat 1 (x reuse) and 4 (occupancy) at M = 4..16
-#endif
   if (MR == 1) {
     constexpr int RF = FMT == 5 ? 4 : 2;  // measured at K = 5120: Q6_K's larger unit state favours 2
     const dim3 g1((unsigned)((N + 4 * RF - 1) / (4 * RF)));
@@ -692,24 +679,12 @@ void launch_gemv_kq_m(const int8_t* x, const float* xs, const uint8_t* w, void* 
     }
     return;
   }
-  constexpr int R = MR >= 4 ? SL8_KQ_ROWS : 1;
+  constexpr int R = 1;
   const dim3 grid((unsigned)((N + 4 * R - 1) / (4 * R)));
-#ifndef SL8_KQ_XLDS
-#define SL8_KQ_XLDS (48 * 1024)
-#endif
-  const size_t xbytes = (size_t)M * K;
-  if (MR >= 4 && xbytes <= SL8_KQ_XLDS) {
-    switch (odt) {
-      case SL8_DTYPE_F16: gemv_kq_kernel<FMT, SL8_DTYPE_F16, MR, R, true><<<grid, 256, xbytes, st>>>(x, xs, w, out, M, N, K); break;
-      case SL8_DTYPE_BF16: gemv_kq_kernel<FMT, SL8_DTYPE_BF16, MR, R, true><<<grid, 256, xbytes, st>>>(x, xs, w, out, M, N, K); break;
-      default: gemv_kq_kernel<FMT, SL8_DTYPE_F32, MR, R, true><<<grid, 256, xbytes, st>>>(x, xs, w, out, M, N, K); break;
-    }
-    return;
-  }
   switch (odt) {
-    case SL8_DTYPE_F16: gemv_kq_kernel<FMT, SL8_DTYPE_F16, MR, R, false><<<grid, 256, 0, st>>>(x, xs, w, out, M, N, K); break;
-    case SL8_DTYPE_BF16: gemv_kq_kernel<FMT, SL8_DTYPE_BF16, MR, R, false><<<grid, 256, 0, st>>>(x, xs, w, out, M, N, K); break;
-    default: gemv_kq_kernel<FMT, SL8_DTYPE_F32, MR, R, false><<<grid, 256, 0, st>>>(x, xs, w, out, M, N, K); break;
+    case SL8_DTYPE_F16: gemv_kq_kernel<FMT, SL8_DTYPE_F16, MR, R><<<grid, 256, 0, st>>>(x, xs, w, out, M, N, K); break;
+    case SL8_DTYPE_BF16: gemv_kq_kernel<FMT, SL8_DTYPE_BF16, MR, R><<<grid, 256, 0, st>>>(x, xs, w, out, M, N, K); break;
+    default: gemv_kq_kernel<FMT, SL8_DTYPE_F32, MR, R><<<grid, 256, 0, st>>>(x, xs, w, out, M, N, K); break;
   }
 }
 
@@ -904,28 +879,16 @@ void launch_gemv_q6k_mfma(const int8_t* x, const float* xs, const uint8_t* w, vo
 #undef SL8_Q6M
 }
 
-#ifndef SL8_Q5_MFMA
-#define SL8_Q5_MFMA 1
-#endif
 template <int FMT>
 void launch_gemv_kq(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
                     int M, int N, int K, hipStream_t st) {
-  if (FMT == 5 && SL8_Q5_MFMA && M >= 3) {  // Q5_K on the int8 MFMA GEMV of gemm_q4k.hip
-    launch_gemv_q5k_mfma(x, xs, w, out, odt, M, N, K, st);
-    return;
-  }
-#ifndef SL8_Q6_MFMA
-#define SL8_Q6_MFMA 1
-#endif
-  if (FMT == 6 && SL8_Q6_MFMA && M >= 3) {
-    launch_gemv_q6k_mfma(x, xs, w, out, odt, M, N, K, st);
+  if (M >= 3) {  // the int8 MFMA GEMVs (Q5_K: the Q4_K kernel of gemm_q4k.hip)
+    if (FMT == 5) launch_gemv_q5k_mfma(x, xs, w, out, odt, M, N, K, st);
+    else launch_gemv_q6k_mfma(x, xs, w, out, odt, M, N, K, st);
     return;
   }
   if (M == 1) launch_gemv_kq_m<FMT, 1>(x, xs, w, out, odt, M, N, K, st);
-  else if (M == 2) launch_gemv_kq_m<FMT, 2>(x, xs, w, out, odt, M, N, K, st);
-  else if (M <= 4) launch_gemv_kq_m<FMT, 4>(x, xs, w, out, odt, M, N, K, st);
-  else if (M <= 8) launch_gemv_kq_m<FMT, 8>(x, xs, w, out, odt, M, N, K, st);
-  else launch_gemv_kq_m<FMT, 16>(x, xs, w, out, odt, M, N, K, st);
+  else launch_gemv_kq_m<FMT, 2>(x, xs, w, out, odt, M, N, K, st);
 }
 
 template <int FMT>
