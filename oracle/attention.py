@@ -224,7 +224,9 @@ def attn_paged_decode(q_i8, q_scale, k_cache, k_scale, v_cache, v_scale, block_t
     per = (max_context_len + num_splits - 1) // num_splits
     out = np.zeros((B, Hq, D))
     for b in range(B):
-        n = int(context_lens[b])
+        # a context length above max_context_len counts as max_context_len (this
+        # build's contract; the reference leaves that case unchecked)
+        n = min(int(context_lens[b]), int(max_context_len))
         if n == 0:
             continue
         kb = gather_paged(k_cache, block_table, b, n)[idx]          # [Hq, n, D]

@@ -103,7 +103,9 @@ decode_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sc
 
   const int per = (n_len + n_splits - 1) / n_splits;
   const int n0 = split * per;
-  const int n1 = min(PG ? pg.ctx[b] : n_len, n0 + per);
+  // paged: a context length above max_context_len (n_len) is read as
+  // max_context_len, so no block-table entry past the table's capacity is used
+  const int n1 = min(PG ? min(pg.ctx[b], n_len) : n_len, n0 + per);
   // cache row of key n (contiguous: relative to this (batch, KV head))
   const int32_t* btb = PG ? pg.bt + (int64_t)b * pg.maxb : nullptr;
   auto krow = [&](int n) -> int64_t {
@@ -437,7 +439,9 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
   const int b = bkv / h_kv, kvh = bkv % h_kv;
   const int per = (n_len + n_splits - 1) / n_splits;
   const int n0 = split * per;
-  const int n1 = min(PG ? pg.ctx[b] : n_len, n0 + per);
+  // paged: a context length above max_context_len (n_len) is read as
+  // max_context_len, so no block-table entry past the table's capacity is used
+  const int n1 = min(PG ? min(pg.ctx[b], n_len) : n_len, n0 + per);
   const int ntiles = n1 > n0 ? (n1 - n0 + T - 1) / T : 0;
   const int nt = ntiles > wave ? (ntiles - wave + DEC_WAVES - 1) / DEC_WAVES : 0;  // this wave's
   const int8_t* kb = k + (PG ? 0 : (int64_t)bkv * n_len * D);

@@ -256,10 +256,16 @@ gemm_q6k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
     const uint8_t* wbase = w + (int64_t)n0 * row_bytes;
     const uint32_t rb32 = (uint32_t)row_bytes, sboff = (uint32_t)sb * Q6K_BYTES;
     const int rmax = min(KBN, N - n0) - 1;
+    // bytes from the row-n0 base to the end of the weight buffer: the last
+    // dword of a 4-byte aligned block (its d field plus 2 bytes past the
+    // block) is not read for the buffer's final block; compute() reads that
+    // block's d from global memory instead
+    const uint32_t wend = (uint32_t)(rmax + 1) * rb32;
 #pragma unroll
     for (int i = 0; i < (T6DW - 64) / 256; ++i) {
       const uint32_t base = (uint32_t)min(row, rmax) * rb32 + sboff;
-      const uint32_t off = (base & ~3u) + 4u * (uint32_t)(row < KBN ? c : Q6DW - 1);
+      uint32_t off = (base & ~3u) + 4u * (uint32_t)(row < KBN ? c : Q6DW - 1);
+      off = off + 4u > wend ? off - 4u : off;
       __builtin_amdgcn_global_load_lds((kq_gptr_t)(wbase + off), (kq_lptr_t)(wd + i * 256 + wave * 64), 4, 0, 0);
       c += 44;
       row += 4;
@@ -289,7 +295,12 @@ gemm_q6k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
       blk[cb] = reinterpret_cast<const uint8_t*>(wt) + r * Q6PITCH + (int)(base & 3u);
       const uint2 s0 = lds8_at(blk[cb] + 192), s1 = lds8_at(blk[cb] + 200);
       scw[cb][0] = s0.x; scw[cb][1] = s0.y; scw[cb][2] = s1.x; scw[cb][3] = s1.y;
-      dcb[cb] = h2f((uint16_t)(lds8_at(blk[cb] + 208).x & 0xFFFFu));
+      const bool tail = base + Q6K_BYTES == (uint32_t)min(KBN, N - n0) * (uint32_t)row_bytes &&
+                        (base & 3u) == 0;  // the buffer's last block, 4-byte aligned
+      const uint16_t dbits =
+          tail ? *reinterpret_cast<const uint16_t*>(w + (int64_t)n0 * row_bytes + base + 208)
+               : (uint16_t)(lds8_at(blk[cb] + 208).x & 0xFFFFu);
+      dcb[cb] = h2f(dbits);
     }
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
@@ -491,10 +502,10 @@ __device__ __forceinline__ void unit_codes(const uint8_t* blk, int g, UnitCodes<
   const uint32_t* sp = reinterpret_cast<const uint32_t*>(sa & ~(uintptr_t)3);
   const uint32_t ssh = (uint32_t)(sa & 3);
   const uint32_t s0w = __builtin_amdgcn_alignbyte(sp[1], sp[0], ssh);  // scales 8hf + 0..3
-  const uint32_t s1w = __builtin_amdgcn_alignbyte(sp[2], sp[1], ssh);  // scales 8hf + 4..7
-  const uintptr_t da = reinterpret_cast<uintptr_t>(blk + 208);
-  const uint32_t dw = *reinterpret_cast<const uint32_t*>(da & ~(uintptr_t)3);
-  u.d = h2f((uint16_t)((da & 3) ? (dw >> 16) : (dw & 0xFFFFu)));
+  // (sp[2] only when the scales are misaligned: for an aligned block it lies
+  // past the block's end)
+  const uint32_t s1w = __builtin_amdgcn_alignbyte(sp[ssh ? 2 : 1], sp[1], ssh);  // scales 8hf + 4..7
+  u.d = h2f(*reinterpret_cast<const uint16_t*>(blk + 208));
   u.sc[0][0] = (int)(int8_t)byte_of(s0w, 2 * p);
   u.sc[0][1] = (int)(int8_t)byte_of(s0w, 2 * p + 1);
   u.sc[1][0] = (int)(int8_t)byte_of(s1w, 2 * p);
@@ -763,9 +774,10 @@ gemv_q6k_mfma_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
       qlp[i][1] = load16_a2(blk + 64 + 16 * lc, sh);
       qhp[i] = load16_a2(blk + 128 + 16 * lc, sh);
       const uint32_t* sp = reinterpret_cast<const uint32_t*>(reinterpret_cast<uintptr_t>(blk + 192 + 4 * lc) & ~(uintptr_t)3);
-      scw[i] = __builtin_amdgcn_alignbyte(sp[1], sp[0], sh);  // scales 4 lc .. 4 lc + 3
-      const uint32_t dd = *reinterpret_cast<const uint32_t*>(reinterpret_cast<uintptr_t>(blk + 208) & ~(uintptr_t)3);
-      dw[i] = sh ? (dd >> 16) : (dd & 0xFFFFu);
+      // sp[1] only when misaligned (aligned: it lies past the block for lc = 3);
+      // d by a 16-bit load (2-byte aligned), never past the block
+      scw[i] = __builtin_amdgcn_alignbyte(sp[sh ? 1 : 0], sp[0], sh);  // scales 4 lc .. 4 lc + 3
+      dw[i] = *reinterpret_cast<const uint16_t*>(blk + 208);
     }
     const int xch = M * (Q6XP / 16);
     for (int j = 0; j * 64 < xch; ++j) {

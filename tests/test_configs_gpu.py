@@ -1,0 +1,93 @@
+"""GPU parity at the benchmark configurations' own shapes.
+
+* config 1: attn_int8_fwd B1 H8 S512 D64 causal, the whole output against the oracle.
+* config 5: attn_w8a8_fwd B2 Hq16 Hkv2 S8192 D256 causal, 1% of the head-dim
+  channels of Q and K scaled by 20, accuracy gate bypassed. The full kernel
+  runs; query blocks of several heads (first, middle and last blocks, both
+  batches and both KV heads) are compared with the oracle against all their
+  keys. At this shape the outlier rows move their softmax reference point
+  several times (the lazy rescale), which only long rows with large outliers
+  exercise. Reference test: tests/test_attn_fwd_w8a8_outliers.py.
+"""
+import numpy as np
+import pytest
+import torch
+
+import superl8_amd as sl8
+from oracle import attention as oa
+from superl8_amd import _C, quant
+from tests.tolerances import assert_close_abs, assert_finite, assert_int8_quality
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(x):
+    return x.detach().cpu().numpy()
+
+
+def test_config1_prefill_full_shape(device):
+    torch.manual_seed(1)
+    q = torch.randn(1, 8, 512, 64, device=device, dtype=torch.float16)
+    k = torch.randn(1, 8, 512, 64, device=device, dtype=torch.float16)
+    v = torch.randn(1, 8, 512, 64, device=device, dtype=torch.float16)
+    q_i8, qs, k_i8, ks, _ = quant.quantize_qk(q, k)
+    qs, ks = qs.squeeze(-1).contiguous(), ks.squeeze(-1).contiguous()
+    out = _C.attn_int8_fwd(q_i8, qs, k_i8, ks, v, True)
+    ref, _ = oa.attn_int8_fwd(_np(q_i8), _np(qs), _np(k_i8), _np(ks), _np(v.float()), True)
+    assert_finite(out)
+    assert_close_abs(out, ref, atol=1e-2, what="config 1 vs oracle")
+    assert_int8_quality(out, ref, min_cos=0.9999, max_rel_l1=3e-3, min_sqnr_db=40)
+    # public API (prologue + kernel) vs fp32 attention: the reference's int8 gate
+    pub = sl8.attn_int8_fwd(q, k, v, causal=True)
+    fp = oa.attention_fp64(_np(q.float()), _np(k.float()), _np(v.float()), True)
+    assert_int8_quality(pub, fp, what="config 1 public API vs fp attention")
+
+
+def _config5_inputs(device):
+    B, Hq, Hkv, S, D = 2, 16, 2, 8192, 256
+    g = torch.Generator(device="cpu").manual_seed(5)
+    idx = torch.randperm(D, generator=g)[:3]  # 1% of 256 channels
+    torch.manual_seed(5)
+    q = torch.randn(B, Hq, S, D, device=device, dtype=torch.float16)
+    k = torch.randn(B, Hkv, S, D, device=device, dtype=torch.float16)
+    v = torch.randn(B, Hkv, S, D, device=device, dtype=torch.float16)
+    q[..., idx] *= 20
+    k[..., idx] *= 20
+    return q, k, v
+
+
+# (batch, query head, first query row) of the 64-row blocks compared
+C5_BLOCKS = [(0, 0, 0), (0, 3, 4096), (0, 9, 8128), (1, 8, 2048), (1, 15, 6080), (1, 1, 8128)]
+
+
+@pytest.mark.parametrize("per_warp", [True, False])
+def test_config5_w8a8_full_shape(device, per_warp):
+    q, k, v = _config5_inputs(device)
+    Hq, Hkv = q.shape[1], k.shape[1]
+    gsz = Hq // Hkv
+    q_i8, qs, k_i8, ks, _ = quant.quantize_qk(q, k)
+    qs, ks = qs.squeeze(-1).contiguous(), ks.squeeze(-1).contiguous()
+    v_i8, vs = _C.quantize_v_perchannel(v)
+    vs = vs.squeeze(-2).contiguous()
+    out = _C.attn_w8a8_fwd(q_i8, qs, k_i8, ks, v_i8, vs, True, 0, per_warp)
+    assert_finite(out)
+    # the public API with the gate bypassed runs the same kernel
+    if per_warp:
+        pub = sl8.attn_int8_fwd(q, k, v, causal=True, int8_pv=True, internal_accuracy_gate=False)
+        assert torch.equal(pub, out)
+    del q, k, v
+    outs, refs = [], []
+    for b, h, r0 in C5_BLOCKS:
+        kv = h // gsz
+        sl = slice(r0, r0 + 64)
+        # the block sees keys <= r0 + i (M = N, bottom-right causal)
+        ref = oa.attn_w8a8_fwd(_np(q_i8[b:b + 1, h:h + 1, sl]), _np(qs[b:b + 1, h:h + 1, sl]),
+                               _np(k_i8[b:b + 1, kv:kv + 1]), _np(ks[b:b + 1, kv:kv + 1]),
+                               _np(v_i8[b:b + 1, kv:kv + 1]), _np(vs[b:b + 1, kv:kv + 1]),
+                               True, r0, per_warp)
+        got = out[b:b + 1, h:h + 1, sl]
+        assert_close_abs(got, ref, atol=2e-2, what=f"config 5 block {(b, h, r0)}")
+        outs.append(_np(got.float()))
+        refs.append(ref)
+    assert_int8_quality(np.concatenate(outs), np.concatenate(refs), min_cos=0.9999,
+                        max_rel_l1=5e-3, min_sqnr_db=35, what="config 5 blocks vs oracle")

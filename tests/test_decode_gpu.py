@@ -197,6 +197,30 @@ def test_paged_kernel_matches_oracle(device, case, ns):
     assert_close_abs(out[:, :, 0], ref, atol=2e-3, rtol=2e-3, what=f"paged {case} ns={ns}")
 
 
+@pytest.mark.parametrize("ns", [-1, 3])
+def test_paged_context_above_max_is_clamped(device, ns):
+    """context_lens[b] > max_context_len: keys past max_context_len (and the
+    block-table entries behind them) are never read; the row decodes as if
+    its length were max_context_len."""
+    case = (2, 8, 2, 64, 16, (64, 40))
+    B, Hq, Hkv, D, bs, lens = case
+    q, qs, kc, ks, vc, vs, bt, ctx = _paged_cache(case, device)
+    nmax = 40
+    ctx_big = torch.tensor([64, 40], dtype=torch.int32, device=device)
+    # row 0's keys 40..63 (which the clamp must leave out) would change the result
+    ref64 = oa.attn_paged_decode(_np(q)[:, :, 0], _np(qs)[:, :, 0], _np(kc), _np(ks), _np(vc),
+                                 _np(vs), _np(bt), np.array([64, 40]), 64, 1)
+    out = _C.attn_paged_decode(q, qs, kc, ks, vc, vs, bt, ctx_big, bs, nmax, ns)
+    n_splits = ns if ns > 0 else _C.paged_choose_n_splits(nmax, B * Hq)
+    ref = oa.attn_paged_decode(_np(q)[:, :, 0], _np(qs)[:, :, 0], _np(kc), _np(ks), _np(vc),
+                               _np(vs), _np(bt), _np(ctx_big), nmax, n_splits)
+    ref40 = oa.attn_paged_decode(_np(q)[:, :, 0], _np(qs)[:, :, 0], _np(kc), _np(ks), _np(vc),
+                                 _np(vs), _np(bt), np.array([40, 40]), nmax, n_splits)
+    np.testing.assert_array_equal(ref, ref40)
+    assert np.abs(ref64[0] - ref40[0]).max() > 1e-2
+    assert_close_abs(out[:, :, 0], ref, atol=2e-3, rtol=2e-3, what="paged clamp")
+
+
 @pytest.mark.parametrize("D", [64, 128, 256])
 def test_kv_write_paged_bit_exact(device, D):
     B, Hkv, nblk, bs = 3, 4, 5, 8

@@ -62,7 +62,10 @@ def test_tile_gemm_matches_exact_sum(device, fmt, M, N, K, odt):
 
 
 DEC_SHAPES = [(1, 4096, 3072), (1, 130, 256), (2, 4096, 5120), (4, 512, 768), (8, 17408, 5120),
-              (16, 1000, 2048), (3, 33, 768), (1, 64, 16384)]
+              (16, 1000, 2048), (3, 33, 768), (1, 64, 16384),
+              # long K: the M >= 3 MFMA kernels loop over several super-block
+              # chunks per wave (K > 5120 for Q5_K, K > 6144 for Q6_K)
+              (3, 40, 17408), (8, 256, 17408), (16, 130, 12544), (9, 64, 8192), (12, 96, 6400)]
 
 
 @pytest.mark.parametrize("odt", [torch.float16, torch.float32])

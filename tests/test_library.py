@@ -39,9 +39,23 @@ def test_version_and_error_slot():
 
 def test_decode_split_heuristic_and_workspace():
     lib = _lib.load()
-    ns = lib.sl8_choose_num_splits(32768, 16, 8)
-    assert 1 <= ns <= 256
-    assert lib.sl8_choose_num_splits(1, 1, 1) == 1
+    # This build's auto split count: one split per ~2048 / (B * Hkv) workgroups
+    # (a workgroup serves every query head of its KV head), at least 256 keys
+    # per split, 1..256. The reference counts per query head (choose_n_splits,
+    # attn_decode.cu:38-53) and picks 128 at config 3 where this picks 16; the
+    # merged output is the same softmax either way (split invariance).
+    cases = {  # (N, B, Hkv) -> splits, evaluated by hand
+        (32768, 16, 8): 16,   # config 3: 2048 / 128
+        (32768, 1, 8): 128,   # 2048 / 8 = 256, capped by N / 256 = 128
+        (4096, 1, 1): 16,     # N / 256
+        (1000, 1, 1): 4,      # ceil(1000 / 256)
+        (200000, 1, 1): 256,  # 2048 -> capped at 256
+        (100, 64, 64): 1,
+        (1, 1, 1): 1,
+        (0, 4, 4): 1,
+    }
+    for (n, b, hkv), want in cases.items():
+        assert lib.sl8_choose_num_splits(n, b, hkv) == want, (n, b, hkv)
     assert lib.sl8_attn_int8_decode_workspace(16, 32, 128, 16) >= 16 * 16 * 32 * (128 + 2) * 4
 
 
