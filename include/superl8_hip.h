@@ -171,6 +171,22 @@ int sl8_attn_int8_decode(const int8_t* q, const float* q_scale, const int8_t* k,
                          int64_t num_splits, void* workspace, size_t workspace_bytes,
                          void* stream);
 
+/* Allocation-free split-KV decode. No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc). Same arguments, checks,
+ * kernels and results as sl8_attn_int8_decode, minus the workspace: the
+ * per-split partials live in a static device array of
+ * sl8_attn_int8_decode_noalloc_max_bytes() bytes (8 MiB) per device, looked up
+ * on the first call on each device and held until the process ends. A call
+ * whose partials (sl8_attn_int8_decode_workspace bytes) exceed it fails with
+ * an error. Calls that overlap on one device share the array and race. Calls
+ * no hipMalloc/hipFree. */
+size_t sl8_attn_int8_decode_noalloc_max_bytes(void);
+int sl8_attn_int8_decode_noalloc(const int8_t* q, const float* q_scale, const int8_t* k,
+                                 const float* k_scale, const void* v, void* out, int64_t B,
+                                 int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                                 int64_t num_splits, void* stream);
+
 /* Split-KV decode over an int8 V cache: v int8 [B,Hkv,N,D] with per-channel
  * v_scale fp32 [B,Hkv,D], folded into each split's partial O. Otherwise as
  * sl8_attn_int8_decode (same workspace). Replaces _C.attn_int8_decode_kv8

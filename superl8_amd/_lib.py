@@ -43,6 +43,9 @@ SIGNATURES = {
     "sl8_attn_int8_decode_workspace": (_SZ, [_I64, _I64, _I64, _I64]),
     "sl8_attn_int8_decode": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
                                   _P, _SZ, _P]),
+    "sl8_attn_int8_decode_noalloc_max_bytes": (_SZ, []),
+    "sl8_attn_int8_decode_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
+                                          _I64, _P]),
     "sl8_attn_int8_decode_kv8": (_I, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
                                       _I64, _P, _SZ, _P]),
     "sl8_paged_choose_num_splits": (_I, [_I64, _I64]),

@@ -20,6 +20,7 @@
 //     state and are merged by LSE in LDS at the end (fixed order, so results
 //     are deterministic).
 
+#include <mutex>
 #include <type_traits>
 
 #include "common.hpp"
@@ -870,6 +871,75 @@ extern "C" int sl8_attn_int8_decode(const int8_t* q, const float* q_scale, const
                 "fni8 decode: workspace needs %zu bytes", need);
   return decode_launch<false>(q, q_scale, k, k_scale, v, nullptr, out, B, Hq, Hkv, N, D,
                               num_splits, workspace, static_cast<hipStream_t>(stream));
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free split-KV decode: the per-split partials (O, m, l) live in a
+// file-scope device array instead of a caller workspace, for callers that may
+// not allocate device memory (HIP graph capture, serving loops). Each device
+// holds its own copy of the array; its address is looked up once per device
+// with hipGetSymbolAddress (the array's name is a host-side stand-in, never a
+// device address) and kept in noalloc_scratch_ptr[]. Every call on a device
+// shares that device's array: calls that overlap on one device (different
+// streams, or other host threads) race on it. The decode kernels write every
+// partial they merge (empty splits write the m = -1e30 sentinel), so nothing
+// has to start at zero.
+// ---------------------------------------------------------------------------
+namespace sl8 {
+namespace {
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)8 << 20;
+constexpr int NOALLOC_MAX_DEVICES = 64;
+__device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+void* noalloc_scratch_ptr[NOALLOC_MAX_DEVICES];
+std::mutex noalloc_mu;
+
+int noalloc_scratch(void** out) {
+  int dev = -1;
+  const hipError_t e0 = hipGetDevice(&dev);
+  SL8_CHECK_ARG(e0 == hipSuccess, "fni8 decode_noalloc: hipGetDevice failed: %s", hipGetErrorString(e0));
+  SL8_CHECK_ARG(dev >= 0 && dev < NOALLOC_MAX_DEVICES, "fni8 decode_noalloc: device %d out of range",
+                dev);
+  std::lock_guard<std::mutex> lock(noalloc_mu);
+  if (!noalloc_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e1 = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    SL8_CHECK_ARG(e1 == hipSuccess, "fni8 decode_noalloc: hipGetSymbolAddress(scratch) failed: %s",
+                  hipGetErrorString(e1));
+    SL8_CHECK_ARG(p != nullptr, "fni8 decode_noalloc: no device address for the scratch array");
+    noalloc_scratch_ptr[dev] = p;
+  }
+  *out = noalloc_scratch_ptr[dev];
+  return SL8_OK;
+}
+}  // namespace
+}  // namespace sl8
+
+extern "C" size_t sl8_attn_int8_decode_noalloc_max_bytes(void) { return NOALLOC_SCRATCH_BYTES; }
+
+extern "C" int sl8_attn_int8_decode_noalloc(const int8_t* q, const float* q_scale, const int8_t* k,
+                                            const float* k_scale, const void* v, void* out,
+                                            int64_t B, int64_t Hq, int64_t Hkv, int64_t N,
+                                            int64_t D, int64_t num_splits, void* stream) {
+  clear_error();
+  // same checks and split choice as sl8_attn_int8_decode; the partials must
+  // fit the scratch array
+  SL8_CHECK_ARG(B >= 0 && Hq >= 0 && Hkv > 0 && N >= 0, "fni8 decode: bad shape");
+  SL8_CHECK_ARG(D == 64 || D == 128 || D == 256, "fni8 decode: head dim must be 64/128/256, got %lld",
+                (long long)D);
+  int64_t ns = num_splits < 0 ? (Hkv > 0 ? sl8_choose_num_splits(N, B, Hkv) : 1) : num_splits;
+  SL8_CHECK_ARG(ns >= 1 && ns <= DEC_MAX_SPLITS, "fni8 decode: num_splits must be 1..%d, got %lld",
+                DEC_MAX_SPLITS, (long long)ns);
+  const size_t need = sl8_attn_int8_decode_workspace(B, Hq, D, ns);
+  SL8_CHECK_ARG(need <= NOALLOC_SCRATCH_BYTES,
+                "fni8 decode_noalloc: partials need %zu bytes, above the %zu-byte scratch array "
+                "(fewer splits or a smaller batch; or sl8_attn_int8_decode with a workspace)",
+                need, NOALLOC_SCRATCH_BYTES);
+  if (B == 0 || Hq == 0) return SL8_OK;
+  void* ws = nullptr;
+  const int rc = noalloc_scratch(&ws);
+  if (rc) return rc;
+  return sl8_attn_int8_decode(q, q_scale, k, k_scale, v, out, B, Hq, Hkv, N, D, ns, ws,
+                              NOALLOC_SCRATCH_BYTES, stream);
 }
 
 extern "C" int sl8_attn_int8_decode_kv8(const int8_t* q, const float* q_scale, const int8_t* k,
