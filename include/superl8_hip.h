@@ -120,9 +120,13 @@ int sl8_quantize_i8_cols(const void* x, int dtype, int64_t G, int64_t N, int64_t
  *   out [B,Hq,M,D] (v_dtype), lse fp32 [B,Hq,M] natural log or NULL.
  *   causal: bottom-right aligned (query i sees keys <= i + N - M).
  *   window_left >= 0: also require key > i + N - M - window_left.
- *   D in {64, 128}. workspace: sl8_attn_int8_fwd_workspace() bytes (V^T staging).
+ *   D in {32, 64, 72, 80, 128, 256} (reference attn_int8_fwd.cu:138). V is
+ *   read in place; D = 32, 72, 80 run the 64- or 128-wide kernel on Q/K/V
+ *   copies zero-padded in the workspace (sl8_attn_int8_fwd_workspace() bytes,
+ *   0 for the other head dims).
  * ---------------------------------------------------------------------- */
-size_t sl8_attn_int8_fwd_workspace(int64_t B, int64_t Hkv, int64_t N, int64_t D);
+size_t sl8_attn_int8_fwd_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N,
+                                   int64_t D);
 int sl8_attn_int8_fwd(const int8_t* q, const float* q_scale, const int8_t* k,
                       const float* k_scale, const void* v, int v_dtype, void* out,
                       float* lse, int64_t B, int64_t Hq, int64_t Hkv, int64_t M,
@@ -143,9 +147,11 @@ int sl8_attn_int8_qk_scores(const int8_t* q, const int8_t* k, int32_t* scores,
  * Replaces _C.attn_w8a8_fwd (reference csrc/fni8_api.cpp:30-33,249-255,
  * csrc/kernel/attn_w8a8_fwd.cu:76-165, csrc/include/attn_w8a8_fwd.cuh:30-444).
  *   v int8 [B,Hkv,N,D], v_scale fp32 [B,Hkv,D], causal_diag: query i sees
- *   keys <= i + causal_diag when causal. D in {64, 128, 256}.
+ *   keys <= i + causal_diag when causal. D in {32, 64, 128, 256} (reference
+ *   attn_w8a8_fwd.cu:113; D = 32 runs zero-padded to 64 in the workspace).
  * ---------------------------------------------------------------------- */
-size_t sl8_attn_w8a8_fwd_workspace(int64_t B, int64_t Hkv, int64_t N, int64_t D);
+size_t sl8_attn_w8a8_fwd_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N,
+                                   int64_t D);
 int sl8_attn_w8a8_fwd(const int8_t* q, const float* q_scale, const int8_t* k,
                       const float* k_scale, const int8_t* v, const float* v_scale,
                       void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t M,
@@ -161,7 +167,7 @@ int sl8_attn_w8a8_fwd(const int8_t* q, const float* q_scale, const int8_t* k,
  *   q int8 [B,Hq,1,D], q_scale fp32 [B,Hq] (folded), k int8 [B,Hkv,N,D],
  *   k_scale fp32 [B,Hkv,N], v fp16 [B,Hkv,N,D] -> out fp16 [B,Hq,1,D].
  *   num_splits: -1 = auto (sl8_choose_num_splits), else 1..256.
- *   D in {64, 128, 256}. workspace: sl8_attn_int8_decode_workspace() bytes.
+ *   D in {32, 64, 128, 256} (reference attn_decode.cu:195). workspace: sl8_attn_int8_decode_workspace() bytes.
  * ---------------------------------------------------------------------- */
 int sl8_choose_num_splits(int64_t N, int64_t B, int64_t Hkv);
 size_t sl8_attn_int8_decode_workspace(int64_t B, int64_t Hq, int64_t D, int64_t num_splits);

@@ -19,9 +19,14 @@ import torch
 from . import _lib
 from ._lib import call, dtype_code, stream_of
 
-_HEAD_DIMS_FWD = (64, 128, 256)
-_HEAD_DIMS_W8A8 = (64, 128, 256)
-_HEAD_DIMS_DECODE = (64, 128, 256)
+# reference csrc/kernel/attn_int8_fwd.cu:138, attn_w8a8_fwd.cu:113, attn_decode.cu:195
+_HEAD_DIMS_FWD = (32, 64, 72, 80, 128, 256)
+_HEAD_DIMS_W8A8 = (32, 64, 128, 256)
+_HEAD_DIMS_DECODE = (32, 64, 128, 256)
+
+
+def _dims_msg(dims) -> str:
+    return "/".join(str(d) for d in dims)
 DEC_MAX_SPLITS = 256
 DEC_MAX_M = 16
 Q4K_TYPE_SIZE = 144
@@ -137,11 +142,11 @@ def quantize_qk_fused(q: torch.Tensor, k: torch.Tensor, q_scale_mul: float,
     return q_i8, q_scale, k_i8, k_scale, k_mean, flag
 
 
-_GATE_HEAD_DIMS = (64, 128, 256)
+_GATE_MAX_D = 256
 
 
 def q_outlier_gate(q: torch.Tensor, ratio: float = 12.0, *, stats: bool = False):
-    """On-device outlier gate over the rows of q[..., D] (D in 64/128/256).
+    """On-device outlier gate over the rows of q[..., D] (D up to 256).
 
     Returns (flag int32 [1], stats fp32 [rows, 2] or None): flag is 1 when some
     row has max|q| / (median|q| + 1e-10) > ratio (fp32, median = lower middle
@@ -150,7 +155,7 @@ def q_outlier_gate(q: torch.Tensor, ratio: float = 12.0, *, stats: bool = False)
     _check(q.dtype in (torch.float16, torch.bfloat16, torch.float32),
            "q_outlier_gate input must be float16/bfloat16/float32")
     D = q.shape[-1]
-    _check(D in _GATE_HEAD_DIMS, f"q_outlier_gate supports D in {_GATE_HEAD_DIMS}, got {D}")
+    _check(1 <= D <= _GATE_MAX_D, f"q_outlier_gate supports head dims 1..{_GATE_MAX_D}, got {D}")
     q = q.contiguous()
     rows = q.numel() // D
     flag = torch.zeros((1,), device=q.device, dtype=torch.int32)
@@ -203,12 +208,12 @@ def _attn_fwd(q, q_scale, k, k_scale, v, causal, window_left, want_lse):
     B, H, Hkv, M, N, D = _fwd_checks(q, q_scale, k, k_scale, v)
     _check(v.dtype in (torch.float16, torch.bfloat16), "v must be float16 or bfloat16")
     _check(q_scale.numel() == B * H * M and k_scale.numel() == B * Hkv * N, "scale shape mismatch")
-    _check(D in _HEAD_DIMS_FWD, f"head dim must be one of {_HEAD_DIMS_FWD}, got {D}")
+    _check(D in _HEAD_DIMS_FWD, f"head dim must be {_dims_msg(_HEAD_DIMS_FWD)}, got {D}")
     out = torch.empty((B, H, M, D), device=v.device, dtype=v.dtype)
     lse = torch.empty((B, H, M) if want_lse else (0,), device=q.device, dtype=torch.float32)
     if M == 0 or B == 0 or H == 0:
         return out, lse
-    ws_bytes = _lib.load().sl8_attn_int8_fwd_workspace(B, Hkv, N, D)
+    ws_bytes = _lib.load().sl8_attn_int8_fwd_workspace(B, H, Hkv, M, N, D)
     ws = torch.empty((ws_bytes,), device=q.device, dtype=torch.uint8) if ws_bytes else None
     with torch.cuda.device(q.device):
         call("sl8_attn_int8_fwd", q.data_ptr(), q_scale.data_ptr(), k.data_ptr(),
@@ -259,11 +264,11 @@ def attn_w8a8_fwd(q, q_scale, k, k_scale, v, v_scale, causal=False, causal_diag=
     _contig(v_scale)
     _check(q_scale.numel() == B * H * M and k_scale.numel() == B * Hkv * N
            and v_scale.numel() == B * Hkv * D, "scale shape mismatch")
-    _check(D in _HEAD_DIMS_W8A8, f"head dim must be one of {_HEAD_DIMS_W8A8}, got {D}")
+    _check(D in _HEAD_DIMS_W8A8, f"head dim must be {_dims_msg(_HEAD_DIMS_W8A8)}, got {D}")
     out = torch.empty((B, H, M, D), device=q.device, dtype=torch.float16)
     if M == 0 or B == 0 or H == 0:
         return out
-    ws_bytes = _lib.load().sl8_attn_w8a8_fwd_workspace(B, Hkv, N, D)
+    ws_bytes = _lib.load().sl8_attn_w8a8_fwd_workspace(B, H, Hkv, M, N, D)
     ws = torch.empty((max(ws_bytes, 1),), device=q.device, dtype=torch.uint8)
     with torch.cuda.device(q.device):
         call("sl8_attn_w8a8_fwd", q.data_ptr(), q_scale.data_ptr(), k.data_ptr(),
@@ -298,7 +303,7 @@ def attn_int8_decode(q, q_scale, k, k_scale, v, num_splits=-1):
     _check(k.shape[3] == D and v.shape[3] == D and v.shape[2] == N, "decode: K/V shape mismatch")
     _check(q_scale.numel() == B * H and k_scale.numel() == B * Hkv * N,
            "decode: scale shape mismatch")
-    _check(D in _HEAD_DIMS_DECODE, f"decode: head dim must be one of {_HEAD_DIMS_DECODE}, got {D}")
+    _check(D in _HEAD_DIMS_DECODE, f"decode: head dim must be {_dims_msg(_HEAD_DIMS_DECODE)}, got {D}")
     num_splits = int(num_splits)
     _check(num_splits != 0, f"decode: num_splits=0 is invalid; use -1 for auto or 1..{DEC_MAX_SPLITS}")
     out = torch.empty((B, H, 1, D), device=v.device, dtype=torch.float16)
@@ -337,7 +342,7 @@ def attn_int8_decode_kv8(q, q_scale, k, k_scale, v, v_scale, num_splits=-1):
     _check(k.shape[3] == D and v.shape[3] == D and v.shape[2] == N, "decode_kv8: K/V shape mismatch")
     _check(q_scale.numel() == B * H and k_scale.numel() == B * Hkv * N and
            v_scale.numel() == B * Hkv * D, "decode_kv8: scale shape mismatch")
-    _check(D in _HEAD_DIMS_DECODE, f"decode_kv8: head dim must be one of {_HEAD_DIMS_DECODE}, got {D}")
+    _check(D in _HEAD_DIMS_DECODE, f"decode_kv8: head dim must be {_dims_msg(_HEAD_DIMS_DECODE)}, got {D}")
     num_splits = int(num_splits)
     _check(num_splits != 0,
            f"decode_kv8: num_splits=0 is invalid; use -1 for auto or 1..{DEC_MAX_SPLITS}")
@@ -392,7 +397,7 @@ def attn_paged_decode(q, q_scale, k_cache, k_scale, v_cache, v_scale, block_tabl
            "paged_decode: block_table must be [B, max_blocks_per_seq]")
     _check(context_lens.dim() == 1 and context_lens.shape[0] == B,
            "paged_decode: context_lens must be [B]")
-    _check(D in _HEAD_DIMS_DECODE, f"paged_decode: head dim must be one of {_HEAD_DIMS_DECODE}, got {D}")
+    _check(D in _HEAD_DIMS_DECODE, f"paged_decode: head dim must be {_dims_msg(_HEAD_DIMS_DECODE)}, got {D}")
     maxb = block_table.shape[1]
     _check(0 <= max_context_len <= maxb * bs,
            "paged_decode: max_context_len exceeds block_table capacity")
@@ -438,7 +443,7 @@ def kv_write_paged(k_new, v_new, slot_mapping, k_cache, k_scale, v_cache, v_scal
            "kv_write_paged: k_scale/v_scale must be float32")
     _check(k_scale.numel() == k_cache.numel() // D and v_scale.numel() == v_cache.numel() // D,
            "kv_write_paged: scale shape mismatch vs cache")
-    _check(D in _HEAD_DIMS_DECODE, f"kv_write_paged: head dim must be one of {_HEAD_DIMS_DECODE}, got {D}")
+    _check(D in _HEAD_DIMS_DECODE, f"kv_write_paged: head dim must be {_dims_msg(_HEAD_DIMS_DECODE)}, got {D}")
     if B == 0:
         return
     with torch.cuda.device(k_new.device):

@@ -32,11 +32,11 @@ SIGNATURES = {
     "sl8_quantize_qk": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _F, _F, _P, _P, _P, _P, _P, _P,
                              _P, _SZ, _P]),
     "sl8_quantize_i8_cols": (_I, [_P, _I, _I64, _I64, _I64, _P, _P, _P]),
-    "sl8_attn_int8_fwd_workspace": (_SZ, [_I64, _I64, _I64, _I64]),
+    "sl8_attn_int8_fwd_workspace": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64]),
     "sl8_attn_int8_fwd": (_I, [_P, _P, _P, _P, _P, _I, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
                                _I, _I64, _P, _SZ, _P]),
     "sl8_attn_int8_qk_scores": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
-    "sl8_attn_w8a8_fwd_workspace": (_SZ, [_I64, _I64, _I64, _I64]),
+    "sl8_attn_w8a8_fwd_workspace": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64]),
     "sl8_attn_w8a8_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
                                _I, _I64, _I, _P, _SZ, _P]),
     "sl8_choose_num_splits": (_I, [_I64, _I64, _I64]),

@@ -270,7 +270,8 @@ __global__ void __launch_bounds__(256)
 decode_combine_wave_kernel(const float* __restrict__ o_part, const float* __restrict__ m_part,
                            const float* __restrict__ l_part, uint16_t* __restrict__ out,
                            int n_splits, int bhq) {
-  constexpr int CPL = D / 64;
+  // D = 32: one channel per lane, lanes 32..63 idle
+  constexpr int CPL = D >= 64 ? D / 64 : 1;
   const int lane = threadIdx.x & 63;
   const int64_t hq = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (hq >= bhq) return;  // wave-uniform
@@ -299,7 +300,8 @@ decode_combine_wave_kernel(const float* __restrict__ o_part, const float* __rest
   float acc[CPL];
 #pragma unroll
   for (int e = 0; e < CPL; ++e) acc[e] = 0.f;
-  const float* ob = o_part + hq * D + CPL * lane;
+  const bool act = CPL * lane < D;
+  const float* ob = o_part + hq * D + (act ? CPL * lane : 0);
   for (int s0 = 0; s0 < n_splits; s0 += SCH) {
     // weights of splits s0 .. s0 + SCH - 1 live in register wt[s0 / 64] of lanes (s0 % 64) ..
     const int c = s0 >> 6;
@@ -331,13 +333,15 @@ decode_combine_wave_kernel(const float* __restrict__ o_part, const float* __rest
   }
   const float inv = den > 0.f ? 1.f / den : 0.f;
 #pragma unroll
-  for (int e = 0; e < CPL; ++e) out[hq * D + CPL * lane + e] = f2h_bits(den > 0.f ? acc[e] * inv : 0.f);
+  for (int e = 0; e < CPL; ++e)
+    if (act) out[hq * D + CPL * lane + e] = f2h_bits(den > 0.f ? acc[e] * inv : 0.f);
 }
 
 template <typename... A>
 void launch_combine(int D, int bhq, hipStream_t st, A... args) {
   const dim3 g((unsigned)((bhq + 3) / 4));
-  if (D == 64) decode_combine_wave_kernel<64><<<g, 256, 0, st>>>(args...);
+  if (D == 32) decode_combine_wave_kernel<32><<<g, 256, 0, st>>>(args...);
+  else if (D == 64) decode_combine_wave_kernel<64><<<g, 256, 0, st>>>(args...);
   else if (D == 128) decode_combine_wave_kernel<128><<<g, 256, 0, st>>>(args...);
   else decode_combine_wave_kernel<256><<<g, 256, 0, st>>>(args...);
 }
@@ -815,7 +819,9 @@ int decode_launch(const int8_t* q, const float* q_scale, const int8_t* k, const 
   float* mp = op + (size_t)ns * bhq * D;
   float* lp = mp + (size_t)ns * bhq;
   const dim3 grid((unsigned)ns, (unsigned)(B * Hkv), (unsigned)((gsz + G - 1) / G));
-  if ((gsz == 2 && D == 128) || gsz == 4 || gsz == 8) {
+  // D = 32 (too few channels for the streaming kernel's lane maps) takes the
+  // per-key split kernel
+  if (D != 32 && ((gsz == 2 && D == 128) || gsz == 4 || gsz == 8)) {
     const dim3 g2((unsigned)ns, (unsigned)(B * Hkv));
 #define SL8_WAVE(DD, GS, NB)                                                                     \
     decode_wave_kernel<DD, GS, NB, VI8, false><<<g2, DEC_THREADS, 0, st>>>(                    \
@@ -833,6 +839,7 @@ int decode_launch(const int8_t* q, const float* q_scale, const int8_t* k, const 
 #undef SL8_WAVE_D
 #undef SL8_WAVE
   } else switch (D) {
+    case 32: launch_d<32, VI8>(G, grid, q, q_scale, k, k_scale, v, vsc, op, mp, lp, (int)N, ns, (int)Hq, (int)Hkv, gsz, bhq, st); break;
     case 64: launch_d<64, VI8>(G, grid, q, q_scale, k, k_scale, v, vsc, op, mp, lp, (int)N, ns, (int)Hq, (int)Hkv, gsz, bhq, st); break;
     case 128: launch_d<128, VI8>(G, grid, q, q_scale, k, k_scale, v, vsc, op, mp, lp, (int)N, ns, (int)Hq, (int)Hkv, gsz, bhq, st); break;
     default: launch_d<256, VI8>(G, grid, q, q_scale, k, k_scale, v, vsc, op, mp, lp, (int)N, ns, (int)Hq, (int)Hkv, gsz, bhq, st); break;
@@ -854,7 +861,7 @@ extern "C" int sl8_attn_int8_decode(const int8_t* q, const float* q_scale, const
   clear_error();
   SL8_CHECK_ARG(B >= 0 && Hq >= 0 && Hkv > 0 && N >= 0, "fni8 decode: bad shape");
   SL8_CHECK_ARG(Hq % Hkv == 0, "fni8 decode: H_q must be divisible by H_kv (GQA)");
-  SL8_CHECK_ARG(D == 64 || D == 128 || D == 256, "fni8 decode: head dim must be 64/128/256, got %lld",
+  SL8_CHECK_ARG(D == 32 || D == 64 || D == 128 || D == 256, "fni8 decode: head dim must be 32/64/128/256, got %lld",
                 (long long)D);
   if (num_splits < 0) num_splits = sl8_choose_num_splits(N, B, Hkv);
   SL8_CHECK_ARG(num_splits >= 1 && num_splits <= DEC_MAX_SPLITS,
@@ -924,7 +931,7 @@ extern "C" int sl8_attn_int8_decode_noalloc(const int8_t* q, const float* q_scal
   // same checks and split choice as sl8_attn_int8_decode; the partials must
   // fit the scratch array
   SL8_CHECK_ARG(B >= 0 && Hq >= 0 && Hkv > 0 && N >= 0, "fni8 decode: bad shape");
-  SL8_CHECK_ARG(D == 64 || D == 128 || D == 256, "fni8 decode: head dim must be 64/128/256, got %lld",
+  SL8_CHECK_ARG(D == 32 || D == 64 || D == 128 || D == 256, "fni8 decode: head dim must be 32/64/128/256, got %lld",
                 (long long)D);
   int64_t ns = num_splits < 0 ? (Hkv > 0 ? sl8_choose_num_splits(N, B, Hkv) : 1) : num_splits;
   SL8_CHECK_ARG(ns >= 1 && ns <= DEC_MAX_SPLITS, "fni8 decode: num_splits must be 1..%d, got %lld",
@@ -950,7 +957,7 @@ extern "C" int sl8_attn_int8_decode_kv8(const int8_t* q, const float* q_scale, c
   clear_error();
   SL8_CHECK_ARG(B >= 0 && Hq >= 0 && Hkv > 0 && N >= 0, "fni8 decode_kv8: bad shape");
   SL8_CHECK_ARG(Hq % Hkv == 0, "fni8 decode_kv8: H_q must be divisible by H_kv (GQA)");
-  SL8_CHECK_ARG(D == 64 || D == 128 || D == 256, "fni8 decode_kv8: head dim must be 64/128/256, got %lld",
+  SL8_CHECK_ARG(D == 32 || D == 64 || D == 128 || D == 256, "fni8 decode_kv8: head dim must be 32/64/128/256, got %lld",
                 (long long)D);
   if (num_splits < 0) num_splits = sl8_choose_num_splits(N, B, Hkv);
   SL8_CHECK_ARG(num_splits >= 1 && num_splits <= DEC_MAX_SPLITS,
@@ -985,16 +992,17 @@ kv_write_paged_kernel(const uint16_t* __restrict__ k_new, const uint16_t* __rest
                       const int32_t* __restrict__ slot_mapping, int8_t* __restrict__ k_cache,
                       float* __restrict__ k_scale, int8_t* __restrict__ v_cache,
                       float* __restrict__ v_scale, int h_kv, int bs) {
-  constexpr int E = D / 64;  // elements per lane
+  constexpr int E = D >= 64 ? D / 64 : 1;  // elements per lane
   const int lane = threadIdx.x;
+  const bool act = lane * E < D;  // D = 32: lanes 32..63 idle
   const int64_t bh = blockIdx.x;
   const int64_t b = bh / h_kv, h = bh % h_kv;
   float kx[E], vx[E];
   float ka = 0.f, va = 0.f;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    kx[e] = h2f(k_new[bh * D + lane * E + e]);
-    vx[e] = h2f(v_new[bh * D + lane * E + e]);
+    kx[e] = act ? h2f(k_new[bh * D + lane * E + e]) : 0.f;
+    vx[e] = act ? h2f(v_new[bh * D + lane * E + e]) : 0.f;
     ka = fmaxf(ka, fabsf(kx[e]));
     va = fmaxf(va, fabsf(vx[e]));
   }
@@ -1008,7 +1016,7 @@ kv_write_paged_kernel(const uint16_t* __restrict__ k_new, const uint16_t* __rest
   const int64_t slot = slot_mapping[b];
   const int64_t row = ((slot / bs) * h_kv + h) * bs + slot % bs;
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
+  for (int e = 0; e < E && act; ++e) {
     k_cache[row * D + lane * E + e] = (int8_t)rintf(fminf(fmaxf(__fdiv_rn(kx[e], ks), -127.f), 127.f));
     v_cache[row * D + lane * E + e] = (int8_t)rintf(fminf(fmaxf(__fdiv_rn(vx[e], vs), -127.f), 127.f));
   }
@@ -1049,8 +1057,8 @@ extern "C" int sl8_attn_paged_decode(const int8_t* q, const float* q_scale, cons
                     max_blocks_per_seq >= 0,
                 "fni8 paged_decode: bad shape");
   SL8_CHECK_ARG(Hq % Hkv == 0, "fni8 paged_decode: H_q must be divisible by H_kv (GQA)");
-  SL8_CHECK_ARG(D == 64 || D == 128 || D == 256,
-                "fni8 paged_decode: head dim must be 64/128/256, got %lld", (long long)D);
+  SL8_CHECK_ARG(D == 32 || D == 64 || D == 128 || D == 256,
+                "fni8 paged_decode: head dim must be 32/64/128/256, got %lld", (long long)D);
   SL8_CHECK_ARG(max_context_len >= 0 && max_context_len <= max_blocks_per_seq * block_size,
                 "fni8 paged_decode: max_context_len exceeds block_table capacity");
   SL8_CHECK_ARG(B * Hq < (1LL << 31) && num_blocks * Hkv * block_size < (1LL << 40) &&
@@ -1083,7 +1091,7 @@ extern "C" int sl8_attn_paged_decode(const int8_t* q, const float* q_scale, cons
   const PagedArgs pg{block_table, context_lens, (int)max_blocks_per_seq, (int)block_size, bs_sh};
   const int nmax = (int)max_context_len;
   const int64_t per = (max_context_len + ns - 1) / ns;
-  const bool stream_ok = pow2 && per / block_size + 2 <= DEC_BT_MAX &&
+  const bool stream_ok = D != 32 && pow2 && per / block_size + 2 <= DEC_BT_MAX &&
                          ((gsz == 2 && D == 128) || gsz == 4 || gsz == 8);
   if (stream_ok) {
     const dim3 g2((unsigned)ns, (unsigned)(B * Hkv));
@@ -1106,7 +1114,8 @@ extern "C" int sl8_attn_paged_decode(const int8_t* q, const float* q_scale, cons
 #define SL8_PAGED(DD)                                                                          \
     launch_d<DD, true, true>(G, grid, q, q_scale, k_cache, k_scale, v_cache, v_scale, op, mp, lp, \
                              nmax, ns, (int)Hq, (int)Hkv, gsz, ibhq, st, pg)
-    if (D == 64) SL8_PAGED(64);
+    if (D == 32) SL8_PAGED(32);
+    else if (D == 64) SL8_PAGED(64);
     else if (D == 128) SL8_PAGED(128);
     else SL8_PAGED(256);
 #undef SL8_PAGED
@@ -1124,8 +1133,8 @@ extern "C" int sl8_kv_write_paged(const void* k_new, const void* v_new, const in
   clear_error();
   SL8_CHECK_ARG(B >= 0 && Hkv > 0 && num_blocks >= 0 && block_size > 0,
                 "fni8 kv_write_paged: bad shape");
-  SL8_CHECK_ARG(D == 64 || D == 128 || D == 256,
-                "fni8 kv_write_paged: head dim must be 64/128/256, got %lld", (long long)D);
+  SL8_CHECK_ARG(D == 32 || D == 64 || D == 128 || D == 256,
+                "fni8 kv_write_paged: head dim must be 32/64/128/256, got %lld", (long long)D);
   if (B == 0) return SL8_OK;
   SL8_CHECK_ARG(k_new && v_new && slot_mapping && k_cache && k_scale && v_cache && v_scale,
                 "fni8 kv_write_paged: null pointer");
@@ -1133,7 +1142,8 @@ extern "C" int sl8_kv_write_paged(const void* k_new, const void* v_new, const in
   const dim3 grid((unsigned)(B * Hkv));
   const uint16_t* kn = static_cast<const uint16_t*>(k_new);
   const uint16_t* vn = static_cast<const uint16_t*>(v_new);
-  if (D == 64) kv_write_paged_kernel<64><<<grid, 64, 0, st>>>(kn, vn, slot_mapping, k_cache, k_scale, v_cache, v_scale, (int)Hkv, (int)block_size);
+  if (D == 32) kv_write_paged_kernel<32><<<grid, 64, 0, st>>>(kn, vn, slot_mapping, k_cache, k_scale, v_cache, v_scale, (int)Hkv, (int)block_size);
+  else if (D == 64) kv_write_paged_kernel<64><<<grid, 64, 0, st>>>(kn, vn, slot_mapping, k_cache, k_scale, v_cache, v_scale, (int)Hkv, (int)block_size);
   else if (D == 128) kv_write_paged_kernel<128><<<grid, 64, 0, st>>>(kn, vn, slot_mapping, k_cache, k_scale, v_cache, v_scale, (int)Hkv, (int)block_size);
   else kv_write_paged_kernel<256><<<grid, 64, 0, st>>>(kn, vn, slot_mapping, k_cache, k_scale, v_cache, v_scale, (int)Hkv, (int)block_size);
   SL8_CHECK_LAUNCH("kv_write_paged");

@@ -157,6 +157,7 @@ struct FwdArgs {
   int diag;            // causal: query i sees keys <= i + diag
   int xcd_map;         // xcd_mode(): XCD-aware block order
   float w8_excess;     // W8A8: headroom of P above the reference point (log2)
+  int dout;            // output row length (= D, or the caller's head dim when D is padded)
 };
 
 // LDS tiles are dense; 16-byte chunks are XOR-swizzled within each row
@@ -985,11 +986,12 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       const float l = l_lane[g] + __shfl_xor(l_lane[g], 32, 64);
       if (m_ok[g]) {
         const float inv = (l > 0.f) ? 1.f / l : 0.f;
-        uint16_t* orow = reinterpret_cast<uint16_t*>(a.out) + ((int64_t)bh * M + mq[g]) * D;
+        uint16_t* orow = reinterpret_cast<uint16_t*>(a.out) + ((int64_t)bh * M + mq[g]) * a.dout;
 #pragma unroll
         for (int tt = 0; tt < DC; ++tt)
 #pragma unroll
           for (int gq = 0; gq < 4; ++gq) {
+            if (32 * tt + 8 * gq + 4 * h >= a.dout) continue;  // zero-padded channels
             float vsc[4] = {1.f, 1.f, 1.f, 1.f};
             if constexpr (W8) {
               const float4 v4 = *reinterpret_cast<const float4*>(a.vs + bkv * D + 32 * tt + 8 * gq + 4 * h);
@@ -1063,8 +1065,8 @@ int64_t npad_of(int64_t N) { return (N + BN - 1) / BN * BN; }
 int check_fwd_shape(int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N, int64_t D) {
   SL8_CHECK_ARG(B >= 0 && Hq >= 0 && Hkv > 0 && M >= 0 && N >= 0, "fni8: bad shape");
   SL8_CHECK_ARG(Hq % Hkv == 0, "fni8: H_q must be divisible by H_kv (GQA)");
-  SL8_CHECK_ARG(D == 64 || D == 128 || D == 256, "fni8: head dim must be 64/128/256, got %lld",
-                (long long)D);
+  SL8_CHECK_ARG(D == 32 || D == 64 || D == 72 || D == 80 || D == 128 || D == 256,
+                "fni8: head dim must be 32/64/72/80/128/256, got %lld", (long long)D);
   SL8_CHECK_ARG(M < (1 << 30) && N < (1 << 30) && B * Hq < (1 << 24), "fni8: shape too large");
   return SL8_OK;
 }
@@ -1079,6 +1081,7 @@ FwdArgs make_args(int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N, int&
   a.nqb = (int)((M + BM - 1) / BM);
   a.window_left = -1;
   a.diag = (int)(N - M);
+  a.dout = 0;  // set by the callers
   grid = (int)(B * Hq * a.nqb);  // causal kernels halve this (paired query blocks)
   a.xcd_map = xcd_mode(B * Hkv, Hq / Hkv, a.nqb);  // non-causal slot count
   return a;
@@ -1086,9 +1089,90 @@ FwdArgs make_args(int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N, int&
 
 }  // namespace
 
-// W8A8 prefill with per-warp P quantisation on the production pipeline
-// (called from attn_w8a8.hip). v: int8 [B*Hkv][N][D]; vt_ws: workspace of
-// w8a8_wide_workspace() bytes for bf16 V^T [B*Hkv][D][Npad].
+namespace {
+
+// ---------------------------------------------------------------------------
+// Head dims without an MFMA tiling of their own (32, 72, 80) run on the
+// kernel of the next supported width DP (64 or 128): Q, K and V rows are
+// copied into a workspace zero-padded to DP channels. Zero channels add
+// nothing to the int32 Q.K^T sums (the scores are bit-identical) and give
+// zero output channels, which the epilogue does not store (FwdArgs::dout).
+// ---------------------------------------------------------------------------
+int padded_head_dim(int64_t D) { return D == 32 ? 64 : (D == 72 || D == 80) ? 128 : (int)D; }
+
+// dst[r][0 .. dw) = src[r][0 .. sw) followed by zeros, in dwords
+__global__ void __launch_bounds__(256)
+pad_rows_kernel(const uint32_t* __restrict__ src, uint32_t* __restrict__ dst, int64_t rows, int sw,
+                int dw) {
+  const int64_t total = rows * dw;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / dw;
+    const int c = (int)(i - r * dw);
+    dst[i] = c < sw ? src[r * sw + c] : 0u;
+  }
+}
+
+// row bytes must be multiples of 4 (every head dim here is a multiple of 8)
+int pad_rows(const void* src, void* dst, int64_t rows, int64_t src_bytes, int64_t dst_bytes,
+             hipStream_t st) {
+  if (rows <= 0) return SL8_OK;
+  const int64_t total = rows * (dst_bytes / 4);
+  const int64_t grid = std::min<int64_t>((total + 255) / 256, 8192);
+  pad_rows_kernel<<<(unsigned)grid, 256, 0, st>>>(static_cast<const uint32_t*>(src),
+                                                   static_cast<uint32_t*>(dst), rows,
+                                                   (int)(src_bytes / 4), (int)(dst_bytes / 4));
+  SL8_CHECK_LAUNCH("pad head dim");
+  return SL8_OK;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// workspace of the padded operands: Q [B*Hq*M][DP], K [B*Hkv*N][DP] (int8),
+// V [B*Hkv*N][DP] of v_bytes per element, and (W8A8) v_scale [B*Hkv][DP]
+size_t pad_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N, int64_t D,
+                     int v_bytes, bool vscale) {
+  const int64_t DP = padded_head_dim(D);
+  if (DP == D || B <= 0) return 0;
+  return align256((size_t)(B * Hq * M * DP)) + align256((size_t)(B * Hkv * N * DP)) +
+         align256((size_t)(B * Hkv * N * DP * v_bytes)) +
+         (vscale ? align256((size_t)(B * Hkv * DP * 4)) : 0);
+}
+
+struct Padded {
+  const int8_t* q;
+  const int8_t* k;
+  const void* v;
+  const float* vs;
+  void* rest;  // workspace past the padded operands
+};
+
+int pad_operands(const int8_t* q, const int8_t* k, const void* v, const float* vs, int64_t B,
+                 int64_t Hq, int64_t Hkv, int64_t M, int64_t N, int64_t D, int v_bytes, void* ws,
+                 hipStream_t st, Padded& p) {
+  const int64_t DP = padded_head_dim(D);
+  char* w = static_cast<char*>(ws);
+  char* qp = w;
+  w += align256((size_t)(B * Hq * M * DP));
+  char* kp = w;
+  w += align256((size_t)(B * Hkv * N * DP));
+  char* vp = w;
+  w += align256((size_t)(B * Hkv * N * DP * v_bytes));
+  char* vsp = w;
+  int rc = pad_rows(q, qp, B * Hq * M, D, DP, st);
+  if (!rc) rc = pad_rows(k, kp, B * Hkv * N, D, DP, st);
+  if (!rc) rc = pad_rows(v, vp, B * Hkv * N, D * v_bytes, DP * v_bytes, st);
+  if (!rc && vs) {
+    rc = pad_rows(vs, vsp, B * Hkv, D * 4, DP * 4, st);
+    w += align256((size_t)(B * Hkv * DP * 4));
+  }
+  p = Padded{reinterpret_cast<int8_t*>(qp), reinterpret_cast<int8_t*>(kp), vp,
+             vs ? reinterpret_cast<float*>(vsp) : nullptr, w};
+  return rc;
+}
+
+}  // namespace
+
 // largest P exponent that keeps the W8A8 sums of N keys below 2^120
 float w8_excess_for(int64_t N) {
   int lg = 0;
@@ -1097,13 +1181,37 @@ float w8_excess_for(int64_t N) {
 }
 
 size_t w8a8_wide_workspace(int64_t B, int64_t Hkv, int64_t N, int64_t D) {
-  return (size_t)(B * Hkv * D * npad_of(N)) * sizeof(uint16_t);
+  return (size_t)(B * Hkv * padded_head_dim(D) * npad_of(N)) * sizeof(uint16_t);
 }
 
+// padded operands (int8 Q/K/V and the per-channel V scale) of a W8A8 call
+size_t w8a8_pad_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N, int64_t D) {
+  return pad_workspace(B, Hq, Hkv, M, N, D, 1, true);
+}
+
+int w8a8_pad_operands(const int8_t*& q, const int8_t*& k, const int8_t*& v, const float*& vs,
+                      int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N, int64_t D,
+                      void*& ws, hipStream_t st) {
+  if (padded_head_dim(D) == D) return SL8_OK;
+  Padded p;
+  const int rc = pad_operands(q, k, v, vs, B, Hq, Hkv, M, N, D, 1, ws, st, p);
+  q = p.q;
+  k = p.k;
+  v = static_cast<const int8_t*>(p.v);
+  vs = p.vs;
+  ws = p.rest;
+  return rc;
+}
+
+// W8A8 prefill with per-warp P quantisation on the production pipeline
+// (called from attn_w8a8.hip). v: int8 [B*Hkv][N][D]; vt_ws: workspace of
+// w8a8_wide_workspace() bytes for bf16 V^T [B*Hkv][D][Npad]. D is a
+// supported width (64/128/256); dout = the output row length (the caller's
+// head dim when the operands were padded).
 int w8a8_wide_launch(const int8_t* q, const float* q_scale, const int8_t* k, const float* k_scale,
                      const int8_t* v, const float* v_scale, void* out, int64_t B, int64_t Hq,
-                     int64_t Hkv, int64_t M, int64_t N, int64_t D, bool causal, int64_t causal_diag,
-                     void* vt_ws, hipStream_t st) {
+                     int64_t Hkv, int64_t M, int64_t N, int64_t D, int64_t dout, bool causal,
+                     int64_t causal_diag, void* vt_ws, hipStream_t st) {
   uint16_t* vt = static_cast<uint16_t*>(vt_ws);
   if (N > 0) {
     const int np = (int)npad_of(N);
@@ -1118,6 +1226,7 @@ int w8a8_wide_launch(const int8_t* q, const float* q_scale, const int8_t* k, con
   a.q = q; a.qs = q_scale; a.k = k; a.ks = k_scale;
   a.vt = vt; a.vs = v_scale; a.out = out; a.lse = nullptr;
   a.diag = (int)causal_diag;
+  a.dout = (int)dout;
   a.w8_excess = w8_excess_for(N);
   a.nqb = (int)((M + wide_bm(D) - 1) / wide_bm(D));
   const int nslot = causal ? (a.nqb + 1) / 2 : a.nqb;
@@ -1142,11 +1251,11 @@ int w8a8_wide_launch(const int8_t* q, const float* q_scale, const int8_t* k, con
 
 using namespace sl8;
 
-// The prefill reads V in place (natural layout): no workspace is needed. The
-// entry point keeps its workspace arguments for ABI stability.
-extern "C" size_t sl8_attn_int8_fwd_workspace(int64_t B, int64_t Hkv, int64_t N, int64_t D) {
-  (void)B; (void)Hkv; (void)N; (void)D;
-  return 0;
+// The prefill reads V in place (natural layout): the workspace only holds the
+// zero-padded operands of head dims 32, 72 and 80.
+extern "C" size_t sl8_attn_int8_fwd_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t M,
+                                              int64_t N, int64_t D) {
+  return pad_workspace(B, Hq, Hkv, M, N, D, 2, false);
 }
 
 extern "C" int sl8_attn_int8_fwd(const int8_t* q, const float* q_scale, const int8_t* k,
@@ -1164,25 +1273,35 @@ extern "C" int sl8_attn_int8_fwd(const int8_t* q, const float* q_scale, const in
   SL8_CHECK_ARG(q && q_scale && out && (N == 0 || (k && k_scale && v)), "fni8: null pointer");
   SL8_CHECK_ARG(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(out, 16),
                 "fni8: q/k/v/out must be 16-byte aligned");
-  const size_t need = sl8_attn_int8_fwd_workspace(B, Hkv, N, D);
+  const size_t need = sl8_attn_int8_fwd_workspace(B, Hq, Hkv, M, N, D);
   SL8_CHECK_ARG(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 16)),
                 "fni8: attn_int8_fwd workspace needs %zu bytes", need);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t DP = padded_head_dim(D);
+  if (DP != D) {
+    Padded p;
+    rc = pad_operands(q, k, v, nullptr, B, Hq, Hkv, M, N, D, 2, workspace, st, p);
+    if (rc) return rc;
+    q = p.q;
+    k = p.k;
+    v = p.v;
+  }
   int grid;
   FwdArgs a = make_args(B, Hq, Hkv, M, N, grid);
   a.q = q; a.qs = q_scale; a.k = k; a.ks = k_scale;
-  a.vt = static_cast<const uint16_t*>(v);  // V [B*Hkv][N][D], read in place
+  a.vt = static_cast<const uint16_t*>(v);  // V [B*Hkv][N][DP], read in place
   a.out = out; a.lse = lse; a.window_left = (int)window_left;
+  a.dout = (int)D;
   const bool c = causal != 0, want_lse = lse != nullptr;
-  a.nqb = (int)((M + wide_bm(D) - 1) / wide_bm(D));
+  a.nqb = (int)((M + wide_bm(DP) - 1) / wide_bm(DP));
   const int nslot = c ? (a.nqb + 1) / 2 : a.nqb;
   grid = (int)(B * Hq * nslot);
   a.xcd_map = xcd_mode(B * Hkv, Hq / Hkv, nslot);
   const bool f16 = v_dtype == SL8_DTYPE_F16;
-  if (D == 64) {
+  if (DP == 64) {
     if (f16) dispatch_wide<64, SL8_DTYPE_F16>(a, grid, c, want_lse, st);
     else dispatch_wide<64, SL8_DTYPE_BF16>(a, grid, c, want_lse, st);
-  } else if (D == 128) {
+  } else if (DP == 128) {
     if (f16) dispatch_wide<128, SL8_DTYPE_F16>(a, grid, c, want_lse, st);
     else dispatch_wide<128, SL8_DTYPE_BF16>(a, grid, c, want_lse, st);
   } else {
@@ -1199,7 +1318,7 @@ extern "C" int sl8_attn_int8_qk_scores(const int8_t* q, const int8_t* k, int32_t
   clear_error();
   int rc = check_fwd_shape(B, Hq, Hkv, M, N, D);
   if (rc) return rc;
-  SL8_CHECK_ARG(D != 256, "fni8: qk_scores supports head dim 64/128");
+  SL8_CHECK_ARG(D == 64 || D == 128, "fni8: qk_scores supports head dim 64/128");
   if (B == 0 || Hq == 0 || M == 0 || N == 0) return SL8_OK;
   SL8_CHECK_ARG(q && k && scores, "fni8: null pointer");
   SL8_CHECK_ARG(aligned(q, 16) && aligned(k, 16), "fni8: q/k must be 16-byte aligned");

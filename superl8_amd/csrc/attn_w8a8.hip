@@ -77,6 +77,7 @@ struct W8Args {
   uint16_t* out;
   int M, N, Npad, Hq, Hkv, nqb, causal_diag;
   int xcd_map;
+  int dout;  // output row length (< D when the operands are zero-padded)
 };
 
 __device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d) {
@@ -295,12 +296,13 @@ attn_w8a8_kernel(const W8Args a) {
     if (m_ok) {
       const float inv = (l > 0.f) ? 1.f / l : 0.f;
       const float* vs = a.vs + bkv * D;
-      uint16_t* orow = a.out + ((int64_t)bh * M + mq) * D;
+      uint16_t* orow = a.out + ((int64_t)bh * M + mq) * a.dout;
 #pragma unroll
       for (int tt = 0; tt < DC; ++tt)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int d0 = 32 * tt + 8 * g + 4 * h;
+          if (d0 >= a.dout) continue;  // zero-padded channels
           const float4 sc = *reinterpret_cast<const float4*>(vs + d0);
           uint2 pk;
           pk.x = f2h_bits(oacc[tt][4 * g + 0] * sc.x * inv) |
@@ -330,24 +332,33 @@ void launch_w8_d(const W8Args& a, int grid, bool causal, bool per_warp, hipStrea
 
 }  // namespace
 
-// per-warp quantisation runs on the prefill pipeline of attn_fwd.hip
+// per-warp quantisation runs on the prefill pipeline of attn_fwd.hip, which
+// also pads head dim 32 to 64 (zero channels; see padded_head_dim there)
 size_t w8a8_wide_workspace(int64_t B, int64_t Hkv, int64_t N, int64_t D);
+size_t w8a8_pad_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N, int64_t D);
+int w8a8_pad_operands(const int8_t*& q, const int8_t*& k, const int8_t*& v, const float*& vs,
+                      int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N, int64_t D,
+                      void*& ws, hipStream_t st);
 int w8a8_wide_launch(const int8_t* q, const float* q_scale, const int8_t* k, const float* k_scale,
                      const int8_t* v, const float* v_scale, void* out, int64_t B, int64_t Hq,
-                     int64_t Hkv, int64_t M, int64_t N, int64_t D, bool causal, int64_t causal_diag,
-                     void* vt_ws, hipStream_t st);
+                     int64_t Hkv, int64_t M, int64_t N, int64_t D, int64_t dout, bool causal,
+                     int64_t causal_diag, void* vt_ws, hipStream_t st);
 
 }  // namespace sl8
 
 using namespace sl8;
 
-extern "C" size_t sl8_attn_w8a8_fwd_workspace(int64_t B, int64_t Hkv, int64_t N, int64_t D) {
-  if (B <= 0 || Hkv <= 0 || N <= 0 || D <= 0) return 0;
-  // the larger of the two layouts: fp16 V^T (per-warp quantisation) and the
-  // int8 V^T of the per-tile kernel
-  const size_t i8 = (size_t)(B * Hkv * D * npad8(N));
+extern "C" size_t sl8_attn_w8a8_fwd_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t M,
+                                               int64_t N, int64_t D) {
+  if (B <= 0 || Hkv <= 0 || D <= 0) return 0;
+  const size_t pad = w8a8_pad_workspace(B, Hq, Hkv, M, N, D);
+  if (N <= 0) return pad;
+  // the larger of the two layouts: bf16 V^T (per-warp quantisation) and the
+  // int8 V^T of the per-tile kernel, after the zero-padded operands (head dim 32)
+  const int64_t DP = D == 32 ? 64 : D;
+  const size_t i8 = (size_t)(B * Hkv * DP * npad8(N));
   const size_t f16 = w8a8_wide_workspace(B, Hkv, N, D);
-  return f16 > i8 ? f16 : i8;
+  return pad + (f16 > i8 ? f16 : i8);
 }
 
 extern "C" int sl8_attn_w8a8_fwd(const int8_t* q, const float* q_scale, const int8_t* k,
@@ -359,8 +370,8 @@ extern "C" int sl8_attn_w8a8_fwd(const int8_t* q, const float* q_scale, const in
   clear_error();
   SL8_CHECK_ARG(B >= 0 && Hq >= 0 && Hkv > 0 && M >= 0 && N >= 0, "fni8: bad shape");
   SL8_CHECK_ARG(Hq % Hkv == 0, "fni8: H_q must be divisible by H_kv (GQA)");
-  SL8_CHECK_ARG(D == 64 || D == 128 || D == 256, "fni8: head dim must be 64/128/256, got %lld",
-                (long long)D);
+  SL8_CHECK_ARG(D == 32 || D == 64 || D == 128 || D == 256,
+                "fni8: head dim must be 32/64/128/256, got %lld", (long long)D);
   SL8_CHECK_ARG(M < (1 << 30) && N < (1 << 30) && B * Hq < (1 << 24), "fni8: shape too large");
   SL8_CHECK_ARG(causal_diag > -(1LL << 30) && causal_diag < (1LL << 30), "fni8: bad causal_diag");
   if (B == 0 || Hq == 0 || M == 0) return SL8_OK;
@@ -369,12 +380,19 @@ extern "C" int sl8_attn_w8a8_fwd(const int8_t* q, const float* q_scale, const in
   SL8_CHECK_ARG(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(out, 16) &&
                     aligned(v_scale, 16),
                 "fni8: q/k/v/v_scale/out must be 16-byte aligned");
-  const size_t need = sl8_attn_w8a8_fwd_workspace(B, Hkv, N, D);
+  const size_t need = sl8_attn_w8a8_fwd_workspace(B, Hq, Hkv, M, N, D);
   SL8_CHECK_ARG(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 16)),
                 "fni8: attn_w8a8_fwd workspace needs %zu bytes", need);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t dout = D;
+  if (D == 32) {
+    // zero-padded to 64 channels: identical scores, zero output channels 32..63
+    const int rc = w8a8_pad_operands(q, k, v, v_scale, B, Hq, Hkv, M, N, D, workspace, st);
+    if (rc) return rc;
+    D = 64;
+  }
   if (per_warp_quant)
-    return w8a8_wide_launch(q, q_scale, k, k_scale, v, v_scale, out, B, Hq, Hkv, M, N, D,
+    return w8a8_wide_launch(q, q_scale, k, k_scale, v, v_scale, out, B, Hq, Hkv, M, N, D, dout,
                             causal != 0, causal_diag, workspace, st);
   const int64_t Npad = npad8(N);
   if (N > 0) {
@@ -390,6 +408,7 @@ extern "C" int sl8_attn_w8a8_fwd(const int8_t* q, const float* q_scale, const in
   a.vt = static_cast<const int8_t*>(workspace);
   a.vs = v_scale;
   a.out = static_cast<uint16_t*>(out);
+  a.dout = (int)dout;
   a.M = (int)M; a.N = (int)N; a.Npad = (int)Npad; a.Hq = (int)Hq; a.Hkv = (int)Hkv;
   a.nqb = (int)((M + WBM - 1) / WBM);
   a.causal_diag = (int)causal_diag;

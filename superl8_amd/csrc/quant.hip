@@ -506,7 +506,8 @@ extern "C" int sl8_k_mean(const void* k, int dtype, int64_t G, int64_t N, int64_
 // ---------------------------------------------------------------------------
 // Outlier gate (reference superl8/quant/core.py:113-145): any row of Q with
 // max|q| / (median|q| + 1e-10) > ratio (fp32) routes the call to full
-// precision. One wave per row of D = 64 E elements. The median is torch's
+// precision. One wave per row of D <= 64 E elements (lanes past D hold no
+// element: they never count as "below" and add 0 to the max). The median is torch's
 // lower median, the ((D-1)/2)-th smallest |q|, found exactly by a radix
 // select on the fp32 bit patterns (non-negative floats order like their bits):
 // 31 rounds of "how many elements lie below this prefix" (ballot + popcount).
@@ -517,9 +518,8 @@ namespace {
 
 template <int DT, int E>
 __global__ void __launch_bounds__(256)
-q_gate_kernel(const void* __restrict__ q, int64_t rows, float ratio, int32_t* __restrict__ flag,
-              float* __restrict__ stats) {
-  constexpr int D = 64 * E;
+q_gate_kernel(const void* __restrict__ q, int64_t rows, int D, float ratio,
+              int32_t* __restrict__ flag, float* __restrict__ stats) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;  // wave-uniform
@@ -528,18 +528,19 @@ q_gate_kernel(const void* __restrict__ q, int64_t rows, float ratio, int32_t* __
   bool nan = false;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    const int64_t i = row * D + e * 64 + lane;
+    const int c = e * 64 + lane;
+    const int64_t i = row * D + (c < D ? c : 0);
     float x;
     if constexpr (DT == SL8_DTYPE_F32) x = static_cast<const float*>(q)[i];
     else x = u16_to_f<DT>(static_cast<const uint16_t*>(q)[i]);
-    x = fabsf(x);
+    x = c < D ? fabsf(x) : 0.f;
     nan |= x != x;
-    bits[e] = __float_as_uint(x);
+    bits[e] = c < D ? __float_as_uint(x) : 0xFFFFFFFFu;
     mx = fmaxf(mx, x);
   }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-  constexpr int K = (D - 1) / 2;
+  const int K = (D - 1) / 2;
   uint32_t ans = 0;
   for (int b = 30; b >= 0; --b) {
     const uint32_t t = ans | (1u << b);
@@ -568,17 +569,17 @@ q_gate_kernel(const void* __restrict__ q, int64_t rows, float ratio, int32_t* __
 extern "C" int sl8_q_outlier_gate(const void* q, int dtype, int64_t rows, int64_t D, float ratio,
                                   int32_t* flag, float* stats, void* stream) {
   clear_error();
-  SL8_CHECK_ARG(rows >= 0 && (D == 64 || D == 128 || D == 256),
-                "fni8 outlier gate: head dim must be 64/128/256, got %lld", (long long)D);
+  SL8_CHECK_ARG(rows >= 0 && D >= 1 && D <= 256,
+                "fni8 outlier gate: head dim must be 1..256, got %lld", (long long)D);
   SL8_CHECK_ARG(dtype == SL8_DTYPE_F16 || dtype == SL8_DTYPE_BF16 || dtype == SL8_DTYPE_F32,
                 "fni8 outlier gate: q must be float16, bfloat16 or float32");
   if (rows == 0) return SL8_OK;
   SL8_CHECK_ARG(q && flag, "fni8 outlier gate: null pointer");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)((rows + 3) / 4));
-#define SL8_GATE(DT, E) q_gate_kernel<DT, E><<<grid, 256, 0, st>>>(q, rows, ratio, flag, stats)
+#define SL8_GATE(DT, E) q_gate_kernel<DT, E><<<grid, 256, 0, st>>>(q, rows, (int)D, ratio, flag, stats)
 #define SL8_GATE_D(DT) \
-  if (D == 64) SL8_GATE(DT, 1); else if (D == 128) SL8_GATE(DT, 2); else SL8_GATE(DT, 4);
+  if (D <= 64) SL8_GATE(DT, 1); else if (D <= 128) SL8_GATE(DT, 2); else SL8_GATE(DT, 4);
   if (dtype == SL8_DTYPE_F16) { SL8_GATE_D(SL8_DTYPE_F16) }
   else if (dtype == SL8_DTYPE_BF16) { SL8_GATE_D(SL8_DTYPE_BF16) }
   else { SL8_GATE_D(SL8_DTYPE_F32) }

@@ -72,7 +72,8 @@ def detect_q_outlier_domination(q: torch.Tensor, *, ratio_threshold: float = 12.
     """True when any Q row has max|q| / median|q| > ratio_threshold (reference core.py:113-145).
 
     One gate kernel (max and exact lower median per row, flag by atomic OR)
-    decides on the GPU for D in 64/128/256; other head dims use torch ops.
+    decides on the GPU for head dims up to 256 (every dim the kernels accept);
+    wider rows use torch ops.
     Skipped (False) while the current stream is capturing a graph, because the
     decision needs a device-to-host read.
     """
@@ -81,7 +82,7 @@ def detect_q_outlier_domination(q: torch.Tensor, *, ratio_threshold: float = 12.
             return False
     except Exception:
         pass
-    if q.is_cuda and q.shape[-1] in _C._GATE_HEAD_DIMS:
+    if q.is_cuda and 1 <= q.shape[-1] <= _C._GATE_MAX_D:
         flag, _ = _C.q_outlier_gate(q, ratio_threshold)
         return bool(flag.item())
     q_abs = q.float().abs()

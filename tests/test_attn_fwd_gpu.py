@@ -69,6 +69,10 @@ KERNEL_CASES = [
     (1, 2, 2, 300, 40, 64, True, -1),       # M > N: leading rows see nothing
     (1, 2, 1, 200, 200, 256, True, -1),     # head dim 256 (one wave per SIMD)
     (1, 2, 2, 70, 90, 256, False, 20),
+    # head dims 32/72/80 (reference attn_int8_fwd.cu:138; zero-padded to 64/128)
+    (2, 8, 2, 257, 257, 72, True, -1), (2, 8, 2, 257, 257, 80, False, -1),
+    (1, 4, 1, 100, 333, 32, True, -1), (1, 2, 2, 130, 130, 32, False, 24),
+    (1, 4, 2, 200, 260, 80, True, 50),
 ]
 
 
@@ -103,7 +107,7 @@ def test_kernel_matches_oracle(device, case, vdt):
 
 
 SHAPES = [(1, 2, 128, 64), (2, 4, 512, 64), (2, 4, 257, 64), (1, 2, 333, 128),
-          (1, 8, 2048, 64), (1, 8, 2048, 128)]
+          (1, 8, 2048, 64), (1, 8, 2048, 128), (2, 4, 257, 32), (1, 4, 513, 72), (1, 4, 300, 80)]
 
 
 @pytest.mark.parametrize("shape", SHAPES)
@@ -147,12 +151,32 @@ def test_deterministic_and_rejects(device):
     for _ in range(3):
         assert torch.equal(sl8.attn_int8_fwd(q, k, v), r0)
     q, k, v = _qkv(1, 2, 2, 128, 128, 96, device)
-    with pytest.raises(RuntimeError):
+    with pytest.raises(RuntimeError, match="32/64/72/80/128/256"):
         sl8.attn_int8_fwd(q, k, v)
     q8 = torch.zeros(1, 2, 8, 64, device=device, dtype=torch.int8)
     s = torch.ones(1, 2, 8, device=device)
     with pytest.raises(RuntimeError, match="float16|bfloat16"):
         _C.attn_int8_fwd(q8, s, q8, s, torch.zeros(1, 2, 8, 64, device=device))
+
+
+@pytest.mark.parametrize("d", [72, 80])
+def test_odd_head_dim_deterministic(device, d):
+    """reference tests/test_odd_dims.py:30-36."""
+    q, k, v = (torch.randn(1, 4, 200, d, device=device, dtype=torch.float16) for _ in range(3))
+    r0 = sl8.attn_int8_fwd(q, k, v)
+    assert r0.shape == q.shape
+    for _ in range(3):
+        assert torch.equal(sl8.attn_int8_fwd(q, k, v), r0)
+
+
+@pytest.mark.parametrize("d", [32, 72, 80])
+@pytest.mark.parametrize("causal", [False, True])
+def test_odd_head_dim_gqa_quality(device, d, causal):
+    """reference tests/test_odd_dims.py:14-27 (ragged M, GQA) against fp attention."""
+    q, k, v = _qkv(2, 8, 2, 257, 257, d, device)
+    out = sl8.attn_int8_fwd(q, k, v, causal=causal)
+    assert out.shape == q.shape
+    assert_int8_quality(out, _fp32_oracle(q, k, v, causal), what=f"odd-dim D={d} causal={causal}")
 
 
 def test_accuracy_gate_and_rotate(device, monkeypatch):

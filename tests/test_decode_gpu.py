@@ -16,6 +16,7 @@ DECODE_SHAPES = [  # reference tests/test_decode.py:28-43
     (1, 32, 1, 300, 128),  # MQA with 32 query heads per KV head
     (3, 6, 2, 5, 64),      # fewer keys than splits
     (2, 8, 2, 1000, 64), (1, 64, 8, 1500, 128), (1, 16, 2, 333, 256), (2, 8, 4, 999, 128),  # streaming paths
+    (2, 8, 2, 1000, 32), (1, 16, 4, 777, 32), (1, 8, 8, 300, 32),  # head dim 32 (reference attn_decode.cu:195)
 ]
 
 
@@ -158,6 +159,7 @@ from oracle import quant as oqn  # noqa: E402
 PAGED_CASES = [  # B, Hq, Hkv, D, block_size, lens
     (2, 8, 2, 64, 16, (50, 7)), (3, 32, 8, 128, 16, (1000, 1, 333)), (1, 16, 4, 256, 32, (257,)),
     (2, 8, 8, 128, 64, (64, 0)), (4, 12, 4, 64, 8, (9, 100, 31, 64)), (1, 32, 1, 128, 16, (600,)),
+    (2, 8, 2, 32, 16, (50, 333)), (1, 16, 4, 32, 32, (257,)),  # head dim 32
 ]
 
 
@@ -221,7 +223,7 @@ def test_paged_context_above_max_is_clamped(device, ns):
     assert_close_abs(out[:, :, 0], ref, atol=2e-3, rtol=2e-3, what="paged clamp")
 
 
-@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("D", [32, 64, 128, 256])
 def test_kv_write_paged_bit_exact(device, D):
     B, Hkv, nblk, bs = 3, 4, 5, 8
     g = torch.Generator().manual_seed(D)
@@ -243,7 +245,7 @@ def test_kv_write_paged_bit_exact(device, D):
     np.testing.assert_array_equal(_np(tens[6]), rvs)
 
 
-@pytest.mark.parametrize("D,lens", [(128, (40, 97, 1)), (64, (130,))])
+@pytest.mark.parametrize("D,lens", [(128, (40, 97, 1)), (64, (130,)), (32, (70, 5))])
 def test_paged_end_to_end(device, D, lens):
     """Token-by-token quantize-on-write into a shuffled block pool, then one paged
     decode for the ragged batch: the reference's int8 quality bars against fp64
