@@ -107,7 +107,9 @@ def bench_public_prefill(iters=20):
     return _events_time(fn, iters, torch.cuda.current_stream())
 
 
-def bench_decode(iters=20):
+def bench_decode(iters=20, ks16=False):
+    """Config 3. ks16: the K cache's per-token scales stored as fp16 (the BASELINE
+    config text; the reference contract is fp32)."""
     from superl8_amd import _C
 
     dev = "cuda"
@@ -122,12 +124,14 @@ def bench_decode(iters=20):
     qs = (qs * (1.0 / np.sqrt(D) * np.log2(np.e))).reshape(B, Hq, 1).contiguous()
     k_i8 = k_i8.reshape(B, Hkv, N, D)
     ks = ks.reshape(B, Hkv, N)
+    if ks16:
+        ks = ks.half()
     v = torch.randn(B, Hkv, N, D, device=dev, dtype=torch.float16, generator=g)
     fn = lambda: _C.attn_int8_decode(q_i8, qs, k_i8, ks, v, 16)  # noqa: E731
     spin_up(fn, 0.2)
     ms = _events_time(fn, iters, torch.cuda.current_stream())
-    nbytes = k_i8.numel() + ks.numel() * 4 + v.numel() * 2 + q_i8.numel() + qs.numel() * 4 \
-        + B * Hq * D * 2
+    nbytes = k_i8.numel() + ks.numel() * ks.element_size() + v.numel() * 2 + q_i8.numel() \
+        + qs.numel() * 4 + B * Hq * D * 2
     return ms, nbytes
 
 
@@ -232,9 +236,11 @@ def bench_prologue(iters=20):
     return fms, sms, nbytes
 
 
-def bench_w8a8(iters=5):
+def bench_w8a8(iters=5, per_wave=False):
     """Full-W8A8 prefill at BASELINE config 5: Q/K/V [2, 16|2, 8192, 256], causal,
-    1% of Q/K channels (3 of 256, fixed) scaled by 20, V per-channel int8."""
+    1% of Q/K channels (3 of 256, fixed) scaled by 20, V per-channel int8.
+    per_wave: Q/K quantised per wavefront tile (32 queries / 64 keys), the config
+    text, instead of the reference's per row (the kernel is the same)."""
     from superl8_amd import _C, quant
 
     dev = "cuda"
@@ -246,7 +252,8 @@ def bench_w8a8(iters=5):
     ch = torch.tensor([17, 101, 203], device=dev)
     q[..., ch] *= 20
     k[..., ch] *= 20
-    q_i8, qs, k_i8, ks, _ = quant.quantize_qk(q, k)
+    qfn = quant.quantize_qk_per_wave if per_wave else quant.quantize_qk
+    q_i8, qs, k_i8, ks, _ = qfn(q, k)
     qs, ks = qs.squeeze(-1).contiguous(), ks.squeeze(-1).contiguous()
     v_i8, vs = _C.quantize_v_perchannel(v)
     vs = vs.reshape(B, Hkv, D).contiguous()
@@ -270,7 +277,9 @@ def _kquant_weights(fmt, N, K, seed):
 KQ_BYTES = {"q4k": 144, "q5k": 176, "q6k": 210}
 
 
-def bench_gemv(M, iters_graph=10, copies=8, fmt="q4k"):
+def bench_gemv(M, iters_graph=10, copies=8, fmt="q4k", xblock=False):
+    """xblock: activations int8 per 256-element block with one fp32 scale each
+    (x_scale [M, K/256], the BASELINE config 4 text) instead of per row."""
     from superl8_amd import _C
 
     dev = "cuda"
@@ -280,7 +289,7 @@ def bench_gemv(M, iters_graph=10, copies=8, fmt="q4k"):
     ws = [base] + [base.roll(i * 1, 0).contiguous() for i in range(1, copies)]  # > 256 MB MALL
     g = torch.Generator(device=dev).manual_seed(5)
     x = torch.randn(M, K, device=dev, dtype=torch.float16, generator=g)
-    x_i8, xs = _C.quantize_i8_rowwise(x)
+    x_i8, xs = _C.quantize_i8_blockwise(x, 256) if xblock else _C.quantize_i8_rowwise(x)
     for w in ws:
         op(x_i8, xs, w)
     torch.cuda.synchronize()
@@ -296,7 +305,7 @@ def bench_gemv(M, iters_graph=10, copies=8, fmt="q4k"):
     torch.cuda.synchronize()
     cur = torch.cuda.current_stream()
     ms = _events_time(graph.replay, iters_graph, cur) / per_graph
-    nbytes = N * (K // 256) * KQ_BYTES[fmt] + M * K + M * 4 + M * N * 2
+    nbytes = N * (K // 256) * KQ_BYTES[fmt] + M * K + xs.numel() * 4 + M * N * 2
     return ms, nbytes
 
 
@@ -417,6 +426,11 @@ def main():
         sec["attn_int8_decode_cfg3"] = {"us": round(dms * 1e3, 2), "GB/s": round(gbs, 1),
                                         "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
                                         "bytes": dbytes}
+        dms, dbytes = bench_decode(ks16=True)
+        gbs = dbytes / (dms * 1e-3) / 1e9
+        sec["attn_int8_decode_cfg3_fp16_kscale"] = {"us": round(dms * 1e3, 2), "GB/s": round(gbs, 1),
+                                                    "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+                                                    "bytes": dbytes}
         kms, kbytes = bench_decode_kv8()
         gbs = kbytes / (kms * 1e-3) / 1e9
         sec["attn_int8_decode_kv8_cfg3shape"] = {"us": round(kms * 1e3, 2), "GB/s": round(gbs, 1),
@@ -433,6 +447,12 @@ def main():
             sec[f"gemm_decode_q4k_cfg4_m{M}"] = {"us": round(gms * 1e3, 2), "GB/s": round(gbs, 1),
                                                  "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
                                                  "bytes": gbytes}
+        for M in (1, 8):
+            gms, gbytes = bench_gemv(M, xblock=True)
+            gbs = gbytes / (gms * 1e-3) / 1e9
+            sec[f"gemm_decode_q4k_cfg4_m{M}_xblock256"] = {
+                "us": round(gms * 1e3, 2), "GB/s": round(gbs, 1),
+                "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": gbytes}
         pms2, pops = bench_gemm_prefill()
         pt = pops / (pms2 * 1e-3) / 1e12
         sec["gemm_q4k_prefill_m512_cfg4w"] = {"us": round(pms2 * 1e3, 1), "TOPS": round(pt, 1),
@@ -460,6 +480,11 @@ def main():
         wt = wops / (wms * 1e-3) / 1e12
         sec["attn_w8a8_fwd_cfg5"] = {"us": round(wms * 1e3, 1), "TOPS": round(wt, 1),
                                      "frac_int8_peak": round(wt / PEAK_INT8_TOPS, 4), "ops": wops}
+        wms, wops = bench_w8a8(per_wave=True)
+        wt = wops / (wms * 1e-3) / 1e12
+        sec["attn_w8a8_fwd_cfg5_per_wave_qk"] = {"us": round(wms * 1e3, 1), "TOPS": round(wt, 1),
+                                                 "frac_int8_peak": round(wt / PEAK_INT8_TOPS, 4),
+                                                 "ops": wops}
         sec["hbm_copy_256MiB_GBps"] = round(bench_copy(), 1)
         out["secondary"] = sec
     if not args.no_cpu:

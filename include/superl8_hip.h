@@ -79,6 +79,17 @@ int sl8_quantize_i8_rows_centered(const void* x, int x_dtype, int64_t G, int64_t
                                   int64_t D, const float* mean, float scale_mul,
                                   int8_t* q, float* scale, void* stream);
 
+/* Row-group int8 quantisation: x [G][N][D] (f16/bf16/f32), one scale per
+ * rows_per_group consecutive rows of each G slice (the last group of a slice
+ * may be short): scale = amax over the group * fp32(1/127) (1 if zero),
+ * codes and the optional mean shift as sl8_quantize_i8_rows_centered; every
+ * row's entry of scale [G][N] holds its group's scale * scale_mul. The
+ * per-wavefront Q / per-key-tile K quantisation of BASELINE config 5; no
+ * counterpart in the reference (its Q/K scales are per row, core.py:164-196). */
+int sl8_quantize_i8_row_groups(const void* x, int x_dtype, int64_t G, int64_t N, int64_t D,
+                               int64_t rows_per_group, const float* mean, float scale_mul,
+                               int8_t* q, float* scale, void* stream);
+
 /* ------------------------------------------------------------------------
  * Fused fp16 attention prologue: quantize_qk (no rotation) plus, optionally,
  * the outlier gate, in three launches (six unfused). Replaces superl8/quant/core.py:164-196
@@ -177,6 +188,18 @@ int sl8_attn_int8_decode(const int8_t* q, const float* q_scale, const int8_t* k,
                          int64_t num_splits, void* workspace, size_t workspace_bytes,
                          void* stream);
 
+/* Split-KV decode with fp16 per-token K scales: k_scale_f16 [B,Hkv,N] (the
+ * cache format of BASELINE config 3, half the scale bytes of the reference's
+ * fp32 contract at csrc/kernel/attn_decode.cu:174-175). Otherwise exactly
+ * sl8_attn_int8_decode (same workspace, checks and arithmetic after the
+ * exact fp16 -> fp32 widening). Reached from _C.attn_int8_decode when
+ * k_scale is float16. */
+int sl8_attn_int8_decode_ks16(const int8_t* q, const float* q_scale, const int8_t* k,
+                              const void* k_scale_f16, const void* v, void* out, int64_t B,
+                              int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                              int64_t num_splits, void* workspace, size_t workspace_bytes,
+                              void* stream);
+
 /* Allocation-free split-KV decode. No counterpart in the reference: it is for
  * callers that cannot allocate device memory (code under HIP graph capture,
  * serving loops, harnesses that forbid hipMalloc). Same arguments, checks,
@@ -255,6 +278,16 @@ int sl8_kv_write_paged(const void* k_new, const void* v_new, const int32_t* slot
 int sl8_gemm_decode_q4k(const int8_t* x, const float* x_scale, const uint8_t* w,
                         void* out, int out_dtype, int64_t M, int64_t N, int64_t K,
                         void* stream);
+
+/* Decode GEMV with per-256-block activation scales: x_scale [M, K/256] fp32
+ * (one scale per super-block-aligned slice of each activation row, the
+ * activation format of BASELINE config 4) multiplies each super-block's
+ * exact integer sums. No counterpart in the reference, whose activations
+ * carry one scale per row (csrc/kernel/gemm_decode_dp4a.cu:398); otherwise as
+ * sl8_gemm_decode_q4k (M <= 16, same checks). */
+int sl8_gemm_decode_q4k_xblock(const int8_t* x, const float* x_scale, const uint8_t* w,
+                               void* out, int out_dtype, int64_t M, int64_t N, int64_t K,
+                               void* stream);
 int sl8_gemm_q4k(const int8_t* x, const float* x_scale, const uint8_t* w, void* out,
                  int out_dtype, int64_t M, int64_t N, int64_t K, void* stream);
 

@@ -108,3 +108,20 @@ def gemv(x_i8: np.ndarray, x_scale: np.ndarray, w: np.ndarray, K: int) -> np.nda
     t = (d[None, :, :, None].astype(np.float64) * sc[None].astype(np.float64) * S
          - dmin[None, :, :, None].astype(np.float64) * mn[None].astype(np.float64) * X[:, None])
     return t.sum(axis=(2, 3)) * x_scale.astype(np.float64)[:, None]
+
+
+def gemv_xblock(x_i8: np.ndarray, x_scale_blk: np.ndarray, w: np.ndarray, K: int) -> np.ndarray:
+    """y [M,N] float64 with one activation scale per 256-element block (x_scale_blk
+    [M, K/256]): sum_b x_scale_blk[m,b] * sum_{j in b}(d*sc_j*S_j - dmin*m_j*X_j).
+    Not in the reference (it has one scale per row, gemm_decode_dp4a.cu:398); the
+    per-block form of BASELINE config 4. Equals gemv() when every block of a row
+    carries the row's scale."""
+    d, dmin, sc, mn, q = fields(w, K)
+    N, nsb = d.shape
+    xs = x_i8.astype(np.float64).reshape(x_i8.shape[0], nsb, 8, 32)
+    S = np.einsum("mbjk,nbjk->mnbj", xs, q.astype(np.float64))
+    X = xs.sum(-1)
+    t = (d[None, :, :, None].astype(np.float64) * sc[None].astype(np.float64) * S
+         - dmin[None, :, :, None].astype(np.float64) * mn[None].astype(np.float64) * X[:, None])
+    return (t.sum(axis=3) * x_scale_blk.astype(np.float64)[:, None, :]).sum(axis=2)
+

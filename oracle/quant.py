@@ -66,6 +66,34 @@ def quantize_rows(xf: np.ndarray, scale_mul: float = 1.0):
     return q, (safe * np.float32(scale_mul)).astype(np.float32)
 
 
+def quantize_row_groups(xf: np.ndarray, rows: int, scale_mul: float = 1.0):
+    """One scale per `rows` consecutive rows (axis -2; the last group may be short)
+    of fp32 values xf[..., N, D]: the row-wise formula with the group's amax.
+    Returns (q int8 like xf, scale fp32 [..., N], each row holding its group's)."""
+    xf = np.asarray(xf, dtype=np.float32)
+    N = xf.shape[-2]
+    q = np.empty(xf.shape, np.int8)
+    sc = np.empty(xf.shape[:-1], np.float32)
+    for r0 in range(0, N, rows):
+        blk = xf[..., r0:r0 + rows, :]
+        flat = blk.reshape(blk.shape[:-2] + (-1,))
+        qq, ss = quantize_rows(flat, scale_mul)
+        q[..., r0:r0 + rows, :] = qq.reshape(blk.shape)
+        sc[..., r0:r0 + rows] = ss[..., None]
+    return q, sc
+
+
+def quantize_qk_per_wave(q: np.ndarray, k: np.ndarray, softmax_scale: float | None = None,
+                         q_rows: int = 32, k_rows: int = 64, dtype: str = "f16"):
+    """quantize_qk with per-tile scales (Q per q_rows queries, smoothed K per k_rows keys)."""
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(q.shape[-1])
+    k_s, mean = smooth_k(k, dtype)
+    q_i8, q_scale = quantize_row_groups(to_f32(q, dtype), q_rows, softmax_scale * LOG2E)
+    k_i8, k_scale = quantize_row_groups(k_s, k_rows)
+    return q_i8, q_scale, k_i8, k_scale, mean
+
+
 def k_mean(k: np.ndarray, dtype: str = "f16") -> np.ndarray:
     """fp32 per-channel mean over axis -2 of k[..., N, D] (reference core.py:29-44).
 

@@ -110,6 +110,31 @@ def quantize_rows_centered(x: torch.Tensor, mean: torch.Tensor | None, scale_mul
     return q, scale
 
 
+def quantize_row_groups(x: torch.Tensor, rows_per_group: int, mean: torch.Tensor | None = None,
+                        scale_mul: float = 1.0):
+    """int8 of x[..., N, D] with one scale per `rows_per_group` consecutive rows
+    (groups restart at every leading index; mean as quantize_rows_centered).
+    Returns (q int8 like x, scale fp32 [..., N]: each row holds its group's scale)."""
+    _check(x.is_cuda, "quantize expects a CUDA tensor")
+    _check(x.dtype in (torch.float16, torch.bfloat16, torch.float32),
+           "quantize input must be float16/bfloat16/float32")
+    _check(rows_per_group >= 1, "rows_per_group must be >= 1")
+    x = x.contiguous()
+    *lead, N, D = x.shape
+    G = math.prod(lead)
+    if mean is not None:
+        mean = mean.to(torch.float32).contiguous()
+        _check(mean.numel() == G * D, "mean shape mismatch")
+    q = torch.empty(x.shape, device=x.device, dtype=torch.int8)
+    scale = torch.empty((*lead, N), device=x.device, dtype=torch.float32)
+    if G and N and D:
+        with torch.cuda.device(x.device):
+            call("sl8_quantize_i8_row_groups", x.data_ptr(), dtype_code(x.dtype), G, N, D,
+                 int(rows_per_group), None if mean is None else mean.data_ptr(),
+                 float(scale_mul), q.data_ptr(), scale.data_ptr(), stream_of(x))
+    return q, scale
+
+
 def quantize_qk_fused(q: torch.Tensor, k: torch.Tensor, q_scale_mul: float,
                       gate_ratio: float = 0.0):
     """Fused fp16 prologue: q [B,Hq,M,D], k [B,Hkv,N,D] -> (q_i8, q_scale [B,Hq,M],
@@ -287,10 +312,13 @@ def choose_n_splits(n_len: int, batch: int, h_kv: int) -> int:
 
 def attn_int8_decode(q, q_scale, k, k_scale, v, num_splits=-1):
     """q int8 [B,Hq,1,D], q_scale fp32 [B,Hq,1], k int8 [B,Hkv,N,D], k_scale fp32
-    [B,Hkv,N], v fp16 [B,Hkv,N,D] -> fp16 [B,Hq,1,D]."""
+    [B,Hkv,N], v fp16 [B,Hkv,N,D] -> fp16 [B,Hq,1,D].
+
+    k_scale may also be fp16 (a cache with half-size per-token scales, BASELINE
+    config 3): the kernels widen it to fp32 exactly and compute as before."""
     _on_gpu(q, q_scale, k, k_scale, v)
     _check(q.dtype == torch.int8 and k.dtype == torch.int8, "decode: q/k must be int8")
-    _check(q_scale.dtype == torch.float32 and k_scale.dtype == torch.float32,
+    _check(q_scale.dtype == torch.float32 and k_scale.dtype in (torch.float32, torch.float16),
            "decode: scales must be float32")
     _check(v.dtype == torch.float16, "decode: v must be float16")
     _check(q.dim() == 4 and k.dim() == 4 and v.dim() == 4, "decode: expect [B,H,S,D]")
@@ -315,8 +343,9 @@ def attn_int8_decode(q, q_scale, k, k_scale, v, num_splits=-1):
     _check(1 <= ns <= DEC_MAX_SPLITS, f"decode: num_splits must be 1..{DEC_MAX_SPLITS}, got {ns}")
     ws_bytes = _lib.load().sl8_attn_int8_decode_workspace(B, H, D, ns)
     ws = torch.empty((ws_bytes,), device=q.device, dtype=torch.uint8)
+    fn = "sl8_attn_int8_decode_ks16" if k_scale.dtype == torch.float16 else "sl8_attn_int8_decode"
     with torch.cuda.device(q.device):
-        call("sl8_attn_int8_decode", q.data_ptr(), q_scale.data_ptr(), k.data_ptr(),
+        call(fn, q.data_ptr(), q_scale.data_ptr(), k.data_ptr(),
              k_scale.data_ptr(), v.data_ptr(), out.data_ptr(), B, H, Hkv, N, D, ns,
              ws.data_ptr(), ws_bytes, stream_of(q))
     return out
@@ -455,7 +484,7 @@ def kv_write_paged(k_new, v_new, slot_mapping, k_cache, k_scale, v_cache, v_scal
 # ---------------------------------------------------------------------------
 # Q4_K (reference csrc/kernel/gemm_dp4a.cu:146-193, gemm_decode_dp4a.cu:375-436)
 # ---------------------------------------------------------------------------
-def _q4k_checks(x, x_scale, w, out_dtype, tag, type_size=Q4K_TYPE_SIZE):
+def _q4k_checks(x, x_scale, w, out_dtype, tag, type_size=Q4K_TYPE_SIZE, x_block_ok=False):
     _on_gpu(x, x_scale, w)
     _check(x.dtype == torch.int8, "x must be int8")
     _check(w.dtype == torch.uint8, f"w must be uint8 (native {tag} bytes)")
@@ -469,7 +498,8 @@ def _q4k_checks(x, x_scale, w, out_dtype, tag, type_size=Q4K_TYPE_SIZE):
     _check(K % 256 == 0, f"{tag} contraction dim K must be %256==0, got {K}")
     _check(w.shape[1] == (K // 256) * type_size,
            f"{tag} weight must be [N, (K/256)*{type_size}], got [{N},{w.shape[1]}] for K={K}")
-    _check(x_scale.numel() == M, "x_scale must be [M]")
+    _check(x_scale.numel() == M or (x_block_ok and x_scale.shape == (M, K // 256)),
+           "x_scale must be [M]")
     return M, N, K
 
 
@@ -489,11 +519,33 @@ def gemm_q4k(x, x_scale, w, out_dtype=torch.float16):
 
 
 def gemm_decode_q4k(x, x_scale, w, out_dtype=torch.float16):
-    """Decode-shape (M <= 16) Q4_K GEMV; same math as gemm_q4k."""
+    """Decode-shape (M <= 16) Q4_K GEMV; same math as gemm_q4k.
+
+    x_scale [M] is the reference's per-row activation scale; x_scale [M, K/256]
+    (one scale per 256-element block, from quantize_i8_blockwise) scales each
+    super-block's integer sums instead (BASELINE config 4's activation format)."""
     _check(x.dim() == 2 and x.shape[0] <= DEC_MAX_M,
            f"gemm_decode_q4k supports M<={DEC_MAX_M}, got M={x.shape[0] if x.dim() else 0}"
            " -- use the tile gemm_q4k for prefill")
+    if x_scale.dim() == 2:
+        M, N, K = _q4k_checks(x, x_scale, w, out_dtype, "Q4_K", Q4K_TYPE_SIZE, x_block_ok=True)
+        out = torch.empty((M, N), device=x.device, dtype=out_dtype)
+        if M and N:
+            with torch.cuda.device(x.device):
+                call("sl8_gemm_decode_q4k_xblock", x.data_ptr(), x_scale.data_ptr(), w.data_ptr(),
+                     out.data_ptr(), dtype_code(out_dtype), M, N, K, stream_of(x))
+        return out
     return _q4k("sl8_gemm_decode_q4k", x, x_scale, w, out_dtype)
+
+
+def quantize_i8_blockwise(x: torch.Tensor, block: int = 256):
+    """x [M, K] -> (int8 [M, K], fp32 scale [M, K/block]): the row-wise quantiser
+    applied to every `block`-element slice of each row."""
+    _check(x.dim() == 2 and block > 0 and x.shape[1] % block == 0,
+           f"quantize_i8_blockwise expects x[M,K] with K % {block} == 0")
+    M, K = x.shape
+    q, s = quantize_i8_rowwise(x.contiguous().reshape(M * (K // block), block))
+    return q.reshape(M, K), s.reshape(M, K // block)
 
 
 def gemm_q5k(x, x_scale, w, out_dtype=torch.float16):

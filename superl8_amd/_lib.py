@@ -28,6 +28,7 @@ SIGNATURES = {
     "sl8_k_mean_workspace": (_SZ, [_I64, _I64]),
     "sl8_k_mean": (_I, [_P, _I, _I64, _I64, _I64, _P, _P, _SZ, _P]),
     "sl8_quantize_i8_rows_centered": (_I, [_P, _I, _I64, _I64, _I64, _P, _F, _P, _P, _P]),
+    "sl8_quantize_i8_row_groups": (_I, [_P, _I, _I64, _I64, _I64, _I64, _P, _F, _P, _P, _P]),
     "sl8_quantize_qk_workspace": (_SZ, [_I64, _I64, _I64, _I64]),
     "sl8_quantize_qk": (_I, [_P, _P, _I, _I64, _I64, _I64, _I64, _F, _F, _P, _P, _P, _P, _P, _P,
                              _P, _SZ, _P]),
@@ -43,6 +44,8 @@ SIGNATURES = {
     "sl8_attn_int8_decode_workspace": (_SZ, [_I64, _I64, _I64, _I64]),
     "sl8_attn_int8_decode": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
                                   _P, _SZ, _P]),
+    "sl8_attn_int8_decode_ks16": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
+                                       _P, _SZ, _P]),
     "sl8_attn_int8_decode_noalloc_max_bytes": (_SZ, []),
     "sl8_attn_int8_decode_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
                                           _I64, _P]),
@@ -54,6 +57,7 @@ SIGNATURES = {
                                    _I64, _I64, _I64, _I64, _I64, _P, _SZ, _P]),
     "sl8_kv_write_paged": (_I, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P]),
     "sl8_gemm_decode_q4k": (_I, [_P, _P, _P, _P, _I, _I64, _I64, _I64, _P]),
+    "sl8_gemm_decode_q4k_xblock": (_I, [_P, _P, _P, _P, _I, _I64, _I64, _I64, _P]),
     "sl8_gemm_q4k": (_I, [_P, _P, _P, _P, _I, _I64, _I64, _I64, _P]),
     "sl8_dequant_q4k": (_I, [_P, _P, _I64, _I64, _P]),
     "sl8_gemm_q5k": (_I, [_P, _P, _P, _P, _I, _I64, _I64, _I64, _P]),

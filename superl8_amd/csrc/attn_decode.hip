@@ -64,10 +64,18 @@ struct PagedArgs {
 // block-table entries of one split staged in LDS by the streaming paged kernel
 constexpr int DEC_BT_MAX = 1024;
 
-template <int D, int G, bool VI8, bool PG>
+// Per-token K scale of key row r: fp32 (the reference contract) or, with
+// KS16, fp16 (half the scale bytes; BASELINE config 3's cache format).
+template <bool KS16>
+__device__ __forceinline__ float load_ks(const void* base, int64_t r) {
+  if constexpr (KS16) return h2f(static_cast<const uint16_t*>(base)[r]);
+  else return static_cast<const float*>(base)[r];
+}
+
+template <int D, int G, bool VI8, bool PG, bool KS16 = false>
 __global__ void __launch_bounds__(DEC_THREADS)
 decode_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_scale,
-                    const int8_t* __restrict__ k, const float* __restrict__ k_scale,
+                    const int8_t* __restrict__ k, const void* __restrict__ k_scale,
                     const void* __restrict__ v, const float* __restrict__ vsc,
                     float* __restrict__ o_part,
                     float* __restrict__ m_part, float* __restrict__ l_part, int n_len,
@@ -114,7 +122,8 @@ decode_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sc
     else return n;
   };
   const int8_t* kb = k + (PG ? 0 : (int64_t)bkv * n_len * D);
-  const float* ksb = k_scale + (PG ? 0 : (int64_t)bkv * n_len);
+  const void* ksb = static_cast<const uint8_t*>(k_scale) +
+                    (PG ? 0 : (int64_t)bkv * n_len * (KS16 ? 2 : 4));
   constexpr int VES = VI8 ? 1 : 2;  // V element bytes
   const uint8_t* vb = static_cast<const uint8_t*>(v) + (PG ? 0 : (int64_t)bkv * n_len * D * VES);
 
@@ -139,7 +148,7 @@ decode_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sc
       const int4* kp = reinterpret_cast<const int4*>(kb + kr_row * D);
 #pragma unroll
       for (int c = 0; c < D / 16; ++c) kr[c] = kp[c];
-      const float ks = valid ? ksb[kr_row] : 0.f;
+      const float ks = valid ? load_ks<KS16>(ksb, kr_row) : 0.f;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         int acc = 0;
@@ -410,10 +419,10 @@ struct WaveCfg {
 // PG: paged int8 cache (see PagedArgs): the split's block-table entries are
 // staged in LDS, every copy lane maps its key to a physical row, and the
 // per-token V scale multiplies p before it is broadcast to the PV lanes.
-template <int D, int GS, int NB, bool VI8, bool PG>
+template <int D, int GS, int NB, bool VI8, bool PG, bool KS16 = false>
 __global__ void __launch_bounds__(DEC_THREADS)
 decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_scale,
-                   const int8_t* __restrict__ k, const float* __restrict__ k_scale,
+                   const int8_t* __restrict__ k, const void* __restrict__ k_scale,
                    const void* __restrict__ v, const float* __restrict__ vsc,
                    float* __restrict__ o_part,
                    float* __restrict__ m_part, float* __restrict__ l_part, int n_len,
@@ -450,7 +459,8 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
   const int ntiles = n1 > n0 ? (n1 - n0 + T - 1) / T : 0;
   const int nt = ntiles > wave ? (ntiles - wave + DEC_WAVES - 1) / DEC_WAVES : 0;  // this wave's
   const int8_t* kb = k + (PG ? 0 : (int64_t)bkv * n_len * D);
-  const float* ksb = k_scale + (PG ? 0 : (int64_t)bkv * n_len);
+  constexpr int KSB = KS16 ? 2 : 4;  // K scale bytes per key
+  const uint8_t* ksb = static_cast<const uint8_t*>(k_scale) + (PG ? 0 : (int64_t)bkv * n_len * KSB);
   const uint8_t* vb = static_cast<const uint8_t*>(v) + (PG ? 0 : (int64_t)bkv * n_len * C::VRB);
   __shared__ int32_t sm_bt[PG ? DEC_BT_MAX : 1];
   const int first_blk = PG ? (n0 >> pg.bs_sh) : 0;
@@ -497,7 +507,10 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
     }
     // lanes past the tile repeat its keys (same cache lines: no extra traffic)
     const int64_t sr = crow(base + (lane % T));
-    __builtin_amdgcn_global_load_lds((gptr_t)(ksb + sr), (lptr_t)(sb + C::KBYTES + C::VBYTES), 4, 0, 0);
+    if constexpr (KS16)
+      __builtin_amdgcn_global_load_lds((gptr_t)(ksb + sr * 2), (lptr_t)(sb + C::KBYTES + C::VBYTES), 2, 0, 0);
+    else
+      __builtin_amdgcn_global_load_lds((gptr_t)(ksb + sr * 4), (lptr_t)(sb + C::KBYTES + C::VBYTES), 4, 0, 0);
     if constexpr (PG)
       __builtin_amdgcn_global_load_lds((gptr_t)(vsc + sr), (lptr_t)(sb + C::KBYTES + C::VBYTES + 256),
                                        4, 0, 0);
@@ -526,7 +539,9 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
         acc = __builtin_amdgcn_sdot4(qv[4 * c + 2], kr.z, acc, false);
         acc = __builtin_amdgcn_sdot4(qv[4 * c + 3], kr.w, acc, false);
       }
-      s[u] = (base + r < n1) ? ((float)acc * qsc) * kst[r] : -INFINITY;
+      // a 2-byte LDS DMA still fills one dword per lane (the value zero-extended)
+      const float ksr = KS16 ? h2f(reinterpret_cast<const uint32_t*>(kst)[r] & 0xFFFFu) : kst[r];
+      s[u] = (base + r < n1) ? ((float)acc * qsc) * ksr : -INFINITY;
       mx = fmaxf(mx, s[u]);
     }
 #pragma unroll
@@ -755,21 +770,21 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
   }
 }
 
-template <int D, int G, bool VI8, bool PG>
-void launch_split(dim3 grid, const int8_t* q, const float* qs, const int8_t* k, const float* ks,
+template <int D, int G, bool VI8, bool PG, bool KS16>
+void launch_split(dim3 grid, const int8_t* q, const float* qs, const int8_t* k, const void* ks,
                   const void* v, const float* vsc, float* op, float* mp, float* lp, int N, int ns,
                   int hq, int hkv, int gsz, int bhq, const PagedArgs& pg, hipStream_t st) {
-  decode_split_kernel<D, G, VI8, PG><<<grid, DEC_THREADS, 0, st>>>(q, qs, k, ks, v, vsc, op, mp, lp,
-                                                                   N, ns, hq, hkv, gsz, bhq, pg);
+  decode_split_kernel<D, G, VI8, PG, KS16><<<grid, DEC_THREADS, 0, st>>>(
+      q, qs, k, ks, v, vsc, op, mp, lp, N, ns, hq, hkv, gsz, bhq, pg);
 }
 
-template <int D, bool VI8, bool PG = false>
+template <int D, bool VI8, bool PG = false, bool KS16 = false>
 void launch_d(int G, dim3 grid, const int8_t* q, const float* qs, const int8_t* k,
-              const float* ks, const void* v, const float* vsc, float* op, float* mp, float* lp,
+              const void* ks, const void* v, const float* vsc, float* op, float* mp, float* lp,
               int N, int ns, int hq, int hkv, int gsz, int bhq, hipStream_t st,
               const PagedArgs& pg = PagedArgs{nullptr, nullptr, 0, 1, 0}) {
 #define SL8_SPLIT(GG) \
-  launch_split<D, GG, VI8, PG>(grid, q, qs, k, ks, v, vsc, op, mp, lp, N, ns, hq, hkv, gsz, bhq, pg, st)
+  launch_split<D, GG, VI8, PG, KS16>(grid, q, qs, k, ks, v, vsc, op, mp, lp, N, ns, hq, hkv, gsz, bhq, pg, st)
   switch (G) {
     case 1: SL8_SPLIT(1); break;
     case 2: SL8_SPLIT(2); break;
@@ -809,8 +824,9 @@ namespace sl8 {
 namespace {
 
 // Split kernels + combine. v: fp16 [B,Hkv,N,D], or int8 with vsc [B,Hkv,D] (VI8).
-template <bool VI8>
-int decode_launch(const int8_t* q, const float* q_scale, const int8_t* k, const float* k_scale,
+// k_scale: fp32 per key, or fp16 with KS16.
+template <bool VI8, bool KS16 = false>
+int decode_launch(const int8_t* q, const float* q_scale, const int8_t* k, const void* k_scale,
                   const void* v, const float* vsc, void* out, int64_t B, int64_t Hq, int64_t Hkv,
                   int64_t N, int64_t D, int64_t num_splits, void* workspace, hipStream_t st) {
   const int ns = (int)num_splits, bhq = (int)(B * Hq), gsz = (int)(Hq / Hkv);
@@ -824,7 +840,7 @@ int decode_launch(const int8_t* q, const float* q_scale, const int8_t* k, const 
   if (D != 32 && ((gsz == 2 && D == 128) || gsz == 4 || gsz == 8)) {
     const dim3 g2((unsigned)ns, (unsigned)(B * Hkv));
 #define SL8_WAVE(DD, GS, NB)                                                                     \
-    decode_wave_kernel<DD, GS, NB, VI8, false><<<g2, DEC_THREADS, 0, st>>>(                    \
+    decode_wave_kernel<DD, GS, NB, VI8, false, KS16><<<g2, DEC_THREADS, 0, st>>>(                    \
         q, q_scale, k, k_scale, v, vsc, op, mp, lp, (int)N, ns, (int)Hq, (int)Hkv, bhq,       \
         PagedArgs{nullptr, nullptr, 0, 1, 0})
 #define SL8_WAVE_D(GS)                         \
@@ -839,10 +855,10 @@ int decode_launch(const int8_t* q, const float* q_scale, const int8_t* k, const 
 #undef SL8_WAVE_D
 #undef SL8_WAVE
   } else switch (D) {
-    case 32: launch_d<32, VI8>(G, grid, q, q_scale, k, k_scale, v, vsc, op, mp, lp, (int)N, ns, (int)Hq, (int)Hkv, gsz, bhq, st); break;
-    case 64: launch_d<64, VI8>(G, grid, q, q_scale, k, k_scale, v, vsc, op, mp, lp, (int)N, ns, (int)Hq, (int)Hkv, gsz, bhq, st); break;
-    case 128: launch_d<128, VI8>(G, grid, q, q_scale, k, k_scale, v, vsc, op, mp, lp, (int)N, ns, (int)Hq, (int)Hkv, gsz, bhq, st); break;
-    default: launch_d<256, VI8>(G, grid, q, q_scale, k, k_scale, v, vsc, op, mp, lp, (int)N, ns, (int)Hq, (int)Hkv, gsz, bhq, st); break;
+    case 32: launch_d<32, VI8, false, KS16>(G, grid, q, q_scale, k, k_scale, v, vsc, op, mp, lp, (int)N, ns, (int)Hq, (int)Hkv, gsz, bhq, st); break;
+    case 64: launch_d<64, VI8, false, KS16>(G, grid, q, q_scale, k, k_scale, v, vsc, op, mp, lp, (int)N, ns, (int)Hq, (int)Hkv, gsz, bhq, st); break;
+    case 128: launch_d<128, VI8, false, KS16>(G, grid, q, q_scale, k, k_scale, v, vsc, op, mp, lp, (int)N, ns, (int)Hq, (int)Hkv, gsz, bhq, st); break;
+    default: launch_d<256, VI8, false, KS16>(G, grid, q, q_scale, k, k_scale, v, vsc, op, mp, lp, (int)N, ns, (int)Hq, (int)Hkv, gsz, bhq, st); break;
   }
   SL8_CHECK_LAUNCH("attn_int8_decode split");
   launch_combine((int)D, bhq, st, op, mp, lp, static_cast<uint16_t*>(out), ns, bhq);
@@ -878,6 +894,37 @@ extern "C" int sl8_attn_int8_decode(const int8_t* q, const float* q_scale, const
                 "fni8 decode: workspace needs %zu bytes", need);
   return decode_launch<false>(q, q_scale, k, k_scale, v, nullptr, out, B, Hq, Hkv, N, D,
                               num_splits, workspace, static_cast<hipStream_t>(stream));
+}
+
+// fp16 per-token K scales (BASELINE config 3's cache format: half the scale
+// bytes of the reference's fp32 contract, attn_decode.cu:174-175). Otherwise
+// identical to sl8_attn_int8_decode: the scale is widened to fp32 exactly
+// before the same arithmetic.
+extern "C" int sl8_attn_int8_decode_ks16(const int8_t* q, const float* q_scale, const int8_t* k,
+                                         const void* k_scale_f16, const void* v, void* out,
+                                         int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                                         int64_t num_splits, void* workspace,
+                                         size_t workspace_bytes, void* stream) {
+  clear_error();
+  SL8_CHECK_ARG(B >= 0 && Hq >= 0 && Hkv > 0 && N >= 0, "fni8 decode: bad shape");
+  SL8_CHECK_ARG(Hq % Hkv == 0, "fni8 decode: H_q must be divisible by H_kv (GQA)");
+  SL8_CHECK_ARG(D == 32 || D == 64 || D == 128 || D == 256,
+                "fni8 decode: head dim must be 32/64/128/256, got %lld", (long long)D);
+  if (num_splits < 0) num_splits = sl8_choose_num_splits(N, B, Hkv);
+  SL8_CHECK_ARG(num_splits >= 1 && num_splits <= DEC_MAX_SPLITS,
+                "fni8 decode: num_splits must be 1..%d, got %lld", DEC_MAX_SPLITS,
+                (long long)num_splits);
+  SL8_CHECK_ARG(B * Hq < (1LL << 31) && N < (1LL << 31), "fni8 decode: shape too large");
+  if (B == 0 || Hq == 0) return SL8_OK;
+  SL8_CHECK_ARG(N > 0, "fni8 decode: empty KV cache (the caller zero-fills the output)");
+  SL8_CHECK_ARG(q && q_scale && k && k_scale_f16 && v && out, "fni8 decode: null pointer");
+  SL8_CHECK_ARG(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(k_scale_f16, 2),
+                "fni8 decode: q/k/v must be 16-byte aligned");
+  const size_t need = sl8_attn_int8_decode_workspace(B, Hq, D, num_splits);
+  SL8_CHECK_ARG(workspace && workspace_bytes >= need && aligned(workspace, 16),
+                "fni8 decode: workspace needs %zu bytes", need);
+  return decode_launch<false, true>(q, q_scale, k, k_scale_f16, v, nullptr, out, B, Hq, Hkv, N, D,
+                                    num_splits, workspace, static_cast<hipStream_t>(stream));
 }
 
 // ---------------------------------------------------------------------------

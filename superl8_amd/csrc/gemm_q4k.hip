@@ -78,12 +78,19 @@ __device__ __forceinline__ uint32_t lane_pull(uint32_t v, int src_lane) {
 // element l of sub-block j, so the operand lane of elements 16(h&1)..+15
 // pulls qh bytes 16(h&1)..+15 of its row and the B operand is the code
 // q = n + 16 b <= 31 (exact in int8); scales and mins as Q4_K.
-template <int OUT_DT, int MT, int FMT = 4>
-__global__ void __launch_bounds__(64 * GWAVES, MT == 1 ? (FMT == 4 ? 5 : 4) : 1)
+// TPW = 16-row weight tiles per workgroup. The launcher uses 1: with 2 (each
+// wave loads both tiles' weights before its single wait, the activation slice
+// is staged once per 32 rows and the whole grid is resident at once) config 4
+// at M = 8 measured 19.9 us against 17.3 us -- every wave then loads and
+// computes in the same phase, so no compute overlaps the memory stream. XB: the
+// activations carry one scale per 256-element block (x_scale [M, K/256],
+// applied per super-block) instead of one per row.
+template <int OUT_DT, int MT, int FMT = 4, int TPW = 1, bool XB = false>
+__global__ void __launch_bounds__(64 * GWAVES, TPW == 2 ? 3 : (MT == 1 ? (FMT == 4 ? 5 : 4) : 1))
 gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
                 const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K) {
   extern __shared__ __attribute__((aligned(16))) int8_t xl[];  // per wave: [M][GXPITCH]
-  __shared__ float red[GWAVES - 1][MT][32][4];
+  __shared__ float red[GWAVES - 1][TPW][MT][32][4];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -93,17 +100,19 @@ gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
   const int hp = h >> 1;     // sub-block parity of this lane's k-slots and C rows
   const int lr = lane >> 2, lc = lane & 3;  // load role: weight row, 16-byte piece
   const int src_q = 4 * lj + h;             // lane holding (row lj, piece h)
-  const int n0 = blockIdx.x * GEMV_ROWS;
+  const int n0 = blockIdx.x * GEMV_ROWS * TPW;
   constexpr int BB = FMT == 4 ? Q4K_BYTES : 176;  // bytes per super-block
   constexpr int QS = FMT == 4 ? 16 : 48;          // offset of the nibbles
   const int64_t row_bytes = (int64_t)nsb * BB;
-  const uint8_t* wrow = w + (int64_t)min(n0 + lr, N - 1) * row_bytes;
+  const uint8_t* wrow[TPW];
+#pragma unroll
+  for (int tt = 0; tt < TPW; ++tt)
+    wrow[tt] = w + (int64_t)min(n0 + GEMV_ROWS * tt + lr, N - 1) * row_bytes;
   const int a_m = lj & 7;    // A-operand row: activation t*8 + a_m, parity lj >> 3
   const bool a_side = (lj >> 3) == hp;  // this lane's k-slots feed its A row
   bool a_on[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) a_on[t] = a_side && (t * 8 + a_m < M);
-  // per-wave area rounded up to whole 1 KiB copies (a copy writes 64 x 16 B)
   // per wave: M activation rows rounded up to whole 1 KiB copies (a copy
   // writes 64 x 16 B, the last one past row M - 1), then one row of zeros
   // that the lanes whose A-operand row is unused read instead (no select
@@ -113,54 +122,76 @@ gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
   int8_t* xz = xw + xarea;
   for (int i = lane; i < GXPITCH / 16; i += 64) reinterpret_cast<uint4*>(xz)[i] = make_uint4(0, 0, 0, 0);
 
-  float f[MT][4];
+  float f[TPW][MT][4];
 #pragma unroll
-  for (int t = 0; t < MT; ++t)
+  for (int tt = 0; tt < TPW; ++tt)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) f[t][r] = 0.f;
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) f[tt][t][r] = 0.f;
 
   // One chunk of up to GCH super-blocks starting at c0.
   auto chunk = [&](const int c0, const int cnt) {
-    // ---- weights: header dword lc and two 16-byte nibble pieces per super-block ----
-    uint32_t hd[GCH];
-    uint4 qa[GCH], qb[GCH];
-    uint2 qh8[FMT == 5 ? GCH : 1];  // Q5_K: qh bytes 8 lc .. 8 lc + 7 of the row
-#pragma unroll
-    for (int i = 0; i < GCH; ++i) {
-      const uint8_t* blk = wrow + (int64_t)min(c0 + i, nsb - 1) * BB;
-      hd[i] = *reinterpret_cast<const uint32_t*>(blk + 4 * lc);
-      qa[i] = *reinterpret_cast<const uint4*>(blk + QS + 16 * lc);
-      qb[i] = *reinterpret_cast<const uint4*>(blk + QS + 64 + 16 * lc);
-      if constexpr (FMT == 5) qh8[i] = *reinterpret_cast<const uint2*>(blk + 16 + 8 * lc);
-    }
     // ---- activations of the chunk: M rows x cnt*256 bytes -> this wave's LDS area ----
-    const int xch = M * (GXPITCH / 16);
-    for (int j = 0; j * 64 < xch; ++j) {
-      const int id = min(j * 64 + lane, xch - 1);
-      const int m = id / (GXPITCH / 16), pos = min(id % (GXPITCH / 16), cnt * 16 - 1);
-      __builtin_amdgcn_global_load_lds((q4_gptr_t)(x + (int64_t)m * K + (int64_t)c0 * 256 + 16 * pos),
-                                       (q4_lptr_t)(xw + j * 1024), 16, 0, 0);
+    // (issued after the weights: issuing them first measured slower)
+    auto stage_x = [&]() {
+      const int xch = M * (GXPITCH / 16);
+      for (int j = 0; j * 64 < xch; ++j) {
+        const int id = min(j * 64 + lane, xch - 1);
+        const int m = id / (GXPITCH / 16), pos = min(id % (GXPITCH / 16), cnt * 16 - 1);
+        __builtin_amdgcn_global_load_lds((q4_gptr_t)(x + (int64_t)m * K + (int64_t)c0 * 256 + 16 * pos),
+                                         (q4_lptr_t)(xw + j * 1024), 16, 0, 0);
+      }
+    };
+    // ---- weights: header dword lc and two 16-byte nibble pieces per super-block ----
+    uint32_t hd[TPW][GCH];
+    uint4 qa[TPW][GCH], qb[TPW][GCH];
+    uint2 qh8[TPW][FMT == 5 ? GCH : 1];  // Q5_K: qh bytes 8 lc .. 8 lc + 7 of the row
+#pragma unroll
+    for (int tt = 0; tt < TPW; ++tt)
+#pragma unroll
+      for (int i = 0; i < GCH; ++i) {
+        const uint8_t* blk = wrow[tt] + (int64_t)min(c0 + i, nsb - 1) * BB;
+        hd[tt][i] = *reinterpret_cast<const uint32_t*>(blk + 4 * lc);
+        qa[tt][i] = *reinterpret_cast<const uint4*>(blk + QS + 16 * lc);
+        qb[tt][i] = *reinterpret_cast<const uint4*>(blk + QS + 64 + 16 * lc);
+        if constexpr (FMT == 5) qh8[tt][i] = *reinterpret_cast<const uint2*>(blk + 16 + 8 * lc);
+      }
+    stage_x();
+    // per-block activation scales of this lane's C rows (XB)
+    float xsb[MT][4][GCH];
+    if constexpr (XB) {
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = min(t * 8 + 4 * (h & 1) + r, M - 1);
+#pragma unroll
+          for (int i = 0; i < GCH; ++i) xsb[t][r][i] = x_scale[(int64_t)m * nsb + min(c0 + i, nsb - 1)];
+        }
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): weights and activations landed
+#pragma unroll
+    for (int tt = 0; tt < TPW; ++tt)
 #pragma unroll
     for (int i = 0; i < GCH; ++i) {
       if (i < cnt) {
         // ---- pieces to the operand layout ----
-        const uint32_t h0 = lane_pull(hd[i], 4 * lj + 0), h1 = lane_pull(hd[i], 4 * lj + 1);
-        const uint32_t h2 = lane_pull(hd[i], 4 * lj + 2), h3 = lane_pull(hd[i], 4 * lj + 3);
+        const uint32_t h0 = lane_pull(hd[tt][i], 4 * lj + 0), h1 = lane_pull(hd[tt][i], 4 * lj + 1);
+        const uint32_t h2 = lane_pull(hd[tt][i], 4 * lj + 2), h3 = lane_pull(hd[tt][i], 4 * lj + 3);
         uint32_t qw[2][4];
-        qw[0][0] = lane_pull(qa[i].x, src_q); qw[0][1] = lane_pull(qa[i].y, src_q);
-        qw[0][2] = lane_pull(qa[i].z, src_q); qw[0][3] = lane_pull(qa[i].w, src_q);
-        qw[1][0] = lane_pull(qb[i].x, src_q); qw[1][1] = lane_pull(qb[i].y, src_q);
-        qw[1][2] = lane_pull(qb[i].z, src_q); qw[1][3] = lane_pull(qb[i].w, src_q);
+        qw[0][0] = lane_pull(qa[tt][i].x, src_q); qw[0][1] = lane_pull(qa[tt][i].y, src_q);
+        qw[0][2] = lane_pull(qa[tt][i].z, src_q); qw[0][3] = lane_pull(qa[tt][i].w, src_q);
+        qw[1][0] = lane_pull(qb[tt][i].x, src_q); qw[1][1] = lane_pull(qb[tt][i].y, src_q);
+        qw[1][2] = lane_pull(qb[tt][i].z, src_q); qw[1][3] = lane_pull(qb[tt][i].w, src_q);
         const ScMin sm = unpack_scmin(h1, h2, h3);
         uint32_t qhw[4] = {0, 0, 0, 0};  // Q5_K: qh bytes 16(h&1) .. +15 of row lj
         if constexpr (FMT == 5) {
           const int s0 = 4 * lj + 2 * (h & 1);
-          qhw[0] = lane_pull(qh8[i].x, s0);
-          qhw[1] = lane_pull(qh8[i].y, s0);
-          qhw[2] = lane_pull(qh8[i].x, s0 + 1);
-          qhw[3] = lane_pull(qh8[i].y, s0 + 1);
+          qhw[0] = lane_pull(qh8[tt][i].x, s0);
+          qhw[1] = lane_pull(qh8[tt][i].y, s0);
+          qhw[2] = lane_pull(qh8[tt][i].x, s0 + 1);
+          qhw[3] = lane_pull(qh8[tt][i].y, s0 + 1);
         }
         int T[MT][4];
         v4i U[MT];
@@ -206,7 +237,11 @@ gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
 #pragma unroll
         for (int t = 0; t < MT; ++t)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) f[t][r] += d * (float)T[t][r] - dmin * (float)U[t][r];
+          for (int r = 0; r < 4; ++r) {
+            const float part = d * (float)T[t][r] - dmin * (float)U[t][r];
+            if constexpr (XB) f[tt][t][r] += xsb[t][r][i] * part;
+            else f[tt][t][r] += part;
+          }
       }
     }
     __builtin_amdgcn_wave_barrier();  // the next chunk's copies overwrite xw
@@ -223,27 +258,33 @@ gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
   // C row i = 4h + r holds activation row t*8 + (i & 7) of sub-block parity i >> 3:
   // add the two parities (lanes h and h^2), then the K quarters, in fixed order.
 #pragma unroll
-  for (int t = 0; t < MT; ++t)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) f[t][r] += __shfl_xor(f[t][r], 32, 64);
-  if (wave > 0 && lane < 32) {
+  for (int tt = 0; tt < TPW; ++tt)
 #pragma unroll
     for (int t = 0; t < MT; ++t)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) red[wave - 1][t][lane][r] = f[t][r];
+      for (int r = 0; r < 4; ++r) f[tt][t][r] += __shfl_xor(f[tt][t][r], 32, 64);
+  if (wave > 0 && lane < 32) {
+#pragma unroll
+    for (int tt = 0; tt < TPW; ++tt)
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[wave - 1][tt][t][lane][r] = f[tt][t][r];
   }
   __syncthreads();
   if (wave == 0 && lane < 32) {
 #pragma unroll
-    for (int t = 0; t < MT; ++t)
+    for (int tt = 0; tt < TPW; ++tt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float v = f[t][r];
+      for (int t = 0; t < MT; ++t)
 #pragma unroll
-        for (int wv = 0; wv < GWAVES - 1; ++wv) v += red[wv][t][lane][r];
-        const int m = t * 8 + 4 * (h & 1) + r, gn = n0 + lj;
-        if (m < M && gn < N) st_out<OUT_DT>(out, (int64_t)m * N + gn, v * x_scale[m]);
-      }
+        for (int r = 0; r < 4; ++r) {
+          float v = f[tt][t][r];
+#pragma unroll
+          for (int wv = 0; wv < GWAVES - 1; ++wv) v += red[wv][tt][t][lane][r];
+          const int m = t * 8 + 4 * (h & 1) + r, gn = n0 + GEMV_ROWS * tt + lj;
+          if (m < M && gn < N) st_out<OUT_DT>(out, (int64_t)m * N + gn, XB ? v : v * x_scale[m]);
+        }
   }
 }
 
@@ -280,7 +321,7 @@ constexpr int SXPITCH = SCH * 256;
 #ifndef SL8_GEMV_SOCC
 #define SL8_GEMV_SOCC 8
 #endif
-template <int OUT_DT, int MR>
+template <int OUT_DT, int MR, bool XB = false>
 __global__ void __launch_bounds__(64 * SWAVES, (SL8_GEMV_SOCC > 0 && MR == 1) ? SL8_GEMV_SOCC : 1)
 gemv_q4k_small_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
                       const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K) {
@@ -385,7 +426,9 @@ gemv_q4k_small_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_
           const int T = __mul24(sc0, p0) + __mul24(sc1, p1) + __mul24(sc4, p4) + __mul24(sc5, p5);
           const int U = __mul24(mn0, s01.x) + __mul24(mn1, s01.y) + __mul24(mn4, s45.x) +
                         __mul24(mn5, s45.y);
-          f[m] += d * (float)T - dmin * (float)U;
+          const float part = d * (float)T - dmin * (float)U;
+          if constexpr (XB) f[m] += x_scale[(int64_t)m * nsb + c0 + i] * part;  // per-256-block scale
+          else f[m] += part;
         }
       }
     }
@@ -417,7 +460,7 @@ gemv_q4k_small_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_
 #pragma unroll
       for (int wv = 0; wv < SWAVES - 1; ++wv) v += red[wv][r][m];
       const int gn = n0 + r;
-      if (m < M && gn < N) st_out<OUT_DT>(out, (int64_t)m * N + gn, v * x_scale[m]);
+      if (m < M && gn < N) st_out<OUT_DT>(out, (int64_t)m * N + gn, XB ? v : v * x_scale[m]);
     }
   }
 }
@@ -603,39 +646,38 @@ __global__ void dequant_q4k_kernel(const uint8_t* __restrict__ w, float* __restr
   for (int e = 0; e < 32; ++e) o[e] = dsc * (float)((qs[e] >> shift) & 0xF) - dm;
 }
 
-template <int MR>
+template <int MR, bool XB = false>
 void launch_gemv_small(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
                        int M, int N, int K, hipStream_t st) {
   const dim3 grid((unsigned)((N + GEMV_ROWS - 1) / GEMV_ROWS));
   switch (odt) {
     case SL8_DTYPE_F16:
-      gemv_q4k_small_kernel<SL8_DTYPE_F16, MR><<<grid, 64 * SWAVES, 0, st>>>(x, xs, w, out, M, N, K);
+      gemv_q4k_small_kernel<SL8_DTYPE_F16, MR, XB><<<grid, 64 * SWAVES, 0, st>>>(x, xs, w, out, M, N, K);
       break;
     case SL8_DTYPE_BF16:
-      gemv_q4k_small_kernel<SL8_DTYPE_BF16, MR><<<grid, 64 * SWAVES, 0, st>>>(x, xs, w, out, M, N, K);
+      gemv_q4k_small_kernel<SL8_DTYPE_BF16, MR, XB><<<grid, 64 * SWAVES, 0, st>>>(x, xs, w, out, M, N, K);
       break;
     default:
-      gemv_q4k_small_kernel<SL8_DTYPE_F32, MR><<<grid, 64 * SWAVES, 0, st>>>(x, xs, w, out, M, N, K);
+      gemv_q4k_small_kernel<SL8_DTYPE_F32, MR, XB><<<grid, 64 * SWAVES, 0, st>>>(x, xs, w, out, M, N, K);
       break;
   }
 }
 
-template <int MT>
+template <int MT, bool XB = false>
 void launch_gemv_mt(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
                     int M, int N, int K, hipStream_t st) {
   const dim3 grid((unsigned)((N + GEMV_ROWS - 1) / GEMV_ROWS));
   const size_t lds = (size_t)GWAVES * ((((size_t)M * GXPITCH + 1023) & ~(size_t)1023) + GXPITCH);
-  switch (odt) {
-    case SL8_DTYPE_F16:
-      gemv_q4k_kernel<SL8_DTYPE_F16, MT><<<grid, 64 * GWAVES, lds, st>>>(x, xs, w, out, M, N, K);
-      break;
-    case SL8_DTYPE_BF16:
-      gemv_q4k_kernel<SL8_DTYPE_BF16, MT><<<grid, 64 * GWAVES, lds, st>>>(x, xs, w, out, M, N, K);
-      break;
-    default:
-      gemv_q4k_kernel<SL8_DTYPE_F32, MT><<<grid, 64 * GWAVES, lds, st>>>(x, xs, w, out, M, N, K);
-      break;
+#define SL8_GM(DT, TP) gemv_q4k_kernel<DT, MT, 4, TP, XB><<<grid, 64 * GWAVES, lds, st>>>(x, xs, w, out, M, N, K)
+#define SL8_GM_DT(TP)                                   \
+  switch (odt) {                                        \
+    case SL8_DTYPE_F16: SL8_GM(SL8_DTYPE_F16, TP); break;   \
+    case SL8_DTYPE_BF16: SL8_GM(SL8_DTYPE_BF16, TP); break; \
+    default: SL8_GM(SL8_DTYPE_F32, TP); break;             \
   }
+  SL8_GM_DT(1)
+#undef SL8_GM_DT
+#undef SL8_GM
 }
 
 }  // namespace
@@ -699,6 +741,29 @@ extern "C" int sl8_gemm_decode_q4k(const int8_t* x, const float* x_scale, const 
   else if (M <= 8) launch_gemv_mt<1>(x, x_scale, w, out, out_dtype, (int)M, (int)N, (int)K, st);
   else launch_gemv_mt<2>(x, x_scale, w, out, out_dtype, (int)M, (int)N, (int)K, st);
   SL8_CHECK_LAUNCH("gemm_decode_q4k");
+  return SL8_OK;
+}
+
+// Decode GEMV with one activation scale per 256-element block (BASELINE
+// config 4's activation format): x_scale [M, K/256] multiplies each
+// super-block's exact integer sums instead of the row total.
+extern "C" int sl8_gemm_decode_q4k_xblock(const int8_t* x, const float* x_scale, const uint8_t* w,
+                                          void* out, int out_dtype, int64_t M, int64_t N, int64_t K,
+                                          void* stream) {
+  clear_error();
+  int rc = check_q4k(x, x_scale, w, out, out_dtype, M, N, K);
+  if (rc != SL8_OK || M == 0 || N == 0 || K == 0) return rc;
+  SL8_CHECK_ARG(M <= 16, "gemm_decode_q4k supports M<=16, got M=%lld -- use the tile gemm_q4k for prefill",
+                (long long)M);
+  SL8_CHECK_ARG(K <= kMaxGemvK, "gemm_decode_q4k: K=%lld exceeds %lld", (long long)K,
+                (long long)kMaxGemvK);
+  SL8_CHECK_ARG(N < (1LL << 31), "gemm_decode_q4k: N too large");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (M == 1) launch_gemv_small<1, true>(x, x_scale, w, out, out_dtype, (int)M, (int)N, (int)K, st);
+  else if (M == 2) launch_gemv_small<2, true>(x, x_scale, w, out, out_dtype, (int)M, (int)N, (int)K, st);
+  else if (M <= 8) launch_gemv_mt<1, true>(x, x_scale, w, out, out_dtype, (int)M, (int)N, (int)K, st);
+  else launch_gemv_mt<2, true>(x, x_scale, w, out, out_dtype, (int)M, (int)N, (int)K, st);
+  SL8_CHECK_LAUNCH("gemm_decode_q4k_xblock");
   return SL8_OK;
 }
 

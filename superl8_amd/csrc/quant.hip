@@ -447,6 +447,81 @@ extern "C" int sl8_quantize_i8_rowwise(const void* x, int x_dtype, int64_t M, in
                         static_cast<hipStream_t>(stream));
 }
 
+namespace sl8 {
+namespace {
+
+// ---------------------------------------------------------------------------
+// Row-group quantisation (one scale per R consecutive rows of a [G][N][K]
+// tensor, groups restarting at every G slice): the per-wavefront Q / per-tile
+// K scheme of BASELINE config 5. One workgroup per group: pass 1 takes the
+// amax of the (optionally mean-shifted, dtype-rounded) values over the R x K
+// block, pass 2 writes the codes (the block is re-read from L2). The scale,
+// safe value and code follow the row-wise contract above with the group's
+// amax in place of the row's; every row of the group stores the group scale.
+// ---------------------------------------------------------------------------
+template <int DT, bool MEAN>
+__global__ void __launch_bounds__(QTHREADS)
+quant_row_groups_kernel(const typename Elem<DT>::T* __restrict__ x, const float* __restrict__ mean,
+                        int8_t* __restrict__ q, float* __restrict__ scale, int64_t N, int K, int R,
+                        float scale_mul) {
+  using T = typename Elem<DT>::T;
+  __shared__ float red[QTHREADS / 64];
+  const int64_t g = blockIdx.y;                  // slice
+  const int64_t r0 = (int64_t)blockIdx.x * R;    // first row of the group in the slice
+  const int nr = (int)min((int64_t)R, N - r0);
+  const T* xb = x + (g * N + r0) * K;
+  const float* mr = MEAN ? mean + g * K : nullptr;
+  const int total = nr * K;
+  float amax = 0.f;
+  for (int i = threadIdx.x; i < total; i += QTHREADS)
+    amax = fmaxf(amax, fabsf(row_val<DT, MEAN>(xb + (i / K) * K, mr, i % K)));
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float s = amax * (1.0f / 127.0f);
+  const float safe = (s == 0.f) ? 1.f : s;
+  for (int i = threadIdx.x; i < nr; i += QTHREADS) scale[g * N + r0 + i] = safe * scale_mul;
+  int8_t* qb = q + (g * N + r0) * K;
+  for (int i = threadIdx.x; i < total; i += QTHREADS)
+    qb[i] = code_of(row_val<DT, MEAN>(xb + (i / K) * K, mr, i % K), safe);
+}
+
+}  // namespace
+}  // namespace sl8
+
+extern "C" int sl8_quantize_i8_row_groups(const void* x, int x_dtype, int64_t G, int64_t N,
+                                          int64_t D, int64_t rows_per_group, const float* mean,
+                                          float scale_mul, int8_t* q, float* scale, void* stream) {
+  clear_error();
+  SL8_CHECK_ARG(x_dtype == SL8_DTYPE_F16 || x_dtype == SL8_DTYPE_BF16 || x_dtype == SL8_DTYPE_F32,
+                "quantize: input must be float16/bfloat16/float32");
+  SL8_CHECK_ARG(G >= 0 && N >= 0 && D >= 0 && D < (1 << 20) && rows_per_group >= 1 &&
+                    rows_per_group * D < (1LL << 30) && G < 65536,
+                "quantize_row_groups: bad shape");
+  if (G == 0 || N == 0 || D == 0) return SL8_OK;
+  SL8_CHECK_ARG(x && q && scale, "quantize: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)((N + rows_per_group - 1) / rows_per_group), (unsigned)G);
+#define SL8_RG(DT, MN)                                                                          \
+  quant_row_groups_kernel<DT, MN><<<grid, QTHREADS, 0, st>>>(                                   \
+      static_cast<const typename Elem<DT>::T*>(x), mean, q, scale, N, (int)D, (int)rows_per_group, \
+      scale_mul)
+  if (mean) {
+    if (x_dtype == SL8_DTYPE_F16) SL8_RG(SL8_DTYPE_F16, true);
+    else if (x_dtype == SL8_DTYPE_BF16) SL8_RG(SL8_DTYPE_BF16, true);
+    else SL8_RG(SL8_DTYPE_F32, true);
+  } else {
+    if (x_dtype == SL8_DTYPE_F16) SL8_RG(SL8_DTYPE_F16, false);
+    else if (x_dtype == SL8_DTYPE_BF16) SL8_RG(SL8_DTYPE_BF16, false);
+    else SL8_RG(SL8_DTYPE_F32, false);
+  }
+#undef SL8_RG
+  SL8_CHECK_LAUNCH("quantize_row_groups");
+  return SL8_OK;
+}
+
 extern "C" int sl8_quantize_i8_rows_centered(const void* x, int x_dtype, int64_t G, int64_t N,
                                              int64_t D, const float* mean, float scale_mul,
                                              int8_t* q, float* scale, void* stream) {

@@ -6,6 +6,7 @@ from .core import (
     quantize_int8_rowwise,
     quantize_qk,
     quantize_qk_gated,
+    quantize_qk_per_wave,
     quantize_v_perchannel,
     quantize_v_rowwise,
     smooth_k,
@@ -14,6 +15,6 @@ from .rotation import hadamard_matrix, rotate_last
 
 __all__ = [
     "LOG2E", "dequantize_int8_rowwise", "detect_q_outlier_domination", "hadamard_matrix",
-    "quantize_int8_rowwise", "quantize_qk", "quantize_qk_gated", "quantize_v_perchannel", "quantize_v_rowwise",
+    "quantize_int8_rowwise", "quantize_qk", "quantize_qk_gated", "quantize_qk_per_wave", "quantize_v_perchannel", "quantize_v_rowwise",
     "rotate_last", "smooth_k",
 ]

@@ -156,3 +156,21 @@ def quantize_qk(q: torch.Tensor, k: torch.Tensor, *, softmax_scale: float | None
     q_i8, q_scale = _C.quantize_rows_centered(q, None, softmax_scale * LOG2E)
     k_i8, k_scale = _C.quantize_rows_centered(k_src, mean, 1.0)
     return q_i8, q_scale.unsqueeze(-1), k_i8, k_scale.unsqueeze(-1), k_mean
+
+
+def quantize_qk_per_wave(q: torch.Tensor, k: torch.Tensor, *, softmax_scale: float | None = None,
+                         q_rows: int = 32, k_rows: int = 64):
+    """quantize_qk with one scale per tile of rows instead of per row: Q per
+    `q_rows` queries (one wavefront's query tile of the prefill kernels, 32) and
+    the smoothed K per `k_rows` keys (one key tile, 64) -- the per-wavefront
+    scheme of BASELINE config 5 (the reference quantises Q/K per row,
+    core.py:164-196). Same outputs as quantize_qk; every row carries its tile's
+    scale, so the attention kernels run unchanged."""
+    _need_gpu(q, "quantize_qk_per_wave")
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(q.shape[-1])
+    k_mean = _C.k_mean(k)
+    q_i8, q_scale = _C.quantize_row_groups(q, q_rows, None, softmax_scale * LOG2E)
+    k_i8, k_scale = _C.quantize_row_groups(k, k_rows, k_mean, 1.0)
+    return q_i8, q_scale.unsqueeze(-1), k_i8, k_scale.unsqueeze(-1), k_mean
+

@@ -50,6 +50,24 @@ def test_kernel_matches_oracle(device, shape, ns):
     assert_close_abs(out[:, :, 0], ref, atol=2e-3, rtol=2e-3, what=f"decode {shape} ns={ns}")
 
 
+@pytest.mark.parametrize("shape", DECODE_SHAPES)
+@pytest.mark.parametrize("ns", [-1, 16])
+def test_fp16_k_scale_matches_oracle(device, shape, ns):
+    """fp16 per-token K scales (BASELINE config 3's cache format): the kernel
+    widens them exactly, so the oracle on the same fp16 values is the bar."""
+    q, k, v = _qkv(shape, device)
+    q_i8, qs, k_i8, ks = _prep(q, k)
+    ks16 = ks.half()
+    out = _C.attn_int8_decode(q_i8, qs, k_i8, ks16, v, ns)
+    n_splits = ns if ns > 0 else _C.choose_n_splits(shape[3], shape[0], shape[2])
+    ref = oa.attn_int8_decode(_np(q_i8)[:, :, 0], _np(qs)[:, :, 0], _np(k_i8),
+                              _np(ks16.float()), _np(v.float()), n_splits)
+    assert_close_abs(out[:, :, 0], ref, atol=2e-3, rtol=2e-3, what=f"decode ks16 {shape} ns={ns}")
+    # same keys with the fp32 contract on the widened scales: identical kernels after the load
+    out32 = _C.attn_int8_decode(q_i8, qs, k_i8, ks16.float(), v, ns)
+    assert torch.equal(out, out32)
+
+
 @pytest.mark.parametrize("shape", DECODE_SHAPES[:8])
 def test_end_to_end_quality(device, shape):
     q, k, v = _qkv(shape, device)

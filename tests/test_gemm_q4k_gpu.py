@@ -54,6 +54,30 @@ def test_gemv_matches_exact_sum(device, M, N, K, odt):
                         min_sqnr_db=40.0)
 
 
+XB_SHAPES = [(1, 17408, 5120), (8, 17408, 5120), (2, 130, 256), (3, 40, 16384), (16, 96, 512),
+             (5, 64, 1024), (1, 64, 16384)]
+
+
+@pytest.mark.parametrize("odt", [torch.float16, torch.float32])
+@pytest.mark.parametrize("M,N,K", XB_SHAPES)
+def test_gemv_block_scales_matches_exact_sum(device, M, N, K, odt):
+    """BASELINE config 4's activation format: int8 per 256-element block with an
+    fp32 scale each (x_scale [M, K/256]) against the oracle's exact sums."""
+    x, w, wd = _case(M, N, K, seed=M * 17 + N, device=device)
+    x[:, :256] *= 30  # blocks of one row at very different scales
+    x_i8, xb = _C.quantize_i8_blockwise(x, 256)
+    assert xb.shape == (M, K // 256)
+    # the block quantiser is the row quantiser on each 256-slice: codes bit-exact
+    rq, rs = oqn.quantize_rows(_np(x.float()).reshape(-1, 256))
+    np.testing.assert_array_equal(_np(x_i8).reshape(-1, 256), rq)
+    np.testing.assert_array_equal(_np(xb).reshape(-1), rs)
+    y = _C.gemm_decode_q4k(x_i8, xb, wd, odt)
+    ref = oq.gemv_xblock(_np(x_i8), _np(xb), w, K)
+    rtol = {torch.float16: 2e-3, torch.float32: 1e-5}[odt]
+    err = np.abs(_np(y.float()).astype(np.float64) - ref)
+    assert (err <= rtol * np.abs(ref) + 1e-5 * np.abs(ref).max()).all(), f"max err {err.max():.3e}"
+
+
 TILE_SHAPES = [(17, 130, 512), (40, 256, 1024), (128, 128, 256), (300, 1000, 2048),
                (257, 17, 768), (512, 4864, 5120)]
 

@@ -67,6 +67,25 @@ def test_quant_rounding_brute_force():
         assert list(q1[1:5]) == [2, 4, -2, -4]
 
 
+def test_quant_row_groups_pins():
+    """Group quantiser: one row per group is the row quantiser; a group's scale is
+    its largest row amax (brute force); codes use the group scale."""
+    x = (RNG.standard_normal((2, 70, 24)) * RNG.random((2, 70, 1)) * 4).astype(np.float32)
+    q1, s1 = oqn.quantize_row_groups(x, 1, 0.5)
+    qr, sr = oqn.quantize_rows(x, 0.5)
+    np.testing.assert_array_equal(q1, qr)
+    np.testing.assert_array_equal(s1, sr)
+    q, s = oqn.quantize_row_groups(x, 32)
+    for b in range(2):
+        for r0 in (0, 32, 64):
+            blk = x[b, r0:r0 + 32]
+            sc = np.float32(np.abs(blk).max()) * oqn.INV127
+            assert (s[b, r0:r0 + 32] == sc).all()
+            np.testing.assert_array_equal(
+                q[b, r0:r0 + 32], np.clip(np.rint(blk / sc), -127, 127).astype(np.int8))
+    assert s[0, 64:].shape == (6,)  # short last group
+
+
 def test_k_mean_exact_and_order_free():
     """fp16 mean: exact sum, so equal to the float64 mean rounded once, and
     invariant under any key permutation (catches a plain fp32 running sum)."""
@@ -162,6 +181,23 @@ def test_q4k_gemv_matches_dequant_matmul():
     ref = (x.astype(np.float64) @ oq.dequant(w, 512).astype(np.float64).T) * xs[:, None]
     # dequant rounds d*sc*q - dmin*m to fp32 once; the oracle sums exactly
     np.testing.assert_allclose(y, ref, rtol=1e-6, atol=1e-6)
+
+
+def test_q4k_gemv_xblock_pins():
+    """Per-256-block activation scales: equals the dequantised matmul with x
+    scaled per block, and reduces to gemv() when each row's blocks share one scale."""
+    w = oq.random_weights(24, 768, seed=5)
+    x = RNG.integers(-127, 128, (3, 768), dtype=np.int8)
+    xb = (RNG.random((3, 3)) + 0.1).astype(np.float32)
+    y = oq.gemv_xblock(x, xb, w, 768)
+    xf = x.astype(np.float64) * np.repeat(xb.astype(np.float64), 256, axis=1)
+    ref = xf @ oq.dequant(w, 768).astype(np.float64).T
+    np.testing.assert_allclose(y, ref, rtol=1e-6, atol=1e-6)
+    row = xb[:, :1]
+    np.testing.assert_allclose(oq.gemv_xblock(x, np.repeat(row, 3, axis=1), w, 768),
+                               oq.gemv(x, row[:, 0], w, 768), rtol=1e-12, atol=1e-9)
+    # a wrong block-to-scale pairing (scales reversed) is caught
+    assert np.abs(oq.gemv_xblock(x, xb[:, ::-1].copy(), w, 768) - ref).max() > 1e-3
 
 
 # ---------------------------------------------------------------- Q5_K / Q6_K

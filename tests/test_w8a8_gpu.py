@@ -136,3 +136,59 @@ def test_rejects(device):
     q, k, v = _qkv(1, 2, 2, 64, 64, 64, device)
     with pytest.raises(ValueError):
         sl8.attn_int8_fwd(q, k, v, int8_pv=True, causal=True, window_left=8)
+
+
+@pytest.mark.parametrize("shape", [(2, 3, 70, 64), (1, 2, 257, 128), (1, 1, 100, 256), (1, 2, 64, 32)])
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_row_groups_bit_exact(device, shape, dt):
+    """Per-tile quantiser (BASELINE config 5's per-wavefront Q/K): codes and
+    scales bit-exact against the oracle, with and without the K mean shift."""
+    x = (torch.randn(*shape, device=device) * 3).to(dt)
+    xf = _np(x.float())
+    for rows in (32, 64):
+        q, s = _C.quantize_row_groups(x, rows, None, 0.25)
+        rq, rs = oqn.quantize_row_groups(xf, rows, 0.25)
+        np.testing.assert_array_equal(_np(q), rq)
+        np.testing.assert_array_equal(_np(s), rs)
+    mean = _C.k_mean(x)
+    q, s = _C.quantize_row_groups(x, 64, mean, 1.0)
+    xs = oqn.round_to(xf - _np(mean), "f16" if dt == torch.float16 else "bf16")
+    rq, rs = oqn.quantize_row_groups(xs, 64)
+    np.testing.assert_array_equal(_np(q), rq)
+    np.testing.assert_array_equal(_np(s), rs)
+
+
+@pytest.mark.parametrize("per_warp", [True, False])
+def test_config5_per_wave_quant(device, per_warp):
+    """BASELINE config 5's recipe with per-wavefront Q/K scales (Q per 32 queries,
+    K per 64 keys) at reduced size: the prologue matches the oracle bit for bit
+    and the W8A8 kernel on those codes matches the oracle. Against fp attention
+    the coarser Q/K scales cost accuracy (cos 0.9975 here, where per-row scales
+    clear the reference's 0.998 int8-PV bar): the bar for this scheme is looser
+    and per-row quantisation must stay the more accurate one."""
+    torch.manual_seed(5)
+    B, Hq, Hkv, S, D = 1, 4, 1, 1024, 256
+    q, k, v = _qkv(B, Hq, Hkv, S, S, D, device)
+    idx = torch.randperm(D, generator=torch.Generator().manual_seed(5))[:3]
+    q[..., idx] *= 20
+    k[..., idx] *= 20
+    q_i8, qs, k_i8, ks, _ = quant.quantize_qk_per_wave(q, k)
+    r = oqn.quantize_qk_per_wave(_np(q), _np(k))
+    np.testing.assert_array_equal(_np(q_i8), r[0])
+    np.testing.assert_array_equal(_np(qs[..., 0]), r[1])
+    np.testing.assert_array_equal(_np(k_i8), r[2])
+    np.testing.assert_array_equal(_np(ks[..., 0]), r[3])
+    v_i8, vs = _C.quantize_v_perchannel(v)
+    qs, ks, vs = qs[..., 0].contiguous(), ks[..., 0].contiguous(), vs[..., 0, :].contiguous()
+    out = _C.attn_w8a8_fwd(q_i8, qs, k_i8, ks, v_i8, vs, True, 0, per_warp)
+    ref = oa.attn_w8a8_fwd(_np(q_i8), _np(qs), _np(k_i8), _np(ks), _np(v_i8), _np(vs), True, 0,
+                           per_warp)
+    assert_int8_quality(out, ref, min_cos=0.9999, max_rel_l1=5e-3, min_sqnr_db=35)
+    fp = oa.attention_fp64(_np(q.float()), _np(k.float()), _np(v.float()), True)
+    assert_int8_quality(out, fp, what="per-wave quant vs fp attention", min_cos=0.995,
+                        max_rel_l1=0.05, min_sqnr_db=15.0)
+    from tests.tolerances import rel_l1
+
+    row = sl8.attn_int8_fwd(q, k, v, causal=True, int8_pv=True, per_warp_quant=per_warp,
+                            internal_accuracy_gate=False)
+    assert rel_l1(row, fp) <= rel_l1(out, fp)
