@@ -131,6 +131,68 @@ def attn_w8a8_fwd(q_i8, q_scale, k_i8, k_scale, v_i8, v_scale, causal=False, cau
     return np.where(l_i[..., None] > 0, o / np.where(l_i > 0, l_i, 1.0)[..., None], 0.0)
 
 
+LOG2_127_F32 = np.float32(6.988684686772166)
+
+
+def _bf16_round(x: np.ndarray) -> np.ndarray:
+    """fp32 values rounded to bf16 (round to nearest even), returned as float64."""
+    from .quant import bf16_bits_to_f32, f32_to_bf16_bits
+    return bf16_bits_to_f32(f32_to_bf16_bits(x.astype(np.float32))).astype(np.float64)
+
+
+def attn_w8a8_fwd_bf16pv_model(q_i8, q_scale, k_i8, k_scale, v_i8, v_scale, causal=False,
+                               causal_diag=0, excess=100.0):
+    """The per-warp W8A8 arithmetic of this build's kernel (not the reference's):
+    per 32-key half h the codes are rint(2^(t*qs - (tmax_h - log2 127))) as in the
+    reference, but each code enters the PV product as bf16(code * f_h) with
+    f_h = 2^(tmax_h - m) / 127 against the int8 V codes, where m is the row's
+    reference point: set by its first visible half's max and raised to a half's
+    max (O and l rescaled) only when that max exceeds m by more than `excess`.
+    The row sum adds the unrounded 2^(t*qs - (tmax_h - log2 127)) * f_h.
+    Logits, codes and factors follow the kernel's fp32 evaluation; sums are
+    float64. Used to bound the bf16 operand rounding: see
+    tests/test_w8a8_gpu.py."""
+    B, Hq, M, D = q_i8.shape
+    N = k_i8.shape[2]
+    kvh = kv_head_index(Hq, k_i8.shape[1])
+    acc = scores_i32(q_i8, k_i8).astype(np.float32)
+    ks = k_scale[:, kvh].astype(np.float32)
+    t = (acc * ks[..., None, :]).astype(np.float32)              # [B,Hq,M,N]
+    ok = valid_mask(M, N, causal, -1, causal_diag if causal else 0)
+    t = np.where(ok, t, np.float32(-np.inf))
+    qs = q_scale.astype(np.float32)[..., None]                   # [B,Hq,M,1]
+    vq = v_i8[:, kvh].astype(np.float64)
+    vs = v_scale[:, kvh].astype(np.float64)
+    o = np.zeros((B, Hq, M, D))
+    l = np.zeros((B, Hq, M))
+    m = np.full((B, Hq, M), -np.inf, np.float32)
+    for h0 in range(0, N, 32):
+        x = t[..., h0:h0 + 32]
+        tm = (x.max(-1) * qs[..., 0]).astype(np.float32)           # [B,Hq,M]
+        live = np.isfinite(tm)
+        first = live & ~np.isfinite(m)
+        m = np.where(first, tm, m)
+        up = live & ~first & (tm > m + np.float32(excess))
+        if up.any():
+            f = np.where(up, np.exp2(m.astype(np.float64) - tm), 1.0)
+            o *= f[..., None]
+            l *= f
+            m = np.where(up, tm, m)
+        sub = np.where(live, (tm - LOG2_127_F32).astype(np.float32), np.float32(0))
+        with np.errstate(invalid="ignore"):
+            z = (x.astype(np.float64) * qs.astype(np.float64) - sub[..., None]).astype(np.float32)
+            y = np.where(np.isfinite(z), np.exp2(z.astype(np.float64)).astype(np.float32),
+                         np.float32(0))
+            fac = np.where(live, (np.exp2((tm - m).astype(np.float64)).astype(np.float32)
+                                  * np.float32(1.0 / 127.0)).astype(np.float32), np.float32(0))
+        code = np.rint(y).astype(np.float32)
+        pe = _bf16_round((code * fac[..., None]).astype(np.float32))
+        o += np.matmul(pe, vq[..., h0:h0 + 32, :])
+        l += y.astype(np.float64).sum(-1) * fac.astype(np.float64)
+    out = np.where(l[..., None] > 0, o / np.where(l > 0, l, 1.0)[..., None], 0.0)
+    return out * vs[:, :, None, :]
+
+
 def attn_int8_decode(q_i8, q_scale, k_i8, k_scale, v, num_splits):
     """Split-KV decode: q_i8 [B,Hq,D], q_scale [B,Hq] -> out [B,Hq,D] float64,
     via per-split partials and the LSE merge (reference attn_decode.cuh:68-71,129,430-466)."""

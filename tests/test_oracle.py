@@ -423,6 +423,54 @@ def test_w8a8_oracle_close_to_fp16v():
             assert_int8_quality(out, ref, min_cos=0.998, max_rel_l1=0.03, min_sqnr_db=18)
 
 
+def _w8_bf16_case():
+    """Logits set exactly through k_scale (q codes 1, k codes 1, D = 128, q_scale =
+    1/128): in every 32-key half one key sits at the half's max and 31 keys
+    log2(127/101) below it, so 31 codes equal 101 and their bf16(101 * f)
+    operands share one rounding error (101/127 is not a bf16 number)."""
+    D, M, N = 128, 64, 128
+    q = np.ones((1, 1, M, D), np.int8)
+    k = np.ones((1, 1, N, D), np.int8)
+    qs = np.full((1, 1, M), 1.0 / 128.0, np.float32)
+    base = np.float32(-1.0)
+    off = np.float32(np.log2(101.0 / 127.0))
+    ks = np.full((1, 1, N), base + off, np.float32)
+    ks[..., ::32] = base
+    g = np.random.default_rng(3)
+    v = g.integers(-127, 128, (1, 1, N, D), dtype=np.int8)
+    vs = np.full((1, 1, D), 0.01, np.float32)
+    return q, qs, k, ks, v, vs
+
+
+def test_w8a8_bf16_model_bounds_and_sensitivity():
+    """The kernel model (bf16 P operands, lazy reference point) against the
+    reference-semantics oracle: within the bf16 bound on random data, and
+    visibly apart on the correlated-rounding case, where a model without the
+    bf16 rounding would agree with the oracle."""
+    g = np.random.default_rng(9)
+    B, H, M, N, D = 1, 2, 96, 200, 64
+    q = g.integers(-127, 128, (B, H, M, D), dtype=np.int8)
+    k = g.integers(-127, 128, (B, H, N, D), dtype=np.int8)
+    v = g.integers(-127, 128, (B, H, N, D), dtype=np.int8)
+    qs = np.full((B, H, M), 1.0 / 2000.0, np.float32)
+    ks = (g.random((B, H, N)) * 0.5 + 0.5).astype(np.float32)
+    vs = np.full((B, H, D), 0.01, np.float32)
+    for causal in (False, True):
+        diag = N - M if causal else 0
+        ref = oa.attn_w8a8_fwd(q, qs, k, ks, v, vs, causal, diag, True)
+        mod = oa.attn_w8a8_fwd_bf16pv_model(q, qs, k, ks, v, vs, causal, diag)
+        assert_int8_quality(mod, ref, min_cos=0.99999, max_rel_l1=4e-3, min_sqnr_db=45)
+        # a zero rescale headroom moves the reference point at every rising half:
+        # the same softmax (other bf16 roundings), still within the bound
+        mod0 = oa.attn_w8a8_fwd_bf16pv_model(q, qs, k, ks, v, vs, causal, diag, excess=0.0)
+        assert_int8_quality(mod0, ref, min_cos=0.99999, max_rel_l1=4e-3, min_sqnr_db=45)
+    q, qs, k, ks, v, vs = _w8_bf16_case()
+    ref = oa.attn_w8a8_fwd(q, qs, k, ks, v, vs, False, 0, True)
+    mod = oa.attn_w8a8_fwd_bf16pv_model(q, qs, k, ks, v, vs, False, 0)
+    rel = np.abs(mod - ref).max() / np.abs(ref).max()
+    assert rel > 1e-3, rel
+
+
 def test_w8a8_p_requant_known_answer():
     """One query, 2 keys in one tile with p = (1, 1/3): p_scale = fp32(1/127),
     codes (127, rint(127/3)=42); output = (127*v0 + 42*v1)*ps*vs / (1 + 1/3)."""

@@ -192,3 +192,47 @@ def test_config5_per_wave_quant(device, per_warp):
     row = sl8.attn_int8_fwd(q, k, v, causal=True, int8_pv=True, per_warp_quant=per_warp,
                             internal_accuracy_gate=False)
     assert rel_l1(row, fp) <= rel_l1(out, fp)
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_per_warp_matches_bf16_model(device, case):
+    """The per-warp kernel against the model of its own arithmetic (bf16 P
+    operands, lazy reference point): much closer than to the reference-semantics
+    oracle, so a change of that rounding is caught here."""
+    B, Hq, Hkv, M, N, D, causal = case
+    q, k, v = _qkv(B, Hq, Hkv, M, N, D, device)
+    q_i8, qs, k_i8, ks, _ = quant.quantize_qk(q, k)
+    qs, ks = qs.squeeze(-1).contiguous(), ks.squeeze(-1).contiguous()
+    v_i8, vs = _C.quantize_v_perchannel(v)
+    vs = vs.squeeze(-2).contiguous()
+    diag = N - M if causal else 0
+    out = _np(_C.attn_w8a8_fwd(q_i8, qs, k_i8, ks, v_i8, vs, causal, diag, True).float())
+    args = (_np(q_i8), _np(qs), _np(k_i8), _np(ks), _np(v_i8), _np(vs), causal, diag)
+    model = oa.attn_w8a8_fwd_bf16pv_model(*args, excess=_w8_excess(N))
+    ref = oa.attn_w8a8_fwd(*args, True)
+    e_model, e_ref = np.abs(out - model).max(), np.abs(out - ref).max()
+    print(f"w8 {case}: |kernel-model| {e_model:.2e}  |kernel-oracle| {e_ref:.2e}")
+    assert_int8_quality(out, model, min_cos=0.99999, max_rel_l1=1e-3, min_sqnr_db=50)
+
+
+def _w8_excess(N):
+    """The kernel's rescale headroom: 120 - 7 - ceil(log2 N), at least 16."""
+    return float(max(16, 113 - max(0, int(np.ceil(np.log2(max(N, 1)))))))
+
+
+def test_per_warp_bf16_rounding_is_the_modelled_one(device):
+    """Correlated-rounding case (tests/test_oracle.py:_w8_bf16_case): the bf16
+    operand rounding moves the output by > 1e-3 relative from the exact-int32
+    arithmetic of the reference; the kernel follows the model of it."""
+    from tests.test_oracle import _w8_bf16_case
+
+    q, qs, k, ks, v, vs = _w8_bf16_case()
+    dv = [torch.from_numpy(t).to(device) for t in (q, qs, k, ks, v, vs)]
+    out = _np(_C.attn_w8a8_fwd(*dv, False, 0, True).float())
+    model = oa.attn_w8a8_fwd_bf16pv_model(q, qs, k, ks, v, vs, False, 0, excess=_w8_excess(128))
+    ref = oa.attn_w8a8_fwd(q, qs, k, ks, v, vs, False, 0, True)
+    scale = np.abs(ref).max()
+    e_model, e_ref = np.abs(out - model).max() / scale, np.abs(out - ref).max() / scale
+    print(f"correlated case: |kernel-model| {e_model:.2e}  |kernel-oracle| {e_ref:.2e} (relative)")
+    assert e_ref > 1e-3
+    assert e_model < 0.25 * e_ref
