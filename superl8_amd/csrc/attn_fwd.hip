@@ -468,6 +468,9 @@ attn_fwd_kernel(const FwdArgs a) {
 // operand reads (1 KB per MFMA), ~7 VALU operations per score.
 // ---------------------------------------------------------------------------
 
+#ifndef SL8_FWD_FAST
+#define SL8_FWD_FAST 1
+#endif
 #ifndef SL8_FWD_OCC
 #define SL8_FWD_OCC 2
 #endif
@@ -479,6 +482,8 @@ template <int D, bool CAUSAL, int VDT, bool LSE, int NG, int WV, bool W8>
 __global__ void __launch_bounds__(WV * 64, (NG == 1 && D <= 128) ? SL8_FWD_OCC * 4 / WV : 1)
 attn_fwd_wide_kernel(const FwdArgs a) {
   constexpr int WT = WV * 64;                  // threads per workgroup
+  // the straight-line steady-state half-step (half_step_fast): D = 128, NG = 1
+  constexpr bool FAST = SL8_FWD_FAST && D == 128 && NG == 1 && !W8;
   constexpr int WQ = 32 * NG;                  // queries per wave
   constexpr int WBM = WV * WQ;                 // queries per workgroup
   constexpr int DC = D / 32;
@@ -599,39 +604,47 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       return (n0 + BN > N) || (CAUSAL && n0 + BN - 1 > wq_lo) || (wl >= 0 && n0 <= wq_hi - wl);
     };
 
-    auto load_k = [&](int n0, int8_t* dst) __attribute__((always_inline)) {
+    // Tile copies through buffer resources: per-lane byte offsets fixed for
+    // the whole kernel, the tile start in the scalar offset; rows at or past N
+    // read as zeros (their keys are masked).
+    const brsrc_t rk = make_rsrc(kb, (uint32_t)N * D);
+    const brsrc_t rv = VT ? make_rsrc(vtb, (uint32_t)D * a.Npad * 2) : make_rsrc(vb, (uint32_t)N * VRB);
+    const brsrc_t rs = make_rsrc(ksb, (uint32_t)N * 4);
+    uint32_t kvo[KCH], vvo[VCH];
 #pragma unroll
-      for (int i = 0; i < KCH; ++i) {
-        const int sl = i * WT + tid;
-        const int row = sl / KCPR;
-        const int c = (sl % KCPR) ^ ((row >> KSH) & (KCPR - 1));
-        dma16_to_lds(kb + (int64_t)min(n0 + row, N - 1) * D + 16 * c,
-                     dst + (i * WT + wave * 64) * 16);
-      }
-    };
-    auto load_v = [&](int n0, uint16_t* dst) __attribute__((always_inline)) {
+    for (int i = 0; i < KCH; ++i) {
+      const int sl = i * WT + tid;
+      const int row = sl / KCPR;
+      const int c = (sl % KCPR) ^ ((row >> KSH) & (KCPR - 1));
+      kvo[i] = (uint32_t)(row * D + 16 * c);
+    }
+#pragma unroll
+    for (int i = 0; i < VCH; ++i) {
+      const int sl = i * WT + tid;
       if constexpr (VT) {
-#pragma unroll
-        for (int i = 0; i < VCH; ++i) {
-          const int sl = i * WT + tid;
-          const int row = sl / 8;
-          const int c = (sl % 8) ^ ((row >> 1) & 7);
-          dma16_to_lds(vtb + (int64_t)row * a.Npad + n0 + 8 * c, dst + (i * WT + wave * 64) * 8);
-        }
-        return;
-      }
-      // LDS chunk (row, c) holds V chunk c ^ 4k of key row n0 + row (k: the row's swizzle)
-#pragma unroll
-      for (int i = 0; i < VCH; ++i) {
-        const int sl = i * WT + tid;
+        const int row = sl / 8;
+        const int c = (sl % 8) ^ ((row >> 1) & 7);
+        vvo[i] = (uint32_t)(row * a.Npad * 2 + 16 * c);
+      } else {
+        // LDS chunk (row, c) holds V chunk c ^ 4k of key row n0 + row (k: the row's swizzle)
         const int row = sl / (D / 8);
         const int k = D == 64 ? ((row >> 1) & 1) : (row & 3);
         const int c = (sl % (D / 8)) ^ (4 * k);
-        dma16_to_lds(vb + (int64_t)min(n0 + row, N - 1) * D + 8 * c, dst + (i * WT + wave * 64) * 8);
+        vvo[i] = (uint32_t)(row * VRB + 16 * c);
       }
+    }
+    auto load_k = [&](int n0, int8_t* dst) __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < KCH; ++i)
+        buf16_to_lds(rk, dst + (i * WT + wave * 64) * 16, kvo[i], (uint32_t)n0 * D);
+    };
+    auto load_v = [&](int n0, uint16_t* dst) __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < VCH; ++i)
+        buf16_to_lds(rv, dst + (i * WT + wave * 64) * 8, vvo[i], (uint32_t)n0 * (VT ? 2 : VRB));
     };
     auto load_s = [&](int n0, float* dst) __attribute__((always_inline)) {
-      if (wave == 0) dma4_to_lds(ksb + min(n0 + lane, N - 1), dst);
+      if (wave == 0) buf4_to_lds(rs, dst, (uint32_t)lane * 4, (uint32_t)n0 * 4);
     };
 
     v16f oacc[NG][DC];
@@ -639,6 +652,7 @@ attn_fwd_wide_kernel(const FwdArgs a) {
 #pragma unroll
     for (int g = 0; g < NG; ++g) mx_all[g] = -INFINITY;
     bool ovf = false;
+    bool all_set = false;  // every row's reference point is fixed (wave-uniform)
 
     // The key loop runs in half-steps of 32 keys (two per 64-key LDS tile).
     // Half-step h issues, as independent work for the matrix cores and VALU:
@@ -869,6 +883,105 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       half_scores(sc, st, j, s, mask, dead, xo);
       if constexpr (W8_LAZY) settle(xo);
     };
+    // Steady-state half-step (no masked key, every row's reference point set):
+    // one straight-line block whose LDS operand reads are all issued first,
+    // then the 12 MFMAs (QK of half h, PV of half h-2) each followed by a
+    // slice of the VALU work (P of half h-1, then the scores of half h), so
+    // the matrix core never waits on an LDS round trip and the VALU runs
+    // under the MFMAs. Same operations as half_step, in a fixed issue order.
+    auto half_step_fast = [&](int s, const int8_t* kt, const float* st, const uint16_t* vt,
+                              xblk& xi, pblk& p1, xblk& xo, pblk& p2) __attribute__((always_inline)) {
+      typedef short v4s __attribute__((ext_vector_type(4)));
+      typedef short v8s __attribute__((ext_vector_type(8)));
+      typedef __attribute__((address_space(3))) v4s* lv4s_t;
+      if constexpr (FAST) {
+      const char* vbytes = reinterpret_cast<const char*>(vt);
+      // operand i of the half-step: i < DC: K chunk i (QK); else V^T (c, tt) for PV
+      auto load_op = [&](int i) __attribute__((always_inline)) -> v4i {
+        if (i < DC) return *reinterpret_cast<const v4i*>(kt + (32 * s + l32) * D + koff[i]);
+        const int c = (i - DC) / DC, tt = (i - DC) % DC;
+        const char* a0 = vbytes + (32 * s + 16 * c) * VRB + voffb[tt];
+        const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lv4s_t)(a0));
+        const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lv4s_t)(a0 + 8 * VRB));
+        const v8s both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        return __builtin_bit_cast(v4i, both);
+      };
+      constexpr int NOP = 3 * DC;
+      const float msub = (m_run[0] == -INFINITY) ? 0.f : m_run[0];
+      float pe[16];
+      float hs = 0.f;
+      float4 kv[4];
+      v16i sc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sc[r] = 0;
+      v4i cur = load_op(0);
+      // Issue order, fixed by scheduling barriers: MFMA i is preceded by the
+      // read of operand i + 1 and followed by a slice of VALU work --
+      //   QK MFMAs 0..3: P of half h-1, four exp2 each;
+      //   PV MFMAs 0..1: pack P to fp16 + row sums (one 16-key step each);
+      //   PV MFMA 2: k_scale reads; PV MFMAs 3..6: scores of half h (cvt, * k_scale).
+#pragma unroll
+      for (int i = 0; i < NOP; ++i) {
+        v4i nxt = cur;
+        if (i + 1 < NOP) nxt = load_op(i + 1);
+        if (i < DC) {
+          sc = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur, qop[0].c[i], sc, 0, 0, 0);
+#pragma unroll
+          for (int e = 4 * i; e < 4 * i + 4; ++e)
+            pe[e] = __builtin_amdgcn_exp2f(fmaf(xi[0][e], qsc[0], -msub));
+        } else {
+          const int c = (i - DC) / DC, tt = (i - DC) % DC;
+          oacc[0][tt] = PV::mfma(__builtin_bit_cast(pvec, cur), p2[0][c], oacc[0][tt]);
+          const int k = i - DC;
+          if (k < 2) {
+            // same packing, row-sum order and overflow test as half_probs
+            p1[0][k] = PV::pack(&pe[8 * k]);
+            hs = PV::sum(p1[0][k], &pe[8 * k], hs);
+            if (k == 1) {
+              l_lane[0] += hs;
+              ovf = ovf || (hs > 32768.f);
+            }
+          } else if (k == 2) {
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq)
+              kv[gq] = *reinterpret_cast<const float4*>(st + 32 * s + 8 * gq + 4 * h);
+          } else if (k < 7) {
+            const int gq = k - 3;
+            xo[0][4 * gq + 0] = (float)sc[4 * gq + 0] * kv[gq].x;
+            xo[0][4 * gq + 1] = (float)sc[4 * gq + 1] * kv[gq].y;
+            xo[0][4 * gq + 2] = (float)sc[4 * gq + 2] * kv[gq].z;
+            xo[0][4 * gq + 3] = (float)sc[4 * gq + 3] * kv[gq].w;
+          }
+        }
+        cur = nxt;
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      }
+    };
+
+    auto half_fixup = [&](int t, int s, bool do_mask, bool dead, xblk& xo) __attribute__((always_inline)) {
+      if (do_mask) {
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+          const int nb = n_beg + t * BN + 32 * s;
+          // key n is visible iff (n - lo) unsigned < (hi - lo), [lo, hi) the visible range
+          const int hi = dead ? nb : min(N, CAUSAL ? qpos[g] + 1 : N);
+          const int lo = (wl >= 0) ? qpos[g] - wl + 1 : INT_MIN / 2;
+          const int lo_c = max(lo, nb - 64);
+          const uint32_t span = hi > lo_c ? (uint32_t)(hi - lo_c) : 0u;
+          const uint32_t rel = (uint32_t)(nb + 4 * h - lo_c);
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            xo[g][e] = (rel + (uint32_t)(8 * (e >> 2) + (e & 3)) < span) ? xo[g][e] : -INFINITY;
+        }
+      }
+      settle(xo);
+      bool unset = false;
+#pragma unroll
+      for (int g = 0; g < NG; ++g) unset = unset || (m_run[g] == -INFINITY);
+      all_set = !__any(unset);
+    };
+
     // QK-only sweep: mx_all = the exact row max (exp2 domain) of the
     // visible logits, with the same double-buffered tile copies as the pass.
     auto sweep_tile = [&](int t, const int8_t* kc, const float* sc_, int8_t* kn, float* sn)
@@ -924,8 +1037,21 @@ attn_fwd_wide_kernel(const FwdArgs a) {
         half_step_w8(j, 0, kcur, scur, vprev, mask, dead, xB, pB, xA, pA);
         half_step_w8(j, 1, kcur, scur, vprev, mask, dead, xA, pA, xB, pB);
       } else {
-        half_step(j, 0, kcur, scur, vprev, mask, dead, xB, pB, xA, pA);
-        half_step(j, 1, kcur, scur, vprev, mask, dead, xA, pA, xB, pB);
+        if constexpr (FAST) {
+          // a masked half, or one that may fix some row's reference point,
+          // gets its mask / settle after the straight-line part
+          half_step_fast(0, kcur, scur, vprev, xB, pB, xA, pA);
+          if (mask || !all_set) half_fixup(j, 0, mask, dead, xA);
+          half_step_fast(1, kcur, scur, vprev, xA, pA, xB, pB);
+          if (mask || !all_set) half_fixup(j, 1, mask, dead, xB);
+        } else {
+          half_step(j, 0, kcur, scur, vprev, mask, dead, xB, pB, xA, pA);
+          half_step(j, 1, kcur, scur, vprev, mask, dead, xA, pA, xB, pB);
+          bool unset = false;
+#pragma unroll
+          for (int g = 0; g < NG; ++g) unset = unset || (m_run[g] == -INFINITY);
+          all_set = !__any(unset);
+        }
       }
       wait_dma();
       __syncthreads();
@@ -943,6 +1069,7 @@ attn_fwd_wide_kernel(const FwdArgs a) {
         l_lane[g] = 0.f;
       }
       ovf = false;
+      all_set = false;
       // Iteration j reads K_j, k_scale_j (halves 2j, 2j+1) and V_{j-1} (PV of
       // halves 2j-2, 2j-1), and copies K_{j+1}, k_scale_{j+1} and V_j into the
       // other buffers.
@@ -1068,6 +1195,8 @@ int check_fwd_shape(int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N, in
   SL8_CHECK_ARG(D == 32 || D == 64 || D == 72 || D == 80 || D == 128 || D == 256,
                 "fni8: head dim must be 32/64/72/80/128/256, got %lld", (long long)D);
   SL8_CHECK_ARG(M < (1 << 30) && N < (1 << 30) && B * Hq < (1 << 24), "fni8: shape too large");
+  // one KV head's V (and W8A8's padded V^T) is addressed by a 32-bit buffer offset
+  SL8_CHECK_ARG(N * 2 * (D + 64) < (1LL << 31), "fni8: shape too large (N=%lld)", (long long)N);
   return SL8_OK;
 }
 
