@@ -23,21 +23,6 @@ __device__ __forceinline__ void dma4_to_lds(const void* g, void* lds_wave_base) 
 }
 __device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
 
-// Buffer-resource copies to LDS: a raw buffer of `bytes` bytes at `base`
-// (stride 0; the gfx9-family format dword). The per-lane byte offset stays in a
-// VGPR and the per-tile advance goes in the scalar offset, so a tile copy costs
-// no vector address arithmetic; offsets at or past `bytes` read as zero.
-typedef __amdgpu_buffer_rsrc_t brsrc_t;
-__device__ __forceinline__ brsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-__device__ __forceinline__ void buf16_to_lds(brsrc_t r, void* lds_wave_base, uint32_t voff, uint32_t soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lptr_t)lds_wave_base, 16, voff, soff, 0, 0);
-}
-__device__ __forceinline__ void buf4_to_lds(brsrc_t r, void* lds_wave_base, uint32_t voff, uint32_t soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lptr_t)lds_wave_base, 4, voff, soff, 0, 0);
-}
-
 // blockIdx.x -> (b*Hq + h, slot). Slots are issued in increasing order, so
 // callers put their heaviest work in slot 0. With xcd_map, workgroup ids are
 // dealt so that each KV head's query heads stay on one XCD (id % 8 is the

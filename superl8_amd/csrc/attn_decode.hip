@@ -20,6 +20,7 @@
 //     state and are merged by LSE in LDS at the end (fixed order, so results
 //     are deterministic).
 
+#include <algorithm>
 #include <mutex>
 #include <type_traits>
 
@@ -60,6 +61,7 @@ struct PagedArgs {
   const int32_t* ctx;  // [B] keys per sequence
   int maxb, bs;
   int bs_sh;           // log2(bs) (streaming kernel: bs a power of two)
+  int cache_rows;      // num_blocks * Hkv * bs (streaming kernel, block-aligned tiles)
 };
 // block-table entries of one split staged in LDS by the streaming paged kernel
 constexpr int DEC_BT_MAX = 1024;
@@ -419,7 +421,10 @@ struct WaveCfg {
 // PG: paged int8 cache (see PagedArgs): the split's block-table entries are
 // staged in LDS, every copy lane maps its key to a physical row, and the
 // per-token V scale multiplies p before it is broadcast to the PV lanes.
-template <int D, int GS, int NB, bool VI8, bool PG, bool KS16 = false>
+// PGA (paged, block-aligned tiles): every T-key tile lies inside one cache
+// block, so a tile's physical rows are one uniform base plus the lane's fixed
+// offset and its copies go through buffer resources like the contiguous ones.
+template <int D, int GS, int NB, bool VI8, bool PG, bool KS16 = false, bool PGA = false>
 __global__ void __launch_bounds__(DEC_THREADS)
 decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_scale,
                    const int8_t* __restrict__ k, const void* __restrict__ k_scale,
@@ -488,9 +493,52 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
   }
   const float qsc = q_scale[hq];
 
+  // Buffer-resource copies (contiguous cache, or paged with block-aligned
+  // tiles): per-lane byte offsets fixed for the kernel, the tile's first row in
+  // the scalar offset; rows past the resource read as zeros, rows past the
+  // split (< N) are real keys that the compute masks.
+  constexpr bool BUF = !PG || PGA;
+  const uint32_t res_rows = PG ? (uint32_t)pg.cache_rows : (uint32_t)n_len;
+  const brsrc_t r_k = make_rsrc(kb, res_rows * D);
+  const brsrc_t r_v = make_rsrc(vb, res_rows * C::VRB);
+  const brsrc_t r_s = make_rsrc(ksb, res_rows * KSB);
+  const brsrc_t r_vs = make_rsrc(PG ? (const void*)vsc : (const void*)ksb, PG ? res_rows * 4 : 0u);
+  uint32_t kvo[C::KDMA], vvo[C::VDMA];
+#pragma unroll
+  for (int j = 0; j < C::KDMA; ++j) {
+    const int id = j * 64 + lane, row = id / KC;
+    const int c = (id % KC) ^ ((row >> KSH) & KSW);
+    kvo[j] = (uint32_t)(row * D + 16 * c);
+  }
+#pragma unroll
+  for (int j = 0; j < C::VDMA; ++j) {
+    const int id = j * 64 + lane, row = id / (C::VRB / 16);
+    vvo[j] = (uint32_t)(row * C::VRB + 16 * (id % (C::VRB / 16)));
+  }
   // tile i of this wave = tile (wave + 4 i) of the split
   auto load_tile = [&](int i, int8_t* sb) {
     const int base = n0 + (wave + DEC_WAVES * i) * T;
+    if constexpr (BUF) {
+      uint32_t r0 = (uint32_t)base;  // the tile's first cache row
+      if constexpr (PG) {
+        const int blk = __builtin_amdgcn_readfirstlane(sm_bt[(base >> pg.bs_sh) - first_blk]);
+        r0 = (uint32_t)(((int64_t)blk * h_kv + kvh) * pg.bs + (base & (pg.bs - 1)));
+      }
+#pragma unroll
+      for (int j = 0; j < C::KDMA; ++j) buf16_to_lds(r_k, sb + j * 1024, kvo[j], r0 * D);
+#pragma unroll
+      for (int j = 0; j < C::VDMA; ++j)
+        buf16_to_lds(r_v, sb + C::KBYTES + j * 1024, vvo[j], r0 * C::VRB);
+      // lanes past the tile repeat its keys (same cache lines: no extra traffic)
+      const uint32_t sl = (uint32_t)(lane % T);
+      if constexpr (KS16)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r_s, (lptr_t)(sb + C::KBYTES + C::VBYTES), 2,
+                                                 sl * 2, r0 * 2, 0, 0);
+      else
+        buf4_to_lds(r_s, sb + C::KBYTES + C::VBYTES, sl * 4, r0 * 4);
+      if constexpr (PG) buf4_to_lds(r_vs, sb + C::KBYTES + C::VBYTES + 256, sl * 4, r0 * 4);
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < C::KDMA; ++j) {
       const int id = j * 64 + lane, row = id / KC;
@@ -563,7 +611,9 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
       float pvs = 0.f;
 #pragma unroll
       for (int u = 0; u < SUB; ++u) {
-        p[u] *= vst[u * KL + kl];
+        // keys past the sequence (p = 0) may sit in unwritten block rows whose
+        // scale is not a number: select instead of multiplying
+        p[u] = (base + u * KL + kl < n1) ? p[u] * vst[u * KL + kl] : 0.f;
         pvs += p[u];
       }
       lv_lane = lv_lane * resc + pvs;
@@ -782,7 +832,7 @@ template <int D, bool VI8, bool PG = false, bool KS16 = false>
 void launch_d(int G, dim3 grid, const int8_t* q, const float* qs, const int8_t* k,
               const void* ks, const void* v, const float* vsc, float* op, float* mp, float* lp,
               int N, int ns, int hq, int hkv, int gsz, int bhq, hipStream_t st,
-              const PagedArgs& pg = PagedArgs{nullptr, nullptr, 0, 1, 0}) {
+              const PagedArgs& pg = PagedArgs{nullptr, nullptr, 0, 1, 0, 0}) {
 #define SL8_SPLIT(GG) \
   launch_split<D, GG, VI8, PG, KS16>(grid, q, qs, k, ks, v, vsc, op, mp, lp, N, ns, hq, hkv, gsz, bhq, pg, st)
   switch (G) {
@@ -829,6 +879,9 @@ template <bool VI8, bool KS16 = false>
 int decode_launch(const int8_t* q, const float* q_scale, const int8_t* k, const void* k_scale,
                   const void* v, const float* vsc, void* out, int64_t B, int64_t Hq, int64_t Hkv,
                   int64_t N, int64_t D, int64_t num_splits, void* workspace, hipStream_t st) {
+  // one KV head's cache is addressed by 32-bit buffer offsets in the streaming kernel
+  SL8_CHECK_ARG(N * D * (VI8 ? 1 : 2) < (1LL << 31), "fni8 decode: shape too large (N=%lld)",
+                (long long)N);
   const int ns = (int)num_splits, bhq = (int)(B * Hq), gsz = (int)(Hq / Hkv);
   const int G = group_width(gsz);
   float* op = static_cast<float*>(workspace);
@@ -842,7 +895,7 @@ int decode_launch(const int8_t* q, const float* q_scale, const int8_t* k, const 
 #define SL8_WAVE(DD, GS, NB)                                                                     \
     decode_wave_kernel<DD, GS, NB, VI8, false, KS16><<<g2, DEC_THREADS, 0, st>>>(                    \
         q, q_scale, k, k_scale, v, vsc, op, mp, lp, (int)N, ns, (int)Hq, (int)Hkv, bhq,       \
-        PagedArgs{nullptr, nullptr, 0, 1, 0})
+        PagedArgs{nullptr, nullptr, 0, 1, 0, 0})
 #define SL8_WAVE_D(GS)                         \
     if (D == 64) SL8_WAVE(64, GS, 4);          \
     else if (D == 128) SL8_WAVE(128, GS, 3);   \
@@ -1135,17 +1188,31 @@ extern "C" int sl8_attn_paged_decode(const int8_t* q, const float* q_scale, cons
   int bs_sh = 0;
   while ((1LL << bs_sh) < block_size) ++bs_sh;
   const bool pow2 = (1LL << bs_sh) == block_size;
-  const PagedArgs pg{block_table, context_lens, (int)max_blocks_per_seq, (int)block_size, bs_sh};
+  const int64_t cache_rows = num_blocks * Hkv * block_size;
+  const PagedArgs pg{block_table, context_lens, (int)max_blocks_per_seq, (int)block_size, bs_sh,
+                     (int)std::min<int64_t>(cache_rows, (int64_t)0x7fffffff)};
   const int nmax = (int)max_context_len;
   const int64_t per = (max_context_len + ns - 1) / ns;
   const bool stream_ok = D != 32 && pow2 && per / block_size + 2 <= DEC_BT_MAX &&
                          ((gsz == 2 && D == 128) || gsz == 4 || gsz == 8);
+  // streaming tiles hold T = 32 (2 heads per KV head) or 16 keys; when blocks
+  // and split boundaries are multiples of T, each tile sits in one block
+  const int64_t tkeys = gsz == 2 ? 32 : 16;
+  const bool aligned_tiles = block_size % tkeys == 0 && per % tkeys == 0 &&
+                             cache_rows * D < (1LL << 31);
   if (stream_ok) {
     const dim3 g2((unsigned)ns, (unsigned)(B * Hkv));
 #define SL8_PWAVE(DD, GS, NB)                                                                   \
-    decode_wave_kernel<DD, GS, NB, true, true><<<g2, DEC_THREADS, 0, st>>>(                      \
-        q, q_scale, k_cache, k_scale, v_cache, v_scale, op, mp, lp, nmax, ns, (int)Hq, (int)Hkv, \
-        ibhq, pg)
+    do {                                                                                         \
+      if (aligned_tiles)                                                                         \
+        decode_wave_kernel<DD, GS, NB, true, true, false, true><<<g2, DEC_THREADS, 0, st>>>(     \
+            q, q_scale, k_cache, k_scale, v_cache, v_scale, op, mp, lp, nmax, ns, (int)Hq,       \
+            (int)Hkv, ibhq, pg);                                                                 \
+      else                                                                                       \
+        decode_wave_kernel<DD, GS, NB, true, true><<<g2, DEC_THREADS, 0, st>>>(                  \
+            q, q_scale, k_cache, k_scale, v_cache, v_scale, op, mp, lp, nmax, ns, (int)Hq,       \
+            (int)Hkv, ibhq, pg);                                                                 \
+    } while (0)
 #define SL8_PWAVE_D(GS)                        \
     if (D == 64) SL8_PWAVE(64, GS, 4);         \
     else if (D == 128) SL8_PWAVE(128, GS, 3);  \

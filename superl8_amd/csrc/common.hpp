@@ -88,4 +88,21 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Buffer-resource copies to LDS: a raw buffer of `bytes` bytes at `base`
+// (stride 0; the gfx9-family format dword). The per-lane byte offset stays in a
+// VGPR and the per-tile advance goes in the scalar offset, so a tile copy costs
+// no vector address arithmetic; offsets at or past `bytes` read as zero.
+typedef __amdgpu_buffer_rsrc_t brsrc_t;
+__device__ __forceinline__ brsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ void buf16_to_lds(brsrc_t r, void* lds_wave_base, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_wave_base, 16,
+                                           voff, soff, 0, 0);
+}
+__device__ __forceinline__ void buf4_to_lds(brsrc_t r, void* lds_wave_base, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_wave_base, 4,
+                                           voff, soff, 0, 0);
+}
+
 }  // namespace sl8

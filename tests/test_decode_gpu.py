@@ -217,6 +217,30 @@ def test_paged_kernel_matches_oracle(device, case, ns):
     assert_close_abs(out[:, :, 0], ref, atol=2e-3, rtol=2e-3, what=f"paged {case} ns={ns}")
 
 
+@pytest.mark.parametrize("case", [(2, 8, 2, 128, 16, (50, 7)), (3, 32, 8, 128, 16, (1000, 1, 333)),
+                                  (1, 16, 2, 128, 32, (100,)), (2, 16, 2, 64, 16, (20, 33))])
+def test_paged_unwritten_slots_never_leak(device, case):
+    """Slots past a sequence's length in its last block hold garbage (here NaN
+    scales and arbitrary codes): the result equals the oracle's on the written
+    rows, for block-aligned tiles (buffer copies of whole blocks) and others."""
+    B, Hq, Hkv, D, bs, lens = case
+    q, qs, kc, ks, vc, vs, bt, ctx = _paged_cache(case, device)
+    ks, vs = ks.clone(), vs.clone()
+    for b, n in enumerate(lens):
+        if n % bs:
+            blk = int(bt[b, n // bs])
+            ks[blk, :, n % bs:] = float("nan")
+            vs[blk, :, n % bs:] = float("nan")
+    nmax = max(lens)
+    for ns in (-1, 1, 4):
+        out = _C.attn_paged_decode(q, qs, kc, ks, vc, vs, bt, ctx, bs, nmax, ns)
+        n_splits = ns if ns > 0 else _C.paged_choose_n_splits(nmax, B * Hq)
+        ref = oa.attn_paged_decode(_np(q)[:, :, 0], _np(qs)[:, :, 0], _np(kc), _np(ks), _np(vc),
+                                   _np(vs), _np(bt), _np(ctx), nmax, n_splits)
+        assert_finite(out)
+        assert_close_abs(out[:, :, 0], ref, atol=2e-3, rtol=2e-3, what=f"paged garbage {case} ns={ns}")
+
+
 @pytest.mark.parametrize("ns", [-1, 3])
 def test_paged_context_above_max_is_clamped(device, ns):
     """context_lens[b] > max_context_len: keys past max_context_len (and the
