@@ -23,6 +23,15 @@ __device__ __forceinline__ void dma4_to_lds(const void* g, void* lds_wave_base) 
 }
 __device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
 
+// Keeps the computation of `x` ahead of this point: an empty volatile asm
+// that reads it, which neither the IR passes nor the machine scheduler move
+// across a scheduling barrier (they may otherwise sink pure arithmetic to its
+// first real use, out of the slice it was placed in).
+template <typename T>
+__device__ __forceinline__ void pin_vgpr(const T& x) {
+  asm volatile("" ::"v"(x));
+}
+
 // blockIdx.x -> (b*Hq + h, slot). Slots are issued in increasing order, so
 // callers put their heaviest work in slot 0. With xcd_map, workgroup ids are
 // dealt so that each KV head's query heads stay on one XCD (id % 8 is the

@@ -471,6 +471,10 @@ attn_fwd_kernel(const FwdArgs a) {
 #ifndef SL8_FWD_FAST
 #define SL8_FWD_FAST 1
 #endif
+// operand prefetch distance of the straight-line half-steps (MFMAs ahead)
+#ifndef SL8_FWD_PD
+#define SL8_FWD_PD 3
+#endif
 #ifndef SL8_FWD_OCC
 #define SL8_FWD_OCC 2
 #endif
@@ -484,6 +488,8 @@ attn_fwd_wide_kernel(const FwdArgs a) {
   constexpr int WT = WV * 64;                  // threads per workgroup
   // the straight-line steady-state half-step (half_step_fast): D = 128, NG = 1
   constexpr bool FAST = SL8_FWD_FAST && D == 128 && NG == 1 && !W8;
+  // ... and its W8A8 counterpart (half_step_fast_w8): D = 256, NG = 1, lazy rescale
+  constexpr bool FAST_W8 = SL8_FWD_FAST && D == 256 && NG == 1 && W8 && W8_LAZY;
   constexpr int WQ = 32 * NG;                  // queries per wave
   constexpr int WBM = WV * WQ;                 // queries per workgroup
   constexpr int DC = D / 32;
@@ -884,8 +890,8 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       if constexpr (W8_LAZY) settle(xo);
     };
     // Steady-state half-step (no masked key, every row's reference point set):
-    // one straight-line block whose LDS operand reads are all issued first,
-    // then the 12 MFMAs (QK of half h, PV of half h-2) each followed by a
+    // one straight-line block in which MFMA i (QK of half h, then PV of half
+    // h-2) is preceded by the LDS read of operand i + SL8_FWD_PD and followed by a
     // slice of the VALU work (P of half h-1, then the scores of half h), so
     // the matrix core never waits on an LDS round trip and the VALU runs
     // under the MFMAs. Same operations as half_step, in a fixed issue order.
@@ -914,21 +920,26 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       v16i sc;
 #pragma unroll
       for (int r = 0; r < 16; ++r) sc[r] = 0;
-      v4i cur = load_op(0);
+      v4i opb[NOP];  // operand i is read SL8_FWD_PD MFMAs ahead of its use
+#pragma unroll
+      for (int i = 0; i < SL8_FWD_PD && i < NOP; ++i) opb[i] = load_op(i);
       // Issue order, fixed by scheduling barriers: MFMA i is preceded by the
-      // read of operand i + 1 and followed by a slice of VALU work --
+      // read of operand i + SL8_FWD_PD and followed by a slice of VALU work --
       //   QK MFMAs 0..3: P of half h-1, four exp2 each;
       //   PV MFMAs 0..1: pack P to fp16 + row sums (one 16-key step each);
       //   PV MFMA 2: k_scale reads; PV MFMAs 3..6: scores of half h (cvt, * k_scale).
 #pragma unroll
       for (int i = 0; i < NOP; ++i) {
-        v4i nxt = cur;
-        if (i + 1 < NOP) nxt = load_op(i + 1);
+        if (i + SL8_FWD_PD < NOP) opb[i + SL8_FWD_PD] = load_op(i + SL8_FWD_PD);
+        __builtin_amdgcn_sched_barrier(0);  // the read goes out before MFMA i
+        const v4i cur = opb[i];
         if (i < DC) {
           sc = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur, qop[0].c[i], sc, 0, 0, 0);
 #pragma unroll
-          for (int e = 4 * i; e < 4 * i + 4; ++e)
+          for (int e = 4 * i; e < 4 * i + 4; ++e) {
             pe[e] = __builtin_amdgcn_exp2f(fmaf(xi[0][e], qsc[0], -msub));
+            pin_vgpr(pe[e]);
+          }
         } else {
           const int c = (i - DC) / DC, tt = (i - DC) % DC;
           oacc[0][tt] = PV::mfma(__builtin_bit_cast(pvec, cur), p2[0][c], oacc[0][tt]);
@@ -937,6 +948,8 @@ attn_fwd_wide_kernel(const FwdArgs a) {
             // same packing, row-sum order and overflow test as half_probs
             p1[0][k] = PV::pack(&pe[8 * k]);
             hs = PV::sum(p1[0][k], &pe[8 * k], hs);
+            pin_vgpr(__builtin_bit_cast(v4i, p1[0][k]));
+            pin_vgpr(hs);
             if (k == 1) {
               l_lane[0] += hs;
               ovf = ovf || (hs > 32768.f);
@@ -951,10 +964,101 @@ attn_fwd_wide_kernel(const FwdArgs a) {
             xo[0][4 * gq + 1] = (float)sc[4 * gq + 1] * kv[gq].y;
             xo[0][4 * gq + 2] = (float)sc[4 * gq + 2] * kv[gq].z;
             xo[0][4 * gq + 3] = (float)sc[4 * gq + 3] * kv[gq].w;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) pin_vgpr(xo[0][4 * gq + e]);
           }
         }
-        cur = nxt;
         __builtin_amdgcn_sched_barrier(0);
+      }
+      }
+    };
+
+    // W8A8 steady-state half-step (D = 256, one wave per SIMD, so the schedule
+    // inside the wave is all there is): the structure of half_step_fast with
+    // half_probs_w8's arithmetic, including its lazy rescale (a branch taken
+    // before the straight-line part, rarely).
+    auto half_step_fast_w8 = [&](int s, const int8_t* kt, const float* st, const uint16_t* vt,
+                                 xblk& xi, pblk& p1, xblk& xo, pblk& p2) __attribute__((always_inline)) {
+      if constexpr (FAST_W8) {
+      constexpr float LOG2_127 = 6.988684686772166f;
+      float tm0;
+      {
+        float tmx[1];
+        half_max(xi, tmx);
+        tm0 = tmx[0] * qsc[0];
+      }
+      // lazy rescale: the row's new reference point is used for this half's
+      // codes now; O (which still gets half h-2's products, relative to the old
+      // point, from the PV MFMAs below) and l are scaled after them
+      const bool ug = tm0 > m_run[0] + a.w8_excess;
+      const bool any_up = __any(ug);
+      const float fr = ug ? __builtin_amdgcn_exp2f(m_run[0] - tm0) : 1.f;
+      if (ug) m_run[0] = tm0;
+      const bool any_key = tm0 != -INFINITY;
+      const float sub = any_key ? tm0 - LOG2_127 : 0.f;
+      const float fac = any_key ? __builtin_amdgcn_exp2f(tm0 - m_run[0]) * (1.0f / 127.0f) : 0.f;
+      const uint16_t* vr = vt + l32 * BN;
+      auto load_op = [&](int i) __attribute__((always_inline)) -> v4i {
+        if (i < DC) return *reinterpret_cast<const v4i*>(kt + (32 * s + l32) * D + koff[i]);
+        const int c = (i - DC) / DC, tt = (i - DC) % DC;
+        return *reinterpret_cast<const v4i*>(vr + 32 * tt * BN + voff[2 * s + c]);
+      };
+      constexpr int NOP = 3 * DC;  // 8 QK + 16 PV MFMAs
+      float pe[16];
+      float hs = 0.f;
+      float4 kv[4];
+      v16i sc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sc[r] = 0;
+      v4i opb[NOP];  // operand i is read SL8_FWD_PD MFMAs ahead of its use
+#pragma unroll
+      for (int i = 0; i < SL8_FWD_PD && i < NOP; ++i) opb[i] = load_op(i);
+      // slices: QK MFMA i: P codes of keys 2i, 2i+1 of half h-1; PV MFMAs
+      // 0..1: pack them (bf16) + row sum; PV 2: k_scale reads; PV 3..10:
+      // scores of half h, two keys each
+#pragma unroll
+      for (int i = 0; i < NOP; ++i) {
+        if (i + SL8_FWD_PD < NOP) opb[i + SL8_FWD_PD] = load_op(i + SL8_FWD_PD);
+        __builtin_amdgcn_sched_barrier(0);  // the read goes out before MFMA i
+        const v4i cur = opb[i];
+        if (i < DC) {
+          sc = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur, qop[0].c[i], sc, 0, 0, 0);
+#pragma unroll
+          for (int e = 2 * i; e < 2 * i + 2; ++e) {
+            const float y = __builtin_amdgcn_exp2f(fmaf(xi[0][e], qsc[0], -sub));
+            hs += y;
+            pe[e] = rintf(y) * fac;
+            pin_vgpr(pe[e]);
+            pin_vgpr(hs);
+          }
+        } else {
+          const int c = (i - DC) / DC, tt = (i - DC) % DC;
+          oacc[0][tt] = PV::mfma(__builtin_bit_cast(pvec, cur), p2[0][c], oacc[0][tt]);
+          const int k = i - DC;
+          if (k < 2) {
+            p1[0][k] = PV::pack(&pe[8 * k]);
+            pin_vgpr(__builtin_bit_cast(v4i, p1[0][k]));
+            if (k == 1) l_lane[0] = l_lane[0] * fr + hs * fac;
+          } else if (k == 2) {
+#pragma unroll
+            for (int gq = 0; gq < 4; ++gq)
+              kv[gq] = *reinterpret_cast<const float4*>(st + 32 * s + 8 * gq + 4 * h);
+          } else if (k < 11) {
+            const int e0 = 2 * (k - 3);
+            const float ka[4] = {kv[e0 >> 2].x, kv[e0 >> 2].y, kv[e0 >> 2].z, kv[e0 >> 2].w};
+            xo[0][e0] = (float)sc[e0] * ka[e0 & 3];
+            xo[0][e0 + 1] = (float)sc[e0 + 1] * ka[(e0 + 1) & 3];
+            pin_vgpr(xo[0][e0]);
+            pin_vgpr(xo[0][e0 + 1]);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (any_up) {
+#pragma unroll
+        for (int t = 0; t < DC; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[0][t][r] *= fr;
       }
       }
     };
@@ -1034,8 +1138,15 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       const bool dead = !live(j);
       const bool mask = dead || masked(j);
       if constexpr (W8) {
-        half_step_w8(j, 0, kcur, scur, vprev, mask, dead, xB, pB, xA, pA);
-        half_step_w8(j, 1, kcur, scur, vprev, mask, dead, xA, pA, xB, pB);
+        if constexpr (FAST_W8) {
+          half_step_fast_w8(0, kcur, scur, vprev, xB, pB, xA, pA);
+          if (mask || !all_set) half_fixup(j, 0, mask, dead, xA);
+          half_step_fast_w8(1, kcur, scur, vprev, xA, pA, xB, pB);
+          if (mask || !all_set) half_fixup(j, 1, mask, dead, xB);
+        } else {
+          half_step_w8(j, 0, kcur, scur, vprev, mask, dead, xB, pB, xA, pA);
+          half_step_w8(j, 1, kcur, scur, vprev, mask, dead, xA, pA, xB, pB);
+        }
       } else {
         if constexpr (FAST) {
           // a masked half, or one that may fix some row's reference point,
