@@ -84,9 +84,11 @@ __device__ __forceinline__ uint32_t lane_pull(uint32_t v, int src_lane) {
 // at M = 8 measured 19.9 us against 17.3 us -- every wave then loads and
 // computes in the same phase, so no compute overlaps the memory stream. XB: the
 // activations carry one scale per 256-element block (x_scale [M, K/256],
-// applied per super-block) instead of one per row.
+// applied per super-block) instead of one per row; its 4 GCH scale registers
+// do not fit the 96-VGPR budget of 5 waves per SIMD (they spilled to
+// scratch), so XB asks for 4.
 template <int OUT_DT, int MT, int FMT = 4, int TPW = 1, bool XB = false>
-__global__ void __launch_bounds__(64 * GWAVES, TPW == 2 ? 3 : (MT == 1 ? (FMT == 4 ? 5 : 4) : 1))
+__global__ void __launch_bounds__(64 * GWAVES, TPW == 2 ? 3 : (MT == 1 ? (FMT == 4 && !XB ? 5 : 4) : 1))
 gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
                 const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K) {
   extern __shared__ __attribute__((aligned(16))) int8_t xl[];  // per wave: [M][GXPITCH]
