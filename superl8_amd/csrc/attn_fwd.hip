@@ -1130,11 +1130,18 @@ attn_fwd_wide_kernel(const FwdArgs a) {
     auto body = [&](int j, const int8_t* kcur, int8_t* knext, uint16_t* vcopy, const uint16_t* vprev,
                     const float* scur, float* snext) __attribute__((always_inline)) {
       const int n0 = n_beg + j * BN;
-      if (j + 1 < ntiles) {
-        load_k(n0 + BN, knext);
-        load_s(n0 + BN, snext);
-      }
-      if (j < ntiles) load_v(n0, vcopy);
+      auto copies = [&]() __attribute__((always_inline)) {
+        if (j + 1 < ntiles) {
+          load_k(n0 + BN, knext);
+          load_s(n0 + BN, snext);
+        }
+        if (j < ntiles) load_v(n0, vcopy);
+      };
+      // The straight-line D = 128 path issues the tile copies after its first
+      // half-step (0.5 % faster at config 2 than at the start of the tile,
+      // where they land in a burst on top of the first half's operand reads;
+      // the W8A8 path measured slower so).
+      if constexpr (!FAST) copies();
       const bool dead = !live(j);
       const bool mask = dead || masked(j);
       if constexpr (W8) {
@@ -1153,6 +1160,7 @@ attn_fwd_wide_kernel(const FwdArgs a) {
           // gets its mask / settle after the straight-line part
           half_step_fast(0, kcur, scur, vprev, xB, pB, xA, pA);
           if (mask || !all_set) half_fixup(j, 0, mask, dead, xA);
+          copies();
           half_step_fast(1, kcur, scur, vprev, xA, pA, xB, pB);
           if (mask || !all_set) half_fixup(j, 1, mask, dead, xB);
         } else {
