@@ -1144,7 +1144,13 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       if constexpr (!FAST) copies();
       const bool dead = !live(j);
       const bool mask = dead || masked(j);
-      if constexpr (W8) {
+      // A dead tile after a dead tile has nothing to do: the one before already
+      // pushed the last visible half's P through PV, and what it left pending
+      // is P = 0 and scores of -inf (in the diagonal block, the waves whose
+      // queries end early skip their last tiles this way).
+      if (dead && !live(j - 1)) {
+        if constexpr (FAST) copies();
+      } else if constexpr (W8) {
         if constexpr (FAST_W8) {
           half_step_fast_w8(0, kcur, scur, vprev, xB, pB, xA, pA);
           if (mask || !all_set) half_fixup(j, 0, mask, dead, xA);
