@@ -144,6 +144,19 @@ int sl8_attn_int8_fwd(const int8_t* q, const float* q_scale, const int8_t* k,
                       int64_t N, int64_t D, int causal, int64_t window_left,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* The same prefill for callers that decide an accuracy gate on the device:
+ * when *gate_flag (device int32, written earlier on the same stream, e.g. by
+ * sl8_quantize_qk) is nonzero every workgroup exits at once and out / lse are
+ * left unwritten. No counterpart in the reference, which reads its gate on
+ * the host before launching (superl8/ops.py:115-147); this lets the host read
+ * the flag while the attention already runs. */
+int sl8_attn_int8_fwd_gated(const int8_t* q, const float* q_scale, const int8_t* k,
+                            const float* k_scale, const void* v, int v_dtype, void* out,
+                            float* lse, int64_t B, int64_t Hq, int64_t Hkv, int64_t M,
+                            int64_t N, int64_t D, int causal, int64_t window_left,
+                            void* workspace, size_t workspace_bytes, const int32_t* gate_flag,
+                            void* stream);
+
 /* Test hook: the int32 Q.K^T scores exactly as the prefill kernel's MFMA
  * tiles produce them (same code path, scores dumped instead of softmaxed).
  *   scores int32 [B,Hq,M,N]. No reference counterpart (the reference never

@@ -229,7 +229,7 @@ def _fwd_checks(q, q_scale, k, k_scale, v):
     return B, H, Hkv, M, N, D
 
 
-def _attn_fwd(q, q_scale, k, k_scale, v, causal, window_left, want_lse):
+def _attn_fwd(q, q_scale, k, k_scale, v, causal, window_left, want_lse, gate_flag=None):
     B, H, Hkv, M, N, D = _fwd_checks(q, q_scale, k, k_scale, v)
     _check(v.dtype in (torch.float16, torch.bfloat16), "v must be float16 or bfloat16")
     _check(q_scale.numel() == B * H * M and k_scale.numel() == B * Hkv * N, "scale shape mismatch")
@@ -240,18 +240,28 @@ def _attn_fwd(q, q_scale, k, k_scale, v, causal, window_left, want_lse):
         return out, lse
     ws_bytes = _lib.load().sl8_attn_int8_fwd_workspace(B, H, Hkv, M, N, D)
     ws = torch.empty((ws_bytes,), device=q.device, dtype=torch.uint8) if ws_bytes else None
+    args = (q.data_ptr(), q_scale.data_ptr(), k.data_ptr(), k_scale.data_ptr(), v.data_ptr(),
+            dtype_code(v.dtype), out.data_ptr(), lse.data_ptr() if want_lse else None,
+            B, H, Hkv, M, N, D, int(bool(causal)), int(window_left),
+            ws.data_ptr() if ws is not None else None, ws_bytes)
     with torch.cuda.device(q.device):
-        call("sl8_attn_int8_fwd", q.data_ptr(), q_scale.data_ptr(), k.data_ptr(),
-             k_scale.data_ptr(), v.data_ptr(), dtype_code(v.dtype), out.data_ptr(),
-             lse.data_ptr() if want_lse else None, B, H, Hkv, M, N, D, int(bool(causal)),
-             int(window_left), ws.data_ptr() if ws is not None else None, ws_bytes, stream_of(q))
+        if gate_flag is None:
+            call("sl8_attn_int8_fwd", *args, stream_of(q))
+        else:
+            _check(gate_flag.is_cuda and gate_flag.dtype == torch.int32 and gate_flag.numel() >= 1,
+                   "gate_flag must be a CUDA int32 tensor")
+            call("sl8_attn_int8_fwd_gated", *args, gate_flag.data_ptr(), stream_of(q))
     return out, lse
 
 
-def attn_int8_fwd(q, q_scale, k, k_scale, v, causal=False, window_left=-1):
+def attn_int8_fwd(q, q_scale, k, k_scale, v, causal=False, window_left=-1, *, gate_flag=None):
     """q int8 [B,Hq,M,D], q_scale fp32 [B,Hq,M] (folded), k int8 [B,Hkv,N,D],
-    k_scale fp32 [B,Hkv,N], v fp16/bf16 [B,Hkv,N,D] -> out [B,Hq,M,D] (v's dtype)."""
-    return _attn_fwd(q, q_scale, k, k_scale, v, causal, window_left, False)[0]
+    k_scale fp32 [B,Hkv,N], v fp16/bf16 [B,Hkv,N,D] -> out [B,Hq,M,D] (v's dtype).
+
+    gate_flag (this build only): a CUDA int32 tensor written earlier on the
+    stream; when it holds a nonzero value the kernel exits at once and the
+    output is left unwritten (the caller discards it)."""
+    return _attn_fwd(q, q_scale, k, k_scale, v, causal, window_left, False, gate_flag)[0]
 
 
 def attn_int8_fwd_train(q, q_scale, k, k_scale, v, causal=False):

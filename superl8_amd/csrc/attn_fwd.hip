@@ -158,6 +158,7 @@ struct FwdArgs {
   int xcd_map;         // xcd_mode(): XCD-aware block order
   float w8_excess;     // W8A8: headroom of P above the reference point (log2)
   int dout;            // output row length (= D, or the caller's head dim when D is padded)
+  const int32_t* skip; // production kernel: nonzero *skip -> every workgroup exits at once
 };
 
 // LDS tiles are dense; 16-byte chunks are XOR-swizzled within each row
@@ -485,6 +486,8 @@ attn_fwd_kernel(const FwdArgs a) {
 template <int D, bool CAUSAL, int VDT, bool LSE, int NG, int WV, bool W8>
 __global__ void __launch_bounds__(WV * 64, (NG == 1 && D <= 128) ? SL8_FWD_OCC * 4 / WV : 1)
 attn_fwd_wide_kernel(const FwdArgs a) {
+  // the caller's accuracy gate fired: its result is discarded, so do nothing
+  if (a.skip != nullptr && *a.skip != 0) return;
   constexpr int WT = WV * 64;                  // threads per workgroup
   // the straight-line steady-state half-step (half_step_fast): D = 128, NG = 1
   constexpr bool FAST = SL8_FWD_FAST && D == 128 && NG == 1 && !W8;
@@ -1512,12 +1515,12 @@ extern "C" size_t sl8_attn_int8_fwd_workspace(int64_t B, int64_t Hq, int64_t Hkv
   return pad_workspace(B, Hq, Hkv, M, N, D, 2, false);
 }
 
-extern "C" int sl8_attn_int8_fwd(const int8_t* q, const float* q_scale, const int8_t* k,
-                                 const float* k_scale, const void* v, int v_dtype, void* out,
-                                 float* lse, int64_t B, int64_t Hq, int64_t Hkv, int64_t M,
-                                 int64_t N, int64_t D, int causal, int64_t window_left,
-                                 void* workspace, size_t workspace_bytes, void* stream) {
-  clear_error();
+namespace {
+int attn_int8_fwd_impl(const int8_t* q, const float* q_scale, const int8_t* k,
+                       const float* k_scale, const void* v, int v_dtype, void* out, float* lse,
+                       int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N, int64_t D,
+                       int causal, int64_t window_left, void* workspace, size_t workspace_bytes,
+                       const int32_t* skip, void* stream) {
   int rc = check_fwd_shape(B, Hq, Hkv, M, N, D);
   if (rc) return rc;
   SL8_CHECK_ARG(v_dtype == SL8_DTYPE_F16 || v_dtype == SL8_DTYPE_BF16,
@@ -1546,6 +1549,7 @@ extern "C" int sl8_attn_int8_fwd(const int8_t* q, const float* q_scale, const in
   a.vt = static_cast<const uint16_t*>(v);  // V [B*Hkv][N][DP], read in place
   a.out = out; a.lse = lse; a.window_left = (int)window_left;
   a.dout = (int)D;
+  a.skip = skip;
   const bool c = causal != 0, want_lse = lse != nullptr;
   a.nqb = (int)((M + wide_bm(DP) - 1) / wide_bm(DP));
   const int nslot = c ? (a.nqb + 1) / 2 : a.nqb;
@@ -1564,6 +1568,30 @@ extern "C" int sl8_attn_int8_fwd(const int8_t* q, const float* q_scale, const in
   }
   SL8_CHECK_LAUNCH("attn_int8_fwd");
   return SL8_OK;
+}
+}  // namespace
+
+extern "C" int sl8_attn_int8_fwd(const int8_t* q, const float* q_scale, const int8_t* k,
+                                 const float* k_scale, const void* v, int v_dtype, void* out,
+                                 float* lse, int64_t B, int64_t Hq, int64_t Hkv, int64_t M,
+                                 int64_t N, int64_t D, int causal, int64_t window_left,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  return attn_int8_fwd_impl(q, q_scale, k, k_scale, v, v_dtype, out, lse, B, Hq, Hkv, M, N, D,
+                            causal, window_left, workspace, workspace_bytes, nullptr, stream);
+}
+
+extern "C" int sl8_attn_int8_fwd_gated(const int8_t* q, const float* q_scale, const int8_t* k,
+                                       const float* k_scale, const void* v, int v_dtype,
+                                       void* out, float* lse, int64_t B, int64_t Hq, int64_t Hkv,
+                                       int64_t M, int64_t N, int64_t D, int causal,
+                                       int64_t window_left, void* workspace,
+                                       size_t workspace_bytes, const int32_t* gate_flag,
+                                       void* stream) {
+  clear_error();
+  SL8_CHECK_ARG(gate_flag != nullptr, "fni8: attn_int8_fwd_gated needs the gate flag");
+  return attn_int8_fwd_impl(q, q_scale, k, k_scale, v, v_dtype, out, lse, B, Hq, Hkv, M, N, D,
+                            causal, window_left, workspace, workspace_bytes, gate_flag, stream);
 }
 
 extern "C" int sl8_attn_int8_qk_scores(const int8_t* q, const int8_t* k, int32_t* scores,

@@ -34,9 +34,20 @@ def attn_int8_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: 
     from . import quant
 
     if internal_accuracy_gate:
-        fired, qk = quant.quantize_qk_gated(q, k, softmax_scale=scale, rotate=rotate)
+        fired, qk = quant.quantize_qk_gated(q, k, softmax_scale=scale, rotate=rotate,
+                                            defer=not int8_pv)
     else:
         fired, qk = False, quant.quantize_qk(q, k, softmax_scale=scale, rotate=rotate)
+    if isinstance(fired, torch.Tensor):
+        # gate decided on the device: launch the attention first (it exits at
+        # once if the gate fired), then read the flag while it runs
+        q_i8, q_scale, k_i8, k_scale, _k_mean = qk
+        out = _C.attn_int8_fwd(q_i8, q_scale.squeeze(-1).contiguous(), k_i8,
+                               k_scale.squeeze(-1).contiguous(), v.contiguous(), causal,
+                               window_left, gate_flag=fired)
+        if not bool(fired.item()):
+            return out
+        fired = True
     if fired:
         import torch.nn.functional as F
 

@@ -100,7 +100,7 @@ def _fused_ok(q: torch.Tensor, k: torch.Tensor) -> bool:
 
 
 def quantize_qk_gated(q: torch.Tensor, k: torch.Tensor, *, softmax_scale: float | None = None,
-                      rotate: bool = False, ratio_threshold: float = 12.0):
+                      rotate: bool = False, ratio_threshold: float = 12.0, defer: bool = False):
     """The attention prologue with the outlier gate (reference ops.py:115-150).
 
     Returns (fired, quantize_qk's five outputs or None). fired is
@@ -109,7 +109,9 @@ def quantize_qk_gated(q: torch.Tensor, k: torch.Tensor, *, softmax_scale: float 
     rotation the gate is decided inside the fused prologue (one flag read);
     otherwise it is evaluated first and quantize_qk runs only when it passes.
     Under graph capture the gate is skipped (False), as in
-    detect_q_outlier_domination.
+    detect_q_outlier_domination. With defer=True the fused path returns the
+    device flag (int32 [1]) in place of fired, unread, with the quantised
+    tensors: the caller reads it later (the other paths still return a bool).
     """
     _need_gpu(q, "quantize_qk")
     try:
@@ -120,6 +122,8 @@ def quantize_qk_gated(q: torch.Tensor, k: torch.Tensor, *, softmax_scale: float 
         s = (1.0 / math.sqrt(q.shape[-1])) if softmax_scale is None else softmax_scale
         q_i8, q_scale, k_i8, k_scale, k_mean, flag = _C.quantize_qk_fused(
             q, k, s * LOG2E, ratio_threshold)
+        if defer:
+            return flag, (q_i8, q_scale.unsqueeze(-1), k_i8, k_scale.unsqueeze(-1), k_mean)
         if bool(flag.item()):
             return True, None
         return False, (q_i8, q_scale.unsqueeze(-1), k_i8, k_scale.unsqueeze(-1), k_mean)

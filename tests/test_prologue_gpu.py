@@ -110,3 +110,49 @@ def test_fused_rejects(device):
         _C.quantize_qk_fused(q, q, 1.0)
     with pytest.raises(RuntimeError):
         _C.quantize_qk_fused(q.float()[..., :64].contiguous(), q.float()[..., :64].contiguous(), 1.0)
+
+
+def test_gated_prefill_skips_or_matches(device):
+    """sl8_attn_int8_fwd_gated through the C ABI: with the flag set every
+    workgroup exits and the output buffer keeps its contents; with it clear the
+    output is bit-identical to sl8_attn_int8_fwd's."""
+    from superl8_amd import _lib
+    from superl8_amd._lib import dtype_code
+
+    torch.manual_seed(5)
+    B, Hq, Hkv, M, N, D = 1, 4, 2, 200, 300, 128
+    q = torch.randn(B, Hq, M, D, device=device, dtype=torch.float16)
+    k = torch.randn(B, Hkv, N, D, device=device, dtype=torch.float16)
+    v = torch.randn(B, Hkv, N, D, device=device, dtype=torch.float16)
+    q_i8, qs, k_i8, ks, _ = quant.quantize_qk(q, k)
+    qs, ks = qs.squeeze(-1).contiguous(), ks.squeeze(-1).contiguous()
+    ref = _C.attn_int8_fwd(q_i8, qs, k_i8, ks, v, True)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    for flag_val in (1, 0):
+        flag = torch.full((1,), flag_val, device=device, dtype=torch.int32)
+        out = torch.full_like(ref, 7.0)
+        rc = lib.sl8_attn_int8_fwd_gated(q_i8.data_ptr(), qs.data_ptr(), k_i8.data_ptr(),
+                                         ks.data_ptr(), v.data_ptr(), dtype_code(v.dtype),
+                                         out.data_ptr(), None, B, Hq, Hkv, M, N, D, 1, -1,
+                                         None, 0, flag.data_ptr(), stream)
+        assert rc == 0, lib.sl8_last_error()
+        torch.cuda.synchronize()
+        if flag_val:
+            assert torch.equal(out, torch.full_like(ref, 7.0))
+        else:
+            assert torch.equal(out, ref)
+
+
+def test_public_prefill_deferred_gate_is_the_two_step_path(device):
+    """ops.attn_int8_fwd reads the fused prologue's gate flag after launching the
+    attention: a call whose gate stays quiet returns exactly prologue + kernel."""
+    torch.manual_seed(6)
+    q = torch.randn(2, 8, 300, 128, device=device, dtype=torch.float16)
+    k = torch.randn(2, 2, 300, 128, device=device, dtype=torch.float16)
+    v = torch.randn(2, 2, 300, 128, device=device, dtype=torch.float16)
+    o = ops.attn_int8_fwd(q, k, v, causal=True)
+    q_i8, qs, k_i8, ks, _ = quant.quantize_qk(q, k)
+    two_step = _C.attn_int8_fwd(q_i8, qs.squeeze(-1).contiguous(), k_i8,
+                                ks.squeeze(-1).contiguous(), v, True)
+    assert torch.equal(o, two_step)
