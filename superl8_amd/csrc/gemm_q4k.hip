@@ -219,7 +219,10 @@ gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
             }
             const int bsel = 8 * (2 * hp + nb);
             const int sc = ((L == 0 ? sm.sc_lo : sm.sc_hi) >> bsel) & 0xFF;
-            const uint32_t mn = (((L == 0 ? sm.mn_lo : sm.mn_hi) >> bsel) & 0xFF) * 0x01010101u;
+            // byte (2hp + nb) of the packed mins in all four bytes (one v_perm
+            // instead of a shift, a mask and a quarter-rate 32-bit multiply)
+            const uint32_t mn = __builtin_amdgcn_perm(0u, L == 0 ? sm.mn_lo : sm.mn_hi,
+                                                      (uint32_t)(2 * hp + nb) * 0x01010101u);
             const v4i bmin = {(int)mn, (int)mn, (int)mn, (int)mn};
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
