@@ -891,12 +891,19 @@ void launch_gemv_q6k_mfma(const int8_t* x, const float* xs, const uint8_t* w, vo
 #undef SL8_Q6M
 }
 
+#ifndef SL8_Q5_SMALL
+#define SL8_Q5_SMALL 1
+#endif
 template <int FMT>
 void launch_gemv_kq(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
                     int M, int N, int K, hipStream_t st) {
   if (M >= 3) {  // the int8 MFMA GEMVs (Q5_K: the Q4_K kernel of gemm_q4k.hip)
     if (FMT == 5) launch_gemv_q5k_mfma(x, xs, w, out, odt, M, N, K, st);
     else launch_gemv_q6k_mfma(x, xs, w, out, odt, M, N, K, st);
+    return;
+  }
+  if (FMT == 5 && SL8_Q5_SMALL) {  // Q5_K, M <= 2: the Q4_K M <= 2 kernel's layout (gemm_q4k.hip)
+    launch_gemv_q5k_small(x, xs, w, out, odt, M, N, K, st);
     return;
   }
   if (M == 1) launch_gemv_kq_m<FMT, 1>(x, xs, w, out, odt, M, N, K, st);

@@ -326,8 +326,15 @@ constexpr int SXPITCH = SCH * 256;
 #ifndef SL8_GEMV_SOCC
 #define SL8_GEMV_SOCC 8
 #endif
-template <int OUT_DT, int MR, bool XB = false>
-__global__ void __launch_bounds__(64 * SWAVES, (SL8_GEMV_SOCC > 0 && MR == 1) ? SL8_GEMV_SOCC : 1)
+#ifndef SL8_GEMV_SOCC5
+#define SL8_GEMV_SOCC5 6
+#endif
+// FMT = 5: Q5_K super-blocks (176 bytes: header, 32 bytes of 5th bits qh, then
+// the Q4_K nibble layout); lane (r, c) also loads qh bytes 16 (c & 1) .. +15,
+// the 5th bits of its elements (byte l holds bit j for element l of
+// sub-block j), and each code is n + 16 b.
+template <int OUT_DT, int MR, bool XB = false, int FMT = 4>
+__global__ void __launch_bounds__(64 * SWAVES, (SL8_GEMV_SOCC > 0 && MR == 1) ? (FMT == 4 ? SL8_GEMV_SOCC : SL8_GEMV_SOCC5) : 1)
 gemv_q4k_small_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
                       const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K) {
   constexpr int XC = (MR * SXPITCH + 1023) / 1024;  // 16-byte activation pieces per lane
@@ -340,7 +347,9 @@ gemv_q4k_small_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_
   const int r = lane >> 2, c = lane & 3;
   const int g = c >> 1, half = c & 1;
   const int n0 = blockIdx.x * GEMV_ROWS;
-  const int64_t row_bytes = (int64_t)nsb * Q4K_BYTES;
+  constexpr int BB = FMT == 4 ? Q4K_BYTES : 176;  // bytes per super-block
+  constexpr int QS = FMT == 4 ? 16 : 48;          // offset of the nibbles
+  const int64_t row_bytes = (int64_t)nsb * BB;
   const uint8_t* wrow = w + (int64_t)min(n0 + r, N - 1) * row_bytes;
   int8_t* xw = &xs_l[wave][0];
 
@@ -366,14 +375,17 @@ gemv_q4k_small_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_
     // re-reads its last super-block instead of running past the row)
     uint32_t hd[SCH];
     uint4 qa[SCH], qb[SCH];
-    const uint8_t* bh = wrow + (int64_t)c0 * Q4K_BYTES + 4 * c;
-    const uint8_t* bq = wrow + (int64_t)c0 * Q4K_BYTES + 16 * c;
+    const uint8_t* bh = wrow + (int64_t)c0 * BB + 4 * c;
+    const uint8_t* bq = wrow + (int64_t)c0 * BB + 16 * c;
+    uint4 qh5[FMT == 5 ? SCH : 1];  // Q5_K: qh bytes 16 half .. +15
 #pragma unroll
     for (int i = 0; i < SCH; ++i) {
       const int ii = cnt == SCH ? i : min(i, cnt - 1);
-      hd[i] = *reinterpret_cast<const uint32_t*>(bh + ii * Q4K_BYTES);
-      qa[i] = *reinterpret_cast<const uint4*>(bq + ii * Q4K_BYTES + 16);
-      qb[i] = *reinterpret_cast<const uint4*>(bq + ii * Q4K_BYTES + 80);
+      hd[i] = *reinterpret_cast<const uint32_t*>(bh + ii * BB);
+      qa[i] = *reinterpret_cast<const uint4*>(bq + ii * BB + QS);
+      qb[i] = *reinterpret_cast<const uint4*>(bq + ii * BB + QS + 64);
+      if constexpr (FMT == 5)
+        qh5[i] = *reinterpret_cast<const uint4*>(wrow + (int64_t)(c0 + ii) * BB + 16 + 16 * half);
     }
     __builtin_amdgcn_sched_barrier(0);
     // ---- activations to LDS ([m][SXPITCH]) and their 16-element sums ----
@@ -420,10 +432,24 @@ gemv_q4k_small_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_
           int p0 = 0, p1 = 0, p4 = 0, p5 = 0;
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
-            p0 = __builtin_amdgcn_sdot4(xa0[k], (int)(wa[k] & 0x0F0F0F0Fu), p0, false);
-            p1 = __builtin_amdgcn_sdot4(xa1[k], (int)((wa[k] >> 4) & 0x0F0F0F0Fu), p1, false);
-            p4 = __builtin_amdgcn_sdot4(xa4[k], (int)(wbq[k] & 0x0F0F0F0Fu), p4, false);
-            p5 = __builtin_amdgcn_sdot4(xa5[k], (int)((wbq[k] >> 4) & 0x0F0F0F0Fu), p5, false);
+            if constexpr (FMT == 4) {
+              p0 = __builtin_amdgcn_sdot4(xa0[k], (int)(wa[k] & 0x0F0F0F0Fu), p0, false);
+              p1 = __builtin_amdgcn_sdot4(xa1[k], (int)((wa[k] >> 4) & 0x0F0F0F0Fu), p1, false);
+              p4 = __builtin_amdgcn_sdot4(xa4[k], (int)(wbq[k] & 0x0F0F0F0Fu), p4, false);
+              p5 = __builtin_amdgcn_sdot4(xa5[k], (int)((wbq[k] >> 4) & 0x0F0F0F0Fu), p5, false);
+            } else {
+              // codes n + 16 b of sub-blocks 2g, 2g+1 (qa) and 2g+4, 2g+5 (qb):
+              // bit j of each qh byte goes to bit 4 of the code of sub-block j
+              const uint32_t hk = k == 0 ? qh5[i].x : k == 1 ? qh5[i].y : k == 2 ? qh5[i].z : qh5[i].w;
+              const uint32_t q0 = (wa[k] & 0x0F0F0F0Fu) | (((hk >> (2 * g)) & 0x01010101u) << 4);
+              const uint32_t q1 = ((wa[k] >> 4) & 0x0F0F0F0Fu) | (((hk >> (2 * g + 1)) & 0x01010101u) << 4);
+              const uint32_t q4 = (wbq[k] & 0x0F0F0F0Fu) | (((hk >> (2 * g + 4)) & 0x01010101u) << 4);
+              const uint32_t q5 = ((wbq[k] >> 4) & 0x0F0F0F0Fu) | (((hk >> (2 * g + 5)) & 0x01010101u) << 4);
+              p0 = __builtin_amdgcn_sdot4(xa0[k], (int)q0, p0, false);
+              p1 = __builtin_amdgcn_sdot4(xa1[k], (int)q1, p1, false);
+              p4 = __builtin_amdgcn_sdot4(xa4[k], (int)q4, p4, false);
+              p5 = __builtin_amdgcn_sdot4(xa5[k], (int)q5, p5, false);
+            }
           }
           const int* xsr = &xsum_l[wave][m][i][half][0];
           const int2 s01 = *reinterpret_cast<const int2*>(xsr + 2 * g);
@@ -651,19 +677,19 @@ __global__ void dequant_q4k_kernel(const uint8_t* __restrict__ w, float* __restr
   for (int e = 0; e < 32; ++e) o[e] = dsc * (float)((qs[e] >> shift) & 0xF) - dm;
 }
 
-template <int MR, bool XB = false>
+template <int MR, bool XB = false, int FMT = 4>
 void launch_gemv_small(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
                        int M, int N, int K, hipStream_t st) {
   const dim3 grid((unsigned)((N + GEMV_ROWS - 1) / GEMV_ROWS));
   switch (odt) {
     case SL8_DTYPE_F16:
-      gemv_q4k_small_kernel<SL8_DTYPE_F16, MR, XB><<<grid, 64 * SWAVES, 0, st>>>(x, xs, w, out, M, N, K);
+      gemv_q4k_small_kernel<SL8_DTYPE_F16, MR, XB, FMT><<<grid, 64 * SWAVES, 0, st>>>(x, xs, w, out, M, N, K);
       break;
     case SL8_DTYPE_BF16:
-      gemv_q4k_small_kernel<SL8_DTYPE_BF16, MR, XB><<<grid, 64 * SWAVES, 0, st>>>(x, xs, w, out, M, N, K);
+      gemv_q4k_small_kernel<SL8_DTYPE_BF16, MR, XB, FMT><<<grid, 64 * SWAVES, 0, st>>>(x, xs, w, out, M, N, K);
       break;
     default:
-      gemv_q4k_small_kernel<SL8_DTYPE_F32, MR, XB><<<grid, 64 * SWAVES, 0, st>>>(x, xs, w, out, M, N, K);
+      gemv_q4k_small_kernel<SL8_DTYPE_F32, MR, XB, FMT><<<grid, 64 * SWAVES, 0, st>>>(x, xs, w, out, M, N, K);
       break;
   }
 }
@@ -686,6 +712,13 @@ void launch_gemv_mt(const int8_t* x, const float* xs, const uint8_t* w, void* ou
 }
 
 }  // namespace
+
+// Q5_K decode GEMV for M <= 2 on the M <= 2 kernel above (called from gemm_kq56.hip).
+void launch_gemv_q5k_small(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
+                           int M, int N, int K, hipStream_t st) {
+  if (M == 1) launch_gemv_small<1, false, 5>(x, xs, w, out, odt, M, N, K, st);
+  else launch_gemv_small<2, false, 5>(x, xs, w, out, odt, M, N, K, st);
+}
 
 // Q5_K decode GEMV (3 <= M <= 16) on the MFMA kernel above (called from gemm_kq56.hip).
 void launch_gemv_q5k_mfma(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,

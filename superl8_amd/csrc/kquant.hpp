@@ -31,6 +31,9 @@ __device__ __forceinline__ uint32_t mul_bytes(uint32_t bytes, uint32_t f) {
   return __builtin_bit_cast(uint32_t, a * b);
 }
 
+// Q5_K decode GEMV for M <= 2 on the Q4_K M <= 2 kernel (gemm_q4k.hip)
+void launch_gemv_q5k_small(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
+                           int M, int N, int K, hipStream_t st);
 // Q5_K decode GEMV for 3 <= M <= 16 on the int8 MFMA (gemm_q4k.hip)
 void launch_gemv_q5k_mfma(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
                           int M, int N, int K, hipStream_t st);
