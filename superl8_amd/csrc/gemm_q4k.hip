@@ -87,7 +87,14 @@ __device__ __forceinline__ uint32_t lane_pull(uint32_t v, int src_lane) {
 // applied per super-block) instead of one per row; its 4 GCH scale registers
 // do not fit the 96-VGPR budget of 5 waves per SIMD (they spilled to
 // scratch), so XB asks for 4.
-template <int OUT_DT, int MT, int FMT = 4, int TPW = 1, bool XB = false>
+// OPL: the weights are loaded straight into the MFMA operand layout (lane
+// (row lj, group h) reads its own 16-byte pieces and the row's whole header)
+// instead of the coalesced layout plus ds_bpermute moves. Same bytes, more
+// cache-line segments per load instruction and no cross-lane moves; measured
+// at config 4's shape: M = 4 15.9 -> 14.9 us, M = 16 36.2 -> 33.4 us, but
+// M = 8 17.6 -> 18.1 us (its header registers spill at 5 waves per SIMD), so
+// the launcher uses it for M <= 4 and M > 8.
+template <int OUT_DT, int MT, int FMT = 4, int TPW = 1, bool XB = false, bool OPL = false>
 __global__ void __launch_bounds__(64 * GWAVES, TPW == 2 ? 3 : (MT == 1 ? (FMT == 4 && !XB ? 5 : 4) : 1))
 gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
                 const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K) {
@@ -109,7 +116,7 @@ gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
   const uint8_t* wrow[TPW];
 #pragma unroll
   for (int tt = 0; tt < TPW; ++tt)
-    wrow[tt] = w + (int64_t)min(n0 + GEMV_ROWS * tt + lr, N - 1) * row_bytes;
+    wrow[tt] = w + (int64_t)min(n0 + GEMV_ROWS * tt + (OPL ? lj : lr), N - 1) * row_bytes;
   const int a_m = lj & 7;    // A-operand row: activation t*8 + a_m, parity lj >> 3
   const bool a_side = (lj >> 3) == hp;  // this lane's k-slots feed its A row
   bool a_on[MT];
@@ -149,11 +156,21 @@ gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
     uint32_t hd[TPW][GCH];
     uint4 qa[TPW][GCH], qb[TPW][GCH];
     uint2 qh8[TPW][FMT == 5 ? GCH : 1];  // Q5_K: qh bytes 8 lc .. 8 lc + 7 of the row
+    uint4 hd4[TPW][OPL ? GCH : 1];       // OPL: the row's whole header
+    uint4 qh16[TPW][OPL && FMT == 5 ? GCH : 1];  // OPL, Q5_K: qh bytes 16 (h & 1) .. +15
 #pragma unroll
     for (int tt = 0; tt < TPW; ++tt)
 #pragma unroll
       for (int i = 0; i < GCH; ++i) {
         const uint8_t* blk = wrow[tt] + (int64_t)min(c0 + i, nsb - 1) * BB;
+        if constexpr (OPL) {
+          // operand layout: lane (row lj, group h) loads its own pieces
+          hd4[tt][i] = *reinterpret_cast<const uint4*>(blk);
+          qa[tt][i] = *reinterpret_cast<const uint4*>(blk + QS + 16 * h);
+          qb[tt][i] = *reinterpret_cast<const uint4*>(blk + QS + 64 + 16 * h);
+          if constexpr (FMT == 5) qh16[tt][i] = *reinterpret_cast<const uint4*>(blk + 16 + 16 * (h & 1));
+          continue;
+        }
         hd[tt][i] = *reinterpret_cast<const uint32_t*>(blk + 4 * lc);
         qa[tt][i] = *reinterpret_cast<const uint4*>(blk + QS + 16 * lc);
         qb[tt][i] = *reinterpret_cast<const uint4*>(blk + QS + 64 + 16 * lc);
@@ -179,16 +196,25 @@ gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
     for (int i = 0; i < GCH; ++i) {
       if (i < cnt) {
         // ---- pieces to the operand layout ----
-        const uint32_t h0 = lane_pull(hd[tt][i], 4 * lj + 0), h1 = lane_pull(hd[tt][i], 4 * lj + 1);
-        const uint32_t h2 = lane_pull(hd[tt][i], 4 * lj + 2), h3 = lane_pull(hd[tt][i], 4 * lj + 3);
+        uint32_t h0, h1, h2, h3;
         uint32_t qw[2][4];
-        qw[0][0] = lane_pull(qa[tt][i].x, src_q); qw[0][1] = lane_pull(qa[tt][i].y, src_q);
-        qw[0][2] = lane_pull(qa[tt][i].z, src_q); qw[0][3] = lane_pull(qa[tt][i].w, src_q);
-        qw[1][0] = lane_pull(qb[tt][i].x, src_q); qw[1][1] = lane_pull(qb[tt][i].y, src_q);
-        qw[1][2] = lane_pull(qb[tt][i].z, src_q); qw[1][3] = lane_pull(qb[tt][i].w, src_q);
+        if constexpr (OPL) {
+          h0 = hd4[tt][i].x; h1 = hd4[tt][i].y; h2 = hd4[tt][i].z; h3 = hd4[tt][i].w;
+          qw[0][0] = qa[tt][i].x; qw[0][1] = qa[tt][i].y; qw[0][2] = qa[tt][i].z; qw[0][3] = qa[tt][i].w;
+          qw[1][0] = qb[tt][i].x; qw[1][1] = qb[tt][i].y; qw[1][2] = qb[tt][i].z; qw[1][3] = qb[tt][i].w;
+        } else {
+          h0 = lane_pull(hd[tt][i], 4 * lj + 0); h1 = lane_pull(hd[tt][i], 4 * lj + 1);
+          h2 = lane_pull(hd[tt][i], 4 * lj + 2); h3 = lane_pull(hd[tt][i], 4 * lj + 3);
+          qw[0][0] = lane_pull(qa[tt][i].x, src_q); qw[0][1] = lane_pull(qa[tt][i].y, src_q);
+          qw[0][2] = lane_pull(qa[tt][i].z, src_q); qw[0][3] = lane_pull(qa[tt][i].w, src_q);
+          qw[1][0] = lane_pull(qb[tt][i].x, src_q); qw[1][1] = lane_pull(qb[tt][i].y, src_q);
+          qw[1][2] = lane_pull(qb[tt][i].z, src_q); qw[1][3] = lane_pull(qb[tt][i].w, src_q);
+        }
         const ScMin sm = unpack_scmin(h1, h2, h3);
         uint32_t qhw[4] = {0, 0, 0, 0};  // Q5_K: qh bytes 16(h&1) .. +15 of row lj
-        if constexpr (FMT == 5) {
+        if constexpr (OPL && FMT == 5) {
+          qhw[0] = qh16[tt][i].x; qhw[1] = qh16[tt][i].y; qhw[2] = qh16[tt][i].z; qhw[3] = qh16[tt][i].w;
+        } else if constexpr (FMT == 5) {
           const int s0 = 4 * lj + 2 * (h & 1);
           qhw[0] = lane_pull(qh8[tt][i].x, s0);
           qhw[1] = lane_pull(qh8[tt][i].y, s0);
@@ -699,14 +725,18 @@ void launch_gemv_mt(const int8_t* x, const float* xs, const uint8_t* w, void* ou
                     int M, int N, int K, hipStream_t st) {
   const dim3 grid((unsigned)((N + GEMV_ROWS - 1) / GEMV_ROWS));
   const size_t lds = (size_t)GWAVES * ((((size_t)M * GXPITCH + 1023) & ~(size_t)1023) + GXPITCH);
-#define SL8_GM(DT, TP) gemv_q4k_kernel<DT, MT, 4, TP, XB><<<grid, 64 * GWAVES, lds, st>>>(x, xs, w, out, M, N, K)
-#define SL8_GM_DT(TP)                                   \
+#define SL8_GM(DT, OP) gemv_q4k_kernel<DT, MT, 4, 1, XB, OP><<<grid, 64 * GWAVES, lds, st>>>(x, xs, w, out, M, N, K)
+#define SL8_GM_DT(OP)                                   \
   switch (odt) {                                        \
-    case SL8_DTYPE_F16: SL8_GM(SL8_DTYPE_F16, TP); break;   \
-    case SL8_DTYPE_BF16: SL8_GM(SL8_DTYPE_BF16, TP); break; \
-    default: SL8_GM(SL8_DTYPE_F32, TP); break;             \
+    case SL8_DTYPE_F16: SL8_GM(SL8_DTYPE_F16, OP); break;   \
+    case SL8_DTYPE_BF16: SL8_GM(SL8_DTYPE_BF16, OP); break; \
+    default: SL8_GM(SL8_DTYPE_F32, OP); break;             \
   }
-  SL8_GM_DT(1)
+  if (MT == 2 || M <= 4) {
+    SL8_GM_DT(true)
+  } else {
+    SL8_GM_DT(false)
+  }
 #undef SL8_GM_DT
 #undef SL8_GM
 }
