@@ -750,18 +750,26 @@ void launch_gemv_q5k_small(const int8_t* x, const float* xs, const uint8_t* w, v
   else launch_gemv_small<2, false, 5>(x, xs, w, out, odt, M, N, K, st);
 }
 
+// operand-layout loads for Q5_K too at M <= 4 and 9 <= M <= 16 (config 4's
+// shape: M = 4 18.9 -> 18.6 us, M = 16 40.8 -> 39.2 us; M = 8 unchanged)
+#ifndef SL8_Q5_OPLM
+#define SL8_Q5_OPLM 4
+#endif
+#ifndef SL8_Q5_OPL2
+#define SL8_Q5_OPL2 1
+#endif
 // Q5_K decode GEMV (3 <= M <= 16) on the MFMA kernel above (called from gemm_kq56.hip).
 void launch_gemv_q5k_mfma(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
                           int M, int N, int K, hipStream_t st) {
   const dim3 grid((unsigned)((N + GEMV_ROWS - 1) / GEMV_ROWS));
   const size_t lds = (size_t)GWAVES * ((((size_t)M * GXPITCH + 1023) & ~(size_t)1023) + GXPITCH);
-#define SL8_Q5M(MT)                                                                                   \
+#define SL8_Q5M(MT, OP)                                                                               \
   switch (odt) {                                                                                      \
-    case SL8_DTYPE_F16: gemv_q4k_kernel<SL8_DTYPE_F16, MT, 5><<<grid, 64 * GWAVES, lds, st>>>(x, xs, w, out, M, N, K); break; \
-    case SL8_DTYPE_BF16: gemv_q4k_kernel<SL8_DTYPE_BF16, MT, 5><<<grid, 64 * GWAVES, lds, st>>>(x, xs, w, out, M, N, K); break; \
-    default: gemv_q4k_kernel<SL8_DTYPE_F32, MT, 5><<<grid, 64 * GWAVES, lds, st>>>(x, xs, w, out, M, N, K); break; \
+    case SL8_DTYPE_F16: gemv_q4k_kernel<SL8_DTYPE_F16, MT, 5, 1, false, OP><<<grid, 64 * GWAVES, lds, st>>>(x, xs, w, out, M, N, K); break; \
+    case SL8_DTYPE_BF16: gemv_q4k_kernel<SL8_DTYPE_BF16, MT, 5, 1, false, OP><<<grid, 64 * GWAVES, lds, st>>>(x, xs, w, out, M, N, K); break; \
+    default: gemv_q4k_kernel<SL8_DTYPE_F32, MT, 5, 1, false, OP><<<grid, 64 * GWAVES, lds, st>>>(x, xs, w, out, M, N, K); break; \
   }
-  if (M <= 8) { SL8_Q5M(1) } else { SL8_Q5M(2) }
+  if (M <= SL8_Q5_OPLM) { SL8_Q5M(1, true) } else if (M <= 8) { SL8_Q5M(1, false) } else if (SL8_Q5_OPL2) { SL8_Q5M(2, true) } else { SL8_Q5M(2, false) }
 #undef SL8_Q5M
 }
 
