@@ -38,6 +38,9 @@ constexpr int DEC_MAX_SPLITS = 256;
 #define SL8_DEC_PAIR 1
 #endif
 constexpr bool DEC_PAIR = SL8_DEC_PAIR;  // int8-V PV: two keys per v_dot2 (see decode_wave_kernel)
+#ifndef SL8_DEC_PV4
+#define SL8_DEC_PV4 1
+#endif
 
 template <int D, int G>
 struct DecSmem {
@@ -425,7 +428,7 @@ struct WaveCfg {
 // block, so a tile's physical rows are one uniform base plus the lane's fixed
 // offset and its copies go through buffer resources like the contiguous ones.
 template <int D, int GS, int NB, bool VI8, bool PG, bool KS16 = false, bool PGA = false>
-__global__ void __launch_bounds__(DEC_THREADS)
+__global__ void __launch_bounds__(DEC_THREADS, (SL8_DEC_PV4 && VI8 && DEC_PAIR && D == 128 && GS == 4) ? 3 : 1)
 decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_scale,
                    const int8_t* __restrict__ k, const void* __restrict__ k_scale,
                    const void* __restrict__ v, const float* __restrict__ vsc,
@@ -568,6 +571,28 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
   float pq_sum = 0.f;  // VI8 pair path: the head's sum of the fp16 p that entered PV
 #pragma unroll
   for (int e = 0; e < CPL; ++e) oacc[e] = 0.f;
+  // PV4 (int8 V, D = 128, 4 query heads per KV head): the PV lanes are
+  // (key-pair parity hk = lane / 32, 4 channels 4 cq .. 4 cq + 3) and each
+  // covers all 4 heads, so a V byte is converted once instead of once per
+  // head: per key pair 4 v_perm (fp16 denormal pairs (v + 128) * 2^-24 of the
+  // two keys) and 16 v_dot2 against the heads' fp16 (p0, p1) pairs, which
+  // the logit lanes stage in LDS (one 16-byte broadcast read per key pair).
+  constexpr bool PV4 = SL8_DEC_PV4 && VI8 && DEC_PAIR && D == 128 && GS == 4;
+  __shared__ __attribute__((aligned(16))) uint32_t pv_l[PV4 ? DEC_WAVES : 1][36];  // [8 pairs][4 heads] p2, [4] resc
+  float o4[PV4 ? 4 : 1][4];  // [head][channel]
+#pragma unroll
+  for (int hh = 0; hh < (PV4 ? 4 : 1); ++hh)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o4[hh][e] = 0.f;
+  const int hk = lane >> 5, cq = lane & 31;
+  // v_perm selectors per channel byte e: [u(k0), 0, u(k1), 0] from (a = first
+  // word read, b = second); the odd half reads key k1 first (its row lies in
+  // the other 32-bank half: no bank conflict between the halves)
+  uint32_t vsel[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    vsel[e] = hk == 0 ? ((uint32_t)e | (12u << 8) | ((uint32_t)(4 + e) << 16) | (12u << 24))
+                      : ((uint32_t)(4 + e) | (12u << 8) | ((uint32_t)e << 16) | (12u << 24));
 
   auto compute_tile = [&](int i, int8_t* sb) {
     const int base = n0 + (wave + DEC_WAVES * i) * T;
@@ -617,6 +642,42 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
         pvs += p[u];
       }
       lv_lane = lv_lane * resc + pvs;
+    }
+    if constexpr (PV4) {
+      static_assert(SUB == 1 && KL == 16 && T == 16, "PV4 tile");
+      typedef _Float16 v2h_t __attribute__((ext_vector_type(2)));
+      // this lane's p (fp16, as it enters PV) into the wave's LDS slot: pair
+      // kl / 2, head h, key kl & 1; the head's rescale factor after the pairs
+      const _Float16 ph = (_Float16)p[0];
+      pq_sum = pq_sum * resc + (float)ph;
+      uint16_t* pt = reinterpret_cast<uint16_t*>(&pv_l[wave][0]);
+      pt[(kl >> 1) * 8 + 2 * h + (kl & 1)] = __builtin_bit_cast(uint16_t, ph);
+      if (kl == 0) reinterpret_cast<float*>(&pv_l[wave][32])[h] = resc;
+      // (this wave's own LDS writes: read back in order)
+      const float4 rs = *reinterpret_cast<const float4*>(&pv_l[wave][32]);
+      const float rsh[4] = {rs.x, rs.y, rs.z, rs.w};
+#pragma unroll
+      for (int hh = 0; hh < 4; ++hh)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o4[hh][e] *= rsh[hh];
+      const uint8_t* vbt = reinterpret_cast<const uint8_t*>(vt);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int pp = 2 * j + hk;  // key pair 2 pp, 2 pp + 1
+        const uint4 pv = *reinterpret_cast<const uint4*>(&pv_l[wave][4 * pp]);
+        const uint32_t pw[4] = {pv.x, pv.y, pv.z, pv.w};
+        const uint32_t wa = *reinterpret_cast<const uint32_t*>(vbt + (2 * pp + hk) * D + 4 * cq) ^ 0x80808080u;
+        const uint32_t wb = *reinterpret_cast<const uint32_t*>(vbt + (2 * pp + 1 - hk) * D + 4 * cq) ^ 0x80808080u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t pr = __builtin_amdgcn_perm(wb, wa, vsel[e]);
+#pragma unroll
+          for (int hh = 0; hh < 4; ++hh)
+            o4[hh][e] = __builtin_amdgcn_fdot2(__builtin_bit_cast(v2h_t, pw[hh]), __builtin_bit_cast(v2h_t, pr),
+                                               o4[hh][e], false);
+        }
+      }
+      return;
     }
 #pragma unroll
     for (int e = 0; e < CPL; ++e) oacc[e] *= resc;
@@ -761,7 +822,24 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
   // ---- per-wave state -> LDS (this wave's own stage-0 area), then LSE merge ----
 #pragma unroll
   for (int o = 1; o < KL; o <<= 1) l_lane += __shfl_xor(l_lane, o, 64);
-  if constexpr (VI8 && DEC_PAIR) {
+  if constexpr (PV4) {
+    // the two key-parity halves, then per head: codes entered PV as
+    // (v + 128) * 2^-24 against the fp16 p (pq_sum: their sum per head)
+#pragma unroll
+    for (int o = 1; o < KL; o <<= 1) pq_sum += __shfl_xor(pq_sum, o, 64);
+    float pqh[4];
+#pragma unroll
+    for (int hh = 0; hh < 4; ++hh) pqh[hh] = __shfl(pq_sum, hh * KL, 64);
+#pragma unroll
+    for (int hh = 0; hh < 4; ++hh)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float v = o4[hh][e] + __shfl_xor(o4[hh][e], 32, 64);
+        v = v * 16777216.f - 128.f * pqh[hh];
+        if constexpr (!PG) v *= vsc[(int64_t)bkv * D + 4 * cq + e];
+        o4[hh][e] = v;
+      }
+  } else if constexpr (VI8 && DEC_PAIR) {
     // codes entered PV as (v + 128) * 2^-24 against the fp16 p: rescale and
     // remove the 128 offset weighted by exactly those p
 #pragma unroll
@@ -787,10 +865,18 @@ decode_wave_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sca
   float* rm = red + DEC_WAVES * GS * D + wave * GS;
   float* rl = red + DEC_WAVES * GS * D + DEC_WAVES * GS + wave * GS;
   __syncthreads();  // every wave is past its last read of stage 0
+  if constexpr (PV4) {
+    if (hk == 0) {
 #pragma unroll
-  for (int e = 0; e < CPL; e += 4)
-    *reinterpret_cast<float4*>(ro + h * D + kl * CPL + e) =
-        make_float4(oacc[e], oacc[e + 1], oacc[e + 2], oacc[e + 3]);
+      for (int hh = 0; hh < 4; ++hh)
+        *reinterpret_cast<float4*>(ro + hh * D + 4 * cq) = make_float4(o4[hh][0], o4[hh][1], o4[hh][2], o4[hh][3]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < CPL; e += 4)
+      *reinterpret_cast<float4*>(ro + h * D + kl * CPL + e) =
+          make_float4(oacc[e], oacc[e + 1], oacc[e + 2], oacc[e + 3]);
+  }
   if (kl == 0) {
     rm[h] = m_run;
     rl[h] = l_lane;
