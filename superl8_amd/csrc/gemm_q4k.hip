@@ -59,6 +59,9 @@ constexpr int XS_MPAD = 16;  // xsum LDS row pitch (activation rows)
 // (half, nibble) pair is one MFMA for <x, q> (scaled by sc_j in the integer
 // domain with v_mad_i32_i24) plus one MFMA whose B operand holds m_j in
 // every slot, accumulating m_j * sum(x_j) per super-block.
+#ifndef SL8_GEMV_XBLDS
+#define SL8_GEMV_XBLDS 1
+#endif
 constexpr int GCH = 5;     // super-blocks per wave and chunk
 constexpr int GWAVES = 4;  // K split
 constexpr int GXPITCH = GCH * 256;  // LDS bytes per activation row and wave
@@ -84,9 +87,9 @@ __device__ __forceinline__ uint32_t lane_pull(uint32_t v, int src_lane) {
 // at M = 8 measured 19.9 us against 17.3 us -- every wave then loads and
 // computes in the same phase, so no compute overlaps the memory stream. XB: the
 // activations carry one scale per 256-element block (x_scale [M, K/256],
-// applied per super-block) instead of one per row; its 4 GCH scale registers
-// do not fit the 96-VGPR budget of 5 waves per SIMD (they spilled to
-// scratch), so XB asks for 4.
+// applied per super-block) instead of one per row; at M <= 8 those scales are
+// copied into LDS with the activations (XBL) and the kernel keeps 5 waves per
+// SIMD, at M > 8 they are held in registers.
 // OPL: the weights are loaded straight into the MFMA operand layout (lane
 // (row lj, group h) reads its own 16-byte pieces and the row's whole header)
 // instead of the coalesced layout plus ds_bpermute moves. Same bytes, more
@@ -95,7 +98,7 @@ __device__ __forceinline__ uint32_t lane_pull(uint32_t v, int src_lane) {
 // M = 8 17.6 -> 18.1 us (its header registers spill at 5 waves per SIMD), so
 // the launcher uses it for M <= 4 and M > 8.
 template <int OUT_DT, int MT, int FMT = 4, int TPW = 1, bool XB = false, bool OPL = false>
-__global__ void __launch_bounds__(64 * GWAVES, TPW == 2 ? 3 : (MT == 1 ? (FMT == 4 && !XB ? 5 : 4) : 1))
+__global__ void __launch_bounds__(64 * GWAVES, TPW == 2 ? 3 : (MT == 1 ? (FMT == 4 && (!XB || SL8_GEMV_XBLDS) ? 5 : 4) : 1))
 gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
                 const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K) {
   extern __shared__ __attribute__((aligned(16))) int8_t xl[];  // per wave: [M][GXPITCH]
@@ -127,8 +130,14 @@ gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
   // that the lanes whose A-operand row is unused read instead (no select
   // per operand)
   const int xarea = (M * GXPITCH + 1023) & ~1023;
-  int8_t* xw = xl + (int64_t)wave * (xarea + GXPITCH);
+  // XBL (XB, M <= 8): after the zero row, the chunk's per-block x scales [i][m],
+  // read per super-block instead of held in 20 registers (which cost the
+  // 5-wave occupancy): config 4 M = 8 18.1 -> 17.6 us (M = 16: 32.8 -> 33.7,
+  // so not there)
+  constexpr bool XBL = XB && SL8_GEMV_XBLDS && MT == 1;
+  int8_t* xw = xl + (int64_t)wave * (xarea + GXPITCH + (XBL ? 256 : 0));
   int8_t* xz = xw + xarea;
+  float* xsl = reinterpret_cast<float*>(xz + GXPITCH);
   for (int i = lane; i < GXPITCH / 16; i += 64) reinterpret_cast<uint4*>(xz)[i] = make_uint4(0, 0, 0, 0);
 
   float f[TPW][MT][4];
@@ -150,6 +159,13 @@ gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
         const int m = id / (GXPITCH / 16), pos = min(id % (GXPITCH / 16), cnt * 16 - 1);
         __builtin_amdgcn_global_load_lds((q4_gptr_t)(x + (int64_t)m * K + (int64_t)c0 * 256 + 16 * pos),
                                          (q4_lptr_t)(xw + j * 1024), 16, 0, 0);
+      }
+      if constexpr (XBL) {
+        // slot s = 8 i + m holds x_scale[m][c0 + i] (clamped: unused slots repeat)
+        const int i = lane / 8, m = lane % 8;
+        __builtin_amdgcn_global_load_lds(
+            (q4_gptr_t)(x_scale + (int64_t)min(m, M - 1) * nsb + min(c0 + min(i, GCH - 1), nsb - 1)),
+            (q4_lptr_t)xsl, 4, 0, 0);
       }
     };
     // ---- weights: header dword lc and two 16-byte nibble pieces per super-block ----
@@ -178,8 +194,8 @@ gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
       }
     stage_x();
     // per-block activation scales of this lane's C rows (XB)
-    float xsb[MT][4][GCH];
-    if constexpr (XB) {
+    float xsb[MT][4][XBL ? 1 : GCH];
+    if constexpr (XB && !XBL) {
 #pragma unroll
       for (int t = 0; t < MT; ++t)
 #pragma unroll
@@ -270,7 +286,8 @@ gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const float part = d * (float)T[t][r] - dmin * (float)U[t][r];
-            if constexpr (XB) f[tt][t][r] += xsb[t][r][i] * part;
+            if constexpr (XBL) f[tt][t][r] += xsl[8 * i + 4 * (h & 1) + r] * part;
+            else if constexpr (XB) f[tt][t][r] += xsb[t][r][i] * part;
             else f[tt][t][r] += part;
           }
       }
@@ -724,7 +741,8 @@ template <int MT, bool XB = false>
 void launch_gemv_mt(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
                     int M, int N, int K, hipStream_t st) {
   const dim3 grid((unsigned)((N + GEMV_ROWS - 1) / GEMV_ROWS));
-  const size_t lds = (size_t)GWAVES * ((((size_t)M * GXPITCH + 1023) & ~(size_t)1023) + GXPITCH);
+  const size_t lds = (size_t)GWAVES * ((((size_t)M * GXPITCH + 1023) & ~(size_t)1023) + GXPITCH +
+                                       (XB && SL8_GEMV_XBLDS && MT == 1 ? 256 : 0));
 #define SL8_GM(DT, OP) gemv_q4k_kernel<DT, MT, 4, 1, XB, OP><<<grid, 64 * GWAVES, lds, st>>>(x, xs, w, out, M, N, K)
 #define SL8_GM_DT(OP)                                   \
   switch (odt) {                                        \
