@@ -324,7 +324,11 @@ gemm_q6k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
             const uint32_t c0 = ((ql.x >> ns) & 0x0F0F0F0Fu) | (((qhc.x >> hs) & 0x03030303u) << 4);
             const uint32_t c1 = ((ql.y >> ns) & 0x0F0F0F0Fu) | (((qhc.y >> hs) & 0x03030303u) << 4);
             H4x2 v = bytes8_to_h1024(c0, c1);  // 1024 + q
-            const uint32_t sw = g ? scw[cb][2 + (qd >> 1)] : scw[cb][qd >> 1];  // scales 4(i>>2)..
+            // scales 4(i>>2).. (both words read first, then a value select on
+            // the loop's g: a select of the two array elements themselves
+            // kept scw in scratch memory)
+            const uint32_t sw_lo = scw[cb][qd >> 1], sw_hi = scw[cb][2 + (qd >> 1)];
+            const uint32_t sw = g ? sw_hi : sw_lo;
             const int sc = (int)(int8_t)((sw >> (8 * (2 * (qd & 1) + ih))) & 0xFF);
             const _Float16 slo = (_Float16)(float)(sc & 15), shi = (_Float16)(float)(sc >> 4);
             const v2h_t slo2 = {slo, slo}, shi2 = {shi, shi};
