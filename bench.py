@@ -190,6 +190,35 @@ def bench_paged_decode(iters=20, bs=16):
     return ms, nbytes
 
 
+def bench_paged_decode_k8v3(iters=20, bs=16):
+    """K8V3 paged decode at config 3's shape: int8 K with per-token scales and
+    3-bit Lloyd-Max V (packed codes + per-128-channel norms + codebook), 16-key
+    blocks scattered by a shuffled block table (reference attn_paged_decode_k8v3)."""
+    from superl8_amd import _C
+    from superl8_amd.quant.lloydmax import gaussian_codebook
+
+    dev = "cuda"
+    B, Hq, Hkv, N, D = 16, 32, 8, 32768, 128
+    g = torch.Generator(device=dev).manual_seed(10)
+    nblk = B * N // bs
+    kc = torch.randint(-127, 128, (nblk, Hkv, bs, D), device=dev, dtype=torch.int8, generator=g)
+    ks = torch.rand(nblk, Hkv, bs, device=dev, generator=g) * 0.02 + 1e-3
+    vp = torch.randint(-2 ** 31, 2 ** 31 - 1, (nblk, Hkv, bs, 3 * D // 32), device=dev,
+                       dtype=torch.int32, generator=g)
+    vn = torch.rand(nblk, Hkv, bs, D // 128, device=dev, generator=g) * 20 + 1
+    cb = gaussian_codebook(3, 128).to(dev)
+    bt = torch.randperm(nblk, device=dev, generator=g).to(torch.int32).reshape(B, N // bs)
+    ctx = torch.full((B,), N, device=dev, dtype=torch.int32)
+    q = torch.randint(-127, 128, (B, Hq, 1, D), device=dev, dtype=torch.int8, generator=g)
+    qs = torch.rand(B, Hq, 1, device=dev, generator=g) * 0.01 + 1e-3
+    fn = lambda: _C.attn_paged_decode_k8v3(q, qs, kc, ks, vp, vn, cb, bt, ctx, bs, N, 16)  # noqa: E731
+    spin_up(fn, 0.2)
+    ms = _events_time(fn, iters, torch.cuda.current_stream())
+    nbytes = kc.numel() + ks.numel() * 4 + vp.numel() * 4 + vn.numel() * 4 + bt.numel() * 4 \
+        + q.numel() + qs.numel() * 4 + B * Hq * D * 2
+    return ms, nbytes
+
+
 def bench_gemm_prefill(M=512, iters=10, fmt="q4k"):
     """k-quant prefill GEMM (M > 16: the tiled MFMA kernel) on config 4's shape."""
     from superl8_amd import _C
@@ -441,6 +470,12 @@ def main():
         sec["attn_paged_decode_cfg3shape_bs16"] = {"us": round(pms * 1e3, 2), "GB/s": round(gbs, 1),
                                                    "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
                                                    "bytes": pbytes}
+        pms, pbytes = bench_paged_decode_k8v3()
+        gbs = pbytes / (pms * 1e-3) / 1e9
+        sec["attn_paged_decode_k8v3_cfg3shape_bs16"] = {"us": round(pms * 1e3, 2),
+                                                        "GB/s": round(gbs, 1),
+                                                        "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+                                                        "bytes": pbytes}
         for M in (1, 8):
             gms, gbytes = bench_gemv(M)
             gbs = gbytes / (gms * 1e-3) / 1e9

@@ -271,6 +271,24 @@ int sl8_attn_paged_decode(const int8_t* q, const float* q_scale, const int8_t* k
                           int64_t block_size, int64_t max_blocks_per_seq,
                           int64_t max_context_len, int64_t num_splits, void* workspace,
                           size_t workspace_bytes, void* stream);
+/* K8V3 paged decode: replaces _C.attn_paged_decode_k8v3 (reference
+ * csrc/fni8_api.cpp:144-151,516-519, csrc/kernel/attn_paged_decode.cu:67-89,229-330,
+ * csrc/include/attn_paged_decode.cuh:134-257 with LowbitV). K, scales, block
+ * table, context lengths, splits and workspace as sl8_attn_paged_decode; V is
+ * the 3-bit Lloyd-Max store: v_packed int32 [num_blocks, Hkv, block_size, 3D/32]
+ * (code of channel d at bits 3d..3d+2 of the row's LSB-first stream), v_norm
+ * fp32 [num_blocks, Hkv, block_size, D/128] (per-128-channel L2 norms),
+ * v_codebook fp32 [8]; value = fp16_rn(codebook[code] * norm). D 128 or 256;
+ * k_cache and v_packed 16-byte aligned. */
+int sl8_attn_paged_decode_k8v3(const int8_t* q, const float* q_scale, const int8_t* k_cache,
+                               const float* k_scale, const int32_t* v_packed,
+                               const float* v_norm, const float* v_codebook,
+                               const int32_t* block_table, const int32_t* context_lens,
+                               void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                               int64_t num_blocks, int64_t block_size,
+                               int64_t max_blocks_per_seq, int64_t max_context_len,
+                               int64_t num_splits, void* workspace, size_t workspace_bytes,
+                               void* stream);
 int sl8_kv_write_paged(const void* k_new, const void* v_new, const int32_t* slot_mapping,
                        int8_t* k_cache, float* k_scale, int8_t* v_cache, float* v_scale,
                        int64_t B, int64_t Hkv, int64_t D, int64_t num_blocks,

@@ -8,4 +8,4 @@ Every function cites the reference file:line it restates. How each function is
 pinned (known answers, closed forms, brute force, invariants) is listed in
 tests/test_oracle.py; no function here is left unpinned.
 """
-from . import attention, kquant, q4k, quant  # noqa: F401
+from . import attention, kquant, lloydmax, q4k, quant  # noqa: F401

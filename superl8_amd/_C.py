@@ -458,6 +458,64 @@ def attn_paged_decode(q, q_scale, k_cache, k_scale, v_cache, v_scale, block_tabl
     return out
 
 
+def attn_paged_decode_k8v3(q, q_scale, k_cache, k_scale, v_packed, v_norm, v_codebook,
+                           block_table, context_lens, block_size, max_context_len,
+                           num_splits=-1):
+    """Paged decode over a K8V3 store (reference csrc/kernel/attn_paged_decode.cu:229-330):
+    K as attn_paged_decode; V as 3-bit Lloyd-Max codes v_packed int32
+    [num_blocks,Hkv,bs,3D/32], per-128-channel norms v_norm fp32 [num_blocks,Hkv,bs,D/128]
+    and a codebook fp32 [8]; D 128 or 256 -> fp16 [B,Hq,1,D]."""
+    tag = "paged_decode_k8v3"
+    _on_gpu(q, q_scale, k_cache, k_scale, v_packed, v_norm, v_codebook, block_table,
+            context_lens)
+    _check(q.dtype == torch.int8 and k_cache.dtype == torch.int8, f"{tag}: q/k_cache must be int8")
+    _check(v_packed.dtype == torch.int32, f"{tag}: v_packed must be int32")
+    _check(q_scale.dtype == torch.float32 and k_scale.dtype == torch.float32 and
+           v_norm.dtype == torch.float32 and v_codebook.dtype == torch.float32,
+           f"{tag}: scales/norms/codebook must be float32")
+    _check(block_table.dtype == torch.int32 and context_lens.dtype == torch.int32,
+           f"{tag}: block_table/context_lens must be int32")
+    _check(q.dim() == 4 and q.shape[2] == 1, f"{tag}: q must be [B,H_q,1,D]")
+    _check(k_cache.dim() == 4 and v_packed.dim() == 4 and v_norm.dim() == 4,
+           f"{tag}: caches must be [num_blocks,H_kv,block_size,...]")
+    _contig(q, q_scale, k_cache, k_scale, v_packed, v_norm, v_codebook, block_table, context_lens)
+    B, H, _, D = q.shape
+    nblk, Hkv, bs = k_cache.shape[0], k_cache.shape[1], k_cache.shape[2]
+    _check(bs == block_size, f"{tag}: block_size mismatch vs k_cache.size(2)")
+    _check(k_cache.shape[3] == D and tuple(v_packed.shape[:3]) == (nblk, Hkv, bs) and
+           tuple(v_norm.shape[:3]) == (nblk, Hkv, bs),
+           f"{tag}: k_cache/v_packed/v_norm shape mismatch")
+    _check(Hkv > 0 and H % Hkv == 0, f"{tag}: H_q must be divisible by H_kv (GQA)")
+    _check(D in (128, 256), f"{tag}: lloydmax3 requires head dim 128 or 256, got {D}")
+    _check(k_cache.numel() == k_scale.numel() * D, f"{tag}: k_scale shape mismatch vs k_cache")
+    _check(v_packed.shape[3] == D * 3 // 32,
+           f"{tag}: v_packed last dim must be D*3/32, got {v_packed.shape[3]}")
+    _check(v_norm.shape[3] == D // 128, f"{tag}: v_norm last dim must be D/128, got {v_norm.shape[3]}")
+    _check(v_codebook.dim() == 1 and v_codebook.numel() == 8, f"{tag}: v_codebook must be [8] fp32")
+    _check(q_scale.numel() == B * H, f"{tag}: q_scale shape mismatch")
+    _check(block_table.dim() == 2 and block_table.shape[0] == B,
+           f"{tag}: block_table must be [B, max_blocks_per_seq]")
+    _check(context_lens.dim() == 1 and context_lens.shape[0] == B, f"{tag}: context_lens must be [B]")
+    maxb = block_table.shape[1]
+    _check(0 <= max_context_len <= maxb * bs, f"{tag}: max_context_len exceeds block_table capacity")
+    num_splits = int(num_splits)
+    _check(num_splits != 0,
+           f"{tag}: num_splits=0 is invalid; use -1 for auto or 1..{DEC_MAX_SPLITS}")
+    out = torch.empty((B, H, 1, D), device=q.device, dtype=torch.float16)
+    if B == 0 or H == 0:
+        return out
+    ns = paged_choose_n_splits(max_context_len, B * H) if num_splits < 0 else num_splits
+    _check(1 <= ns <= DEC_MAX_SPLITS, f"{tag}: num_splits must be 1..{DEC_MAX_SPLITS}, got {ns}")
+    ws_bytes = _lib.load().sl8_attn_int8_decode_workspace(B, H, D, ns)
+    ws = torch.empty((ws_bytes,), device=q.device, dtype=torch.uint8)
+    with torch.cuda.device(q.device):
+        call("sl8_attn_paged_decode_k8v3", q.data_ptr(), q_scale.data_ptr(), k_cache.data_ptr(),
+             k_scale.data_ptr(), v_packed.data_ptr(), v_norm.data_ptr(), v_codebook.data_ptr(),
+             block_table.data_ptr(), context_lens.data_ptr(), out.data_ptr(), B, H, Hkv, D, nblk,
+             bs, maxb, int(max_context_len), ns, ws.data_ptr(), ws_bytes, stream_of(q))
+    return out
+
+
 def kv_write_paged(k_new, v_new, slot_mapping, k_cache, k_scale, v_cache, v_scale):
     """Quantize-on-write of one new token per (batch, KV head) into the paged int8
     cache, in place (reference csrc/kernel/attn_paged_decode.cu:360-421)."""

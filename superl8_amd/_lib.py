@@ -57,6 +57,8 @@ SIGNATURES = {
     "sl8_q_outlier_gate": (_I, [_P, _I, _I64, _I64, ctypes.c_float, _P, _P, _P]),
     "sl8_attn_paged_decode": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
                                    _I64, _I64, _I64, _I64, _I64, _P, _SZ, _P]),
+    "sl8_attn_paged_decode_k8v3": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64,
+                                        _I64, _I64, _I64, _I64, _I64, _I64, _P, _SZ, _P]),
     "sl8_kv_write_paged": (_I, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P]),
     "sl8_gemm_decode_q4k": (_I, [_P, _P, _P, _P, _I, _I64, _I64, _I64, _P]),
     "sl8_gemm_decode_q4k_xblock": (_I, [_P, _P, _P, _P, _I, _I64, _I64, _I64, _P]),

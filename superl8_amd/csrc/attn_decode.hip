@@ -1212,6 +1212,268 @@ kv_write_paged_kernel(const uint16_t* __restrict__ k_new, const uint16_t* __rest
   }
 }
 
+// ---------------------------------------------------------------------------
+// K8V3 paged decode (reference attn_paged_decode.cuh:114-257 with LowbitV,
+// attn_paged_decode.cu:229-330). K and the split / softmax / merge contract are
+// those of the paged int8 decode; V is a 3-bit Lloyd-Max store per token:
+// v_packed [rows, 3D/32] u32 holds the code of channel d at bits 3d..3d+2 of
+// the row's LSB-first bit stream, v_norm [rows, D/128] fp32 one L2 norm per
+// 128-channel block, codebook [8] fp32; channel d of token row r is
+//   v = fp16_rn(codebook[code] * v_norm[r][d / 128]),
+// accumulated as p * v in fp32.
+//
+// QK phase (lane = key): besides the K row, each lane loads its key's packed
+// codes (16-byte loads) into LDS and builds the key's value table per
+// 128-channel block, the eight fp16 values above, stored as a low-byte plane
+// (2 dwords) and a high-byte plane (2 dwords). PV phase (lane = 8 consecutive
+// channels x key phase): the lane's 24 code bits become byte selectors 0..7
+// and v_perm_b32 picks four table bytes per instruction, so the lookup needs
+// no indexed register access and no per-element LDS read.
+template <int D, int G>
+struct K3Smem {
+  int q[G][D / 4];
+  float qs[G];
+  union {
+    struct {
+      uint32_t codes[DEC_WAVES][DEC_TILE][3 * D / 32];
+      uint4 tbl[DEC_WAVES][DEC_TILE][D / 128];  // {lo 0-3, lo 4-7, hi 0-3, hi 4-7}
+      float p[DEC_WAVES][DEC_TILE][G];
+    } t;
+    struct {
+      float m[DEC_WAVES][G];
+      float l[DEC_WAVES][G];
+      float o[DEC_WAVES][G][D];
+    } r;
+  };
+};
+
+// four 3-bit fields (bits 0..11) -> the low 3 bits of four bytes
+__device__ __forceinline__ uint32_t spread3x4(uint32_t a) {
+  const uint32_t t = (a & 0x3fu) | ((a & 0xfc0u) << 10);
+  return (t & 0x00070007u) | ((t & 0x00380038u) << 5);
+}
+
+template <int D, int G>
+__global__ void __launch_bounds__(DEC_THREADS)
+k8v3_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_scale,
+                  const int8_t* __restrict__ k, const float* __restrict__ k_scale,
+                  const uint32_t* __restrict__ vpk, const float* __restrict__ vnorm,
+                  const float* __restrict__ codebook, float* __restrict__ o_part,
+                  float* __restrict__ m_part, float* __restrict__ l_part, int n_len,
+                  int n_splits, int h_q, int h_kv, int gsz, int bhq, const PagedArgs pg) {
+  constexpr int D4 = D / 4;
+  constexpr int DG = D / 8;            // 8-channel groups
+  constexpr int KPH = 64 / DG;         // key phases in the PV lane map
+  constexpr int KPL = DEC_TILE / KPH;  // keys per lane per tile in PV
+  constexpr int VW = 3 * D / 32;       // code dwords per row
+  constexpr int VB = D / 128;          // norms per row
+  __shared__ K3Smem<D, G> sm;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int split = blockIdx.x;
+  const int bkv = blockIdx.y;
+  const int b = bkv / h_kv, kvh = bkv % h_kv;
+  const int j0 = blockIdx.z * G;
+  const int ng = min(G, gsz - j0);
+
+  for (int i = tid; i < G * D4; i += DEC_THREADS) {
+    const int g = i / D4, c = i % D4;
+    int val = 0;
+    if (g < ng) {
+      const int64_t hq = (int64_t)b * h_q + kvh * gsz + j0 + g;
+      val = reinterpret_cast<const int*>(q + hq * D)[c];
+    }
+    sm.q[g][c] = val;
+  }
+  if (tid < G) {
+    const int64_t hq = (int64_t)b * h_q + kvh * gsz + j0 + tid;
+    sm.qs[tid] = tid < ng ? q_scale[hq] : 0.f;
+  }
+  float cb[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) cb[i] = codebook[i];
+  __syncthreads();
+
+  const int per = (n_len + n_splits - 1) / n_splits;
+  const int n0 = split * per;
+  // a context length above max_context_len (n_len) is read as max_context_len
+  const int n1 = min(min(pg.ctx[b], n_len), n0 + per);
+  const int32_t* btb = pg.bt + (int64_t)b * pg.maxb;
+
+  float m_run[G], l_lane[G], oacc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m_run[g] = -INFINITY;
+    l_lane[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) oacc[g][e] = 0.f;
+  }
+  const int dg = lane % DG, kph = lane / DG;
+  // PV lane: code bits 24*dg .. 24*dg+23 of the row = dwords cw, cw1 from bit csh
+  const int cw = (3 * dg) >> 2, csh = (24 * dg) & 31;
+  const int cw1 = min(cw + 1, VW - 1);  // (csh <= 8 reads no bit of it)
+  const int vblk = dg / (128 / 8);
+
+  for (int t0 = n0 + wave * DEC_TILE; t0 < n1; t0 += DEC_WAVES * DEC_TILE) {
+    // ---- lane = key: logits, codes to LDS, value tables ----
+    const int n = t0 + lane;
+    const bool valid = n < n1;
+    float s[G];
+    {
+      const int nn = valid ? n : n0;
+      const int64_t row = ((int64_t)btb[nn / pg.bs] * h_kv + kvh) * pg.bs + nn % pg.bs;
+      int4 kr[D / 16];
+      const int4* kp = reinterpret_cast<const int4*>(k + row * D);
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) kr[c] = kp[c];
+      uint4 cr[VW / 4];
+      const uint4* cp = reinterpret_cast<const uint4*>(vpk + row * VW);
+#pragma unroll
+      for (int c = 0; c < VW / 4; ++c) cr[c] = cp[c];
+      float nrm[VB];
+#pragma unroll
+      for (int j = 0; j < VB; ++j) nrm[j] = vnorm[row * VB + j];
+      const float ks = valid ? k_scale[row] : 0.f;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        int acc = 0;
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) {
+          const int4 qv = *reinterpret_cast<const int4*>(&sm.q[g][4 * c]);
+          acc = __builtin_amdgcn_sdot4(qv.x, kr[c].x, acc, false);
+          acc = __builtin_amdgcn_sdot4(qv.y, kr[c].y, acc, false);
+          acc = __builtin_amdgcn_sdot4(qv.z, kr[c].z, acc, false);
+          acc = __builtin_amdgcn_sdot4(qv.w, kr[c].w, acc, false);
+        }
+        s[g] = valid ? ((float)acc * sm.qs[g]) * ks : -INFINITY;
+      }
+#pragma unroll
+      for (int c = 0; c < VW / 4; ++c)
+        *reinterpret_cast<uint4*>(&sm.t.codes[wave][lane][4 * c]) = cr[c];
+#pragma unroll
+      for (int j = 0; j < VB; ++j) {
+        // fp16 values of entries 2e, 2e+1: the product rounded to fp32 first,
+        // then to fp16. The empty asm keeps the fp32 product in a register:
+        // otherwise the multiply and the conversion fuse into one
+        // v_fma_mixlo_f16, which rounds the exact product once (a different
+        // fp16 value when the fp32 product lands on an fp16 midpoint).
+        float pr[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          pr[e] = cb[e] * nrm[j];
+          asm volatile("" : "+v"(pr[e]));
+        }
+        uint32_t h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          h[e] = (uint32_t)f2h_bits(pr[2 * e]) | ((uint32_t)f2h_bits(pr[2 * e + 1]) << 16);
+        uint4 tb;
+        tb.x = __builtin_amdgcn_perm(h[1], h[0], 0x06040200u);  // low bytes of 0..3
+        tb.y = __builtin_amdgcn_perm(h[3], h[2], 0x06040200u);  // low bytes of 4..7
+        tb.z = __builtin_amdgcn_perm(h[1], h[0], 0x07050301u);  // high bytes of 0..3
+        tb.w = __builtin_amdgcn_perm(h[3], h[2], 0x07050301u);  // high bytes of 4..7
+        sm.t.tbl[wave][lane][j] = tb;
+      }
+    }
+    // ---- online softmax (wave-uniform running max per head) ----
+    float resc[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float mt = wave_max(s[g]);
+      const float mn = fmaxf(m_run[g], mt);
+      resc[g] = exp2f(m_run[g] - mn);
+      m_run[g] = mn;
+      const float p = exp2f(s[g] - mn);
+      l_lane[g] = l_lane[g] * resc[g] + p;
+      sm.t.p[wave][lane][g] = p;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- PV: lane = (channel group dg, key phase kph) ----
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) oacc[g][e] *= resc[g];
+#pragma unroll 4
+    for (int i = 0; i < KPL; ++i) {
+      const int kk = kph + i * KPH;
+      if (t0 + kk < n1) {
+        const uint32_t x = __builtin_amdgcn_alignbit(sm.t.codes[wave][kk][cw1],
+                                                     sm.t.codes[wave][kk][cw], csh);
+        const uint4 tb = sm.t.tbl[wave][kk][vblk];
+        float vf[8];
+#pragma unroll
+        for (int hlf = 0; hlf < 2; ++hlf) {
+          const uint32_t sel = spread3x4((x >> (12 * hlf)) & 0xfffu);
+          const uint32_t lo = __builtin_amdgcn_perm(tb.y, tb.x, sel);
+          const uint32_t hi = __builtin_amdgcn_perm(tb.w, tb.z, sel);
+          const uint32_t p01 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
+          const uint32_t p23 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
+          vf[4 * hlf + 0] = h2f((uint16_t)(p01 & 0xffffu));
+          vf[4 * hlf + 1] = h2f((uint16_t)(p01 >> 16));
+          vf[4 * hlf + 2] = h2f((uint16_t)(p23 & 0xffffu));
+          vf[4 * hlf + 3] = h2f((uint16_t)(p23 >> 16));
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float p = sm.t.p[wave][kk][g];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) oacc[g][e] = fmaf(p, vf[e], oacc[g][e]);
+        }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();  // the wave's tile region is rewritten next tile
+  }
+  __syncthreads();  // every wave is done with the tile region (aliased below)
+
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float lw = wave_sum(l_lane[g]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float x = oacc[g][e];
+#pragma unroll
+      for (int o = DG; o < 64; o <<= 1) x += __shfl_xor(x, o, 64);
+      oacc[g][e] = x;
+    }
+    if (lane == 0) {
+      sm.r.m[wave][g] = m_run[g];
+      sm.r.l[wave][g] = lw;
+    }
+    if (kph == 0) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sm.r.o[wave][g][dg * 8 + e] = oacc[g][e];
+    }
+  }
+  __syncthreads();
+
+  for (int i = tid; i < G * D; i += DEC_THREADS) {
+    const int g = i / D, d = i % D;
+    if (g >= ng) continue;
+    float mm = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < DEC_WAVES; ++w) mm = fmaxf(mm, sm.r.m[w][g]);
+    float acc = 0.f, den = 0.f;
+    if (mm != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < DEC_WAVES; ++w) {
+        const float wt = exp2f(sm.r.m[w][g] - mm);
+        acc += sm.r.o[w][g][d] * wt;
+        den += sm.r.l[w][g] * wt;
+      }
+    }
+    const int64_t hq = (int64_t)b * h_q + kvh * gsz + j0 + g;
+    const int64_t orow = (int64_t)split * bhq + hq;
+    o_part[orow * D + d] = acc;
+    if (d == 0) {
+      m_part[orow] = (mm == -INFINITY) ? DEC_NEG_INF : mm;
+      l_part[orow] = den;
+    }
+  }
+}
+
 }  // namespace
 }  // namespace sl8
 
@@ -1327,6 +1589,72 @@ extern "C" int sl8_attn_paged_decode(const int8_t* q, const float* q_scale, cons
   SL8_CHECK_LAUNCH("attn_paged_decode split");
   launch_combine((int)D, ibhq, st, op, mp, lp, static_cast<uint16_t*>(out), ns, ibhq);
   SL8_CHECK_LAUNCH("attn_paged_decode combine");
+  return SL8_OK;
+}
+
+extern "C" int sl8_attn_paged_decode_k8v3(const int8_t* q, const float* q_scale,
+                                          const int8_t* k_cache, const float* k_scale,
+                                          const int32_t* v_packed, const float* v_norm,
+                                          const float* v_codebook, const int32_t* block_table,
+                                          const int32_t* context_lens, void* out, int64_t B,
+                                          int64_t Hq, int64_t Hkv, int64_t D, int64_t num_blocks,
+                                          int64_t block_size, int64_t max_blocks_per_seq,
+                                          int64_t max_context_len, int64_t num_splits,
+                                          void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  SL8_CHECK_ARG(B >= 0 && Hq >= 0 && Hkv > 0 && num_blocks >= 0 && block_size > 0 &&
+                    max_blocks_per_seq >= 0,
+                "fni8 paged_decode_k8v3: bad shape");
+  SL8_CHECK_ARG(Hq % Hkv == 0, "fni8 paged_decode_k8v3: H_q must be divisible by H_kv (GQA)");
+  SL8_CHECK_ARG(D == 128 || D == 256,
+                "fni8 paged_decode_k8v3: lloydmax3 requires head dim 128 or 256, got %lld",
+                (long long)D);
+  SL8_CHECK_ARG(max_context_len >= 0 && max_context_len <= max_blocks_per_seq * block_size,
+                "fni8 paged_decode_k8v3: max_context_len exceeds block_table capacity");
+  SL8_CHECK_ARG(B * Hq < (1LL << 31) && num_blocks * Hkv * block_size < (1LL << 40) &&
+                    max_context_len < (1LL << 31),
+                "fni8 paged_decode_k8v3: shape too large");
+  const int64_t bhq = B * Hq;
+  if (num_splits < 0) num_splits = sl8_paged_choose_num_splits(max_context_len, bhq);
+  SL8_CHECK_ARG(num_splits >= 1 && num_splits <= DEC_MAX_SPLITS,
+                "fni8 paged_decode_k8v3: num_splits must be 1..%d, got %lld", DEC_MAX_SPLITS,
+                (long long)num_splits);
+  if (B == 0 || Hq == 0) return SL8_OK;
+  SL8_CHECK_ARG(q && q_scale && block_table && context_lens && out && v_codebook &&
+                    (num_blocks == 0 || (k_cache && k_scale && v_packed && v_norm)),
+                "fni8 paged_decode_k8v3: null pointer");
+  SL8_CHECK_ARG(aligned(q, 4) && aligned(k_cache, 16) && aligned(v_packed, 16),
+                "fni8 paged_decode_k8v3: q must be 4-byte aligned, k_cache/v_packed 16-byte aligned");
+  const size_t need = sl8_attn_int8_decode_workspace(B, Hq, D, num_splits);
+  SL8_CHECK_ARG(workspace && workspace_bytes >= need && aligned(workspace, 16),
+                "fni8 paged_decode_k8v3: workspace needs %zu bytes", need);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int ns = (int)num_splits, ibhq = (int)bhq, gsz = (int)(Hq / Hkv);
+  const int G = group_width(gsz);
+  float* op = static_cast<float*>(workspace);
+  float* mp = op + (size_t)ns * ibhq * D;
+  float* lp = mp + (size_t)ns * ibhq;
+  const dim3 grid((unsigned)ns, (unsigned)(B * Hkv), (unsigned)((gsz + G - 1) / G));
+  const PagedArgs pg{block_table, context_lens, (int)max_blocks_per_seq, (int)block_size, 0, 0};
+  const uint32_t* vp = reinterpret_cast<const uint32_t*>(v_packed);
+#define SL8_K3(DD, GG)                                                                      \
+  k8v3_split_kernel<DD, GG><<<grid, DEC_THREADS, 0, st>>>(                                  \
+      q, q_scale, k_cache, k_scale, vp, v_norm, v_codebook, op, mp, lp, (int)max_context_len, \
+      ns, (int)Hq, (int)Hkv, gsz, ibhq, pg)
+#define SL8_K3D(DD)                     \
+  switch (G) {                          \
+    case 1: SL8_K3(DD, 1); break;       \
+    case 2: SL8_K3(DD, 2); break;       \
+    case 4: SL8_K3(DD, 4); break;       \
+    default: SL8_K3(DD, 8); break;      \
+  }
+  if (D == 128) SL8_K3D(128)
+  else SL8_K3D(256)
+#undef SL8_K3D
+#undef SL8_K3
+  SL8_CHECK_LAUNCH("attn_paged_decode_k8v3 split");
+  launch_combine((int)D, ibhq, st, op, mp, lp, static_cast<uint16_t*>(out), ns, ibhq);
+  SL8_CHECK_LAUNCH("attn_paged_decode_k8v3 combine");
   return SL8_OK;
 }
 

@@ -191,6 +191,117 @@ def attn_paged_decode_cached(q: torch.Tensor, k_cache: torch.Tensor, k_scale: to
                                 int(block_size), int(max_context_len), ns)
 
 
+def attn_paged_decode_k8v3(q: torch.Tensor, k_cache: torch.Tensor, k_scale: torch.Tensor,
+                           v_packed: torch.Tensor, v_norm: torch.Tensor, v_codebook: torch.Tensor,
+                           block_table: torch.Tensor, context_lens: torch.Tensor,
+                           block_size: int, *, max_context_len: int | None = None,
+                           scale: float | None = None, rotate: bool = True,
+                           num_splits: int | None = None) -> torch.Tensor:
+    """Decode (M=1) against a paged K8V3 store (reference ops.py:852-915): int8 K
+    (rotated when `rotate`, per-token fp32 scale) and 3-bit Lloyd-Max V (packed
+    codes int32 [num_blocks,Hkv,bs,3D/32], norms fp32 [num_blocks,Hkv,bs,D/128],
+    codebook fp32 [8]) read inside one paged split-KV launch; D 128 or 256.
+    Returns fp16 [B,Hq,1,D]."""
+    from .quant import LOG2E
+    from .quant.rotation import rotate_last
+
+    if q.shape[-2] != 1:
+        raise AssertionError(f"paged decode expects M=1, got M={q.shape[-2]}")
+    if max_context_len is None:
+        max_context_len = int(context_lens.max().item())
+    softmax_scale = (1.0 / (q.shape[-1] ** 0.5)) if scale is None else scale
+    if rotate:
+        q = rotate_last(q)
+    q_shape = q.shape
+    q_i8, q_scale = quantize_i8_rowwise(q.reshape(-1, q_shape[-1]).contiguous())
+    q_i8 = q_i8.reshape(q_shape)
+    q_scale = (q_scale.float() * (softmax_scale * LOG2E)).reshape(q_shape[0], q_shape[1], 1).contiguous()
+    ns = -1 if num_splits is None else int(num_splits)
+    return _C.attn_paged_decode_k8v3(q_i8.contiguous(), q_scale, k_cache.contiguous(),
+                                     k_scale.contiguous(), v_packed.contiguous(),
+                                     v_norm.contiguous(), v_codebook.contiguous(),
+                                     block_table.contiguous(), context_lens.contiguous(),
+                                     int(block_size), int(max_context_len), ns)
+
+
+def quantize_kv_write_paged_k8v3(k_new: torch.Tensor, v_new: torch.Tensor,
+                                 k_cache: torch.Tensor, k_scale: torch.Tensor,
+                                 v_packed: torch.Tensor, v_norm: torch.Tensor,
+                                 slot_mapping: torch.Tensor, *, rotate: bool = True,
+                                 codebook: torch.Tensor | None = None) -> torch.Tensor:
+    """Write one new token per (batch, KV head) into a paged K8V3 store, in place:
+    K rotated (when `rotate`) and quantised per row to int8; V quantised to 3-bit
+    Lloyd-Max codes over 128-channel blocks (`codebook`, default the fixed
+    Gaussian one) and packed. k_new, v_new fp16 [B,Hkv,D]; slot_mapping int32 [B]
+    (flat slot = block * block_size + offset). Returns the codebook used, the
+    `v_codebook` argument of attn_paged_decode_k8v3. (The reference store is
+    written the same way by its serving code, reference
+    tests/test_k8v3_paged_decode.py:32-83.)"""
+    from .quant.lloydmax import pack_indices_lowbit, quantize_lloydmax
+    from .quant.rotation import rotate_last
+
+    B, Hkv, D = k_new.shape
+    bs = k_cache.shape[2]
+    if rotate:
+        k_new = rotate_last(k_new)
+    k_i8, k_sc = quantize_i8_rowwise(k_new.reshape(-1, D).contiguous())
+    codes, norms, cb = quantize_lloydmax(v_new, bits=3, block_size=128, codebook=codebook)
+    packed = pack_indices_lowbit(codes, 3)
+    slots = slot_mapping.long()
+    rows = ((slots // bs)[:, None] * Hkv + torch.arange(Hkv, device=slots.device)) * bs + \
+        (slots % bs)[:, None]
+    rows = rows.reshape(-1)
+    k_cache.view(-1, D)[rows] = k_i8
+    k_scale.view(-1)[rows] = k_sc
+    v_packed.view(-1, v_packed.shape[-1])[rows] = packed.reshape(-1, packed.shape[-1])
+    v_norm.view(-1, v_norm.shape[-1])[rows] = norms.reshape(-1, norms.shape[-1])
+    return cb
+
+
+def quantize_kv_cache_3bit(k: torch.Tensor, v: torch.Tensor, *, rotate: bool = True,
+                           fit: bool = True, block_size: int = 128) -> dict:
+    """3-bit Lloyd-Max storage codec of a whole K/V cache (reference ops.py:590-655):
+    K smoothed (+ rotated), both packed with a codebook fitted to the
+    unit-normalised blocks (`fit`) or the fixed Gaussian one."""
+    from .quant import smooth_k
+    from .quant.lloydmax import (lloyd_max_fit, lloydmax_bits_levels, pack_indices_lowbit,
+                                 quantize_lloydmax)
+    from .quant.rotation import rotate_last
+
+    k_s, k_mean = smooth_k(k)
+    if rotate:
+        k_s = rotate_last(k_s)
+
+    def enc(x):
+        cb = None
+        if fit:
+            xb = x.float().reshape(*x.shape[:-1], x.shape[-1] // block_size, block_size)
+            norm = torch.sqrt((xb * xb).sum(-1, keepdim=True))
+            cb = lloyd_max_fit(xb / torch.where(norm == 0, torch.ones_like(norm), norm),
+                               lloydmax_bits_levels(3))
+        codes, norm, codebook = quantize_lloydmax(x, bits=3, block_size=block_size, codebook=cb)
+        return pack_indices_lowbit(codes, 3).contiguous(), norm.contiguous(), codebook
+
+    k_packed, k_norm, k_cb = enc(k_s)
+    v_packed, v_norm, v_cb = enc(v)
+    return {"k_packed": k_packed, "k_norm": k_norm, "k_codebook": k_cb, "v_packed": v_packed,
+            "v_norm": v_norm, "v_codebook": v_cb, "k_mean": k_mean, "rotate": rotate,
+            "block_size": block_size, "bits": 3}
+
+
+def dequantize_kv_cache_3bit(packed: dict, d: int):
+    """Inverse of quantize_kv_cache_3bit -> (k, v) fp16, K still smoothed and
+    rotated (reference ops.py:658-668)."""
+    from .quant.lloydmax import dequantize_lloydmax, unpack_indices_lowbit
+
+    bs = packed["block_size"]
+    k = dequantize_lloydmax(unpack_indices_lowbit(packed["k_packed"], 3, d), packed["k_norm"],
+                            packed["k_codebook"], block_size=bs)
+    v = dequantize_lloydmax(unpack_indices_lowbit(packed["v_packed"], 3, d), packed["v_norm"],
+                            packed["v_codebook"], block_size=bs)
+    return k.half(), v.half()
+
+
 def quantize_i8_rowwise(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """Fused per-row symmetric int8: x[M,K] -> (q int8 [M,K], scale fp32 [M])."""
     return _C.quantize_i8_rowwise(x)
