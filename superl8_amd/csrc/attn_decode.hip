@@ -63,7 +63,7 @@ struct PagedArgs {
   const int32_t* bt;   // [B, maxb] physical block per logical block
   const int32_t* ctx;  // [B] keys per sequence
   int maxb, bs;
-  int bs_sh;           // log2(bs) (streaming kernel: bs a power of two)
+  int bs_sh;           // log2(bs) (streaming kernels: bs a power of two; K8V3: -1 if not)
   int cache_rows;      // num_blocks * Hkv * bs (streaming kernel, block-aligned tiles)
 };
 // block-table entries of one split staged in LDS by the streaming paged kernel
@@ -1219,25 +1219,35 @@ kv_write_paged_kernel(const uint16_t* __restrict__ k_new, const uint16_t* __rest
 // v_packed [rows, 3D/32] u32 holds the code of channel d at bits 3d..3d+2 of
 // the row's LSB-first bit stream, v_norm [rows, D/128] fp32 one L2 norm per
 // 128-channel block, codebook [8] fp32; channel d of token row r is
-//   v = fp16_rn(codebook[code] * v_norm[r][d / 128]),
-// accumulated as p * v in fp32.
+//   v = fp16_rn(fp32(codebook[code] * v_norm[r][d / 128])).
 //
-// QK phase (lane = key): besides the K row, each lane loads its key's packed
-// codes (16-byte loads) into LDS and builds the key's value table per
-// 128-channel block, the eight fp16 values above, stored as a low-byte plane
-// (2 dwords) and a high-byte plane (2 dwords). PV phase (lane = 8 consecutive
-// channels x key phase): the lane's 24 code bits become byte selectors 0..7
-// and v_perm_b32 picks four table bytes per instruction, so the lookup needs
-// no indexed register access and no per-element LDS read.
+// One wave streams 64-key tiles of its split:
+//   * QK (lane = key): the int8 K row dotted with the G query heads
+//     (v_dot4), and the key's value table per 128-channel block built once:
+//     the eight fp16 values above as a low-byte plane (2 dwords) and a
+//     high-byte plane (2 dwords);
+//   * softmax: wave-uniform running max per head; p stored as fp16 in LDS,
+//     one 64-key row per head (rows G..15 stay zero);
+//   * PV in two 32-key halves: v_permlane32_swap hands lane l the code words
+//     and table of key l % 32 (+32 in the second half) for channel half l / 32,
+//     the lane turns 8 codes at a time into byte selectors 0..7 and picks the
+//     fp16 values out of the table planes with v_perm_b32, and writes its half
+//     row to an 8 KB (D = 128) LDS tile; the tile is then read transposed
+//     (ds_read_b64_tr_b16) as the A operand of v_mfma_f32_16x16x32_f16
+//     (16 channels x 32 keys) against P^T (32 keys x 16 heads).
+// P enters the MFMA as fp16 (relative rounding 2^-11 per probability; the
+// reference multiplies the fp32 p); the V values are exactly the reference's.
 template <int D, int G>
 struct K3Smem {
+  static constexpr int PP = 72;  // P row pitch in halves (64 keys + 8: bank spread)
   int q[G][D / 4];
   float qs[G];
-  union {
+  // 16-byte aligned: 16-byte tile writes and the transposed 8-byte reads need
+  // naturally aligned LDS addresses (q and qs end at 4 mod 16 when G = 1)
+  union alignas(16) {
     struct {
-      uint32_t codes[DEC_WAVES][DEC_TILE][3 * D / 32];
-      uint4 tbl[DEC_WAVES][DEC_TILE][D / 128];  // {lo 0-3, lo 4-7, hi 0-3, hi 4-7}
-      float p[DEC_WAVES][DEC_TILE][G];
+      uint16_t v[DEC_WAVES][32 * D];   // fp16 V half tile [32 keys][D], 32-byte chunks swizzled
+      uint16_t p[DEC_WAVES][16 * PP];  // fp16 P [16 heads][64 keys]
     } t;
     struct {
       float m[DEC_WAVES][G];
@@ -1253,21 +1263,51 @@ __device__ __forceinline__ uint32_t spread3x4(uint32_t a) {
   return (t & 0x00070007u) | ((t & 0x00380038u) << 5);
 }
 
+// 8 fp16 values (channel order) of the 8 codes in bits 0..23 of x, looked up
+// in the table planes tb = {lo 0-3, lo 4-7, hi 0-3, hi 4-7}
+__device__ __forceinline__ uint4 lm3_lookup8(uint32_t x, const uint4& tb) {
+  uint4 r;
+  const uint32_t s0 = spread3x4(x & 0xfffu), s1 = spread3x4((x >> 12) & 0xfffu);
+  uint32_t lo = __builtin_amdgcn_perm(tb.y, tb.x, s0);
+  uint32_t hi = __builtin_amdgcn_perm(tb.w, tb.z, s0);
+  r.x = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
+  r.y = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
+  lo = __builtin_amdgcn_perm(tb.y, tb.x, s1);
+  hi = __builtin_amdgcn_perm(tb.w, tb.z, s1);
+  r.z = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
+  r.w = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
+  return r;
+}
+
+__device__ __forceinline__ uint32_t swap32_lo(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_permlane32_swap(a, b, false, false)[0];
+}
+__device__ __forceinline__ uint32_t swap32_hi(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_permlane32_swap(a, b, false, false)[1];
+}
+
 template <int D, int G>
-__global__ void __launch_bounds__(DEC_THREADS)
+// workgroups per CU: the most that fit without spills (3 needs <= 168 VGPRs)
+__global__ void __launch_bounds__(DEC_THREADS, D == 128 ? (G <= 4 ? 3 : 2) : 1)
 k8v3_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_scale,
                   const int8_t* __restrict__ k, const float* __restrict__ k_scale,
                   const uint32_t* __restrict__ vpk, const float* __restrict__ vnorm,
                   const float* __restrict__ codebook, float* __restrict__ o_part,
                   float* __restrict__ m_part, float* __restrict__ l_part, int n_len,
                   int n_splits, int h_q, int h_kv, int gsz, int bhq, const PagedArgs pg) {
+  static_assert(G <= 16, "P^T has 16 head columns");
+  using SM = K3Smem<D, G>;
   constexpr int D4 = D / 4;
-  constexpr int DG = D / 8;            // 8-channel groups
-  constexpr int KPH = 64 / DG;         // key phases in the PV lane map
-  constexpr int KPL = DEC_TILE / KPH;  // keys per lane per tile in PV
-  constexpr int VW = 3 * D / 32;       // code dwords per row
-  constexpr int VB = D / 128;          // norms per row
-  __shared__ K3Smem<D, G> sm;
+  constexpr int VW = 3 * D / 32;  // code dwords per row
+  constexpr int VB = D / 128;     // norms per row
+  constexpr int HW = VW / 2;      // code dwords of one channel half
+  constexpr int DT = D / 16;      // 16-channel MFMA tiles
+  constexpr int RB = 2 * D;       // bytes per V row in LDS
+  constexpr int PP = SM::PP;
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  __shared__ SM sm;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int split = blockIdx.x;
@@ -1289,6 +1329,8 @@ k8v3_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_scal
     const int64_t hq = (int64_t)b * h_q + kvh * gsz + j0 + tid;
     sm.qs[tid] = tid < ng ? q_scale[hq] : 0.f;
   }
+  // P rows of the unused head columns stay zero
+  for (int i = lane; i < 16 * PP; i += 64) sm.t.p[wave][i] = 0;
   float cb[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) cb[i] = codebook[i];
@@ -1300,60 +1342,114 @@ k8v3_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_scal
   const int n1 = min(min(pg.ctx[b], n_len), n0 + per);
   const int32_t* btb = pg.bt + (int64_t)b * pg.maxb;
 
-  float m_run[G], l_lane[G], oacc[G][8];
+  // MFMA lane roles: column (head) n = lane % 16, row group g4 = lane / 16
+  const int col = lane & 15, g4 = lane >> 4;
+  const int kh = lane >> 5;  // PV: channel half
+  const int kr = lane & 31;  // PV: key row of the half tile this lane writes
+  // 32-byte chunk swizzle of V row r: 8 distinct values over the 16 rows one
+  // transposed read touches (rows 8g + 0..3 and 8g + 4..7)
+  auto vswz = [](int r) { return (r & 3) | (((r >> 3) & 1) << 2); };
+  const int wsw = vswz(kr);
+  // transposed read of lane (g4, j = col): rows 8 g4 + j / 4 (+4), channels 4 (j % 4)
+  const int rr = 8 * g4 + (col >> 2);
+  const int rsw = vswz(rr);
+  const int rbase = rr * RB + 8 * (col & 3);
+  uint16_t* vt = sm.t.v[wave];
+  uint16_t* pt = sm.t.p[wave];
+
+  float m_run[G], l_lane[G];
+  f4 oacc[DT];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     m_run[g] = -INFINITY;
     l_lane[g] = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) oacc[g][e] = 0.f;
   }
-  const int dg = lane % DG, kph = lane / DG;
-  // PV lane: code bits 24*dg .. 24*dg+23 of the row = dwords cw, cw1 from bit csh
-  const int cw = (3 * dg) >> 2, csh = (24 * dg) & 31;
-  const int cw1 = min(cw + 1, VW - 1);  // (csh <= 8 reads no bit of it)
-  const int vblk = dg / (128 / 8);
+#pragma unroll
+  for (int t = 0; t < DT; ++t) oacc[t] = f4{0.f, 0.f, 0.f, 0.f};
 
-  for (int t0 = n0 + wave * DEC_TILE; t0 < n1; t0 += DEC_WAVES * DEC_TILE) {
-    // ---- lane = key: logits, codes to LDS, value tables ----
-    const int n = t0 + lane;
-    const bool valid = n < n1;
+  // Tile inputs are loaded one tile ahead (and the block-table entry two
+  // tiles ahead), so a wave's next loads are in flight while it computes.
+  struct TileIn {
+    int4 kr[D / 16];
+    uint32_t cw[VW];
+    float nrm[VB];
+    float ks;
+  };
+  // block-table entry of the key lane + t (lanes past the split read key n0's)
+  auto bt_entry = [&](int t) -> int {
+    const int nn = t + lane < n1 ? t + lane : n0;
+    return btb[pg.bs_sh >= 0 ? nn >> pg.bs_sh : nn / pg.bs];
+  };
+  auto key_row = [&](int t, int blk) -> int64_t {
+    const int nn = t + lane < n1 ? t + lane : n0;
+    const int off = pg.bs_sh >= 0 ? nn & (pg.bs - 1) : nn % pg.bs;
+    return ((int64_t)blk * h_kv + kvh) * pg.bs + off;
+  };
+  auto load_k = [&](int64_t row, TileIn& ti) {
+    const int4* kp = reinterpret_cast<const int4*>(k + row * D);
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) ti.kr[c] = kp[c];
+    ti.ks = k_scale[row];
+  };
+  auto load_v = [&](int64_t row, TileIn& ti) {
+    const uint4* cp = reinterpret_cast<const uint4*>(vpk + row * VW);
+#pragma unroll
+    for (int c = 0; c < VW / 4; ++c) {
+      const uint4 w = cp[c];
+      ti.cw[4 * c] = w.x; ti.cw[4 * c + 1] = w.y; ti.cw[4 * c + 2] = w.z; ti.cw[4 * c + 3] = w.w;
+    }
+#pragma unroll
+    for (int j = 0; j < VB; ++j) ti.nrm[j] = vnorm[row * VB + j];
+  };
+  constexpr int TSTEP = DEC_WAVES * DEC_TILE;
+  int t0 = n0 + wave * DEC_TILE;
+  TileIn cur;
+  int btn = 0;  // block-table entry of the next tile's key
+  if (t0 < n1) {  // (an empty split has no valid key row to read)
+    const int64_t row = key_row(t0, bt_entry(t0));
+    load_k(row, cur);
+    load_v(row, cur);
+    btn = bt_entry(t0 + TSTEP);
+  }
+  // One tile. The next tile's inputs are loaded into the same registers right
+  // after their last use here (K and its scale after the logits, codes and
+  // norms after the value tables and lane swaps), and the block-table entry
+  // of the tile after it last: one register set, loads in flight during most
+  // of the tile's compute. The loads are unconditional (inside the loop
+  // n0 < n1, and lanes past the split read key n0's row): loads under a branch
+  // would make the compiler wait for all of them at the join.
+  auto step = [&]() __attribute__((always_inline)) {
+    const int64_t nrow = key_row(t0 + TSTEP, btn);
+    // ---- lane = key: logits, value tables ----
+    const bool valid = t0 + lane < n1;
     float s[G];
+    uint32_t cw[VW];
+    uint4 tbl[VB];
     {
-      const int nn = valid ? n : n0;
-      const int64_t row = ((int64_t)btb[nn / pg.bs] * h_kv + kvh) * pg.bs + nn % pg.bs;
-      int4 kr[D / 16];
-      const int4* kp = reinterpret_cast<const int4*>(k + row * D);
 #pragma unroll
-      for (int c = 0; c < D / 16; ++c) kr[c] = kp[c];
-      uint4 cr[VW / 4];
-      const uint4* cp = reinterpret_cast<const uint4*>(vpk + row * VW);
-#pragma unroll
-      for (int c = 0; c < VW / 4; ++c) cr[c] = cp[c];
-      float nrm[VB];
-#pragma unroll
-      for (int j = 0; j < VB; ++j) nrm[j] = vnorm[row * VB + j];
-      const float ks = valid ? k_scale[row] : 0.f;
+      for (int w = 0; w < VW; ++w) cw[w] = cur.cw[w];
+      const float ks = valid ? cur.ks : 0.f;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         int acc = 0;
 #pragma unroll
         for (int c = 0; c < D / 16; ++c) {
           const int4 qv = *reinterpret_cast<const int4*>(&sm.q[g][4 * c]);
-          acc = __builtin_amdgcn_sdot4(qv.x, kr[c].x, acc, false);
-          acc = __builtin_amdgcn_sdot4(qv.y, kr[c].y, acc, false);
-          acc = __builtin_amdgcn_sdot4(qv.z, kr[c].z, acc, false);
-          acc = __builtin_amdgcn_sdot4(qv.w, kr[c].w, acc, false);
+          acc = __builtin_amdgcn_sdot4(qv.x, cur.kr[c].x, acc, false);
+          acc = __builtin_amdgcn_sdot4(qv.y, cur.kr[c].y, acc, false);
+          acc = __builtin_amdgcn_sdot4(qv.z, cur.kr[c].z, acc, false);
+          acc = __builtin_amdgcn_sdot4(qv.w, cur.kr[c].w, acc, false);
         }
         s[g] = valid ? ((float)acc * sm.qs[g]) * ks : -INFINITY;
       }
+      load_k(nrow, cur);
+      float nrm[VB];
 #pragma unroll
-      for (int c = 0; c < VW / 4; ++c)
-        *reinterpret_cast<uint4*>(&sm.t.codes[wave][lane][4 * c]) = cr[c];
+      for (int j = 0; j < VB; ++j) nrm[j] = cur.nrm[j];
 #pragma unroll
       for (int j = 0; j < VB; ++j) {
-        // fp16 values of entries 2e, 2e+1: the product rounded to fp32 first,
-        // then to fp16. The empty asm keeps the fp32 product in a register:
+        // fp16 values of entries 0..7: the product rounded to fp32 first, then
+        // to fp16. The empty asm keeps the fp32 product in a register:
         // otherwise the multiply and the conversion fuse into one
         // v_fma_mixlo_f16, which rounds the exact product once (a different
         // fp16 value when the fp32 product lands on an fp16 midpoint).
@@ -1367,15 +1463,13 @@ k8v3_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_scal
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           h[e] = (uint32_t)f2h_bits(pr[2 * e]) | ((uint32_t)f2h_bits(pr[2 * e + 1]) << 16);
-        uint4 tb;
-        tb.x = __builtin_amdgcn_perm(h[1], h[0], 0x06040200u);  // low bytes of 0..3
-        tb.y = __builtin_amdgcn_perm(h[3], h[2], 0x06040200u);  // low bytes of 4..7
-        tb.z = __builtin_amdgcn_perm(h[1], h[0], 0x07050301u);  // high bytes of 0..3
-        tb.w = __builtin_amdgcn_perm(h[3], h[2], 0x07050301u);  // high bytes of 4..7
-        sm.t.tbl[wave][lane][j] = tb;
+        tbl[j].x = __builtin_amdgcn_perm(h[1], h[0], 0x06040200u);  // low bytes of 0..3
+        tbl[j].y = __builtin_amdgcn_perm(h[3], h[2], 0x06040200u);  // low bytes of 4..7
+        tbl[j].z = __builtin_amdgcn_perm(h[1], h[0], 0x07050301u);  // high bytes of 0..3
+        tbl[j].w = __builtin_amdgcn_perm(h[3], h[2], 0x07050301u);  // high bytes of 4..7
       }
     }
-    // ---- online softmax (wave-uniform running max per head) ----
+    // ---- online softmax; p (fp16) to the head rows of P ----
     float resc[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -1385,67 +1479,85 @@ k8v3_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_scal
       m_run[g] = mn;
       const float p = exp2f(s[g] - mn);
       l_lane[g] = l_lane[g] * resc[g] + p;
-      sm.t.p[wave][lane][g] = p;
+      pt[g * PP + lane] = f2h_bits(p);
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float rl = 1.f;  // rescale of this lane's accumulator column (head col)
+#pragma unroll
+    for (int g = 0; g < G; ++g) rl = col == g ? resc[g] : rl;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) oacc[t] *= rl;
 
-    // ---- PV: lane = (channel group dg, key phase kph) ----
+    // ---- PV, two 32-key halves ----
+    // half 0: key kr, channel half kh; half 1: key kr + 32
+    uint32_t c0[HW], c1[HW];
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+    for (int w = 0; w < HW; ++w) {
+      c0[w] = swap32_lo(cw[w], cw[HW + w]);
+      c1[w] = swap32_hi(cw[w], cw[HW + w]);
+    }
+    uint4 t0v, t1v;  // tables of the lane's 128-channel block, both halves
+    {
+      const uint4& tf = tbl[0];
+      const uint4& ts = tbl[VB - 1];
+      t0v.x = swap32_lo(tf.x, ts.x); t1v.x = swap32_hi(tf.x, ts.x);
+      t0v.y = swap32_lo(tf.y, ts.y); t1v.y = swap32_hi(tf.y, ts.y);
+      t0v.z = swap32_lo(tf.z, ts.z); t1v.z = swap32_hi(tf.z, ts.z);
+      t0v.w = swap32_lo(tf.w, ts.w); t1v.w = swap32_hi(tf.w, ts.w);
+    }
+    load_v(nrow, cur);
+    btn = bt_entry(t0 + 2 * TSTEP);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) oacc[g][e] *= resc[g];
-#pragma unroll 4
-    for (int i = 0; i < KPL; ++i) {
-      const int kk = kph + i * KPH;
-      if (t0 + kk < n1) {
-        const uint32_t x = __builtin_amdgcn_alignbit(sm.t.codes[wave][kk][cw1],
-                                                     sm.t.codes[wave][kk][cw], csh);
-        const uint4 tb = sm.t.tbl[wave][kk][vblk];
-        float vf[8];
+    for (int hf = 0; hf < 2; ++hf) {
+      const uint32_t* cc = hf ? c1 : c0;
+      const uint4 tb = hf ? t1v : t0v;
+      if (hf) __builtin_amdgcn_wave_barrier();  // half 0's tile reads are done
+      // dequantise D/2 channels (D/16 groups of 8) of key row kr to LDS
 #pragma unroll
-        for (int hlf = 0; hlf < 2; ++hlf) {
-          const uint32_t sel = spread3x4((x >> (12 * hlf)) & 0xfffu);
-          const uint32_t lo = __builtin_amdgcn_perm(tb.y, tb.x, sel);
-          const uint32_t hi = __builtin_amdgcn_perm(tb.w, tb.z, sel);
-          const uint32_t p01 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
-          const uint32_t p23 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
-          vf[4 * hlf + 0] = h2f((uint16_t)(p01 & 0xffffu));
-          vf[4 * hlf + 1] = h2f((uint16_t)(p01 >> 16));
-          vf[4 * hlf + 2] = h2f((uint16_t)(p23 & 0xffffu));
-          vf[4 * hlf + 3] = h2f((uint16_t)(p23 >> 16));
-        }
+      for (int gi = 0; gi < D / 16; ++gi) {
+        const int bit = 24 * gi, w = bit >> 5, sh = bit & 31;
+        const uint32_t x = sh <= 8 ? (cc[w] >> sh)
+                                   : __builtin_amdgcn_alignbit(cc[w + 1], cc[w], sh);
+        const int c16 = kh * (D / 16) + gi;  // 16-byte chunk of the row
+        const int off = kr * RB + ((((c16 >> 1) ^ wsw) << 1) | (c16 & 1)) * 16;
+        *reinterpret_cast<uint4*>(reinterpret_cast<char*>(vt) + off) = lm3_lookup8(x, tb);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      // B = P^T: keys 32 hf + 8 g4 .. +7 of head col
+      const h8 pb = *reinterpret_cast<const h8*>(pt + col * PP + 32 * hf + 8 * g4);
+      const char* vbytes = reinterpret_cast<const char*>(vt);
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-          const float p = sm.t.p[wave][kk][g];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) oacc[g][e] = fmaf(p, vf[e], oacc[g][e]);
-        }
+      for (int t = 0; t < DT; ++t) {
+        const char* a0 = vbytes + rbase + ((t ^ rsw) << 5);
+        const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(a0));
+        const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(a0 + 4 * RB));
+        typedef short v8s __attribute__((ext_vector_type(8)));
+        const v8s both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        oacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, both), pb, oacc[t],
+                                                         0, 0, 0);
       }
     }
     __builtin_amdgcn_wave_barrier();  // the wave's tile region is rewritten next tile
-  }
+    t0 += TSTEP;
+  };
+  while (t0 < n1) step();
   __syncthreads();  // every wave is done with the tile region (aliased below)
 
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const float lw = wave_sum(l_lane[g]);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float x = oacc[g][e];
-#pragma unroll
-      for (int o = DG; o < 64; o <<= 1) x += __shfl_xor(x, o, 64);
-      oacc[g][e] = x;
-    }
     if (lane == 0) {
       sm.r.m[wave][g] = m_run[g];
       sm.r.l[wave][g] = lw;
     }
-    if (kph == 0) {
+  }
+  // accumulator lane (g4, col) holds channels 16 t + 4 g4 + i of head col
+  if (col < G) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sm.r.o[wave][g][dg * 8 + e] = oacc[g][e];
-    }
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sm.r.o[wave][col][16 * t + 4 * g4 + i] = oacc[t][i];
   }
   __syncthreads();
 
@@ -1635,7 +1747,10 @@ extern "C" int sl8_attn_paged_decode_k8v3(const int8_t* q, const float* q_scale,
   float* mp = op + (size_t)ns * ibhq * D;
   float* lp = mp + (size_t)ns * ibhq;
   const dim3 grid((unsigned)ns, (unsigned)(B * Hkv), (unsigned)((gsz + G - 1) / G));
-  const PagedArgs pg{block_table, context_lens, (int)max_blocks_per_seq, (int)block_size, 0, 0};
+  int bs_sh = 0;
+  while ((1LL << bs_sh) < block_size) ++bs_sh;
+  if ((1LL << bs_sh) != block_size) bs_sh = -1;  // not a power of two: divide
+  const PagedArgs pg{block_table, context_lens, (int)max_blocks_per_seq, (int)block_size, bs_sh, 0};
   const uint32_t* vp = reinterpret_cast<const uint32_t*>(v_packed);
 #define SL8_K3(DD, GG)                                                                      \
   k8v3_split_kernel<DD, GG><<<grid, DEC_THREADS, 0, st>>>(                                  \
