@@ -1,7 +1,8 @@
 """Serve this package under the reference's module names.
 
 ``install()`` registers ``superl8``, ``superl8.ops``, ``superl8._C``,
-``superl8.quant``, ``superl8.format`` and ``superl8.gguf`` in ``sys.modules``
+``superl8.quant`` (with ``.core``, ``.rotation`` and ``.lloydmax``),
+``superl8.format`` and ``superl8.gguf`` in ``sys.modules``
 so that code written against the reference's hot-path surface
 (``from superl8.ops import attn_int8_fwd``, ``from superl8 import _C``, ...)
 runs on this build unchanged. Names that already exist in ``sys.modules`` (the
@@ -12,7 +13,7 @@ from __future__ import annotations
 
 import sys
 
-_SUBMODULES = ("ops", "_C", "quant", "format", "gguf")
+_SUBMODULES = ("ops", "_C", "quant", "quant.core", "quant.rotation", "quant.lloydmax", "format", "gguf")
 
 
 def install(force: bool = False) -> None:

@@ -1481,11 +1481,18 @@ k8v3_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_scal
       l_lane[g] = l_lane[g] * resc[g] + p;
       pt[g * PP + lane] = f2h_bits(p);
     }
-    float rl = 1.f;  // rescale of this lane's accumulator column (head col)
+    // rescale the accumulators only when some head's running max moved (the
+    // factors are wave-uniform; an unchanged max gives exactly 1)
+    bool moved = false;
 #pragma unroll
-    for (int g = 0; g < G; ++g) rl = col == g ? resc[g] : rl;
+    for (int g = 0; g < G; ++g) moved |= resc[g] != 1.f;
+    if (moved) {
+      float rl = 1.f;  // rescale of this lane's accumulator column (head col)
 #pragma unroll
-    for (int t = 0; t < DT; ++t) oacc[t] *= rl;
+      for (int g = 0; g < G; ++g) rl = col == g ? resc[g] : rl;
+#pragma unroll
+      for (int t = 0; t < DT; ++t) oacc[t] *= rl;
+    }
 
     // ---- PV, two 32-key halves ----
     // half 0: key kr, channel half kh; half 1: key kr + 32

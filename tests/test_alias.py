@@ -29,6 +29,13 @@ REF_OPS = [
                                   ("v_scale", P, E), ("block_table", P, E), ("context_lens", P, E),
                                   ("block_size", P, E), ("max_context_len", K, None), ("scale", K, None),
                                   ("rotate", K, True), ("num_splits", K, None)]),          # ops.py:778-792
+    ("attn_paged_decode_k8v3", [("q", P, E), ("k_cache", P, E), ("k_scale", P, E), ("v_packed", P, E),
+                                ("v_norm", P, E), ("v_codebook", P, E), ("block_table", P, E),
+                                ("context_lens", P, E), ("block_size", P, E), ("max_context_len", K, None),
+                                ("scale", K, None), ("rotate", K, True), ("num_splits", K, None)]),  # ops.py:852-866
+    ("quantize_kv_cache_3bit", [("k", P, E), ("v", P, E), ("rotate", K, True), ("fit", K, True),
+                                ("block_size", K, 128)]),                                  # ops.py:590-597
+    ("dequantize_kv_cache_3bit", [("packed", P, E), ("d", P, E)]),                         # ops.py:658
     ("quantize_i8_rowwise", [("x", P, E)]),                                                # ops.py:975
     ("linear_q4k", [("x", P, E), ("w_bytes", P, E), ("bias", K, None), ("out_dtype", K, "torch.float16")]),  # ops.py:1254-1260
     ("linear", [("x", P, E), ("qt", P, E), ("bias", K, None), ("out_dtype", K, "torch.float16")]),  # ops.py:2088-2094
@@ -36,7 +43,7 @@ REF_OPS = [
 
 # _C functions of this path (reference csrc/fni8_api.cpp m.def names)
 REF_C = ["quantize_i8_rowwise", "attn_int8_fwd", "attn_int8_fwd_train", "attn_w8a8_fwd", "attn_int8_decode",
-         "attn_int8_decode_kv8", "attn_paged_decode", "kv_write_paged", "gemm_q4k", "gemm_decode_q4k",
+         "attn_int8_decode_kv8", "attn_paged_decode", "attn_paged_decode_k8v3", "kv_write_paged", "gemm_q4k", "gemm_decode_q4k",
          "gemm_q5k", "gemm_q6k", "gemm_decode_q5k", "gemm_decode_q6k"]
 
 
@@ -64,6 +71,8 @@ def test_reference_import_paths_resolve(aliased):
     from superl8 import _C, format, gguf, quant  # noqa: F401
     from superl8.ops import attn_decode_cached, attn_int8_decode, attn_int8_fwd  # noqa: F401
     from superl8.quant import quantize_qk, smooth_k  # noqa: F401
+    from superl8.quant.lloydmax import pack_indices_lowbit, quantize_lloydmax  # noqa: F401
+    from superl8.quant.rotation import rotate_last  # noqa: F401
 
     assert superl8.attn_int8_fwd is attn_int8_fwd
     for fn in REF_C:
