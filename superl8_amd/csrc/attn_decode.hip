@@ -1221,22 +1221,32 @@ kv_write_paged_kernel(const uint16_t* __restrict__ k_new, const uint16_t* __rest
 // 128-channel block, codebook [8] fp32; channel d of token row r is
 //   v = fp16_rn(fp32(codebook[code] * v_norm[r][d / 128])).
 //
-// One wave streams 64-key tiles of its split:
-//   * QK (lane = key): the int8 K row dotted with the G query heads
-//     (v_dot4), and the key's value table per 128-channel block built once:
-//     the eight fp16 values above as a low-byte plane (2 dwords) and a
-//     high-byte plane (2 dwords);
-//   * softmax: wave-uniform running max per head; p stored as fp16 in LDS,
-//     one 64-key row per head (rows G..15 stay zero);
-//   * PV in two 32-key halves: v_permlane32_swap hands lane l the code words
-//     and table of key l % 32 (+32 in the second half) for channel half l / 32,
-//     the lane turns 8 codes at a time into byte selectors 0..7 and picks the
-//     fp16 values out of the table planes with v_perm_b32, and writes its half
-//     row to an 8 KB (D = 128) LDS tile; the tile is then read transposed
+// One wave streams 64-key tiles of its split. Lane roles: (g4, col) =
+// (lane / 16, lane % 16) for the MFMAs, key = lane for the per-key work,
+// (kr, kh) = (lane % 32, lane / 32) for the V dequantisation.
+//   * QK: S^T (64 keys x 16 head columns) on v_mfma_i32_16x16x64_i8 straight
+//     from the loads: the A operand of key block kb is key 16 kb + col,
+//     bytes 16 g4 .. +15 of each 64-byte K slice, which is also a coalesced
+//     load (64 contiguous bytes per row and instruction); Q^T (B) stays in
+//     registers, head columns >= G zero;
+//   * softmax in the MFMA output layout: lane (g4, col) holds keys
+//     16 kb + 4 g4 + i of head col; logit = (acc * k_scale) * q_scale, the
+//     tile max over the lane's 16 values and the 4 lanes of the column; p
+//     stored as fp16 in LDS, one 64-key row per head (rows G..15 stay zero);
+//   * value tables (key = lane): fp16 of codebook[i] * norm for i = 0..7 per
+//     128-channel block, as a low-byte plane (2 dwords) and a high-byte plane
+//     (2 dwords), handed to the dequantising lanes by v_permlane32_swap;
+//   * PV in two 32-key halves: lane (kr, kh) loads the code bits of channel
+//     half kh of key 32 h + kr, turns 8 codes at a time into byte selectors
+//     0..7, picks the fp16 values out of the table planes with v_perm_b32, and
+//     writes the half row to an 8 KB (D = 128) LDS tile, read back transposed
 //     (ds_read_b64_tr_b16) as the A operand of v_mfma_f32_16x16x32_f16
 //     (16 channels x 32 keys) against P^T (32 keys x 16 heads).
-// P enters the MFMA as fp16 (relative rounding 2^-11 per probability; the
-// reference multiplies the fp32 p); the V values are exactly the reference's.
+// Each of the next tile's loads goes into the registers of the current tile's
+// input right after its last use, so they are in flight during the rest of
+// the tile. P enters the MFMA as fp16 (relative rounding 2^-11 per
+// probability; the reference multiplies the fp32 p); the V values are exactly
+// the reference's.
 template <int D, int G>
 struct K3Smem {
   static constexpr int PP = 72;  // P row pitch in halves (64 keys + 8: bank spread)
@@ -1248,6 +1258,7 @@ struct K3Smem {
     struct {
       uint16_t v[DEC_WAVES][32 * D];   // fp16 V half tile [32 keys][D], 32-byte chunks swizzled
       uint16_t p[DEC_WAVES][16 * PP];  // fp16 P [16 heads][64 keys]
+      float ks[DEC_WAVES][DEC_TILE];   // the tile's k_scale
     } t;
     struct {
       float m[DEC_WAVES][G];
@@ -1287,7 +1298,7 @@ __device__ __forceinline__ uint32_t swap32_hi(uint32_t a, uint32_t b) {
 }
 
 template <int D, int G>
-// workgroups per CU: the most that fit without spills (3 needs <= 168 VGPRs)
+// workgroups per CU: the most that fit without spills
 __global__ void __launch_bounds__(DEC_THREADS, D == 128 ? (G <= 4 ? 3 : 2) : 1)
 k8v3_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_scale,
                   const int8_t* __restrict__ k, const float* __restrict__ k_scale,
@@ -1295,9 +1306,10 @@ k8v3_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_scal
                   const float* __restrict__ codebook, float* __restrict__ o_part,
                   float* __restrict__ m_part, float* __restrict__ l_part, int n_len,
                   int n_splits, int h_q, int h_kv, int gsz, int bhq, const PagedArgs pg) {
-  static_assert(G <= 16, "P^T has 16 head columns");
+  static_assert(G <= 16, "S^T and P^T have 16 head columns");
   using SM = K3Smem<D, G>;
   constexpr int D4 = D / 4;
+  constexpr int KS = D / 64;      // 64-channel QK steps
   constexpr int VW = 3 * D / 32;  // code dwords per row
   constexpr int VB = D / 128;     // norms per row
   constexpr int HW = VW / 2;      // code dwords of one channel half
@@ -1307,6 +1319,7 @@ k8v3_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_scal
   typedef _Float16 h8 __attribute__((ext_vector_type(8)));
   typedef short v4s __attribute__((ext_vector_type(4)));
   typedef float f4 __attribute__((ext_vector_type(4)));
+  typedef int v4i __attribute__((ext_vector_type(4)));
   __shared__ SM sm;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1336,16 +1349,21 @@ k8v3_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_scal
   for (int i = 0; i < 8; ++i) cb[i] = codebook[i];
   __syncthreads();
 
+  const int col = lane & 15, g4 = lane >> 4;  // MFMA roles
+  const int kh = lane >> 5, kr = lane & 31;   // dequantisation roles
+  // Q^T (B operand of QK): head col, channels 64 s + 16 g4 .. +15
+  v4i qb[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s)
+    qb[s] = col < G ? *reinterpret_cast<const v4i*>(&sm.q[col][16 * s + 4 * g4]) : v4i{0, 0, 0, 0};
+  const float qsl = col < G ? sm.qs[col] : 0.f;
+
   const int per = (n_len + n_splits - 1) / n_splits;
   const int n0 = split * per;
   // a context length above max_context_len (n_len) is read as max_context_len
   const int n1 = min(min(pg.ctx[b], n_len), n0 + per);
   const int32_t* btb = pg.bt + (int64_t)b * pg.maxb;
 
-  // MFMA lane roles: column (head) n = lane % 16, row group g4 = lane / 16
-  const int col = lane & 15, g4 = lane >> 4;
-  const int kh = lane >> 5;  // PV: channel half
-  const int kr = lane & 31;  // PV: key row of the half tile this lane writes
   // 32-byte chunk swizzle of V row r: 8 distinct values over the 16 rows one
   // transposed read touches (rows 8g + 0..3 and 8g + 4..7)
   auto vswz = [](int r) { return (r & 3) | (((r >> 3) & 1) << 2); };
@@ -1356,177 +1374,189 @@ k8v3_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_scal
   const int rbase = rr * RB + 8 * (col & 3);
   uint16_t* vt = sm.t.v[wave];
   uint16_t* pt = sm.t.p[wave];
+  float* kst = sm.t.ks[wave];
 
-  float m_run[G], l_lane[G];
-  f4 oacc[DT];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    m_run[g] = -INFINITY;
-    l_lane[g] = 0.f;
-  }
-#pragma unroll
-  for (int t = 0; t < DT; ++t) oacc[t] = f4{0.f, 0.f, 0.f, 0.f};
-
-  // Tile inputs are loaded one tile ahead (and the block-table entry two
-  // tiles ahead), so a wave's next loads are in flight while it computes.
-  struct TileIn {
-    int4 kr[D / 16];
-    uint32_t cw[VW];
-    float nrm[VB];
-    float ks;
-  };
-  // block-table entry of the key lane + t (lanes past the split read key n0's)
+  // block-table entry of key lane + t (lanes past the split read key n0's)
   auto bt_entry = [&](int t) -> int {
     const int nn = t + lane < n1 ? t + lane : n0;
     return btb[pg.bs_sh >= 0 ? nn >> pg.bs_sh : nn / pg.bs];
   };
-  auto key_row = [&](int t, int blk) -> int64_t {
+  // cache row of key lane + t (< 2^31: checked by the launcher)
+  auto key_row = [&](int t, int blk) -> int {
     const int nn = t + lane < n1 ? t + lane : n0;
     const int off = pg.bs_sh >= 0 ? nn & (pg.bs - 1) : nn % pg.bs;
-    return ((int64_t)blk * h_kv + kvh) * pg.bs + off;
+    return (blk * h_kv + kvh) * pg.bs + off;
   };
-  auto load_k = [&](int64_t row, TileIn& ti) {
-    const int4* kp = reinterpret_cast<const int4*>(k + row * D);
+  // tile inputs (one register set, reloaded piece by piece after last use)
+  v4i ka[4][KS];        // K: key 16 kb + col, channels 64 s + 16 g4 .. +15
+  float ksv;            // k_scale of key lane
+  float nrm[VB];        // norms of key lane
+  uint2 cw[2][HW / 2];  // code bits of channel half kh of key 32 h + kr
+  auto load_k = [&](int row) {
 #pragma unroll
-    for (int c = 0; c < D / 16; ++c) ti.kr[c] = kp[c];
-    ti.ks = k_scale[row];
-  };
-  auto load_v = [&](int64_t row, TileIn& ti) {
-    const uint4* cp = reinterpret_cast<const uint4*>(vpk + row * VW);
+    for (int kb = 0; kb < 4; ++kb) {
+      const int r = __shfl(row, 16 * kb + col, 64);
+      const int8_t* kp = k + (int64_t)r * D + 16 * g4;
 #pragma unroll
-    for (int c = 0; c < VW / 4; ++c) {
-      const uint4 w = cp[c];
-      ti.cw[4 * c] = w.x; ti.cw[4 * c + 1] = w.y; ti.cw[4 * c + 2] = w.z; ti.cw[4 * c + 3] = w.w;
+      for (int s = 0; s < KS; ++s) ka[kb][s] = *reinterpret_cast<const v4i*>(kp + 64 * s);
     }
-#pragma unroll
-    for (int j = 0; j < VB; ++j) ti.nrm[j] = vnorm[row * VB + j];
+    ksv = k_scale[row];
   };
+  auto load_nrm = [&](int row) {
+#pragma unroll
+    for (int j = 0; j < VB; ++j) nrm[j] = vnorm[(int64_t)row * VB + j];
+  };
+  auto load_codes = [&](int row, int h) {
+    const int r = __shfl(row, 32 * h + kr, 64);
+    const uint2* cp = reinterpret_cast<const uint2*>(vpk + (int64_t)r * VW + kh * HW);
+#pragma unroll
+    for (int w = 0; w < HW / 2; ++w) cw[h][w] = cp[w];
+  };
+
+  float m_run = -INFINITY, l_lane = 0.f;  // head col
+  f4 oacc[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) oacc[t] = f4{0.f, 0.f, 0.f, 0.f};
+
   constexpr int TSTEP = DEC_WAVES * DEC_TILE;
   int t0 = n0 + wave * DEC_TILE;
-  TileIn cur;
-  int btn = 0;  // block-table entry of the next tile's key
+  int btn = 0;  // block-table entry of the next tile's key lane
   if (t0 < n1) {  // (an empty split has no valid key row to read)
-    const int64_t row = key_row(t0, bt_entry(t0));
-    load_k(row, cur);
-    load_v(row, cur);
+    const int row = key_row(t0, bt_entry(t0));
+    load_k(row);
+    load_nrm(row);
+    load_codes(row, 0);
+    load_codes(row, 1);
     btn = bt_entry(t0 + TSTEP);
   }
-  // One tile. The next tile's inputs are loaded into the same registers right
-  // after their last use here (K and its scale after the logits, codes and
-  // norms after the value tables and lane swaps), and the block-table entry
-  // of the tile after it last: one register set, loads in flight during most
-  // of the tile's compute. The loads are unconditional (inside the loop
-  // n0 < n1, and lanes past the split read key n0's row): loads under a branch
-  // would make the compiler wait for all of them at the join.
-  auto step = [&]() __attribute__((always_inline)) {
-    const int64_t nrow = key_row(t0 + TSTEP, btn);
-    // ---- lane = key: logits, value tables ----
-    const bool valid = t0 + lane < n1;
-    float s[G];
-    uint32_t cw[VW];
+  // The loads are unconditional inside the loop (n0 < n1 there, and lanes
+  // past the split read key n0's row): loads under a branch would make the
+  // compiler wait for all of them at the join.
+  while (t0 < n1) {
+    const int nrow = key_row(t0 + TSTEP, btn);
+    kst[lane] = ksv;
+    // ---- QK on the matrix core ----
+    v4i sacc[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      sacc[kb] = v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        sacc[kb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ka[kb][s], qb[s], sacc[kb], 0, 0, 0);
+    }
+    load_k(nrow);
+    btn = bt_entry(t0 + 2 * TSTEP);
+    // ---- value tables of key lane ----
     uint4 tbl[VB];
-    {
 #pragma unroll
-      for (int w = 0; w < VW; ++w) cw[w] = cur.cw[w];
-      const float ks = valid ? cur.ks : 0.f;
+    for (int j = 0; j < VB; ++j) {
+      // fp16 values of entries 0..7: the product rounded to fp32 first, then
+      // to fp16. The empty asm keeps the fp32 product in a register:
+      // otherwise the multiply and the conversion fuse into one
+      // v_fma_mixlo_f16, which rounds the exact product once (a different
+      // fp16 value when the fp32 product lands on an fp16 midpoint).
+      float pr[8];
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        int acc = 0;
-#pragma unroll
-        for (int c = 0; c < D / 16; ++c) {
-          const int4 qv = *reinterpret_cast<const int4*>(&sm.q[g][4 * c]);
-          acc = __builtin_amdgcn_sdot4(qv.x, cur.kr[c].x, acc, false);
-          acc = __builtin_amdgcn_sdot4(qv.y, cur.kr[c].y, acc, false);
-          acc = __builtin_amdgcn_sdot4(qv.z, cur.kr[c].z, acc, false);
-          acc = __builtin_amdgcn_sdot4(qv.w, cur.kr[c].w, acc, false);
-        }
-        s[g] = valid ? ((float)acc * sm.qs[g]) * ks : -INFINITY;
+      for (int e = 0; e < 8; ++e) {
+        pr[e] = cb[e] * nrm[j];
+        asm volatile("" : "+v"(pr[e]));
       }
-      load_k(nrow, cur);
-      float nrm[VB];
+      uint32_t h[4];
 #pragma unroll
-      for (int j = 0; j < VB; ++j) nrm[j] = cur.nrm[j];
-#pragma unroll
-      for (int j = 0; j < VB; ++j) {
-        // fp16 values of entries 0..7: the product rounded to fp32 first, then
-        // to fp16. The empty asm keeps the fp32 product in a register:
-        // otherwise the multiply and the conversion fuse into one
-        // v_fma_mixlo_f16, which rounds the exact product once (a different
-        // fp16 value when the fp32 product lands on an fp16 midpoint).
-        float pr[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          pr[e] = cb[e] * nrm[j];
-          asm volatile("" : "+v"(pr[e]));
-        }
-        uint32_t h[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          h[e] = (uint32_t)f2h_bits(pr[2 * e]) | ((uint32_t)f2h_bits(pr[2 * e + 1]) << 16);
-        tbl[j].x = __builtin_amdgcn_perm(h[1], h[0], 0x06040200u);  // low bytes of 0..3
-        tbl[j].y = __builtin_amdgcn_perm(h[3], h[2], 0x06040200u);  // low bytes of 4..7
-        tbl[j].z = __builtin_amdgcn_perm(h[1], h[0], 0x07050301u);  // high bytes of 0..3
-        tbl[j].w = __builtin_amdgcn_perm(h[3], h[2], 0x07050301u);  // high bytes of 4..7
-      }
+      for (int e = 0; e < 4; ++e)
+        h[e] = (uint32_t)f2h_bits(pr[2 * e]) | ((uint32_t)f2h_bits(pr[2 * e + 1]) << 16);
+      tbl[j].x = __builtin_amdgcn_perm(h[1], h[0], 0x06040200u);  // low bytes of 0..3
+      tbl[j].y = __builtin_amdgcn_perm(h[3], h[2], 0x06040200u);  // low bytes of 4..7
+      tbl[j].z = __builtin_amdgcn_perm(h[1], h[0], 0x07050301u);  // high bytes of 0..3
+      tbl[j].w = __builtin_amdgcn_perm(h[3], h[2], 0x07050301u);  // high bytes of 4..7
     }
-    // ---- online softmax; p (fp16) to the head rows of P ----
-    float resc[G];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float mt = wave_max(s[g]);
-      const float mn = fmaxf(m_run[g], mt);
-      resc[g] = exp2f(m_run[g] - mn);
-      m_run[g] = mn;
-      const float p = exp2f(s[g] - mn);
-      l_lane[g] = l_lane[g] * resc[g] + p;
-      pt[g * PP + lane] = f2h_bits(p);
-    }
-    // rescale the accumulators only when some head's running max moved (the
-    // factors are wave-uniform; an unchanged max gives exactly 1)
-    bool moved = false;
-#pragma unroll
-    for (int g = 0; g < G; ++g) moved |= resc[g] != 1.f;
-    if (moved) {
-      float rl = 1.f;  // rescale of this lane's accumulator column (head col)
-#pragma unroll
-      for (int g = 0; g < G; ++g) rl = col == g ? resc[g] : rl;
-#pragma unroll
-      for (int t = 0; t < DT; ++t) oacc[t] *= rl;
-    }
-
-    // ---- PV, two 32-key halves ----
-    // half 0: key kr, channel half kh; half 1: key kr + 32
-    uint32_t c0[HW], c1[HW];
-#pragma unroll
-    for (int w = 0; w < HW; ++w) {
-      c0[w] = swap32_lo(cw[w], cw[HW + w]);
-      c1[w] = swap32_hi(cw[w], cw[HW + w]);
-    }
-    uint4 t0v, t1v;  // tables of the lane's 128-channel block, both halves
+    load_nrm(nrow);
+    // tables of the dequantising lane's 128-channel block, both halves
+    uint4 tv[2];
     {
       const uint4& tf = tbl[0];
       const uint4& ts = tbl[VB - 1];
-      t0v.x = swap32_lo(tf.x, ts.x); t1v.x = swap32_hi(tf.x, ts.x);
-      t0v.y = swap32_lo(tf.y, ts.y); t1v.y = swap32_hi(tf.y, ts.y);
-      t0v.z = swap32_lo(tf.z, ts.z); t1v.z = swap32_hi(tf.z, ts.z);
-      t0v.w = swap32_lo(tf.w, ts.w); t1v.w = swap32_hi(tf.w, ts.w);
+      tv[0].x = swap32_lo(tf.x, ts.x); tv[1].x = swap32_hi(tf.x, ts.x);
+      tv[0].y = swap32_lo(tf.y, ts.y); tv[1].y = swap32_hi(tf.y, ts.y);
+      tv[0].z = swap32_lo(tf.z, ts.z); tv[1].z = swap32_hi(tf.z, ts.z);
+      tv[0].w = swap32_lo(tf.w, ts.w); tv[1].w = swap32_hi(tf.w, ts.w);
     }
-    load_v(nrow, cur);
-    btn = bt_entry(t0 + 2 * TSTEP);
+    // ---- softmax of head col over the tile ----
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float x[4][4];
+    float mt = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const float4 kv = *reinterpret_cast<const float4*>(kst + 16 * kb + 4 * g4);
+      const float kk[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x[kb][i] = (float)sacc[kb][i] * kk[i];
+        mt = fmaxf(mt, x[kb][i]);
+      }
+    }
+    if (t0 + DEC_TILE > n1) {  // the split's last tile: keys past it are masked
+      mt = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (t0 + 16 * kb + 4 * g4 + i >= n1) x[kb][i] = -INFINITY;
+          mt = fmaxf(mt, x[kb][i]);
+        }
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    const float mn = fmaxf(m_run, mt * qsl);
+    const float resc = __builtin_amdgcn_exp2f(m_run - mn);  // first tile: exp2(-inf) = 0
+    m_run = mn;
+    float ls = 0.f;
+    uint32_t ph[4][2];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      float p[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        p[i] = __builtin_amdgcn_exp2f(fmaf(x[kb][i], qsl, -mn));  // masked key: -inf -> 0
+        ls += p[i];
+      }
+      ph[kb][0] = (uint32_t)f2h_bits(p[0]) | ((uint32_t)f2h_bits(p[1]) << 16);
+      ph[kb][1] = (uint32_t)f2h_bits(p[2]) | ((uint32_t)f2h_bits(p[3]) << 16);
+    }
+    l_lane = l_lane * resc + ls;
+    if (col < G) {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+        *reinterpret_cast<uint2*>(pt + col * PP + 16 * kb + 4 * g4) = uint2{ph[kb][0], ph[kb][1]};
+    }
+    // rescale the accumulators only when some head's running max moved
+    if (__builtin_amdgcn_ballot_w64(col < G && resc != 1.f)) {
+#pragma unroll
+      for (int t = 0; t < DT; ++t) oacc[t] *= resc;
+    }
+
+    // ---- PV, two 32-key halves ----
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
-      const uint32_t* cc = hf ? c1 : c0;
-      const uint4 tb = hf ? t1v : t0v;
       if (hf) __builtin_amdgcn_wave_barrier();  // half 0's tile reads are done
+      uint32_t cc[HW];
+#pragma unroll
+      for (int w = 0; w < HW / 2; ++w) {
+        cc[2 * w] = cw[hf][w].x;
+        cc[2 * w + 1] = cw[hf][w].y;
+      }
+      load_codes(nrow, hf);
       // dequantise D/2 channels (D/16 groups of 8) of key row kr to LDS
 #pragma unroll
       for (int gi = 0; gi < D / 16; ++gi) {
         const int bit = 24 * gi, w = bit >> 5, sh = bit & 31;
-        const uint32_t x = sh <= 8 ? (cc[w] >> sh)
-                                   : __builtin_amdgcn_alignbit(cc[w + 1], cc[w], sh);
+        const uint32_t xw = sh <= 8 ? (cc[w] >> sh)
+                                    : __builtin_amdgcn_alignbit(cc[w + 1], cc[w], sh);
         const int c16 = kh * (D / 16) + gi;  // 16-byte chunk of the row
         const int off = kr * RB + ((((c16 >> 1) ^ wsw) << 1) | (c16 & 1)) * 16;
-        *reinterpret_cast<uint4*>(reinterpret_cast<char*>(vt) + off) = lm3_lookup8(x, tb);
+        *reinterpret_cast<uint4*>(reinterpret_cast<char*>(vt) + off) = lm3_lookup8(xw, tv[hf]);
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
@@ -1547,17 +1577,15 @@ k8v3_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_scal
     }
     __builtin_amdgcn_wave_barrier();  // the wave's tile region is rewritten next tile
     t0 += TSTEP;
-  };
-  while (t0 < n1) step();
+  }
   __syncthreads();  // every wave is done with the tile region (aliased below)
 
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float lw = wave_sum(l_lane[g]);
-    if (lane == 0) {
-      sm.r.m[wave][g] = m_run[g];
-      sm.r.l[wave][g] = lw;
-    }
+  // head col: l over the 4 lanes of the column
+  l_lane += __shfl_xor(l_lane, 16, 64);
+  l_lane += __shfl_xor(l_lane, 32, 64);
+  if (g4 == 0 && col < G) {
+    sm.r.m[wave][col] = m_run;
+    sm.r.l[wave][col] = l_lane;
   }
   // accumulator lane (g4, col) holds channels 16 t + 4 g4 + i of head col
   if (col < G) {
@@ -1742,6 +1770,8 @@ extern "C" int sl8_attn_paged_decode_k8v3(const int8_t* q, const float* q_scale,
   SL8_CHECK_ARG(q && q_scale && block_table && context_lens && out && v_codebook &&
                     (num_blocks == 0 || (k_cache && k_scale && v_packed && v_norm)),
                 "fni8 paged_decode_k8v3: null pointer");
+  SL8_CHECK_ARG(num_blocks * Hkv * block_size < (1LL << 31),
+                "fni8 paged_decode_k8v3: cache too large (rows must fit in 31 bits)");
   SL8_CHECK_ARG(aligned(q, 4) && aligned(k_cache, 16) && aligned(v_packed, 16),
                 "fni8 paged_decode_k8v3: q must be 4-byte aligned, k_cache/v_packed 16-byte aligned");
   const size_t need = sl8_attn_int8_decode_workspace(B, Hq, D, num_splits);
