@@ -1356,7 +1356,8 @@ k8v3_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_scal
 #pragma unroll
   for (int s = 0; s < KS; ++s)
     qb[s] = col < G ? *reinterpret_cast<const v4i*>(&sm.q[col][16 * s + 4 * g4]) : v4i{0, 0, 0, 0};
-  const float qsl = col < G ? sm.qs[col] : 0.f;
+  // (at least FLT_MIN: a masked key's -inf logit must stay -inf, never 0 * -inf)
+  const float qsl = col < G ? fmaxf(sm.qs[col], 1.17549435e-38f) : 0.f;
 
   const int per = (n_len + n_splits - 1) / n_splits;
   const int n0 = split * per;

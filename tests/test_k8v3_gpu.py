@@ -127,6 +127,31 @@ def test_k8v3_context_above_max_is_clamped(device):
     assert_close_abs(out[:, :, 0], ref40, atol=2e-2, rtol=2e-3, what="k8v3 clamp")
 
 
+def test_k8v3_zero_q_scale_is_the_mean_of_valid_rows(device):
+    """q_scale = 0: every valid key gets p = 1 (the output is the mean of the
+    valid dequantised V rows; keys past the split's end must not leak in)."""
+    case = (2, 8, 4, 128, 16, (37, 70))
+    args = _store(case, device, seed=11)
+    args[1] = torch.zeros_like(args[1])
+    for ns in (1, 3):
+        out = _C.attn_paged_decode_k8v3(*args, 16, 70, ns)
+        assert_finite(out)
+        assert_close_abs(out[:, :, 0], _ref(args, 70, ns), atol=2e-2, rtol=2e-3,
+                         what=f"zero q_scale ns={ns}")
+
+
+@pytest.mark.parametrize("ns", [16, -1])
+def test_k8v3_larger_batch_matches_oracle(device, ns):
+    """Config 3's head layout (Hq 32, Hkv 8) on ragged sequences of a few
+    thousand keys in scattered 16-key blocks."""
+    case = (2, 32, 8, 128, 16, (4096, 3000))
+    args = _store(case, device, seed=12)
+    out = _C.attn_paged_decode_k8v3(*args, 16, 4096, ns)
+    n_splits = ns if ns > 0 else _C.paged_choose_n_splits(4096, 2 * 32)
+    assert_close_abs(out[:, :, 0], _ref(args, 4096, n_splits), atol=2e-2, rtol=2e-3,
+                     what=f"k8v3 larger ns={ns}")
+
+
 def test_k8v3_permuted_blocks_and_deterministic(device):
     """The same logical tokens under two block tables decode bitwise-identically,
     and repeated calls are bitwise-identical (reference test_k8v3_paged_decode.py:181-260)."""
