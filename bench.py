@@ -190,7 +190,7 @@ def bench_paged_decode(iters=20, bs=16):
     return ms, nbytes
 
 
-def bench_paged_decode_k8v3(iters=20, bs=16):
+def bench_paged_decode_k8v3(iters=20, bs=16, D=128):
     """K8V3 paged decode at config 3's shape: int8 K with per-token scales and
     3-bit Lloyd-Max V (packed codes + per-128-channel norms + codebook), 16-key
     blocks scattered by a shuffled block table (reference attn_paged_decode_k8v3)."""
@@ -198,7 +198,7 @@ def bench_paged_decode_k8v3(iters=20, bs=16):
     from superl8_amd.quant.lloydmax import gaussian_codebook
 
     dev = "cuda"
-    B, Hq, Hkv, N, D = 16, 32, 8, 32768, 128
+    B, Hq, Hkv, N = 16, 32, 8, 32768
     g = torch.Generator(device=dev).manual_seed(10)
     nblk = B * N // bs
     kc = torch.randint(-127, 128, (nblk, Hkv, bs, D), device=dev, dtype=torch.int8, generator=g)

@@ -1299,7 +1299,7 @@ __device__ __forceinline__ uint32_t swap32_hi(uint32_t a, uint32_t b) {
 
 template <int D, int G>
 // workgroups per CU: the most that fit without spills
-__global__ void __launch_bounds__(DEC_THREADS, D == 128 ? (G <= 4 ? 3 : 2) : 1)
+__global__ void __launch_bounds__(DEC_THREADS, (D == 128 && G <= 4) ? 3 : 2)
 k8v3_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_scale,
                   const int8_t* __restrict__ k, const float* __restrict__ k_scale,
                   const uint32_t* __restrict__ vpk, const float* __restrict__ vnorm,
