@@ -38,6 +38,9 @@ constexpr int DEC_MAX_SPLITS = 256;
 #define SL8_DEC_PAIR 1
 #endif
 constexpr bool DEC_PAIR = SL8_DEC_PAIR;  // int8-V PV: two keys per v_dot2 (see decode_wave_kernel)
+// query heads (waves) per merge workgroup: one, so config 3's 512 heads spread
+// over all CUs (4 per workgroup measured ~1 us slower per decode call)
+constexpr int CMB_WAVES = 1;
 #ifndef SL8_DEC_PV4
 #define SL8_DEC_PV4 1
 #endif
@@ -280,16 +283,39 @@ decode_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sc
 // split by the lane that loaded m_s and broadcast, and the sums run over the
 // splits in index order (deterministic).
 template <int D>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(CMB_WAVES * 64)
 decode_combine_wave_kernel(const float* __restrict__ o_part, const float* __restrict__ m_part,
                            const float* __restrict__ l_part, uint16_t* __restrict__ out,
                            int n_splits, int bhq) {
   // D = 32: one channel per lane, lanes 32..63 idle
   constexpr int CPL = D >= 64 ? D / 64 : 1;
   const int lane = threadIdx.x & 63;
-  const int64_t hq = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t hq = (int64_t)blockIdx.x * CMB_WAVES + (threadIdx.x >> 6);
   if (hq >= bhq) return;  // wave-uniform
   constexpr int SCH = 16;  // splits whose partials are in flight together
+  const bool act = CPL * lane < D;
+  const float* ob = o_part + hq * D + (act ? CPL * lane : 0);
+  // partial O of splits s0 .. s0 + SCH - 1 (clamped to the last split)
+  auto load_o = [&](int s0, float (&ov)[SCH][CPL]) {
+#pragma unroll
+    for (int i = 0; i < SCH; ++i) {
+      const int sp = min(s0 + i, n_splits - 1);
+      const float* src = ob + (int64_t)sp * bhq * D;
+      if constexpr (CPL == 4) {
+        const float4 v4 = *reinterpret_cast<const float4*>(src);
+        ov[i][0] = v4.x; ov[i][1] = v4.y; ov[i][2] = v4.z; ov[i][3] = v4.w;
+      } else if constexpr (CPL == 2) {
+        const float2 v2 = *reinterpret_cast<const float2*>(src);
+        ov[i][0] = v2.x; ov[i][1] = v2.y;
+      } else {
+        ov[i][0] = *src;
+      }
+    }
+  };
+  // the first SCH splits' O is loaded together with every m and l (one round trip
+  // for n_splits <= SCH)
+  float ov[SCH][CPL];
+  load_o(0, ov);
   // m, l of splits lane, lane + 64, ... (n_splits <= DEC_MAX_SPLITS = 4 x 64)
   float ms[DEC_MAX_SPLITS / 64], ls[DEC_MAX_SPLITS / 64];
   float gm = DEC_NEG_INF;
@@ -314,27 +340,11 @@ decode_combine_wave_kernel(const float* __restrict__ o_part, const float* __rest
   float acc[CPL];
 #pragma unroll
   for (int e = 0; e < CPL; ++e) acc[e] = 0.f;
-  const bool act = CPL * lane < D;
-  const float* ob = o_part + hq * D + (act ? CPL * lane : 0);
   for (int s0 = 0; s0 < n_splits; s0 += SCH) {
+    if (s0) load_o(s0, ov);
     // weights of splits s0 .. s0 + SCH - 1 live in register wt[s0 / 64] of lanes (s0 % 64) ..
     const int c = s0 >> 6;
     const float wc = c == 0 ? wt[0] : (c == 1 ? wt[1] : (c == 2 ? wt[2] : wt[3]));
-    float ov[SCH][CPL];
-#pragma unroll
-    for (int i = 0; i < SCH; ++i) {
-      const int sp = min(s0 + i, n_splits - 1);
-      const float* src = ob + (int64_t)sp * bhq * D;
-      if constexpr (CPL == 4) {
-        const float4 v4 = *reinterpret_cast<const float4*>(src);
-        ov[i][0] = v4.x; ov[i][1] = v4.y; ov[i][2] = v4.z; ov[i][3] = v4.w;
-      } else if constexpr (CPL == 2) {
-        const float2 v2 = *reinterpret_cast<const float2*>(src);
-        ov[i][0] = v2.x; ov[i][1] = v2.y;
-      } else {
-        ov[i][0] = *src;
-      }
-    }
 #pragma unroll
     for (int i = 0; i < SCH; ++i) {
       const int sp = s0 + i;
@@ -353,11 +363,12 @@ decode_combine_wave_kernel(const float* __restrict__ o_part, const float* __rest
 
 template <typename... A>
 void launch_combine(int D, int bhq, hipStream_t st, A... args) {
-  const dim3 g((unsigned)((bhq + 3) / 4));
-  if (D == 32) decode_combine_wave_kernel<32><<<g, 256, 0, st>>>(args...);
-  else if (D == 64) decode_combine_wave_kernel<64><<<g, 256, 0, st>>>(args...);
-  else if (D == 128) decode_combine_wave_kernel<128><<<g, 256, 0, st>>>(args...);
-  else decode_combine_wave_kernel<256><<<g, 256, 0, st>>>(args...);
+  const dim3 g((unsigned)((bhq + CMB_WAVES - 1) / CMB_WAVES));
+  const dim3 b(CMB_WAVES * 64);
+  if (D == 32) decode_combine_wave_kernel<32><<<g, b, 0, st>>>(args...);
+  else if (D == 64) decode_combine_wave_kernel<64><<<g, b, 0, st>>>(args...);
+  else if (D == 128) decode_combine_wave_kernel<128><<<g, b, 0, st>>>(args...);
+  else decode_combine_wave_kernel<256><<<g, b, 0, st>>>(args...);
 }
 
 // ---------------------------------------------------------------------------
