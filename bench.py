@@ -135,7 +135,7 @@ def bench_decode(iters=20, ks16=False):
     return ms, nbytes
 
 
-def bench_decode_kv8(iters=20):
+def bench_decode_kv8(iters=20, ns=16):
     """Decode over an int8 V cache (per-channel scale) at config 3's shape: K and V
     int8 [16, 8, 32768, 128], the row of reference attn_int8_decode_kv8 (survey next)."""
     from superl8_amd import _C
@@ -156,7 +156,7 @@ def bench_decode_kv8(iters=20):
     v_i8, vs = _C.quantize_v_perchannel(v)
     del v
     vs = vs.reshape(B, Hkv, D).contiguous()
-    fn = lambda: _C.attn_int8_decode_kv8(q_i8, qs, k_i8, ks, v_i8, vs, 16)  # noqa: E731
+    fn = lambda: _C.attn_int8_decode_kv8(q_i8, qs, k_i8, ks, v_i8, vs, ns)  # noqa: E731
     spin_up(fn, 0.2)
     ms = _events_time(fn, iters, torch.cuda.current_stream())
     nbytes = k_i8.numel() + ks.numel() * 4 + v_i8.numel() + vs.numel() * 4 + q_i8.numel() \
