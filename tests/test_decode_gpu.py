@@ -178,6 +178,7 @@ PAGED_CASES = [  # B, Hq, Hkv, D, block_size, lens
     (2, 8, 2, 64, 16, (50, 7)), (3, 32, 8, 128, 16, (1000, 1, 333)), (1, 16, 4, 256, 32, (257,)),
     (2, 8, 8, 128, 64, (64, 0)), (4, 12, 4, 64, 8, (9, 100, 31, 64)), (1, 32, 1, 128, 16, (600,)),
     (2, 8, 2, 32, 16, (50, 333)), (1, 16, 4, 32, 32, (257,)),  # head dim 32
+    (2, 8, 2, 128, 12, (100, 37)), (1, 32, 8, 64, 24, (300,)),  # block sizes not powers of two
 ]
 
 

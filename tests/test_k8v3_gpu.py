@@ -18,6 +18,8 @@ CASES = [  # B, Hq, Hkv, D, block_size, lens
     (3, 4, 4, 128, 16, (5, 33, 64)), (3, 4, 4, 256, 16, (5, 33, 64)), (3, 8, 4, 256, 16, (5, 33, 64)),
     (3, 32, 8, 128, 16, (1000, 1, 333)), (2, 16, 2, 128, 32, (257, 64)), (1, 8, 1, 256, 64, (600,)),
     (2, 8, 8, 128, 16, (64, 0)), (4, 12, 4, 128, 8, (9, 100, 31, 64)), (1, 16, 16, 128, 16, (77,)),
+    # block sizes that are not powers of two (the kernel divides instead of shifting)
+    (2, 8, 2, 128, 12, (100, 37)), (1, 32, 8, 256, 24, (300,)), (3, 4, 4, 128, 48, (5, 49, 200)),
 ]
 
 
