@@ -191,7 +191,8 @@ def bench_paged_decode(iters=20, bs=16):
 
 
 def bench_paged_decode_k8v3(iters=20, bs=16, D=128):
-    """K8V3 paged decode at config 3's shape: int8 K with per-token scales and
+    """K8V3 paged decode at config 3's shape (D = 256: the same layout with the
+    head dim of the reference's K8V3 models): int8 K with per-token scales and
     3-bit Lloyd-Max V (packed codes + per-128-channel norms + codebook), 16-key
     blocks scattered by a shuffled block table (reference attn_paged_decode_k8v3)."""
     from superl8_amd import _C
@@ -470,12 +471,12 @@ def main():
         sec["attn_paged_decode_cfg3shape_bs16"] = {"us": round(pms * 1e3, 2), "GB/s": round(gbs, 1),
                                                    "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
                                                    "bytes": pbytes}
-        pms, pbytes = bench_paged_decode_k8v3()
-        gbs = pbytes / (pms * 1e-3) / 1e9
-        sec["attn_paged_decode_k8v3_cfg3shape_bs16"] = {"us": round(pms * 1e3, 2),
-                                                        "GB/s": round(gbs, 1),
-                                                        "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
-                                                        "bytes": pbytes}
+        for dk, key in ((128, "attn_paged_decode_k8v3_cfg3shape_bs16"),
+                        (256, "attn_paged_decode_k8v3_cfg3layout_d256_bs16")):
+            pms, pbytes = bench_paged_decode_k8v3(D=dk)
+            gbs = pbytes / (pms * 1e-3) / 1e9
+            sec[key] = {"us": round(pms * 1e3, 2), "GB/s": round(gbs, 1),
+                        "frac_hbm": round(gbs / PEAK_HBM_GBS, 4), "bytes": pbytes}
         for M in (1, 8):
             gms, gbytes = bench_gemv(M)
             gbs = gbytes / (gms * 1e-3) / 1e9
