@@ -21,14 +21,11 @@
 //     (a 32-bit multiply scales 4 codes at once without carries). Three
 //     MFMAs into T_lo, T_hi, T_hi plus one with m_j broadcast (the min term);
 //     per super-block f += d * (T_lo + 8 T_hi) - dmin * U.
-//   Q6_K on v_mfma_f32_32x32x16_f16, one K = 16 step per sub-block: x (int8)
-//     and (q - 32) * s are small integers, exact in fp16, with sc = 16 s_hi +
-//     s_lo (s_lo in [0,15], s_hi in [-8,7]) so |(q-32) * s| <= 480; the fp32
-//     accumulators T_lo, T_hi stay below 2^24 over a super-block (exact), and
-//     f += d * (T_lo + 16 T_hi).
-// Q6_K super-blocks are 210 bytes, so they start on 2-byte boundaries: each is
-// copied as the 53 dwords from its address rounded down to 4, and read back
-// from LDS with v_alignbyte.
+//   Q6_K on v_mfma_i32_32x32x32_i8 as well, one K = 32 step per pair of
+//     16-element sub-blocks (each lane half holds one sub-block, so one scale
+//     per lane): P = (q - 32) * sc in [-4096, 4064] is split exactly into two
+//     int8 B operands, P = 256 B_hi + B_lo, two MFMAs into T_lo, T_hi, and
+//     f += d * (T_lo + 256 T_hi) per super-block (details at the kernel).
 
 #include "kquant.hpp"
 
@@ -37,17 +34,11 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i_t __attribute__((ext_vector_type(16)));
-typedef float v16f_t __attribute__((ext_vector_type(16)));
-typedef _Float16 v8h_t __attribute__((ext_vector_type(8)));
-typedef _Float16 v2h_t __attribute__((ext_vector_type(2)));
 
 constexpr int Q5K_BYTES = 176;
 constexpr int Q6K_BYTES = 210;
 constexpr int KBM = 128, KBN = 128;                       // output tile
 constexpr int T5CH = (KBN * 11 + 255) / 256 * 256;       // Q5_K weight-tile 16-B chunks
-constexpr int Q6DW = 53;                                  // dwords per staged Q6_K block
-constexpr int Q6PITCH = Q6DW * 4;                         // 212 bytes
-constexpr int T6DW = (KBN * Q6DW + 255) / 256 * 256 + 64; // Q6_K weight-tile dwords (+ read slack)
 
 // x tile copy: 128 rows x 256 int8 of super-block sb; 16-byte chunk c of row r
 // lands at r * 256 + 16 * (c ^ (r & 15)) (rows are one 256-byte bank line).
@@ -60,34 +51,6 @@ __device__ __forceinline__ void copy_x_tile(const int8_t* x, int8_t* xd, int m0,
     const int8_t* src = x + (int64_t)min(m0 + row, M - 1) * K + (int64_t)sb * 256 + 16 * c;
     __builtin_amdgcn_global_load_lds((kq_gptr_t)src, (kq_lptr_t)(xd + (i * 256 + wave * 64) * 16), 16, 0, 0);
   }
-}
-
-// Four bytes b (as two dwords' halves) -> fp16 1024 + b, packed two per dword.
-struct H4x2 {
-  v2h_t p[4];
-};
-__device__ __forceinline__ H4x2 bytes8_to_h1024(uint32_t a, uint32_t b) {
-  H4x2 r;
-  r.p[0] = __builtin_bit_cast(v2h_t, __builtin_amdgcn_perm(0x64646464u, a, 0x04010400u));
-  r.p[1] = __builtin_bit_cast(v2h_t, __builtin_amdgcn_perm(0x64646464u, a, 0x04030402u));
-  r.p[2] = __builtin_bit_cast(v2h_t, __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u));
-  r.p[3] = __builtin_bit_cast(v2h_t, __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u));
-  return r;
-}
-__device__ __forceinline__ v8h_t h4x2_to_v8(const H4x2& h) {
-  uint32_t u[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) u[i] = __builtin_bit_cast(uint32_t, h.p[i]);
-  return __builtin_bit_cast(v8h_t, u);
-}
-
-// 8 int8 -> 8 fp16 (exact): byte u = x + 128 becomes fp16 bits 0x64uu = 1024 + u.
-__device__ __forceinline__ v8h_t i8x8_to_h(uint2 w) {
-  H4x2 h = bytes8_to_h1024(w.x ^ 0x80808080u, w.y ^ 0x80808080u);
-  const v2h_t off = {(_Float16)1152.0f, (_Float16)1152.0f};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) h.p[i] = h.p[i] - off;  // v_pk_add_f16
-  return h4x2_to_v8(h);
 }
 
 // ---------------------------------------------------------------------------
@@ -221,10 +184,57 @@ gemm_q5k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
 // 8 bytes at a 2-byte aligned LDS address (aligned dword reads + v_alignbyte).
 __device__ __forceinline__ uint2 lds8_at(const uint8_t* p) {
   const uintptr_t ad = reinterpret_cast<uintptr_t>(p);
-  const uint32_t* a = reinterpret_cast<const uint32_t*>(ad & ~(uintptr_t)3);
+  const uint32_t* a = reinterpret_cast<const uint32_t*>(p - (ad & 3));  // keeps the LDS address space
   const uint32_t sh = (uint32_t)(ad & 3);
   const uint32_t d0 = a[0], d1 = a[1], d2 = a[2];
   return make_uint2(__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh));
+}
+
+// Q6_K tile GEMM on v_mfma_i32_32x32x32_i8. Wave w owns the 32 weight rows
+// 32 w .. 32 w + 31 (output columns) for all 128 activation rows, so each
+// weight operand is built once per workgroup. One K = 32 step s of a
+// super-block covers elements 32 s .. 32 s + 31 (ql half s / 4, quadrant
+// s % 4); lane half h holds elements 32 s + 16 h .. +15 of its column, which
+// are exactly sub-block i = 2 s + h, so one scale per lane and step. Per
+// element P = (q - 32) * sc_i lies in [-4096, 4064]; P + 128 is formed in
+// packed 16-bit lanes and split exactly as P = 256 B_hi + B_lo with
+// B_hi = (P + 128) >> 8 in [-16, 16] (its high byte) and B_lo in [-128, 127]
+// (its low byte minus 128), both int8 B operands: two MFMAs per step into
+// T_lo, T_hi (|T| < 2^28 over a super-block), then
+// f += d * (float)(T_lo + 256 T_hi) per super-block.
+// Weight staging: row r's block of super-block sb is copied as the 14 aligned
+// 16-byte pieces from its address rounded down to 16 (224 bytes cover the
+// 210-byte block at any even misalignment) to LDS row r * 224; every piece
+// starts before the block's last byte, so no read leaves the 16-byte granule
+// of valid data.
+typedef short v2s_t __attribute__((ext_vector_type(2)));
+#ifndef SL8_Q6T_SCHED
+#define SL8_Q6T_SCHED 1
+#endif
+
+// 16 bytes at a 2-byte aligned LDS address
+__device__ __forceinline__ uint4 lds16_at(const uint8_t* p) {
+  const uintptr_t ad = reinterpret_cast<uintptr_t>(p);
+  const uint32_t* a = reinterpret_cast<const uint32_t*>(p - (ad & 3));  // keeps the LDS address space
+  const uint32_t sh = (uint32_t)(ad & 3);
+  const uint32_t d0 = a[0], d1 = a[1], d2 = a[2], d3 = a[3], d4 = a[4];
+  return make_uint4(__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh),
+                    __builtin_amdgcn_alignbyte(d3, d2, sh), __builtin_amdgcn_alignbyte(d4, d3, sh));
+}
+
+constexpr int Q6P16 = 224;                     // LDS pitch of a staged Q6_K block (14 pieces)
+constexpr int T6W = KBN * Q6P16 / 4 + 16;        // weight-tile dwords (+ read slack)
+
+// 4 six-bit codes (bytes) -> the B_lo and B_hi bytes of (q - 32) * sc;
+// off2 = 128 - 32 sc in both 16-bit lanes
+__device__ __forceinline__ void q6_split4(uint32_t q, v2s_t sc2, v2s_t off2, uint32_t& lo, uint32_t& hi) {
+  // bytes 0, 1 and 2, 3 of q into 16-bit lanes (selector byte 0x0C gives zero)
+  const v2s_t e0 = __builtin_bit_cast(v2s_t, __builtin_amdgcn_perm(0u, q, 0x0C010C00u));
+  const v2s_t e1 = __builtin_bit_cast(v2s_t, __builtin_amdgcn_perm(0u, q, 0x0C030C02u));
+  const v2s_t p0 = e0 * sc2 + off2, p1 = e1 * sc2 + off2;  // P + 128, v_pk_mad_i16, exact
+  const uint32_t u0 = __builtin_bit_cast(uint32_t, p0), u1 = __builtin_bit_cast(uint32_t, p1);
+  lo = __builtin_amdgcn_perm(u1, u0, 0x06040200u) ^ 0x80808080u;  // low bytes - 128
+  hi = __builtin_amdgcn_perm(u1, u0, 0x07050301u);                // high bytes
 }
 
 template <int OUT_DT>
@@ -233,129 +243,115 @@ gemm_q6k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
                      const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K) {
   __shared__ __attribute__((aligned(16))) int8_t xs0[KBM * 256];
   __shared__ __attribute__((aligned(16))) int8_t xs1[KBM * 256];
-  __shared__ __attribute__((aligned(16))) uint32_t ws0[T6DW];
-  __shared__ __attribute__((aligned(16))) uint32_t ws1[T6DW];
+  __shared__ __attribute__((aligned(16))) uint32_t ws0[T6W];
+  __shared__ __attribute__((aligned(16))) uint32_t ws1[T6W];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave & 1, wn = wave >> 1;
   const int l32 = lane & 31, h = lane >> 5;
   const int n0 = blockIdx.x * KBN, m0 = blockIdx.y * KBM;
   const int nsb = K >> 8;
   const int64_t row_bytes = (int64_t)nsb * Q6K_BYTES;
+  const int rmax = min(KBN, N - n0) - 1;
 
-  // staged block of weight row r: LDS bytes r * 212 + (its global address & 3)
+  // piece P = 256 i + tid of the weight tile: row P / 14, piece P % 14 (fixed
+  // per thread); offsets are 32-bit from the workgroup's row-n0 base, which
+  // is 256-byte aligned (n0 of 128, row_bytes even): 128 rows of < 2^24 bytes
+  const uint8_t* wbase = w + (int64_t)n0 * row_bytes;
   auto load = [&](int sb, int8_t* xd, uint32_t* wd) __attribute__((always_inline)) {
     copy_x_tile(x, xd, m0, M, K, sb, tid, wave);
-    // dword P = 256 i + tid of the tile is dword c of row P / 53; walked as a
-    // recurrence (256 = 4 * 53 + 44) so no per-i row address stays live
-    // offsets are 32-bit from the workgroup's (uniform) row-n0 base: 128 rows of
-    // < 2^24 bytes each
-    int t0 = tid;
-    asm volatile("" : "+v"(t0));  // keep the walk inside the super-block loop (no hoisted addresses)
-    int row = t0 / Q6DW, c = t0 - Q6DW * (t0 / Q6DW);
-    const uint8_t* wbase = w + (int64_t)n0 * row_bytes;
-    const uint32_t rb32 = (uint32_t)row_bytes, sboff = (uint32_t)sb * Q6K_BYTES;
-    const int rmax = min(KBN, N - n0) - 1;
-    // bytes from the row-n0 base to the end of the weight buffer: the last
-    // dword of a 4-byte aligned block (its d field plus 2 bytes past the
-    // block) is not read for the buffer's final block; compute() reads that
-    // block's d from global memory instead
-    const uint32_t wend = (uint32_t)(rmax + 1) * rb32;
+    const uint32_t sboff = (uint32_t)sb * Q6K_BYTES;
 #pragma unroll
-    for (int i = 0; i < (T6DW - 64) / 256; ++i) {
-      const uint32_t base = (uint32_t)min(row, rmax) * rb32 + sboff;
-      uint32_t off = (base & ~3u) + 4u * (uint32_t)(row < KBN ? c : Q6DW - 1);
-      off = off + 4u > wend ? off - 4u : off;
-      __builtin_amdgcn_global_load_lds((kq_gptr_t)(wbase + off), (kq_lptr_t)(wd + i * 256 + wave * 64), 4, 0, 0);
-      c += 44;
-      row += 4;
-      if (c >= Q6DW) { c -= Q6DW; ++row; }
+    for (int i = 0; i < KBN * 14 / 256; ++i) {
+      const int P = i * 256 + tid, row = P / 14, c = P - 14 * (P / 14);
+      const uint32_t off = (((uint32_t)min(row, rmax) * (uint32_t)row_bytes + sboff) & ~15u) + 16u * (uint32_t)c;
+      __builtin_amdgcn_global_load_lds((kq_gptr_t)(wbase + off), (kq_lptr_t)(wd + (i * 256 + wave * 64) * 4), 16, 0, 0);
     }
   };
 
-  float f[2][2][16];
+  float f[4][16];
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-    for (int b2 = 0; b2 < 2; ++b2)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) f[a][b2][e] = 0.f;
+    for (int e = 0; e < 16; ++e) f[rb][e] = 0.f;
 
+  const int r = 32 * wave + l32;  // this lane's weight row in the tile
   auto compute = [&](int sb, const int8_t* xt, const uint32_t* wt) __attribute__((always_inline)) {
-    const uint8_t* blk[2];
-    float dcb[2];
-    uint32_t scw[2][4];
+    // the block's misalignment is that of its offset from the row-n0 base
+    const uint32_t base = (uint32_t)min(r, rmax) * (uint32_t)row_bytes + (uint32_t)sb * Q6K_BYTES;
+    const uint8_t* blk = reinterpret_cast<const uint8_t*>(wt) + r * Q6P16 + (int)(base & 15u);
+    const uint4 scv = lds16_at(blk + 192);
+    const float d = h2f((uint16_t)(lds8_at(blk + 208).x & 0xFFFFu));
+    v16i_t tl[4], th[4];
+    // software pipeline over the 8 K steps: step s + 1's A reads and B
+    // operands are formed while step s's 8 MFMAs run (double-buffered
+    // registers; one scheduling region per step, MFMAs interleaved with VALU)
+    uint32_t qv[2][12];  // ql quadrants 0/2, 1/3 and qh of each ql half
+    auto load_q = [&](int hf) __attribute__((always_inline)) {
+      const uint4 qa = lds16_at(blk + 64 * hf + 16 * h);       // quadrants 0, 2
+      const uint4 qb = lds16_at(blk + 64 * hf + 32 + 16 * h);  // quadrants 1, 3
+      const uint4 qc = lds16_at(blk + 128 + 32 * hf + 16 * h);
+      qv[hf][0] = qa.x; qv[hf][1] = qa.y; qv[hf][2] = qa.z; qv[hf][3] = qa.w;
+      qv[hf][4] = qb.x; qv[hf][5] = qb.y; qv[hf][6] = qb.z; qv[hf][7] = qb.w;
+      qv[hf][8] = qc.x; qv[hf][9] = qc.y; qv[hf][10] = qc.z; qv[hf][11] = qc.w;
+    };
+    v4i bl[2], bh[2], A[2][4];
+    auto build = [&](int s, int buf) __attribute__((always_inline)) {
+      const int hf = s >> 2, qd = s & 3, i = 2 * s + h;  // ql half, quadrant, sub-block (scale index)
+      const uint32_t sw = (s >> 1) == 0 ? scv.x : (s >> 1) == 1 ? scv.y : (s >> 1) == 2 ? scv.z : scv.w;
+      const int sc = (int)(int8_t)(sw >> (8 * (i & 3)));
+      const v2s_t sc2 = {(short)sc, (short)sc}, off2 = {(short)(128 - 32 * sc), (short)(128 - 32 * sc)};
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-      const int r = 64 * wn + 32 * cb + l32;
-      // n0 * row_bytes is a multiple of 4 (n0 of 128, row_bytes even): the
-      // block's misalignment is that of its offset from the row-n0 base
-      const uint32_t base = (uint32_t)min(r, min(KBN, N - n0) - 1) * (uint32_t)row_bytes +
-                            (uint32_t)sb * Q6K_BYTES;
-      blk[cb] = reinterpret_cast<const uint8_t*>(wt) + r * Q6PITCH + (int)(base & 3u);
-      const uint2 s0 = lds8_at(blk[cb] + 192), s1 = lds8_at(blk[cb] + 200);
-      scw[cb][0] = s0.x; scw[cb][1] = s0.y; scw[cb][2] = s1.x; scw[cb][3] = s1.y;
-      const bool tail = base + Q6K_BYTES == (uint32_t)min(KBN, N - n0) * (uint32_t)row_bytes &&
-                        (base & 3u) == 0;  // the buffer's last block, 4-byte aligned
-      const uint16_t dbits =
-          tail ? *reinterpret_cast<const uint16_t*>(w + (int64_t)n0 * row_bytes + base + 208)
-               : (uint16_t)(lds8_at(blk[cb] + 208).x & 0xFFFFu);
-      dcb[cb] = h2f(dbits);
-    }
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t ql = qv[hf][4 * (qd & 1) + e];
+        const uint32_t q = ((ql >> (4 * (qd >> 1))) & 0x0F0F0F0Fu) | (((qv[hf][8 + e] >> (2 * qd)) & 0x03030303u) << 4);
+        uint32_t lo, hi;
+        q6_split4(q, sc2, off2, lo, hi);
+        bl[buf][e] = (int)lo;
+        bh[buf][e] = (int)hi;
+      }
+    };
+    auto read_a = [&](int s, int buf) __attribute__((always_inline)) {
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-      v16f_t tl[2], th[2];
+      for (int rb = 0; rb < 4; ++rb) {
+        const int row = 32 * rb + l32;
+        A[buf][rb] = *reinterpret_cast<const v4i*>(xt + row * 256 + 16 * ((2 * s + h) ^ (row & 15)));
+      }
+    };
+    load_q(0);
+    read_a(0, 0);
+    build(0, 0);
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
+    for (int s = 0; s < 8; ++s) {
+      const int c = s & 1;
+#if SL8_Q6T_SCHED
+      __builtin_amdgcn_sched_barrier(0);
+#endif
+      if (s == 1) load_q(1);
+      if (s < 7) read_a(s + 1, c ^ 1);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) tl[rb][e] = th[rb][e] = 0.f;
-#pragma unroll 1
-      for (int gi = 0; gi < 4; ++gi) {
-        const int g = gi >> 1, ih = gi & 1;
-          // lane h feeds elements l = 16 ih + 8 h .. +7 of each quadrant of half g
-          const uint2 qla = lds8_at(blk[cb] + 64 * g + 16 * ih + 8 * h);
-          const uint2 qlb = lds8_at(blk[cb] + 64 * g + 32 + 16 * ih + 8 * h);
-          const uint2 qhc = lds8_at(blk[cb] + 128 + 32 * g + 16 * ih + 8 * h);
-#pragma unroll
-          for (int qd = 0; qd < 4; ++qd) {
-            const int i = 8 * g + 2 * qd + ih;  // sub-block (scale index)
-            const uint2 ql = (qd & 1) ? qlb : qla;
-            const int ns = 4 * (qd >> 1), hs = 2 * qd;
-            const uint32_t c0 = ((ql.x >> ns) & 0x0F0F0F0Fu) | (((qhc.x >> hs) & 0x03030303u) << 4);
-            const uint32_t c1 = ((ql.y >> ns) & 0x0F0F0F0Fu) | (((qhc.y >> hs) & 0x03030303u) << 4);
-            H4x2 v = bytes8_to_h1024(c0, c1);  // 1024 + q
-            // scales 4(i>>2).. (both words read first, then a value select on
-            // the loop's g: a select of the two array elements themselves
-            // kept scw in scratch memory)
-            const uint32_t sw_lo = scw[cb][qd >> 1], sw_hi = scw[cb][2 + (qd >> 1)];
-            const uint32_t sw = g ? sw_hi : sw_lo;
-            const int sc = (int)(int8_t)((sw >> (8 * (2 * (qd & 1) + ih))) & 0xFF);
-            const _Float16 slo = (_Float16)(float)(sc & 15), shi = (_Float16)(float)(sc >> 4);
-            const v2h_t slo2 = {slo, slo}, shi2 = {shi, shi};
-            const v2h_t off = {(_Float16)1056.0f, (_Float16)1056.0f};
-            H4x2 lo, hi;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-              const v2h_t q = v.p[k] - off;  // q - 32, exact
-              lo.p[k] = q * slo2;            // v_pk_mul_f16, exact (|.| <= 480)
-              hi.p[k] = q * shi2;
-            }
-            const v8h_t blo = h4x2_to_v8(lo), bhi = h4x2_to_v8(hi);
-#pragma unroll
-            for (int rb = 0; rb < 2; ++rb) {
-              const int row = 64 * wm + 32 * rb + l32;
-              const v8h_t A = i8x8_to_h(
-                  *reinterpret_cast<const uint2*>(xt + row * 256 + 16 * (i ^ (row & 15)) + 8 * h));
-              tl[rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, blo, tl[rb], 0, 0, 0);
-              th[rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, bhi, th[rb], 0, 0, 0);
-            }
-          }
+      for (int rb = 0; rb < 4; ++rb) {
+        if (s == 0) {
+          tl[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bl[c], v16i_t{}, 0, 0, 0);
+          th[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bh[c], v16i_t{}, 0, 0, 0);
+        } else {
+          tl[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bl[c], tl[rb], 0, 0, 0);
+          th[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bh[c], th[rb], 0, 0, 0);
         }
+      }
+      if (s < 7) build(s + 1, c ^ 1);
+#if SL8_Q6T_SCHED
+      __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);  // the LDS reads first
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) f[rb][cb][e] += dcb[cb] * (tl[rb][e] + 16.f * th[rb][e]);
+      for (int k = 0; k < 8; ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // 6 VALU
+      }
+#endif
     }
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) f[rb][e] += d * (float)(tl[rb][e] + 256 * th[rb][e]);
   };
 
   load(0, xs0, ws0);
@@ -374,19 +370,13 @@ gemm_q6k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
   }
   if (sb < nsb) compute(sb, xs0, ws0);
 
+  const int n = n0 + r;
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
+  for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const int m = m0 + 64 * wm + 32 * rb + 8 * (e >> 2) + 4 * h + (e & 3);
-      if (m < M) {
-        const float xsm = x_scale[m];
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-          const int n = n0 + 64 * wn + 32 * cb + l32;
-          if (n < N) st_out<OUT_DT>(out, (int64_t)m * N + n, f[rb][cb][e] * xsm);
-        }
-      }
+      const int m = m0 + 32 * rb + 8 * (e >> 2) + 4 * h + (e & 3);
+      if (m < M && n < N) st_out<OUT_DT>(out, (int64_t)m * N + n, f[rb][e] * x_scale[m]);
     }
 }
 
@@ -446,7 +436,7 @@ typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));
 // 8 dwords starting at a 2-byte aligned global address (9 aligned dwords + v_alignbyte)
 __device__ __forceinline__ void load8_a2(const uint8_t* p, uint32_t (&o)[8]) {
   const uintptr_t ad = reinterpret_cast<uintptr_t>(p);
-  const uint32_t* a = reinterpret_cast<const uint32_t*>(ad & ~(uintptr_t)3);
+  const uint32_t* a = reinterpret_cast<const uint32_t*>(p - (ad & 3));  // keeps the global address space
   const uint32_t sh = (uint32_t)(ad & 3);
   const u32x4a d0 = *reinterpret_cast<const u32x4a*>(a);
   const u32x4a d1 = *reinterpret_cast<const u32x4a*>(a + 4);
@@ -503,7 +493,7 @@ __device__ __forceinline__ void unit_codes(const uint8_t* blk, int g, UnitCodes<
   load8_a2(blk + 64 * hf + 32 * p, ql);
   load8_a2(blk + 128 + 32 * hf, qh);
   const uintptr_t sa = reinterpret_cast<uintptr_t>(blk + 192 + 8 * hf);
-  const uint32_t* sp = reinterpret_cast<const uint32_t*>(sa & ~(uintptr_t)3);
+  const uint32_t* sp = reinterpret_cast<const uint32_t*>(blk + 192 + 8 * hf - (sa & 3));
   const uint32_t ssh = (uint32_t)(sa & 3);
   const uint32_t s0w = __builtin_amdgcn_alignbyte(sp[1], sp[0], ssh);  // scales 8hf + 0..3
   // (sp[2] only when the scales are misaligned: for an aligned block it lies
