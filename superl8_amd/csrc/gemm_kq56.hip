@@ -11,7 +11,8 @@
 // x is the per-row int8 activation with its fp32 scale.
 //
 // Tile GEMM (M > 16; the decode GEMV below serves M <= 16): a 128 x 128 output tile per workgroup,
-// 4 waves of 64 x 64 (2 x 2 blocks of 32 x 32), the x tile and the 128 weight
+// each of the 4 waves owning 32 output columns x all 128 rows (4 blocks of
+// 32 x 32, so each B operand is built once), the x tile and the 128 weight
 // super-blocks copied global -> LDS one super-block ahead (double-buffered).
 // The integer dot products stay exact:
 //   Q5_K on v_mfma_i32_32x32x32_i8, one K = 32 step per sub-block: with
@@ -66,7 +67,6 @@ gemm_q5k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
   __shared__ __attribute__((aligned(16))) uint8_t ws1[T5CH * 16];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave & 1, wn = wave >> 1;
   const int l32 = lane & 31, h = lane >> 5;
   const int n0 = blockIdx.x * KBN, m0 = blockIdx.y * KBM;
   const int nsb = K >> 8;
@@ -82,68 +82,87 @@ gemm_q5k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
     }
   };
 
-  float f[2][2][16];
+  // wave w owns weight rows 32 w .. 32 w + 31 (output columns) for all 128
+  // activation rows (4 row blocks), so each B operand is built once per
+  // workgroup; step j + 1's A reads and B operands are formed while step j's
+  // 16 MFMAs run (one scheduling region per step)
+  float f[4][16];
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-    for (int b2 = 0; b2 < 2; ++b2)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) f[a][b2][e] = 0.f;
+    for (int e = 0; e < 16; ++e) f[rb][e] = 0.f;
 
   auto compute = [&](const int8_t* xt, const uint8_t* wt) __attribute__((always_inline)) {
+    const uint8_t* wr = wt + (32 * wave + l32) * Q5K_BYTES;
+    const uint4 hd = *reinterpret_cast<const uint4*>(wr);
+    const float d = h2f(hd.x & 0xFFFFu), dmin = h2f(hd.x >> 16);
+    const ScMin sm = unpack_scmin(hd.y, hd.z, hd.w);
+    const uint4 qhv = *reinterpret_cast<const uint4*>(wr + 16 + 16 * h);  // qh of l = 16h..16h+15
+    const uint32_t qh[4] = {qhv.x, qhv.y, qhv.z, qhv.w};
+    uint32_t qw[4][4];
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-      const uint8_t* wr = wt + (64 * wn + 32 * cb + l32) * Q5K_BYTES;
-      const uint4 hd = *reinterpret_cast<const uint4*>(wr);
-      const float d = h2f(hd.x & 0xFFFFu), dmin = h2f(hd.x >> 16);
-      const ScMin sm = unpack_scmin(hd.y, hd.z, hd.w);
-      const uint4 qhv = *reinterpret_cast<const uint4*>(wr + 16 + 16 * h);  // qh of l = 16h..16h+15
-      const uint32_t qh[4] = {qhv.x, qhv.y, qhv.z, qhv.w};
-      v16i_t tl[2], th[2], tu[2];
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) tl[rb][e] = th[rb][e] = tu[rb][e] = 0;
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const uint4 qv = *reinterpret_cast<const uint4*>(wr + 48 + 32 * g + 16 * h);
-        const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
-#pragma unroll
-        for (int hi = 0; hi < 2; ++hi) {
-          const int j = 2 * g + hi;
-          const uint32_t scw = j < 4 ? sm.sc_lo : sm.sc_hi, mnw = j < 4 ? sm.mn_lo : sm.mn_hi;
-          const uint32_t sc = (scw >> (8 * (j & 3))) & 0xFF, mn = (mnw >> (8 * (j & 3))) & 0xFF;
-          // q = n + 16 b (n the nibble, b the 5th bit): q * sc = n (sc & 7) +
-          // 8 (n (sc >> 3) + 2 b sc); every B byte <= 126
-          v4i bl, bh, bb;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t nib = (qw[e] >> (4 * hi)) & 0x0F0F0F0Fu;
-            const uint32_t hb = (qh[e] >> j) & 0x01010101u;
-            bl[e] = (int)mul_bytes(nib, sc & 7);  // <= 15 * 7, 15 * 7 and 1 * 126 per byte
-            bh[e] = (int)mul_bytes(nib, sc >> 3);
-            bb[e] = (int)mul_bytes(hb, 2 * sc);
-          }
-          const int bmv = (int)__builtin_amdgcn_perm(0u, mn, 0u);  // byte 0 of mn in all four bytes
-          const v4i bm = {bmv, bmv, bmv, bmv};
-#pragma unroll
-          for (int rb = 0; rb < 2; ++rb) {
-            // A: rows 64 wm + 32 rb + l32, elements 32 j + 16 h .. +15
-            const int row = 64 * wm + 32 * rb + l32;
-            const v4i A = *reinterpret_cast<const v4i*>(xt + row * 256 + 16 * ((2 * j + h) ^ (row & 15)));
-            tl[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, bl, tl[rb], 0, 0, 0);
-            th[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, bh, th[rb], 0, 0, 0);
-            th[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, bb, th[rb], 0, 0, 0);
-            tu[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, bm, tu[rb], 0, 0, 0);
-          }
-        }
-      }
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-        for (int e = 0; e < 16; ++e)
-          f[rb][cb][e] += d * (float)(tl[rb][e] + 8 * th[rb][e]) - dmin * (float)tu[rb][e];
+    for (int g = 0; g < 4; ++g) {
+      const uint4 qv = *reinterpret_cast<const uint4*>(wr + 48 + 32 * g + 16 * h);
+      qw[g][0] = qv.x; qw[g][1] = qv.y; qw[g][2] = qv.z; qw[g][3] = qv.w;
     }
+    v4i A[2][4], bl[2], bh[2], bb[2], bm[2];
+    auto read_a = [&](int j, int buf) __attribute__((always_inline)) {
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) {
+        const int row = 32 * rb + l32;
+        A[buf][rb] = *reinterpret_cast<const v4i*>(xt + row * 256 + 16 * ((2 * j + h) ^ (row & 15)));
+      }
+    };
+    auto build = [&](int j, int buf) __attribute__((always_inline)) {
+      const uint32_t scw = j < 4 ? sm.sc_lo : sm.sc_hi, mnw = j < 4 ? sm.mn_lo : sm.mn_hi;
+      const uint32_t sc = (scw >> (8 * (j & 3))) & 0xFF, mn = (mnw >> (8 * (j & 3))) & 0xFF;
+      // q = n + 16 b (n the nibble, b the 5th bit): q * sc = n (sc & 7) +
+      // 8 (n (sc >> 3) + 2 b sc); every B byte <= 126
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t nib = (qw[j >> 1][e] >> (4 * (j & 1))) & 0x0F0F0F0Fu;
+        const uint32_t hb = (qh[e] >> j) & 0x01010101u;
+        bl[buf][e] = (int)mul_bytes(nib, sc & 7);  // <= 15 * 7, 15 * 7 and 1 * 126 per byte
+        bh[buf][e] = (int)mul_bytes(nib, sc >> 3);
+        bb[buf][e] = (int)mul_bytes(hb, 2 * sc);
+      }
+      const int bmv = (int)__builtin_amdgcn_perm(0u, mn, 0u);  // byte 0 of mn in all four bytes
+      bm[buf] = v4i{bmv, bmv, bmv, bmv};
+    };
+    v16i_t tl[4], th[4], tu[4];
+    read_a(0, 0);
+    build(0, 0);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int c = j & 1;
+      __builtin_amdgcn_sched_barrier(0);
+      if (j < 7) read_a(j + 1, c ^ 1);
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb) {
+        if (j == 0) {
+          tl[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bl[c], v16i_t{}, 0, 0, 0);
+          th[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bh[c], v16i_t{}, 0, 0, 0);
+          tu[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bm[c], v16i_t{}, 0, 0, 0);
+        } else {
+          tl[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bl[c], tl[rb], 0, 0, 0);
+          th[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bh[c], th[rb], 0, 0, 0);
+          tu[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bm[c], tu[rb], 0, 0, 0);
+        }
+        th[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bb[c], th[rb], 0, 0, 0);
+      }
+      if (j < 7) build(j + 1, c ^ 1);
+      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // the LDS reads first
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // 3 VALU
+      }
+    }
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        f[rb][e] += d * (float)(tl[rb][e] + 8 * th[rb][e]) - dmin * (float)tu[rb][e];
   };
 
   load(0, xs0, ws0);
@@ -162,19 +181,13 @@ gemm_q5k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
   }
   if (sb < nsb) compute(xs0, ws0);
 
+  const int n = n0 + 32 * wave + l32;
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
+  for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const int m = m0 + 64 * wm + 32 * rb + 8 * (e >> 2) + 4 * h + (e & 3);
-      if (m < M) {
-        const float xsm = x_scale[m];
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-          const int n = n0 + 64 * wn + 32 * cb + l32;
-          if (n < N) st_out<OUT_DT>(out, (int64_t)m * N + n, f[rb][cb][e] * xsm);
-        }
-      }
+      const int m = m0 + 32 * rb + 8 * (e >> 2) + 4 * h + (e & 3);
+      if (m < M && n < N) st_out<OUT_DT>(out, (int64_t)m * N + n, f[rb][e] * x_scale[m]);
     }
 }
 

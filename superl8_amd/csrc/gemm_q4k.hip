@@ -542,7 +542,8 @@ gemv_q4k_small_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_
 // ---------------------------------------------------------------------------
 // Tiled Q4_K GEMM for M > 16 (prefill; reference csrc/include/gemm_q4k_dp4a.cuh:
 // 60-199, csrc/kernel/gemm_dp4a.cu:146-193): a 128 x 128 output tile per
-// workgroup, 4 waves of 64 x 64 (2 x 2 blocks of 32 x 32). Per super-block the
+// workgroup, each of the 4 waves owning 32 output columns x all 128 rows (4
+// blocks of 32 x 32, so each B operand is built once). Per super-block the
 // x tile (128 x 256 int8) and the 128 weight super-blocks (144 B each) are
 // copied global -> LDS one super-block ahead (double-buffered). The products
 // stay exact integers on v_mfma_i32_32x32x32_i8, one MFMA per 32-element
