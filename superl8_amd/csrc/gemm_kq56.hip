@@ -57,10 +57,11 @@ __device__ __forceinline__ void copy_x_tile(const int8_t* x, int8_t* xd, int m0,
 // ---------------------------------------------------------------------------
 // Q5_K tile GEMM
 // ---------------------------------------------------------------------------
-template <int OUT_DT>
+template <int OUT_DT, int RB>
 __global__ void __launch_bounds__(256, 1)
 gemm_q5k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
-                     const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K) {
+                     const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K,
+                     int nt_x, int tile0) {
   __shared__ __attribute__((aligned(16))) int8_t xs0[KBM * 256];
   __shared__ __attribute__((aligned(16))) int8_t xs1[KBM * 256];
   __shared__ __attribute__((aligned(16))) uint8_t ws0[T5CH * 16];
@@ -68,7 +69,12 @@ gemm_q5k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, h = lane >> 5;
-  const int n0 = blockIdx.x * KBN, m0 = blockIdx.y * KBM;
+  // RB = 4: one 128 x 128 tile per workgroup (tiles tile0, tile0 + 1, ...);
+  // RB = 1: the quarter blockIdx.x & 3 (32 rows) of tile tile0 + blockIdx.x / 4,
+  // so a short last round of tiles spreads over 4x the workgroups
+  const int tile = tile0 + (RB == 4 ? (int)blockIdx.x : (int)(blockIdx.x >> 2));
+  const int n0 = (tile % nt_x) * KBN, m0 = (tile / nt_x) * KBM;
+  const int rb0 = RB == 4 ? 0 : (int)(blockIdx.x & 3);
   const int nsb = K >> 8;
   const int64_t row_bytes = (int64_t)nsb * Q5K_BYTES;
 
@@ -88,7 +94,7 @@ gemm_q5k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
   // 16 MFMAs run (one scheduling region per step)
   float f[4][16];
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb)
+  for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int e = 0; e < 16; ++e) f[rb][e] = 0.f;
 
@@ -108,8 +114,8 @@ gemm_q5k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
     v4i A[2][4], bl[2], bh[2], bb[2], bm[2];
     auto read_a = [&](int j, int buf) __attribute__((always_inline)) {
 #pragma unroll
-      for (int rb = 0; rb < 4; ++rb) {
-        const int row = 32 * rb + l32;
+      for (int rb = 0; rb < RB; ++rb) {
+        const int row = 32 * (rb + rb0) + l32;
         A[buf][rb] = *reinterpret_cast<const v4i*>(xt + row * 256 + 16 * ((2 * j + h) ^ (row & 15)));
       }
     };
@@ -138,7 +144,7 @@ gemm_q5k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
       __builtin_amdgcn_sched_barrier(0);
       if (j < 7) read_a(j + 1, c ^ 1);
 #pragma unroll
-      for (int rb = 0; rb < 4; ++rb) {
+      for (int rb = 0; rb < RB; ++rb) {
         if (j == 0) {
           tl[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bl[c], v16i_t{}, 0, 0, 0);
           th[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bh[c], v16i_t{}, 0, 0, 0);
@@ -159,7 +165,7 @@ gemm_q5k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
       }
     }
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
+    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
       for (int e = 0; e < 16; ++e)
         f[rb][e] += d * (float)(tl[rb][e] + 8 * th[rb][e]) - dmin * (float)tu[rb][e];
@@ -183,10 +189,10 @@ gemm_q5k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
 
   const int n = n0 + 32 * wave + l32;
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb)
+  for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const int m = m0 + 32 * rb + 8 * (e >> 2) + 4 * h + (e & 3);
+      const int m = m0 + 32 * (rb + rb0) + 8 * (e >> 2) + 4 * h + (e & 3);
       if (m < M && n < N) st_out<OUT_DT>(out, (int64_t)m * N + n, f[rb][e] * x_scale[m]);
     }
 }
@@ -250,10 +256,11 @@ __device__ __forceinline__ void q6_split4(uint32_t q, v2s_t sc2, v2s_t off2, uin
   hi = __builtin_amdgcn_perm(u1, u0, 0x07050301u);                // high bytes
 }
 
-template <int OUT_DT>
+template <int OUT_DT, int RB>
 __global__ void __launch_bounds__(256, 1)
 gemm_q6k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
-                     const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K) {
+                     const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K,
+                     int nt_x, int tile0) {
   __shared__ __attribute__((aligned(16))) int8_t xs0[KBM * 256];
   __shared__ __attribute__((aligned(16))) int8_t xs1[KBM * 256];
   __shared__ __attribute__((aligned(16))) uint32_t ws0[T6W];
@@ -261,7 +268,12 @@ gemm_q6k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, h = lane >> 5;
-  const int n0 = blockIdx.x * KBN, m0 = blockIdx.y * KBM;
+  // RB = 4: one 128 x 128 tile per workgroup (tiles tile0, tile0 + 1, ...);
+  // RB = 1: the quarter blockIdx.x & 3 (32 rows) of tile tile0 + blockIdx.x / 4,
+  // so a short last round of tiles spreads over 4x the workgroups
+  const int tile = tile0 + (RB == 4 ? (int)blockIdx.x : (int)(blockIdx.x >> 2));
+  const int n0 = (tile % nt_x) * KBN, m0 = (tile / nt_x) * KBM;
+  const int rb0 = RB == 4 ? 0 : (int)(blockIdx.x & 3);
   const int nsb = K >> 8;
   const int64_t row_bytes = (int64_t)nsb * Q6K_BYTES;
   const int rmax = min(KBN, N - n0) - 1;
@@ -283,7 +295,7 @@ gemm_q6k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
 
   float f[4][16];
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb)
+  for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int e = 0; e < 16; ++e) f[rb][e] = 0.f;
 
@@ -325,8 +337,8 @@ gemm_q6k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
     };
     auto read_a = [&](int s, int buf) __attribute__((always_inline)) {
 #pragma unroll
-      for (int rb = 0; rb < 4; ++rb) {
-        const int row = 32 * rb + l32;
+      for (int rb = 0; rb < RB; ++rb) {
+        const int row = 32 * (rb + rb0) + l32;
         A[buf][rb] = *reinterpret_cast<const v4i*>(xt + row * 256 + 16 * ((2 * s + h) ^ (row & 15)));
       }
     };
@@ -342,7 +354,7 @@ gemm_q6k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
       if (s == 1) load_q(1);
       if (s < 7) read_a(s + 1, c ^ 1);
 #pragma unroll
-      for (int rb = 0; rb < 4; ++rb) {
+      for (int rb = 0; rb < RB; ++rb) {
         if (s == 0) {
           tl[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bl[c], v16i_t{}, 0, 0, 0);
           th[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bh[c], v16i_t{}, 0, 0, 0);
@@ -362,7 +374,7 @@ gemm_q6k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
 #endif
     }
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
+    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
       for (int e = 0; e < 16; ++e) f[rb][e] += d * (float)(tl[rb][e] + 256 * th[rb][e]);
   };
@@ -385,10 +397,10 @@ gemm_q6k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
 
   const int n = n0 + r;
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb)
+  for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const int m = m0 + 32 * rb + 8 * (e >> 2) + 4 * h + (e & 3);
+      const int m = m0 + 32 * (rb + rb0) + 8 * (e >> 2) + 4 * h + (e & 3);
       if (m < M && n < N) st_out<OUT_DT>(out, (int64_t)m * N + n, f[rb][e] * x_scale[m]);
     }
 }
@@ -920,15 +932,24 @@ void launch_gemv_kq(const int8_t* x, const float* xs, const uint8_t* w, void* ou
 template <int FMT>
 void launch_kq_tile(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
                     int M, int N, int K, hipStream_t st) {
-  const dim3 grid((unsigned)((N + KBN - 1) / KBN), (unsigned)((M + KBM - 1) / KBM));
-#define SL8_KQT(KERN)                                                                          \
-  switch (odt) {                                                                               \
-    case SL8_DTYPE_F16: KERN<SL8_DTYPE_F16><<<grid, 256, 0, st>>>(x, xs, w, out, M, N, K); break; \
-    case SL8_DTYPE_BF16: KERN<SL8_DTYPE_BF16><<<grid, 256, 0, st>>>(x, xs, w, out, M, N, K); break; \
-    default: KERN<SL8_DTYPE_F32><<<grid, 256, 0, st>>>(x, xs, w, out, M, N, K); break;        \
+  // one workgroup per 128 x 128 tile; when the last round of tiles would hold
+  // at most half the CUs, those tiles run as 4 row quarters each (a second
+  // launch), which shortens that round (same per-element arithmetic)
+  const int ntx = (N + KBN - 1) / KBN, T = ntx * ((M + KBM - 1) / KBM), P = cu_count();
+  const int rem = T % P, nfull = (T >= P && rem > 0 && rem <= P / 2) ? T - rem : T;
+#define SL8_KQT(KERN, RB, G, T0)                                                                   \
+  switch (odt) {                                                                                   \
+    case SL8_DTYPE_F16: KERN<SL8_DTYPE_F16, RB><<<G, 256, 0, st>>>(x, xs, w, out, M, N, K, ntx, T0); break; \
+    case SL8_DTYPE_BF16: KERN<SL8_DTYPE_BF16, RB><<<G, 256, 0, st>>>(x, xs, w, out, M, N, K, ntx, T0); break; \
+    default: KERN<SL8_DTYPE_F32, RB><<<G, 256, 0, st>>>(x, xs, w, out, M, N, K, ntx, T0); break;        \
   }
-  if (FMT == 5) { SL8_KQT(gemm_q5k_tile_kernel) }
-  else { SL8_KQT(gemm_q6k_tile_kernel) }
+  if (FMT == 5) {
+    SL8_KQT(gemm_q5k_tile_kernel, 4, nfull, 0)
+    if (nfull < T) SL8_KQT(gemm_q5k_tile_kernel, 1, 4 * (T - nfull), nfull)
+  } else {
+    SL8_KQT(gemm_q6k_tile_kernel, 4, nfull, 0)
+    if (nfull < T) SL8_KQT(gemm_q6k_tile_kernel, 1, 4 * (T - nfull), nfull)
+  }
 #undef SL8_KQT
 }
 
@@ -944,7 +965,7 @@ int check_kq(const char* name, const int8_t* x, const float* xs, const uint8_t* 
   SL8_CHECK_ARG(x && xs && w && out, "%s: null pointer", name);
   SL8_CHECK_ARG(aligned(x, 16), "x must be 16-byte aligned for the vectorized int4 loads");
   SL8_CHECK_ARG(aligned(w, 16), "%s: weight must be 16-byte aligned", name);
-  SL8_CHECK_ARG((M + KBM - 1) / KBM < 65536, "%s: M too large", name);
+  SL8_CHECK_ARG((M + KBM - 1) / KBM * ((N + KBN - 1) / KBN) < (1LL << 28), "%s: M*N too large", name);
   return SL8_OK;
 }
 

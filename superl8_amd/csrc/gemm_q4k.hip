@@ -560,10 +560,11 @@ gemv_q4k_small_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_
 constexpr int TBM = 128, TBN = 128;  // output tile
 constexpr int TWCH = (TBN * 9 + 255) / 256 * 256;  // weight-tile 16-B chunks, padded to whole copies
 
-template <int OUT_DT>
+template <int OUT_DT, int RB>
 __global__ void __launch_bounds__(256, 1)
 gemm_q4k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
-                     const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K) {
+                     const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K,
+                     int nt_x, int tile0) {
   __shared__ __attribute__((aligned(16))) int8_t xs0[TBM * 256];
   __shared__ __attribute__((aligned(16))) int8_t xs1[TBM * 256];
   __shared__ __attribute__((aligned(16))) uint8_t ws0[TWCH * 16];
@@ -571,7 +572,12 @@ gemm_q4k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, h = lane >> 5;
-  const int n0 = blockIdx.x * TBN, m0 = blockIdx.y * TBM;
+  // RB = 4: one 128 x 128 tile per workgroup (tiles tile0, tile0 + 1, ...);
+  // RB = 1: the quarter blockIdx.x & 3 (32 rows) of tile tile0 + blockIdx.x / 4,
+  // so a short last round of tiles spreads over 4x the workgroups
+  const int tile = tile0 + (RB == 4 ? (int)blockIdx.x : (int)(blockIdx.x >> 2));
+  const int n0 = (tile % nt_x) * TBN, m0 = (tile / nt_x) * TBM;
+  const int rb0 = RB == 4 ? 0 : (int)(blockIdx.x & 3);
   const int nsb = K >> 8;
   const int64_t row_bytes = (int64_t)nsb * Q4K_BYTES;
 
@@ -600,7 +606,7 @@ gemm_q4k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
   // while step j's 12 MFMAs run (one scheduling region per step).
   float f[4][16];
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb)
+  for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int e = 0; e < 16; ++e) f[rb][e] = 0.f;
 
@@ -618,8 +624,8 @@ gemm_q4k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
     v4i A[2][4], bl[2], bh[2], bm[2];
     auto read_a = [&](int j, int buf) __attribute__((always_inline)) {
 #pragma unroll
-      for (int rb = 0; rb < 4; ++rb) {
-        const int row = 32 * rb + l32;
+      for (int rb = 0; rb < RB; ++rb) {
+        const int row = 32 * (rb + rb0) + l32;
         A[buf][rb] = *reinterpret_cast<const v4i*>(xt + row * 256 + 16 * ((2 * j + h) ^ (row & 15)));
       }
     };
@@ -644,7 +650,7 @@ gemm_q4k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
       __builtin_amdgcn_sched_barrier(0);
       if (j < 7) read_a(j + 1, c ^ 1);
 #pragma unroll
-      for (int rb = 0; rb < 4; ++rb) {
+      for (int rb = 0; rb < RB; ++rb) {
         if (j == 0) {
           tl[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bl[c], v16i_t{}, 0, 0, 0);
           th[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bh[c], v16i_t{}, 0, 0, 0);
@@ -664,7 +670,7 @@ gemm_q4k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
       }
     }
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
+    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
       for (int e = 0; e < 16; ++e)
         f[rb][e] += d * (float)(tl[rb][e] + (th[rb][e] << 3)) - dmin * (float)tu[rb][e];
@@ -688,22 +694,30 @@ gemm_q4k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
 
   const int n = n0 + 32 * wave + l32;
 #pragma unroll
-  for (int rb = 0; rb < 4; ++rb)
+  for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const int m = m0 + 32 * rb + 8 * (e >> 2) + 4 * h + (e & 3);
+      const int m = m0 + 32 * (rb + rb0) + 8 * (e >> 2) + 4 * h + (e & 3);
       if (m < M && n < N) st_out<OUT_DT>(out, (int64_t)m * N + n, f[rb][e] * x_scale[m]);
     }
 }
 
 void launch_gemm_tile(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
                       int M, int N, int K, hipStream_t st) {
-  const dim3 grid((unsigned)((N + TBN - 1) / TBN), (unsigned)((M + TBM - 1) / TBM));
-  switch (odt) {
-    case SL8_DTYPE_F16: gemm_q4k_tile_kernel<SL8_DTYPE_F16><<<grid, 256, 0, st>>>(x, xs, w, out, M, N, K); break;
-    case SL8_DTYPE_BF16: gemm_q4k_tile_kernel<SL8_DTYPE_BF16><<<grid, 256, 0, st>>>(x, xs, w, out, M, N, K); break;
-    default: gemm_q4k_tile_kernel<SL8_DTYPE_F32><<<grid, 256, 0, st>>>(x, xs, w, out, M, N, K); break;
+  // one workgroup per 128 x 128 tile; when the last round of tiles would hold
+  // at most half the CUs, those tiles run as 4 row quarters each (a second
+  // launch), which shortens that round (same per-element arithmetic)
+  const int ntx = (N + TBN - 1) / TBN, T = ntx * ((M + TBM - 1) / TBM), P = cu_count();
+  const int rem = T % P, nfull = (T >= P && rem > 0 && rem <= P / 2) ? T - rem : T;
+#define SL8_Q4T(RB, G, T0)                                                                                  \
+  switch (odt) {                                                                                            \
+    case SL8_DTYPE_F16: gemm_q4k_tile_kernel<SL8_DTYPE_F16, RB><<<G, 256, 0, st>>>(x, xs, w, out, M, N, K, ntx, T0); break; \
+    case SL8_DTYPE_BF16: gemm_q4k_tile_kernel<SL8_DTYPE_BF16, RB><<<G, 256, 0, st>>>(x, xs, w, out, M, N, K, ntx, T0); break; \
+    default: gemm_q4k_tile_kernel<SL8_DTYPE_F32, RB><<<G, 256, 0, st>>>(x, xs, w, out, M, N, K, ntx, T0); break;        \
   }
+  SL8_Q4T(4, nfull, 0)
+  if (nfull < T) SL8_Q4T(1, 4 * (T - nfull), nfull)
+#undef SL8_Q4T
 }
 
 __global__ void dequant_q4k_kernel(const uint8_t* __restrict__ w, float* __restrict__ out,
@@ -879,7 +893,7 @@ extern "C" int sl8_gemm_q4k(const int8_t* x, const float* x_scale, const uint8_t
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int esz = out_dtype == SL8_DTYPE_F32 ? 4 : 2;
   if (M > 16) {
-    SL8_CHECK_ARG(M < (1LL << 31) / 1 && (M + TBM - 1) / TBM < 65536, "gemm_q4k: M too large");
+    SL8_CHECK_ARG(M < (1LL << 31) && (M + TBM - 1) / TBM * ((N + TBN - 1) / TBN) < (1LL << 28), "gemm_q4k: M*N too large");
     launch_gemm_tile(x, x_scale, w, out, out_dtype, (int)M, (int)N, (int)K, st);
     SL8_CHECK_LAUNCH("gemm_q4k");
     return SL8_OK;

@@ -61,6 +61,23 @@ def test_tile_gemm_matches_exact_sum(device, fmt, M, N, K, odt):
     _check_exact_sum(y, FMT[fmt][2](_np(x_i8), _np(xs), w, K), odt)
 
 
+# at least one full round of 128 x 128 tiles on 256 CUs plus a short last
+# round (260 and 258 tiles): the last tiles run as row quarters in a second
+# launch; (257, 10890): the split tiles are the ragged last ones in M and N
+SPLIT_SHAPES = [(160, 16635, 512), (257, 10890, 256)]
+
+
+@pytest.mark.parametrize("M,N,K", SPLIT_SHAPES)
+@pytest.mark.parametrize("fmt", ["q5k", "q6k"])
+def test_tile_gemm_last_round_split(device, fmt, M, N, K):
+    x, w, wd = _case(fmt, M, N, K, seed=M + N, device=device)
+    x_i8, xs = _C.quantize_i8_rowwise(x)
+    y = getattr(_C, FMT[fmt][4])(x_i8, xs, wd, torch.float32)
+    xn, xsn = _np(x_i8), _np(xs)
+    ref = np.concatenate([FMT[fmt][2](xn, xsn, w[n:n + 1024], K) for n in range(0, N, 1024)], axis=1)
+    _check_exact_sum(y, ref, torch.float32)
+
+
 DEC_SHAPES = [(1, 4096, 3072), (1, 130, 256), (2, 4096, 5120), (4, 512, 768), (8, 17408, 5120),
               (16, 1000, 2048), (3, 33, 768), (1, 64, 16384),
               # long K: the M >= 3 MFMA kernels loop over several super-block

@@ -97,6 +97,20 @@ def test_tile_gemm_matches_exact_sum(device, M, N, K, odt):
     assert (err <= rtol * np.abs(ref) + 1e-5 * scale).all(), f"max err {err.max():.3e}"
 
 
+# at least one full round of 128 x 128 tiles on 256 CUs plus a short last
+# round (260 and 258 tiles): the last tiles run as row quarters in a second
+# launch; (257, 10890): the split tiles are the ragged last ones in M and N
+@pytest.mark.parametrize("M,N,K", [(160, 16635, 512), (257, 10890, 256)])
+def test_tile_gemm_last_round_split(device, M, N, K):
+    x, w, wd = _case(M, N, K, seed=M + N, device=device)
+    x_i8, xs = _C.quantize_i8_rowwise(x)
+    y = _C.gemm_q4k(x_i8, xs, wd, torch.float32)
+    xn, xsn = _np(x_i8), _np(xs)
+    ref = np.concatenate([oq.gemv(xn, xsn, w[n:n + 1024], K) for n in range(0, N, 1024)], axis=1)
+    err = np.abs(_np(y).astype(np.float64) - ref)
+    assert (err <= 1e-5 * np.abs(ref) + 1e-5 * np.abs(ref).max()).all(), f"max err {err.max():.3e}"
+
+
 def test_tile_matches_decode_and_large_m(device):
     """reference test_gemm_q4k.py:715-728: the tile path and the decode path agree
     (to fp16 output rounding) on the rows they share."""
