@@ -188,27 +188,25 @@ gemm_q5k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
   if (sb < nsb) compute(xs0, ws0);
 
   const int n = n0 + 32 * wave + l32;
+  // the row scales first, unconditionally (clamped rows): one wait, not one per element
+  float xsv[RB][16];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      xsv[rb][e] = x_scale[min(m0 + 32 * (rb + rb0) + 8 * (e >> 2) + 4 * h + (e & 3), M - 1)];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int m = m0 + 32 * (rb + rb0) + 8 * (e >> 2) + 4 * h + (e & 3);
-      if (m < M && n < N) st_out<OUT_DT>(out, (int64_t)m * N + n, f[rb][e] * x_scale[m]);
+      if (m < M && n < N) st_out<OUT_DT>(out, (int64_t)m * N + n, f[rb][e] * xsv[rb][e]);
     }
 }
 
 // ---------------------------------------------------------------------------
 // Q6_K tile GEMM
 // ---------------------------------------------------------------------------
-// 8 bytes at a 2-byte aligned LDS address (aligned dword reads + v_alignbyte).
-__device__ __forceinline__ uint2 lds8_at(const uint8_t* p) {
-  const uintptr_t ad = reinterpret_cast<uintptr_t>(p);
-  const uint32_t* a = reinterpret_cast<const uint32_t*>(p - (ad & 3));  // keeps the LDS address space
-  const uint32_t sh = (uint32_t)(ad & 3);
-  const uint32_t d0 = a[0], d1 = a[1], d2 = a[2];
-  return make_uint2(__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh));
-}
-
 // Q6_K tile GEMM on v_mfma_i32_32x32x32_i8. Wave w owns the 32 weight rows
 // 32 w .. 32 w + 31 (output columns) for all 128 activation rows, so each
 // weight operand is built once per workgroup. One K = 32 step s of a
@@ -231,11 +229,13 @@ typedef short v2s_t __attribute__((ext_vector_type(2)));
 #define SL8_Q6T_SCHED 1
 #endif
 
-// 16 bytes at a 2-byte aligned LDS address
-__device__ __forceinline__ uint4 lds16_at(const uint8_t* p) {
-  const uintptr_t ad = reinterpret_cast<uintptr_t>(p);
-  const uint32_t* a = reinterpret_cast<const uint32_t*>(p - (ad & 3));  // keeps the LDS address space
-  const uint32_t sh = (uint32_t)(ad & 3);
+// 16 bytes at byte offset b (even) of a dword array in LDS: aligned dword
+// reads + v_alignbyte. The address is formed by indexing the array itself (no
+// pointer-to-integer round trip), so the compiler keeps its provenance and
+// does not wait for the other buffer's in-flight copies before the read.
+__device__ __forceinline__ uint4 lds16_off(const uint32_t* w, int b) {
+  const uint32_t* a = w + (b >> 2);
+  const uint32_t sh = (uint32_t)(b & 3);
   const uint32_t d0 = a[0], d1 = a[1], d2 = a[2], d3 = a[3], d4 = a[4];
   return make_uint4(__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh),
                     __builtin_amdgcn_alignbyte(d3, d2, sh), __builtin_amdgcn_alignbyte(d4, d3, sh));
@@ -303,18 +303,19 @@ gemm_q6k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
   auto compute = [&](int sb, const int8_t* xt, const uint32_t* wt) __attribute__((always_inline)) {
     // the block's misalignment is that of its offset from the row-n0 base
     const uint32_t base = (uint32_t)min(r, rmax) * (uint32_t)row_bytes + (uint32_t)sb * Q6K_BYTES;
-    const uint8_t* blk = reinterpret_cast<const uint8_t*>(wt) + r * Q6P16 + (int)(base & 15u);
-    const uint4 scv = lds16_at(blk + 192);
-    const float d = h2f((uint16_t)(lds8_at(blk + 208).x & 0xFFFFu));
+    const int blk = r * Q6P16 + (int)(base & 15u);  // byte offset of the block in the tile
+    const uint4 scv = lds16_off(wt, blk + 192);
+    const float d = h2f((uint16_t)(__builtin_amdgcn_alignbyte(wt[((blk + 208) >> 2) + 1], wt[(blk + 208) >> 2],
+                                                             (uint32_t)((blk + 208) & 3)) & 0xFFFFu));
     v16i_t tl[4], th[4];
     // software pipeline over the 8 K steps: step s + 1's A reads and B
     // operands are formed while step s's 8 MFMAs run (double-buffered
     // registers; one scheduling region per step, MFMAs interleaved with VALU)
     uint32_t qv[2][12];  // ql quadrants 0/2, 1/3 and qh of each ql half
     auto load_q = [&](int hf) __attribute__((always_inline)) {
-      const uint4 qa = lds16_at(blk + 64 * hf + 16 * h);       // quadrants 0, 2
-      const uint4 qb = lds16_at(blk + 64 * hf + 32 + 16 * h);  // quadrants 1, 3
-      const uint4 qc = lds16_at(blk + 128 + 32 * hf + 16 * h);
+      const uint4 qa = lds16_off(wt, blk + 64 * hf + 16 * h);       // quadrants 0, 2
+      const uint4 qb = lds16_off(wt, blk + 64 * hf + 32 + 16 * h);  // quadrants 1, 3
+      const uint4 qc = lds16_off(wt, blk + 128 + 32 * hf + 16 * h);
       qv[hf][0] = qa.x; qv[hf][1] = qa.y; qv[hf][2] = qa.z; qv[hf][3] = qa.w;
       qv[hf][4] = qb.x; qv[hf][5] = qb.y; qv[hf][6] = qb.z; qv[hf][7] = qb.w;
       qv[hf][8] = qc.x; qv[hf][9] = qc.y; qv[hf][10] = qc.z; qv[hf][11] = qc.w;
@@ -396,12 +397,19 @@ gemm_q6k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
   if (sb < nsb) compute(sb, xs0, ws0);
 
   const int n = n0 + r;
+  // the row scales first, unconditionally (clamped rows): one wait, not one per element
+  float xsv[RB][16];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      xsv[rb][e] = x_scale[min(m0 + 32 * (rb + rb0) + 8 * (e >> 2) + 4 * h + (e & 3), M - 1)];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int m = m0 + 32 * (rb + rb0) + 8 * (e >> 2) + 4 * h + (e & 3);
-      if (m < M && n < N) st_out<OUT_DT>(out, (int64_t)m * N + n, f[rb][e] * x_scale[m]);
+      if (m < M && n < N) st_out<OUT_DT>(out, (int64_t)m * N + n, f[rb][e] * xsv[rb][e]);
     }
 }
 

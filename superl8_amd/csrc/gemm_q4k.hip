@@ -693,12 +693,19 @@ gemm_q4k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
   if (sb < nsb) compute(xs0, ws0);
 
   const int n = n0 + 32 * wave + l32;
+  // the row scales first, unconditionally (clamped rows): one wait, not one per element
+  float xsv[RB][16];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      xsv[rb][e] = x_scale[min(m0 + 32 * (rb + rb0) + 8 * (e >> 2) + 4 * h + (e & 3), M - 1)];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int m = m0 + 32 * (rb + rb0) + 8 * (e >> 2) + 4 * h + (e & 3);
-      if (m < M && n < N) st_out<OUT_DT>(out, (int64_t)m * N + n, f[rb][e] * x_scale[m]);
+      if (m < M && n < N) st_out<OUT_DT>(out, (int64_t)m * N + n, f[rb][e] * xsv[rb][e]);
     }
 }
 
