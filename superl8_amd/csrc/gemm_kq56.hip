@@ -43,10 +43,14 @@ constexpr int T5CH = (KBN * 11 + 255) / 256 * 256;       // Q5_K weight-tile 16-
 
 // x tile copy: 128 rows x 256 int8 of super-block sb; 16-byte chunk c of row r
 // lands at r * 256 + 16 * (c ^ (r & 15)) (rows are one 256-byte bank line).
+// NI = 8: all 128 rows; NI = 2: rows 32 q .. 32 q + 31 only (i from 2 q; a
+// last-round quarter workgroup reads no other rows)
+template <int NI = KBM * 16 / 256>
 __device__ __forceinline__ void copy_x_tile(const int8_t* x, int8_t* xd, int m0, int M, int K, int sb,
-                                            int tid, int wave) {
+                                            int tid, int wave, int q = 0) {
 #pragma unroll
-  for (int i = 0; i < KBM * 16 / 256; ++i) {
+  for (int ii = 0; ii < NI; ++ii) {
+    const int i = (NI == KBM * 16 / 256 ? 0 : 2 * q) + ii;
     const int P = i * 256 + tid, row = P >> 4;
     const int c = (P & 15) ^ (row & 15);
     const int8_t* src = x + (int64_t)min(m0 + row, M - 1) * K + (int64_t)sb * 256 + 16 * c;
@@ -79,7 +83,7 @@ gemm_q5k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
   const int64_t row_bytes = (int64_t)nsb * Q5K_BYTES;
 
   auto load = [&](int sb, int8_t* xd, uint8_t* wd) __attribute__((always_inline)) {
-    copy_x_tile(x, xd, m0, M, K, sb, tid, wave);
+    copy_x_tile<RB == 4 ? KBM * 16 / 256 : 2>(x, xd, m0, M, K, sb, tid, wave, rb0);
 #pragma unroll
     for (int i = 0; i < T5CH / 256; ++i) {
       const int P = min(i * 256 + tid, KBN * 11 - 1), row = P / 11, c = P - 11 * row;
@@ -283,7 +287,7 @@ gemm_q6k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
   // is 256-byte aligned (n0 of 128, row_bytes even): 128 rows of < 2^24 bytes
   const uint8_t* wbase = w + (int64_t)n0 * row_bytes;
   auto load = [&](int sb, int8_t* xd, uint32_t* wd) __attribute__((always_inline)) {
-    copy_x_tile(x, xd, m0, M, K, sb, tid, wave);
+    copy_x_tile<RB == 4 ? KBM * 16 / 256 : 2>(x, xd, m0, M, K, sb, tid, wave, rb0);
     const uint32_t sboff = (uint32_t)sb * Q6K_BYTES;
 #pragma unroll
     for (int i = 0; i < KBN * 14 / 256; ++i) {

@@ -584,7 +584,8 @@ gemm_q4k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
   // copies of super-block sb into (xd, wd); chunk P of the tile lands at P*16
   auto load = [&](int sb, int8_t* xd, uint8_t* wd) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < TBM * 16 / 256; ++i) {
+    for (int ii = 0; ii < (RB == 4 ? TBM * 16 / 256 : 2); ++ii) {
+      const int i = (RB == 4 ? 0 : 2 * rb0) + ii;  // a quarter copies only its 32 rows
       const int P = i * 256 + tid, row = P >> 4;
       const int c = (P & 15) ^ (row & 15);
       const int8_t* src = x + (int64_t)min(m0 + row, M - 1) * K + (int64_t)sb * 256 + 16 * c;
