@@ -157,13 +157,18 @@ int sl8_attn_int8_fwd_gated(const int8_t* q, const float* q_scale, const int8_t*
                             void* workspace, size_t workspace_bytes, const int32_t* gate_flag,
                             void* stream);
 
-/* Test hook: the int32 Q.K^T scores exactly as the prefill kernel's MFMA
- * tiles produce them (same code path, scores dumped instead of softmaxed).
- *   scores int32 [B,Hq,M,N]. No reference counterpart (the reference never
- *   exposes its dp4a accumulators); used to prove bit-exact int32 QK^T. */
+/* Test hook: the int32 Q.K^T scores exactly as the production prefill kernel
+ * (sl8_attn_int8_fwd's attn_fwd_wide_kernel) computes them: the same template
+ * instantiated with a dump epilogue, same tiling, pipeline and MFMA operands.
+ *   scores int32 [B,Hq,M,N]; causal != 0 runs the causal kernel, which stores
+ *   only the key tiles a wave computes (the caller pre-fills the rest).
+ *   Head dims 32/72/80 need sl8_attn_int8_fwd_workspace() bytes of workspace.
+ * No reference counterpart (the reference never exposes its dp4a
+ * accumulators); used to prove bit-exact int32 QK^T. */
 int sl8_attn_int8_qk_scores(const int8_t* q, const int8_t* k, int32_t* scores,
                             int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N,
-                            int64_t D, void* stream);
+                            int64_t D, int causal, void* workspace, size_t workspace_bytes,
+                            void* stream);
 
 /* ------------------------------------------------------------------------
  * Full W8A8 prefill: int8 QK^T and int8 PV (P re-quantised in-loop, per row

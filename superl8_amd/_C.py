@@ -269,20 +269,26 @@ def attn_int8_fwd_train(q, q_scale, k, k_scale, v, causal=False):
     return _attn_fwd(q, q_scale, k, k_scale, v, causal, -1, True)
 
 
-def attn_int8_qk_scores(q, k):
-    """int32 Q.K^T [B,Hq,M,N] straight from the prefill kernel's MFMA tiles (test hook)."""
+def attn_int8_qk_scores(q, k, causal=False, fill=0):
+    """int32 Q.K^T [B,Hq,M,N] from the production prefill kernel's own MFMA tiles
+    (its score-dump instantiation; test hook). causal=True runs the causal
+    kernel, which only computes key tiles a wave can see: entries it does not
+    store keep `fill`."""
     _on_gpu(q, k)
     _check(q.dtype == torch.int8 and k.dtype == torch.int8, "q/k must be int8")
     _contig(q, k)
     B, H, M, D = q.shape
     Hkv, N = k.shape[1], k.shape[2]
-    _check(H % Hkv == 0 and k.shape[3] == D and k.shape[0] == B, "q/k shape mismatch")
-    _check(D in (64, 128), f"head dim must be one of (64, 128), got {D}")
-    s = torch.empty((B, H, M, N), device=q.device, dtype=torch.int32)
+    _check(Hkv > 0 and H % Hkv == 0 and k.shape[3] == D and k.shape[0] == B, "q/k shape mismatch")
+    _check(D in _HEAD_DIMS_FWD, f"head dim must be {_dims_msg(_HEAD_DIMS_FWD)}, got {D}")
+    s = torch.full((B, H, M, N), fill, device=q.device, dtype=torch.int32)
     if s.numel():
+        ws_bytes = _lib.load().sl8_attn_int8_fwd_workspace(B, H, Hkv, M, N, D)
+        ws = torch.empty((ws_bytes,), device=q.device, dtype=torch.uint8) if ws_bytes else None
         with torch.cuda.device(q.device):
             call("sl8_attn_int8_qk_scores", q.data_ptr(), k.data_ptr(), s.data_ptr(), B, H, Hkv,
-                 M, N, D, stream_of(q))
+                 M, N, D, int(bool(causal)), ws.data_ptr() if ws is not None else None, ws_bytes,
+                 stream_of(q))
     return s
 
 
@@ -566,8 +572,12 @@ def _q4k_checks(x, x_scale, w, out_dtype, tag, type_size=Q4K_TYPE_SIZE, x_block_
     _check(K % 256 == 0, f"{tag} contraction dim K must be %256==0, got {K}")
     _check(w.shape[1] == (K // 256) * type_size,
            f"{tag} weight must be [N, (K/256)*{type_size}], got [{N},{w.shape[1]}] for K={K}")
-    _check(x_scale.numel() == M or (x_block_ok and x_scale.shape == (M, K // 256)),
-           "x_scale must be [M]")
+    if x_block_ok:
+        _check(x_scale.numel() == M or tuple(x_scale.shape) == (M, K // 256),
+               f"x_scale must be [M] (per row) or [M, K/256] (per 256-block), got "
+               f"{list(x_scale.shape)} for M={M}, K={K}")
+    else:
+        _check(x_scale.numel() == M, f"x_scale must be [M] (per row), got {list(x_scale.shape)}")
     return M, N, K
 
 
@@ -595,15 +605,17 @@ def gemm_decode_q4k(x, x_scale, w, out_dtype=torch.float16):
     _check(x.dim() == 2 and x.shape[0] <= DEC_MAX_M,
            f"gemm_decode_q4k supports M<={DEC_MAX_M}, got M={x.shape[0] if x.dim() else 0}"
            " -- use the tile gemm_q4k for prefill")
-    if x_scale.dim() == 2:
-        M, N, K = _q4k_checks(x, x_scale, w, out_dtype, "Q4_K", Q4K_TYPE_SIZE, x_block_ok=True)
+    M, N, K = _q4k_checks(x, x_scale, w, out_dtype, "Q4_K", Q4K_TYPE_SIZE, x_block_ok=True)
+    # per-256-block scales only when the shape says so; any other x_scale with
+    # M elements (e.g. [M, 1]) is the reference's per-row scale
+    if x_scale.dim() == 2 and tuple(x_scale.shape) == (M, K // 256) and K // 256 > 1:
         out = torch.empty((M, N), device=x.device, dtype=out_dtype)
         if M and N:
             with torch.cuda.device(x.device):
                 call("sl8_gemm_decode_q4k_xblock", x.data_ptr(), x_scale.data_ptr(), w.data_ptr(),
                      out.data_ptr(), dtype_code(out_dtype), M, N, K, stream_of(x))
         return out
-    return _q4k("sl8_gemm_decode_q4k", x, x_scale, w, out_dtype)
+    return _q4k("sl8_gemm_decode_q4k", x, x_scale.reshape(-1), w, out_dtype)
 
 
 def quantize_i8_blockwise(x: torch.Tensor, block: int = 256):

@@ -38,7 +38,7 @@ SIGNATURES = {
                                _I, _I64, _P, _SZ, _P]),
     "sl8_attn_int8_fwd_gated": (_I, [_P, _P, _P, _P, _P, _I, _P, _P, _I64, _I64, _I64, _I64, _I64,
                                      _I64, _I, _I64, _P, _SZ, _P, _P]),
-    "sl8_attn_int8_qk_scores": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P]),
+    "sl8_attn_int8_qk_scores": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P, _SZ, _P]),
     "sl8_attn_w8a8_fwd_workspace": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64]),
     "sl8_attn_w8a8_fwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
                                _I, _I64, _I, _P, _SZ, _P]),

@@ -10,9 +10,9 @@
 //            key is 0 and its LSE -inf; LSE = max*ln2 + ln(l).
 //   GQA: query head h reads K/V head h / (Hq/Hkv).
 //
-// Work decomposition (attn_fwd_wide_kernel, the production kernel; the
-// narrow attn_fwd_kernel below only serves the int32 score dump): a wave owns
-// 32 queries for the whole key loop, a workgroup 4 or 8 waves; 64-key K,
+// Work decomposition (attn_fwd_wide_kernel, the one kernel; its DUMP
+// instantiation stores the int32 scores for the bit-exactness test): a wave
+// owns 32 queries for the whole key loop, a workgroup 4 or 8 waves; 64-key K,
 // k_scale and V tiles are copied global -> LDS one tile ahead and shared by
 // the waves.
 //
@@ -39,9 +39,6 @@
 namespace sl8 {
 namespace {
 
-constexpr int FWD_THREADS = 256;
-constexpr int FWD_WAVES = 4;
-constexpr int BM = 128;  // queries per workgroup
 constexpr int BN = 64;   // keys per tile
 constexpr float LN2F = 0.6931471805599453f;
 #ifndef SL8_W8_LAZY
@@ -175,286 +172,6 @@ struct QOp {
   v4i c[DC];
 };
 
-// S^T tile (64 keys x 32 queries) of one wave: two 32-key MFMA accumulators.
-// kt: the lane's K row base in LDS; koff[ch]: swizzled byte offset of chunk ch.
-template <int D>
-__device__ __forceinline__ void qk_tile(const int8_t* kt, const int (&koff)[D / 32],
-                                        const QOp<D / 32>& q, v16i& s0, v16i& s1) {
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    s0[r] = 0;
-    s1[r] = 0;
-  }
-#pragma unroll
-  for (int ch = 0; ch < D / 32; ++ch) {
-    const v4i k0 = *reinterpret_cast<const v4i*>(kt + koff[ch]);
-    const v4i k1 = *reinterpret_cast<const v4i*>(kt + 32 * D + koff[ch]);
-    s0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(k0, q.c[ch], s0, 0, 0, 0);
-    s1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(k1, q.c[ch], s1, 0, 0, 0);
-  }
-}
-
-template <int D, bool CAUSAL, int VDT, bool DUMP, bool LSE>
-__global__ void __launch_bounds__(FWD_THREADS, 2)
-attn_fwd_kernel(const FwdArgs a) {
-  constexpr int DC = D / 32;                          // 32-channel chunks
-  constexpr int KCH = BN * D / 16 / FWD_THREADS;      // 16-B K chunks per thread
-  constexpr int VCH = D * BN * 2 / 16 / FWD_THREADS;  // 16-B V^T chunks per thread
-  static_assert(KCH >= 1 && VCH >= 1, "tile copies cover D in {64,128}");
-  // tile buffers: separate LDS objects (see the pipeline comment below)
-  __shared__ __attribute__((aligned(16))) int8_t sm_k0[BN * D];
-  __shared__ __attribute__((aligned(16))) int8_t sm_k1[BN * D];
-  __shared__ __attribute__((aligned(16))) uint16_t sm_v0[D * BN];
-  __shared__ __attribute__((aligned(16))) uint16_t sm_v1[D * BN];
-  __shared__ __attribute__((aligned(16))) float sm_s0[BN];
-  __shared__ __attribute__((aligned(16))) float sm_s1[BN];
-  using PV = PvOp<VDT>;
-
-  // Causal launches pair query block qb with nqb-1-qb so every workgroup
-  // does the same amount of work.
-  const int nslot = CAUSAL ? (a.nqb + 1) / 2 : a.nqb;
-  int bh, slot;
-  block_coords(a, nslot, bh, slot);
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int h = lane >> 5, l32 = lane & 31;
-  const int gsz = a.Hq / a.Hkv;
-  const int b = bh / a.Hq, hq = bh % a.Hq;
-  const int64_t bkv = (int64_t)b * a.Hkv + hq / gsz;
-  const int M = a.M, N = a.N;
-  const int diag = CAUSAL ? a.diag : 0;
-  const int wl = a.window_left;
-
-  const int8_t* kb = a.k + bkv * (int64_t)N * D;
-  const float* ksb = a.ks + bkv * (int64_t)N;
-  const uint16_t* vtb = a.vt + bkv * (int64_t)D * a.Npad;
-
-  int qbs[2];
-  int npass = 1;
-  qbs[0] = a.nqb - 1 - slot;
-  qbs[1] = slot;
-  if (CAUSAL) npass = (qbs[1] != qbs[0]) ? 2 : 1;
-
-  // LDS operand offsets (swizzled chunks), fixed for the whole kernel
-  constexpr int KCPR = D / 16;  // 16-B chunks per K row
-  int koff[DC], voff[4];
-#pragma unroll
-  for (int ch = 0; ch < DC; ++ch) koff[ch] = ((2 * ch + h) ^ (l32 & (KCPR - 1))) * 16;
-#pragma unroll
-  for (int c4 = 0; c4 < 4; ++c4) voff[c4] = ((2 * c4 + h) ^ (l32 & 7)) * 8;  // in halves
-
-  for (int pass = 0; pass < npass; ++pass) {
-    const int m_blk = qbs[pass] * BM;
-    const int mq = m_blk + wave * 32 + l32;  // this lane's query
-    const bool m_ok = mq < M;
-    const int qpos = mq + diag;
-
-    QOp<DC> qop;
-    {
-      const int8_t* qrow = a.q + ((int64_t)bh * M + (m_ok ? mq : M - 1)) * D + 16 * h;
-#pragma unroll
-      for (int c = 0; c < DC; ++c) {
-        qop.c[c] = *reinterpret_cast<const v4i*>(qrow + 32 * c);
-        if (!m_ok) qop.c[c] = v4i{0, 0, 0, 0};
-      }
-    }
-    // rows past M use scale 1 so no NaN appears in their (unstored) lanes
-    const float qsc = (m_ok && !DUMP) ? a.qs[(int64_t)bh * M + mq] : 1.f;
-
-    // key tiles of the workgroup: [n_beg, n_end)
-    int n_end = N;
-    if (CAUSAL) n_end = max(0, min(N, m_blk + BM + diag));
-    int n_beg = 0;
-    if (wl >= 0) n_beg = min(n_end, max(0, m_blk + diag - wl + 1) & ~(BN - 1));
-    const int ntiles = (n_end - n_beg + BN - 1) / BN;
-    const int wq_lo = m_blk + wave * 32 + diag;  // first query position of the wave
-    const int wq_hi = wq_lo + 31;
-    auto live = [&](int n0) {
-      bool ok = true;
-      if (CAUSAL && n0 > wq_hi) ok = false;
-      if (wl >= 0 && n0 + BN - 1 <= wq_lo - wl) ok = false;
-      return DUMP || ok;
-    };
-
-    // global -> LDS tile copies (no staging registers)
-    auto load_k = [&](int n0, int8_t* dst) {
-#pragma unroll
-      for (int i = 0; i < KCH; ++i) {
-        const int slot = i * FWD_THREADS + tid;
-        const int row = slot / KCPR;
-        const int c = (slot % KCPR) ^ (row & (KCPR - 1));
-        dma16_to_lds(kb + (int64_t)min(n0 + row, N - 1) * D + 16 * c,
-                     dst + (i * FWD_THREADS + wave * 64) * 16);
-      }
-    };
-    auto load_v = [&](int n0, uint16_t* dst, float* kdst) {
-      if constexpr (!DUMP) {
-#pragma unroll
-        for (int i = 0; i < VCH; ++i) {
-          const int slot = i * FWD_THREADS + tid;
-          const int row = slot / 8;
-          const int c = (slot % 8) ^ (row & 7);
-          dma16_to_lds(vtb + (int64_t)row * a.Npad + n0 + 8 * c,
-                       dst + (i * FWD_THREADS + wave * 64) * 8);
-        }
-        if (wave == 0) dma4_to_lds(ksb + min(n0 + lane, N - 1), kdst);
-      }
-    };
-
-    v16f oacc[DC];
-#pragma unroll
-    for (int t = 0; t < DC; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) oacc[t][r] = 0.f;
-    float m_run = -INFINITY, l_lane = 0.f;
-
-    // Pipeline: while the softmax and P.V of tile j run, the MFMAs of
-    // S_{j+1} are already in flight and the copies of K_{j+2} and
-    // V_{j+1}/k_scale_{j+1} are landing in LDS. Every buffer is a separate LDS
-    // object and the loop is unrolled by two, so the compiler can see that the
-    // in-flight copies never alias the tiles being read (no early vmcnt wait).
-    if (ntiles > 0) {
-      load_k(n_beg, sm_k0);
-      load_v(n_beg, sm_v0, sm_s0);
-      if (ntiles > 1) load_k(n_beg + BN, sm_k1);
-    }
-    wait_dma();
-    __syncthreads();
-
-    v16i sc0, sc1;  // S_j
-    if (ntiles > 0 && live(n_beg)) qk_tile<D>(sm_k0 + l32 * D, koff, qop, sc0, sc1);
-    __syncthreads();  // all waves done with K_0 before K_2 lands there
-
-    auto body = [&](int j, int8_t* kc, const int8_t* kn, const uint16_t* vc, uint16_t* vn,
-                    const float* scur, float* snext) {
-      const int n0 = n_beg + j * BN;
-      if (j + 2 < ntiles) load_k(n0 + 2 * BN, kc);
-      if (j + 1 < ntiles) load_v(n0 + BN, vn, snext);
-
-      // S_{j+1}: issue its MFMAs before the softmax of tile j
-      v16i sn0, sn1;
-      if (j + 1 < ntiles && live(n0 + BN)) qk_tile<D>(kn + l32 * D, koff, qop, sn0, sn1);
-
-      if (live(n0)) {
-        if constexpr (DUMP) {
-          if (m_ok) {
-            int32_t* srow = a.scores + ((int64_t)bh * M + mq) * N;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int n = n0 + 8 * (r >> 2) + 4 * h + (r & 3);
-              if (n < N) srow[n] = sc0[r];
-              if (n + 32 < N) srow[n + 32] = sc1[r];
-            }
-          }
-        } else {
-          // t = acc * k_scale; logit = t * q_scale (q_scale > 0, so max(t) gives max(logit))
-          float t[32];
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const float4 ka = *reinterpret_cast<const float4*>(scur + 8 * g + 4 * h);
-            const float4 kc4 = *reinterpret_cast<const float4*>(scur + 32 + 8 * g + 4 * h);
-            t[4 * g + 0] = (float)sc0[4 * g + 0] * ka.x;
-            t[4 * g + 1] = (float)sc0[4 * g + 1] * ka.y;
-            t[4 * g + 2] = (float)sc0[4 * g + 2] * ka.z;
-            t[4 * g + 3] = (float)sc0[4 * g + 3] * ka.w;
-            t[16 + 4 * g + 0] = (float)sc1[4 * g + 0] * kc4.x;
-            t[16 + 4 * g + 1] = (float)sc1[4 * g + 1] * kc4.y;
-            t[16 + 4 * g + 2] = (float)sc1[4 * g + 2] * kc4.z;
-            t[16 + 4 * g + 3] = (float)sc1[4 * g + 3] * kc4.w;
-          }
-          const bool need_mask = (n0 + BN > N) || (CAUSAL && n0 + BN - 1 > wq_lo) ||
-                                 (wl >= 0 && n0 <= wq_hi - wl);
-          if (need_mask) {
-#pragma unroll
-            for (int e = 0; e < 32; ++e) {
-              const int n = n0 + 32 * (e >> 4) + 8 * ((e & 15) >> 2) + 4 * h + (e & 3);
-              bool ok = n < N;
-              if (CAUSAL) ok = ok && n <= qpos;
-              if (wl >= 0) ok = ok && n > qpos - wl;
-              t[e] = ok ? t[e] : -INFINITY;
-            }
-          }
-          float tmax = -INFINITY;
-#pragma unroll
-          for (int e = 0; e < 32; ++e) tmax = fmaxf(tmax, t[e]);
-          tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-          // Lazy rescaling: the reference point m_run (exp2 domain) only moves
-          // when the tile max exceeds it by more than 8, so P <= 2^8 (safe in
-          // fp16/bf16 and fp32). Any reference point gives the same softmax.
-          const float m_new = fmaxf(m_run, tmax * qsc);
-          const bool need = m_new > m_run + 8.f;
-          if (__any(need)) {
-            const float resc = need ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;
-            if (need) m_run = m_new;
-            l_lane *= resc;
-#pragma unroll
-            for (int tt = 0; tt < DC; ++tt)
-#pragma unroll
-              for (int r = 0; r < 16; ++r) oacc[tt][r] *= resc;
-          }
-          const float msub = (m_run == -INFINITY) ? 0.f : m_run;
-          float psum = 0.f;
-#pragma unroll
-          for (int e = 0; e < 32; ++e) {
-            const float p = __builtin_amdgcn_exp2f(fmaf(t[e], qsc, -msub));  // -inf -> 0
-            t[e] = p;
-            psum += p;
-          }
-          l_lane += psum;
-
-          // ---- O^T += V^T . P^T, four 16-key steps ----
-          const uint16_t* vrow = vc + l32 * BN;
-#pragma unroll
-          for (int c4 = 0; c4 < 4; ++c4) {
-            const typename PV::vec pop = PV::pack(&t[8 * c4]);
-#pragma unroll
-            for (int tt = 0; tt < DC; ++tt) {
-              const typename PV::vec vop = *reinterpret_cast<const typename PV::vec*>(
-                  vrow + 32 * tt * BN + voff[c4]);
-              oacc[tt] = PV::mfma(vop, pop, oacc[tt]);
-            }
-          }
-        }
-      }
-      wait_dma();
-      __syncthreads();
-      sc0 = sn0;
-      sc1 = sn1;
-    };
-
-    for (int j = 0; j < ntiles; j += 2) {
-      body(j, sm_k0, sm_k1, sm_v0, sm_v1, sm_s0, sm_s1);
-      if (j + 1 < ntiles) body(j + 1, sm_k1, sm_k0, sm_v1, sm_v0, sm_s1, sm_s0);
-    }
-
-    if constexpr (!DUMP) {
-      const float l = l_lane + __shfl_xor(l_lane, 32, 64);
-      if (m_ok) {
-        const float inv = (l > 0.f) ? 1.f / l : 0.f;
-        uint16_t* orow = reinterpret_cast<uint16_t*>(a.out) + ((int64_t)bh * M + mq) * D;
-#pragma unroll
-        for (int tt = 0; tt < DC; ++tt)
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            uint16_t hv[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const float x = oacc[tt][4 * g + e] * inv;
-              hv[e] = (VDT == SL8_DTYPE_F16) ? f2h_bits(x) : f2bf_bits(x);
-            }
-            uint2 pk;
-            pk.x = hv[0] | ((uint32_t)hv[1] << 16);
-            pk.y = hv[2] | ((uint32_t)hv[3] << 16);
-            *reinterpret_cast<uint2*>(orow + 32 * tt + 8 * g + 4 * h) = pk;
-          }
-        if (LSE && h == 0)
-          a.lse[(int64_t)bh * M + mq] = (l > 0.f) ? (m_run * LN2F + logf(l)) : -INFINITY;
-      }
-    }
-  }
-}
-
-
 // ---------------------------------------------------------------------------
 // Production kernel. A wave owns NG x 32 queries (NG = 1: one MFMA column
 // block) for the whole key loop; WV waves per workgroup (8 for D = 128, 4 for
@@ -483,7 +200,11 @@ attn_fwd_kernel(const FwdArgs a) {
 // workgroup (they share every K / V^T tile copied into LDS). W8 = the full
 // W8A8 semantics (P re-quantised to int8 per 32-key half, int8 V with a
 // per-channel scale); see half_probs_w8.
-template <int D, bool CAUSAL, int VDT, bool LSE, int NG, int WV, bool W8>
+// DUMP = the same kernel with the int32 S^T tiles of every live 32-key half
+// stored to a.scores [B*Hq][M][N] (the test hook that proves the production
+// MFMA path's Q.K^T bit-exact); V and the scales are not read, nothing else
+// is written.
+template <int D, bool CAUSAL, int VDT, bool LSE, int NG, int WV, bool W8, bool DUMP = false>
 __global__ void __launch_bounds__(WV * 64, (NG == 1 && D <= 128) ? SL8_FWD_OCC * 4 / WV : 1)
 attn_fwd_wide_kernel(const FwdArgs a) {
   // the caller's accuracy gate fired: its result is discarded, so do nothing
@@ -500,6 +221,7 @@ attn_fwd_wide_kernel(const FwdArgs a) {
   constexpr int VCH = D * BN * 2 / 16 / WT;
   static_assert(KCH >= 1 && VCH >= 1, "tile copies cover D in {64,128,256}");
   static_assert(!W8 || (VDT == SL8_DTYPE_BF16 && !LSE), "W8A8: bf16 PV, no LSE");
+  static_assert(!DUMP || (!W8 && !LSE), "score dump: the int8 prefill only");
   __shared__ __attribute__((aligned(16))) int8_t sm_k0[BN * D];
   __shared__ __attribute__((aligned(16))) int8_t sm_k1[BN * D];
   __shared__ __attribute__((aligned(16))) uint16_t sm_v0[D * BN];
@@ -571,6 +293,9 @@ attn_fwd_wide_kernel(const FwdArgs a) {
     reinterpret_cast<uint4*>(sm_v0)[i] = make_uint4(0, 0, 0, 0);
     reinterpret_cast<uint4*>(sm_v1)[i] = make_uint4(0, 0, 0, 0);
   }
+  if constexpr (DUMP) {  // the scales are not read: unit k_scale keeps the softmax finite
+    for (int i = tid; i < BN; i += WT) sm_s0[i] = sm_s1[i] = 1.f;
+  }
 
   for (int pass = 0; pass < npass; ++pass) {
     const int m_blk = qbs[pass] * WBM;
@@ -590,7 +315,7 @@ attn_fwd_wide_kernel(const FwdArgs a) {
         qop[g].c[c] = *reinterpret_cast<const v4i*>(qrow + 32 * c);
         if (!m_ok[g]) qop[g].c[c] = v4i{0, 0, 0, 0};
       }
-      qsc[g] = m_ok[g] ? a.qs[(int64_t)bh * M + mq[g]] : 1.f;
+      qsc[g] = (m_ok[g] && !DUMP) ? a.qs[(int64_t)bh * M + mq[g]] : 1.f;
     }
 
     int n_end = N;
@@ -648,11 +373,13 @@ attn_fwd_wide_kernel(const FwdArgs a) {
         buf16_to_lds(rk, dst + (i * WT + wave * 64) * 16, kvo[i], (uint32_t)n0 * D);
     };
     auto load_v = [&](int n0, uint16_t* dst) __attribute__((always_inline)) {
+      if constexpr (DUMP) return;
 #pragma unroll
       for (int i = 0; i < VCH; ++i)
         buf16_to_lds(rv, dst + (i * WT + wave * 64) * 8, vvo[i], (uint32_t)n0 * (VT ? 2 : VRB));
     };
     auto load_s = [&](int n0, float* dst) __attribute__((always_inline)) {
+      if constexpr (DUMP) return;
       if (wave == 0) buf4_to_lds(rs, dst, (uint32_t)lane * 4, (uint32_t)n0 * 4);
     };
 
@@ -866,6 +593,22 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       }
     };
 
+    // DUMP: the int32 scores of half s of tile t (keys n_beg + 64t + 32s ..),
+    // stored where the tile is live for the wave; lane (h, l32) holds query
+    // mq and keys 8(r / 4) + 4h + r % 4 of the half
+    auto dump = [&](int g, const v16i& sc, int t, int s) __attribute__((always_inline)) {
+      if constexpr (DUMP) {
+        if (!live(t) || !m_ok[g]) return;
+        int32_t* row = a.scores + ((int64_t)bh * M + mq[g]) * N;
+        const int nb = n_beg + t * BN + 32 * s + 4 * h;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int n = nb + 8 * (r >> 2) + (r & 3);
+          if (n < N) row[n] = sc[r];
+        }
+      }
+    };
+
     xblk xA, xB;  // scores of the last two halves (alternating)
     pblk pA, pB;  // P of the last two halves (alternating)
     // One half-step, a single straight-line block per variant: xi/p1 = the
@@ -877,6 +620,8 @@ attn_fwd_wide_kernel(const FwdArgs a) {
                          pblk& p2) __attribute__((always_inline)) {
       v16i sc[NG];
       half_qk(kt, s, sc);
+#pragma unroll
+      for (int g = 0; g < NG; ++g) dump(g, sc[g], j, s);
       half_pv(vt, s, p2);
       half_probs(xi, p1);
       half_scores(sc, st, j, s, mask, dead, xo);
@@ -898,7 +643,7 @@ attn_fwd_wide_kernel(const FwdArgs a) {
     // slice of the VALU work (P of half h-1, then the scores of half h), so
     // the matrix core never waits on an LDS round trip and the VALU runs
     // under the MFMAs. Same operations as half_step, in a fixed issue order.
-    auto half_step_fast = [&](int s, const int8_t* kt, const float* st, const uint16_t* vt,
+    auto half_step_fast = [&](int j, int s, const int8_t* kt, const float* st, const uint16_t* vt,
                               xblk& xi, pblk& p1, xblk& xo, pblk& p2) __attribute__((always_inline)) {
       typedef short v4s __attribute__((ext_vector_type(4)));
       typedef short v8s __attribute__((ext_vector_type(8)));
@@ -973,6 +718,7 @@ attn_fwd_wide_kernel(const FwdArgs a) {
         }
         __builtin_amdgcn_sched_barrier(0);
       }
+      dump(0, sc, j, s);
       }
     };
 
@@ -1167,10 +913,10 @@ attn_fwd_wide_kernel(const FwdArgs a) {
         if constexpr (FAST) {
           // a masked half, or one that may fix some row's reference point,
           // gets its mask / settle after the straight-line part
-          half_step_fast(0, kcur, scur, vprev, xB, pB, xA, pA);
+          half_step_fast(j, 0, kcur, scur, vprev, xB, pB, xA, pA);
           if (mask || !all_set) half_fixup(j, 0, mask, dead, xA);
           copies();
-          half_step_fast(1, kcur, scur, vprev, xA, pA, xB, pB);
+          half_step_fast(j, 1, kcur, scur, vprev, xA, pA, xB, pB);
           if (mask || !all_set) half_fixup(j, 1, mask, dead, xB);
         } else {
           half_step(j, 0, kcur, scur, vprev, mask, dead, xB, pB, xA, pA);
@@ -1231,13 +977,14 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       }
       if (j <= ntiles) body(j, sm_k0, sm_k1, sm_v0, sm_v1, sm_s0, sm_s1);
 
-      if (!__syncthreads_or(ovf ? 1 : 0)) break;
+      if (DUMP || !__syncthreads_or(ovf ? 1 : 0)) break;
       // QK-only sweep for the exact row max (the whole workgroup takes part)
       sweep();
     }
 
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
+      if constexpr (DUMP) break;
       const float l = l_lane[g] + __shfl_xor(l_lane[g], 32, 64);
       if (m_ok[g]) {
         const float inv = (l > 0.f) ? 1.f / l : 0.f;
@@ -1308,12 +1055,6 @@ void dispatch_wide(const FwdArgs& a, int grid, bool causal, bool lse, hipStream_
   }
 }
 
-template <int D, bool CAUSAL, int VDT, bool DUMP, bool LSE>
-void launch_fwd(const FwdArgs& a, int grid, hipStream_t st) {
-  attn_fwd_kernel<D, CAUSAL, VDT, DUMP, LSE><<<grid, FWD_THREADS, 0, st>>>(a);
-}
-
-
 int64_t npad_of(int64_t N) { return (N + BN - 1) / BN * BN; }
 
 
@@ -1328,19 +1069,24 @@ int check_fwd_shape(int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N, in
   return SL8_OK;
 }
 
-FwdArgs make_args(int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N, int& grid) {
+// launch geometry of the production kernel for (padded) head dim DP: query
+// blocks of wide_bm(DP) rows; causal launches pair block qb with nqb-1-qb, so
+// the grid holds (nqb + 1) / 2 slots per head
+FwdArgs make_args(int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N, int64_t DP,
+                  bool causal, int& grid) {
   FwdArgs a{};
   a.M = (int)M;
   a.N = (int)N;
   a.Npad = (int)npad_of(N);
   a.Hq = (int)Hq;
   a.Hkv = (int)Hkv;
-  a.nqb = (int)((M + BM - 1) / BM);
+  a.nqb = (int)((M + wide_bm(DP) - 1) / wide_bm(DP));
   a.window_left = -1;
   a.diag = (int)(N - M);
   a.dout = 0;  // set by the callers
-  grid = (int)(B * Hq * a.nqb);  // causal kernels halve this (paired query blocks)
-  a.xcd_map = xcd_mode(B * Hkv, Hq / Hkv, a.nqb);  // non-causal slot count
+  const int nslot = causal ? (a.nqb + 1) / 2 : a.nqb;
+  grid = (int)(B * Hq * nslot);
+  a.xcd_map = xcd_mode(B * Hkv, Hq / Hkv, nslot);
   return a;
 }
 
@@ -1418,7 +1164,7 @@ int pad_operands(const int8_t* q, const int8_t* k, const void* v, const float* v
   char* vsp = w;
   int rc = pad_rows(q, qp, B * Hq * M, D, DP, st);
   if (!rc) rc = pad_rows(k, kp, B * Hkv * N, D, DP, st);
-  if (!rc) rc = pad_rows(v, vp, B * Hkv * N, D * v_bytes, DP * v_bytes, st);
+  if (!rc && v) rc = pad_rows(v, vp, B * Hkv * N, D * v_bytes, DP * v_bytes, st);
   if (!rc && vs) {
     rc = pad_rows(vs, vsp, B * Hkv, D * 4, DP * 4, st);
     w += align256((size_t)(B * Hkv * DP * 4));
@@ -1479,16 +1225,12 @@ int w8a8_wide_launch(const int8_t* q, const float* q_scale, const int8_t* k, con
     SL8_CHECK_LAUNCH("attn_w8a8_fwd v to bf16 V^T");
   }
   int grid;
-  FwdArgs a = make_args(B, Hq, Hkv, M, N, grid);
+  FwdArgs a = make_args(B, Hq, Hkv, M, N, D, causal, grid);
   a.q = q; a.qs = q_scale; a.k = k; a.ks = k_scale;
   a.vt = vt; a.vs = v_scale; a.out = out; a.lse = nullptr;
   a.diag = (int)causal_diag;
   a.dout = (int)dout;
   a.w8_excess = w8_excess_for(N);
-  a.nqb = (int)((M + wide_bm(D) - 1) / wide_bm(D));
-  const int nslot = causal ? (a.nqb + 1) / 2 : a.nqb;
-  grid = (int)(B * Hq * nslot);
-  a.xcd_map = xcd_mode(B * Hkv, Hq / Hkv, nslot);
   constexpr int F = SL8_DTYPE_BF16;
   if (D == 64) {
     if (causal) launch_wide<64, true, F, false, true>(a, grid, st);
@@ -1543,18 +1285,14 @@ int attn_int8_fwd_impl(const int8_t* q, const float* q_scale, const int8_t* k,
     k = p.k;
     v = p.v;
   }
+  const bool c = causal != 0, want_lse = lse != nullptr;
   int grid;
-  FwdArgs a = make_args(B, Hq, Hkv, M, N, grid);
+  FwdArgs a = make_args(B, Hq, Hkv, M, N, DP, c, grid);
   a.q = q; a.qs = q_scale; a.k = k; a.ks = k_scale;
   a.vt = static_cast<const uint16_t*>(v);  // V [B*Hkv][N][DP], read in place
   a.out = out; a.lse = lse; a.window_left = (int)window_left;
   a.dout = (int)D;
   a.skip = skip;
-  const bool c = causal != 0, want_lse = lse != nullptr;
-  a.nqb = (int)((M + wide_bm(DP) - 1) / wide_bm(DP));
-  const int nslot = c ? (a.nqb + 1) / 2 : a.nqb;
-  grid = (int)(B * Hq * nslot);
-  a.xcd_map = xcd_mode(B * Hkv, Hq / Hkv, nslot);
   const bool f16 = v_dtype == SL8_DTYPE_F16;
   if (DP == 64) {
     if (f16) dispatch_wide<64, SL8_DTYPE_F16>(a, grid, c, want_lse, st);
@@ -1596,24 +1334,49 @@ extern "C" int sl8_attn_int8_fwd_gated(const int8_t* q, const float* q_scale, co
 
 extern "C" int sl8_attn_int8_qk_scores(const int8_t* q, const int8_t* k, int32_t* scores,
                                        int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N,
-                                       int64_t D, void* stream) {
+                                       int64_t D, int causal, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
   clear_error();
   int rc = check_fwd_shape(B, Hq, Hkv, M, N, D);
   if (rc) return rc;
-  SL8_CHECK_ARG(D == 64 || D == 128, "fni8: qk_scores supports head dim 64/128");
   if (B == 0 || Hq == 0 || M == 0 || N == 0) return SL8_OK;
   SL8_CHECK_ARG(q && k && scores, "fni8: null pointer");
   SL8_CHECK_ARG(aligned(q, 16) && aligned(k, 16), "fni8: q/k must be 16-byte aligned");
-  int grid;
-  FwdArgs a = make_args(B, Hq, Hkv, M, N, grid);
-  a.q = q; a.k = k; a.scores = scores;
-  // The dump path never reads V or the scales.
-  a.vt = nullptr;
-  a.qs = nullptr;
-  a.ks = nullptr;
+  const size_t need = sl8_attn_int8_fwd_workspace(B, Hq, Hkv, M, N, D);
+  SL8_CHECK_ARG(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 16)),
+                "fni8: attn_int8_qk_scores workspace needs %zu bytes", need);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (D == 64) launch_fwd<64, false, SL8_DTYPE_F16, true, false>(a, grid, st);
-  else launch_fwd<128, false, SL8_DTYPE_F16, true, false>(a, grid, st);
+  const int64_t DP = padded_head_dim(D);
+  if (DP != D) {  // zero channels add nothing to the int32 sums
+    Padded p;
+    rc = pad_operands(q, k, nullptr, nullptr, B, Hq, Hkv, M, N, D, 2, workspace, st, p);
+    if (rc) return rc;
+    q = p.q;
+    k = p.k;
+  }
+  const bool c = causal != 0;
+  int grid;
+  FwdArgs a = make_args(B, Hq, Hkv, M, N, DP, c, grid);
+  a.q = q; a.k = k; a.scores = scores;
+  a.dout = (int)D;
+  // V and the scales are never read by the dump instantiation
+  constexpr int F = SL8_DTYPE_F16;
+  if (DP == 64) {
+    if (c) attn_fwd_wide_kernel<64, true, F, false, wide_ng(64), wide_waves(64), false, true>
+        <<<grid, wide_waves(64) * 64, 0, st>>>(a);
+    else attn_fwd_wide_kernel<64, false, F, false, wide_ng(64), wide_waves(64), false, true>
+        <<<grid, wide_waves(64) * 64, 0, st>>>(a);
+  } else if (DP == 128) {
+    if (c) attn_fwd_wide_kernel<128, true, F, false, wide_ng(128), wide_waves(128), false, true>
+        <<<grid, wide_waves(128) * 64, 0, st>>>(a);
+    else attn_fwd_wide_kernel<128, false, F, false, wide_ng(128), wide_waves(128), false, true>
+        <<<grid, wide_waves(128) * 64, 0, st>>>(a);
+  } else {
+    if (c) attn_fwd_wide_kernel<256, true, F, false, wide_ng(256), wide_waves(256), false, true>
+        <<<grid, wide_waves(256) * 64, 0, st>>>(a);
+    else attn_fwd_wide_kernel<256, false, F, false, wide_ng(256), wide_waves(256), false, true>
+        <<<grid, wide_waves(256) * 64, 0, st>>>(a);
+  }
   SL8_CHECK_LAUNCH("attn_int8_qk_scores");
   return SL8_OK;
 }

@@ -431,6 +431,13 @@ class FQReader:
 
     def get_qtensor(self, name: str, device="cpu") -> QTensor:
         e = self.header["tensors"][name]
+        scheme, codebook = e.get("scheme", "raw"), e.get("codebook", "")
+        if scheme not in SCHEMES:
+            raise ValueError(f"superl8 format: unsupported scheme {scheme!r} on {name!r} "
+                             f"(this build runs {', '.join(SCHEMES)})")
+        if scheme == "gguf_kquant" and codebook not in GGUF_KQUANT_BLOCK:
+            raise ValueError(f"superl8 format: unsupported gguf_kquant type {codebook!r} on "
+                             f"{name!r} (this build runs {', '.join(GGUF_KQUANT_BLOCK)})")
         scale = self.get(e["scale"], device) if e.get("scale") else None
         return QTensor(self.get(name, device), scale, e["scheme"], bool(e.get("rotated", False)),
                        int(e.get("hadamard_dim", 0)), bool(e.get("smoothed", False)),

@@ -43,17 +43,65 @@ def _fp32_oracle(q, k, v, causal=False):
     return oa.attention_fp64(_np(q.float()), _np(k.float()), _np(v.float()), causal)
 
 
-QK_SHAPES = [(1, 2, 2, 128, 128, 64), (2, 4, 2, 257, 300, 64), (1, 4, 1, 1, 77, 128),
-             (1, 2, 2, 333, 129, 128), (1, 8, 8, 64, 1, 64)]
+QK_SHAPES = [  # B, Hq, Hkv, M, N, D: every head dim, ragged M/N, GQA
+    (1, 2, 2, 128, 128, 64), (2, 4, 2, 257, 300, 64), (1, 4, 1, 1, 77, 128),
+    (1, 2, 2, 333, 129, 128), (1, 8, 8, 64, 1, 64), (1, 4, 2, 200, 190, 32),
+    (2, 6, 3, 130, 97, 72), (1, 4, 1, 65, 513, 80), (1, 4, 2, 300, 333, 256),
+    (1, 8, 2, 1000, 1031, 128)]
+NOT_STORED = -(2 ** 31)  # |int32 score| <= 256 * 127^2, so this is never a real score
 
 
+def _check_scores(s, q_i8, k_i8, causal, heads=None):
+    """Every stored score equals the exact integer Q.K^T, and (causal) every
+    score the mask lets through was stored."""
+    s, q_i8, k_i8 = _np(s), _np(q_i8), _np(k_i8)
+    Hq, M, N = s.shape[1], s.shape[2], s.shape[3]
+    gsz = Hq // k_i8.shape[1]
+    for h in (range(Hq) if heads is None else heads):
+        exact = oa.scores_i32(q_i8[:, h:h + 1], k_i8[:, h // gsz:h // gsz + 1])
+        got = s[:, h:h + 1]
+        if not causal:
+            np.testing.assert_array_equal(got, exact, err_msg=f"head {h}")
+            continue
+        stored = got != NOT_STORED
+        np.testing.assert_array_equal(got[stored], exact[stored], err_msg=f"head {h}")
+        vis = np.broadcast_to(oa.valid_mask(M, N, True), got.shape)
+        assert stored[vis].all(), f"head {h}: visible scores not computed"
+
+
+@pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("shape", QK_SHAPES)
-def test_qk_scores_bit_exact(device, shape):
+def test_qk_scores_bit_exact(device, shape, causal):
+    """int32 S from the production kernel (attn_fwd_wide_kernel's dump
+    instantiation) against the exact integer product (reference
+    attn_int8_fwd.cuh:127-138: dp4a int32 accumulation)."""
     B, Hq, Hkv, M, N, D = shape
     q = torch.randint(-127, 128, (B, Hq, M, D), device=device, dtype=torch.int8)
     k = torch.randint(-127, 128, (B, Hkv, N, D), device=device, dtype=torch.int8)
-    s = _C.attn_int8_qk_scores(q, k)
-    np.testing.assert_array_equal(_np(s), oa.scores_i32(_np(q), _np(k)))
+    s = _C.attn_int8_qk_scores(q, k, causal=causal, fill=NOT_STORED)
+    _check_scores(s, q, k, causal)
+
+
+def test_qk_scores_extreme_codes(device):
+    """All codes +-127 (the largest |sum| = D * 127^2) at D = 256 and 128."""
+    for D in (128, 256):
+        q = torch.full((1, 2, 70, D), 127, device=device, dtype=torch.int8)
+        k = torch.full((1, 1, 90, D), -127, device=device, dtype=torch.int8)
+        q[0, 1, ::2] = -127
+        s = _C.attn_int8_qk_scores(q, k)
+        _check_scores(s, q, k, False)
+        assert int(s.abs().max()) == D * 127 * 127
+
+
+def test_qk_scores_config2_head_subset(device):
+    """BASELINE config 2 (B1 Hq32 Hkv8 S4096 D128 causal) on 8 query heads (two
+    KV heads), K quantised with smoothing as the path does: bit-exact."""
+    torch.manual_seed(2)
+    q = torch.randn(1, 8, 4096, 128, device=device, dtype=torch.float16)
+    k = torch.randn(1, 2, 4096, 128, device=device, dtype=torch.float16)
+    q_i8, _, k_i8, _, _ = quant.quantize_qk(q, k)
+    s = _C.attn_int8_qk_scores(q_i8, k_i8, causal=True, fill=NOT_STORED)
+    _check_scores(s, q_i8, k_i8, True, heads=(0, 3, 4, 7))
 
 
 KERNEL_CASES = [
@@ -199,17 +247,19 @@ def test_accuracy_gate_and_rotate(device, monkeypatch):
 
 
 def test_config2_shape_against_oracle(device):
-    """BASELINE config 2 (B1 Hq32 Hkv8 S4096 D128 causal), checked on a head subset."""
+    """BASELINE config 2 (B1 Hq32 Hkv8 S4096 D128 causal), checked on 8 of the 32
+    heads (every KV head once, both heads of KV head 3)."""
     torch.manual_seed(2)
     q, k, v = _qkv(1, 32, 8, 4096, 4096, 128, device)
     q_i8, qs, k_i8, ks, _ = quant.quantize_qk(q, k)
     qs, ks = qs.squeeze(-1).contiguous(), ks.squeeze(-1).contiguous()
     out = _C.attn_int8_fwd(q_i8, qs, k_i8, ks, v, True)
-    for h in (0, 13, 31):
+    for h in (0, 5, 10, 13, 14, 19, 26, 31):
         kvh = h // 4
         ref, _ = oa.attn_int8_fwd(_np(q_i8[:, h:h + 1]), _np(qs[:, h:h + 1]),
                                   _np(k_i8[:, kvh:kvh + 1]), _np(ks[:, kvh:kvh + 1]),
                                   _np(v[:, kvh:kvh + 1].float()), True)
+        assert_close_abs(out[:, h:h + 1], ref, atol=1e-2, what=f"config2 head {h}")
         assert_int8_quality(out[:, h:h + 1], ref, min_cos=0.9999, max_rel_l1=3e-3, min_sqnr_db=40,
                             what=f"config2 head {h}")
 

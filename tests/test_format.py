@@ -142,6 +142,26 @@ def test_literal_reference_tagged_file(tmp_path, streaming):
         assert r.verify()
 
 
+@pytest.mark.parametrize("scheme,codebook,msg", [
+    ("per_group_i4", "", "unsupported scheme 'per_group_i4'"),
+    ("gguf_kquant", "q2_k", "unsupported gguf_kquant type 'q2_k'"),
+])
+def test_reference_tagged_unsupported_scheme_rejected(tmp_path, scheme, codebook, msg):
+    """A reference-tagged file whose tensor uses a scheme this build does not run
+    reads (header, raw blobs) but get_qtensor refuses it with a clear error."""
+    data = np.arange(16, dtype=np.uint8)
+    ent = {"w": {"dtype": "uint8", "shape": [2, 8], "offset": 0, "nbytes": 16,
+                 "crc32": zlib.crc32(data.tobytes()), "scheme": scheme, "scale": None,
+                 "rotated": False, "hadamard_dim": 0, "smoothed": False, "group_size": 32,
+                 "codebook": codebook}}
+    p = tmp_path / "unsup.superl8"
+    p.write_bytes(_literal(ent, [(0, data.tobytes())], streaming=False))
+    with FQReader(str(p)) as r:
+        np.testing.assert_array_equal(r.get("w").numpy().ravel(), data)
+        with pytest.raises(ValueError, match=msg):
+            r.get_qtensor("w")
+
+
 def test_sm70_target_writes_reference_tags(tmp_path):
     p = tmp_path / "m.superl8"
     _write(p, _tensors(), True, target="sm70")

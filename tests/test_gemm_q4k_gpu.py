@@ -153,3 +153,20 @@ def test_rejects_bad_k(device):
     with pytest.raises(RuntimeError, match="M<=16"):
         _C.gemm_decode_q4k(torch.zeros(17, 256, device=device, dtype=torch.int8),
                            torch.ones(17, device=device), blk[:, :144].contiguous())
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_gemv_per_row_scale_shaped_m1(device, M):
+    """A per-row x_scale shaped [M, 1] at K = 1024 is the reference's per-row scale
+    (numel == M), not per-256-block scales: same result as x_scale [M]."""
+    N, K = 96, 1024
+    x, w, wd = _case(M, N, K, seed=M + 5, device=device)
+    x_i8, xs = _C.quantize_i8_rowwise(x)
+    y_flat = _C.gemm_decode_q4k(x_i8, xs, wd, torch.float32)
+    y_col = _C.gemm_decode_q4k(x_i8, xs.reshape(M, 1).contiguous(), wd, torch.float32)
+    assert torch.equal(y_flat, y_col)
+    ref = oq.gemv(_np(x_i8), _np(xs), w, K)
+    err = np.abs(_np(y_col).astype(np.float64) - ref)
+    assert (err <= 1e-5 * np.abs(ref) + 1e-5 * np.abs(ref).max()).all()
+    with pytest.raises(RuntimeError, match=r"\[M\] \(per row\) or \[M, K/256\]"):
+        _C.gemm_decode_q4k(x_i8, torch.ones(M, 3, device=device), wd, torch.float32)
