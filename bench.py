@@ -379,12 +379,13 @@ def cpu_baseline(budget_s=12.0):
         t0 = time.perf_counter()
         run()
         samples.append(time.perf_counter() - t0)
-    limiter.unregister()
     samples.sort()
     k_trim = max(1, len(samples) // 10) if len(samples) > 4 else 0
     trimmed = samples[k_trim:len(samples) - k_trim] if k_trim else samples
     med = float(np.median(trimmed))
     ops = 4 * 1 * 8 * 512 * 512 * 64 // 2
+    secondary = cpu_secondary()
+    limiter.unregister()
     return {
         "value": round(ops / med / 1e9, 3),
         "unit": "GOPS",
@@ -394,7 +395,52 @@ def cpu_baseline(budget_s=12.0):
         "kind": "port",
         "sample": f"config 1 (B1 H8 S512 D64 causal, quantize_qk + attention), numpy oracle, "
                   f"{len(samples)} runs, trimmed median {med * 1e3:.1f} ms/run",
+        "secondary": secondary,
     }
+
+
+def _median_time(fn, runs):
+    fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts))
+
+
+def cpu_secondary(runs=3):
+    """The decode and GEMV lines' CPU counterparts (numpy oracle, same byte
+    accounting as the GPU lines): config 3 decode on one of its 16 sequences
+    (the per-sequence work is identical), config 4's Q4_K GEMV at full size."""
+    from oracle import attention as oa
+    from oracle import q4k as oq
+    from oracle import quant as oqn
+
+    out = {}
+    rng = np.random.default_rng(3)
+    Hq, Hkv, N, D = 32, 8, 32768, 128
+    q = rng.integers(-127, 128, (1, Hq, D)).astype(np.int8)
+    qs = np.full((1, Hq), 1e-3, np.float32)
+    k = rng.integers(-127, 128, (1, Hkv, N, D)).astype(np.int8)
+    ks = (rng.random((1, Hkv, N)) * 0.02).astype(np.float32)
+    v16 = rng.standard_normal((1, Hkv, N, D)).astype(np.float16)
+    v = v16.astype(np.float32)  # fp16 values; the conversion is outside the timing
+    t = _median_time(lambda: oa.attn_int8_decode(q, qs, k, ks, v, 16), runs)
+    nbytes = k.size + ks.size * 4 + v16.size * 2 + q.size + qs.size * 4 + Hq * D * 2
+    out["attn_int8_decode_cfg3_one_sequence"] = {
+        "ms": round(t * 1e3, 1), "GB/s": round(nbytes / t / 1e9, 3), "bytes": int(nbytes)}
+    del k, v, v16
+    N4, K4 = 17408, 5120
+    w = oq.random_weights(N4, K4, seed=4)
+    for M in (1, 8):
+        x = rng.standard_normal((M, K4)).astype(np.float16).astype(np.float32)
+        xi, xsc = oqn.quantize_rows(x)
+        t = _median_time(lambda: oq.gemv(xi, xsc, w, K4), runs)
+        nbytes = N4 * (K4 // 256) * 144 + M * K4 + M * 4 + M * N4 * 2
+        out[f"gemm_decode_q4k_cfg4_m{M}"] = {
+            "ms": round(t * 1e3, 1), "GB/s": round(nbytes / t / 1e9, 3), "bytes": int(nbytes)}
+    return out
 
 
 def main():
@@ -404,9 +450,16 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
+                    help="summarise a rocprofv3 --kernel-trace CSV of a `--no-secondary` run "
+                         "(the timed calls = the prefill kernel's last --steps dispatches) "
+                         "and exit; runs without a GPU")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 256 MiB device copy (scale for PMC byte counters)")
     args = ap.parse_args()
+    if args.trace_summary:
+        print(trace_summary(args.trace_summary, args.steps))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(see the sharding plan in DESIGN.md); run with --gpus 1", file=sys.stderr)
@@ -524,8 +577,68 @@ def main():
         sec["hbm_copy_256MiB_GBps"] = round(bench_copy(), 1)
         out["secondary"] = sec
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline()
+        cb = cpu_baseline()
+        # GPU-over-CPU ratios of the same metric (a baseline, not a target)
+        cb["gpu_over_cpu"] = {"attn_int8_fwd": round(out["value"] * 1e3 / cb["value"], 1)}
+        sec = out.get("secondary", {})
+        for key, gkey in (("attn_int8_decode_cfg3_one_sequence", "attn_int8_decode_cfg3"),
+                          ("gemm_decode_q4k_cfg4_m1", "gemm_decode_q4k_cfg4_m1"),
+                          ("gemm_decode_q4k_cfg4_m8", "gemm_decode_q4k_cfg4_m8")):
+            if gkey in sec:
+                cb["gpu_over_cpu"][gkey] = round(sec[gkey]["GB/s"] / cb["secondary"][key]["GB/s"], 1)
+        out["cpu_baseline"] = cb
     print(json.dumps(out), flush=True)
+
+
+PREFILL_KERNEL = "attn_fwd_wide_kernel<128, true, 0, false, 1, 8, false, false>"
+
+
+def _short_kernel_name(name: str) -> str:
+    """'void sl8::(anonymous namespace)::k<..>(sl8::..)' -> 'k<..>' (full template
+    arguments kept)."""
+    import re
+
+    name = re.sub(r"^void ", "", name)
+    name = re.sub(r"sl8::\(anonymous namespace\)::", "", name)
+    name = name.replace("(anonymous namespace)", "anon")
+    depth, end = 0, len(name)
+    for i, ch in enumerate(name):  # cut the parameter list after the template arguments
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            end = i
+            break
+    return name[:end]
+
+
+def trace_summary(path: str, steps: int) -> str:
+    """Markdown table from a rocprofv3 kernel-trace CSV. Every dispatch is listed
+    per kernel (count, mean, median, min, max); for the config 2 prefill kernel the
+    timed calls of `bench.py --no-secondary --steps K` are its last K dispatches
+    (the spin-up and warmup calls come first), reported separately."""
+    import csv
+
+    by = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            n = _short_kernel_name(r["Kernel_Name"])
+            t0, t1 = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+            by.setdefault(n, []).append((t0, (t1 - t0) / 1e3))
+    lines = ["| kernel | calls | mean us | median us | min us | max us |", "|---|---|---|---|---|---|"]
+    for n, v in sorted(by.items(), key=lambda kv: -sum(d for _, d in kv[1])):
+        d = [x for _, x in v]
+        lines.append(f"| {n} | {len(d)} | {np.mean(d):.2f} | {np.median(d):.2f} | {min(d):.2f} | "
+                     f"{max(d):.2f} |")
+    if PREFILL_KERNEL in by:
+        v = sorted(by[PREFILL_KERNEL])[-steps:]
+        d = [x for _, x in v]
+        span = (v[-1][0] - v[0][0]) / 1e3 / max(1, len(v) - 1) if len(v) > 1 else float("nan")
+        lines += ["", f"Timed calls ({len(d)}: the last {steps} dispatches of `{PREFILL_KERNEL}`): "
+                      f"mean {np.mean(d):.2f} us, median {np.median(d):.2f} us, min {min(d):.2f}, "
+                      f"max {max(d):.2f}; start-to-start spacing {span:.2f} us."]
+    return "\n".join(lines)
 
 
 def _traffic(kernel: str):

@@ -15,6 +15,7 @@ import torch
 
 import superl8_amd as sl8
 from oracle import attention as oa
+from oracle import quant as oqn
 from superl8_amd import _C, quant
 from tests.tolerances import assert_close_abs, assert_finite, assert_int8_quality
 
@@ -60,19 +61,33 @@ def _config5_inputs(device):
 C5_BLOCKS = [(0, 0, 0), (0, 3, 4096), (0, 9, 8128), (1, 8, 2048), (1, 15, 6080), (1, 1, 8128)]
 
 
+@pytest.mark.parametrize("qk_quant", ["per_row", "per_wave"])
 @pytest.mark.parametrize("per_warp", [True, False])
-def test_config5_w8a8_full_shape(device, per_warp):
+def test_config5_w8a8_full_shape(device, per_warp, qk_quant):
+    """per_wave: config 5's own text, Q/K quantised per wavefront tile (32 queries,
+    64 keys) by quantize_qk_per_wave; its codes are checked bit-exact against the
+    oracle on the compared rows' heads before the attention is."""
     q, k, v = _config5_inputs(device)
     Hq, Hkv = q.shape[1], k.shape[1]
     gsz = Hq // Hkv
-    q_i8, qs, k_i8, ks, _ = quant.quantize_qk(q, k)
+    if qk_quant == "per_wave":
+        q_i8, qs, k_i8, ks, _ = quant.quantize_qk_per_wave(q, k)
+        for b, h, _r0 in C5_BLOCKS[:2]:
+            kv = h // gsz
+            r = oqn.quantize_qk_per_wave(_np(q[b:b + 1, h:h + 1]), _np(k[b:b + 1, kv:kv + 1]))
+            np.testing.assert_array_equal(_np(q_i8[b:b + 1, h:h + 1]), r[0])
+            np.testing.assert_array_equal(_np(qs[b:b + 1, h:h + 1, :, 0]), r[1])
+            np.testing.assert_array_equal(_np(k_i8[b:b + 1, kv:kv + 1]), r[2])
+            np.testing.assert_array_equal(_np(ks[b:b + 1, kv:kv + 1, :, 0]), r[3])
+    else:
+        q_i8, qs, k_i8, ks, _ = quant.quantize_qk(q, k)
     qs, ks = qs.squeeze(-1).contiguous(), ks.squeeze(-1).contiguous()
     v_i8, vs = _C.quantize_v_perchannel(v)
     vs = vs.squeeze(-2).contiguous()
     out = _C.attn_w8a8_fwd(q_i8, qs, k_i8, ks, v_i8, vs, True, 0, per_warp)
     assert_finite(out)
     # the public API with the gate bypassed runs the same kernel
-    if per_warp:
+    if per_warp and qk_quant == "per_row":
         pub = sl8.attn_int8_fwd(q, k, v, causal=True, int8_pv=True, internal_accuracy_gate=False)
         assert torch.equal(pub, out)
     del q, k, v

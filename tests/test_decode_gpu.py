@@ -5,6 +5,7 @@ import torch
 
 import superl8_amd as sl8
 from oracle import attention as oa
+from oracle import quant as oqn
 from superl8_amd import _C, quant
 from tests.tolerances import assert_close_abs, assert_finite, assert_int8_quality
 
@@ -103,21 +104,35 @@ def test_deterministic_and_validation(device):
     assert not empty.any()
 
 
-def test_config3_shape_against_oracle(device):
-    """BASELINE config 3 (B16 Hq32 Hkv8 N32768 D128, 16 splits), checked on 2 sequences."""
+@pytest.mark.parametrize("ks16", [False, True])
+def test_config3_shape_against_oracle(device, ks16):
+    """BASELINE config 3 (B16 Hq32 Hkv8 N32768 D128, 16 splits) as the config
+    states it: the K cache is N(0,1) fp16 K quantised per token (codes and scales
+    checked bit-exact against the oracle on the compared sequences), its scales
+    kept as fp32 (the reference contract) or fp16 (the config text); checked on
+    2 sequences."""
     torch.manual_seed(3)
     B, Hq, Hkv, N, D = 16, 32, 8, 32768, 128
     q = torch.randn(B, Hq, 1, D, device=device, dtype=torch.float16)
-    k_i8 = torch.randint(-127, 128, (B, Hkv, N, D), device=device, dtype=torch.int8)
-    ks = torch.rand(B, Hkv, N, device=device) * 0.02
+    k = torch.randn(B, Hkv, N, D, device=device, dtype=torch.float16)
     v = torch.randn(B, Hkv, N, D, device=device, dtype=torch.float16)
+    k_i8, ks = _C.quantize_i8_rowwise(k.reshape(-1, D))
+    k_i8, ks = k_i8.reshape(B, Hkv, N, D), ks.reshape(B, Hkv, N)
+    for b in (0, 15):
+        rq, rs = oqn.quantize_rows(_np(k[b].float()).reshape(-1, D))
+        np.testing.assert_array_equal(_np(k_i8[b]).reshape(-1, D), rq)
+        np.testing.assert_array_equal(_np(ks[b]).reshape(-1), rs)
+    del k
+    if ks16:
+        ks = ks.half()
     q_i8, qs = _C.quantize_i8_rowwise(q.reshape(-1, D))
     qs = (qs * 0.1275).reshape(B, Hq, 1).contiguous()
     q_i8 = q_i8.reshape(B, Hq, 1, D)
     out = _C.attn_int8_decode(q_i8, qs, k_i8, ks, v, 16)
     for b in (0, 15):
         ref = oa.attn_int8_decode(_np(q_i8[b:b + 1])[:, :, 0], _np(qs[b:b + 1])[:, :, 0],
-                                  _np(k_i8[b:b + 1]), _np(ks[b:b + 1]), _np(v[b:b + 1].float()), 16)
+                                  _np(k_i8[b:b + 1]), _np(ks[b:b + 1].float()),
+                                  _np(v[b:b + 1].float()), 16)
         assert_close_abs(out[b:b + 1, :, 0], ref, atol=2e-3, rtol=2e-3, what=f"config3 b={b}")
 
 
@@ -172,7 +187,6 @@ def test_decode_cached_rejects(device):
 # ---------------------------------------------------------------------------
 # Paged int8 KV cache (reference attn_paged_decode.cuh, ops.py:730-849)
 # ---------------------------------------------------------------------------
-from oracle import quant as oqn  # noqa: E402
 
 PAGED_CASES = [  # B, Hq, Hkv, D, block_size, lens
     (2, 8, 2, 64, 16, (50, 7)), (3, 32, 8, 128, 16, (1000, 1, 333)), (1, 16, 4, 256, 32, (257,)),
