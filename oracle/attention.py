@@ -53,6 +53,33 @@ def logits(acc: np.ndarray, q_scale: np.ndarray, k_scale: np.ndarray, Hq: int) -
     return (t * ks[..., None, :].astype(np.float32)).astype(np.float32)
 
 
+SEED_BITS = 0x3E22F983  # the float 1/(2 pi) rounded to fp32
+
+
+def seeded_logits(acc: np.ndarray, q_scale: np.ndarray, k_scale: np.ndarray,
+                  m: np.ndarray | float = 0.0) -> np.ndarray:
+    """The D <= 128 prefill kernel's exp2 argument from a seeded accumulator
+    (this build's formulation; the reference computes ((float)acc * qs) * ks,
+    attn_int8_fwd.cuh:141-150): the int8 MFMA starts from the bits of
+    C0 = fp32(1/(2 pi)), so its int32 result read as a float is
+    f = C0 + acc * 2^-26 exactly (|acc| <= 2^21); then
+        w = fma(f, qs * 2^26, -rn(C0 * qs * 2^26)),   x = fma(w, ks, -m)
+    with single fp32 roundings (evaluated here in float64, which holds the
+    products exactly, then rounded once to fp32; the sums of a 48-bit product
+    and a float are exact in float64 when their exponents are close, which the
+    tests' bound allows for). acc int [..], q_scale/k_scale broadcastable fp32."""
+    acc = np.asarray(acc, np.int64)
+    assert np.all(np.abs(acc) <= 1 << 21), "seeded accumulator range is |acc| <= 2^21"
+    f = (acc + SEED_BITS).astype(np.uint32).view(np.float32).astype(np.float64)
+    qs26 = (np.asarray(q_scale, np.float32) * np.float32(2.0 ** 26)).astype(np.float32)
+    c0 = np.uint32(SEED_BITS).view(np.float32)
+    cq = (-(c0 * qs26)).astype(np.float32)
+    w = (f * qs26.astype(np.float64) + cq.astype(np.float64)).astype(np.float32)
+    x = (w.astype(np.float64) * np.asarray(k_scale, np.float32).astype(np.float64)
+         - np.float64(np.float32(m))).astype(np.float32)
+    return x
+
+
 def valid_mask(M: int, N: int, causal: bool, window_left: int = -1,
                causal_diag: int | None = None) -> np.ndarray:
     """[M,N] bool. Query i sits at key position i + (N - M) when causal."""

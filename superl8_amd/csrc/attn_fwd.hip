@@ -41,6 +41,19 @@ namespace {
 
 constexpr int BN = 64;   // keys per tile
 constexpr float LN2F = 0.6931471805599453f;
+// Seeded QK accumulator of the D = 128 straight-line path: the int8 MFMA
+// starts from the bit pattern of C0 = 1/(2 pi) (0x3E22F983, an inline
+// constant of the MFMA's C operand, so no register has to be set), so the
+// accumulator holds the integer C0BITS + acc. C0 lies in the binade
+// [2^-3, 2^-2), whose float spacing is 2^-26, 2,292,099 steps above its
+// lower end and 6,096,509 below its upper end: for |acc| <= 128 * 128^2 =
+// 2,097,152 (D <= 128, any int8 codes) the bits read as the float
+// C0 + acc * 2^-26 exactly, so no int -> float conversion is needed:
+//   w = fma(f, q_scale * 2^26, -rn(C0 * q_scale * 2^26)) = q_scale * (acc + d),
+//   |d| <= 2^-24 * C0 * 2^26 * (1 + 2^-23) ~ 0.64 (the rounding of the constant),
+// and then x = fma(w, k_scale, -m): the exp2 argument in two fmas.
+constexpr int C0BITS = 0x3E22F983;
+constexpr float C0F = 0.15915494309189535f;  // the float with bits C0BITS
 #ifndef SL8_W8_LAZY
 #define SL8_W8_LAZY 1
 #endif
@@ -317,6 +330,9 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       }
       qsc[g] = (m_ok[g] && !DUMP) ? a.qs[(int64_t)bh * M + mq[g]] : 1.f;
     }
+    // seeded-accumulator constants of the straight-line path (see C0BITS)
+    const float qs26 = qsc[0] * 67108864.f;  // q_scale * 2^26, exact
+    const float cq26 = -(C0F * qs26);
 
     int n_end = N;
     if (CAUSAL) n_end = max(0, min(N, m_blk + WBM + diag));
@@ -667,15 +683,16 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       float4 kv[4];
       v16i sc;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sc[r] = 0;
+      for (int r = 0; r < 16; ++r) sc[r] = C0BITS;
       v4i opb[NOP];  // operand i is read SL8_FWD_PD MFMAs ahead of its use
 #pragma unroll
       for (int i = 0; i < SL8_FWD_PD && i < NOP; ++i) opb[i] = load_op(i);
       // Issue order, fixed by scheduling barriers: MFMA i is preceded by the
       // read of operand i + SL8_FWD_PD and followed by a slice of VALU work --
-      //   QK MFMAs 0..3: P of half h-1, four exp2 each;
+      //   QK MFMAs 0..3: P of half h-1, four exp2 each (xi holds the exp2 argument);
       //   PV MFMAs 0..1: pack P to fp16 + row sums (one 16-key step each);
-      //   PV MFMA 2: k_scale reads; PV MFMAs 3..6: scores of half h (cvt, * k_scale).
+      //   PV MFMA 2: k_scale reads; PV MFMAs 3..6: exp2 arguments of half h
+      //   (two fmas each from the seeded accumulator, see C0BITS).
 #pragma unroll
       for (int i = 0; i < NOP; ++i) {
         if (i + SL8_FWD_PD < NOP) opb[i + SL8_FWD_PD] = load_op(i + SL8_FWD_PD);
@@ -685,7 +702,7 @@ attn_fwd_wide_kernel(const FwdArgs a) {
           sc = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur, qop[0].c[i], sc, 0, 0, 0);
 #pragma unroll
           for (int e = 4 * i; e < 4 * i + 4; ++e) {
-            pe[e] = __builtin_amdgcn_exp2f(fmaf(xi[0][e], qsc[0], -msub));
+            pe[e] = __builtin_amdgcn_exp2f(xi[0][e]);  // -inf -> 0
             pin_vgpr(pe[e]);
           }
         } else {
@@ -708,17 +725,23 @@ attn_fwd_wide_kernel(const FwdArgs a) {
               kv[gq] = *reinterpret_cast<const float4*>(st + 32 * s + 8 * gq + 4 * h);
           } else if (k < 7) {
             const int gq = k - 3;
-            xo[0][4 * gq + 0] = (float)sc[4 * gq + 0] * kv[gq].x;
-            xo[0][4 * gq + 1] = (float)sc[4 * gq + 1] * kv[gq].y;
-            xo[0][4 * gq + 2] = (float)sc[4 * gq + 2] * kv[gq].z;
-            xo[0][4 * gq + 3] = (float)sc[4 * gq + 3] * kv[gq].w;
+            const float kk[4] = {kv[gq].x, kv[gq].y, kv[gq].z, kv[gq].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float w = fmaf(__int_as_float(sc[4 * gq + e]), qs26, cq26);
+              xo[0][4 * gq + e] = fmaf(w, kk[e], -msub);
+            }
 #pragma unroll
             for (int e = 0; e < 4; ++e) pin_vgpr(xo[0][4 * gq + e]);
           }
         }
         __builtin_amdgcn_sched_barrier(0);
       }
-      dump(0, sc, j, s);
+      if constexpr (DUMP) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sc[r] -= C0BITS;  // the bits hold C0BITS + acc
+        dump(0, sc, j, s);
+      }
       }
     };
 
@@ -812,6 +835,19 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       }
     };
 
+    // FAST path: xo already holds the exp2 argument logit - m (logit itself for a
+    // row whose reference point is not set yet); a row set here shifts its xo
+    auto settle_fast = [&](xblk& xo) __attribute__((always_inline)) {
+      if (__any(m_run[0] == -INFINITY)) {
+        float tmax[1];
+        half_max(xo, tmax);
+        if (m_run[0] == -INFINITY && tmax[0] != -INFINITY) {
+          m_run[0] = tmax[0];
+#pragma unroll
+          for (int e = 0; e < 16; ++e) xo[0][e] -= tmax[0];
+        }
+      }
+    };
     auto half_fixup = [&](int t, int s, bool do_mask, bool dead, xblk& xo) __attribute__((always_inline)) {
       if (do_mask) {
 #pragma unroll
@@ -828,7 +864,8 @@ attn_fwd_wide_kernel(const FwdArgs a) {
             xo[g][e] = (rel + (uint32_t)(8 * (e >> 2) + (e & 3)) < span) ? xo[g][e] : -INFINITY;
         }
       }
-      settle(xo);
+      if constexpr (FAST) settle_fast(xo);
+      else settle(xo);
       bool unset = false;
 #pragma unroll
       for (int g = 0; g < NG; ++g) unset = unset || (m_run[g] == -INFINITY);

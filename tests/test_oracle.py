@@ -633,3 +633,30 @@ def test_q_outlier_gate_definition():
         cnt_lt = (a[r] < md[r]).sum()
         cnt_le = (a[r] <= md[r]).sum()
         assert cnt_lt <= 16 < cnt_le
+
+
+def test_seeded_accumulator_logit_bound():
+    """The prefill's seeded-accumulator logit (oracle/attention.py:seeded_logits)
+    against the exact rational qs * ks * acc - m: the only error beyond fp32
+    rounding is the rounding of the constant rn(C0 * qs * 2^26), worth at most
+    0.64 integer units of acc. Extremes (+-128^3, 0, +-1) and random accs over
+    q/k scales across 12 decades. A dropped seed offset (f read as acc * 2^-26)
+    or a wrong binade (2^-25 spacing) fails by orders of magnitude."""
+    from fractions import Fraction
+
+    rng = np.random.default_rng(11)
+    acc = np.concatenate([[0, 1, -1, 2 ** 21, -(2 ** 21), 128 * 127 * 127, -128 * 127 * 127],
+                          rng.integers(-(2 ** 21), 2 ** 21, 3000)])
+    qs = (10.0 ** rng.uniform(-8, 2, acc.size)).astype(np.float32)
+    ks = (10.0 ** rng.uniform(-4, 2, acc.size)).astype(np.float32)
+    m = rng.uniform(-20, 20, acc.size).astype(np.float32)
+    x = oa.seeded_logits(acc, qs, ks, m)
+    for a, q, k, mm, xx in zip(acc, qs, ks, m, x):
+        exact = Fraction(float(q)) * Fraction(float(k)) * int(a) - Fraction(float(mm))
+        mag = abs(Fraction(float(q)) * Fraction(float(k)) * int(a)) + abs(Fraction(float(mm)))
+        bound = Fraction(0.65) * Fraction(float(q)) * Fraction(float(k)) + mag * Fraction(2.0 ** -22)
+        assert abs(Fraction(float(xx)) - exact) <= bound, (a, q, k, mm, xx, float(exact))
+    # f is exact: the seeded bits minus the seed are acc itself
+    f = (acc + oa.SEED_BITS).astype(np.uint32).view(np.float32).astype(np.float64)
+    c0 = float(np.uint32(oa.SEED_BITS).view(np.float32))
+    np.testing.assert_array_equal((f - c0) * 2.0 ** 26, acc.astype(np.float64))
