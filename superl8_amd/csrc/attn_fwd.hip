@@ -206,6 +206,9 @@ struct QOp {
 #ifndef SL8_FWD_PD
 #define SL8_FWD_PD 3
 #endif
+#ifndef SL8_FWD_BAL
+#define SL8_FWD_BAL 1
+#endif
 #ifndef SL8_FWD_OCC
 #define SL8_FWD_OCC 2
 #endif
@@ -698,6 +701,52 @@ attn_fwd_wide_kernel(const FwdArgs a) {
         if (i + SL8_FWD_PD < NOP) opb[i + SL8_FWD_PD] = load_op(i + SL8_FWD_PD);
         __builtin_amdgcn_sched_barrier(0);  // the read goes out before MFMA i
         const v4i cur = opb[i];
+#if SL8_FWD_BAL
+        // Balanced slices (VALU cycles per MFMA slot ~32-40; exp2 is quarter
+        // rate): slots 0..7 exp2 of keys 2i, 2i+1 of half h-1, with the pack +
+        // row sum of keys 0..7 after slot 3 and of keys 8..15 after slot 7;
+        // slot 6 reads k_scale; slots 8..11 form the exp2 arguments of half h,
+        // four keys each (the QK chain ended at slot 3).
+        static_assert(NOP == 12, "balanced slices: D = 128");
+        if (i < DC) sc = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur, qop[0].c[i], sc, 0, 0, 0);
+        else oacc[0][(i - DC) % DC] = PV::mfma(__builtin_bit_cast(pvec, cur), p2[0][(i - DC) / DC],
+                                               oacc[0][(i - DC) % DC]);
+        if (i < 8) {
+#pragma unroll
+          for (int e = 2 * i; e < 2 * i + 2; ++e) {
+            pe[e] = __builtin_amdgcn_exp2f(xi[0][e]);  // -inf -> 0
+            pin_vgpr(pe[e]);
+          }
+        }
+        if (i == 3 || i == 7) {
+          const int k = i / 4;
+          // same packing, row-sum order and overflow test as half_probs
+          p1[0][k] = PV::pack(&pe[8 * k]);
+          hs = PV::sum(p1[0][k], &pe[8 * k], hs);
+          pin_vgpr(__builtin_bit_cast(v4i, p1[0][k]));
+          pin_vgpr(hs);
+          if (k == 1) {
+            l_lane[0] += hs;
+            ovf = ovf || (hs > 32768.f);
+          }
+        }
+        if (i == 6) {
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq)
+            kv[gq] = *reinterpret_cast<const float4*>(st + 32 * s + 8 * gq + 4 * h);
+        }
+        if (i >= 8) {
+          const int gq = i - 8;
+          const float kk[4] = {kv[gq].x, kv[gq].y, kv[gq].z, kv[gq].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float w = fmaf(__int_as_float(sc[4 * gq + e]), qs26, cq26);
+            xo[0][4 * gq + e] = fmaf(w, kk[e], -msub);
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) pin_vgpr(xo[0][4 * gq + e]);
+        }
+#else
         if (i < DC) {
           sc = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur, qop[0].c[i], sc, 0, 0, 0);
 #pragma unroll
@@ -735,6 +784,7 @@ attn_fwd_wide_kernel(const FwdArgs a) {
             for (int e = 0; e < 4; ++e) pin_vgpr(xo[0][4 * gq + e]);
           }
         }
+#endif
         __builtin_amdgcn_sched_barrier(0);
       }
       if constexpr (DUMP) {
