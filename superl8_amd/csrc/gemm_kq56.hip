@@ -65,7 +65,7 @@ template <int OUT_DT, int RB>
 __global__ void __launch_bounds__(256, 1)
 gemm_q5k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
                      const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K,
-                     int nt_x, int tile0) {
+                     int nt_x, int xcd_m, int tile0) {
   __shared__ __attribute__((aligned(16))) int8_t xs0[KBM * 256];
   __shared__ __attribute__((aligned(16))) int8_t xs1[KBM * 256];
   __shared__ __attribute__((aligned(16))) uint8_t ws0[T5CH * 16];
@@ -77,7 +77,9 @@ gemm_q5k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
   // RB = 1: the quarter blockIdx.x & 3 (32 rows) of tile tile0 + blockIdx.x / 4,
   // so a short last round of tiles spreads over 4x the workgroups
   const int tile = tile0 + (RB == 4 ? (int)blockIdx.x : (int)(blockIdx.x >> 2));
-  const int n0 = (tile % nt_x) * KBN, m0 = (tile / nt_x) * KBM;
+  int ct, rt;
+  kq_tile_coords(tile, nt_x, xcd_m, ct, rt);
+  const int n0 = ct * KBN, m0 = rt * KBM;
   const int rb0 = RB == 4 ? 0 : (int)(blockIdx.x & 3);
   const int nsb = K >> 8;
   const int64_t row_bytes = (int64_t)nsb * Q5K_BYTES;
@@ -264,7 +266,7 @@ template <int OUT_DT, int RB>
 __global__ void __launch_bounds__(256, 1)
 gemm_q6k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
                      const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K,
-                     int nt_x, int tile0) {
+                     int nt_x, int xcd_m, int tile0) {
   __shared__ __attribute__((aligned(16))) int8_t xs0[KBM * 256];
   __shared__ __attribute__((aligned(16))) int8_t xs1[KBM * 256];
   __shared__ __attribute__((aligned(16))) uint32_t ws0[T6W];
@@ -276,7 +278,9 @@ gemm_q6k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
   // RB = 1: the quarter blockIdx.x & 3 (32 rows) of tile tile0 + blockIdx.x / 4,
   // so a short last round of tiles spreads over 4x the workgroups
   const int tile = tile0 + (RB == 4 ? (int)blockIdx.x : (int)(blockIdx.x >> 2));
-  const int n0 = (tile % nt_x) * KBN, m0 = (tile / nt_x) * KBM;
+  int ct, rt;
+  kq_tile_coords(tile, nt_x, xcd_m, ct, rt);
+  const int n0 = ct * KBN, m0 = rt * KBM;
   const int rb0 = RB == 4 ? 0 : (int)(blockIdx.x & 3);
   const int nsb = K >> 8;
   const int64_t row_bytes = (int64_t)nsb * Q6K_BYTES;
@@ -949,11 +953,13 @@ void launch_kq_tile(const int8_t* x, const float* xs, const uint8_t* w, void* ou
   // launch), which shortens that round (same per-element arithmetic)
   const int ntx = (N + KBN - 1) / KBN, T = ntx * ((M + KBM - 1) / KBM), P = cu_count();
   const int rem = T % P, nfull = (T >= P && rem > 0 && rem <= P / 2) ? T - rem : T;
+  // XCD-aware tile order (kq_tile_coords) when the column tiles split evenly over the 8 XCDs
+  const int xm = (SL8_KQ_XCD && ntx % 8 == 0) ? (M + KBM - 1) / KBM : 0;
 #define SL8_KQT(KERN, RB, G, T0)                                                                   \
   switch (odt) {                                                                                   \
-    case SL8_DTYPE_F16: KERN<SL8_DTYPE_F16, RB><<<G, 256, 0, st>>>(x, xs, w, out, M, N, K, ntx, T0); break; \
-    case SL8_DTYPE_BF16: KERN<SL8_DTYPE_BF16, RB><<<G, 256, 0, st>>>(x, xs, w, out, M, N, K, ntx, T0); break; \
-    default: KERN<SL8_DTYPE_F32, RB><<<G, 256, 0, st>>>(x, xs, w, out, M, N, K, ntx, T0); break;        \
+    case SL8_DTYPE_F16: KERN<SL8_DTYPE_F16, RB><<<G, 256, 0, st>>>(x, xs, w, out, M, N, K, ntx, xm, T0); break; \
+    case SL8_DTYPE_BF16: KERN<SL8_DTYPE_BF16, RB><<<G, 256, 0, st>>>(x, xs, w, out, M, N, K, ntx, xm, T0); break; \
+    default: KERN<SL8_DTYPE_F32, RB><<<G, 256, 0, st>>>(x, xs, w, out, M, N, K, ntx, xm, T0); break;        \
   }
   if (FMT == 5) {
     SL8_KQT(gemm_q5k_tile_kernel, 4, nfull, 0)

@@ -564,7 +564,7 @@ template <int OUT_DT, int RB>
 __global__ void __launch_bounds__(256, 1)
 gemm_q4k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
                      const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K,
-                     int nt_x, int tile0) {
+                     int nt_x, int xcd_m, int tile0) {
   __shared__ __attribute__((aligned(16))) int8_t xs0[TBM * 256];
   __shared__ __attribute__((aligned(16))) int8_t xs1[TBM * 256];
   __shared__ __attribute__((aligned(16))) uint8_t ws0[TWCH * 16];
@@ -576,7 +576,9 @@ gemm_q4k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
   // RB = 1: the quarter blockIdx.x & 3 (32 rows) of tile tile0 + blockIdx.x / 4,
   // so a short last round of tiles spreads over 4x the workgroups
   const int tile = tile0 + (RB == 4 ? (int)blockIdx.x : (int)(blockIdx.x >> 2));
-  const int n0 = (tile % nt_x) * TBN, m0 = (tile / nt_x) * TBM;
+  int ct, rt;
+  kq_tile_coords(tile, nt_x, xcd_m, ct, rt);
+  const int n0 = ct * TBN, m0 = rt * TBM;
   const int rb0 = RB == 4 ? 0 : (int)(blockIdx.x & 3);
   const int nsb = K >> 8;
   const int64_t row_bytes = (int64_t)nsb * Q4K_BYTES;
@@ -717,11 +719,13 @@ void launch_gemm_tile(const int8_t* x, const float* xs, const uint8_t* w, void* 
   // launch), which shortens that round (same per-element arithmetic)
   const int ntx = (N + TBN - 1) / TBN, T = ntx * ((M + TBM - 1) / TBM), P = cu_count();
   const int rem = T % P, nfull = (T >= P && rem > 0 && rem <= P / 2) ? T - rem : T;
+  // XCD-aware tile order (kq_tile_coords) when the column tiles split evenly over the 8 XCDs
+  const int xm = (SL8_KQ_XCD && ntx % 8 == 0) ? (M + TBM - 1) / TBM : 0;
 #define SL8_Q4T(RB, G, T0)                                                                                  \
   switch (odt) {                                                                                            \
-    case SL8_DTYPE_F16: gemm_q4k_tile_kernel<SL8_DTYPE_F16, RB><<<G, 256, 0, st>>>(x, xs, w, out, M, N, K, ntx, T0); break; \
-    case SL8_DTYPE_BF16: gemm_q4k_tile_kernel<SL8_DTYPE_BF16, RB><<<G, 256, 0, st>>>(x, xs, w, out, M, N, K, ntx, T0); break; \
-    default: gemm_q4k_tile_kernel<SL8_DTYPE_F32, RB><<<G, 256, 0, st>>>(x, xs, w, out, M, N, K, ntx, T0); break;        \
+    case SL8_DTYPE_F16: gemm_q4k_tile_kernel<SL8_DTYPE_F16, RB><<<G, 256, 0, st>>>(x, xs, w, out, M, N, K, ntx, xm, T0); break; \
+    case SL8_DTYPE_BF16: gemm_q4k_tile_kernel<SL8_DTYPE_BF16, RB><<<G, 256, 0, st>>>(x, xs, w, out, M, N, K, ntx, xm, T0); break; \
+    default: gemm_q4k_tile_kernel<SL8_DTYPE_F32, RB><<<G, 256, 0, st>>>(x, xs, w, out, M, N, K, ntx, xm, T0); break;        \
   }
   SL8_Q4T(4, nfull, 0)
   if (nfull < T) SL8_Q4T(1, 4 * (T - nfull), nfull)

@@ -3,6 +3,10 @@
 
 #include "common.hpp"
 
+#ifndef SL8_KQ_XCD
+#define SL8_KQ_XCD 1
+#endif
+
 namespace sl8 {
 
 // Packed 6-bit sub-scales / mins of a Q4_K / Q5_K super-block (4 per dword,
@@ -17,6 +21,22 @@ __device__ __forceinline__ ScMin unpack_scmin(uint32_t s0, uint32_t s1, uint32_t
   r.sc_hi = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
   r.mn_hi = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
   return r;
+}
+// Tile order o -> (column tile ct, row tile rt) of the k-quant tile GEMMs.
+// xcd_m > 0 (the number of row tiles; used when the column-tile count is a
+// multiple of 8): workgroup o runs on XCD o % 8, and the xcd_m row tiles of
+// one weight column tile are consecutive workgroups of the same XCD, so the
+// column's weights come from HBM into that XCD's L2 once and are re-read
+// from there by the other row tiles running beside it. xcd_m = 0: row-major.
+__device__ __forceinline__ void kq_tile_coords(int o, int nt_x, int xcd_m, int& ct, int& rt) {
+  if (xcd_m > 0) {
+    const int k = o >> 3;
+    ct = (o & 7) + 8 * (k / xcd_m);
+    rt = k % xcd_m;
+  } else {
+    ct = o % nt_x;
+    rt = o / nt_x;
+  }
 }
 __device__ __forceinline__ int byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xFF; }
 
