@@ -39,13 +39,22 @@ def attn_int8_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: 
     else:
         fired, qk = False, quant.quantize_qk(q, k, softmax_scale=scale, rotate=rotate)
     if isinstance(fired, torch.Tensor):
-        # gate decided on the device: launch the attention first (it exits at
-        # once if the gate fired), then read the flag while it runs
+        # gate decided on the device: its flag is copied to pinned host memory
+        # right after the prologue, the attention is launched behind the copy
+        # (it exits at once if the gate fired), and the host waits only for the
+        # copy -- not for the attention, so the next call's prologue is queued
+        # while this attention runs (a plain .item() after the launch would
+        # wait for the attention and leave the GPU idle during the next enqueue)
         q_i8, q_scale, k_i8, k_scale, _k_mean = qk
+        flag_host = torch.empty(1, dtype=torch.int32, pin_memory=True)
+        flag_host.copy_(fired, non_blocking=True)
+        flag_ready = torch.cuda.Event()
+        flag_ready.record(torch.cuda.current_stream(q.device))
         out = _C.attn_int8_fwd(q_i8, q_scale.squeeze(-1).contiguous(), k_i8,
                                k_scale.squeeze(-1).contiguous(), v.contiguous(), causal,
                                window_left, gate_flag=fired)
-        if not bool(fired.item()):
+        flag_ready.synchronize()
+        if int(flag_host[0]) == 0:
             return out
         fired = True
     if fired:

@@ -284,3 +284,26 @@ def test_reference_point_restart(device, causal):
     assert_close_abs(out, ref, atol=1e-2, what="restart path vs oracle")
     finite = np.isfinite(ref_lse)
     np.testing.assert_allclose(_np(lse)[finite], ref_lse[finite], rtol=0, atol=5e-4)
+
+
+@pytest.mark.parametrize("qv,kv", [(127, 127), (-128, -128), (-128, 127)])
+def test_seeded_accumulator_extreme_codes(device, qv, kv):
+    """The D = 128 straight-line path reads the QK accumulator seeded with the
+    bits of 1/(2 pi) as a float; it is exact for |acc| <= 2,292,099 and the
+    largest int8 sums (128 * 128^2 = 2,097,152 for codes -128) stay inside. Rows
+    of constant codes with a few flipped keys: every score is +-|acc|max or
+    close to it, so a wrong binade or a lost seed shows in the softmax."""
+    B, Hq, Hkv, M, N, D = 1, 2, 1, 256, 320, 128
+    q = torch.full((B, Hq, M, D), qv, device=device, dtype=torch.int8)
+    k = torch.full((B, Hkv, N, D), kv, device=device, dtype=torch.int8)
+    k[:, :, 5::7, :40] = 0  # some keys with smaller |score|
+    q[:, 1, :, 64:] = 1
+    qs = torch.full((B, Hq, M), 2e-6, device=device)  # logits ~ +-4 log2 units
+    ks = torch.rand(B, Hkv, N, device=device) + 0.5
+    v = torch.randn(B, Hkv, N, D, device=device, dtype=torch.float16)
+    for causal in (False, True):
+        out = _C.attn_int8_fwd(q, qs, k, ks, v, causal)
+        ref, _ = oa.attn_int8_fwd(_np(q), _np(qs), _np(k), _np(ks), _np(v.float()), causal)
+        assert_close_abs(out, ref, atol=1e-2, what=f"codes {qv}/{kv} causal={causal}")
+        s = _C.attn_int8_qk_scores(q, k)
+        _check_scores(s, q, k, False)

@@ -156,3 +156,25 @@ def test_public_prefill_deferred_gate_is_the_two_step_path(device):
     two_step = _C.attn_int8_fwd(q_i8, qs.squeeze(-1).contiguous(), k_i8,
                                 ks.squeeze(-1).contiguous(), v, True)
     assert torch.equal(o, two_step)
+
+
+def test_public_prefill_gate_read_back_to_back(device):
+    """Calls issued back to back, alternating inputs whose gate fires and stays
+    quiet: each call's decision is its own (the flag is read from a pinned copy
+    made right after its prologue, while its attention may still be running)."""
+    torch.manual_seed(8)
+    q = torch.randn(1, 4, 256, 128, device=device, dtype=torch.float16)
+    k = torch.randn(1, 2, 256, 128, device=device, dtype=torch.float16)
+    v = torch.randn(1, 2, 256, 128, device=device, dtype=torch.float16)
+    q_out = q.clone()
+    q_out[0, 1, 7, 3] = 300.0  # one dominated row: the gate fires for this input
+    quiet = ops.attn_int8_fwd(q, k, v, causal=True)
+    loud = ops.attn_int8_fwd(q_out, k, v, causal=True)
+    fp_loud = torch.nn.functional.scaled_dot_product_attention(
+        q_out, k, v, is_causal=True, enable_gqa=True)
+    assert torch.allclose(loud.float(), fp_loud.float(), atol=2e-3, rtol=0)
+    assert not torch.equal(quiet, loud)
+    outs = [ops.attn_int8_fwd(x, k, v, causal=True) for x in (q, q_out, q, q, q_out, q_out, q)]
+    torch.cuda.synchronize()
+    for x, o in zip((q, q_out, q, q, q_out, q_out, q), outs):
+        assert torch.equal(o, quiet if x is q else loud)
