@@ -454,11 +454,17 @@ def main():
                     help="summarise a rocprofv3 --kernel-trace CSV of a `--no-secondary` run "
                          "(the timed calls = the prefill kernel's last --steps dispatches) "
                          "and exit; runs without a GPU")
+    ap.add_argument("--pmc-summary", metavar="COUNTER_COLLECTION_CSV",
+                    help="summarise a rocprofv3 --pmc CSV: per kernel, the median (and max) over "
+                         "its dispatches of each counter summed over the dispatch's rows; exits")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 256 MiB device copy (scale for PMC byte counters)")
     args = ap.parse_args()
     if args.trace_summary:
         print(trace_summary(args.trace_summary, args.steps))
+        return
+    if args.pmc_summary:
+        print(pmc_summary(args.pmc_summary))
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -629,7 +635,8 @@ def trace_summary(path: str, steps: int) -> str:
     lines = ["| kernel | calls | mean us | median us | min us | max us |", "|---|---|---|---|---|---|"]
     for n, v in sorted(by.items(), key=lambda kv: -sum(d for _, d in kv[1])):
         d = [x for _, x in v]
-        lines.append(f"| {n} | {len(d)} | {np.mean(d):.2f} | {np.median(d):.2f} | {min(d):.2f} | "
+        nm = n if len(n) <= 120 else n[:117] + "..."
+        lines.append(f"| {nm} | {len(d)} | {np.mean(d):.2f} | {np.median(d):.2f} | {min(d):.2f} | "
                      f"{max(d):.2f} |")
     if PREFILL_KERNEL in by:
         v = sorted(by[PREFILL_KERNEL])[-steps:]
@@ -638,6 +645,30 @@ def trace_summary(path: str, steps: int) -> str:
         lines += ["", f"Timed calls ({len(d)}: the last {steps} dispatches of `{PREFILL_KERNEL}`): "
                       f"mean {np.mean(d):.2f} us, median {np.median(d):.2f} us, min {min(d):.2f}, "
                       f"max {max(d):.2f}; start-to-start spacing {span:.2f} us."]
+    return "\n".join(lines)
+
+
+def pmc_summary(path: str) -> str:
+    """Markdown table from a rocprofv3 --pmc counter-collection CSV: per kernel and
+    counter, the value of each dispatch (its rows summed: one per XCD or
+    instance) and the median and max over the dispatches."""
+    import csv
+
+    agg = {}
+    for r in csv.DictReader(open(path)):
+        n = _short_kernel_name(r["Kernel_Name"])
+        d = agg.setdefault(n, {}).setdefault(r["Counter_Name"], {})
+        d[r["Dispatch_Id"]] = d.get(r["Dispatch_Id"], 0.0) + float(r["Counter_Value"])
+    counters = sorted({c for v in agg.values() for c in v})
+    lines = ["| kernel | dispatches | " + " | ".join(f"{c} median / max" for c in counters) + " |",
+             "|---|---|" + "---|" * len(counters)]
+    for n, cs in sorted(agg.items()):
+        nd = max(len(v) for v in cs.values())
+        cells = []
+        for c in counters:
+            v = list(cs.get(c, {}).values())
+            cells.append(f"{np.median(v):.6g} / {max(v):.6g}" if v else "-")
+        lines.append(f"| {n if len(n) <= 120 else n[:117] + '...'} | {nd} | " + " | ".join(cells) + " |")
     return "\n".join(lines)
 
 
