@@ -759,126 +759,52 @@ __device__ __forceinline__ uint2 codes8(const float* f, float safe) {
   return make_uint2(w[0], w[1]);
 }
 
-template <int D, bool GATE>
+// A: exact int64 fixed-point K-mean partials of PRO_CHUNK-row chunks (one
+// block per (group, chunk)); block 0 also clears the gate flag, which the Q
+// blocks of B set.
+template <int D>
 __global__ void __launch_bounds__(256, 8)
-prologue_a_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, int64_t qrows,
-                  int64_t N, int nkb, int C, float qmul, float ratio, int8_t* __restrict__ q_i8,
-                  float* __restrict__ q_scale, long long* __restrict__ part,
-                  int32_t* __restrict__ fire) {
+prologue_a_kernel(const uint16_t* __restrict__ k, int64_t N, int C,
+                  long long* __restrict__ part, int32_t* __restrict__ flag) {
   constexpr int LPR = D / 8;       // lanes per row, 8 elements (16 bytes) each
   constexpr int RPP = 256 / LPR;   // rows per block pass
   const int lane = threadIdx.x % LPR, sub = threadIdx.x / LPR;
-  if ((int)blockIdx.x < nkb) {
-    __shared__ long long red[RPP][D];
-    const int64_t g = blockIdx.x / C;
-    const int c = blockIdx.x % C;
-    const int64_t n0 = (int64_t)c * PRO_CHUNK, n1 = min(N, n0 + PRO_CHUNK);
-    const uint16_t* kg = k + g * N * D + lane * 8;
-    long long acc[8];
+  if (flag && blockIdx.x == 0 && threadIdx.x == 0) *flag = 0;
+  __shared__ long long red[RPP][D];
+  const int64_t g = blockIdx.x / C;
+  const int c = blockIdx.x % C;
+  const int64_t n0 = (int64_t)c * PRO_CHUNK, n1 = min(N, n0 + PRO_CHUNK);
+  const uint16_t* kg = k + g * N * D + lane * 8;
+  long long acc[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] = 0;
+  for (int e = 0; e < 8; ++e) acc[e] = 0;
 #pragma unroll 2
-    for (int64_t n = n0 + sub; n < n1; n += RPP) {
-      const uint4 raw = *reinterpret_cast<const uint4*>(kg + n * D);
-      const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+  for (int64_t n = n0 + sub; n < n1; n += RPP) {
+    const uint4 raw = *reinterpret_cast<const uint4*>(kg + n * D);
+    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        acc[2 * i] += f16_fixed24(w[i] & 0xFFFFu);
-        acc[2 * i + 1] += f16_fixed24(w[i] >> 16);
-      }
+    for (int i = 0; i < 4; ++i) {
+      acc[2 * i] += f16_fixed24(w[i] & 0xFFFFu);
+      acc[2 * i + 1] += f16_fixed24(w[i] >> 16);
     }
+  }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) red[sub][lane * 8 + e] = acc[e];
-    __syncthreads();
-    for (int d = threadIdx.x; d < D; d += 256) {
-      long long t = 0;
+  for (int e = 0; e < 8; ++e) red[sub][lane * 8 + e] = acc[e];
+  __syncthreads();
+  for (int d = threadIdx.x; d < D; d += 256) {
+    long long t = 0;
 #pragma unroll 8
-      for (int p = 0; p < RPP; ++p) t += red[p][d];
-      part[(g * C + c) * D + d] = t;
-    }
-    return;
-  }
-  const int qb = blockIdx.x - nkb, nqb = gridDim.x - nkb;
-  int fired = 0;
-  const float rinv = 1.f / ratio;
-  for (int64_t base = (int64_t)qb * RPP * PRO_QP; base < qrows;
-       base += (int64_t)nqb * RPP * PRO_QP) {
-    uint4 raw[PRO_QP];  // all of this thread's rows are fetched before any is processed
-#pragma unroll
-    for (int p = 0; p < PRO_QP; ++p) {
-      const int64_t r = base + p * RPP + sub;
-      raw[p] = r < qrows ? reinterpret_cast<const uint4*>(q + r * D)[lane] : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-  for (int p = 0; p < PRO_QP; ++p) {
-    const int64_t r = base + p * RPP + sub;
-    const bool live = r < qrows;
-    float f[8];
-    unpack_h8(raw[p], f);
-    float mx = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(f[e]));
-    mx = group_max<LPR>(mx);
-    const float s = mx * (1.0f / 127.0f);
-    const float safe = (s == 0.f) ? 1.f : s;
-    if (live) {
-      if (lane == 0) q_scale[r] = safe * qmul;
-      reinterpret_cast<uint2*>(q_i8 + r * D)[lane] = codes8(f, safe);
-    }
-    if constexpr (GATE) {
-      // y = fl(|x| + 1e-10) against t = max / ratio: far from t the exact test
-      // fl(max / y) > ratio is decided by y < t; within 2^-18 of t (relative)
-      // the IEEE division decides.
-      // (t below 2^-100: every element takes the division.)
-      const float t = mx * rinv;
-      const bool tiny = t < 0x1p-100f;
-      const float tlo = tiny ? 0.f : t * (1.f - 0x1p-18f);
-      const float thi = tiny ? INFINITY : t * (1.f + 0x1p-18f);
-      int cnt = 0, nan = 0;
-      bool amb = false;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float a = fabsf(f[e]);
-        nan |= a != a;
-        const float y = a + 1e-10f;
-        cnt += y < tlo;
-        amb |= y >= tlo && y <= thi;
-      }
-      if (__builtin_expect(__ballot(amb) != 0, 0)) {
-        if (amb) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float y = fabsf(f[e]) + 1e-10f;
-            if (y >= tlo && y <= thi) cnt += __fdiv_rn(mx, y) > ratio;
-          }
-        }
-      }
-      cnt = group_sum<LPR>(cnt + (nan << 16));  // NaN count in the high half
-      if (live && (cnt >> 16) == 0 && (cnt & 0xFFFF) > (D - 1) / 2) fired = 1;
-    }
-  }
-  }
-  if constexpr (GATE) {
-    fired = __syncthreads_or(fired);
-    if (threadIdx.x == 0) fire[qb] = fired;
+    for (int p = 0; p < RPP; ++p) t += red[p][d];
+    part[(g * C + c) * D + d] = t;
   }
 }
 
-// Mean of each (group, column) from its partial sums, and the gate flag.
+// Mean of each (group, column) from its partial sums.
 __global__ void __launch_bounds__(256)
 prologue_mean_kernel(const long long* __restrict__ part, int64_t G, int C, int D, int64_t N,
-                     float* __restrict__ k_mean, const int32_t* __restrict__ fire, int nfire,
-                     int32_t* __restrict__ flag) {
-  if (flag && blockIdx.x == 0) {
-    int any = 0;
-#pragma unroll 8
-    for (int i = threadIdx.x; i < nfire; i += 256) any |= fire[i];
-    any = __syncthreads_or(any);
-    if (threadIdx.x == 0) *flag = any;
-    return;  // block 0 only reduces the flag
-  }
+                     float* __restrict__ k_mean) {
   // 8 lanes per column, each summing every 8th partial, then a lane reduction
-  const int64_t t8 = (int64_t)(blockIdx.x - (flag ? 1 : 0)) * 256 + threadIdx.x;
+  const int64_t t8 = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t i = t8 >> 3;
   const int cl = (int)(t8 & 7);
   const bool live = i < G * D;  // uniform per 8-lane group
@@ -898,44 +824,118 @@ prologue_mean_kernel(const long long* __restrict__ part, int64_t G, int C, int D
   if (live && cl == 0) k_mean[i] = (float)(((double)t * 0x1p-24) / (double)N);
 }
 
-template <int D>
+// B: the smoothed K rows (blocks [0, nkb): PRO_KROWS rows of group
+// blockIdx / kbg each) and the Q rows with the outlier gate (the rest). The Q
+// work does not depend on the mean, but sharing this launch keeps it off the
+// critical path A -> mean -> B of the K side.
+template <int D, bool GATE>
 __global__ void __launch_bounds__(256)
 prologue_b_kernel(const uint16_t* __restrict__ k, int64_t N, const float* __restrict__ k_mean,
-                  int8_t* __restrict__ k_i8, float* __restrict__ k_scale) {
+                  int8_t* __restrict__ k_i8, float* __restrict__ k_scale, int kbg, int nkb,
+                  const uint16_t* __restrict__ q, int64_t qrows, float qmul, float ratio,
+                  int8_t* __restrict__ q_i8, float* __restrict__ q_scale,
+                  int32_t* __restrict__ flag) {
   constexpr int LPR = D / 8, RPP = 256 / LPR;
-  constexpr int NP = PRO_KROWS / RPP;
-  const int64_t g = blockIdx.y;
   const int lane = threadIdx.x % LPR, sub = threadIdx.x / LPR;
-  const int64_t n0 = (int64_t)blockIdx.x * PRO_KROWS;
-  const uint16_t* kg = k + g * N * D;
-  uint4 raw[NP];
+  if ((int)blockIdx.x < nkb) {
+    constexpr int NP = PRO_KROWS / RPP;
+    const int64_t g = blockIdx.x / kbg;
+    const int64_t n0 = (int64_t)(blockIdx.x % kbg) * PRO_KROWS;
+    const uint16_t* kg = k + g * N * D;
+    uint4 raw[NP];
 #pragma unroll
-  for (int i = 0; i < NP; ++i) {
-    const int64_t n = n0 + i * RPP + sub;
-    raw[i] = n < N ? reinterpret_cast<const uint4*>(kg + n * D)[lane] : make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < NP; ++i) {
+      const int64_t n = n0 + i * RPP + sub;
+      raw[i] = n < N ? reinterpret_cast<const uint4*>(kg + n * D)[lane] : make_uint4(0, 0, 0, 0);
+    }
+    const float4 m0 = reinterpret_cast<const float4*>(k_mean + g * D)[2 * lane];
+    const float4 m1 = reinterpret_cast<const float4*>(k_mean + g * D)[2 * lane + 1];
+    const float mv[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const int64_t n = n0 + i * RPP + sub;
+      const bool live = n < N;
+      float f[8];
+      unpack_h8(raw[i], f);
+      float mx = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        f[e] = Elem<SL8_DTYPE_F16>::round(f[e] - mv[e]);
+        mx = fmaxf(mx, fabsf(f[e]));
+      }
+      mx = group_max<LPR>(mx);
+      const float s = mx * (1.0f / 127.0f);
+      const float safe = (s == 0.f) ? 1.f : s;
+      if (live) {
+        if (lane == 0) k_scale[g * N + n] = safe;
+        reinterpret_cast<uint2*>(k_i8 + (g * N + n) * D)[lane] = codes8(f, safe);
+      }
+    }
+    return;
   }
-  const float4 m0 = reinterpret_cast<const float4*>(k_mean + g * D)[2 * lane];
-  const float4 m1 = reinterpret_cast<const float4*>(k_mean + g * D)[2 * lane + 1];
-  const float mv[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+  const int qb = blockIdx.x - nkb, nqb = gridDim.x - nkb;
+  int fired = 0;
+  const float rinv = 1.f / ratio;
+  for (int64_t base = (int64_t)qb * RPP * PRO_QP; base < qrows;
+       base += (int64_t)nqb * RPP * PRO_QP) {
+    uint4 raw[PRO_QP];  // all of this thread's rows are fetched before any is processed
 #pragma unroll
-  for (int i = 0; i < NP; ++i) {
-    const int64_t n = n0 + i * RPP + sub;
-    const bool live = n < N;
-    float f[8];
-    unpack_h8(raw[i], f);
-    float mx = 0.f;
+    for (int p = 0; p < PRO_QP; ++p) {
+      const int64_t r = base + p * RPP + sub;
+      raw[p] = r < qrows ? reinterpret_cast<const uint4*>(q + r * D)[lane] : make_uint4(0, 0, 0, 0);
+    }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      f[e] = Elem<SL8_DTYPE_F16>::round(f[e] - mv[e]);
-      mx = fmaxf(mx, fabsf(f[e]));
+    for (int p = 0; p < PRO_QP; ++p) {
+      const int64_t r = base + p * RPP + sub;
+      const bool live = r < qrows;
+      float f[8];
+      unpack_h8(raw[p], f);
+      float mx = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(f[e]));
+      mx = group_max<LPR>(mx);
+      const float s = mx * (1.0f / 127.0f);
+      const float safe = (s == 0.f) ? 1.f : s;
+      if (live) {
+        if (lane == 0) q_scale[r] = safe * qmul;
+        reinterpret_cast<uint2*>(q_i8 + r * D)[lane] = codes8(f, safe);
+      }
+      if constexpr (GATE) {
+        // y = fl(|x| + 1e-10) against t = max / ratio: far from t the exact test
+        // fl(max / y) > ratio is decided by y < t; within 2^-18 of t (relative)
+        // the IEEE division decides.
+        // (t below 2^-100: every element takes the division.)
+        const float t = mx * rinv;
+        const bool tiny = t < 0x1p-100f;
+        const float tlo = tiny ? 0.f : t * (1.f - 0x1p-18f);
+        const float thi = tiny ? INFINITY : t * (1.f + 0x1p-18f);
+        int cnt = 0, nan = 0;
+        bool amb = false;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float a = fabsf(f[e]);
+          nan |= a != a;
+          const float y = a + 1e-10f;
+          cnt += y < tlo;
+          amb |= y >= tlo && y <= thi;
+        }
+        if (__builtin_expect(__ballot(amb) != 0, 0)) {
+          if (amb) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const float y = fabsf(f[e]) + 1e-10f;
+              if (y >= tlo && y <= thi) cnt += __fdiv_rn(mx, y) > ratio;
+            }
+          }
+        }
+        cnt = group_sum<LPR>(cnt + (nan << 16));  // NaN count in the high half
+        if (live && (cnt >> 16) == 0 && (cnt & 0xFFFF) > (D - 1) / 2) fired = 1;
+      }
     }
-    mx = group_max<LPR>(mx);
-    const float s = mx * (1.0f / 127.0f);
-    const float safe = (s == 0.f) ? 1.f : s;
-    if (live) {
-      if (lane == 0) k_scale[g * N + n] = safe;
-      reinterpret_cast<uint2*>(k_i8 + (g * N + n) * D)[lane] = codes8(f, safe);
-    }
+  }
+  if constexpr (GATE) {
+    fired = __syncthreads_or(fired);
+    if (fired && threadIdx.x == 0) atomicOr(flag, 1);  // cleared by A, earlier on the stream
   }
 }
 
@@ -950,8 +950,8 @@ int prologue_nqb(int64_t qrows, int64_t D) {
 extern "C" size_t sl8_quantize_qk_workspace(int64_t BHq_M, int64_t G, int64_t N, int64_t D) {
   if (G <= 0 || N <= 0 || D <= 0) return 0;
   const int64_t C = (N + PRO_CHUNK - 1) / PRO_CHUNK;
-  const size_t parts = (size_t)(G * C * D) * sizeof(long long);
-  return parts + (size_t)(BHq_M > 0 ? prologue_nqb(BHq_M, D) : 0) * sizeof(int32_t);
+  (void)BHq_M;  // the Q rows need no workspace (the gate sets the flag directly)
+  return (size_t)(G * C * D) * sizeof(long long);  // the K-mean partials
 }
 
 extern "C" int sl8_quantize_qk(const void* q, const void* k, int dtype, int64_t qrows, int64_t G,
@@ -975,26 +975,28 @@ extern "C" int sl8_quantize_qk(const void* q, const void* k, int dtype, int64_t 
   SL8_CHECK_ARG(workspace && workspace_bytes >= need && aligned(workspace, 8),
                 "fused prologue: workspace needs %zu bytes", need);
   const int C = (int)((N + PRO_CHUNK - 1) / PRO_CHUNK);
-  const int64_t nkb64 = G * C;
-  SL8_CHECK_ARG(nkb64 < (1LL << 30) && G < 65536, "fused prologue: too many key groups");
-  const int nkb = (int)nkb64, nqb = prologue_nqb(qrows, D);
+  const int64_t kbg = (N + PRO_KROWS - 1) / PRO_KROWS;  // quantise blocks per group
+  SL8_CHECK_ARG(G * C < (1LL << 30) && G * kbg < (1LL << 30) && G < 65536,
+                "fused prologue: too many key groups");
+  const int nka = (int)(G * C), nkb = (int)(G * kbg), nqb = prologue_nqb(qrows, D);
   long long* part = static_cast<long long*>(workspace);
-  int32_t* fire = reinterpret_cast<int32_t*>(part + G * C * D);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint16_t* qh = static_cast<const uint16_t*>(q);
   const uint16_t* kh = static_cast<const uint16_t*>(k);
-  const dim3 gb((unsigned)((N + PRO_KROWS - 1) / PRO_KROWS), (unsigned)G);
+  int32_t* fl = gate ? gate_flag : nullptr;
+  // A (K-mean partials) -> mean -> B (K and Q rows, gate): the Q rows, the
+  // bulk of the bytes, run beside the K rows in B instead of ahead of the mean
 #define SL8_PRO(DD)                                                                              \
   do {                                                                                          \
+    prologue_a_kernel<DD><<<nka, 256, 0, st>>>(kh, N, C, part, fl);                              \
+    prologue_mean_kernel<<<(unsigned)((G * DD * 8 + 255) / 256), 256, 0, st>>>(part, G, C, DD,  \
+                                                                              N, k_mean);       \
     if (gate)                                                                                   \
-      prologue_a_kernel<DD, true><<<nkb + nqb, 256, 0, st>>>(qh, kh, qrows, N, nkb, C,          \
-          q_scale_mul, gate_ratio, q_i8, q_scale, part, fire);                                  \
+      prologue_b_kernel<DD, true><<<nkb + nqb, 256, 0, st>>>(kh, N, k_mean, k_i8, k_scale,      \
+          (int)kbg, nkb, qh, qrows, q_scale_mul, gate_ratio, q_i8, q_scale, fl);                \
     else                                                                                        \
-      prologue_a_kernel<DD, false><<<nkb + nqb, 256, 0, st>>>(qh, kh, qrows, N, nkb, C,         \
-          q_scale_mul, gate_ratio, q_i8, q_scale, part, fire);                                  \
-    prologue_mean_kernel<<<(unsigned)((G * DD * 8 + 255) / 256 + (gate ? 1 : 0)), 256, 0, st>>>(\
-        part, G, C, DD, N, k_mean, fire, nqb, gate ? gate_flag : nullptr);                       \
-    prologue_b_kernel<DD><<<gb, 256, 0, st>>>(kh, N, k_mean, k_i8, k_scale);                     \
+      prologue_b_kernel<DD, false><<<nkb + nqb, 256, 0, st>>>(kh, N, k_mean, k_i8, k_scale,     \
+          (int)kbg, nkb, qh, qrows, q_scale_mul, gate_ratio, q_i8, q_scale, fl);                \
   } while (0)
   if (D == 64) SL8_PRO(64);
   else if (D == 128) SL8_PRO(128);
