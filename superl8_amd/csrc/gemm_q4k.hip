@@ -62,6 +62,17 @@ constexpr int XS_MPAD = 16;  // xsum LDS row pitch (activation rows)
 #ifndef SL8_GEMV_XBLDS
 #define SL8_GEMV_XBLDS 1
 #endif
+// SL8_GEMV_FULLC: the K = 5 * GCH * GWAVES decode shapes take the straight-line
+// path with a compile-time chunk count (see the dispatch at the end).
+// SL8_GEMV_XFIRST: at MT = 1 the activation copies are issued before the
+// weight loads. Config 4's shape, same box: M = 8 17.5 -> 17.0 us, M = 8 with
+// per-block x scales 17.9 -> 16.9 us, M = 16 33.5 -> 32.9 us, Q5_K M = 8 20.4 -> 20.0 us.
+#ifndef SL8_GEMV_FULLC
+#define SL8_GEMV_FULLC 1
+#endif
+#ifndef SL8_GEMV_XFIRST
+#define SL8_GEMV_XFIRST 1
+#endif
 constexpr int GCH = 5;     // super-blocks per wave and chunk
 constexpr int GWAVES = 4;  // K split
 constexpr int GXPITCH = GCH * 256;  // LDS bytes per activation row and wave
@@ -151,7 +162,7 @@ gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
   // One chunk of up to GCH super-blocks starting at c0.
   auto chunk = [&](const int c0, const int cnt) {
     // ---- activations of the chunk: M rows x cnt*256 bytes -> this wave's LDS area ----
-    // (issued after the weights: issuing them first measured slower)
+    // (at MT = 1 issued before the weights, else after them)
     auto stage_x = [&]() {
       const int xch = M * (GXPITCH / 16);
       for (int j = 0; j * 64 < xch; ++j) {
@@ -174,6 +185,11 @@ gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
     uint2 qh8[TPW][FMT == 5 ? GCH : 1];  // Q5_K: qh bytes 8 lc .. 8 lc + 7 of the row
     uint4 hd4[TPW][OPL ? GCH : 1];       // OPL: the row's whole header
     uint4 qh16[TPW][OPL && FMT == 5 ? GCH : 1];  // OPL, Q5_K: qh bytes 16 (h & 1) .. +15
+    constexpr bool XF = MT == 1 && TPW == 1 && !OPL && SL8_GEMV_XFIRST;
+    if constexpr (XF) {
+      stage_x();
+      __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
     for (int tt = 0; tt < TPW; ++tt)
 #pragma unroll
@@ -192,7 +208,8 @@ gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
         qb[tt][i] = *reinterpret_cast<const uint4*>(blk + QS + 64 + 16 * lc);
         if constexpr (FMT == 5) qh8[tt][i] = *reinterpret_cast<const uint2*>(blk + 16 + 8 * lc);
       }
-    stage_x();
+    if constexpr (XF) __builtin_amdgcn_sched_barrier(0);
+    else stage_x();
     // per-block activation scales of this lane's C rows (XB)
     float xsb[MT][4][XBL ? 1 : GCH];
     if constexpr (XB && !XBL) {
@@ -296,8 +313,14 @@ gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
   };
 
   const int sb0 = (wave * nsb) / GWAVES, sb1 = ((wave + 1) * nsb) / GWAVES;  // may be empty
-  if (sb1 - sb0 <= GCH) {
-    // the decode shapes: one chunk, straight-line code (precise load waits)
+  if (SL8_GEMV_FULLC && sb1 - sb0 == GCH) {
+    // the decode shapes (K = 5120: 20 super-blocks, 5 per wave): one full
+    // chunk with a compile-time count, so that no super-block's compute is
+    // conditional -- with a run-time count the compiler sinks a conditional
+    // block's weight loads into it, a second memory round trip per wave
+    chunk(sb0, GCH);
+  } else if (sb1 - sb0 <= GCH) {
+    // one chunk, straight-line code (precise load waits)
     if (sb1 > sb0) chunk(sb0, sb1 - sb0);
   } else {
     for (int c0 = sb0; c0 < sb1; c0 += GCH) chunk(c0, min(GCH, sb1 - c0));
