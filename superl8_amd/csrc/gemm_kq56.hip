@@ -35,6 +35,8 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i_t __attribute__((ext_vector_type(16)));
+typedef float v16f_t __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
 constexpr int Q5K_BYTES = 176;
 constexpr int Q6K_BYTES = 210;
@@ -70,6 +72,9 @@ gemm_q5k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
   __shared__ __attribute__((aligned(16))) int8_t xs1[KBM * 256];
   __shared__ __attribute__((aligned(16))) uint8_t ws0[T5CH * 16];
   __shared__ __attribute__((aligned(16))) uint8_t ws1[T5CH * 16];
+  // RB = 4: the min-term MFMA's A operands (x half-sums) of one super-block,
+  // [slot][row block][lane]; the scheme of the Q4_K tile kernel
+  __shared__ __attribute__((aligned(16))) uint4 xh_l[RB == 4 ? 2 : 1][RB == 4 ? 4 : 1][64];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, h = lane >> 5;
@@ -104,7 +109,22 @@ gemm_q5k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
 #pragma unroll
     for (int e = 0; e < 16; ++e) f[rb][e] = 0.f;
 
-  auto compute = [&](const int8_t* xt, const uint8_t* wt) __attribute__((always_inline)) {
+  // min term U = sum_j m_j * xsum_j on one fp16 MFMA per row block and
+  // super-block (exact: fp16 half-sums and mins, fp32 integer result); with
+  // RB = 4 one super-block late through LDS, as in the Q4_K tile kernel
+  float u_dmin = 0.f;
+  v8h u_b = {}, u_a = {};  // its m_j operand and (RB = 1) its half-sum operand
+  auto u_step = [&](int slot) __attribute__((always_inline)) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const v8h a = RB == 4 ? __builtin_bit_cast(v8h, xh_l[slot][rb][lane]) : u_a;
+      const v16f_t u = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, u_b, v16f_t{}, 0, 0, 0);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) f[rb][e] -= u_dmin * u[e];
+    }
+  };
+
+  auto compute = [&](const int8_t* xt, const uint8_t* wt, int slot) __attribute__((always_inline)) {
     const uint8_t* wr = wt + (32 * wave + l32) * Q5K_BYTES;
     const uint4 hd = *reinterpret_cast<const uint4*>(wr);
     const float d = h2f(hd.x & 0xFFFFu), dmin = h2f(hd.x >> 16);
@@ -117,7 +137,9 @@ gemm_q5k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
       const uint4 qv = *reinterpret_cast<const uint4*>(wr + 48 + 32 * g + 16 * h);
       qw[g][0] = qv.x; qw[g][1] = qv.y; qw[g][2] = qv.z; qw[g][3] = qv.w;
     }
-    v4i A[2][4], bl[2], bh[2], bb[2], bm[2];
+    const int urow = 32 * (RB == 4 ? wave : rb0) + l32;
+    float hsum[8];
+    v4i A[2][4], bl[2], bh[2], bb[2];
     auto read_a = [&](int j, int buf) __attribute__((always_inline)) {
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
@@ -125,9 +147,18 @@ gemm_q5k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
         A[buf][rb] = *reinterpret_cast<const v4i*>(xt + row * 256 + 16 * ((2 * j + h) ^ (row & 15)));
       }
     };
+    auto xsum_half = [&](int j) __attribute__((always_inline)) {
+      const v4i xv = RB == 1 ? A[j & 1][0]
+                             : *reinterpret_cast<const v4i*>(xt + urow * 256 + 16 * ((2 * j + h) ^ (urow & 15)));
+      int sacc = __builtin_amdgcn_sdot4(xv[0], 0x01010101, 0, false);
+      sacc = __builtin_amdgcn_sdot4(xv[1], 0x01010101, sacc, false);
+      sacc = __builtin_amdgcn_sdot4(xv[2], 0x01010101, sacc, false);
+      sacc = __builtin_amdgcn_sdot4(xv[3], 0x01010101, sacc, false);
+      hsum[j] = (float)sacc;
+    };
     auto build = [&](int j, int buf) __attribute__((always_inline)) {
-      const uint32_t scw = j < 4 ? sm.sc_lo : sm.sc_hi, mnw = j < 4 ? sm.mn_lo : sm.mn_hi;
-      const uint32_t sc = (scw >> (8 * (j & 3))) & 0xFF, mn = (mnw >> (8 * (j & 3))) & 0xFF;
+      const uint32_t scw = j < 4 ? sm.sc_lo : sm.sc_hi;
+      const uint32_t sc = (scw >> (8 * (j & 3))) & 0xFF;
       // q = n + 16 b (n the nibble, b the 5th bit): q * sc = n (sc & 7) +
       // 8 (n (sc >> 3) + 2 b sc); every B byte <= 126
 #pragma unroll
@@ -138,10 +169,8 @@ gemm_q5k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
         bh[buf][e] = (int)mul_bytes(nib, sc >> 3);
         bb[buf][e] = (int)mul_bytes(hb, 2 * sc);
       }
-      const int bmv = (int)__builtin_amdgcn_perm(0u, mn, 0u);  // byte 0 of mn in all four bytes
-      bm[buf] = v4i{bmv, bmv, bmv, bmv};
     };
-    v16i_t tl[4], th[4], tu[4];
+    v16i_t tl[4], th[4];
     read_a(0, 0);
     build(0, 0);
 #pragma unroll
@@ -154,27 +183,39 @@ gemm_q5k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
         if (j == 0) {
           tl[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bl[c], v16i_t{}, 0, 0, 0);
           th[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bh[c], v16i_t{}, 0, 0, 0);
-          tu[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bm[c], v16i_t{}, 0, 0, 0);
         } else {
           tl[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bl[c], tl[rb], 0, 0, 0);
           th[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bh[c], th[rb], 0, 0, 0);
-          tu[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bm[c], tu[rb], 0, 0, 0);
         }
         th[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bb[c], th[rb], 0, 0, 0);
       }
+      xsum_half(j);
       if (j < 7) build(j + 1, c ^ 1);
-      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // the LDS reads first
+      __builtin_amdgcn_sched_group_barrier(0x100, RB == 4 ? 5 : 1, 0);  // the LDS reads first
 #pragma unroll
-      for (int k = 0; k < 16; ++k) {
+      for (int k = 0; k < 3 * RB; ++k) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // 3 VALU
+        __builtin_amdgcn_sched_group_barrier(0x002, RB == 4 ? 3 : 8, 0);  // VALU
       }
+    }
+    v8h ua, ub;
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      ua[jj] = (_Float16)hsum[jj];
+      ub[jj] = (_Float16)(float)(((jj < 4 ? sm.mn_lo : sm.mn_hi) >> (8 * (jj & 3))) & 0xFF);
     }
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-      for (int e = 0; e < 16; ++e)
-        f[rb][e] += d * (float)(tl[rb][e] + 8 * th[rb][e]) - dmin * (float)tu[rb][e];
+      for (int e = 0; e < 16; ++e) f[rb][e] += d * (float)(tl[rb][e] + 8 * th[rb][e]);
+    // the previous super-block's U (with RB = 4 its operands were published
+    // before the barrier this compute follows), then this one's goes pending;
+    // both launches apply the same operations in the same order
+    if (slot >= 0) u_step(slot ^ 1);
+    if constexpr (RB == 4) xh_l[slot & 1][wave][lane] = __builtin_bit_cast(uint4, ua);
+    else u_a = ua;
+    u_dmin = dmin;
+    u_b = ub;
   };
 
   load(0, xs0, ws0);
@@ -183,15 +224,19 @@ gemm_q5k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
   int sb = 0;
   for (; sb + 1 < nsb; sb += 2) {
     load(sb + 1, xs1, ws1);
-    compute(xs0, ws0);
+    compute(xs0, ws0, sb == 0 ? -2 : 0);
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
     if (sb + 2 < nsb) load(sb + 2, xs0, ws0);
-    compute(xs1, ws1);
+    compute(xs1, ws1, 1);
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
   }
-  if (sb < nsb) compute(xs0, ws0);
+  if (sb < nsb) {
+    compute(xs0, ws0, sb == 0 ? -2 : 0);
+    if constexpr (RB == 4) __syncthreads();
+  }
+  u_step((nsb - 1) & 1);  // the last super-block's U
 
   const int n = n0 + 32 * wave + l32;
   // the row scales first, unconditionally (clamped rows): one wait, not one per element

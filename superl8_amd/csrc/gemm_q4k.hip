@@ -35,6 +35,7 @@ namespace sl8 {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
 constexpr int Q4K_BYTES = 144;
 constexpr int GEMV_ROWS = 16;
@@ -575,8 +576,11 @@ gemv_q4k_small_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_
 //         B operand fits int8: q * (sc & 7) and q * (sc >> 3) (<= 105; one
 //         32-bit multiply scales 4 nibbles at once, no carries), combined as
 //         T_lo + 8 T_hi;
-//   U_j = <x_j, m_j> with m_j broadcast in the B operand (the min term);
-// and once per super-block f += d * (T_lo + 8 T_hi) - dmin * U (fp32).
+// and once per super-block f += d * (T_lo + 8 T_hi) (fp32). The min term
+//   U = sum_j m_j * sum(x_j) is one v_mfma_f32_32x32x16_f16 per row block and
+// super-block on the x half-sums and the mins (both exact in fp16; U is an
+// exact fp32 integer), applied as f -= dmin * U one super-block later (the
+// half-sums of a row block are formed by one wave and shared through LDS).
 // x chunks are XOR-swizzled in LDS by row (rows are 256 B = one bank line);
 // weight rows are 144 B apart, which already spreads 16 rows over all banks.
 // ---------------------------------------------------------------------------
@@ -592,6 +596,10 @@ gemm_q4k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
   __shared__ __attribute__((aligned(16))) int8_t xs1[TBM * 256];
   __shared__ __attribute__((aligned(16))) uint8_t ws0[TWCH * 16];
   __shared__ __attribute__((aligned(16))) uint8_t ws1[TWCH * 16];
+  // RB = 4: the fp16 A operands of the min-term MFMA (x half-sums) of one
+  // super-block, [slot][row block][lane] -- each wave forms its own row
+  // block's and reads all four after the next workgroup barrier
+  __shared__ __attribute__((aligned(16))) uint4 xh_l[RB == 4 ? 2 : 1][RB == 4 ? 4 : 1][64];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, h = lane >> 5;
@@ -625,6 +633,7 @@ gemm_q4k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
   };
 
   typedef int v16i_t __attribute__((ext_vector_type(16)));
+  typedef float v16f_t __attribute__((ext_vector_type(16)));
   // wave w owns weight rows 32 w .. 32 w + 31 (output columns) for all 128
   // activation rows (4 row blocks), so each B operand is built once per
   // workgroup. K step j of a super-block is sub-block j (lane half h holds its
@@ -636,7 +645,29 @@ gemm_q4k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
 #pragma unroll
     for (int e = 0; e < 16; ++e) f[rb][e] = 0.f;
 
-  auto compute = [&](const int8_t* xt, const uint8_t* wt) __attribute__((always_inline)) {
+  // Min term U = sum_j m_j * xsum_j on one v_mfma_f32_32x32x16_f16 per row
+  // block and super-block: A = the 16-element half-sums of x (k = 8 h + j,
+  // |sum| <= 16 * 127 = 2032: exact in fp16), B = m_j (6-bit, exact) for both
+  // halves, so U comes out as an exact fp32 integer (|U| <= 8 * 4064 * 63 <
+  // 2^24). With RB = 4 each wave sums its own row block (32 of the 128 rows)
+  // and publishes the operand in LDS; the other waves read it after the next
+  // super-block's barrier, so U of super-block sb is formed (and f -= dmin * U
+  // applied) one super-block late. RB = 1 waves share their rows and form
+  // their operand themselves, and apply U just as late, so the quarter
+  // launch's per-element arithmetic stays that of the full tiles.
+  float u_dmin = 0.f;  // dmin of the super-block whose U is pending
+  v8h u_b = {}, u_a = {};  // its m_j operand and (RB = 1) its half-sum operand
+  auto u_step = [&](int slot) __attribute__((always_inline)) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const v8h a = RB == 4 ? __builtin_bit_cast(v8h, xh_l[slot][rb][lane]) : u_a;
+      const v16f_t u = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, u_b, v16f_t{}, 0, 0, 0);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) f[rb][e] -= u_dmin * u[e];
+    }
+  };
+
+  auto compute = [&](const int8_t* xt, const uint8_t* wt, int slot) __attribute__((always_inline)) {
     const uint8_t* wr = wt + (32 * wave + l32) * Q4K_BYTES;
     const uint4 hd = *reinterpret_cast<const uint4*>(wr);
     const float d = h2f(hd.x & 0xFFFFu), dmin = h2f(hd.x >> 16);
@@ -647,7 +678,10 @@ gemm_q4k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
       const uint4 qv = *reinterpret_cast<const uint4*>(wr + 16 + 32 * g + 16 * h);
       qw[g][0] = qv.x; qw[g][1] = qv.y; qw[g][2] = qv.z; qw[g][3] = qv.w;
     }
-    v4i A[2][4], bl[2], bh[2], bm[2];
+    // this lane's x half-sums: row 32 * (own row block) + l32, half h, sub-block j
+    const int urow = 32 * (RB == 4 ? wave : rb0) + l32;
+    float hsum[8];
+    v4i A[2][4], bl[2], bh[2];
     auto read_a = [&](int j, int buf) __attribute__((always_inline)) {
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
@@ -655,19 +689,26 @@ gemm_q4k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
         A[buf][rb] = *reinterpret_cast<const v4i*>(xt + row * 256 + 16 * ((2 * j + h) ^ (row & 15)));
       }
     };
+    auto xsum_half = [&](int j) __attribute__((always_inline)) {
+      const v4i xv = RB == 1 ? A[j & 1][0]
+                             : *reinterpret_cast<const v4i*>(xt + urow * 256 + 16 * ((2 * j + h) ^ (urow & 15)));
+      int sacc = __builtin_amdgcn_sdot4(xv[0], 0x01010101, 0, false);
+      sacc = __builtin_amdgcn_sdot4(xv[1], 0x01010101, sacc, false);
+      sacc = __builtin_amdgcn_sdot4(xv[2], 0x01010101, sacc, false);
+      sacc = __builtin_amdgcn_sdot4(xv[3], 0x01010101, sacc, false);
+      hsum[j] = (float)sacc;
+    };
     auto build = [&](int j, int buf) __attribute__((always_inline)) {
-      const uint32_t scw = j < 4 ? sm.sc_lo : sm.sc_hi, mnw = j < 4 ? sm.mn_lo : sm.mn_hi;
-      const uint32_t sc = (scw >> (8 * (j & 3))) & 0xFF, mn = (mnw >> (8 * (j & 3))) & 0xFF;
+      const uint32_t scw = j < 4 ? sm.sc_lo : sm.sc_hi;
+      const uint32_t sc = (scw >> (8 * (j & 3))) & 0xFF;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const uint32_t nib = (qw[j >> 1][e] >> (4 * (j & 1))) & 0x0F0F0F0Fu;
         bl[buf][e] = (int)mul_bytes(nib, sc & 7);  // <= 15 * 7 per byte
         bh[buf][e] = (int)mul_bytes(nib, sc >> 3);
       }
-      const int bmv = (int)__builtin_amdgcn_perm(0u, mn, 0u);  // byte 0 of mn in all four bytes
-      bm[buf] = v4i{bmv, bmv, bmv, bmv};
     };
-    v16i_t tl[4], th[4], tu[4];
+    v16i_t tl[4], th[4];
     read_a(0, 0);
     build(0, 0);
 #pragma unroll
@@ -680,43 +721,63 @@ gemm_q4k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
         if (j == 0) {
           tl[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bl[c], v16i_t{}, 0, 0, 0);
           th[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bh[c], v16i_t{}, 0, 0, 0);
-          tu[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bm[c], v16i_t{}, 0, 0, 0);
         } else {
           tl[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bl[c], tl[rb], 0, 0, 0);
           th[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bh[c], th[rb], 0, 0, 0);
-          tu[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bm[c], tu[rb], 0, 0, 0);
         }
       }
+      xsum_half(j);
       if (j < 7) build(j + 1, c ^ 1);
-      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // the LDS reads first
+      __builtin_amdgcn_sched_group_barrier(0x100, RB == 4 ? 5 : 1, 0);  // the LDS reads first
 #pragma unroll
-      for (int k = 0; k < 12; ++k) {
+      for (int k = 0; k < 2 * RB; ++k) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // 3 VALU
+        __builtin_amdgcn_sched_group_barrier(0x002, RB == 4 ? 4 : 8, 0);  // VALU
       }
     }
+    // the min-term operands of this super-block
+    v8h ua;
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) ua[jj] = (_Float16)hsum[jj];
+    v8h ub;
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj)
+      ub[jj] = (_Float16)(float)(((jj < 4 ? sm.mn_lo : sm.mn_hi) >> (8 * (jj & 3))) & 0xFF);
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-      for (int e = 0; e < 16; ++e)
-        f[rb][e] += d * (float)(tl[rb][e] + (th[rb][e] << 3)) - dmin * (float)tu[rb][e];
+      for (int e = 0; e < 16; ++e) f[rb][e] += d * (float)(tl[rb][e] + (th[rb][e] << 3));
+    // the previous super-block's U (with RB = 4 its operands were published
+    // before the barrier this compute follows), then this one's goes pending;
+    // both launches apply the same operations in the same order
+    if (slot >= 0) u_step(slot ^ 1);
+    if constexpr (RB == 4) xh_l[slot & 1][wave][lane] = __builtin_bit_cast(uint4, ua);
+    else u_a = ua;
+    u_dmin = dmin;
+    u_b = ub;
   };
 
   load(0, xs0, ws0);
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __syncthreads();
+  // slot: the LDS slot this super-block's half-sums go to (RB = 4); -2 / -1
+  // for the first super-block (no U pending yet, slot 0)
   int sb = 0;
   for (; sb + 1 < nsb; sb += 2) {
     load(sb + 1, xs1, ws1);
-    compute(xs0, ws0);
+    compute(xs0, ws0, sb == 0 ? -2 : 0);
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
     if (sb + 2 < nsb) load(sb + 2, xs0, ws0);
-    compute(xs1, ws1);
+    compute(xs1, ws1, 1);
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
   }
-  if (sb < nsb) compute(xs0, ws0);
+  if (sb < nsb) {
+    compute(xs0, ws0, sb == 0 ? -2 : 0);
+    if constexpr (RB == 4) __syncthreads();
+  }
+  u_step((nsb - 1) & 1);  // the last super-block's U
 
   const int n = n0 + 32 * wave + l32;
   // the row scales first, unconditionally (clamped rows): one wait, not one per element

@@ -78,6 +78,20 @@ def test_tile_gemm_last_round_split(device, fmt, M, N, K):
     _check_exact_sum(y, ref, torch.float32)
 
 
+@pytest.mark.parametrize("fmt", ["q5k", "q6k"])
+def test_tile_quarters_bit_match_full_tiles(device, fmt):
+    """The quarter tiles of the short last round (rows 128..159, columns 16128..
+    at M = 160, N = 16635) match the same columns computed in full tiles bit
+    for bit (same per-element operations in the same order)."""
+    M, N, K, c0 = 160, 16635, 512, 126 * 128
+    x, w, wd = _case(fmt, M, N, K, seed=31, device=device)
+    x_i8, xs = _C.quantize_i8_rowwise(x)
+    fn = getattr(_C, FMT[fmt][4])
+    y = fn(x_i8, xs, wd, torch.float32)
+    y_sub = fn(x_i8, xs, wd[c0:].contiguous(), torch.float32)
+    assert torch.equal(y[:, c0:], y_sub)
+
+
 DEC_SHAPES = [(1, 4096, 3072), (1, 130, 256), (2, 4096, 5120), (4, 512, 768), (8, 17408, 5120),
               (16, 1000, 2048), (3, 33, 768), (1, 64, 16384),
               # long K: the M >= 3 MFMA kernels loop over several super-block

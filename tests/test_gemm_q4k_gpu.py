@@ -111,6 +111,20 @@ def test_tile_gemm_last_round_split(device, M, N, K):
     assert (err <= 1e-5 * np.abs(ref) + 1e-5 * np.abs(ref).max()).all(), f"max err {err.max():.3e}"
 
 
+def test_tile_quarters_bit_match_full_tiles(device):
+    """The last-round quarter launch applies the full tiles' per-element
+    operations in the same order: at M = 160, N = 16635 (260 tiles in row-major
+    order on 256 CUs) tiles 256..259 -- rows 128..159, columns 16128.. -- run as
+    quarters; the same columns computed alone (130 full tiles over the sliced
+    weights) must match them bit for bit."""
+    M, N, K, c0 = 160, 16635, 512, 126 * 128
+    x, w, wd = _case(M, N, K, seed=31, device=device)
+    x_i8, xs = _C.quantize_i8_rowwise(x)
+    y = _C.gemm_q4k(x_i8, xs, wd, torch.float32)
+    y_sub = _C.gemm_q4k(x_i8, xs, wd[c0:].contiguous(), torch.float32)
+    assert torch.equal(y[:, c0:], y_sub)
+
+
 def test_tile_matches_decode_and_large_m(device):
     """reference test_gemm_q4k.py:715-728: the tile path and the decode path agree
     (to fp16 output rounding) on the rows they share."""
