@@ -20,8 +20,10 @@
 //     n (sc_j & 7) + 8 (n (sc_j >> 3) + 2 b sc_j), and each of the three B
 //     operands n (sc & 7), n (sc >> 3), 2 b sc is at most 126, so it fits int8
 //     (a 32-bit multiply scales 4 codes at once without carries). Three
-//     MFMAs into T_lo, T_hi, T_hi plus one with m_j broadcast (the min term);
-//     per super-block f += d * (T_lo + 8 T_hi) - dmin * U.
+//     MFMAs into T_lo, T_hi, T_hi; per super-block f += d * (T_lo + 8 T_hi).
+//     The min term U = sum_j m_j * sum(x_j) on one fp16 MFMA per row block
+//     and super-block (x half-sums x mins, exact), f -= dmin * U one
+//     super-block later, as in the Q4_K tile kernel.
 //   Q6_K on v_mfma_i32_32x32x32_i8 as well, one K = 32 step per pair of
 //     16-element sub-blocks (each lane half holds one sub-block, so one scale
 //     per lane): P = (q - 32) * sc in [-4096, 4064] is split exactly into two
