@@ -669,24 +669,24 @@ extern "C" int sl8_q_outlier_gate(const void* q, int dtype, int64_t rows, int64_
 // quantize_qk + smooth_k, and the outlier gate of superl8/ops.py:115-147):
 // three launches instead of six, Q read once, K read twice, no zeroing pass.
 //
-// Launch A (one grid, two roles chosen per block):
-//   * K-mean partials: block (g, c) sums key rows [128c, 128c + 128) of
-//     group g exactly in int64 fixed point (value * 2^24, decoded from the
-//     fp16 bits) with 16-byte loads, and stores its D partial sums. The
-//     mean is exact, hence independent of the summation order.
+// Launch A: K-mean partials. Block (g, c) sums key rows [128c, 128c + 128)
+//   of group g exactly in int64 fixed point (value * 2^24, decoded from the
+//   fp16 bits) with 16-byte loads and stores its D partial sums; the mean is
+//   exact, hence independent of the summation order. Block 0 also clears the
+//   gate flag.
+// Launch M: the mean of each (group, column) from its partials (int64 ->
+//   fp64 -> / N -> fp32, as sl8_k_mean).
+// Launch B, two roles chosen per block:
+//   * K: subtracts the mean from each key row with the fp16 rounding of
+//     torch.sub and quantises it;
 //   * Q: per-row int8 quantisation (scale * q_scale_mul) and, with a gate
 //     ratio, the outlier decision for every row. f(x) = fl(max / fl(x + 1e-10))
 //     is non-increasing in x >= 0, so f(median) > ratio iff more than (D-1)/2
 //     of the row's |x| have f(|x|) > ratio: the row is decided exactly with
 //     no median search (the division is needed only for elements within
 //     2^-18 of max / ratio). A row holding a NaN never fires (torch's amax and
-//     median are NaN there). Each Q block writes one word: whether any of
-//     its rows fired.
-// Launch M: the mean of each (group, column) from its partials (int64 ->
-//   fp64 -> / N -> fp32, as sl8_k_mean); one extra block ORs the Q blocks'
-//   words into the gate flag (so the flag needs no clearing by the caller).
-// Launch B: subtracts the mean from each key row with the fp16 rounding of
-//   torch.sub and quantises it.
+//     median are NaN there). A block with a firing row ORs 1 into the flag
+//     (atomicOr), so the flag is set iff some row fires.
 // ---------------------------------------------------------------------------
 namespace sl8 {
 namespace {
