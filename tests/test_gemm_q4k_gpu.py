@@ -34,7 +34,10 @@ SHAPES = [(1, 4096, 3072), (1, 1024, 4096), (4, 4096, 4096), (8, 512, 768), (16,
           (1, 130, 256), (1, 4864, 1024), (1, 17408, 5120), (8, 17408, 5120), (5, 7, 256),
           (11, 96, 512),
           # M <= 2 (VALU path), partial and multi-chunk K splits
-          (2, 4096, 3072), (2, 130, 256), (1, 64, 16384), (2, 50, 12544), (3, 40, 16384)]
+          (2, 4096, 3072), (2, 130, 256), (1, 64, 16384), (2, 50, 12544), (3, 40, 16384),
+          # 5 <= M <= 8 (activation copies first): the K = 5120 straight-line
+          # chunk with a ragged N, and several chunks per wave
+          (6, 130, 5120), (6, 40, 16384), (8, 64, 12544)]
 
 
 @pytest.mark.parametrize("odt", [torch.float16, torch.bfloat16, torch.float32])
@@ -55,7 +58,7 @@ def test_gemv_matches_exact_sum(device, M, N, K, odt):
 
 
 XB_SHAPES = [(1, 17408, 5120), (8, 17408, 5120), (2, 130, 256), (3, 40, 16384), (16, 96, 512),
-             (5, 64, 1024), (1, 64, 16384)]
+             (5, 64, 1024), (1, 64, 16384), (7, 48, 12288), (6, 130, 5120)]
 
 
 @pytest.mark.parametrize("odt", [torch.float16, torch.float32])
