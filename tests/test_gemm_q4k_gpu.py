@@ -128,6 +128,34 @@ def test_tile_quarters_bit_match_full_tiles(device):
     assert torch.equal(y[:, c0:], y_sub)
 
 
+def test_tile_min_term_at_its_exactness_limits(device):
+    """The min term's fp16 operands at their extremes: x rows of all +127 / all
+    -127 / alternating signs per 16-element half (half-sums +-2032, the largest
+    magnitude the fp16 operand must hold exactly), every scale and min 63, every
+    nibble 15, d = dmin = 1: the tile GEMM (and the M <= 16 GEMV) against the
+    oracle's exact sums."""
+    M, N, K = 40, 256, 1024
+    nsb = K // 256
+    d = np.ones((N, nsb), np.float16)
+    sc = np.full((N, nsb, 8), 63, np.uint8)
+    q = np.full((N, nsb, 8, 32), 15, np.uint8)
+    q[1::2, :, :, ::3] = 0                      # some rows not all-15
+    w = oq.make_blocks(d, d, sc, sc.copy(), q).reshape(N, nsb * oq.TYPE_SIZE)
+    x = np.empty((M, K), np.int8)
+    x[0::3] = 127
+    x[1::3] = -127
+    x[2::3] = np.where((np.arange(K) // 16) % 2 == 0, 127, -127)
+    xs = np.ones(M, np.float32)
+    ref = oq.gemv(x, xs, w, K)
+    xt, xst, wd = (torch.from_numpy(a).to(device) for a in (x, xs, w))
+    y = _C.gemm_q4k(xt, xst, wd, torch.float32)
+    err = np.abs(_np(y).astype(np.float64) - ref)
+    assert (err <= 1e-6 * np.abs(ref).max()).all(), f"tile: max err {err.max():.3e}"
+    y16 = _C.gemm_decode_q4k(xt[:16].contiguous(), xst[:16].contiguous(), wd, torch.float32)
+    err = np.abs(_np(y16).astype(np.float64) - ref[:16])
+    assert (err <= 1e-6 * np.abs(ref).max()).all(), f"gemv: max err {err.max():.3e}"
+
+
 def test_tile_matches_decode_and_large_m(device):
     """reference test_gemm_q4k.py:715-728: the tile path and the decode path agree
     (to fp16 output rounding) on the rows they share."""
