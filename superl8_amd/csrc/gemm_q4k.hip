@@ -584,62 +584,74 @@ gemv_q4k_small_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_
 // x chunks are XOR-swizzled in LDS by row (rows are 256 B = one bank line);
 // weight rows are 144 B apart, which already spreads 16 rows over all banks.
 // ---------------------------------------------------------------------------
+#ifndef SL8_KQ_NW8
+#define SL8_KQ_NW8 1
+#endif
 constexpr int TBM = 128, TBN = 128;  // output tile
-constexpr int TWCH = (TBN * 9 + 255) / 256 * 256;  // weight-tile 16-B chunks, padded to whole copies
 
-template <int OUT_DT, int RB>
-__global__ void __launch_bounds__(256, 1)
+template <int OUT_DT, int RB, int NW = 4>
+__global__ void __launch_bounds__(64 * NW, 1)
 gemm_q4k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
                      const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K,
                      int nt_x, int xcd_m, int tile0) {
+  // RB row blocks (32 rows) per wave, NW waves per workgroup: a full tile is
+  // RB = 4, NW = 4 (one wave per SIMD, every wave over all 128 rows) or RB = 2,
+  // NW = 8 (two waves per SIMD, each over 64 rows); RB = 1, NW = 4 is a row
+  // quarter of a tile (the short last round)
+  constexpr bool QTR = RB * NW < 16;
+  constexpr int NT = 64 * NW;
+  constexpr int WCH = (TBN * 9 + NT - 1) / NT * NT;  // weight-tile 16-B chunks, whole copies
   __shared__ __attribute__((aligned(16))) int8_t xs0[TBM * 256];
   __shared__ __attribute__((aligned(16))) int8_t xs1[TBM * 256];
-  __shared__ __attribute__((aligned(16))) uint8_t ws0[TWCH * 16];
-  __shared__ __attribute__((aligned(16))) uint8_t ws1[TWCH * 16];
-  // RB = 4: the fp16 A operands of the min-term MFMA (x half-sums) of one
-  // super-block, [slot][row block][lane] -- each wave forms its own row
-  // block's and reads all four after the next workgroup barrier
-  __shared__ __attribute__((aligned(16))) uint4 xh_l[RB == 4 ? 2 : 1][RB == 4 ? 4 : 1][64];
+  __shared__ __attribute__((aligned(16))) uint8_t ws0[WCH * 16];
+  __shared__ __attribute__((aligned(16))) uint8_t ws1[WCH * 16];
+  // full tiles: the fp16 A operands of the min-term MFMA (x half-sums) of one
+  // super-block, [slot][row block][lane], formed by the waves together and
+  // read after the next workgroup barrier
+  __shared__ __attribute__((aligned(16))) uint4 xh_l[QTR ? 1 : 2][QTR ? 1 : 4][64];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, h = lane >> 5;
-  // RB = 4: one 128 x 128 tile per workgroup (tiles tile0, tile0 + 1, ...);
-  // RB = 1: the quarter blockIdx.x & 3 (32 rows) of tile tile0 + blockIdx.x / 4,
+  // full tiles: one 128 x 128 tile per workgroup (tiles tile0, tile0 + 1, ...);
+  // quarters: the quarter blockIdx.x & 3 (32 rows) of tile tile0 + blockIdx.x / 4,
   // so a short last round of tiles spreads over 4x the workgroups
-  const int tile = tile0 + (RB == 4 ? (int)blockIdx.x : (int)(blockIdx.x >> 2));
+  const int tile = tile0 + (QTR ? (int)(blockIdx.x >> 2) : (int)blockIdx.x);
   int ct, rt;
   kq_tile_coords(tile, nt_x, xcd_m, ct, rt);
   const int n0 = ct * TBN, m0 = rt * TBM;
-  const int rb0 = RB == 4 ? 0 : (int)(blockIdx.x & 3);
+  const int rb0 = QTR ? (int)(blockIdx.x & 3) : 0;
+  const int cg = wave & 3;                                  // the wave's 32 output columns
+  const int rbw = QTR ? rb0 : (NW == 8 ? (wave >> 2) * RB : 0);  // its first row block
   const int nsb = K >> 8;
   const int64_t row_bytes = (int64_t)nsb * Q4K_BYTES;
 
   // copies of super-block sb into (xd, wd); chunk P of the tile lands at P*16
   auto load = [&](int sb, int8_t* xd, uint8_t* wd) __attribute__((always_inline)) {
+    constexpr int XCH = QTR ? 512 : TBM * 16;  // a quarter copies only its 32 rows
 #pragma unroll
-    for (int ii = 0; ii < (RB == 4 ? TBM * 16 / 256 : 2); ++ii) {
-      const int i = (RB == 4 ? 0 : 2 * rb0) + ii;  // a quarter copies only its 32 rows
-      const int P = i * 256 + tid, row = P >> 4;
+    for (int i = 0; i < XCH / NT; ++i) {
+      const int P0 = (QTR ? rb0 * 512 : 0) + i * NT;
+      const int P = P0 + tid, row = P >> 4;
       const int c = (P & 15) ^ (row & 15);
       const int8_t* src = x + (int64_t)min(m0 + row, M - 1) * K + (int64_t)sb * 256 + 16 * c;
-      __builtin_amdgcn_global_load_lds((q4_gptr_t)src, (q4_lptr_t)(xd + (i * 256 + wave * 64) * 16), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((q4_gptr_t)src, (q4_lptr_t)(xd + (P0 + wave * 64) * 16), 16, 0, 0);
     }
 #pragma unroll
-    for (int i = 0; i < TWCH / 256; ++i) {
-      const int P = min(i * 256 + tid, TBN * 9 - 1), row = P / 9, c = P - 9 * row;
+    for (int i = 0; i < WCH / NT; ++i) {
+      const int P = min(i * NT + tid, TBN * 9 - 1), row = P / 9, c = P - 9 * row;
       const uint8_t* src = w + (int64_t)min(n0 + row, N - 1) * row_bytes + (int64_t)sb * Q4K_BYTES + 16 * c;
-      __builtin_amdgcn_global_load_lds((q4_gptr_t)src, (q4_lptr_t)(wd + (i * 256 + wave * 64) * 16), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((q4_gptr_t)src, (q4_lptr_t)(wd + (i * NT + wave * 64) * 16), 16, 0, 0);
     }
   };
 
   typedef int v16i_t __attribute__((ext_vector_type(16)));
   typedef float v16f_t __attribute__((ext_vector_type(16)));
-  // wave w owns weight rows 32 w .. 32 w + 31 (output columns) for all 128
-  // activation rows (4 row blocks), so each B operand is built once per
-  // workgroup. K step j of a super-block is sub-block j (lane half h holds its
-  // elements 16 h .. 16 h + 15); step j + 1's A reads and B operands are formed
-  // while step j's 12 MFMAs run (one scheduling region per step).
-  float f[4][16];
+  // wave (cg, row group) owns weight rows 32 cg .. 32 cg + 31 (output columns)
+  // for the activation rows of its RB row blocks. K step j of a super-block is
+  // sub-block j (lane half h holds its elements 16 h .. 16 h + 15); step j + 1's
+  // A reads and B operands are formed while step j's MFMAs run (one
+  // scheduling region per step).
+  float f[RB][16];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
@@ -649,26 +661,32 @@ gemm_q4k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
   // block and super-block: A = the 16-element half-sums of x (k = 8 h + j,
   // |sum| <= 16 * 127 = 2032: exact in fp16), B = m_j (6-bit, exact) for both
   // halves, so U comes out as an exact fp32 integer (|U| <= 8 * 4064 * 63 <
-  // 2^24). With RB = 4 each wave sums its own row block (32 of the 128 rows)
-  // and publishes the operand in LDS; the other waves read it after the next
-  // super-block's barrier, so U of super-block sb is formed (and f -= dmin * U
-  // applied) one super-block late. RB = 1 waves share their rows and form
-  // their operand themselves, and apply U just as late, so the quarter
-  // launch's per-element arithmetic stays that of the full tiles.
+  // 2^24). In a full tile the half-sums of the 4 row blocks are formed once
+  // (NW = 4: wave w sums row block w; NW = 8: wave w row block w & 3, sub-blocks
+  // 4 (w >> 2) .. +3) and published in LDS; every wave reads its row blocks'
+  // after the next super-block's barrier, so U of super-block sb is formed
+  // (and f -= dmin * U applied) one super-block late. Quarter waves share their
+  // rows and form their operand themselves, and apply U just as late, so the
+  // quarter launch's per-element arithmetic stays that of the full tiles.
   float u_dmin = 0.f;  // dmin of the super-block whose U is pending
-  v8h u_b = {}, u_a = {};  // its m_j operand and (RB = 1) its half-sum operand
+  v8h u_b = {}, u_a = {};  // its m_j operand and (quarters) its half-sum operand
   auto u_step = [&](int slot) __attribute__((always_inline)) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
-      const v8h a = RB == 4 ? __builtin_bit_cast(v8h, xh_l[slot][rb][lane]) : u_a;
+      const v8h a = QTR ? u_a : __builtin_bit_cast(v8h, xh_l[slot][rbw + rb][lane]);
       const v16f_t u = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, u_b, v16f_t{}, 0, 0, 0);
 #pragma unroll
       for (int e = 0; e < 16; ++e) f[rb][e] -= u_dmin * u[e];
     }
   };
+  // the half-sums this wave forms: row block urb, sub-blocks ju0 .. ju0 + JN - 1
+  constexpr int JN = (NW == 8 && !QTR) ? 4 : 8;
+  const int urb = QTR ? rb0 : (wave & 3);
+  const int ju0 = (NW == 8 && !QTR) ? 4 * (wave >> 2) : 0;
+  const int urow = 32 * urb + l32;
 
   auto compute = [&](const int8_t* xt, const uint8_t* wt, int slot) __attribute__((always_inline)) {
-    const uint8_t* wr = wt + (32 * wave + l32) * Q4K_BYTES;
+    const uint8_t* wr = wt + (32 * cg + l32) * Q4K_BYTES;
     const uint4 hd = *reinterpret_cast<const uint4*>(wr);
     const float d = h2f(hd.x & 0xFFFFu), dmin = h2f(hd.x >> 16);
     const ScMin sm = unpack_scmin(hd.y, hd.z, hd.w);
@@ -678,25 +696,25 @@ gemm_q4k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
       const uint4 qv = *reinterpret_cast<const uint4*>(wr + 16 + 32 * g + 16 * h);
       qw[g][0] = qv.x; qw[g][1] = qv.y; qw[g][2] = qv.z; qw[g][3] = qv.w;
     }
-    // this lane's x half-sums: row 32 * (own row block) + l32, half h, sub-block j
-    const int urow = 32 * (RB == 4 ? wave : rb0) + l32;
     float hsum[8];
-    v4i A[2][4], bl[2], bh[2];
+    v4i A[2][RB], bl[2], bh[2];
     auto read_a = [&](int j, int buf) __attribute__((always_inline)) {
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
-        const int row = 32 * (rb + rb0) + l32;
+        const int row = 32 * (rbw + rb) + l32;
         A[buf][rb] = *reinterpret_cast<const v4i*>(xt + row * 256 + 16 * ((2 * j + h) ^ (row & 15)));
       }
     };
-    auto xsum_half = [&](int j) __attribute__((always_inline)) {
-      const v4i xv = RB == 1 ? A[j & 1][0]
-                             : *reinterpret_cast<const v4i*>(xt + urow * 256 + 16 * ((2 * j + h) ^ (urow & 15)));
+    // half-sum of sub-block ju0 + jj (jj < JN) of this lane's row urow, half h
+    auto xsum_half = [&](int jj) __attribute__((always_inline)) {
+      const int j = ju0 + jj;
+      const v4i xv = QTR ? A[jj & 1][0]
+                         : *reinterpret_cast<const v4i*>(xt + urow * 256 + 16 * ((2 * j + h) ^ (urow & 15)));
       int sacc = __builtin_amdgcn_sdot4(xv[0], 0x01010101, 0, false);
       sacc = __builtin_amdgcn_sdot4(xv[1], 0x01010101, sacc, false);
       sacc = __builtin_amdgcn_sdot4(xv[2], 0x01010101, sacc, false);
       sacc = __builtin_amdgcn_sdot4(xv[3], 0x01010101, sacc, false);
-      hsum[j] = (float)sacc;
+      hsum[jj] = (float)sacc;
     };
     auto build = [&](int j, int buf) __attribute__((always_inline)) {
       const uint32_t scw = j < 4 ? sm.sc_lo : sm.sc_hi;
@@ -708,7 +726,7 @@ gemm_q4k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
         bh[buf][e] = (int)mul_bytes(nib, sc >> 3);
       }
     };
-    v16i_t tl[4], th[4];
+    v16i_t tl[RB], th[RB];
     read_a(0, 0);
     build(0, 0);
 #pragma unroll
@@ -726,9 +744,12 @@ gemm_q4k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
           th[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bh[c], th[rb], 0, 0, 0);
         }
       }
-      xsum_half(j);
+      // the half-sums: a quarter wave sums step j's own A operand; in a full
+      // tile this wave's JN sub-blocks are spread over the steps
+      if constexpr (JN == 8) xsum_half(j);
+      else if (j & 1) xsum_half(j >> 1);
       if (j < 7) build(j + 1, c ^ 1);
-      __builtin_amdgcn_sched_group_barrier(0x100, RB == 4 ? 5 : 1, 0);  // the LDS reads first
+      __builtin_amdgcn_sched_group_barrier(0x100, RB + (QTR ? 0 : 1), 0);  // the LDS reads first
 #pragma unroll
       for (int k = 0; k < 2 * RB; ++k) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
@@ -736,9 +757,6 @@ gemm_q4k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
       }
     }
     // the min-term operands of this super-block
-    v8h ua;
-#pragma unroll
-    for (int jj = 0; jj < 8; ++jj) ua[jj] = (_Float16)hsum[jj];
     v8h ub;
 #pragma unroll
     for (int jj = 0; jj < 8; ++jj)
@@ -747,12 +765,25 @@ gemm_q4k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
       for (int e = 0; e < 16; ++e) f[rb][e] += d * (float)(tl[rb][e] + (th[rb][e] << 3));
-    // the previous super-block's U (with RB = 4 its operands were published
+    // the previous super-block's U (in a full tile its operands were published
     // before the barrier this compute follows), then this one's goes pending;
     // both launches apply the same operations in the same order
     if (slot >= 0) u_step(slot ^ 1);
-    if constexpr (RB == 4) xh_l[slot & 1][wave][lane] = __builtin_bit_cast(uint4, ua);
-    else u_a = ua;
+    if constexpr (QTR) {
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) u_a[jj] = (_Float16)hsum[jj];
+    } else if constexpr (JN == 8) {
+      v8h ua;
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) ua[jj] = (_Float16)hsum[jj];
+      xh_l[slot & 1][urb][lane] = __builtin_bit_cast(uint4, ua);
+    } else {
+      typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+      v4h ua;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) ua[jj] = (_Float16)hsum[jj];
+      reinterpret_cast<uint2*>(&xh_l[slot & 1][urb][lane])[ju0 >> 2] = __builtin_bit_cast(uint2, ua);
+    }
     u_dmin = dmin;
     u_b = ub;
   };
@@ -760,7 +791,7 @@ gemm_q4k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
   load(0, xs0, ws0);
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __syncthreads();
-  // slot: the LDS slot this super-block's half-sums go to (RB = 4); -2 / -1
+  // slot: the LDS slot this super-block's half-sums go to (full tiles); -2
   // for the first super-block (no U pending yet, slot 0)
   int sb = 0;
   for (; sb + 1 < nsb; sb += 2) {
@@ -775,23 +806,23 @@ gemm_q4k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
   }
   if (sb < nsb) {
     compute(xs0, ws0, sb == 0 ? -2 : 0);
-    if constexpr (RB == 4) __syncthreads();
+    if constexpr (!QTR) __syncthreads();
   }
   u_step((nsb - 1) & 1);  // the last super-block's U
 
-  const int n = n0 + 32 * wave + l32;
+  const int n = n0 + 32 * cg + l32;
   // the row scales first, unconditionally (clamped rows): one wait, not one per element
   float xsv[RB][16];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int e = 0; e < 16; ++e)
-      xsv[rb][e] = x_scale[min(m0 + 32 * (rb + rb0) + 8 * (e >> 2) + 4 * h + (e & 3), M - 1)];
+      xsv[rb][e] = x_scale[min(m0 + 32 * (rbw + rb) + 8 * (e >> 2) + 4 * h + (e & 3), M - 1)];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const int m = m0 + 32 * (rb + rb0) + 8 * (e >> 2) + 4 * h + (e & 3);
+      const int m = m0 + 32 * (rbw + rb) + 8 * (e >> 2) + 4 * h + (e & 3);
       if (m < M && n < N) st_out<OUT_DT>(out, (int64_t)m * N + n, f[rb][e] * xsv[rb][e]);
     }
 }
@@ -805,14 +836,14 @@ void launch_gemm_tile(const int8_t* x, const float* xs, const uint8_t* w, void* 
   const int rem = T % P, nfull = (T >= P && rem > 0 && rem <= P / 2) ? T - rem : T;
   // XCD-aware tile order (kq_tile_coords) when the column tiles split evenly over the 8 XCDs
   const int xm = (SL8_KQ_XCD && ntx % 8 == 0) ? (M + TBM - 1) / TBM : 0;
-#define SL8_Q4T(RB, G, T0)                                                                                  \
+#define SL8_Q4T(RB, NW, G, T0)                                                                              \
   switch (odt) {                                                                                            \
-    case SL8_DTYPE_F16: gemm_q4k_tile_kernel<SL8_DTYPE_F16, RB><<<G, 256, 0, st>>>(x, xs, w, out, M, N, K, ntx, xm, T0); break; \
-    case SL8_DTYPE_BF16: gemm_q4k_tile_kernel<SL8_DTYPE_BF16, RB><<<G, 256, 0, st>>>(x, xs, w, out, M, N, K, ntx, xm, T0); break; \
-    default: gemm_q4k_tile_kernel<SL8_DTYPE_F32, RB><<<G, 256, 0, st>>>(x, xs, w, out, M, N, K, ntx, xm, T0); break;        \
+    case SL8_DTYPE_F16: gemm_q4k_tile_kernel<SL8_DTYPE_F16, RB, NW><<<G, 64 * NW, 0, st>>>(x, xs, w, out, M, N, K, ntx, xm, T0); break; \
+    case SL8_DTYPE_BF16: gemm_q4k_tile_kernel<SL8_DTYPE_BF16, RB, NW><<<G, 64 * NW, 0, st>>>(x, xs, w, out, M, N, K, ntx, xm, T0); break; \
+    default: gemm_q4k_tile_kernel<SL8_DTYPE_F32, RB, NW><<<G, 64 * NW, 0, st>>>(x, xs, w, out, M, N, K, ntx, xm, T0); break;        \
   }
-  SL8_Q4T(4, nfull, 0)
-  if (nfull < T) SL8_Q4T(1, 4 * (T - nfull), nfull)
+  if (SL8_KQ_NW8) { SL8_Q4T(2, 8, nfull, 0) } else { SL8_Q4T(4, 4, nfull, 0) }
+  if (nfull < T) SL8_Q4T(1, 4, 4 * (T - nfull), nfull)
 #undef SL8_Q4T
 }
 
