@@ -43,91 +43,114 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 constexpr int Q5K_BYTES = 176;
 constexpr int Q6K_BYTES = 210;
 constexpr int KBM = 128, KBN = 128;                       // output tile
-constexpr int T5CH = (KBN * 11 + 255) / 256 * 256;       // Q5_K weight-tile 16-B chunks
+// full k-quant tiles on 8 waves (two per SIMD, RB = 2): config 4's shape at
+// M = 512, same box, Q4_K 143 -> 123 us, Q5_K 174 -> 159 us; Q6_K, whose B
+// operands cost the most VALU to build (each is then built by two waves),
+// 186 -> 205 us, so it keeps 4 waves
+#ifndef SL8_KQ_NW8
+#define SL8_KQ_NW8 1
+#endif
+#ifndef SL8_Q6_NW8
+#define SL8_Q6_NW8 0
+#endif
 
-// x tile copy: 128 rows x 256 int8 of super-block sb; 16-byte chunk c of row r
-// lands at r * 256 + 16 * (c ^ (r & 15)) (rows are one 256-byte bank line).
-// NI = 8: all 128 rows; NI = 2: rows 32 q .. 32 q + 31 only (i from 2 q; a
-// last-round quarter workgroup reads no other rows)
-template <int NI = KBM * 16 / 256>
+// x tile copy by NT threads: 128 rows x 256 int8 of super-block sb; 16-byte
+// chunk c of row r lands at r * 256 + 16 * (c ^ (r & 15)) (rows are one
+// 256-byte bank line). QTR: rows 32 q .. 32 q + 31 only (a last-round
+// quarter workgroup reads no other rows)
+template <int NT, bool QTR>
 __device__ __forceinline__ void copy_x_tile(const int8_t* x, int8_t* xd, int m0, int M, int K, int sb,
                                             int tid, int wave, int q = 0) {
+  constexpr int XCH = QTR ? 512 : KBM * 16;
 #pragma unroll
-  for (int ii = 0; ii < NI; ++ii) {
-    const int i = (NI == KBM * 16 / 256 ? 0 : 2 * q) + ii;
-    const int P = i * 256 + tid, row = P >> 4;
+  for (int i = 0; i < XCH / NT; ++i) {
+    const int P0 = (QTR ? q * 512 : 0) + i * NT;
+    const int P = P0 + tid, row = P >> 4;
     const int c = (P & 15) ^ (row & 15);
     const int8_t* src = x + (int64_t)min(m0 + row, M - 1) * K + (int64_t)sb * 256 + 16 * c;
-    __builtin_amdgcn_global_load_lds((kq_gptr_t)src, (kq_lptr_t)(xd + (i * 256 + wave * 64) * 16), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((kq_gptr_t)src, (kq_lptr_t)(xd + (P0 + wave * 64) * 16), 16, 0, 0);
   }
 }
 
 // ---------------------------------------------------------------------------
 // Q5_K tile GEMM
 // ---------------------------------------------------------------------------
-template <int OUT_DT, int RB>
-__global__ void __launch_bounds__(256, 1)
+// RB row blocks (32 rows) per wave, NW waves per workgroup, as the Q4_K tile
+// kernel: full tiles RB = 2, NW = 8 (two waves per SIMD, each over 64 rows)
+// or RB = 4, NW = 4; RB = 1, NW = 4 is a row quarter of a tile
+template <int OUT_DT, int RB, int NW = 4>
+__global__ void __launch_bounds__(64 * NW, 1)
 gemm_q5k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
                      const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K,
                      int nt_x, int xcd_m, int tile0) {
+  constexpr bool QTR = RB * NW < 16;
+  constexpr int NT = 64 * NW;
+  constexpr int WCH = (KBN * 11 + NT - 1) / NT * NT;  // weight-tile 16-B chunks, whole copies
   __shared__ __attribute__((aligned(16))) int8_t xs0[KBM * 256];
   __shared__ __attribute__((aligned(16))) int8_t xs1[KBM * 256];
-  __shared__ __attribute__((aligned(16))) uint8_t ws0[T5CH * 16];
-  __shared__ __attribute__((aligned(16))) uint8_t ws1[T5CH * 16];
-  // RB = 4: the min-term MFMA's A operands (x half-sums) of one super-block,
-  // [slot][row block][lane]; the scheme of the Q4_K tile kernel
-  __shared__ __attribute__((aligned(16))) uint4 xh_l[RB == 4 ? 2 : 1][RB == 4 ? 4 : 1][64];
+  __shared__ __attribute__((aligned(16))) uint8_t ws0[WCH * 16];
+  __shared__ __attribute__((aligned(16))) uint8_t ws1[WCH * 16];
+  // full tiles: the min-term MFMA's A operands (x half-sums) of one
+  // super-block, [slot][row block][lane]; the scheme of the Q4_K tile kernel
+  __shared__ __attribute__((aligned(16))) uint4 xh_l[QTR ? 1 : 2][QTR ? 1 : 4][64];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, h = lane >> 5;
-  // RB = 4: one 128 x 128 tile per workgroup (tiles tile0, tile0 + 1, ...);
-  // RB = 1: the quarter blockIdx.x & 3 (32 rows) of tile tile0 + blockIdx.x / 4,
+  // full tiles: one 128 x 128 tile per workgroup (tiles tile0, tile0 + 1, ...);
+  // quarters: the quarter blockIdx.x & 3 (32 rows) of tile tile0 + blockIdx.x / 4,
   // so a short last round of tiles spreads over 4x the workgroups
-  const int tile = tile0 + (RB == 4 ? (int)blockIdx.x : (int)(blockIdx.x >> 2));
+  const int tile = tile0 + (QTR ? (int)(blockIdx.x >> 2) : (int)blockIdx.x);
   int ct, rt;
   kq_tile_coords(tile, nt_x, xcd_m, ct, rt);
   const int n0 = ct * KBN, m0 = rt * KBM;
-  const int rb0 = RB == 4 ? 0 : (int)(blockIdx.x & 3);
+  const int rb0 = QTR ? (int)(blockIdx.x & 3) : 0;
+  const int cg = wave & 3;                                       // the wave's 32 output columns
+  const int rbw = QTR ? rb0 : (NW == 8 ? (wave >> 2) * RB : 0);  // its first row block
   const int nsb = K >> 8;
   const int64_t row_bytes = (int64_t)nsb * Q5K_BYTES;
 
   auto load = [&](int sb, int8_t* xd, uint8_t* wd) __attribute__((always_inline)) {
-    copy_x_tile<RB == 4 ? KBM * 16 / 256 : 2>(x, xd, m0, M, K, sb, tid, wave, rb0);
+    copy_x_tile<NT, QTR>(x, xd, m0, M, K, sb, tid, wave, rb0);
 #pragma unroll
-    for (int i = 0; i < T5CH / 256; ++i) {
-      const int P = min(i * 256 + tid, KBN * 11 - 1), row = P / 11, c = P - 11 * row;
+    for (int i = 0; i < WCH / NT; ++i) {
+      const int P = min(i * NT + tid, KBN * 11 - 1), row = P / 11, c = P - 11 * row;
       const uint8_t* src = w + (int64_t)min(n0 + row, N - 1) * row_bytes + (int64_t)sb * Q5K_BYTES + 16 * c;
-      __builtin_amdgcn_global_load_lds((kq_gptr_t)src, (kq_lptr_t)(wd + (i * 256 + wave * 64) * 16), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((kq_gptr_t)src, (kq_lptr_t)(wd + (i * NT + wave * 64) * 16), 16, 0, 0);
     }
   };
 
-  // wave w owns weight rows 32 w .. 32 w + 31 (output columns) for all 128
-  // activation rows (4 row blocks), so each B operand is built once per
-  // workgroup; step j + 1's A reads and B operands are formed while step j's
-  // 16 MFMAs run (one scheduling region per step)
-  float f[4][16];
+  // wave (cg, row group) owns weight rows 32 cg .. 32 cg + 31 (output
+  // columns) for its RB row blocks; step j + 1's A reads and B operands are
+  // formed while step j's MFMAs run (one scheduling region per step)
+  float f[RB][16];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int e = 0; e < 16; ++e) f[rb][e] = 0.f;
 
   // min term U = sum_j m_j * xsum_j on one fp16 MFMA per row block and
-  // super-block (exact: fp16 half-sums and mins, fp32 integer result); with
-  // RB = 4 one super-block late through LDS, as in the Q4_K tile kernel
+  // super-block (exact: fp16 half-sums and mins, fp32 integer result); in a
+  // full tile one super-block late through LDS, as in the Q4_K tile kernel
   float u_dmin = 0.f;
-  v8h u_b = {}, u_a = {};  // its m_j operand and (RB = 1) its half-sum operand
+  v8h u_b = {}, u_a = {};  // its m_j operand and (quarters) its half-sum operand
   auto u_step = [&](int slot) __attribute__((always_inline)) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
-      const v8h a = RB == 4 ? __builtin_bit_cast(v8h, xh_l[slot][rb][lane]) : u_a;
+      const v8h a = QTR ? u_a : __builtin_bit_cast(v8h, xh_l[slot][rbw + rb][lane]);
       const v16f_t u = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, u_b, v16f_t{}, 0, 0, 0);
 #pragma unroll
       for (int e = 0; e < 16; ++e) f[rb][e] -= u_dmin * u[e];
     }
   };
 
+  // the half-sums this wave forms: row block urb, sub-blocks ju0 .. ju0 + JN - 1
+  constexpr int JN = (NW == 8 && !QTR) ? 4 : 8;
+  const int urb = QTR ? rb0 : (wave & 3);
+  const int ju0 = (NW == 8 && !QTR) ? 4 * (wave >> 2) : 0;
+  const int urow = 32 * urb + l32;
+
   auto compute = [&](const int8_t* xt, const uint8_t* wt, int slot) __attribute__((always_inline)) {
-    const uint8_t* wr = wt + (32 * wave + l32) * Q5K_BYTES;
+    const uint8_t* wr = wt + (32 * cg + l32) * Q5K_BYTES;
     const uint4 hd = *reinterpret_cast<const uint4*>(wr);
     const float d = h2f(hd.x & 0xFFFFu), dmin = h2f(hd.x >> 16);
     const ScMin sm = unpack_scmin(hd.y, hd.z, hd.w);
@@ -139,24 +162,25 @@ gemm_q5k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
       const uint4 qv = *reinterpret_cast<const uint4*>(wr + 48 + 32 * g + 16 * h);
       qw[g][0] = qv.x; qw[g][1] = qv.y; qw[g][2] = qv.z; qw[g][3] = qv.w;
     }
-    const int urow = 32 * (RB == 4 ? wave : rb0) + l32;
     float hsum[8];
-    v4i A[2][4], bl[2], bh[2], bb[2];
+    v4i A[2][RB], bl[2], bh[2], bb[2];
     auto read_a = [&](int j, int buf) __attribute__((always_inline)) {
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
-        const int row = 32 * (rb + rb0) + l32;
+        const int row = 32 * (rbw + rb) + l32;
         A[buf][rb] = *reinterpret_cast<const v4i*>(xt + row * 256 + 16 * ((2 * j + h) ^ (row & 15)));
       }
     };
-    auto xsum_half = [&](int j) __attribute__((always_inline)) {
-      const v4i xv = RB == 1 ? A[j & 1][0]
-                             : *reinterpret_cast<const v4i*>(xt + urow * 256 + 16 * ((2 * j + h) ^ (urow & 15)));
+    // half-sum of sub-block ju0 + jj (jj < JN) of this lane's row urow, half h
+    auto xsum_half = [&](int jj) __attribute__((always_inline)) {
+      const int j = ju0 + jj;
+      const v4i xv = QTR ? A[jj & 1][0]
+                         : *reinterpret_cast<const v4i*>(xt + urow * 256 + 16 * ((2 * j + h) ^ (urow & 15)));
       int sacc = __builtin_amdgcn_sdot4(xv[0], 0x01010101, 0, false);
       sacc = __builtin_amdgcn_sdot4(xv[1], 0x01010101, sacc, false);
       sacc = __builtin_amdgcn_sdot4(xv[2], 0x01010101, sacc, false);
       sacc = __builtin_amdgcn_sdot4(xv[3], 0x01010101, sacc, false);
-      hsum[j] = (float)sacc;
+      hsum[jj] = (float)sacc;
     };
     auto build = [&](int j, int buf) __attribute__((always_inline)) {
       const uint32_t scw = j < 4 ? sm.sc_lo : sm.sc_hi;
@@ -172,7 +196,7 @@ gemm_q5k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
         bb[buf][e] = (int)mul_bytes(hb, 2 * sc);
       }
     };
-    v16i_t tl[4], th[4];
+    v16i_t tl[RB], th[RB];
     read_a(0, 0);
     build(0, 0);
 #pragma unroll
@@ -191,31 +215,43 @@ gemm_q5k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
         }
         th[rb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[c][rb], bb[c], th[rb], 0, 0, 0);
       }
-      xsum_half(j);
+      if constexpr (JN == 8) xsum_half(j);
+      else if (j & 1) xsum_half(j >> 1);
       if (j < 7) build(j + 1, c ^ 1);
-      __builtin_amdgcn_sched_group_barrier(0x100, RB == 4 ? 5 : 1, 0);  // the LDS reads first
+      __builtin_amdgcn_sched_group_barrier(0x100, RB + (QTR ? 0 : 1), 0);  // the LDS reads first
 #pragma unroll
       for (int k = 0; k < 3 * RB; ++k) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
         __builtin_amdgcn_sched_group_barrier(0x002, RB == 4 ? 3 : 8, 0);  // VALU
       }
     }
-    v8h ua, ub;
+    v8h ub;
 #pragma unroll
-    for (int jj = 0; jj < 8; ++jj) {
-      ua[jj] = (_Float16)hsum[jj];
+    for (int jj = 0; jj < 8; ++jj)
       ub[jj] = (_Float16)(float)(((jj < 4 ? sm.mn_lo : sm.mn_hi) >> (8 * (jj & 3))) & 0xFF);
-    }
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
       for (int e = 0; e < 16; ++e) f[rb][e] += d * (float)(tl[rb][e] + 8 * th[rb][e]);
-    // the previous super-block's U (with RB = 4 its operands were published
+    // the previous super-block's U (in a full tile its operands were published
     // before the barrier this compute follows), then this one's goes pending;
     // both launches apply the same operations in the same order
     if (slot >= 0) u_step(slot ^ 1);
-    if constexpr (RB == 4) xh_l[slot & 1][wave][lane] = __builtin_bit_cast(uint4, ua);
-    else u_a = ua;
+    if constexpr (QTR) {
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) u_a[jj] = (_Float16)hsum[jj];
+    } else if constexpr (JN == 8) {
+      v8h ua;
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) ua[jj] = (_Float16)hsum[jj];
+      xh_l[slot & 1][urb][lane] = __builtin_bit_cast(uint4, ua);
+    } else {
+      typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+      v4h ua;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) ua[jj] = (_Float16)hsum[jj];
+      reinterpret_cast<uint2*>(&xh_l[slot & 1][urb][lane])[ju0 >> 2] = __builtin_bit_cast(uint2, ua);
+    }
     u_dmin = dmin;
     u_b = ub;
   };
@@ -236,23 +272,23 @@ gemm_q5k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
   }
   if (sb < nsb) {
     compute(xs0, ws0, sb == 0 ? -2 : 0);
-    if constexpr (RB == 4) __syncthreads();
+    if constexpr (!QTR) __syncthreads();
   }
   u_step((nsb - 1) & 1);  // the last super-block's U
 
-  const int n = n0 + 32 * wave + l32;
+  const int n = n0 + 32 * cg + l32;
   // the row scales first, unconditionally (clamped rows): one wait, not one per element
   float xsv[RB][16];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int e = 0; e < 16; ++e)
-      xsv[rb][e] = x_scale[min(m0 + 32 * (rb + rb0) + 8 * (e >> 2) + 4 * h + (e & 3), M - 1)];
+      xsv[rb][e] = x_scale[min(m0 + 32 * (rbw + rb) + 8 * (e >> 2) + 4 * h + (e & 3), M - 1)];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const int m = m0 + 32 * (rb + rb0) + 8 * (e >> 2) + 4 * h + (e & 3);
+      const int m = m0 + 32 * (rbw + rb) + 8 * (e >> 2) + 4 * h + (e & 3);
       if (m < M && n < N) st_out<OUT_DT>(out, (int64_t)m * N + n, f[rb][e] * xsv[rb][e]);
     }
 }
@@ -295,7 +331,10 @@ __device__ __forceinline__ uint4 lds16_off(const uint32_t* w, int b) {
 }
 
 constexpr int Q6P16 = 224;                     // LDS pitch of a staged Q6_K block (14 pieces)
-constexpr int T6W = KBN * Q6P16 / 4 + 16;        // weight-tile dwords (+ read slack)
+// weight-tile dwords: the KBN x 14 pieces rounded up to whole copies of NT
+// threads (+ read slack)
+template <int NT>
+constexpr int t6w() { return (KBN * 14 + NT - 1) / NT * NT * 4 + 16; }
 
 // 4 six-bit codes (bytes) -> the B_lo and B_hi bytes of (q - 32) * sc;
 // off2 = 128 - 32 sc in both 16-bit lanes
@@ -309,52 +348,59 @@ __device__ __forceinline__ void q6_split4(uint32_t q, v2s_t sc2, v2s_t off2, uin
   hi = __builtin_amdgcn_perm(u1, u0, 0x07050301u);                // high bytes
 }
 
-template <int OUT_DT, int RB>
-__global__ void __launch_bounds__(256, 1)
+// RB row blocks per wave, NW waves per workgroup, as the Q4_K tile kernel
+template <int OUT_DT, int RB, int NW = 4>
+__global__ void __launch_bounds__(64 * NW, 1)
 gemm_q6k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
                      const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K,
                      int nt_x, int xcd_m, int tile0) {
+  constexpr bool QTR = RB * NW < 16;
+  constexpr int NT = 64 * NW;
   __shared__ __attribute__((aligned(16))) int8_t xs0[KBM * 256];
   __shared__ __attribute__((aligned(16))) int8_t xs1[KBM * 256];
-  __shared__ __attribute__((aligned(16))) uint32_t ws0[T6W];
-  __shared__ __attribute__((aligned(16))) uint32_t ws1[T6W];
+  __shared__ __attribute__((aligned(16))) uint32_t ws0[t6w<NT>()];
+  __shared__ __attribute__((aligned(16))) uint32_t ws1[t6w<NT>()];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, h = lane >> 5;
-  // RB = 4: one 128 x 128 tile per workgroup (tiles tile0, tile0 + 1, ...);
-  // RB = 1: the quarter blockIdx.x & 3 (32 rows) of tile tile0 + blockIdx.x / 4,
+  // full tiles: one 128 x 128 tile per workgroup (tiles tile0, tile0 + 1, ...);
+  // quarters: the quarter blockIdx.x & 3 (32 rows) of tile tile0 + blockIdx.x / 4,
   // so a short last round of tiles spreads over 4x the workgroups
-  const int tile = tile0 + (RB == 4 ? (int)blockIdx.x : (int)(blockIdx.x >> 2));
+  const int tile = tile0 + (QTR ? (int)(blockIdx.x >> 2) : (int)blockIdx.x);
   int ct, rt;
   kq_tile_coords(tile, nt_x, xcd_m, ct, rt);
   const int n0 = ct * KBN, m0 = rt * KBM;
-  const int rb0 = RB == 4 ? 0 : (int)(blockIdx.x & 3);
+  const int rb0 = QTR ? (int)(blockIdx.x & 3) : 0;
+  const int cg = wave & 3;                                       // the wave's 32 output columns
+  const int rbw = QTR ? rb0 : (NW == 8 ? (wave >> 2) * RB : 0);  // its first row block
   const int nsb = K >> 8;
   const int64_t row_bytes = (int64_t)nsb * Q6K_BYTES;
   const int rmax = min(KBN, N - n0) - 1;
 
-  // piece P = 256 i + tid of the weight tile: row P / 14, piece P % 14 (fixed
-  // per thread); offsets are 32-bit from the workgroup's row-n0 base, which
-  // is 256-byte aligned (n0 of 128, row_bytes even): 128 rows of < 2^24 bytes
+  // piece P = NT i + tid of the weight tile: row P / 14, piece P % 14 (fixed
+  // per thread; pieces past the tile, from rounding up to whole copies,
+  // re-read the last row into the padding); offsets are 32-bit from the
+  // workgroup's row-n0 base, which is 256-byte aligned (n0 of 128, row_bytes
+  // even): 128 rows of < 2^24 bytes
   const uint8_t* wbase = w + (int64_t)n0 * row_bytes;
   auto load = [&](int sb, int8_t* xd, uint32_t* wd) __attribute__((always_inline)) {
-    copy_x_tile<RB == 4 ? KBM * 16 / 256 : 2>(x, xd, m0, M, K, sb, tid, wave, rb0);
+    copy_x_tile<NT, QTR>(x, xd, m0, M, K, sb, tid, wave, rb0);
     const uint32_t sboff = (uint32_t)sb * Q6K_BYTES;
 #pragma unroll
-    for (int i = 0; i < KBN * 14 / 256; ++i) {
-      const int P = i * 256 + tid, row = P / 14, c = P - 14 * (P / 14);
+    for (int i = 0; i < (KBN * 14 + NT - 1) / NT; ++i) {
+      const int P = i * NT + tid, Pc = min(P, KBN * 14 - 1), row = Pc / 14, c = Pc - 14 * (Pc / 14);
       const uint32_t off = (((uint32_t)min(row, rmax) * (uint32_t)row_bytes + sboff) & ~15u) + 16u * (uint32_t)c;
-      __builtin_amdgcn_global_load_lds((kq_gptr_t)(wbase + off), (kq_lptr_t)(wd + (i * 256 + wave * 64) * 4), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((kq_gptr_t)(wbase + off), (kq_lptr_t)(wd + (i * NT + wave * 64) * 4), 16, 0, 0);
     }
   };
 
-  float f[4][16];
+  float f[RB][16];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int e = 0; e < 16; ++e) f[rb][e] = 0.f;
 
-  const int r = 32 * wave + l32;  // this lane's weight row in the tile
+  const int r = 32 * cg + l32;  // this lane's weight row in the tile
   auto compute = [&](int sb, const int8_t* xt, const uint32_t* wt) __attribute__((always_inline)) {
     // the block's misalignment is that of its offset from the row-n0 base
     const uint32_t base = (uint32_t)min(r, rmax) * (uint32_t)row_bytes + (uint32_t)sb * Q6K_BYTES;
@@ -362,7 +408,7 @@ gemm_q6k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
     const uint4 scv = lds16_off(wt, blk + 192);
     const float d = h2f((uint16_t)(__builtin_amdgcn_alignbyte(wt[((blk + 208) >> 2) + 1], wt[(blk + 208) >> 2],
                                                              (uint32_t)((blk + 208) & 3)) & 0xFFFFu));
-    v16i_t tl[4], th[4];
+    v16i_t tl[RB], th[RB];
     // software pipeline over the 8 K steps: step s + 1's A reads and B
     // operands are formed while step s's 8 MFMAs run (double-buffered
     // registers; one scheduling region per step, MFMAs interleaved with VALU)
@@ -375,7 +421,7 @@ gemm_q6k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
       qv[hf][4] = qb.x; qv[hf][5] = qb.y; qv[hf][6] = qb.z; qv[hf][7] = qb.w;
       qv[hf][8] = qc.x; qv[hf][9] = qc.y; qv[hf][10] = qc.z; qv[hf][11] = qc.w;
     };
-    v4i bl[2], bh[2], A[2][4];
+    v4i bl[2], bh[2], A[2][RB];
     auto build = [&](int s, int buf) __attribute__((always_inline)) {
       const int hf = s >> 2, qd = s & 3, i = 2 * s + h;  // ql half, quadrant, sub-block (scale index)
       const uint32_t sw = (s >> 1) == 0 ? scv.x : (s >> 1) == 1 ? scv.y : (s >> 1) == 2 ? scv.z : scv.w;
@@ -394,7 +440,7 @@ gemm_q6k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
     auto read_a = [&](int s, int buf) __attribute__((always_inline)) {
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
-        const int row = 32 * (rb + rb0) + l32;
+        const int row = 32 * (rbw + rb) + l32;
         A[buf][rb] = *reinterpret_cast<const v4i*>(xt + row * 256 + 16 * ((2 * s + h) ^ (row & 15)));
       }
     };
@@ -458,12 +504,12 @@ gemm_q6k_tile_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_s
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int e = 0; e < 16; ++e)
-      xsv[rb][e] = x_scale[min(m0 + 32 * (rb + rb0) + 8 * (e >> 2) + 4 * h + (e & 3), M - 1)];
+      xsv[rb][e] = x_scale[min(m0 + 32 * (rbw + rb) + 8 * (e >> 2) + 4 * h + (e & 3), M - 1)];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const int m = m0 + 32 * (rb + rb0) + 8 * (e >> 2) + 4 * h + (e & 3);
+      const int m = m0 + 32 * (rbw + rb) + 8 * (e >> 2) + 4 * h + (e & 3);
       if (m < M && n < N) st_out<OUT_DT>(out, (int64_t)m * N + n, f[rb][e] * xsv[rb][e]);
     }
 }
@@ -1002,18 +1048,18 @@ void launch_kq_tile(const int8_t* x, const float* xs, const uint8_t* w, void* ou
   const int rem = T % P, nfull = (T >= P && rem > 0 && rem <= P / 2) ? T - rem : T;
   // XCD-aware tile order (kq_tile_coords) when the column tiles split evenly over the 8 XCDs
   const int xm = (SL8_KQ_XCD && ntx % 8 == 0) ? (M + KBM - 1) / KBM : 0;
-#define SL8_KQT(KERN, RB, G, T0)                                                                   \
+#define SL8_KQT(KERN, RB, NW, G, T0)                                                               \
   switch (odt) {                                                                                   \
-    case SL8_DTYPE_F16: KERN<SL8_DTYPE_F16, RB><<<G, 256, 0, st>>>(x, xs, w, out, M, N, K, ntx, xm, T0); break; \
-    case SL8_DTYPE_BF16: KERN<SL8_DTYPE_BF16, RB><<<G, 256, 0, st>>>(x, xs, w, out, M, N, K, ntx, xm, T0); break; \
-    default: KERN<SL8_DTYPE_F32, RB><<<G, 256, 0, st>>>(x, xs, w, out, M, N, K, ntx, xm, T0); break;        \
+    case SL8_DTYPE_F16: KERN<SL8_DTYPE_F16, RB, NW><<<G, 64 * NW, 0, st>>>(x, xs, w, out, M, N, K, ntx, xm, T0); break; \
+    case SL8_DTYPE_BF16: KERN<SL8_DTYPE_BF16, RB, NW><<<G, 64 * NW, 0, st>>>(x, xs, w, out, M, N, K, ntx, xm, T0); break; \
+    default: KERN<SL8_DTYPE_F32, RB, NW><<<G, 64 * NW, 0, st>>>(x, xs, w, out, M, N, K, ntx, xm, T0); break;        \
   }
   if (FMT == 5) {
-    SL8_KQT(gemm_q5k_tile_kernel, 4, nfull, 0)
-    if (nfull < T) SL8_KQT(gemm_q5k_tile_kernel, 1, 4 * (T - nfull), nfull)
+    if (SL8_KQ_NW8) { SL8_KQT(gemm_q5k_tile_kernel, 2, 8, nfull, 0) } else { SL8_KQT(gemm_q5k_tile_kernel, 4, 4, nfull, 0) }
+    if (nfull < T) SL8_KQT(gemm_q5k_tile_kernel, 1, 4, 4 * (T - nfull), nfull)
   } else {
-    SL8_KQT(gemm_q6k_tile_kernel, 4, nfull, 0)
-    if (nfull < T) SL8_KQT(gemm_q6k_tile_kernel, 1, 4 * (T - nfull), nfull)
+    if (SL8_Q6_NW8) { SL8_KQT(gemm_q6k_tile_kernel, 2, 8, nfull, 0) } else { SL8_KQT(gemm_q6k_tile_kernel, 4, 4, nfull, 0) }
+    if (nfull < T) SL8_KQT(gemm_q6k_tile_kernel, 1, 4, 4 * (T - nfull), nfull)
   }
 #undef SL8_KQT
 }
