@@ -68,6 +68,13 @@ constexpr int XS_MPAD = 16;  // xsum LDS row pitch (activation rows)
 // SL8_GEMV_XFIRST: at MT = 1 the activation copies are issued before the
 // weight loads. Config 4's shape, same box: M = 8 17.5 -> 17.0 us, M = 8 with
 // per-block x scales 17.9 -> 16.9 us, M = 16 33.5 -> 32.9 us, Q5_K M = 8 20.4 -> 20.0 us.
+// SL8_GEMV_MT2OCC: waves per SIMD of the 9 <= M <= 16 kernels (MT = 2). Config
+// 4's shape, M = 16, same box: 1 (the register budget then left them at 2-3)
+// 32.8 us, 3 31.1 us (per-block x scales 32.5 -> 30.7, Q5_K 38.5 -> 37.0), 4
+// 31.0 us but 44.6 with per-block scales (spills).
+#ifndef SL8_GEMV_MT2OCC
+#define SL8_GEMV_MT2OCC 3
+#endif
 #ifndef SL8_GEMV_FULLC
 #define SL8_GEMV_FULLC 1
 #endif
@@ -110,7 +117,7 @@ __device__ __forceinline__ uint32_t lane_pull(uint32_t v, int src_lane) {
 // M = 8 17.6 -> 18.1 us (its header registers spill at 5 waves per SIMD), so
 // the launcher uses it for M <= 4 and M > 8.
 template <int OUT_DT, int MT, int FMT = 4, int TPW = 1, bool XB = false, bool OPL = false>
-__global__ void __launch_bounds__(64 * GWAVES, TPW == 2 ? 3 : (MT == 1 ? (FMT == 4 && (!XB || SL8_GEMV_XBLDS) ? 5 : 4) : 1))
+__global__ void __launch_bounds__(64 * GWAVES, TPW == 2 ? 3 : (MT == 1 ? (FMT == 4 && (!XB || SL8_GEMV_XBLDS) ? 5 : 4) : SL8_GEMV_MT2OCC))
 gemv_q4k_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_scale,
                 const uint8_t* __restrict__ w, void* __restrict__ out, int M, int N, int K) {
   extern __shared__ __attribute__((aligned(16))) int8_t xl[];  // per wave: [M][GXPITCH]
