@@ -247,14 +247,14 @@ def test_accuracy_gate_and_rotate(device, monkeypatch):
 
 
 def test_config2_shape_against_oracle(device):
-    """BASELINE config 2 (B1 Hq32 Hkv8 S4096 D128 causal), checked on 8 of the 32
-    heads (every KV head once, both heads of KV head 3)."""
+    """BASELINE config 2 (B1 Hq32 Hkv8 S4096 D128 causal), every one of the 32
+    query heads against the oracle (~1 s of numpy per head)."""
     torch.manual_seed(2)
     q, k, v = _qkv(1, 32, 8, 4096, 4096, 128, device)
     q_i8, qs, k_i8, ks, _ = quant.quantize_qk(q, k)
     qs, ks = qs.squeeze(-1).contiguous(), ks.squeeze(-1).contiguous()
     out = _C.attn_int8_fwd(q_i8, qs, k_i8, ks, v, True)
-    for h in (0, 5, 10, 13, 14, 19, 26, 31):
+    for h in range(32):
         kvh = h // 4
         ref, _ = oa.attn_int8_fwd(_np(q_i8[:, h:h + 1]), _np(qs[:, h:h + 1]),
                                   _np(k_i8[:, kvh:kvh + 1]), _np(ks[:, kvh:kvh + 1]),
