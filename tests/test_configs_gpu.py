@@ -3,9 +3,9 @@
 * config 1: attn_int8_fwd B1 H8 S512 D64 causal, the whole output against the oracle.
 * config 5: attn_w8a8_fwd B2 Hq16 Hkv2 S8192 D256 causal, 1% of the head-dim
   channels of Q and K scaled by 20, accuracy gate bypassed. The full kernel
-  runs; query blocks of several heads (first, middle and last blocks, both
-  batches and both KV heads) are compared with the oracle against all their
-  keys. At this shape the outlier rows move their softmax reference point
+  runs; a 64-row query block of every query head of both batches (positions
+  spread over the sequence, plus the first and the last block) is compared
+  with the oracle against all its keys. At this shape the outlier rows move their softmax reference point
   several times (the lazy rescale), which only long rows with large outliers
   exercise. Reference test: tests/test_attn_fwd_w8a8_outliers.py.
 """
@@ -57,8 +57,11 @@ def _config5_inputs(device):
     return q, k, v
 
 
-# (batch, query head, first query row) of the 64-row blocks compared
-C5_BLOCKS = [(0, 0, 0), (0, 3, 4096), (0, 9, 8128), (1, 8, 2048), (1, 15, 6080), (1, 1, 8128)]
+# (batch, query head, first query row) of the 64-row blocks compared: every
+# query head of both batches, at query positions spread over the sequence
+# (first, last and interior blocks)
+C5_BLOCKS = [(b, h, ((7 * h + 3 * b) % 128) * 64) for b in range(2) for h in range(16)] + \
+    [(0, 0, 0), (1, 15, 8128)]
 
 
 @pytest.mark.parametrize("qk_quant", ["per_row", "per_wave"])
