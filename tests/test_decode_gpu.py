@@ -109,8 +109,9 @@ def test_config3_shape_against_oracle(device, ks16):
     """BASELINE config 3 (B16 Hq32 Hkv8 N32768 D128, 16 splits) as the config
     states it: the K cache is N(0,1) fp16 K quantised per token (codes and scales
     checked bit-exact against the oracle on the compared sequences), its scales
-    kept as fp32 (the reference contract) or fp16 (the config text); checked on
-    2 sequences."""
+    kept as fp32 (the reference contract) or fp16 (the config text). The output of
+    all 16 sequences (every query head) is checked against the oracle, the K
+    codes of 4 sequences bit for bit."""
     torch.manual_seed(3)
     B, Hq, Hkv, N, D = 16, 32, 8, 32768, 128
     q = torch.randn(B, Hq, 1, D, device=device, dtype=torch.float16)
@@ -118,7 +119,7 @@ def test_config3_shape_against_oracle(device, ks16):
     v = torch.randn(B, Hkv, N, D, device=device, dtype=torch.float16)
     k_i8, ks = _C.quantize_i8_rowwise(k.reshape(-1, D))
     k_i8, ks = k_i8.reshape(B, Hkv, N, D), ks.reshape(B, Hkv, N)
-    for b in (0, 15):
+    for b in (0, 5, 10, 15):
         rq, rs = oqn.quantize_rows(_np(k[b].float()).reshape(-1, D))
         np.testing.assert_array_equal(_np(k_i8[b]).reshape(-1, D), rq)
         np.testing.assert_array_equal(_np(ks[b]).reshape(-1), rs)
@@ -129,7 +130,7 @@ def test_config3_shape_against_oracle(device, ks16):
     qs = (qs * 0.1275).reshape(B, Hq, 1).contiguous()
     q_i8 = q_i8.reshape(B, Hq, 1, D)
     out = _C.attn_int8_decode(q_i8, qs, k_i8, ks, v, 16)
-    for b in (0, 15):
+    for b in range(B):
         ref = oa.attn_int8_decode(_np(q_i8[b:b + 1])[:, :, 0], _np(qs[b:b + 1])[:, :, 0],
                                   _np(k_i8[b:b + 1]), _np(ks[b:b + 1].float()),
                                   _np(v[b:b + 1].float()), 16)
