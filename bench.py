@@ -266,11 +266,12 @@ def bench_prologue(iters=20):
     return fms, sms, nbytes
 
 
-def bench_w8a8(iters=5, per_wave=False):
+def bench_w8a8(iters=5, per_wave=False, exact_pv=False):
     """Full-W8A8 prefill at BASELINE config 5: Q/K/V [2, 16|2, 8192, 256], causal,
     1% of Q/K channels (3 of 256, fixed) scaled by 20, V per-channel int8.
     per_wave: Q/K quantised per wavefront tile (32 queries / 64 keys), the config
-    text, instead of the reference's per row (the kernel is the same)."""
+    text, instead of the reference's per row (the kernel is the same).
+    exact_pv: the reference's per-warp arithmetic exactly (int32 P.V per half)."""
     from superl8_amd import _C, quant
 
     dev = "cuda"
@@ -288,7 +289,7 @@ def bench_w8a8(iters=5, per_wave=False):
     v_i8, vs = _C.quantize_v_perchannel(v)
     vs = vs.reshape(B, Hkv, D).contiguous()
     del q, k, v
-    fn = lambda: _C.attn_w8a8_fwd(q_i8, qs, k_i8, ks, v_i8, vs, True)  # noqa: E731
+    fn = lambda: _C.attn_w8a8_fwd(q_i8, qs, k_i8, ks, v_i8, vs, True, exact_pv=exact_pv)  # noqa: E731
     spin_up(fn, 0.2)
     ms = _events_time(fn, iters, torch.cuda.current_stream())
     ops = 4 * B * Hq * S * S * D // 2
@@ -580,6 +581,12 @@ def main():
         sec["attn_w8a8_fwd_cfg5_per_wave_qk"] = {"us": round(wms * 1e3, 1), "TOPS": round(wt, 1),
                                                  "frac_int8_peak": round(wt / PEAK_INT8_TOPS, 4),
                                                  "ops": wops}
+        wms, wops = bench_w8a8(exact_pv=True)
+        wt = wops / (wms * 1e-3) / 1e12
+        sec["attn_w8a8_fwd_cfg5_exact_pv"] = {"us": round(wms * 1e3, 1), "TOPS": round(wt, 1),
+                                              "frac_int8_peak": round(wt / PEAK_INT8_TOPS, 4),
+                                              "ops": wops,
+                                              "mode": "per-warp P, exact int32 P.V per 32-key half"}
         sec["hbm_copy_256MiB_GBps"] = round(bench_copy(), 1)
         out["secondary"] = sec
     if not args.no_cpu:

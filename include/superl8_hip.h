@@ -178,6 +178,13 @@ int sl8_attn_int8_qk_scores(const int8_t* q, const int8_t* k, int32_t* scores,
  *   v int8 [B,Hkv,N,D], v_scale fp32 [B,Hkv,D], causal_diag: query i sees
  *   keys <= i + causal_diag when causal. D in {32, 64, 128, 256} (reference
  *   attn_w8a8_fwd.cu:113; D = 32 runs zero-padded to 64 in the workspace).
+ *   per_warp_quant: 0 = one P scale per 64-key tile (the reference's
+ *   per_warp_quant=False); 1 = one P scale per 32-key half (the reference's
+ *   default), P fed to the bf16 MFMA as code * 2^(max_half - m) / 127 (the
+ *   rounding of that factor to bf16 is this build's only deviation); 2 = the
+ *   same quantisation with the reference's exact arithmetic (int32 P.V per
+ *   half, scaled in fp32), about twice the time of 1. No reference counterpart
+ *   for 2 (the reference's per-warp path computes it this way).
  * ---------------------------------------------------------------------- */
 size_t sl8_attn_w8a8_fwd_workspace(int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N,
                                    int64_t D);

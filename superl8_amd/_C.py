@@ -296,8 +296,12 @@ def attn_int8_qk_scores(q, k, causal=False, fill=0):
 # W8A8 prefill (reference csrc/kernel/attn_w8a8_fwd.cu:76-165)
 # ---------------------------------------------------------------------------
 def attn_w8a8_fwd(q, q_scale, k, k_scale, v, v_scale, causal=False, causal_diag=0,
-                  per_warp_quant=True):
-    """int8 QK^T + int8 PV; v int8 [B,Hkv,N,D], v_scale fp32 [B,Hkv,D] -> fp16 out."""
+                  per_warp_quant=True, *, exact_pv=False):
+    """int8 QK^T + int8 PV; v int8 [B,Hkv,N,D], v_scale fp32 [B,Hkv,D] -> fp16 out.
+
+    exact_pv (keyword of this build only; per_warp_quant=True): the reference's
+    per-warp arithmetic exactly -- an int32 P.V per 32-key half scaled in fp32 --
+    instead of the default bf16-P MFMA pipeline, at about twice the time."""
     _on_gpu(v_scale)
     B, H, Hkv, M, N, D = _fwd_checks(q, q_scale, k, k_scale, v)
     _check(v.dtype == torch.int8, "q/k/v must be int8")
@@ -314,7 +318,8 @@ def attn_w8a8_fwd(q, q_scale, k, k_scale, v, v_scale, causal=False, causal_diag=
     with torch.cuda.device(q.device):
         call("sl8_attn_w8a8_fwd", q.data_ptr(), q_scale.data_ptr(), k.data_ptr(),
              k_scale.data_ptr(), v.data_ptr(), v_scale.data_ptr(), out.data_ptr(), B, H, Hkv, M,
-             N, D, int(bool(causal)), int(causal_diag), int(bool(per_warp_quant)),
+             N, D, int(bool(causal)), int(causal_diag),
+             (2 if exact_pv else 1) if per_warp_quant else 0,
              ws.data_ptr(), ws_bytes, stream_of(q))
     return out
 

@@ -1,11 +1,14 @@
 // Full-W8A8 prefill attention for gfx950.
 //
-// per_warp_quant (the reference default) runs on the prefill pipeline of
+// per_warp_quant = 1 (the reference default) runs on the prefill pipeline of
 // attn_fwd.hip (attn_fwd_wide_kernel, W8 = true): int8 Q.K^T on the int8
 // MFMA, P codes re-quantised per 32-key half and fed to the bf16 MFMA as
 // code * per-row factor against int8 V held exactly in bf16 (w8a8_wide_launch).
-// This file holds the per-tile variant (per_warp_quant = false): int8 Q.K^T
-// and int8 P.V, both on the int8 MFMA (v_mfma_i32_32x32x32_i8).
+// This file holds the kernel with int8 Q.K^T and int8 P.V, both on the int8
+// MFMA (v_mfma_i32_32x32x32_i8): per_warp_quant = 0 (one P scale per 64-key
+// tile) and per_warp_quant = 2, the reference's per-warp arithmetic exactly
+// (one P scale per 32-key half, an exact int32 P.V per half scaled in fp32,
+// the running max updated every tile) at about twice the time of mode 1.
 //
 // Semantics follow the reference (csrc/include/attn_w8a8_fwd.cuh:30-235):
 //   logits and the online softmax as attn_int8_fwd, over 64-key tiles, with
@@ -391,7 +394,9 @@ extern "C" int sl8_attn_w8a8_fwd(const int8_t* q, const float* q_scale, const in
     if (rc) return rc;
     D = 64;
   }
-  if (per_warp_quant)
+  SL8_CHECK_ARG(per_warp_quant >= 0 && per_warp_quant <= 2,
+                "fni8: per_warp_quant must be 0 (per tile), 1 (per warp) or 2 (per warp, exact int32 PV)");
+  if (per_warp_quant == 1)
     return w8a8_wide_launch(q, q_scale, k, k_scale, v, v_scale, out, B, Hq, Hkv, M, N, D, dout,
                             causal != 0, causal_diag, workspace, st);
   const int64_t Npad = npad8(N);
@@ -412,7 +417,7 @@ extern "C" int sl8_attn_w8a8_fwd(const int8_t* q, const float* q_scale, const in
   a.M = (int)M; a.N = (int)N; a.Npad = (int)Npad; a.Hq = (int)Hq; a.Hkv = (int)Hkv;
   a.nqb = (int)((M + WBM - 1) / WBM);
   a.causal_diag = (int)causal_diag;
-  const bool c = causal != 0, pw = per_warp_quant != 0;
+  const bool c = causal != 0, pw = per_warp_quant == 2;
   const int nslot = c ? (a.nqb + 1) / 2 : a.nqb;
   a.xcd_map = xcd_mode(B * Hkv, Hq / Hkv, nslot);
   const int grid = (int)(B * Hq * nslot);

@@ -42,16 +42,18 @@ CASES = [  # B, Hq, Hkv, M, N, D, causal
 
 
 @pytest.mark.parametrize("case", CASES)
-@pytest.mark.parametrize("per_warp", [True, False])
-def test_kernel_matches_oracle(device, case, per_warp):
+@pytest.mark.parametrize("mode", ["per_warp", "per_tile", "per_warp_exact"])
+def test_kernel_matches_oracle(device, case, mode):
     B, Hq, Hkv, M, N, D, causal = case
+    per_warp = mode != "per_tile"
     q, k, v = _qkv(B, Hq, Hkv, M, N, D, device)
     q_i8, qs, k_i8, ks, _ = quant.quantize_qk(q, k)
     qs, ks = qs.squeeze(-1).contiguous(), ks.squeeze(-1).contiguous()
     v_i8, vs = _C.quantize_v_perchannel(v)
     vs = vs.squeeze(-2).contiguous()
     diag = N - M if causal else 0
-    out = _C.attn_w8a8_fwd(q_i8, qs, k_i8, ks, v_i8, vs, causal, diag, per_warp)
+    out = _C.attn_w8a8_fwd(q_i8, qs, k_i8, ks, v_i8, vs, causal, diag, per_warp,
+                           exact_pv=mode == "per_warp_exact")
     assert out.dtype == torch.float16 and out.shape == (B, Hq, M, D)
     ref = oa.attn_w8a8_fwd(_np(q_i8), _np(qs), _np(k_i8), _np(ks), _np(v_i8), _np(vs), causal, diag,
                            per_warp)
@@ -130,6 +132,19 @@ def test_config5_outliers_small(device):
 
 
 def test_rejects(device):
+    from superl8_amd import _lib
+
+    # per_warp_quant is 0, 1 or 2 at the C ABI
+    q, k, v = _qkv(1, 2, 2, 64, 64, 64, device)
+    q_i8, qs, k_i8, ks, _ = quant.quantize_qk(q, k)
+    v_i8, vs = _C.quantize_v_perchannel(v)
+    out = torch.empty_like(q)
+    nbytes = _lib.load().sl8_attn_w8a8_fwd_workspace(1, 2, 2, 64, 64, 64)
+    ws = torch.empty((max(nbytes, 1),), device=device, dtype=torch.uint8)
+    with pytest.raises(RuntimeError, match="per_warp_quant"):
+        _lib.call("sl8_attn_w8a8_fwd", q_i8.data_ptr(), qs.data_ptr(), k_i8.data_ptr(),
+                  ks.data_ptr(), v_i8.data_ptr(), vs.data_ptr(), out.data_ptr(), 1, 2, 2, 64, 64, 64,
+                  0, 0, 3, ws.data_ptr(), nbytes, torch.cuda.current_stream().cuda_stream)
     q, k, v = _qkv(1, 2, 2, 64, 64, 96, device)
     with pytest.raises(RuntimeError):
         sl8.attn_int8_fwd(q, k, v, int8_pv=True)
@@ -236,3 +251,23 @@ def test_per_warp_bf16_rounding_is_the_modelled_one(device):
     print(f"correlated case: |kernel-model| {e_model:.2e}  |kernel-oracle| {e_ref:.2e} (relative)")
     assert e_ref > 1e-3
     assert e_model < 0.25 * e_ref
+
+
+def test_exact_per_warp_follows_the_reference_arithmetic(device):
+    """The correlated-rounding case again: per_warp_quant with exact_pv runs the
+    reference's arithmetic (int32 P.V per 32-key half, fp32 scale), so it stays
+    far closer to the exact-int32 oracle than the default bf16-operand mode,
+    whose rounding moves the output by > 1e-3 relative there."""
+    from tests.test_oracle import _w8_bf16_case
+
+    q, qs, k, ks, v, vs = _w8_bf16_case()
+    dv = [torch.from_numpy(t).to(device) for t in (q, qs, k, ks, v, vs)]
+    ref = oa.attn_w8a8_fwd(q, qs, k, ks, v, vs, False, 0, True)
+    scale = np.abs(ref).max()
+    fast = _np(_C.attn_w8a8_fwd(*dv, False, 0, True).float())
+    exact = _np(_C.attn_w8a8_fwd(*dv, False, 0, True, exact_pv=True).float())
+    e_fast, e_exact = np.abs(fast - ref).max() / scale, np.abs(exact - ref).max() / scale
+    print(f"correlated case: |bf16 mode - oracle| {e_fast:.2e}  |exact mode - oracle| {e_exact:.2e}")
+    assert e_fast > 1e-3
+    # within the fp16 output's rounding (half an ulp at the output scale: 2^-11)
+    assert e_exact < 2.0 ** -11 and e_exact < 0.25 * e_fast
