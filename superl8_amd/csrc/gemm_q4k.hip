@@ -573,8 +573,10 @@ gemv_q4k_small_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_
 // ---------------------------------------------------------------------------
 // Tiled Q4_K GEMM for M > 16 (prefill; reference csrc/include/gemm_q4k_dp4a.cuh:
 // 60-199, csrc/kernel/gemm_dp4a.cu:146-193): a 128 x 128 output tile per
-// workgroup, each of the 4 waves owning 32 output columns x all 128 rows (4
-// blocks of 32 x 32, so each B operand is built once). Per super-block the
+// workgroup of 8 waves, two per SIMD, each owning 32 output columns x 64 rows
+// (2 blocks of 32 x 32; each B operand is built by the two waves of its
+// columns: with 4 waves over all 128 rows, one per SIMD, a single wave's VALU
+// issue rate bounded the kernel). Per super-block the
 // x tile (128 x 256 int8) and the 128 weight super-blocks (144 B each) are
 // copied global -> LDS one super-block ahead (double-buffered). The products
 // stay exact integers on v_mfma_i32_32x32x32_i8, one MFMA per 32-element
@@ -587,10 +589,12 @@ gemv_q4k_small_kernel(const int8_t* __restrict__ x, const float* __restrict__ x_
 //   U = sum_j m_j * sum(x_j) is one v_mfma_f32_32x32x16_f16 per row block and
 // super-block on the x half-sums and the mins (both exact in fp16; U is an
 // exact fp32 integer), applied as f -= dmin * U one super-block later (the
-// half-sums of a row block are formed by one wave and shared through LDS).
+// half-sums of the tile's rows are formed once, spread over the waves, and
+// shared through LDS).
 // x chunks are XOR-swizzled in LDS by row (rows are 256 B = one bank line);
 // weight rows are 144 B apart, which already spreads 16 rows over all banks.
 // ---------------------------------------------------------------------------
+// SL8_KQ_NW8=0: the full tiles on 4 waves (one per SIMD, RB = 4)
 #ifndef SL8_KQ_NW8
 #define SL8_KQ_NW8 1
 #endif
