@@ -10,10 +10,13 @@
 //         sc_i signed int8.
 // x is the per-row int8 activation with its fp32 scale.
 //
-// Tile GEMM (M > 16; the decode GEMV below serves M <= 16): a 128 x 128 output tile per workgroup,
-// each of the 4 waves owning 32 output columns x all 128 rows (4 blocks of
-// 32 x 32, so each B operand is built once), the x tile and the 128 weight
-// super-blocks copied global -> LDS one super-block ahead (double-buffered).
+// Tile GEMM (M > 16; the decode GEMV below serves M <= 16): a 128 x 128 output
+// tile per workgroup, the x tile and the 128 weight super-blocks copied
+// global -> LDS one super-block ahead (double-buffered). Q5_K runs 8 waves,
+// two per SIMD, each owning 32 output columns x 64 rows (each B operand built
+// by the two waves of its columns); Q6_K, whose operand build costs the most,
+// runs 4 waves, one per SIMD, each over 32 columns x all 128 rows (each B
+// operand built once).
 // The integer dot products stay exact:
 //   Q5_K on v_mfma_i32_32x32x32_i8, one K = 32 step per sub-block: with
 //     q = n + 16 b (n the low nibble, b the 5th bit), q * sc_j =
