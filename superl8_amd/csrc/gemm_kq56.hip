@@ -1022,13 +1022,22 @@ void launch_gemv_q6k_mfma(const int8_t* x, const float* xs, const uint8_t* w, vo
 #undef SL8_Q6M
 }
 
+// smallest M on the int8 MFMA GEMVs (below: the VALU kernels). Config 4's
+// shape, same box: M = 2 Q5_K 19.7 -> 17.0 us, Q6_K 29.4 -> 22.5 us; at M = 1
+// the VALU kernels stay ahead (Q6_K 21.2 against 21.7 us)
+#ifndef SL8_Q5_MFMA_MIN
+#define SL8_Q5_MFMA_MIN 2
+#endif
+#ifndef SL8_Q6_MFMA_MIN
+#define SL8_Q6_MFMA_MIN 2
+#endif
 #ifndef SL8_Q5_SMALL
 #define SL8_Q5_SMALL 1
 #endif
 template <int FMT>
 void launch_gemv_kq(const int8_t* x, const float* xs, const uint8_t* w, void* out, int odt,
                     int M, int N, int K, hipStream_t st) {
-  if (M >= 3) {  // the int8 MFMA GEMVs (Q5_K: the Q4_K kernel of gemm_q4k.hip)
+  if (M >= (FMT == 6 ? SL8_Q6_MFMA_MIN : SL8_Q5_MFMA_MIN)) {  // the int8 MFMA GEMVs (Q5_K: the Q4_K kernel of gemm_q4k.hip)
     if (FMT == 5) launch_gemv_q5k_mfma(x, xs, w, out, odt, M, N, K, st);
     else launch_gemv_q6k_mfma(x, xs, w, out, odt, M, N, K, st);
     return;
