@@ -188,7 +188,8 @@ struct QOp {
 // ---------------------------------------------------------------------------
 // Production kernel. A wave owns NG x 32 queries (NG = 1: one MFMA column
 // block) for the whole key loop; WV waves per workgroup (8 for D = 128, 4 for
-// D = 64; two waves per SIMD) share each 64-key K / k_scale / V^T tile, copied
+// D = 64, halved down to 2 while the grid is smaller than the CU count; two
+// waves per SIMD) share each 64-key K / k_scale / V^T tile, copied
 // global -> LDS one tile ahead, so a larger workgroup means fewer copies per
 // query. Each tile is processed as two 32-key half-steps; half-step h issues
 // QK of half h and PV of half h-2 on the matrix cores while the VALU does the
@@ -1125,21 +1126,51 @@ constexpr int wide_waves(int64_t D) { return D == 128 ? SL8_FWD_WV128 : (D == 64
 constexpr int wide_ng(int64_t D) { return D == 256 ? SL8_FWD_NG256 : WIDE_NG; }
 constexpr int wide_bm(int64_t D) { return wide_waves(D) * 32 * wide_ng(D); }
 
-template <int D, bool CAUSAL, int VDT, bool LSE, bool W8 = false>
+template <int D, bool CAUSAL, int VDT, bool LSE, bool W8 = false, int WV = wide_waves(D)>
 void launch_wide(const FwdArgs& a, int grid, hipStream_t st) {
-  constexpr int WV = wide_waves(D);
   attn_fwd_wide_kernel<D, CAUSAL, VDT, LSE, wide_ng(D), WV, W8><<<grid, WV * 64, 0, st>>>(a);
 }
 
-template <int D, int VDT>
-void dispatch_wide(const FwdArgs& a, int grid, bool causal, bool lse, hipStream_t st) {
-  if (causal) {
-    if (lse) launch_wide<D, true, VDT, true>(a, grid, st);
-    else launch_wide<D, true, VDT, false>(a, grid, st);
-  } else {
-    if (lse) launch_wide<D, false, VDT, true>(a, grid, st);
-    else launch_wide<D, false, VDT, false>(a, grid, st);
+// Small grids (short sequences, few heads): fewer waves per workgroup, i.e.
+// fewer queries per workgroup and more workgroups, until the grid covers the
+// CUs (the waves per SIMD stay 2: see the launch bounds). D = 128: 8, 4 or 2
+// waves; D = 64: 4 or 2; D = 256 keeps 4.
+#ifndef SL8_FWD_SMALLGRID
+#define SL8_FWD_SMALLGRID 1
+#endif
+int wide_waves_for(int64_t DP, int64_t B, int64_t Hq, int64_t M, bool causal) {
+  int wv = wide_waves(DP);
+  if (!SL8_FWD_SMALLGRID || (DP != 128 && DP != 64) || wide_ng(DP) != 1) return wv;
+  const int64_t cus = cu_count();
+  while (wv > 2) {
+    const int64_t bm = (int64_t)wv * 32, nqb = (M + bm - 1) / bm;
+    const int64_t grid = B * Hq * (causal ? (nqb + 1) / 2 : nqb);
+    if (grid >= cus) break;
+    wv /= 2;
   }
+  return wv;
+}
+
+template <int D, int VDT, int WV>
+void dispatch_wide_wv(const FwdArgs& a, int grid, bool causal, bool lse, hipStream_t st) {
+  if (causal) {
+    if (lse) launch_wide<D, true, VDT, true, false, WV>(a, grid, st);
+    else launch_wide<D, true, VDT, false, false, WV>(a, grid, st);
+  } else {
+    if (lse) launch_wide<D, false, VDT, true, false, WV>(a, grid, st);
+    else launch_wide<D, false, VDT, false, false, WV>(a, grid, st);
+  }
+}
+
+template <int D, int VDT>
+void dispatch_wide(const FwdArgs& a, int grid, bool causal, bool lse, int wv, hipStream_t st) {
+  if constexpr (D == 128) {
+    if (wv == 2) return dispatch_wide_wv<D, VDT, 2>(a, grid, causal, lse, st);
+    if (wv == 4) return dispatch_wide_wv<D, VDT, 4>(a, grid, causal, lse, st);
+  } else if constexpr (D == 64) {
+    if (wv == 2) return dispatch_wide_wv<D, VDT, 2>(a, grid, causal, lse, st);
+  }
+  dispatch_wide_wv<D, VDT, wide_waves(D)>(a, grid, causal, lse, st);
 }
 
 int64_t npad_of(int64_t N) { return (N + BN - 1) / BN * BN; }
@@ -1157,17 +1188,18 @@ int check_fwd_shape(int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N, in
 }
 
 // launch geometry of the production kernel for (padded) head dim DP: query
-// blocks of wide_bm(DP) rows; causal launches pair block qb with nqb-1-qb, so
+// blocks of wv x 32 x wide_ng(DP) rows (wv = 0: wide_waves(DP)); causal launches pair block qb with nqb-1-qb, so
 // the grid holds (nqb + 1) / 2 slots per head
 FwdArgs make_args(int64_t B, int64_t Hq, int64_t Hkv, int64_t M, int64_t N, int64_t DP,
-                  bool causal, int& grid) {
+                  bool causal, int& grid, int wv = 0) {
+  const int bm = (wv > 0 ? wv : wide_waves(DP)) * 32 * wide_ng(DP);
   FwdArgs a{};
   a.M = (int)M;
   a.N = (int)N;
   a.Npad = (int)npad_of(N);
   a.Hq = (int)Hq;
   a.Hkv = (int)Hkv;
-  a.nqb = (int)((M + wide_bm(DP) - 1) / wide_bm(DP));
+  a.nqb = (int)((M + bm - 1) / bm);
   a.window_left = -1;
   a.diag = (int)(N - M);
   a.dout = 0;  // set by the callers
@@ -1374,7 +1406,8 @@ int attn_int8_fwd_impl(const int8_t* q, const float* q_scale, const int8_t* k,
   }
   const bool c = causal != 0, want_lse = lse != nullptr;
   int grid;
-  FwdArgs a = make_args(B, Hq, Hkv, M, N, DP, c, grid);
+  const int wv = wide_waves_for(DP, B, Hq, M, c);
+  FwdArgs a = make_args(B, Hq, Hkv, M, N, DP, c, grid, wv);
   a.q = q; a.qs = q_scale; a.k = k; a.ks = k_scale;
   a.vt = static_cast<const uint16_t*>(v);  // V [B*Hkv][N][DP], read in place
   a.out = out; a.lse = lse; a.window_left = (int)window_left;
@@ -1382,14 +1415,14 @@ int attn_int8_fwd_impl(const int8_t* q, const float* q_scale, const int8_t* k,
   a.skip = skip;
   const bool f16 = v_dtype == SL8_DTYPE_F16;
   if (DP == 64) {
-    if (f16) dispatch_wide<64, SL8_DTYPE_F16>(a, grid, c, want_lse, st);
-    else dispatch_wide<64, SL8_DTYPE_BF16>(a, grid, c, want_lse, st);
+    if (f16) dispatch_wide<64, SL8_DTYPE_F16>(a, grid, c, want_lse, wv, st);
+    else dispatch_wide<64, SL8_DTYPE_BF16>(a, grid, c, want_lse, wv, st);
   } else if (DP == 128) {
-    if (f16) dispatch_wide<128, SL8_DTYPE_F16>(a, grid, c, want_lse, st);
-    else dispatch_wide<128, SL8_DTYPE_BF16>(a, grid, c, want_lse, st);
+    if (f16) dispatch_wide<128, SL8_DTYPE_F16>(a, grid, c, want_lse, wv, st);
+    else dispatch_wide<128, SL8_DTYPE_BF16>(a, grid, c, want_lse, wv, st);
   } else {
-    if (f16) dispatch_wide<256, SL8_DTYPE_F16>(a, grid, c, want_lse, st);
-    else dispatch_wide<256, SL8_DTYPE_BF16>(a, grid, c, want_lse, st);
+    if (f16) dispatch_wide<256, SL8_DTYPE_F16>(a, grid, c, want_lse, wv, st);
+    else dispatch_wide<256, SL8_DTYPE_BF16>(a, grid, c, want_lse, wv, st);
   }
   SL8_CHECK_LAUNCH("attn_int8_fwd");
   return SL8_OK;

@@ -105,4 +105,14 @@ __device__ __forceinline__ void buf4_to_lds(brsrc_t r, void* lds_wave_base, uint
                                            voff, soff, 0, 0);
 }
 
+// CUs of the current device (cached per device)
+inline int cu_count() {
+  static int cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev] && hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus[dev] = 256;
+  return cus[dev] > 0 ? cus[dev] : 256;
+}
+
 }  // namespace sl8

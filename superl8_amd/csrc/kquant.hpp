@@ -61,14 +61,4 @@ void launch_gemv_q5k_mfma(const int8_t* x, const float* xs, const uint8_t* w, vo
 typedef __attribute__((address_space(1))) const void* kq_gptr_t;
 typedef __attribute__((address_space(3))) void* kq_lptr_t;
 
-// CUs of the current device (cached per device)
-inline int cu_count() {
-  static int cus[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cus[dev] && hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    cus[dev] = 256;
-  return cus[dev] > 0 ? cus[dev] : 256;
-}
-
 }  // namespace sl8

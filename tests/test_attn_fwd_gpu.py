@@ -307,3 +307,49 @@ def test_seeded_accumulator_extreme_codes(device, qv, kv):
         assert_close_abs(out, ref, atol=1e-2, what=f"codes {qv}/{kv} causal={causal}")
         s = _C.attn_int8_qk_scores(q, k)
         _check_scores(s, q, k, False)
+
+
+def _waves_for(B, Hq, M, D, causal, cus=256):
+    """The workgroup size the launcher picks (waves of 32 queries): the default
+    (8 for D = 128, 4 for D = 64) halved while the grid is below the CU count."""
+    wv = 8 if D == 128 else 4
+    while wv > 2:
+        nqb = -(-M // (32 * wv))
+        if B * Hq * ((nqb + 1) // 2 if causal else nqb) >= cus:
+            break
+        wv //= 2
+    return wv
+
+
+# small grids run 2- or 4-wave workgroups: each wave count and dtype against the oracle
+WAVE_CASES = [
+    (1, 32, 8, 1024, 1024, 128, True),   # 2 waves
+    (1, 32, 8, 2048, 2048, 128, True),   # 4 waves
+    (1, 32, 8, 1024, 1024, 128, False),  # 4 waves
+    (1, 32, 8, 1024, 1024, 64, True),    # 2 waves
+    (2, 8, 8, 1000, 1000, 128, True),    # 2 waves, ragged last block
+    (1, 32, 8, 300, 1000, 128, True),    # 2 waves, bottom-right causal offset
+]
+
+
+@pytest.mark.parametrize("case", WAVE_CASES, ids=lambda c: "B%dH%d_%dS%dx%dD%d%s" % (*c[:6], "c" if c[6] else ""))
+def test_small_grid_wave_counts(device, case):
+    B, Hq, Hkv, M, N, D, causal = case
+    torch.manual_seed(M + D)
+    if torch.cuda.get_device_properties(device).multi_processor_count == 256:
+        assert _waves_for(B, Hq, M, D, causal) in (2, 4)
+    q, k, v = _qkv(B, Hq, Hkv, M, N, D, device)
+    q_i8, qs, k_i8, ks, _ = quant.quantize_qk(q, k)
+    qs, ks = qs.squeeze(-1).contiguous(), ks.squeeze(-1).contiguous()
+    out = _C.attn_int8_fwd(q_i8, qs, k_i8, ks, v, causal)
+    assert_finite(out)
+    gsz = Hq // Hkv
+    for b, h in [(0, 0), (B - 1, Hq - 1), (B - 1, Hq // 2 + 1)]:
+        kvh = h // gsz
+        ref, _ = oa.attn_int8_fwd(_np(q_i8[b:b + 1, h:h + 1]), _np(qs[b:b + 1, h:h + 1]),
+                                  _np(k_i8[b:b + 1, kvh:kvh + 1]), _np(ks[b:b + 1, kvh:kvh + 1]),
+                                  _np(v[b:b + 1, kvh:kvh + 1].float()), causal)
+        got = out[b:b + 1, h:h + 1]
+        assert_close_abs(got, ref, atol=1e-2, what=f"{case} head {(b, h)}")
+        assert_int8_quality(got, ref, min_cos=0.9999, max_rel_l1=3e-3, min_sqnr_db=40,
+                            what=f"{case} head {(b, h)}")
