@@ -32,6 +32,13 @@ __device__ __forceinline__ void pin_vgpr(const T& x) {
   asm volatile("" ::"v"(x));
 }
 
+// max(x, x of lane ^ 32) in every lane of the wave: one v_permlane32_swap
+// (lanes 0-31 receive lanes 32-63 and back; a VALU op, no LDS round trip)
+__device__ __forceinline__ float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // blockIdx.x -> (b*Hq + h, slot). Slots are issued in increasing order, so
 // callers put their heaviest work in slot 0. With xcd_map, workgroup ids are
 // dealt so that each KV head's query heads stay on one XCD (id % 8 is the

@@ -509,7 +509,7 @@ attn_fwd_wide_kernel(const FwdArgs a) {
         float mx = -INFINITY;
 #pragma unroll
         for (int e = 0; e < 16; ++e) mx = fmaxf(mx, xo[g][e]);
-        tmax[g] = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        tmax[g] = max_xor32(mx);
       }
     };
     // P = 2^(t*q_scale - m), packed per 16-key step, plus the row sums
@@ -631,6 +631,12 @@ attn_fwd_wide_kernel(const FwdArgs a) {
 
     xblk xA, xB;  // scores of the last two halves (alternating)
     pblk pA, pB;  // P of the last two halves (alternating)
+    float xmA = -INFINITY, xmB = -INFINITY;  // W8A8 fast path: their row maxima (NG = 1)
+    auto row_max = [&](const xblk& xo) __attribute__((always_inline)) {
+      float t[NG];
+      half_max(xo, t);
+      return t[0];
+    };
     // One half-step, a single straight-line block per variant: xi/p1 = the
     // half before (scores in, P out), xo = this half (scores out), p2 = P of
     // the half two back (consumed by PV). dead = this half has no tile (all
@@ -800,16 +806,28 @@ attn_fwd_wide_kernel(const FwdArgs a) {
     // inside the wave is all there is): the structure of half_step_fast with
     // half_probs_w8's arithmetic, including its lazy rescale (a branch taken
     // before the straight-line part, rarely).
+    // xmi: the row max of xi (both lane halves), formed by the step that
+    // produced xi (or by the fixup that changed it); this step forms xmo for
+    // xo in the slices after its scores, so no max and no cross-lane round
+    // trip stands between two half-steps.
     auto half_step_fast_w8 = [&](int s, const int8_t* kt, const float* st, const uint16_t* vt,
-                                 xblk& xi, pblk& p1, xblk& xo, pblk& p2) __attribute__((always_inline)) {
+                                 xblk& xi, float xmi, pblk& p1, xblk& xo, float& xmo,
+                                 pblk& p2) __attribute__((always_inline)) {
       if constexpr (FAST_W8) {
       constexpr float LOG2_127 = 6.988684686772166f;
-      float tm0;
-      {
-        float tmx[1];
-        half_max(xi, tmx);
-        tm0 = tmx[0] * qsc[0];
-      }
+      const uint16_t* vr = vt + l32 * BN;
+      auto load_op = [&](int i) __attribute__((always_inline)) -> v4i {
+        if (i < DC) return *reinterpret_cast<const v4i*>(kt + (32 * s + l32) * D + koff[i]);
+        const int c = (i - DC) / DC, tt = (i - DC) % DC;
+        return *reinterpret_cast<const v4i*>(vr + 32 * tt * BN + voff[2 * s + c]);
+      };
+      constexpr int NOP = 3 * DC;  // 8 QK + 16 PV MFMAs
+      v4i opb[NOP];  // operand i is read SL8_FWD_PD MFMAs ahead of its use
+      // the first operands go out before the reference-point arithmetic
+#pragma unroll
+      for (int i = 0; i < SL8_FWD_PD && i < NOP; ++i) opb[i] = load_op(i);
+      __builtin_amdgcn_sched_barrier(0);
+      const float tm0 = xmi * qsc[0];
       // lazy rescale: the row's new reference point is used for this half's
       // codes now; O (which still gets half h-2's products, relative to the old
       // point, from the PV MFMAs below) and l are scaled after them
@@ -820,25 +838,17 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       const bool any_key = tm0 != -INFINITY;
       const float sub = any_key ? tm0 - LOG2_127 : 0.f;
       const float fac = any_key ? __builtin_amdgcn_exp2f(tm0 - m_run[0]) * (1.0f / 127.0f) : 0.f;
-      const uint16_t* vr = vt + l32 * BN;
-      auto load_op = [&](int i) __attribute__((always_inline)) -> v4i {
-        if (i < DC) return *reinterpret_cast<const v4i*>(kt + (32 * s + l32) * D + koff[i]);
-        const int c = (i - DC) / DC, tt = (i - DC) % DC;
-        return *reinterpret_cast<const v4i*>(vr + 32 * tt * BN + voff[2 * s + c]);
-      };
-      constexpr int NOP = 3 * DC;  // 8 QK + 16 PV MFMAs
       float pe[16];
       float hs = 0.f;
       float4 kv[4];
+      float xm = -INFINITY;
       v16i sc;
 #pragma unroll
       for (int r = 0; r < 16; ++r) sc[r] = 0;
-      v4i opb[NOP];  // operand i is read SL8_FWD_PD MFMAs ahead of its use
-#pragma unroll
-      for (int i = 0; i < SL8_FWD_PD && i < NOP; ++i) opb[i] = load_op(i);
       // slices: QK MFMA i: P codes of keys 2i, 2i+1 of half h-1; PV MFMAs
       // 0..1: pack them (bf16) + row sum; PV 2: k_scale reads; PV 3..10:
-      // scores of half h, two keys each
+      // scores of half h, two keys each; PV 11: their max in this lane;
+      // PV 12: the max over both lane halves (xmo)
 #pragma unroll
       for (int i = 0; i < NOP; ++i) {
         if (i + SL8_FWD_PD < NOP) opb[i + SL8_FWD_PD] = load_op(i + SL8_FWD_PD);
@@ -873,6 +883,13 @@ attn_fwd_wide_kernel(const FwdArgs a) {
             xo[0][e0 + 1] = (float)sc[e0 + 1] * ka[(e0 + 1) & 3];
             pin_vgpr(xo[0][e0]);
             pin_vgpr(xo[0][e0 + 1]);
+          } else if (k == 11) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) xm = fmaxf(xm, xo[0][e]);
+            pin_vgpr(xm);
+          } else if (k == 12) {
+            xmo = max_xor32(xm);
+            pin_vgpr(xmo);
           }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -989,10 +1006,17 @@ attn_fwd_wide_kernel(const FwdArgs a) {
         if constexpr (FAST) copies();
       } else if constexpr (W8) {
         if constexpr (FAST_W8) {
-          half_step_fast_w8(0, kcur, scur, vprev, xB, pB, xA, pA);
-          if (mask || !all_set) half_fixup(j, 0, mask, dead, xA);
-          half_step_fast_w8(1, kcur, scur, vprev, xA, pA, xB, pB);
-          if (mask || !all_set) half_fixup(j, 1, mask, dead, xB);
+          // a fixup may mask scores: the carried max is formed again
+          half_step_fast_w8(0, kcur, scur, vprev, xB, xmB, pB, xA, xmA, pA);
+          if (mask || !all_set) {
+            half_fixup(j, 0, mask, dead, xA);
+            xmA = row_max(xA);
+          }
+          half_step_fast_w8(1, kcur, scur, vprev, xA, xmA, pA, xB, xmB, pB);
+          if (mask || !all_set) {
+            half_fixup(j, 1, mask, dead, xB);
+            xmB = row_max(xB);
+          }
         } else {
           half_step_w8(j, 0, kcur, scur, vprev, mask, dead, xB, pB, xA, pA);
           half_step_w8(j, 1, kcur, scur, vprev, mask, dead, xA, pA, xB, pB);
@@ -1049,6 +1073,7 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       for (int g = 0; g < NG; ++g) {
   #pragma unroll
         for (int e = 0; e < 16; ++e) xA[g][e] = xB[g][e] = -INFINITY;
+        xmA = xmB = -INFINITY;
   #pragma unroll
         for (int c = 0; c < 2; ++c) {
           float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
