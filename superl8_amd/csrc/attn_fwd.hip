@@ -984,6 +984,15 @@ attn_fwd_wide_kernel(const FwdArgs a) {
     auto body = [&](int j, const int8_t* kcur, int8_t* knext, uint16_t* vcopy, const uint16_t* vprev,
                     const float* scur, float* snext) __attribute__((always_inline)) {
       const int n0 = n_beg + j * BN;
+      auto copies_v = [&]() __attribute__((always_inline)) {
+        if (j < ntiles) load_v(n0, vcopy);
+      };
+      auto copies_k = [&]() __attribute__((always_inline)) {
+        if (j + 1 < ntiles) {
+          load_k(n0 + BN, knext);
+          load_s(n0 + BN, snext);
+        }
+      };
       auto copies = [&]() __attribute__((always_inline)) {
         if (j + 1 < ntiles) {
           load_k(n0 + BN, knext);
@@ -994,8 +1003,12 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       // The straight-line D = 128 path issues the tile copies after its first
       // half-step (0.5 % faster at config 2 than at the start of the tile,
       // where they land in a burst on top of the first half's operand reads;
-      // the W8A8 path measured slower so).
-      if constexpr (!FAST) copies();
+      // the W8A8 path measured slower so). The W8A8 straight-line path copies
+      // K and k_scale at the tile start and V (32 KB) after the first
+      // half-step: config 5 1100 -> 1082 us (all after it: 1128 us, V first
+      // and K after it: 1135 us).
+      if constexpr (!FAST && !FAST_W8) copies();
+      if constexpr (FAST_W8) copies_k();
       const bool dead = !live(j);
       const bool mask = dead || masked(j);
       // A dead tile after a dead tile has nothing to do: the one before already
@@ -1004,6 +1017,7 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       // queries end early skip their last tiles this way).
       if (dead && !live(j - 1)) {
         if constexpr (FAST) copies();
+        if constexpr (FAST_W8) copies_v();
       } else if constexpr (W8) {
         if constexpr (FAST_W8) {
           // a fixup may mask scores: the carried max is formed again
@@ -1012,6 +1026,7 @@ attn_fwd_wide_kernel(const FwdArgs a) {
             half_fixup(j, 0, mask, dead, xA);
             xmA = row_max(xA);
           }
+          copies_v();
           half_step_fast_w8(1, kcur, scur, vprev, xA, xmA, pA, xB, xmB, pB);
           if (mask || !all_set) {
             half_fixup(j, 1, mask, dead, xB);
