@@ -1000,15 +1000,14 @@ attn_fwd_wide_kernel(const FwdArgs a) {
         }
         if (j < ntiles) load_v(n0, vcopy);
       };
-      // The straight-line D = 128 path issues the tile copies after its first
-      // half-step (0.5 % faster at config 2 than at the start of the tile,
-      // where they land in a burst on top of the first half's operand reads;
-      // the W8A8 path measured slower so). The W8A8 straight-line path copies
-      // K and k_scale at the tile start and V (32 KB) after the first
-      // half-step: config 5 1100 -> 1082 us (all after it: 1128 us, V first
-      // and K after it: 1135 us).
+      // The straight-line paths copy K and k_scale at the tile start and V
+      // after the first half-step, so the two copies do not land in one burst
+      // on top of a half-step's operand reads. Config 2: all copies after the
+      // first half-step 126.4 us, split 124.9 us (V first, K after it: 125.9);
+      // config 5: all at the start 1100 us, all after the first half-step
+      // 1128 us, split 1082 us (V first, K after it: 1135 us).
       if constexpr (!FAST && !FAST_W8) copies();
-      if constexpr (FAST_W8) copies_k();
+      if constexpr (FAST || FAST_W8) copies_k();
       const bool dead = !live(j);
       const bool mask = dead || masked(j);
       // A dead tile after a dead tile has nothing to do: the one before already
@@ -1016,8 +1015,7 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       // is P = 0 and scores of -inf (in the diagonal block, the waves whose
       // queries end early skip their last tiles this way).
       if (dead && !live(j - 1)) {
-        if constexpr (FAST) copies();
-        if constexpr (FAST_W8) copies_v();
+        if constexpr (FAST || FAST_W8) copies_v();
       } else if constexpr (W8) {
         if constexpr (FAST_W8) {
           // a fixup may mask scores: the carried max is formed again
@@ -1042,7 +1040,7 @@ attn_fwd_wide_kernel(const FwdArgs a) {
           // gets its mask / settle after the straight-line part
           half_step_fast(j, 0, kcur, scur, vprev, xB, pB, xA, pA);
           if (mask || !all_set) half_fixup(j, 0, mask, dead, xA);
-          copies();
+          copies_v();
           half_step_fast(j, 1, kcur, scur, vprev, xA, pA, xB, pB);
           if (mask || !all_set) half_fixup(j, 1, mask, dead, xB);
         } else {
