@@ -810,10 +810,15 @@ attn_fwd_wide_kernel(const FwdArgs a) {
     // produced xi (or by the fixup that changed it); this step forms xmo for
     // xo in the slices after its scores, so no max and no cross-lane round
     // trip stands between two half-steps.
+    // pf: the first SL8_FWD_PD operands of half-step s, already read by the
+    // step before it in the same tile (s = 1); step 0 reads them for step 1
+    // in its last slices, so that no half-step inside a tile starts with a
+    // full LDS round trip (one wave per SIMD: nothing else covers it).
     auto half_step_fast_w8 = [&](int s, const int8_t* kt, const float* st, const uint16_t* vt,
                                  xblk& xi, float xmi, pblk& p1, xblk& xo, float& xmo,
-                                 pblk& p2) __attribute__((always_inline)) {
+                                 pblk& p2, v4i (&pf)[SL8_FWD_PD]) __attribute__((always_inline)) {
       if constexpr (FAST_W8) {
+      static_assert(SL8_FWD_PD <= DC, "the prefetched operands are K operands");
       constexpr float LOG2_127 = 6.988684686772166f;
       const uint16_t* vr = vt + l32 * BN;
       auto load_op = [&](int i) __attribute__((always_inline)) -> v4i {
@@ -825,7 +830,7 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       v4i opb[NOP];  // operand i is read SL8_FWD_PD MFMAs ahead of its use
       // the first operands go out before the reference-point arithmetic
 #pragma unroll
-      for (int i = 0; i < SL8_FWD_PD && i < NOP; ++i) opb[i] = load_op(i);
+      for (int i = 0; i < SL8_FWD_PD && i < NOP; ++i) opb[i] = s ? pf[i] : load_op(i);
       __builtin_amdgcn_sched_barrier(0);
       const float tm0 = xmi * qsc[0];
       // lazy rescale: the row's new reference point is used for this half's
@@ -890,6 +895,10 @@ attn_fwd_wide_kernel(const FwdArgs a) {
           } else if (k == 12) {
             xmo = max_xor32(xm);
             pin_vgpr(xmo);
+          } else if (k >= 16 - SL8_FWD_PD && s == 0) {
+            // the next half-step's first K operand (same tile, keys 32..63)
+            const int n = k - (16 - SL8_FWD_PD);
+            pf[n] = *reinterpret_cast<const v4i*>(kt + (32 + l32) * D + koff[n]);
           }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -1019,13 +1028,14 @@ attn_fwd_wide_kernel(const FwdArgs a) {
       } else if constexpr (W8) {
         if constexpr (FAST_W8) {
           // a fixup may mask scores: the carried max is formed again
-          half_step_fast_w8(0, kcur, scur, vprev, xB, xmB, pB, xA, xmA, pA);
+          v4i pf[SL8_FWD_PD];
+          half_step_fast_w8(0, kcur, scur, vprev, xB, xmB, pB, xA, xmA, pA, pf);
           if (mask || !all_set) {
             half_fixup(j, 0, mask, dead, xA);
             xmA = row_max(xA);
           }
           copies_v();
-          half_step_fast_w8(1, kcur, scur, vprev, xA, xmA, pA, xB, xmB, pB);
+          half_step_fast_w8(1, kcur, scur, vprev, xA, xmA, pA, xB, xmB, pB, pf);
           if (mask || !all_set) {
             half_fixup(j, 1, mask, dead, xB);
             xmB = row_max(xB);
