@@ -37,6 +37,44 @@ namespace {
 
 constexpr int QTHREADS = 256;
 
+// Reduction over aligned groups of LPR lanes (a power of two <= 64) with no
+// LDS round trip: DPP inside a 16-lane row (quad_perm [1,0,3,2], quad_perm
+// [2,3,0,1], row_half_mirror, row_mirror: after each step a lane holds the
+// reduction over 2, 4, 8, 16 lanes), then v_permlane16_swap across the row
+// pair and v_permlane32_swap across the wave halves. Every lane of the group
+// ends with the result; op must be associative and commutative (max, integer
+// add: exact in any order).
+template <int LPR, typename F>
+__device__ __forceinline__ uint32_t lane_group_reduce(uint32_t v, F op) {
+  static_assert(LPR >= 1 && LPR <= 64 && (LPR & (LPR - 1)) == 0, "LPR: a power of two <= 64");
+  auto dpp = [](uint32_t x, auto ctrl) __attribute__((always_inline)) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, decltype(ctrl)::value, 0xF, 0xF, false);
+  };
+  if constexpr (LPR >= 2) v = op(v, dpp(v, std::integral_constant<int, 0xB1>{}));
+  if constexpr (LPR >= 4) v = op(v, dpp(v, std::integral_constant<int, 0x4E>{}));
+  if constexpr (LPR >= 8) v = op(v, dpp(v, std::integral_constant<int, 0x141>{}));
+  if constexpr (LPR >= 16) v = op(v, dpp(v, std::integral_constant<int, 0x140>{}));
+  if constexpr (LPR >= 32) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = op(r[0], r[1]);
+  }
+  if constexpr (LPR >= 64) {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    v = op(r[0], r[1]);
+  }
+  return v;
+}
+template <int LPR>
+__device__ __forceinline__ float lane_group_max(float v) {
+  return __uint_as_float(lane_group_reduce<LPR>(__float_as_uint(v), [](uint32_t a, uint32_t b) {
+    return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
+  }));
+}
+template <int LPR>
+__device__ __forceinline__ int lane_group_sum(int v) {
+  return (int)lane_group_reduce<LPR>((uint32_t)v, [](uint32_t a, uint32_t b) { return a + b; });
+}
+
 template <int DT> struct Elem;
 template <> struct Elem<SL8_DTYPE_F16> {
   using T = uint16_t;
@@ -86,8 +124,7 @@ quant_rows_kernel(const typename Elem<DT>::T* __restrict__ x, const float* __res
   if (live) {
     for (int d = lane; d < K; d += LPR) amax = fmaxf(amax, fabsf(row_val<DT, MEAN>(xr, mr, d)));
   }
-#pragma unroll
-  for (int o = LPR / 2; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+  amax = lane_group_max<LPR>(amax);
   if (!live) return;
 
   const float s = amax * (1.0f / 127.0f);
@@ -172,8 +209,7 @@ quant_rows_vec_kernel(const typename Elem<DT>::T* __restrict__ x, const float* _
     for (int e = 0; e < EPV; ++e) amax = fmaxf(amax, fabsf(f[v][e]));
   }
   if constexpr (LPR <= 64) {
-#pragma unroll
-    for (int o = LPR / 2; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    amax = lane_group_max<LPR>(amax);
   } else {
     __shared__ float red[QTHREADS / 64];
 #pragma unroll
@@ -667,18 +703,18 @@ extern "C" int sl8_q_outlier_gate(const void* q, int dtype, int64_t rows, int64_
 // ---------------------------------------------------------------------------
 // Fused attention prologue for fp16 Q/K (reference superl8/quant/core.py
 // quantize_qk + smooth_k, and the outlier gate of superl8/ops.py:115-147):
-// three launches instead of six, Q read once, K read twice, no zeroing pass.
+// two launches instead of six, Q read once, K read twice, no zeroing pass.
 //
 // Launch A: K-mean partials. Block (g, c) sums key rows [128c, 128c + 128)
 //   of group g exactly in int64 fixed point (value * 2^24, decoded from the
-//   fp16 bits) with 16-byte loads and stores its D partial sums; the mean is
-//   exact, hence independent of the summation order. Block 0 also clears the
-//   gate flag.
-// Launch M: the mean of each (group, column) from its partials (int64 ->
-//   fp64 -> / N -> fp32, as sl8_k_mean).
+//   fp16 bits) with 16-byte loads, all of a thread's rows in flight at once,
+//   and stores its D partial sums; the mean is exact, hence independent of
+//   the summation order. Block 0 also clears the gate flag.
 // Launch B, two roles chosen per block:
-//   * K: subtracts the mean from each key row with the fp16 rounding of
-//     torch.sub and quantises it;
+//   * K: issues its key rows' loads, forms the group's mean from the C
+//     partials meanwhile (int64 -> fp64 -> / N -> fp32, as sl8_k_mean; the
+//     first block of each group also stores it), subtracts it from each row
+//     with the fp16 rounding of torch.sub and quantises the row;
 //   * Q: per-row int8 quantisation (scale * q_scale_mul) and, with a gate
 //     ratio, the outlier decision for every row. f(x) = fl(max / fl(x + 1e-10))
 //     is non-increasing in x >= 0, so f(median) > ratio iff more than (D-1)/2
@@ -692,7 +728,7 @@ namespace sl8 {
 namespace {
 
 constexpr int PRO_CHUNK = 128;      // key rows per mean partial
-constexpr int PRO_KROWS = 32;       // key rows per quantise block
+constexpr int PRO_KROWS = 64;       // key rows per quantise block (each K block also forms its group's mean: 32 measured 1 us slower at config 2, 128 0.3 us)
 constexpr int PRO_QBLOCKS_MAX = 16384;
 constexpr int PRO_QP = 1;           // Q rows per thread per pass (1: measured fastest; more rows per thread cost occupancy)
 
@@ -704,17 +740,9 @@ __device__ __forceinline__ long long f16_fixed24(uint32_t h) {
 }
 
 template <int LPR>
-__device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-  for (int o = LPR / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
+__device__ __forceinline__ float group_max(float v) { return lane_group_max<LPR>(v); }
 template <int LPR>
-__device__ __forceinline__ int group_sum(int v) {
-#pragma unroll
-  for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
+__device__ __forceinline__ int group_sum(int v) { return lane_group_sum<LPR>(v); }
 
 __device__ __forceinline__ void unpack_h8(const uint4& raw, float* f) {
   const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
@@ -778,10 +806,18 @@ prologue_a_kernel(const uint16_t* __restrict__ k, int64_t N, int C,
   long long acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0;
-#pragma unroll 2
-  for (int64_t n = n0 + sub; n < n1; n += RPP) {
-    const uint4 raw = *reinterpret_cast<const uint4*>(kg + n * D);
-    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+  // every row load of the chunk is issued before any is summed (one round
+  // trip; with two in flight the launch was latency-bound: config 2 9.1 us)
+  constexpr int NIT = PRO_CHUNK / RPP;
+  uint4 raw[NIT];
+#pragma unroll
+  for (int i = 0; i < NIT; ++i) {
+    const int64_t n = n0 + sub + (int64_t)i * RPP;
+    raw[i] = n < n1 ? *reinterpret_cast<const uint4*>(kg + n * D) : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const uint32_t w[4] = {raw[it].x, raw[it].y, raw[it].z, raw[it].w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       acc[2 * i] += f16_fixed24(w[i] & 0xFFFFu);
@@ -799,38 +835,14 @@ prologue_a_kernel(const uint16_t* __restrict__ k, int64_t N, int C,
   }
 }
 
-// Mean of each (group, column) from its partial sums.
-__global__ void __launch_bounds__(256)
-prologue_mean_kernel(const long long* __restrict__ part, int64_t G, int C, int D, int64_t N,
-                     float* __restrict__ k_mean) {
-  // 8 lanes per column, each summing every 8th partial, then a lane reduction
-  const int64_t t8 = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t i = t8 >> 3;
-  const int cl = (int)(t8 & 7);
-  const bool live = i < G * D;  // uniform per 8-lane group
-  long long t = 0;
-  if (live) {
-    const int64_t g = i / D, d = i % D;
-    const long long* p = part + g * C * D + d;
-#pragma unroll 4
-    for (int c = cl; c < C; c += 8) t += p[(int64_t)c * D];
-  }
-#pragma unroll
-  for (int o = 4; o > 0; o >>= 1) {
-    const int lo = __shfl_xor((int)(unsigned)t, o, 64);
-    const int hi = __shfl_xor((int)(t >> 32), o, 64);
-    t += (long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
-  }
-  if (live && cl == 0) k_mean[i] = (float)(((double)t * 0x1p-24) / (double)N);
-}
-
 // B: the smoothed K rows (blocks [0, nkb): PRO_KROWS rows of group
 // blockIdx / kbg each) and the Q rows with the outlier gate (the rest). The Q
 // work does not depend on the mean, but sharing this launch keeps it off the
 // critical path A -> mean -> B of the K side.
 template <int D, bool GATE>
 __global__ void __launch_bounds__(256)
-prologue_b_kernel(const uint16_t* __restrict__ k, int64_t N, const float* __restrict__ k_mean,
+prologue_b_kernel(const uint16_t* __restrict__ k, int64_t N, const long long* __restrict__ part,
+                  int C, float* __restrict__ k_mean,
                   int8_t* __restrict__ k_i8, float* __restrict__ k_scale, int kbg, int nkb,
                   const uint16_t* __restrict__ q, int64_t qrows, float qmul, float ratio,
                   int8_t* __restrict__ q_i8, float* __restrict__ q_scale,
@@ -848,9 +860,32 @@ prologue_b_kernel(const uint16_t* __restrict__ k, int64_t N, const float* __rest
       const int64_t n = n0 + i * RPP + sub;
       raw[i] = n < N ? reinterpret_cast<const uint4*>(kg + n * D)[lane] : make_uint4(0, 0, 0, 0);
     }
-    const float4 m0 = reinterpret_cast<const float4*>(k_mean + g * D)[2 * lane];
-    const float4 m1 = reinterpret_cast<const float4*>(k_mean + g * D)[2 * lane + 1];
-    const float mv[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+    // the group's mean from A's partials while the rows are in flight:
+    // column d summed by PS threads over every PS-th partial, then in LDS
+    constexpr int PS = 256 / D;
+    __shared__ long long mred[PS][D];
+    __shared__ float mean_s[D];
+    {
+      const int d = threadIdx.x % D, ps = threadIdx.x / D;
+      const long long* pg = part + g * C * D + d;
+      long long t = 0;
+#pragma unroll 8
+      for (int c = ps; c < C; c += PS) t += pg[(int64_t)c * D];
+      mred[ps][d] = t;
+    }
+    __syncthreads();
+    if (threadIdx.x < D) {
+      long long t = 0;
+#pragma unroll
+      for (int p = 0; p < PS; ++p) t += mred[p][threadIdx.x];
+      const float m = (float)(((double)t * 0x1p-24) / (double)N);
+      mean_s[threadIdx.x] = m;
+      if (blockIdx.x % kbg == 0) k_mean[g * D + threadIdx.x] = m;
+    }
+    __syncthreads();
+    float mv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mv[e] = mean_s[lane * 8 + e];
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
       const int64_t n = n0 + i * RPP + sub;
@@ -984,19 +1019,17 @@ extern "C" int sl8_quantize_qk(const void* q, const void* k, int dtype, int64_t 
   const uint16_t* qh = static_cast<const uint16_t*>(q);
   const uint16_t* kh = static_cast<const uint16_t*>(k);
   int32_t* fl = gate ? gate_flag : nullptr;
-  // A (K-mean partials) -> mean -> B (K and Q rows, gate): the Q rows, the
+  // A (K-mean partials) -> B (the mean, K and Q rows, gate): the Q rows, the
   // bulk of the bytes, run beside the K rows in B instead of ahead of the mean
 #define SL8_PRO(DD)                                                                              \
   do {                                                                                          \
     prologue_a_kernel<DD><<<nka, 256, 0, st>>>(kh, N, C, part, fl);                              \
-    prologue_mean_kernel<<<(unsigned)((G * DD * 8 + 255) / 256), 256, 0, st>>>(part, G, C, DD,  \
-                                                                              N, k_mean);       \
     if (gate)                                                                                   \
-      prologue_b_kernel<DD, true><<<nkb + nqb, 256, 0, st>>>(kh, N, k_mean, k_i8, k_scale,      \
-          (int)kbg, nkb, qh, qrows, q_scale_mul, gate_ratio, q_i8, q_scale, fl);                \
+      prologue_b_kernel<DD, true><<<nkb + nqb, 256, 0, st>>>(kh, N, part, C, k_mean, k_i8,      \
+          k_scale, (int)kbg, nkb, qh, qrows, q_scale_mul, gate_ratio, q_i8, q_scale, fl);       \
     else                                                                                        \
-      prologue_b_kernel<DD, false><<<nkb + nqb, 256, 0, st>>>(kh, N, k_mean, k_i8, k_scale,     \
-          (int)kbg, nkb, qh, qrows, q_scale_mul, gate_ratio, q_i8, q_scale, fl);                \
+      prologue_b_kernel<DD, false><<<nkb + nqb, 256, 0, st>>>(kh, N, part, C, k_mean, k_i8,     \
+          k_scale, (int)kbg, nkb, qh, qrows, q_scale_mul, gate_ratio, q_i8, q_scale, fl);       \
   } while (0)
   if (D == 64) SL8_PRO(64);
   else if (D == 128) SL8_PRO(128);
