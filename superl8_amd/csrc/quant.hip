@@ -64,10 +64,13 @@ __device__ __forceinline__ uint32_t lane_group_reduce(uint32_t v, F op) {
   }
   return v;
 }
+// v >= 0 and not NaN (an amax started at 0 and grown by fmaxf, which drops
+// NaN): the unsigned order of the bit patterns is the float order, and 0 is
+// the identity of the unsigned max the DPP moves fold into
 template <int LPR>
 __device__ __forceinline__ float lane_group_max(float v) {
   return __uint_as_float(lane_group_reduce<LPR>(__float_as_uint(v), [](uint32_t a, uint32_t b) {
-    return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
+    return a > b ? a : b;
   }));
 }
 template <int LPR>
@@ -751,14 +754,17 @@ __device__ __forceinline__ void unpack_h8(const uint4& raw, float* f) {
 }
 
 // Eight codes clamp(rint(fl(x / safe))) without a division per element.
-// |x| <= amax, so |fl(x / safe)| < 128 and r = x * fl(1/safe) is within
-// 1.5 * 2^-23 * 128 < 2^-14 of it. n = r rounded to nearest-even by the
-// 1.5 * 2^23 magic constant; unless |r - n| > 0.5 - 2^-14 (r near a
-// half-integer) both r and fl(x / safe) round to n. Lanes holding such an
-// element (about 1e-4 of them) take the IEEE division, under a wave-uniform
-// branch so the common path never executes it.
+// |x| <= amax, so |x / safe| <= 127 * (1 + 2^-23) and, with inv = v_rcp_f32(safe)
+// (at most 1 ulp from 1 / safe; safe >= 2^-24 / 127 here, a normal number),
+// r = fl(x * inv) is within 128 * (2^-23 + 2^-24) = 1.5 * 2^-16 of x / safe,
+// and fl(x / safe) within 2^-17 of it: |r - fl(x / safe)| < 2^-14. n = r
+// rounded to nearest-even by the 1.5 * 2^23 magic constant; unless
+// |r - n| > 0.5 - 2^-14 (r near a half-integer) both r and fl(x / safe)
+// round to n. Lanes holding such an element (about 1e-4 of them) take the
+// IEEE division, under a wave-uniform branch so the common path never
+// executes it.
 __device__ __forceinline__ uint2 codes8(const float* f, float safe) {
-  const float inv = 1.0f / safe;
+  const float inv = __builtin_amdgcn_rcpf(safe);
   constexpr float MAGIC = 12582912.f;  // 1.5 * 2^23
   float n[8];
   bool amb = false;
@@ -771,18 +777,24 @@ __device__ __forceinline__ uint2 codes8(const float* f, float safe) {
   if (__builtin_expect(__ballot(amb) != 0, 0)) {
     if (amb) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) n[e] = rintf(__fdiv_rn(f[e], safe));
+      for (int e = 0; e < 8; ++e) {
+        n[e] = rintf(__fdiv_rn(f[e], safe));
+        if (n[e] != n[e]) n[e] = -127.f;  // NaN: the clamp of fmaxf / fminf gives -127
+      }
     }
   }
+  // n is an integer in [-128, 128] (or the division's result): clamp as int
   uint32_t w[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    w[i] = 0;
+    int c[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float c = fminf(fmaxf(n[4 * i + e], -127.f), 127.f);
-      w[i] |= ((uint32_t)(int)c & 0xFFu) << (8 * e);
-    }
+    for (int e = 0; e < 4; ++e) c[e] = __builtin_amdgcn_fmed3f(n[4 * i + e], -127.f, 127.f);
+    // bytes 0 of c0..c3 -> one dword (v_perm_b32: selectors 0-3 pick the
+    // second operand's bytes, 4-7 the first's, 0x0c a zero byte)
+    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)c[1], (uint32_t)c[0], 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)c[3], (uint32_t)c[2], 0x04000c0cu);
+    w[i] = lo | hi;
   }
   return make_uint2(w[0], w[1]);
 }

@@ -55,6 +55,32 @@ def test_fused_prologue_matches_separate_kernels(device, B, Hq, Hkv, M, N, D):
 
 
 @pytest.mark.parametrize("D", [64, 128, 256])
+def test_fused_prologue_nonfinite_rows(device, D):
+    """NaN and +-inf elements: the fused codes (reciprocal + exact-division
+    fallback) equal the separate kernels' (IEEE division per element) bit for
+    bit: a NaN element codes to -127 (the clamp fmaxf / fminf), an inf row has
+    an inf scale, its inf element codes to -127 and its finite ones to 0."""
+    g = torch.Generator(device="cpu").manual_seed(D + 7)
+    q = torch.randn(1, 2, 40, D, generator=g).half().to(device)
+    k = torch.randn(1, 1, 40, D, generator=g).half().to(device)
+    q[0, 0, 3, 5] = float("nan")
+    q[0, 1, 7, 0] = float("inf")
+    q[0, 1, 8, D - 1] = float("-inf")
+    q[0, 0, 9, :] = float("nan")
+    qi, qs, _, _, _, _ = _C.quantize_qk_fused(q, k, 1.0, 0.0)
+    qi_ref, qs_ref = _C.quantize_rows_centered(q, None, 1.0)
+    assert torch.equal(qi, qi_ref)
+    assert torch.equal(qs.isnan(), qs_ref.isnan()) and torch.equal(qs.nan_to_num(), qs_ref.nan_to_num())
+    assert int(qi[0, 0, 3, 5]) == -127 and (qi[0, 0, 9] == -127).all()
+    assert int(qi[0, 1, 7, 0]) == -127 and (qi[0, 1, 7, 1:] == 0).all()
+    assert torch.isinf(qs[0, 1, 7]).all()
+    # the finite rows are untouched by the others
+    fin = torch.isfinite(q.float()).all(-1)
+    qi2, qs2, _, _, _, _ = _C.quantize_qk_fused(torch.where(fin[..., None], q, 0), k, 1.0, 0.0)
+    assert torch.equal(qi[fin], qi2[fin]) and torch.equal(qs[fin], qs2[fin])
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
 def test_fused_gate_decisions(device, D):
     torch.manual_seed(D)
     k = torch.randn(1, 2, 64, D, device=device, dtype=torch.float16)
