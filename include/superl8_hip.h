@@ -92,7 +92,7 @@ int sl8_quantize_i8_row_groups(const void* x, int x_dtype, int64_t G, int64_t N,
 
 /* ------------------------------------------------------------------------
  * Fused fp16 attention prologue: quantize_qk (no rotation) plus, optionally,
- * the outlier gate, in three launches (six unfused). Replaces superl8/quant/core.py:164-196
+ * the outlier gate, in two launches (six unfused). Replaces superl8/quant/core.py:164-196
  * (smooth_k + quantize_qk) and detect_q_outlier_domination (core.py:113-145)
  * as called from superl8/ops.py:115-150; results equal sl8_k_mean,
  * sl8_quantize_i8_rows_centered and sl8_q_outlier_gate bit for bit.

@@ -818,8 +818,7 @@ prologue_a_kernel(const uint16_t* __restrict__ k, int64_t N, int C,
   long long acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0;
-  // every row load of the chunk is issued before any is summed (one round
-  // trip; with two in flight the launch was latency-bound: config 2 9.1 us)
+  // every row load of the chunk is issued before any is summed (one round trip)
   constexpr int NIT = PRO_CHUNK / RPP;
   uint4 raw[NIT];
 #pragma unroll
