@@ -1378,6 +1378,353 @@ int w8a8_pad_operands(const int8_t*& q, const int8_t*& k, const int8_t*& v, cons
 // w8a8_wide_workspace() bytes for bf16 V^T [B*Hkv][D][Npad]. D is a
 // supported width (64/128/256); dout = the output row length (the caller's
 // head dim when the operands were padded).
+// ---------------------------------------------------------------------------
+// W8A8 prefill at D = 256 with 16 queries per wave (SL8_W8_Q16). The 32-query
+// waves of attn_fwd_wide_kernel hold O in 128 accumulators and run one wave
+// per SIMD, where nothing covers a wave's own latencies or the per-tile
+// barrier. Here a wave owns 16 queries on the 16x16 MFMAs: O^T is 16 blocks
+// of 16 dims x 16 queries (64 accumulators), and a workgroup of 8 waves (two
+// per SIMD) covers the same 128 queries and shares the same K / V^T tiles.
+//   QK: S^T = K Q^T on v_mfma_i32_16x16x64_i8, per 32-key half 2 key blocks
+//       x 4 dim chunks; lane (l16, g) ends with keys 16 kb + 4 g + i of query
+//       l16 (kb = 0, 1; i = 0..3).
+//   PV: O^T += V^T P^T on v_mfma_f32_16x16x32_bf16 with the half's 32 keys in
+//       the order sigma(8 g + e) = 16 (e / 4) + 4 g + e % 4: exactly the keys
+//       lane (l16, g) holds, so P needs no lane exchange; the V^T operand is
+//       two 8-byte reads per MFMA in the same order.
+// The arithmetic per row is the wide kernel's W8A8 path (P re-quantised per
+// 32-key half against the half's max, the lazy reference-point rescale), and
+// so is the straight-line half-step. Config 5: 1081 -> 986 us (the same
+// kernel with the compiler's schedule, each operand read right before its
+// MFMA: 1633 us). SL8_W8_Q16 = 0 runs attn_fwd_wide_kernel's W8A8 path.
+#ifndef SL8_W8_Q16
+#define SL8_W8_Q16 1
+#endif
+typedef float v4f_t __attribute__((ext_vector_type(4)));
+
+template <bool CAUSAL>
+__global__ void __launch_bounds__(512, 1)
+attn_w8a8_q16_kernel(const FwdArgs a) {
+  if (a.skip != nullptr && *a.skip != 0) return;
+  constexpr int D = 256, WT = 512, WQ = 16, WBM = 128;
+  constexpr int KCH = BN * D / 16 / WT;      // K tile copies per thread
+  constexpr int VCH = D * BN * 2 / 16 / WT;  // V^T tile copies per thread
+  constexpr float LOG2_127 = 6.988684686772166f;
+  __shared__ __attribute__((aligned(16))) int8_t sk0[BN * D];
+  __shared__ __attribute__((aligned(16))) int8_t sk1[BN * D];
+  __shared__ __attribute__((aligned(16))) uint16_t sv0[D * BN];
+  __shared__ __attribute__((aligned(16))) uint16_t sv1[D * BN];
+  __shared__ __attribute__((aligned(16))) float ss0[BN];
+  __shared__ __attribute__((aligned(16))) float ss1[BN];
+
+  const int nslot = CAUSAL ? (a.nqb + 1) / 2 : a.nqb;
+  int bh, slot;
+  block_coords(a, nslot, bh, slot);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, g = lane >> 4;
+  const int gsz = a.Hq / a.Hkv;
+  const int b = bh / a.Hq, hq = bh % a.Hq;
+  const int64_t bkv = (int64_t)b * a.Hkv + hq / gsz;
+  const int M = a.M, N = a.N;
+  const int diag = CAUSAL ? N - M : 0;
+  const int wl = a.window_left;
+  const int8_t* kb = a.k + bkv * (int64_t)N * D;
+  const float* ksb = a.ks + bkv * (int64_t)N;
+  const uint16_t* vtb = a.vt + bkv * (int64_t)D * a.Npad;
+
+  int qbs[2];
+  int npass = 1;
+  qbs[0] = a.nqb - 1 - slot;
+  qbs[1] = slot;
+  if (CAUSAL) npass = (qbs[1] != qbs[0]) ? 2 : 1;
+
+  // K operand (A, 16 keys x 64 dims): lane (l16, g) reads the 16-byte chunk
+  // 4 c + g of key row l16 of the block; the tile keeps chunk c of row r at
+  // c ^ (r & 15) (the copy below), so 16 rows read 16 distinct bank groups
+  int koff[4];
+#pragma unroll
+  for (int c4 = 0; c4 < 4; ++c4) koff[c4] = ((4 * c4 + g) ^ l16) * 16;
+  // V^T operand (A, 16 dims x 32 keys in sigma order): keys 4 g .. +3 and
+  // 16 + 4 g .. +3 of the half, 8 bytes each, of V^T row l16 of the dim
+  // block. v8_to_bf16_t_kernel stores each 16-key group with bits 2 and 3 of
+  // the key index exchanged (key 8 b3 + 4 b2 + i at position 8 b2 + 4 b3 + i),
+  // so keys 4 g + i of a group sit at 8 (g & 1) + 4 (g >> 1) + i: chunk
+  // (g & 1) of the group, byte 8 (g >> 1); the tile keeps 16-byte chunk c of
+  // row d at c ^ ((d >> 1) & 7)
+  int voff[2][2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+      voff[s][p] = ((4 * s + 2 * p + (g & 1)) ^ ((l16 >> 1) & 7)) * 16 + (g >> 1) * 8;
+  // V buffers start as zeros (finite): the first half-steps multiply them by P = 0
+  for (int i = tid; i < D * BN / 8; i += WT) {
+    reinterpret_cast<uint4*>(sv0)[i] = make_uint4(0, 0, 0, 0);
+    reinterpret_cast<uint4*>(sv1)[i] = make_uint4(0, 0, 0, 0);
+  }
+
+  for (int pass = 0; pass < npass; ++pass) {
+    const int m_blk = qbs[pass] * WBM;
+    const int q0 = m_blk + wave * WQ;
+    const int mq = q0 + l16;
+    const bool m_ok = mq < M;
+    const int qpos = mq + diag;
+    // Q operand (B, 64 dims x 16 queries): query mq, dims 64 c + 16 g .. +15
+    v4i qop[4];
+    {
+      const int8_t* qrow = a.q + ((int64_t)bh * M + (m_ok ? mq : M - 1)) * D + 16 * g;
+#pragma unroll
+      for (int c4 = 0; c4 < 4; ++c4) {
+        qop[c4] = *reinterpret_cast<const v4i*>(qrow + 64 * c4);
+        if (!m_ok) qop[c4] = v4i{0, 0, 0, 0};
+      }
+    }
+    const float qsc = m_ok ? a.qs[(int64_t)bh * M + mq] : 1.f;
+
+    int n_end = N;
+    if (CAUSAL) n_end = max(0, min(N, m_blk + WBM + diag));
+    int n_beg = 0;
+    if (wl >= 0) n_beg = min(n_end, max(0, m_blk + diag - wl + 1) & ~(BN - 1));
+    const int ntiles = (n_end - n_beg + BN - 1) / BN;
+    const int wq_lo = q0 + diag, wq_hi = q0 + WQ - 1 + diag;
+    auto live = [&](int t) __attribute__((always_inline)) {
+      if (t < 0 || t >= ntiles) return false;
+      const int n0 = n_beg + t * BN;
+      bool ok = true;
+      if (CAUSAL && n0 > wq_hi) ok = false;
+      if (wl >= 0 && n0 + BN - 1 <= wq_lo - wl) ok = false;
+      return ok;
+    };
+    auto masked = [&](int t) __attribute__((always_inline)) {
+      const int n0 = n_beg + t * BN;
+      return (n0 + BN > N) || (CAUSAL && n0 + BN - 1 > wq_lo) || (wl >= 0 && n0 <= wq_hi - wl);
+    };
+
+    // tile copies, as the wide kernel's (rows past N read as zeros)
+    const brsrc_t rk = make_rsrc(kb, (uint32_t)N * D);
+    const brsrc_t rv = make_rsrc(vtb, (uint32_t)D * a.Npad * 2);
+    const brsrc_t rs = make_rsrc(ksb, (uint32_t)N * 4);
+    uint32_t kvo[KCH], vvo[VCH];
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      const int sl = i * WT + tid;
+      const int row = sl / 16;
+      const int c = (sl % 16) ^ (row & 15);
+      kvo[i] = (uint32_t)(row * D + 16 * c);
+    }
+#pragma unroll
+    for (int i = 0; i < VCH; ++i) {
+      const int sl = i * WT + tid;
+      const int row = sl / 8;
+      const int c = (sl % 8) ^ ((row >> 1) & 7);
+      vvo[i] = (uint32_t)(row * a.Npad * 2 + 16 * c);
+    }
+    auto load_k = [&](int n0, int8_t* dst) __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < KCH; ++i)
+        buf16_to_lds(rk, dst + (i * WT + wave * 64) * 16, kvo[i], (uint32_t)n0 * D);
+    };
+    auto load_v = [&](int n0, uint16_t* dst) __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < VCH; ++i)
+        buf16_to_lds(rv, dst + (i * WT + wave * 64) * 8, vvo[i], (uint32_t)n0 * 2);
+    };
+    auto load_s = [&](int n0, float* dst) __attribute__((always_inline)) {
+      if (wave == 0) buf4_to_lds(rs, dst, (uint32_t)lane * 4, (uint32_t)n0 * 4);
+    };
+
+    v4f_t oacc[16];
+#pragma unroll
+    for (int t = 0; t < 16; ++t) oacc[t] = v4f_t{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_lane = 0.f;
+    typedef float xblk16[8];  // a half's scores: slot 4 kb + i = key 16 kb + 4 g + i
+
+    // max over the 32 keys of the row: the lane's 8, then the 4 lane groups
+    auto row_max = [&](const xblk16& x) __attribute__((always_inline)) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mx = fmaxf(mx, x[e]);
+      const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+      mx = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+      return max_xor32(mx);
+    };
+    xblk16 xA, xB;
+    v8bf pA, pB;
+    float xmA = -INFINITY, xmB = -INFINITY;  // their row maxima (both lane groups)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      xA[e] = xB[e] = -INFINITY;
+      pA[e] = pB[e] = (__bf16)0.f;
+    }
+    bool all_set = false;  // every row's reference point is fixed (wave-uniform)
+    // Straight-line half-step (the wide kernel's half_step_fast_w8 in this
+    // layout): MFMA i (QK of half h: i < 8; PV of half h - 2: i >= 8) is
+    // preceded by the LDS read of operand i + 3 and followed by a slice of
+    // VALU work: P code of key i of half h - 1 (i < 8); the k_scale reads and
+    // the pack of P (i = 8); the score of key i - 9 of half h (i = 9..16);
+    // its max (i = 17, 18). xmi: the row max of xi; xmo: that of xo (before
+    // masking: the fixup forms it again).
+    auto half_step_fast = [&](int s, const int8_t* kt, const float* st, const uint16_t* vt,
+                              xblk16& xi, float xmi, v8bf& p1, xblk16& xo, float& xmo,
+                              v8bf& p2) __attribute__((always_inline)) {
+      const char* vb = reinterpret_cast<const char*>(vt) + l16 * (2 * BN);
+      auto load_op = [&](int i) __attribute__((always_inline)) -> v4i {
+        if (i < 8) {
+          const int k2 = i >> 2, c4 = i & 3;
+          return *reinterpret_cast<const v4i*>(kt + (32 * s + 16 * k2 + l16) * D + koff[c4]);
+        }
+        const char* row = vb + (i - 8) * 16 * (2 * BN);
+        const uint2 lo = *reinterpret_cast<const uint2*>(row + voff[s][0]);
+        const uint2 hi = *reinterpret_cast<const uint2*>(row + voff[s][1]);
+        return v4i{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+      };
+      constexpr int NOP = 24;
+      constexpr int PD = 3;
+      v4i opb[NOP];
+#pragma unroll
+      for (int i = 0; i < PD; ++i) opb[i] = load_op(i);
+      __builtin_amdgcn_sched_barrier(0);
+      const float tm0 = xmi * qsc;
+      const bool ug = tm0 > m_run + a.w8_excess;
+      const bool any_up = __any(ug);
+      const float fr = ug ? __builtin_amdgcn_exp2f(m_run - tm0) : 1.f;
+      if (ug) m_run = tm0;
+      const bool any_key = tm0 != -INFINITY;
+      const float sub = any_key ? tm0 - LOG2_127 : 0.f;
+      const float fac = any_key ? __builtin_amdgcn_exp2f(tm0 - m_run) * (1.0f / 127.0f) : 0.f;
+      float pe[8];
+      float hs = 0.f, xm = -INFINITY;
+      float4 kv[2];
+      v4i sc[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
+#pragma unroll
+      for (int i = 0; i < NOP; ++i) {
+        if (i + PD < NOP) opb[i + PD] = load_op(i + PD);
+        __builtin_amdgcn_sched_barrier(0);
+        if (i < 8) {
+          sc[i >> 2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(opb[i], qop[i & 3], sc[i >> 2], 0, 0, 0);
+          const float y = __builtin_amdgcn_exp2f(fmaf(xi[i], qsc, -sub));
+          hs += y;
+          pe[i] = rintf(y) * fac;
+          pin_vgpr(pe[i]);
+          pin_vgpr(hs);
+        } else {
+          const int tb = i - 8;
+          oacc[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, opb[i]), p2, oacc[tb], 0, 0, 0);
+          if (i == 8) {
+            kv[0] = *reinterpret_cast<const float4*>(st + 32 * s + 4 * g);
+            kv[1] = *reinterpret_cast<const float4*>(st + 32 * s + 16 + 4 * g);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) p1[e] = (__bf16)pe[e];
+            pin_vgpr(__builtin_bit_cast(v4i, p1));
+            l_lane = l_lane * fr + hs * fac;
+          } else if (i <= 16) {
+            const int e = i - 9;
+            const float kk[4] = {kv[e >> 2].x, kv[e >> 2].y, kv[e >> 2].z, kv[e >> 2].w};
+            xo[e] = (float)sc[e >> 2][e & 3] * kk[e & 3];
+            pin_vgpr(xo[e]);
+          } else if (i == 17) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xm = fmaxf(xm, xo[e]);
+            pin_vgpr(xm);
+          } else if (i == 18) {
+            const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(xm), __float_as_uint(xm), false, false);
+            xmo = max_xor32(fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1])));
+            pin_vgpr(xmo);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (any_up) {
+#pragma unroll
+        for (int t = 0; t < 16; ++t) oacc[t] *= fr;
+      }
+    };
+    // masked halves and halves that may fix a row's reference point
+    auto half_fixup = [&](int t, int s, bool do_mask, bool dead, xblk16& xo, float& xmo)
+        __attribute__((always_inline)) {
+      if (do_mask) {
+        const int nb = n_beg + t * BN + 32 * s;
+        // key n is visible iff (n - lo) unsigned < (hi - lo)
+        const int hi = dead ? nb : min(N, CAUSAL ? qpos + 1 : N);
+        const int lo = (wl >= 0) ? qpos - wl + 1 : INT_MIN / 2;
+        const int lo_c = max(lo, nb - 64);
+        const uint32_t span = hi > lo_c ? (uint32_t)(hi - lo_c) : 0u;
+        const uint32_t rel = (uint32_t)(nb + 4 * g - lo_c);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          xo[e] = (rel + (uint32_t)(16 * (e >> 2) + (e & 3)) < span) ? xo[e] : -INFINITY;
+      }
+      xmo = row_max(xo);
+      // the first visible half fixes the row's reference point
+      if (m_run == -INFINITY && xmo != -INFINITY) m_run = xmo * qsc;
+      all_set = !__any(m_run == -INFINITY);
+    };
+    auto body = [&](int j, const int8_t* kcur, int8_t* knext, uint16_t* vcopy, const uint16_t* vprev,
+                    const float* scur, float* snext) __attribute__((always_inline)) {
+      const int n0 = n_beg + j * BN;
+      if (j + 1 < ntiles) {
+        load_k(n0 + BN, knext);
+        load_s(n0 + BN, snext);
+      }
+      const bool dead = !live(j);
+      const bool mask = dead || masked(j);
+      const bool skip = dead && !live(j - 1);  // nothing pending: P = 0, scores -inf
+      if (!skip) {
+        half_step_fast(0, kcur, scur, vprev, xB, xmB, pB, xA, xmA, pA);
+        if (mask || !all_set) half_fixup(j, 0, mask, dead, xA, xmA);
+      }
+      if (j < ntiles) load_v(n0, vcopy);
+      if (!skip) {
+        half_step_fast(1, kcur, scur, vprev, xA, xmA, pA, xB, xmB, pB);
+        if (mask || !all_set) half_fixup(j, 1, mask, dead, xB, xmB);
+      }
+      wait_dma();
+      __syncthreads();
+    };
+    if (ntiles > 0) {
+      load_k(n_beg, sk0);
+      load_s(n_beg, ss0);
+    }
+    wait_dma();
+    __syncthreads();
+    int j = 0;
+    for (; j + 1 <= ntiles; j += 2) {
+      body(j, sk0, sk1, sv0, sv1, ss0, ss1);
+      body(j + 1, sk1, sk0, sv1, sv0, ss1, ss0);
+    }
+    if (j <= ntiles) body(j, sk0, sk1, sv0, sv1, ss0, ss1);
+
+    // l over the 4 lane groups of the query
+    float l = l_lane;
+    {
+      const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(l), __float_as_uint(l), false, false);
+      l = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+      const auto r2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(l), __float_as_uint(l), false, false);
+      l = __uint_as_float(r2[0]) + __uint_as_float(r2[1]);
+    }
+    if (m_ok) {
+      const float inv = (l > 0.f) ? 1.f / l : 0.f;
+      uint16_t* orow = reinterpret_cast<uint16_t*>(a.out) + ((int64_t)bh * M + mq) * a.dout;
+#pragma unroll
+      for (int tb = 0; tb < 16; ++tb) {
+        const int d0 = 16 * tb + 4 * g;
+        if (d0 >= a.dout) continue;  // zero-padded channels
+        const float4 v4 = *reinterpret_cast<const float4*>(a.vs + bkv * D + d0);
+        const float vsc[4] = {v4.x, v4.y, v4.z, v4.w};
+        uint16_t hv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) hv[e] = f2h_bits(oacc[tb][e] * inv * vsc[e]);
+        uint2 pk;
+        pk.x = hv[0] | ((uint32_t)hv[1] << 16);
+        pk.y = hv[2] | ((uint32_t)hv[3] << 16);
+        *reinterpret_cast<uint2*>(orow + d0) = pk;
+      }
+    }
+    __syncthreads();  // the next pass's first copies reuse the tiles
+  }
+}
+
 int w8a8_wide_launch(const int8_t* q, const float* q_scale, const int8_t* k, const float* k_scale,
                      const int8_t* v, const float* v_scale, void* out, int64_t B, int64_t Hq,
                      int64_t Hkv, int64_t M, int64_t N, int64_t D, int64_t dout, bool causal,
@@ -1399,7 +1746,10 @@ int w8a8_wide_launch(const int8_t* q, const float* q_scale, const int8_t* k, con
   a.dout = (int)dout;
   a.w8_excess = w8_excess_for(N);
   constexpr int F = SL8_DTYPE_BF16;
-  if (D == 64) {
+  if (SL8_W8_Q16 && D == 256) {
+    if (causal) attn_w8a8_q16_kernel<true><<<grid, 512, 0, st>>>(a);
+    else attn_w8a8_q16_kernel<false><<<grid, 512, 0, st>>>(a);
+  } else if (D == 64) {
     if (causal) launch_wide<64, true, F, false, true>(a, grid, st);
     else launch_wide<64, false, F, false, true>(a, grid, st);
   } else if (D == 128) {
