@@ -1386,12 +1386,18 @@ int w8a8_pad_operands(const int8_t*& q, const int8_t*& k, const int8_t*& v, cons
 // of 16 dims x 16 queries (64 accumulators), and a workgroup of 8 waves (two
 // per SIMD) covers the same 128 queries and shares the same K / V^T tiles.
 //   QK: S^T = K Q^T on v_mfma_i32_16x16x64_i8, per 32-key half 2 key blocks
-//       x 4 dim chunks; lane (l16, g) ends with keys 16 kb + 4 g + i of query
-//       l16 (kb = 0, 1; i = 0..3).
+//       x 4 dim chunks. A-operand row r of a block is key rho(r) =
+//       8 ((r / 4) & 1) + 4 (r / 8) + r % 4 (any row order is valid), so lane
+//       (l16, g) ends with keys 16 kb + kg + i of query l16, kg = rho(4 g)
+//       (kb = 0, 1; i = 0..3).
 //   PV: O^T += V^T P^T on v_mfma_f32_16x16x32_bf16 with the half's 32 keys in
-//       the order sigma(8 g + e) = 16 (e / 4) + 4 g + e % 4: exactly the keys
+//       the order sigma(8 g + e) = 16 (e / 4) + kg + e % 4: exactly the keys
 //       lane (l16, g) holds, so P needs no lane exchange; the V^T operand is
-//       two 8-byte reads per MFMA in the same order.
+//       two 8-byte reads per MFMA in the same order. rho makes lane groups
+//       g = 0, 1 (one pass of an 8-byte LDS read) read the two 8-byte halves
+//       of their chunks: with keys 4 g + i they read the same half and
+//       collided 2-way on every V^T read (LDS bank conflicts ~23 % of the
+//       launch at config 5).
 // The arithmetic per row is the wide kernel's W8A8 path (P re-quantised per
 // 32-key half against the half's max, the lazy reference-point rescale), and
 // so is the straight-line half-step. Config 5: 1081 -> 986 us (the same
@@ -1442,22 +1448,24 @@ attn_w8a8_q16_kernel(const FwdArgs a) {
   // K operand (A, 16 keys x 64 dims): lane (l16, g) reads the 16-byte chunk
   // 4 c + g of key row l16 of the block; the tile keeps chunk c of row r at
   // c ^ (r & 15) (the copy below), so 16 rows read 16 distinct bank groups
+  const int rl = 8 * ((l16 >> 2) & 1) + 4 * (l16 >> 3) + (l16 & 3);  // rho(l16)
+  const int kg = 8 * (g & 1) + 4 * (g >> 1);                          // rho(4 g)
   int koff[4];
 #pragma unroll
-  for (int c4 = 0; c4 < 4; ++c4) koff[c4] = ((4 * c4 + g) ^ l16) * 16;
-  // V^T operand (A, 16 dims x 32 keys in sigma order): keys 4 g .. +3 and
-  // 16 + 4 g .. +3 of the half, 8 bytes each, of V^T row l16 of the dim
+  for (int c4 = 0; c4 < 4; ++c4) koff[c4] = ((4 * c4 + g) ^ rl) * 16;
+  // V^T operand (A, 16 dims x 32 keys in sigma order): keys kg .. +3 and
+  // 16 + kg .. +3 of the half, 8 bytes each, of V^T row l16 of the dim
   // block. v8_to_bf16_t_kernel stores each 16-key group with bits 2 and 3 of
   // the key index exchanged (key 8 b3 + 4 b2 + i at position 8 b2 + 4 b3 + i),
-  // so keys 4 g + i of a group sit at 8 (g & 1) + 4 (g >> 1) + i: chunk
-  // (g & 1) of the group, byte 8 (g >> 1); the tile keeps 16-byte chunk c of
-  // row d at c ^ ((d >> 1) & 7)
+  // so keys kg + i = 8 (g & 1) + 4 (g >> 1) + i of a group sit at
+  // 8 (g >> 1) + 4 (g & 1) + i: chunk (g >> 1) of the group, byte 8 (g & 1);
+  // the tile keeps 16-byte chunk c of row d at c ^ ((d >> 1) & 7)
   int voff[2][2];
 #pragma unroll
   for (int s = 0; s < 2; ++s)
 #pragma unroll
     for (int p = 0; p < 2; ++p)
-      voff[s][p] = ((4 * s + 2 * p + (g & 1)) ^ ((l16 >> 1) & 7)) * 16 + (g >> 1) * 8;
+      voff[s][p] = ((4 * s + 2 * p + (g >> 1)) ^ ((l16 >> 1) & 7)) * 16 + (g & 1) * 8;
   // V buffers start as zeros (finite): the first half-steps multiply them by P = 0
   for (int i = tid; i < D * BN / 8; i += WT) {
     reinterpret_cast<uint4*>(sv0)[i] = make_uint4(0, 0, 0, 0);
@@ -1538,7 +1546,7 @@ attn_w8a8_q16_kernel(const FwdArgs a) {
 #pragma unroll
     for (int t = 0; t < 16; ++t) oacc[t] = v4f_t{0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY, l_lane = 0.f;
-    typedef float xblk16[8];  // a half's scores: slot 4 kb + i = key 16 kb + 4 g + i
+    typedef float xblk16[8];  // a half's scores: slot 4 kb + i = key 16 kb + kg + i
 
     // max over the 32 keys of the row: the lane's 8, then the 4 lane groups
     auto row_max = [&](const xblk16& x) __attribute__((always_inline)) {
@@ -1572,7 +1580,7 @@ attn_w8a8_q16_kernel(const FwdArgs a) {
       auto load_op = [&](int i) __attribute__((always_inline)) -> v4i {
         if (i < 8) {
           const int k2 = i >> 2, c4 = i & 3;
-          return *reinterpret_cast<const v4i*>(kt + (32 * s + 16 * k2 + l16) * D + koff[c4]);
+          return *reinterpret_cast<const v4i*>(kt + (32 * s + 16 * k2 + rl) * D + koff[c4]);
         }
         const char* row = vb + (i - 8) * 16 * (2 * BN);
         const uint2 lo = *reinterpret_cast<const uint2*>(row + voff[s][0]);
@@ -1612,8 +1620,8 @@ attn_w8a8_q16_kernel(const FwdArgs a) {
           const int tb = i - 8;
           oacc[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, opb[i]), p2, oacc[tb], 0, 0, 0);
           if (i == 8) {
-            kv[0] = *reinterpret_cast<const float4*>(st + 32 * s + 4 * g);
-            kv[1] = *reinterpret_cast<const float4*>(st + 32 * s + 16 + 4 * g);
+            kv[0] = *reinterpret_cast<const float4*>(st + 32 * s + kg);
+            kv[1] = *reinterpret_cast<const float4*>(st + 32 * s + 16 + kg);
 #pragma unroll
             for (int e = 0; e < 8; ++e) p1[e] = (__bf16)pe[e];
             pin_vgpr(__builtin_bit_cast(v4i, p1));
@@ -1650,7 +1658,7 @@ attn_w8a8_q16_kernel(const FwdArgs a) {
         const int lo = (wl >= 0) ? qpos - wl + 1 : INT_MIN / 2;
         const int lo_c = max(lo, nb - 64);
         const uint32_t span = hi > lo_c ? (uint32_t)(hi - lo_c) : 0u;
-        const uint32_t rel = (uint32_t)(nb + 4 * g - lo_c);
+        const uint32_t rel = (uint32_t)(nb + kg - lo_c);
 #pragma unroll
         for (int e = 0; e < 8; ++e)
           xo[e] = (rel + (uint32_t)(16 * (e >> 2) + (e & 3)) < span) ? xo[e] : -INFINITY;
