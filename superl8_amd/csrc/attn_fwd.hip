@@ -1406,6 +1406,9 @@ int w8a8_pad_operands(const int8_t*& q, const int8_t*& k, const int8_t*& v, cons
 #ifndef SL8_W8_Q16
 #define SL8_W8_Q16 1
 #endif
+#ifndef SL8_Q16_PD
+#define SL8_Q16_PD 3  // operand reads ahead of their MFMA
+#endif
 typedef float v4f_t __attribute__((ext_vector_type(4)));
 
 template <bool CAUSAL>
@@ -1588,7 +1591,7 @@ attn_w8a8_q16_kernel(const FwdArgs a) {
         return v4i{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
       };
       constexpr int NOP = 24;
-      constexpr int PD = 3;
+      constexpr int PD = SL8_Q16_PD;
       v4i opb[NOP];
 #pragma unroll
       for (int i = 0; i < PD; ++i) opb[i] = load_op(i);
@@ -1601,41 +1604,62 @@ attn_w8a8_q16_kernel(const FwdArgs a) {
       const bool any_key = tm0 != -INFINITY;
       const float sub = any_key ? tm0 - LOG2_127 : 0.f;
       const float fac = any_key ? __builtin_amdgcn_exp2f(tm0 - m_run) * (1.0f / 127.0f) : 0.f;
-      float pe[8];
+      float pe[8], py[8];
       float hs = 0.f, xm = -INFINITY;
       float4 kv[2];
       v4i sc[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
+      // the P code of key e in two steps two MFMAs apart, so that the exp2
+      // latency is covered: a: y = exp2(x q_scale - sub); b: the row sum,
+      // rint and the scale
+      auto pc_a = [&](int e) __attribute__((always_inline)) {
+        py[e] = __builtin_amdgcn_exp2f(fmaf(xi[e], qsc, -sub));
+        pin_vgpr(py[e]);
+      };
+      auto pc_b = [&](int e) __attribute__((always_inline)) {
+        hs += py[e];
+        pe[e] = rintf(py[e]) * fac;
+        pin_vgpr(pe[e]);
+        pin_vgpr(hs);
+      };
+      auto conv = [&](int e) __attribute__((always_inline)) {
+        const float kk[4] = {kv[e >> 2].x, kv[e >> 2].y, kv[e >> 2].z, kv[e >> 2].w};
+        xo[e] = (float)sc[e >> 2][e & 3] * kk[e & 3];
+        pin_vgpr(xo[e]);
+      };
+      // slices: MFMA 0..7 (QK): P codes of keys 0..3 (a of key i / 2 after
+      // MFMA i even, b after i + 1); MFMA 8 (PV 0): the k_scale reads;
+      // MFMAs 9..16: the score of key i - 9 and the P codes of keys 4..7 the
+      // same way; 17: pack P, l; 18: the scores' max in this lane; 19: across
+      // the lane groups (xmo)
 #pragma unroll
       for (int i = 0; i < NOP; ++i) {
         if (i + PD < NOP) opb[i + PD] = load_op(i + PD);
         __builtin_amdgcn_sched_barrier(0);
         if (i < 8) {
           sc[i >> 2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(opb[i], qop[i & 3], sc[i >> 2], 0, 0, 0);
-          const float y = __builtin_amdgcn_exp2f(fmaf(xi[i], qsc, -sub));
-          hs += y;
-          pe[i] = rintf(y) * fac;
-          pin_vgpr(pe[i]);
-          pin_vgpr(hs);
+          if (i & 1) pc_b(i >> 1);
+          else pc_a(i >> 1);
         } else {
           const int tb = i - 8;
           oacc[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, opb[i]), p2, oacc[tb], 0, 0, 0);
           if (i == 8) {
             kv[0] = *reinterpret_cast<const float4*>(st + 32 * s + kg);
             kv[1] = *reinterpret_cast<const float4*>(st + 32 * s + 16 + kg);
+          } else if (i <= 16) {
+            conv(i - 9);
+            const int k = 4 + ((i - 9) >> 1);
+            if ((i - 9) & 1) pc_b(k);
+            else pc_a(k);
+          } else if (i == 17) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) p1[e] = (__bf16)pe[e];
             pin_vgpr(__builtin_bit_cast(v4i, p1));
             l_lane = l_lane * fr + hs * fac;
-          } else if (i <= 16) {
-            const int e = i - 9;
-            const float kk[4] = {kv[e >> 2].x, kv[e >> 2].y, kv[e >> 2].z, kv[e >> 2].w};
-            xo[e] = (float)sc[e >> 2][e & 3] * kk[e & 3];
-            pin_vgpr(xo[e]);
-          } else if (i == 17) {
+          } else if (i == 18) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) xm = fmaxf(xm, xo[e]);
             pin_vgpr(xm);
-          } else if (i == 18) {
+          } else if (i == 19) {
             const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(xm), __float_as_uint(xm), false, false);
             xmo = max_xor32(fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1])));
             pin_vgpr(xmo);
