@@ -1407,7 +1407,7 @@ int w8a8_pad_operands(const int8_t*& q, const int8_t*& k, const int8_t*& v, cons
 #define SL8_W8_Q16 1
 #endif
 #ifndef SL8_Q16_PD
-#define SL8_Q16_PD 3  // operand reads ahead of their MFMA
+#define SL8_Q16_PD 4  // operand reads ahead of their MFMA (2 / 3 / 4 / 6 at config 5: 972 / 969 / 963 / 967 us)
 #endif
 typedef float v4f_t __attribute__((ext_vector_type(4)));
 
