@@ -1411,6 +1411,8 @@ int w8a8_pad_operands(const int8_t*& q, const int8_t*& k, const int8_t*& v, cons
 #endif
 typedef float v4f_t __attribute__((ext_vector_type(4)));
 
+namespace {
+
 template <bool CAUSAL>
 __global__ void __launch_bounds__(512, 1)
 attn_w8a8_q16_kernel(const FwdArgs a) {
@@ -1756,6 +1758,8 @@ attn_w8a8_q16_kernel(const FwdArgs a) {
     __syncthreads();  // the next pass's first copies reuse the tiles
   }
 }
+
+}  // namespace
 
 int w8a8_wide_launch(const int8_t* q, const float* q_scale, const int8_t* k, const float* k_scale,
                      const int8_t* v, const float* v_scale, void* out, int64_t B, int64_t Hq,
