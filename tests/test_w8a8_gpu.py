@@ -37,6 +37,7 @@ CASES = [  # B, Hq, Hkv, M, N, D, causal
     (1, 2, 2, 128, 128, 64, False), (1, 2, 2, 128, 128, 64, True), (2, 4, 2, 257, 257, 64, True),
     (1, 2, 2, 333, 333, 128, False), (1, 4, 1, 100, 333, 128, True), (1, 2, 1, 200, 200, 256, True),
     (1, 2, 2, 70, 90, 256, False),
+    (1, 4, 1, 100, 333, 256, True), (3, 3, 1, 161, 161, 256, True),  # D = 256: M < N causal, odd B*Hq
     (1, 4, 2, 200, 200, 32, True), (2, 2, 1, 130, 77, 32, False),  # head dim 32 (padded to 64)
 ]
 
