@@ -277,8 +277,7 @@ decode_split_kernel(const int8_t* __restrict__ q, const float* __restrict__ q_sc
 // Cross-split LSE merge (reference attn_decode.cuh:430-466):
 //   gm = max_s m_s, out = sum_s o_s 2^(m_s - gm) / sum_s l_s 2^(m_s - gm),
 // empty splits (m_s = DEC_NEG_INF) contributing nothing. One wave per query
-// head (4 per workgroup): the lanes
-// hold D / 64 channels each and every partial load of the head is issued
+// head (CMB_WAVES per workgroup): the lanes hold D / 64 channels each and every partial load of the head is issued
 // before any is used; the split weights 2^(m_s - gm) are formed once per
 // split by the lane that loaded m_s and broadcast, and the sums run over the
 // splits in index order (deterministic).
