@@ -469,7 +469,8 @@ def main():
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(see the sharding plan in DESIGN.md); run with --gpus 1", file=sys.stderr)
+              "(prefill and decode would shard over batch x KV-head groups with no exchange "
+              "beyond the decode's LSE merge); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
