@@ -210,6 +210,11 @@ struct QOp {
 #ifndef SL8_FWD_BAL
 #define SL8_FWD_BAL 1
 #endif
+// balanced slices: the slot whose VALU slice starts the k_scale reads (config 2:
+// slot 4 ~0.5 % faster than slot 6 on two machines)
+#ifndef SL8_FWD_KVS
+#define SL8_FWD_KVS 4
+#endif
 #ifndef SL8_FWD_OCC
 #define SL8_FWD_OCC 2
 #endif
@@ -712,8 +717,9 @@ attn_fwd_wide_kernel(const FwdArgs a) {
         // Balanced slices (VALU cycles per MFMA slot ~32-40; exp2 is quarter
         // rate): slots 0..7 exp2 of keys 2i, 2i+1 of half h-1, with the pack +
         // row sum of keys 0..7 after slot 3 and of keys 8..15 after slot 7;
-        // slot 6 reads k_scale; slots 8..11 form the exp2 arguments of half h,
-        // four keys each (the QK chain ended at slot 3).
+        // slot SL8_FWD_KVS reads k_scale, four slots before its first use;
+        // slots 8..11 form the exp2 arguments of half h, four keys each (the QK
+        // chain ended at slot 3).
         static_assert(NOP == 12, "balanced slices: D = 128");
         if (i < DC) sc = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur, qop[0].c[i], sc, 0, 0, 0);
         else oacc[0][(i - DC) % DC] = PV::mfma(__builtin_bit_cast(pvec, cur), p2[0][(i - DC) / DC],
@@ -737,7 +743,7 @@ attn_fwd_wide_kernel(const FwdArgs a) {
             ovf = ovf || (hs > 32768.f);
           }
         }
-        if (i == 6) {
+        if (i == SL8_FWD_KVS) {
 #pragma unroll
           for (int gq = 0; gq < 4; ++gq)
             kv[gq] = *reinterpret_cast<const float4*>(st + 32 * s + 8 * gq + 4 * h);
